@@ -1,0 +1,133 @@
+// Device helpers shared by the gfx950 kernels of the quantized weight path.
+//
+// Block formats (skyla-gguf/src/lib.rs:33-43, quant.rs:5-89) as the planner splits
+// them into 16-byte regions (skyla-engine/src/planner.rs:8-15):
+//   Q4_K 144 B / 256 values: region 0 = qs (128 B, 8 uint4), region 1 = header
+//        (16 B: d f16 | dmin f16 | 12 packed 6-bit scale/min bytes).
+//   Q6_K 210 B / 256 values: ql (128 B), qh (64 B), sc (16 x i8), d (f16 array).
+//   Q8_0 34 B / 32 values: q (32 x i8 = 2 uint4), d (f16 array).
+// Offsets arriving in push words are in units of the binding they index.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef _Float16 f16;
+typedef f16 f16x2 __attribute__((ext_vector_type(2)));
+typedef f16 f16x4 __attribute__((ext_vector_type(4)));
+typedef f16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+#define SK_DEV static __device__ __forceinline__
+
+SK_DEV float f16_bits_to_f32(uint32_t bits16) {
+  return (float)__builtin_bit_cast(f16, (uint16_t)bits16);
+}
+
+SK_DEV f16x2 as_f16x2(uint32_t u) { return __builtin_bit_cast(f16x2, u); }
+SK_DEV uint32_t as_u32(f16x2 h) { return __builtin_bit_cast(uint32_t, h); }
+
+// Round-to-nearest-even pack of two floats (v_cvt_pk_f16_f32 on gfx950).
+SK_DEV f16x2 pack_f16x2(float a, float b) {
+  f16x2 r = {(f16)a, (f16)b};
+  return r;
+}
+
+// acc + a.x*b.x + a.y*b.y with f32 accumulation (v_dot2_f32_f16).
+SK_DEV float dot2(f16x2 a, f16x2 b, float acc) {
+  return __builtin_amdgcn_fdot2(a, b, acc, false);
+}
+
+// Sum over groups of LPR consecutive lanes of a wave64 (LPR in {16, 32, 64}); every lane
+// of a group receives the group total.
+template <int LPR>
+SK_DEV float group_sum(float v) {
+#pragma unroll
+  for (int d = LPR / 2; d >= 1; d >>= 1) v += __shfl_xor(v, d, 64);
+  return v;
+}
+
+SK_DEV uint32_t ctl_word(const uint32_t *ctl, uint32_t i) { return ctl[i]; }
+
+// ---------------------------------------------------------------------------------------
+// Bit-exact dequantisation of one 32-value group, in the reference's operation order.
+// FP contraction is switched off inside these bodies: Rust never fuses a*b-c.
+// ---------------------------------------------------------------------------------------
+
+// q4k_scale_min (quant.rs:40-49) over the 12 scale bytes held in words y, z, w of the
+// 16-byte header.
+SK_DEV void q4k_scale_min(uint32_t j, uint32_t sy, uint32_t sz, uint32_t sw, uint32_t &sc,
+                          uint32_t &m) {
+  auto byte = [&](uint32_t k) -> uint32_t {
+    uint32_t word = k < 4 ? sy : (k < 8 ? sz : sw);
+    return (word >> (8 * (k & 3))) & 255u;
+  };
+  if (j < 4) {
+    sc = byte(j) & 63u;
+    m = byte(j + 4) & 63u;
+  } else {
+    sc = (byte(j + 4) & 15u) | ((byte(j - 4) >> 6) << 4);
+    m = (byte(j + 4) >> 4) | ((byte(j) >> 6) << 4);
+  }
+}
+
+// Q4_K sub-block `sub` (0..7) of one super-block: 32 values
+//   o[i] = (d * sc) * q - (dmin * m)               (quant.rs:60-65)
+// `qa`, `qb` are the two uint4 of qs holding chunk sub/2 (32 bytes); low nibbles for even
+// sub, high nibbles for odd.
+SK_DEV void dequant_q4k_sub(uint4 hdr, uint4 qa, uint4 qb, uint32_t sub, float o[32]) {
+#pragma clang fp contract(off)
+  float d = f16_bits_to_f32(hdr.x & 0xffffu);
+  float dmin = f16_bits_to_f32(hdr.x >> 16);
+  uint32_t sc, m;
+  q4k_scale_min(sub, hdr.y, hdr.z, hdr.w, sc, m);
+  float d0 = d * (float)sc;
+  float min0 = dmin * (float)m;
+  uint32_t shift = (sub & 1) * 4;
+  uint32_t wds[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+#pragma unroll
+  for (int i = 0; i < 32; i++) {
+    uint32_t q = (wds[i >> 2] >> (8 * (i & 3) + shift)) & 15u;
+    o[i] = d0 * (float)q - min0;
+  }
+}
+
+// Q6_K: 32 values of group g (0..3) in half `hf` (0..1) of one super-block
+//   o[l + 32 g] = (d * sc[is + 2g]) * q_g(l)       (quant.rs:70-89), is = l / 16
+// ql: the 4 uint4 of ql for this half (64 B), qh: the 2 uint4 of qh (32 B), sc: 16 x i8.
+SK_DEV void dequant_q6k_group(const uint4 ql[4], const uint4 qh[2], uint4 scw, float d,
+                              uint32_t hf, uint32_t g, float o[32]) {
+#pragma clang fp contract(off)
+  uint32_t lw[16] = {ql[0].x, ql[0].y, ql[0].z, ql[0].w, ql[1].x, ql[1].y, ql[1].z, ql[1].w,
+                     ql[2].x, ql[2].y, ql[2].z, ql[2].w, ql[3].x, ql[3].y, ql[3].z, ql[3].w};
+  uint32_t hw[8] = {qh[0].x, qh[0].y, qh[0].z, qh[0].w, qh[1].x, qh[1].y, qh[1].z, qh[1].w};
+  uint32_t sw[4] = {scw.x, scw.y, scw.z, scw.w};
+  // q1: ql[l] lo, qh bits 0-1; q2: ql[l+32] lo, bits 2-3; q3: ql[l] hi, bits 4-5;
+  // q4: ql[l+32] hi, bits 6-7.
+  uint32_t lbase = (g & 1) ? 32 : 0;
+  uint32_t nshift = (g >> 1) * 4;
+  uint32_t hshift = 2 * g;
+#pragma unroll
+  for (int l = 0; l < 32; l++) {
+    uint32_t li = lbase + l;
+    uint32_t lb = (lw[li >> 2] >> (8 * (li & 3) + nshift)) & 15u;
+    uint32_t hb = (hw[l >> 2] >> (8 * (l & 3) + hshift)) & 3u;
+    int q = (int)(lb | (hb << 4)) - 32;
+    uint32_t k = hf * 8 + (uint32_t)(l / 16) + 2 * g;
+    int s = (int)(int8_t)((sw[k >> 2] >> (8 * (k & 3))) & 255u);
+    o[l] = d * (float)s * (float)q;
+  }
+  (void)hf;
+}
+
+// Q8_0 block: o[i] = d * q[i]   (quant.rs:17-24)
+SK_DEV void dequant_q8_0_block(uint4 qa, uint4 qb, float d, float o[32]) {
+#pragma clang fp contract(off)
+  uint32_t wds[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+#pragma unroll
+  for (int i = 0; i < 32; i++) {
+    int q = (int)(int8_t)((wds[i >> 2] >> (8 * (i & 3))) & 255u);
+    o[i] = d * (float)q;
+  }
+}

@@ -1,0 +1,377 @@
+// Prefill matmul over raw Q8_0 / Q4_K / Q6_K blocks on gfx950 MFMA.
+//
+// Contract (matmul.comp:113-184, graph.rs:23-34, graph/moe.rs:26-40):
+//   spec [TYPE, ACCUM, MOE(, X_HALF)]: TYPE 0/1/2 = Q8_0/Q4_K/Q6_K.  Workgroup = 128 output
+//   rows (MATMUL_TILE_ROWS) x TN tokens; grid = [ceil(n_out/128), 1 | n_expert, z] and tile z
+//   covers tokens [z*TN, z*TN+TN).  Dense: token count = ctl[2], token i reads x row i and
+//   writes y row i.  MOE: expert e = grid.y, (count, start) = table[e], token i of the
+//   group is slot s = list[start + i]; it reads x row s / x_div and writes y row s; the
+//   weight rows are offset by e * n_out.  Output is token-major: y[y_off + row_tok *
+//   y_stride + out_row] (+= with ACCUM).  X is f32, or f16 when X_HALF (then x_off and
+//   x_stride count f16 elements).
+//
+// MI355X design:
+//   * v_mfma_f32_32x32x16_f16 with f32 accumulation.  D = X * W^T so each lane owns one
+//     output row and stores are 128-byte coalesced runs along the row dimension.
+//   * weights never touch LDS: each wave owns 32 rows and dequantises its fragments in
+//     registers, 8 values per lane per MFMA step, into exactly the operand layout the MFMA
+//     reads (lane l: row l%32, lane half l/32 selects which 8 k of the step).  Quants
+//     become f16 through the 0x6400 mantissa trick, then one packed f16 add removes the
+//     offset (exact) and one packed f16 fma/mul applies scale and min.
+//   * the K order inside a 256-value super-block is permuted freely (a sum does not care),
+//     so each lane half always reads from a single sub-block per step; activations are
+//     staged in the same order: 8 consecutive k per lane, pairs stored as (0,2),(1,3),(4,6),
+//     (5,7) to match the packed-quant extraction.
+//   * activations go through LDS as f16, double buffered: the next super-block's global
+//     loads are in flight while the current one runs on the matrix cores.
+#include "common.h"
+
+namespace {
+
+constexpr int TM = 128;        // rows per workgroup
+constexpr int KC = 256;        // k per LDS stage (one K-quant super-block)
+constexpr int PITCH = KC + 8;  // f16 per staged token row (16 B pad: conflict-free b128)
+
+struct MatmulPush {  // 13 words (graph.rs:28, graph/moe.rs:264-266)
+  uint32_t o0, o1, o2, o3, x_off, y_off, n_in, n_out, x_stride, y_stride, table_off, list_off,
+      x_div;
+};
+
+SK_DEV f16x2 splat(f16 v) {
+  f16x2 r = {v, v};
+  return r;
+}
+
+// k offset (inside the current 256-k stage) of the 8 values lane-half hh holds at step t
+template <int TYPE>
+SK_DEV uint32_t koff(int t, uint32_t hh) {
+  if (TYPE == 1) return 64 * (t >> 2) + 32 * hh + 8 * (t & 3);                  // Q4_K
+  if (TYPE == 2) return 128 * (t >> 3) + 32 * ((t >> 1) & 3) + 16 * (t & 1) + 8 * hh;  // Q6_K
+  return 16 * t + 8 * hh;                                                            // Q8_0
+}
+
+// Raw weight bytes of one row for one 256-k stage, held by each lane.
+template <int TYPE>
+struct WStage;
+
+template <>
+struct WStage<1> {  // Q4_K: 128 B qs + 16 B header
+  uint4 qs[8];
+  uint4 hd;
+};
+template <>
+struct WStage<2> {  // Q6_K: ql 128 B, qh 64 B, 16 scales, d
+  uint4 ql[8];
+  uint4 qh[4];
+  uint4 sc;
+  uint32_t d;
+};
+template <>
+struct WStage<0> {  // Q8_0: 8 blocks of 32 quants + 8 scales
+  uint4 q[16];
+  uint32_t d[8];
+};
+
+template <int TYPE>
+SK_DEV void load_stage(WStage<TYPE> &s, const uint4 *w, const uint16_t *wd, const MatmulPush &p,
+                       uint32_t row, uint32_t kc, uint32_t nk) {
+  if constexpr (TYPE == 1) {
+    const uint32_t units = p.n_in >> 5, supers = p.n_in >> 8, sb = kc >> 8;
+    const uint4 *q = w + p.o0 + row * units + sb * 8;
+#pragma unroll
+    for (int i = 0; i < 8; i++) s.qs[i] = q[i];
+    s.hd = w[p.o1 + row * supers + sb];
+  } else if constexpr (TYPE == 2) {
+    const uint32_t rs = row * (p.n_in >> 8) + (kc >> 8);
+#pragma unroll
+    for (int i = 0; i < 8; i++) s.ql[i] = w[p.o0 + rs * 8 + i];
+#pragma unroll
+    for (int i = 0; i < 4; i++) s.qh[i] = w[p.o1 + rs * 4 + i];
+    s.sc = w[p.o2 + rs];
+    s.d = wd[p.o3 + rs];
+  } else {
+    const uint32_t chunks = p.n_in >> 4, blocks = p.n_in >> 5;
+    const uint4 *q = w + p.o0 + row * chunks + (kc >> 4);
+    const uint16_t *d = wd + p.o1 + row * blocks + (kc >> 5);
+    const uint32_t nb = nk >> 5;  // whole blocks in this stage
+#pragma unroll
+    for (int b = 0; b < 8; b++) {
+      if ((uint32_t)b < nb) {
+        s.q[2 * b] = q[2 * b];
+        s.q[2 * b + 1] = q[2 * b + 1];
+        s.d[b] = d[b];
+      } else {
+        s.q[2 * b] = make_uint4(0, 0, 0, 0);
+        s.q[2 * b + 1] = make_uint4(0, 0, 0, 0);
+        s.d[b] = 0;
+      }
+    }
+  }
+}
+
+// Dequantised f16 operand (8 values, pair-permuted) of lane half hh at step t.
+template <int TYPE>
+SK_DEV f16x8 weight_frag(const WStage<TYPE> &s, int t, uint32_t hh, f16x2 scale, f16x2 negmin) {
+  const uint32_t M = 0x64006400u;
+  uint32_t d0, d1, m0, m1;
+  f16x2 off;
+  if constexpr (TYPE == 1) {
+    // chunk c = t/4 holds sub-blocks 2c (low nibbles, hh = 0) and 2c+1 (high, hh = 1)
+    const int c = t >> 2, pc = t & 3;
+    const uint4 v = s.qs[2 * c + (pc >> 1)];
+    d0 = (pc & 1) ? v.z : v.x;
+    d1 = (pc & 1) ? v.w : v.y;
+    const uint32_t mask = hh ? 0x00f000f0u : 0x000f000fu;
+    m0 = mask;
+    m1 = mask;
+    off = splat((f16)-1024.0f);
+    const uint32_t a = (d0 & m0) | M, b = ((d0 >> 8) & m0) | M;
+    const uint32_t e = (d1 & m1) | M, f = ((d1 >> 8) & m1) | M;
+    f16x2 w0 = __builtin_elementwise_fma(as_f16x2(a) + off, scale, negmin);
+    f16x2 w1 = __builtin_elementwise_fma(as_f16x2(b) + off, scale, negmin);
+    f16x2 w2 = __builtin_elementwise_fma(as_f16x2(e) + off, scale, negmin);
+    f16x2 w3 = __builtin_elementwise_fma(as_f16x2(f) + off, scale, negmin);
+    f16x8 r = {w0.x, w0.y, w1.x, w1.y, w2.x, w2.y, w3.x, w3.y};
+    return r;
+  } else if constexpr (TYPE == 2) {
+    // step t: half hf = t/8, group g = (t/2)%4, l0 = 16 (t%2) + 8 hh
+    const int hf = t >> 3, g = (t >> 1) & 3;
+    const uint32_t l0 = 16 * (t & 1) + 8 * hh;  // byte offset inside the 32-byte run
+    const uint32_t lbyte = hf * 64 + ((g & 1) ? 32 : 0) + l0;
+    const uint32_t hbyte = hf * 32 + l0;
+    auto word = [](const uint4 *v, uint32_t byte) -> uint32_t {
+      const uint4 q = v[byte >> 4];
+      const uint32_t k = (byte >> 2) & 3;
+      return k == 0 ? q.x : (k == 1 ? q.y : (k == 2 ? q.z : q.w));
+    };
+    const uint32_t l_0 = word(s.ql, lbyte), l_1 = word(s.ql, lbyte + 4);
+    const uint32_t h_0 = word(s.qh, hbyte), h_1 = word(s.qh, hbyte + 4);
+    const uint32_t lmask = (g >= 2) ? 0x00f000f0u : 0x000f000fu;
+    const uint32_t hmask = (g >= 2) ? 0x03000300u : 0x00300030u;
+    const int hs = 4 - 2 * (g & 1);
+    auto q6 = [&](uint32_t l, uint32_t h) -> uint32_t { return (l & lmask) | M | ((h << hs) & hmask); };
+    off = splat((g >= 2) ? (f16)-1536.0f : (f16)-1056.0f);
+    f16x2 w0 = (as_f16x2(q6(l_0, h_0)) + off) * scale;
+    f16x2 w1 = (as_f16x2(q6(l_0 >> 8, h_0 >> 8)) + off) * scale;
+    f16x2 w2 = (as_f16x2(q6(l_1, h_1)) + off) * scale;
+    f16x2 w3 = (as_f16x2(q6(l_1 >> 8, h_1 >> 8)) + off) * scale;
+    (void)negmin;
+    (void)m0;
+    (void)m1;
+    f16x8 r = {w0.x, w0.y, w1.x, w1.y, w2.x, w2.y, w3.x, w3.y};
+    return r;
+  } else {
+    const uint4 v = s.q[t];
+    d0 = hh ? v.z : v.x;
+    d1 = hh ? v.w : v.y;
+    d0 ^= 0x80808080u;
+    d1 ^= 0x80808080u;
+    off = splat((f16)-1152.0f);
+    f16x2 w0 = (as_f16x2((d0 & 0x00ff00ffu) | M) + off) * scale;
+    f16x2 w1 = (as_f16x2(((d0 >> 8) & 0x00ff00ffu) | M) + off) * scale;
+    f16x2 w2 = (as_f16x2((d1 & 0x00ff00ffu) | M) + off) * scale;
+    f16x2 w3 = (as_f16x2(((d1 >> 8) & 0x00ff00ffu) | M) + off) * scale;
+    (void)negmin;
+    (void)m0;
+    (void)m1;
+    f16x8 r = {w0.x, w0.y, w1.x, w1.y, w2.x, w2.y, w3.x, w3.y};
+    return r;
+  }
+}
+
+// Scale (and negated min) of lane half hh at step t, as f16 pairs.  The f32 products
+// d*sc and dmin*m are the reference's d0 / min0 (quant.rs:60-61), rounded once to f16.
+template <int TYPE>
+SK_DEV void step_scale(const WStage<TYPE> &s, int t, uint32_t hh, f16x2 &scale, f16x2 &negmin) {
+  if constexpr (TYPE == 1) {
+    const uint32_t j = 2 * (t >> 2) + hh;
+    uint32_t sc, m;
+    q4k_scale_min(j, s.hd.y, s.hd.z, s.hd.w, sc, m);
+    const float d = f16_bits_to_f32(s.hd.x & 0xffffu);
+    const float dmin = f16_bits_to_f32(s.hd.x >> 16);
+    // high nibbles arrive as 16q: fold the 1/16 into the scale
+    const float sc_f = d * (float)sc * (hh ? 0.0625f : 1.0f);
+    scale = splat((f16)sc_f);
+    negmin = splat((f16)(-(dmin * (float)m)));
+  } else if constexpr (TYPE == 2) {
+    const int hf = t >> 3, g = (t >> 1) & 3;
+    const uint32_t k = 8 * hf + (t & 1) + 2 * g;
+    const uint32_t wv = k < 4 ? s.sc.x : (k < 8 ? s.sc.y : (k < 12 ? s.sc.z : s.sc.w));
+    const int sc = (int)(int8_t)((wv >> (8 * (k & 3))) & 255u);
+    const float d = f16_bits_to_f32(s.d);
+    scale = splat((f16)(d * (float)sc * (g >= 2 ? 0.0625f : 1.0f)));
+    negmin = splat((f16)0.0f);
+  } else {
+    scale = splat(__builtin_bit_cast(f16, (uint16_t)s.d[t >> 1]));
+    negmin = splat((f16)0.0f);
+  }
+}
+
+// Activations of one stage: TN tokens x nk k, read by 256 threads as 8-k items (token
+// n = item / 32, k group g = item % 32), converted to f16 and pair-permuted per 8.
+template <int TN>
+struct XStage {
+  static constexpr int ITEMS = TN * (KC / 8) / 256;
+  uint4 v[ITEMS];
+};
+
+template <int TN, int XHALF>
+SK_DEV void load_x(XStage<TN> &xr, const void *xv, const uint32_t *xrow, uint32_t x_off,
+                   uint32_t x_stride, uint32_t kc, uint32_t nk) {
+  const uint32_t tid = threadIdx.x;
+#pragma unroll
+  for (int it = 0; it < XStage<TN>::ITEMS; it++) {
+    const uint32_t id = tid + 256 * it;
+    const uint32_t n = id >> 5, g = id & 31;
+    uint4 out = make_uint4(0, 0, 0, 0);
+    if (8 * g < nk) {
+      const size_t base = (size_t)x_off + (size_t)xrow[n] * x_stride + kc + 8 * g;
+      if (XHALF) {
+        const uint4 v = *(const uint4 *)((const f16 *)xv + base);
+        // (x0,x1),(x2,x3) -> (x0,x2),(x1,x3)
+        out.x = __builtin_amdgcn_perm(v.y, v.x, 0x05040100u);
+        out.y = __builtin_amdgcn_perm(v.y, v.x, 0x07060302u);
+        out.z = __builtin_amdgcn_perm(v.w, v.z, 0x05040100u);
+        out.w = __builtin_amdgcn_perm(v.w, v.z, 0x07060302u);
+      } else {
+        const float *xp = (const float *)xv + base;
+        const float4 a = *(const float4 *)xp, b = *(const float4 *)(xp + 4);
+        out.x = as_u32(pack_f16x2(a.x, a.z));
+        out.y = as_u32(pack_f16x2(a.y, a.w));
+        out.z = as_u32(pack_f16x2(b.x, b.z));
+        out.w = as_u32(pack_f16x2(b.y, b.w));
+      }
+    }
+    xr.v[it] = out;
+  }
+}
+
+template <int TN>
+SK_DEV void store_x(f16 *lds, const XStage<TN> &xr) {
+  const uint32_t tid = threadIdx.x;
+#pragma unroll
+  for (int it = 0; it < XStage<TN>::ITEMS; it++) {
+    const uint32_t id = tid + 256 * it;
+    *(uint4 *)(lds + (id >> 5) * PITCH + 8 * (id & 31)) = xr.v[it];
+  }
+}
+
+template <int TYPE, int ACCUM, int MOE, int XHALF>
+SK_DEV void matmul_body(const uint4 *__restrict__ w, const uint16_t *__restrict__ wd,
+                        const void *x, float *y, const uint32_t *ctl, const MatmulPush &p) {
+  constexpr int TN = MOE ? 32 : 64;  // MOE_TILE_COLS / MATMUL_TILE_COLS of this backend
+  constexpr int NB = TN / 32;
+  __shared__ __attribute__((aligned(16))) f16 xs[2][TN * PITCH];
+  __shared__ uint32_t xrow[TN];
+  __shared__ uint32_t yrow[TN];
+
+  const uint32_t tid = threadIdx.x;
+  const uint32_t lane = tid & 63, wave = tid >> 6;
+  const uint32_t hh = lane >> 5;
+  const uint32_t row0 = blockIdx.x * TM;
+  const uint32_t e = blockIdx.y;
+  const uint32_t n_all = MOE ? ctl[p.table_off + 2 * e] : ctl[2];
+  const uint32_t col0 = blockIdx.z * TN;
+  if (col0 >= n_all) return;
+  const uint32_t n_tok = min(n_all - col0, (uint32_t)TN);
+  const uint32_t list = p.list_off + col0 + (MOE ? ctl[p.table_off + 2 * e + 1] : 0);
+  if (tid < TN) {
+    const uint32_t i = min(tid, n_tok - 1);
+    const uint32_t slot = MOE ? ctl[list + i] : col0 + i;
+    xrow[tid] = MOE ? slot / p.x_div : slot;
+    yrow[tid] = slot;
+  }
+  __syncthreads();
+
+  const uint32_t my_row = row0 + wave * 32 + (lane & 31);
+  const uint32_t wrow = (MOE ? e * p.n_out : 0) + min(my_row, p.n_out - 1);
+
+  f32x16 acc[NB];
+#pragma unroll
+  for (int j = 0; j < NB; j++)
+#pragma unroll
+    for (int i = 0; i < 16; i++) acc[j][i] = 0.0f;
+
+  const uint32_t n_stage = (p.n_in + KC - 1) / KC;
+  WStage<TYPE> ws;
+  {
+    XStage<TN> x0;
+    load_x<TN, XHALF>(x0, x, xrow, p.x_off, p.x_stride, 0, min(p.n_in, (uint32_t)KC));
+    load_stage<TYPE>(ws, w, wd, p, wrow, 0, min(p.n_in, (uint32_t)KC));
+    store_x<TN>(xs[0], x0);
+  }
+  __syncthreads();
+
+  for (uint32_t st = 0; st < n_stage; st++) {
+    const uint32_t kc = st * KC;
+    const uint32_t nk = min(p.n_in - kc, (uint32_t)KC);
+    const f16 *cur = xs[st & 1];
+    WStage<TYPE> wn;
+    XStage<TN> xn;
+    const bool more = st + 1 < n_stage;
+    if (more) {
+      const uint32_t kn = kc + KC;
+      load_stage<TYPE>(wn, w, wd, p, wrow, kn, min(p.n_in - kn, (uint32_t)KC));
+      load_x<TN, XHALF>(xn, x, xrow, p.x_off, p.x_stride, kn, min(p.n_in - kn, (uint32_t)KC));
+    }
+    const int steps = (int)(nk >> 4);
+#pragma unroll
+    for (int t = 0; t < 16; t++) {
+      if (t < steps) {
+        f16x2 sc, nm;
+        step_scale<TYPE>(ws, t, hh, sc, nm);
+        const f16x8 wf = weight_frag<TYPE>(ws, t, hh, sc, nm);
+        const uint32_t ko = koff<TYPE>(t, hh);
+#pragma unroll
+        for (int j = 0; j < NB; j++) {
+          const f16x8 xf = *(const f16x8 *)(cur + (32 * j + (lane & 31)) * PITCH + ko);
+          acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(xf, wf, acc[j], 0, 0, 0);
+        }
+      }
+    }
+    if (more) {
+      store_x<TN>(xs[(st + 1) & 1], xn);
+      ws = wn;
+    }
+    __syncthreads();
+  }
+
+  // D[token][row]: lane l holds row l%32, tokens 8(i/4) + 4(l/32) + i%4 of block j
+  if (my_row < p.n_out) {
+#pragma unroll
+    for (int j = 0; j < NB; j++) {
+#pragma unroll
+      for (int i = 0; i < 16; i++) {
+        const uint32_t tok = 32 * j + 8 * (i >> 2) + 4 * hh + (i & 3);
+        if (tok < n_tok) {
+          float *o = y + p.y_off + (size_t)yrow[tok] * p.y_stride + my_row;
+          *o = ACCUM ? *o + acc[j][i] : acc[j][i];
+        }
+      }
+    }
+  }
+}
+
+}  // namespace
+
+#define MM(T, A, M)                                                                          \
+  extern "C" __global__ __launch_bounds__(256) void matmul__##T##_##A##_##M(                 \
+      const uint4 *w, const uint16_t *wd, const float *x, float *y, const uint32_t *ctl,     \
+      MatmulPush p) {                                                                        \
+    matmul_body<T, A, M, 0>(w, wd, x, y, ctl, p);                                            \
+  }                                                                                          \
+  extern "C" __global__ __launch_bounds__(256) void matmul__##T##_##A##_##M##_1(             \
+      const uint4 *w, const uint16_t *wd, const f16 *x, float *y, const uint32_t *ctl,       \
+      MatmulPush p) {                                                                        \
+    matmul_body<T, A, M, 1>(w, wd, x, y, ctl, p);                                            \
+  }
+
+#define MM_TYPE(T) \
+  MM(T, 0, 0)      \
+  MM(T, 1, 0)      \
+  MM(T, 0, 1)      \
+  MM(T, 1, 1)
+
+MM_TYPE(0)
+MM_TYPE(1)
+MM_TYPE(2)

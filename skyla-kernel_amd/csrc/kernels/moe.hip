@@ -1,0 +1,205 @@
+// MoE top-k dispatch and the elementwise kernels around the expert matvec/matmul, gfx950.
+//
+// All of them address one f32 arena `a` (plus its u32 and f16 views); offsets are element
+// indices (arena.rs:85-113).  The arena's control words are ctl[0] = first token,
+// ctl[1] = position, ctl[2] = token count (engine.rs:119-123).
+#include "common.h"
+
+namespace {
+
+constexpr uint32_t MAX_SLOTS = 1024;  // moe_sort.comp:15 (BATCH * n_used <= 1024)
+
+struct LogitsPush { uint32_t x_off, router_off, logits_off, n_embd, x_stride; };
+struct RoutePush { uint32_t logits_off, ids_off, weights_off, n_expert, n_used; };
+struct SortPush { uint32_t ids_off, table_off, list_off, n_expert, n_used; };
+struct CombinePush { uint32_t x_off, y_off, weights_off, n, stride, n_used; };
+struct SiluPush { uint32_t g_off, u_off, n, stride; };
+struct HalfPush { uint32_t src_off, dst_off, n, src_stride, dst_stride, per_token; };
+
+// Monotone u32 key of a float with -0 folded onto +0 (so equal values tie exactly as the
+// float comparisons of moe_route.comp:66-81 do).
+SK_DEV uint32_t order_key(float v) {
+  const uint32_t b = __builtin_bit_cast(uint32_t, v + 0.0f);
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+SK_DEV float key_value(uint32_t k) {
+  const uint32_t b = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
+  return __builtin_bit_cast(float, b);
+}
+
+SK_DEV uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) {
+    const uint64_t o = __shfl_xor(v, d, 64);
+    v = o > v ? o : v;
+  }
+  return v;
+}
+
+}  // namespace
+
+// moe_logits (moe_logits.comp:18-31): logits[tok * n_expert + e] = router_e . x_tok, one
+// workgroup of 256 threads per (expert, token); grid [n_expert, tokens, 1].
+extern "C" __global__ __launch_bounds__(256) void moe_logits(const float *w, const float *a,
+                                                              float *logits, LogitsPush p) {
+  __shared__ float part[4];
+  const uint32_t e = blockIdx.x, tok = blockIdx.y, tid = threadIdx.x;
+  const float4 *row = (const float4 *)(w + p.router_off + e * p.n_embd);
+  const float4 *x = (const float4 *)(a + p.x_off + tok * p.x_stride);
+  float s = 0.0f;
+  for (uint32_t i = tid; i < p.n_embd / 4; i += 256) {
+    const float4 r = row[i], v = x[i];
+    s += r.x * v.x + r.y * v.y + r.z * v.z + r.w * v.w;
+  }
+  s = group_sum<64>(s);
+  if ((tid & 63) == 0) part[tid >> 6] = s;
+  __syncthreads();
+  if (tid == 0) logits[p.logits_off + tok * gridDim.x + e] = part[0] + part[1] + part[2] + part[3];
+}
+
+// moe_route (moe_route.comp:55-106): per token, n_used rounds of "largest logit, lowest
+// index on ties", then weights exp(v_k - v_0) / sum.  One workgroup per token, expert t
+// held by thread t (n_expert <= 256); tokens at or beyond ctl[2] do nothing.
+extern "C" __global__ __launch_bounds__(256) void moe_route(float *a, uint32_t *ids, RoutePush p) {
+  __shared__ uint64_t wave_best[2][4];
+  __shared__ float chosen_value[16];
+  __shared__ uint32_t chosen_index[16];
+  const uint32_t tok = blockIdx.y;
+  const uint32_t n_tok = __builtin_bit_cast(uint32_t, a[2]);
+  if (tok >= n_tok) return;
+  const uint32_t t = threadIdx.x, wave = t >> 6;
+  const uint32_t n_used = min(p.n_used, 16u);
+  const uint32_t logits_off = p.logits_off + tok * p.n_expert;
+  // key = (value order, ~index): the u64 maximum is the largest value, lowest index
+  uint64_t key = 0;
+  if (t < p.n_expert) key = ((uint64_t)order_key(a[logits_off + t]) << 32) | (uint32_t)~t;
+  for (uint32_t k = 0; k < n_used; k++) {
+    const uint64_t m = wave_max_u64(key);
+    if ((t & 63) == 0) wave_best[k & 1][wave] = m;
+    __syncthreads();
+    uint64_t best = wave_best[k & 1][0];
+#pragma unroll
+    for (int v = 1; v < 4; v++) best = wave_best[k & 1][v] > best ? wave_best[k & 1][v] : best;
+    const uint32_t idx = ~(uint32_t)best;
+    if (t == 0) {
+      chosen_value[k] = key_value((uint32_t)(best >> 32));
+      chosen_index[k] = idx;
+    }
+    if (t == idx) key = 0;
+  }
+  __syncthreads();
+  if (t != 0) return;
+  const float largest = chosen_value[0];
+  float total = 0.0f;
+  for (uint32_t k = 0; k < n_used; k++) total += expf(chosen_value[k] - largest);
+  for (uint32_t k = 0; k < n_used; k++) {
+    ids[p.ids_off + tok * p.n_used + k] = chosen_index[k];
+    a[p.weights_off + tok * p.n_used + k] = expf(chosen_value[k] - largest) / total;
+  }
+}
+
+// moe_sort (moe_sort.comp:21-55): slot s = tok * n_used + k is routed to ids[s].  Writes
+// table[2e] = count, table[2e+1] = start (exclusive scan in expert order) and list[start +
+// rank] = s with rank = number of earlier slots of the same expert (stable).  One
+// workgroup; the ranking runs on wave 0, 64 slots at a time, using ballots to find the
+// lanes that share an expert.
+extern "C" __global__ __launch_bounds__(256) void moe_sort(uint32_t *a, SortPush p) {
+  __shared__ uint32_t count[256];
+  __shared__ uint32_t next[256];
+  const uint32_t t = threadIdx.x;
+  const uint32_t n = min(a[2] * p.n_used, MAX_SLOTS);
+  const uint32_t n_expert = min(p.n_expert, 256u);
+  count[t] = 0;
+  __syncthreads();
+  for (uint32_t i = t; i < n; i += 256) {
+    const uint32_t e = a[p.ids_off + i];
+    if (e < n_expert) atomicAdd(&count[e], 1u);
+  }
+  __syncthreads();
+  if (t < 64) {
+    // exclusive scan of count over 256 experts: 4 per lane, then a wave scan
+    uint32_t c[4], s = 0;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      c[j] = count[4 * t + j];
+      s += c[j];
+    }
+    uint32_t incl = s;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const uint32_t o = __shfl_up(incl, d, 64);
+      if (t >= (uint32_t)d) incl += o;
+    }
+    uint32_t run = incl - s;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const uint32_t e = 4 * t + j;
+      next[e] = run;
+      if (e < n_expert) {
+        a[p.table_off + 2 * e] = c[j];
+        a[p.table_off + 2 * e + 1] = run;
+      }
+      run += c[j];
+    }
+    const uint64_t below = (1ull << t) - 1;
+    for (uint32_t base = 0; base < n; base += 64) {
+      const uint32_t i = base + t;
+      const bool live = i < n;
+      const uint32_t e = live ? a[p.ids_off + i] : 0xffffffffu;
+      const bool ok = live && e < n_expert;
+      // lanes with the same expert: intersect the ballots of all 8 expert bits
+      uint64_t same = __ballot(ok);
+#pragma unroll
+      for (int b = 0; b < 8; b++) {
+        const uint64_t ones = __ballot(ok && ((e >> b) & 1u));
+        same &= ((e >> b) & 1u) ? ones : ~ones;
+      }
+      if (ok) {
+        const uint32_t rank = __popcll(same & below);
+        const uint32_t at = next[e] + rank;
+        a[p.list_off + at] = i;
+        // the highest lane of the group advances the expert's cursor
+        if ((same >> t) == 1ull) next[e] = at + 1;
+      }
+      // a single wave's LDS accesses complete in program order; the fence only keeps the
+      // compiler from moving the next step's cursor reads above these writes
+      __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    }
+  }
+}
+
+// moe_combine (moe_combine.comp:16-27): x[tok] += sum_s w[tok, s] * down[tok * n_used + s],
+// summed in route order from 0 as the oracle does (ffn.rs:67-74, model.rs:113-114).
+extern "C" __global__ __launch_bounds__(256) void moe_combine(float *a, CombinePush p) {
+#pragma clang fp contract(off)
+  const uint32_t i = blockIdx.x * 256 + threadIdx.x, tok = blockIdx.y;
+  if (i >= p.n) return;
+  float sum = 0.0f;
+  for (uint32_t s = 0; s < p.n_used; s++) {
+    const uint32_t slot = tok * p.n_used + s;
+    sum += a[p.weights_off + slot] * a[p.y_off + slot * p.stride + i];
+  }
+  a[p.x_off + tok * p.stride + i] += sum;
+}
+
+// silu_mul (silu_mul.comp:15-23): g <- g / (1 + e^-g) * u for tokens below ctl[2].
+extern "C" __global__ __launch_bounds__(256) void silu_mul(float *a, const uint32_t *ctl,
+                                                            SiluPush p) {
+  const uint32_t i = blockIdx.x * 256 + threadIdx.x, tok = blockIdx.y;
+  if (i >= p.n || tok >= ctl[2]) return;
+  const uint32_t g = p.g_off + tok * p.stride + i;
+  const float x = a[g];
+  a[g] = x / (1.0f + expf(-x)) * a[p.u_off + tok * p.stride + i];
+}
+
+// to_half (to_half.metal:13-28): f32 -> f16 copy of the GEMM input rows, 4 per thread,
+// rows below ctl[2] * per_token.
+extern "C" __global__ __launch_bounds__(256) void to_half(const float *a, f16 *h,
+                                                           const uint32_t *ctl, HalfPush p) {
+  const uint32_t i = (blockIdx.x * 256 + threadIdx.x) * 4, row = blockIdx.y;
+  if (i >= p.n || row >= ctl[2] * p.per_token) return;
+  const float4 v = *(const float4 *)(a + p.src_off + row * p.src_stride + i);
+  const f16x4 o = {(f16)v.x, (f16)v.y, (f16)v.z, (f16)v.w};
+  *(f16x4 *)(h + p.dst_off + row * p.dst_stride + i) = o;
+}

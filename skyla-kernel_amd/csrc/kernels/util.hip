@@ -1,0 +1,91 @@
+// Measurement and checking kernels.
+#include "common.h"
+
+struct BandwidthPush { uint32_t n_vec4; };
+
+// bandwidth (bandwidth.comp:1-23): grid-stride XOR stream over n_vec4 uint4; writes only
+// if the fold hits a fixed constant, which keeps the loads live.  Roofline probe for the
+// HBM-bound kernels.  spec [threads per workgroup].
+template <int THREADS>
+SK_DEV void bandwidth_body(const uint4 *src, uint32_t *dst, BandwidthPush p) {
+  const uint32_t gid = blockIdx.x * THREADS + threadIdx.x;
+  const uint32_t stride = gridDim.x * THREADS;
+  uint4 acc = make_uint4(0, 0, 0, 0);
+  uint32_t i = gid;
+  for (; i + 3 * stride < p.n_vec4; i += 4 * stride) {
+    const uint4 a = src[i], b = src[i + stride], c = src[i + 2 * stride], d = src[i + 3 * stride];
+    acc.x ^= a.x ^ b.x ^ c.x ^ d.x;
+    acc.y ^= a.y ^ b.y ^ c.y ^ d.y;
+    acc.z ^= a.z ^ b.z ^ c.z ^ d.z;
+    acc.w ^= a.w ^ b.w ^ c.w ^ d.w;
+  }
+  for (; i < p.n_vec4; i += stride) {
+    const uint4 a = src[i];
+    acc.x ^= a.x;
+    acc.y ^= a.y;
+    acc.z ^= a.z;
+    acc.w ^= a.w;
+  }
+  const uint32_t r = acc.x ^ acc.y ^ acc.z ^ acc.w;
+  if (r == 0x9e3779b9u) dst[gid] = r;
+}
+
+#define BW(T)                                                                               \
+  extern "C" __global__ __launch_bounds__(T) void bandwidth__##T(const uint4 *src,          \
+                                                                 uint32_t *dst,             \
+                                                                 BandwidthPush p) {         \
+    bandwidth_body<T>(src, dst, p);                                                         \
+  }
+BW(64)
+BW(128)
+BW(256)
+BW(512)
+BW(1024)
+
+// dequant: the bit-exact dequantisation the path's arithmetic is judged against
+// (quant.rs:5-89), run on the GPU over planner regions.  One thread per 32-value group,
+// output row-major f32: y[y_off + row * n_in + k].  spec [TYPE] (0/1/2 = Q8_0/Q4_K/Q6_K).
+// Push: o0..o3 region offsets (as the matmul push), n_in, n_rows, y_off.
+struct DequantPush { uint32_t o0, o1, o2, o3, n_in, n_rows, y_off; };
+
+template <int TYPE>
+SK_DEV void dequant_body(const uint4 *w, const uint16_t *wd, float *y, DequantPush p) {
+  const uint32_t groups = p.n_in >> 5;
+  const uint32_t gid = blockIdx.x * 256 + threadIdx.x;
+  if (gid >= groups * p.n_rows) return;
+  const uint32_t row = gid / groups, gi = gid % groups;
+  float o[32];
+  uint32_t first;
+  if (TYPE == 1) {
+    const uint32_t sb = gi >> 3, sub = gi & 7;
+    const uint32_t rs = row * (p.n_in >> 8) + sb;
+    const uint4 *qs = w + p.o0 + rs * 8 + (sub >> 1) * 2;
+    dequant_q4k_sub(w[p.o1 + rs], qs[0], qs[1], sub, o);
+    first = sb * 256 + (sub >> 1) * 64 + (sub & 1) * 32;
+  } else if (TYPE == 2) {
+    const uint32_t sb = gi >> 3, hf = (gi >> 2) & 1, g = gi & 3;
+    const uint32_t rs = row * (p.n_in >> 8) + sb;
+    uint4 ql[4], qh[2];
+    for (int i = 0; i < 4; i++) ql[i] = w[p.o0 + rs * 8 + hf * 4 + i];
+    for (int i = 0; i < 2; i++) qh[i] = w[p.o1 + rs * 4 + hf * 2 + i];
+    dequant_q6k_group(ql, qh, w[p.o2 + rs], f16_bits_to_f32(wd[p.o3 + rs]), hf, g, o);
+    first = sb * 256 + hf * 128 + g * 32;
+  } else {
+    const uint4 *q = w + p.o0 + row * (p.n_in >> 4) + gi * 2;
+    dequant_q8_0_block(q[0], q[1], f16_bits_to_f32(wd[p.o1 + row * groups + gi]), o);
+    first = gi * 32;
+  }
+  float4 *dst = (float4 *)(y + p.y_off + (size_t)row * p.n_in + first);
+#pragma unroll
+  for (int i = 0; i < 8; i++) dst[i] = make_float4(o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]);
+}
+
+#define DQ(T)                                                                                \
+  extern "C" __global__ __launch_bounds__(256) void dequant__##T(const uint4 *w,              \
+                                                                  const uint16_t *wd,        \
+                                                                  float *y, DequantPush p) {  \
+    dequant_body<T>(w, wd, y, p);                                                            \
+  }
+DQ(0)
+DQ(1)
+DQ(2)

@@ -1,0 +1,664 @@
+// Host runtime of the gfx950 backend: the implementation of include/skyla_hip.h.
+//
+// It plays the role skyla-vk (Vulkan) and skyla-metal (Metal) play for skyla-engine
+// (skyla-engine/src/backend.rs:1-19): contexts, buffers, pipelines, recordings.
+//   * Kernels are compiled ahead of time for gfx950 into code objects that are linked
+//     into this library and loaded with hipModuleLoadData; a pipeline resolves the
+//     (shader name, spec constants) pair to the exported symbol name__s0_s1_.. with
+//     hipModuleGetFunction, and launches it with hipModuleLaunchKernel.
+//   * A recording is a launch list.  Replaying it launches one HIP graph (built once by
+//     capturing the list on the context stream), so a decode step costs one submission
+//     instead of one per kernel; a profiled recording replays eagerly with a HIP event
+//     after every mark.
+//   * Buffers are HBM allocations with a host mirror that the caller synchronises
+//     explicitly (the reference's buffers are host-coherent; a discrete GPU's are not).
+#include "../../../include/skyla_hip.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <memory>
+#include <string>
+#include <vector>
+
+// Code objects embedded by embed.S.
+extern "C" const unsigned char skyla_co_matvec[], skyla_co_matvec_end[];
+extern "C" const unsigned char skyla_co_matmul[], skyla_co_matmul_end[];
+extern "C" const unsigned char skyla_co_moe[], skyla_co_moe_end[];
+extern "C" const unsigned char skyla_co_util[], skyla_co_util_end[];
+
+namespace {
+
+thread_local std::string g_error;
+
+int fail(int code, const char *fmt, ...) {
+  char buf[1024];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_error = buf;
+  return code;
+}
+
+#define HIP_TRY(call)                                                                       \
+  do {                                                                                      \
+    hipError_t e_ = (call);                                                                 \
+    if (e_ != hipSuccess)                                                                   \
+      return fail(SKYLA_HIP_E_DEVICE, "%s failed: %s", #call, hipGetErrorString(e_));       \
+  } while (0)
+
+constexpr uint64_t kMaxBuffer = 4ull << 30;  // keeps u32 element offsets valid
+constexpr uint32_t kMaxMarks = 2048;          // skyla-vk/src/record.rs:6
+
+// Bindings, push words and workgroup shape of every kernel the engine creates
+// (kernels.rs:170-205; workgroup shapes as skyla-metal/src/pipeline.rs:14-24).
+struct KernelInfo {
+  const char *name;
+  uint32_t n_buffers;
+  uint32_t push_words;
+  uint32_t spec_len_min, spec_len_max;
+  int threads_from_spec;  // -1: fixed 256; k >= 0: 64 * spec[k] (matvec waves) or spec[k]
+  bool waves;
+};
+
+const KernelInfo kKernels[] = {
+    {"matvec_q4k", 4, 9, 5, 5, 0, true},
+    {"matvec_q6k", 5, 11, 5, 5, 0, true},
+    {"matvec_q8_0", 5, 9, 5, 5, 0, true},
+    {"matmul", 5, 13, 3, 4, -1, false},
+    {"moe_logits", 3, 5, 0, 0, -1, false},
+    {"moe_route", 2, 5, 0, 0, -1, false},
+    {"moe_sort", 1, 5, 0, 0, -1, false},
+    {"moe_combine", 1, 6, 0, 0, -1, false},
+    {"silu_mul", 2, 4, 0, 0, -1, false},
+    {"to_half", 3, 6, 0, 0, -1, false},
+    {"bandwidth", 2, 1, 1, 1, 0, false},
+    {"dequant", 3, 7, 1, 1, -1, false},
+};
+
+const KernelInfo *find_kernel(const char *name) {
+  for (const auto &k : kKernels)
+    if (std::strcmp(k.name, name) == 0) return &k;
+  return nullptr;
+}
+
+}  // namespace
+
+struct skyla_hip_context {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  std::vector<hipModule_t> modules;
+  std::string name;
+  uint32_t warp = 64;
+};
+
+struct skyla_hip_buffer {
+  skyla_hip_context *ctx = nullptr;
+  void *dev = nullptr;
+  std::unique_ptr<unsigned char[]> host;
+  uint64_t size = 0;
+};
+
+struct skyla_hip_pipeline {
+  skyla_hip_context *ctx = nullptr;
+  std::string symbol;
+  hipFunction_t fn = nullptr;
+  uint32_t n_buffers = 0;
+  uint32_t push_words = 0;
+  uint32_t threads = 256;
+  std::vector<std::vector<void *>> sets;
+};
+
+namespace {
+
+struct Command {
+  enum Kind { Dispatch, Barrier, Mark } kind;
+  hipFunction_t fn = nullptr;
+  uint32_t threads = 0;
+  uint32_t groups[3] = {0, 0, 0};
+  std::vector<void *> bufs;
+  std::vector<uint32_t> push;
+  std::string label;
+};
+
+int launch(hipStream_t stream, const Command &c) {
+  // kernel parameters: binding pointers in order, then the push struct by value
+  std::vector<void *> params;
+  params.reserve(c.bufs.size() + 1);
+  for (void *const &p : c.bufs) params.push_back(const_cast<void **>(&p));
+  params.push_back(const_cast<uint32_t *>(c.push.data()));
+  HIP_TRY(hipModuleLaunchKernel(c.fn, c.groups[0], c.groups[1], c.groups[2], c.threads, 1, 1, 0,
+                                stream, params.data(), nullptr));
+  return SKYLA_HIP_OK;
+}
+
+}  // namespace
+
+struct skyla_hip_recorder {
+  skyla_hip_context *ctx = nullptr;
+  bool profile = false;
+  std::vector<Command> cmds;
+  int status = SKYLA_HIP_OK;
+  std::string error;
+  uint32_t marks = 0;
+};
+
+struct skyla_hip_recording {
+  skyla_hip_context *ctx = nullptr;
+  bool profile = false;
+  std::vector<Command> cmds;
+  hipGraphExec_t exec = nullptr;
+  hipGraph_t graph = nullptr;
+  std::vector<std::string> labels;
+  std::vector<double> mark_ns;
+  bool replayed = false;
+};
+
+extern "C" {
+
+const char *skyla_hip_last_error(void) { return g_error.c_str(); }
+
+int skyla_hip_context_new(int device, skyla_hip_context **out) {
+  if (!out) return fail(SKYLA_HIP_E_ARG, "context_new: null output");
+  *out = nullptr;
+  int count = 0;
+  hipError_t e = hipGetDeviceCount(&count);
+  if (e != hipSuccess || count == 0)
+    return fail(SKYLA_HIP_E_DEVICE, "no HIP device available (%s)",
+                e == hipSuccess ? "0 devices" : hipGetErrorString(e));
+  if (device < 0) {
+    const char *env = std::getenv("SKYLA_DEVICE");  // skyla-vk/src/context.rs:50-55
+    device = env ? std::atoi(env) : 0;
+  }
+  if (device < 0 || device >= count)
+    return fail(SKYLA_HIP_E_ARG, "device %d out of range (%d devices)", device, count);
+  auto ctx = std::make_unique<skyla_hip_context>();
+  ctx->device = device;
+  HIP_TRY(hipSetDevice(device));
+  hipDeviceProp_t prop;
+  HIP_TRY(hipGetDeviceProperties(&prop, device));
+  if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+    return fail(SKYLA_HIP_E_DEVICE, "device %d is %s; this backend carries gfx950 code only",
+                device, prop.gcnArchName);
+  ctx->name = prop.name;
+  ctx->warp = (uint32_t)prop.warpSize;
+  HIP_TRY(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking));
+  const unsigned char *images[] = {skyla_co_matvec, skyla_co_matmul, skyla_co_moe, skyla_co_util};
+  for (const unsigned char *img : images) {
+    hipModule_t m = nullptr;
+    hipError_t le = hipModuleLoadData(&m, img);
+    if (le != hipSuccess) {
+      skyla_hip_context_free(ctx.release());
+      return fail(SKYLA_HIP_E_DEVICE, "hipModuleLoadData: %s", hipGetErrorString(le));
+    }
+    ctx->modules.push_back(m);
+  }
+  *out = ctx.release();
+  return SKYLA_HIP_OK;
+}
+
+void skyla_hip_context_free(skyla_hip_context *ctx) {
+  if (!ctx) return;
+  hipSetDevice(ctx->device);
+  if (ctx->stream) hipStreamSynchronize(ctx->stream);
+  for (hipModule_t m : ctx->modules) hipModuleUnload(m);
+  if (ctx->stream) hipStreamDestroy(ctx->stream);
+  delete ctx;
+}
+
+uint32_t skyla_hip_subgroup_size(const skyla_hip_context *ctx) { return ctx ? ctx->warp : 0; }
+
+uint64_t skyla_hip_max_buffer(const skyla_hip_context *ctx) { return ctx ? kMaxBuffer : 0; }
+
+int skyla_hip_device_name(const skyla_hip_context *ctx, char *out, size_t cap) {
+  if (!ctx || !out || cap == 0) return fail(SKYLA_HIP_E_ARG, "device_name: bad argument");
+  std::snprintf(out, cap, "%s", ctx->name.c_str());
+  return SKYLA_HIP_OK;
+}
+
+int skyla_hip_alloc(skyla_hip_context *ctx, uint64_t size, skyla_hip_buffer **out) {
+  if (!ctx || !out) return fail(SKYLA_HIP_E_ARG, "alloc: bad argument");
+  *out = nullptr;
+  if (size == 0) return fail(SKYLA_HIP_E_ARG, "alloc: zero-sized buffer");
+  if (size > kMaxBuffer)
+    return fail(SKYLA_HIP_E_OOM, "alloc: %llu bytes is above the %llu-byte buffer cap",
+                (unsigned long long)size, (unsigned long long)kMaxBuffer);
+  HIP_TRY(hipSetDevice(ctx->device));
+  auto b = std::make_unique<skyla_hip_buffer>();
+  b->ctx = ctx;
+  b->size = size;
+  hipError_t e = hipMalloc(&b->dev, size);
+  if (e != hipSuccess)
+    return fail(SKYLA_HIP_E_OOM, "hipMalloc(%llu): %s", (unsigned long long)size,
+                hipGetErrorString(e));
+  e = hipMemsetAsync(b->dev, 0, size, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) {
+    hipFree(b->dev);
+    return fail(SKYLA_HIP_E_DEVICE, "clearing a new buffer: %s", hipGetErrorString(e));
+  }
+  *out = b.release();
+  return SKYLA_HIP_OK;
+}
+
+void skyla_hip_buffer_free(skyla_hip_buffer *buf) {
+  if (!buf) return;
+  hipSetDevice(buf->ctx->device);
+  hipStreamSynchronize(buf->ctx->stream);
+  hipFree(buf->dev);
+  delete buf;
+}
+
+uint64_t skyla_hip_buffer_size(const skyla_hip_buffer *buf) { return buf ? buf->size : 0; }
+
+void *skyla_hip_buffer_host(skyla_hip_buffer *buf) {
+  if (!buf) {
+    fail(SKYLA_HIP_E_ARG, "buffer_host: null buffer");
+    return nullptr;
+  }
+  if (!buf->host) {
+    buf->host.reset(new (std::nothrow) unsigned char[buf->size]);
+    if (!buf->host) {
+      fail(SKYLA_HIP_E_OOM, "buffer_host: cannot allocate %llu host bytes",
+           (unsigned long long)buf->size);
+      return nullptr;
+    }
+    std::memset(buf->host.get(), 0, buf->size);
+  }
+  return buf->host.get();
+}
+
+static int check_range(const skyla_hip_buffer *buf, uint64_t off, uint64_t len, const char *what) {
+  if (!buf) return fail(SKYLA_HIP_E_ARG, "%s: null buffer", what);
+  if (off > buf->size || len > buf->size - off)
+    return fail(SKYLA_HIP_E_ARG, "%s: range [%llu, +%llu) outside a %llu-byte buffer", what,
+                (unsigned long long)off, (unsigned long long)len, (unsigned long long)buf->size);
+  return SKYLA_HIP_OK;
+}
+
+int skyla_hip_buffer_upload(skyla_hip_buffer *buf, uint64_t off, uint64_t len) {
+  int s = check_range(buf, off, len, "buffer_upload");
+  if (s) return s;
+  if (!skyla_hip_buffer_host(buf)) return SKYLA_HIP_E_OOM;
+  HIP_TRY(hipSetDevice(buf->ctx->device));
+  HIP_TRY(hipMemcpyAsync((char *)buf->dev + off, buf->host.get() + off, len,
+                         hipMemcpyHostToDevice, buf->ctx->stream));
+  HIP_TRY(hipStreamSynchronize(buf->ctx->stream));
+  return SKYLA_HIP_OK;
+}
+
+int skyla_hip_buffer_download(skyla_hip_buffer *buf, uint64_t off, uint64_t len) {
+  int s = check_range(buf, off, len, "buffer_download");
+  if (s) return s;
+  if (!skyla_hip_buffer_host(buf)) return SKYLA_HIP_E_OOM;
+  HIP_TRY(hipSetDevice(buf->ctx->device));
+  HIP_TRY(hipMemcpyAsync(buf->host.get() + off, (char *)buf->dev + off, len,
+                         hipMemcpyDeviceToHost, buf->ctx->stream));
+  HIP_TRY(hipStreamSynchronize(buf->ctx->stream));
+  return SKYLA_HIP_OK;
+}
+
+void *skyla_hip_buffer_device(skyla_hip_buffer *buf) { return buf ? buf->dev : nullptr; }
+
+int skyla_hip_buffer_copy(skyla_hip_buffer *dst, uint64_t dst_off, const skyla_hip_buffer *src,
+                          uint64_t src_off, uint64_t len) {
+  int s = check_range(dst, dst_off, len, "buffer_copy dst");
+  if (s) return s;
+  s = check_range(src, src_off, len, "buffer_copy src");
+  if (s) return s;
+  HIP_TRY(hipSetDevice(dst->ctx->device));
+  HIP_TRY(hipMemcpyAsync((char *)dst->dev + dst_off, (const char *)src->dev + src_off, len,
+                         hipMemcpyDeviceToDevice, dst->ctx->stream));
+  HIP_TRY(hipStreamSynchronize(dst->ctx->stream));
+  return SKYLA_HIP_OK;
+}
+
+int skyla_hip_pipeline_new(skyla_hip_context *ctx, const char *name, uint32_t n_buffers,
+                           uint32_t push_size, const uint32_t *spec, uint32_t n_spec,
+                           uint32_t n_sets, skyla_hip_pipeline **out) {
+  if (!ctx || !name || !out || (n_spec && !spec))
+    return fail(SKYLA_HIP_E_ARG, "pipeline_new: bad argument");
+  *out = nullptr;
+  const KernelInfo *k = find_kernel(name);
+  if (!k) return fail(SKYLA_HIP_E_NO_KERNEL, "no gfx950 kernel named %s", name);
+  if (n_spec < k->spec_len_min || n_spec > k->spec_len_max)
+    return fail(SKYLA_HIP_E_NO_KERNEL, "%s takes %u..%u spec constants, got %u", name,
+                k->spec_len_min, k->spec_len_max, n_spec);
+  if (n_buffers != k->n_buffers)
+    return fail(SKYLA_HIP_E_ARG, "%s binds %u buffers, pipeline asks for %u", name,
+                k->n_buffers, n_buffers);
+  if (push_size != 4 * k->push_words)
+    return fail(SKYLA_HIP_E_ARG, "%s takes %u push bytes, pipeline asks for %u", name,
+                4 * k->push_words, push_size);
+  if (n_sets == 0) n_sets = 1;
+  // symbol: name__s0_s1_...; matmul's trailing X_HALF = 0 is the plain variant
+  uint32_t n_key = n_spec;
+  if (std::strcmp(name, "matmul") == 0 && n_spec == 4 && spec[3] == 0) n_key = 3;
+  std::string sym = name;
+  for (uint32_t i = 0; i < n_key; i++) sym += (i ? "_" : "__") + std::to_string(spec[i]);
+  uint32_t threads = 256;
+  if (k->threads_from_spec >= 0)
+    threads = k->waves ? 64 * spec[k->threads_from_spec] : spec[k->threads_from_spec];
+  auto p = std::make_unique<skyla_hip_pipeline>();
+  p->ctx = ctx;
+  p->symbol = sym;
+  p->n_buffers = n_buffers;
+  p->push_words = k->push_words;
+  p->threads = threads;
+  p->sets.assign(n_sets, std::vector<void *>(n_buffers, nullptr));
+  HIP_TRY(hipSetDevice(ctx->device));
+  for (hipModule_t m : ctx->modules) {
+    hipFunction_t fn = nullptr;
+    if (hipModuleGetFunction(&fn, m, sym.c_str()) == hipSuccess && fn) {
+      p->fn = fn;
+      break;
+    }
+  }
+  (void)hipGetLastError();  // lookups that missed leave a sticky error behind
+  if (!p->fn)
+    return fail(SKYLA_HIP_E_NO_KERNEL, "no gfx950 kernel %s for this spec", sym.c_str());
+  int max_threads = 0;
+  if (hipFuncGetAttribute(&max_threads, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, p->fn) ==
+          hipSuccess &&
+      max_threads > 0 && threads > (uint32_t)max_threads)
+    return fail(SKYLA_HIP_E_NO_KERNEL, "%s: %u threads above its limit %d", sym.c_str(),
+                threads, max_threads);
+  *out = p.release();
+  return SKYLA_HIP_OK;
+}
+
+void skyla_hip_pipeline_free(skyla_hip_pipeline *p) { delete p; }
+
+int skyla_hip_pipeline_bind(skyla_hip_pipeline *p, uint32_t set, skyla_hip_buffer *const *bufs,
+                            uint32_t n) {
+  if (!p || (n && !bufs)) return fail(SKYLA_HIP_E_ARG, "pipeline_bind: bad argument");
+  if (set >= p->sets.size())
+    return fail(SKYLA_HIP_E_ARG, "pipeline_bind: set %u of %zu", set, p->sets.size());
+  if (n != p->n_buffers)
+    return fail(SKYLA_HIP_E_ARG, "pipeline_bind: %s binds %u buffers, got %u",
+                p->symbol.c_str(), p->n_buffers, n);
+  for (uint32_t i = 0; i < n; i++) {
+    if (!bufs[i]) return fail(SKYLA_HIP_E_ARG, "pipeline_bind: binding %u is null", i);
+    if (bufs[i]->ctx != p->ctx)
+      return fail(SKYLA_HIP_E_ARG, "pipeline_bind: binding %u belongs to another context", i);
+  }
+  for (uint32_t i = 0; i < n; i++) p->sets[set][i] = bufs[i]->dev;
+  return SKYLA_HIP_OK;
+}
+
+int skyla_hip_pipeline_threads(const skyla_hip_pipeline *p, uint32_t out[3]) {
+  if (!p || !out) return fail(SKYLA_HIP_E_ARG, "pipeline_threads: bad argument");
+  out[0] = p->threads;
+  out[1] = 1;
+  out[2] = 1;
+  return SKYLA_HIP_OK;
+}
+
+int skyla_hip_record_begin(skyla_hip_context *ctx, int profile, skyla_hip_recorder **out) {
+  if (!ctx || !out) return fail(SKYLA_HIP_E_ARG, "record_begin: bad argument");
+  auto r = new (std::nothrow) skyla_hip_recorder();
+  if (!r) return fail(SKYLA_HIP_E_OOM, "record_begin: out of memory");
+  r->ctx = ctx;
+  r->profile = profile != 0;
+  *out = r;
+  return SKYLA_HIP_OK;
+}
+
+static int record_fail(skyla_hip_recorder *r, int code) {
+  if (r->status == SKYLA_HIP_OK) {
+    r->status = code;
+    r->error = g_error;
+  }
+  return code;
+}
+
+int skyla_hip_record_dispatch(skyla_hip_recorder *r, const skyla_hip_pipeline *p, uint32_t set,
+                              const uint32_t groups[3], const uint32_t *push, uint32_t n_push) {
+  if (!r) return fail(SKYLA_HIP_E_ARG, "record_dispatch: null recorder");
+  if (!p || !groups || (n_push && !push))
+    return record_fail(r, fail(SKYLA_HIP_E_ARG, "record_dispatch: bad argument"));
+  if (p->ctx != r->ctx)
+    return record_fail(r, fail(SKYLA_HIP_E_ARG, "record_dispatch: pipeline of another context"));
+  if (set >= p->sets.size())
+    return record_fail(r, fail(SKYLA_HIP_E_ARG, "record_dispatch: set %u of %zu", set,
+                               p->sets.size()));
+  if (n_push != p->push_words)
+    return record_fail(r, fail(SKYLA_HIP_E_ARG, "record_dispatch: %s takes %u push words, got %u",
+                               p->symbol.c_str(), p->push_words, n_push));
+  for (void *b : p->sets[set])
+    if (!b)
+      return record_fail(r, fail(SKYLA_HIP_E_STATE, "record_dispatch: %s set %u is not bound",
+                                 p->symbol.c_str(), set));
+  Command c;
+  c.kind = Command::Dispatch;
+  c.fn = p->fn;
+  c.threads = p->threads;
+  for (int i = 0; i < 3; i++) c.groups[i] = groups[i];
+  c.bufs = p->sets[set];
+  c.push.assign(push, push + n_push);
+  if (groups[0] && groups[1] && groups[2]) r->cmds.push_back(std::move(c));
+  return SKYLA_HIP_OK;
+}
+
+int skyla_hip_record_barrier(skyla_hip_recorder *r) {
+  if (!r) return fail(SKYLA_HIP_E_ARG, "record_barrier: null recorder");
+  Command c;
+  c.kind = Command::Barrier;
+  r->cmds.push_back(std::move(c));
+  return SKYLA_HIP_OK;
+}
+
+int skyla_hip_record_host_barrier(skyla_hip_recorder *r) {
+  // replay waits for the stream, so host visibility needs no command of its own
+  return skyla_hip_record_barrier(r);
+}
+
+int skyla_hip_record_mark(skyla_hip_recorder *r, const char *label) {
+  if (!r) return fail(SKYLA_HIP_E_ARG, "record_mark: null recorder");
+  if (!r->profile) return SKYLA_HIP_OK;
+  if (r->marks + 1 >= kMaxMarks)
+    return record_fail(r, fail(SKYLA_HIP_E_STATE, "too many profiling marks"));
+  Command c;
+  c.kind = Command::Mark;
+  c.label = label ? label : "";
+  r->cmds.push_back(std::move(c));
+  r->marks++;
+  return SKYLA_HIP_OK;
+}
+
+int skyla_hip_record_end(skyla_hip_recorder *r, skyla_hip_recording **out) {
+  if (!r) return fail(SKYLA_HIP_E_ARG, "record_end: null recorder");
+  std::unique_ptr<skyla_hip_recorder> own(r);
+  if (!out) return fail(SKYLA_HIP_E_ARG, "record_end: null output");
+  *out = nullptr;
+  if (r->status != SKYLA_HIP_OK) {
+    g_error = "recording failed earlier: " + r->error;
+    return r->status;
+  }
+  auto rec = std::make_unique<skyla_hip_recording>();
+  rec->ctx = r->ctx;
+  rec->profile = r->profile;
+  rec->cmds = std::move(r->cmds);
+  for (const Command &c : rec->cmds)
+    if (c.kind == Command::Mark) rec->labels.push_back(c.label);
+  rec->mark_ns.assign(rec->labels.size(), 0.0);
+  if (!rec->profile && skyla_hip_recording_len(rec.get()) > 0) {
+    // One graph for the whole recording, captured from the launch list on the stream.
+    skyla_hip_context *ctx = rec->ctx;
+    HIP_TRY(hipSetDevice(ctx->device));
+    HIP_TRY(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+    int s = SKYLA_HIP_OK;
+    for (const Command &c : rec->cmds)
+      if (c.kind == Command::Dispatch && (s = launch(ctx->stream, c)) != SKYLA_HIP_OK) break;
+    hipGraph_t graph = nullptr;
+    hipError_t e = hipStreamEndCapture(ctx->stream, &graph);
+    if (s != SKYLA_HIP_OK) {
+      if (graph) hipGraphDestroy(graph);
+      return s;
+    }
+    if (e != hipSuccess)
+      return fail(SKYLA_HIP_E_DEVICE, "hipStreamEndCapture: %s", hipGetErrorString(e));
+    rec->graph = graph;
+    if (graph) {
+      e = hipGraphInstantiate(&rec->exec, graph, nullptr, nullptr, 0);
+      if (e != hipSuccess) {
+        hipGraphDestroy(graph);
+        rec->graph = nullptr;
+        return fail(SKYLA_HIP_E_DEVICE, "hipGraphInstantiate: %s", hipGetErrorString(e));
+      }
+    }
+  }
+  *out = rec.release();
+  return SKYLA_HIP_OK;
+}
+
+void skyla_hip_recording_free(skyla_hip_recording *rec) {
+  if (!rec) return;
+  hipSetDevice(rec->ctx->device);
+  hipStreamSynchronize(rec->ctx->stream);
+  if (rec->exec) hipGraphExecDestroy(rec->exec);
+  if (rec->graph) hipGraphDestroy(rec->graph);
+  delete rec;
+}
+
+uint32_t skyla_hip_recording_len(const skyla_hip_recording *rec) {
+  if (!rec) return 0;
+  uint32_t n = 0;
+  for (const Command &c : rec->cmds) n += c.kind == Command::Dispatch;
+  return n;
+}
+
+namespace {
+
+// Launches a recording on the context stream.  With `events`, one event is recorded at
+// the start and one at every mark.
+static int submit(skyla_hip_context *ctx, const skyla_hip_recording *rec, std::vector<hipEvent_t> *events) {
+  if (rec->exec && !events) {
+    HIP_TRY(hipGraphLaunch(rec->exec, ctx->stream));
+    return SKYLA_HIP_OK;
+  }
+  if (events) HIP_TRY(hipEventRecord((*events)[0], ctx->stream));
+  size_t m = 1;
+  for (const Command &c : rec->cmds) {
+    if (c.kind == Command::Dispatch) {
+      int s = launch(ctx->stream, c);
+      if (s) return s;
+    } else if (c.kind == Command::Mark && events) {
+      HIP_TRY(hipEventRecord((*events)[m++], ctx->stream));
+    }
+  }
+  return SKYLA_HIP_OK;
+}
+
+struct Events {
+  std::vector<hipEvent_t> ev;
+  ~Events() {
+    for (hipEvent_t e : ev) hipEventDestroy(e);
+  }
+  int make(size_t n) {
+    ev.assign(n, nullptr);
+    for (auto &e : ev) HIP_TRY(hipEventCreate(&e));
+    return SKYLA_HIP_OK;
+  }
+};
+
+}  // namespace
+
+int skyla_hip_replay(skyla_hip_context *ctx, const skyla_hip_recording *rec) {
+  if (!ctx || !rec) return fail(SKYLA_HIP_E_ARG, "replay: bad argument");
+  if (rec->ctx != ctx) return fail(SKYLA_HIP_E_ARG, "replay: recording of another context");
+  HIP_TRY(hipSetDevice(ctx->device));
+  if (!rec->profile) {
+    int s = submit(ctx, rec, nullptr);
+    if (s) return s;
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    return SKYLA_HIP_OK;
+  }
+  Events e;
+  int s = e.make(rec->labels.size() + 1);
+  if (s) return s;
+  s = submit(ctx, rec, &e.ev);
+  if (s) return s;
+  HIP_TRY(hipStreamSynchronize(ctx->stream));
+  auto *mut = const_cast<skyla_hip_recording *>(rec);
+  for (size_t i = 0; i < rec->labels.size(); i++) {
+    float ms = 0.0f;
+    HIP_TRY(hipEventElapsedTime(&ms, e.ev[i], e.ev[i + 1]));
+    mut->mark_ns[i] = (double)ms * 1e6;
+  }
+  mut->replayed = true;
+  return SKYLA_HIP_OK;
+}
+
+int skyla_hip_replay_timed(skyla_hip_context *ctx, const skyla_hip_recording *rec, double *ns) {
+  if (!ctx || !rec || !ns) return fail(SKYLA_HIP_E_ARG, "replay_timed: bad argument");
+  if (rec->ctx != ctx) return fail(SKYLA_HIP_E_ARG, "replay_timed: recording of another context");
+  HIP_TRY(hipSetDevice(ctx->device));
+  Events e;
+  int s = e.make(2);
+  if (s) return s;
+  HIP_TRY(hipEventRecord(e.ev[0], ctx->stream));
+  s = submit(ctx, rec, nullptr);
+  if (s) return s;
+  HIP_TRY(hipEventRecord(e.ev[1], ctx->stream));
+  HIP_TRY(hipEventSynchronize(e.ev[1]));
+  float ms = 0.0f;
+  HIP_TRY(hipEventElapsedTime(&ms, e.ev[0], e.ev[1]));
+  *ns = (double)ms * 1e6;
+  return SKYLA_HIP_OK;
+}
+
+int skyla_hip_marks(skyla_hip_context *ctx, const skyla_hip_recording *rec, const char **labels,
+                    double *ns, uint32_t cap, uint32_t *count) {
+  if (!ctx || !rec || !count) return fail(SKYLA_HIP_E_ARG, "marks: bad argument");
+  if (!rec->profile) return fail(SKYLA_HIP_E_STATE, "recording was not profiled");
+  if (!rec->replayed) return fail(SKYLA_HIP_E_STATE, "profiled recording was not replayed");
+  *count = (uint32_t)rec->labels.size();
+  for (uint32_t i = 0; i < cap && i < rec->labels.size(); i++) {
+    if (labels) labels[i] = rec->labels[i].c_str();
+    if (ns) ns[i] = rec->mark_ns[i];
+  }
+  return SKYLA_HIP_OK;
+}
+
+int skyla_hip_time_dispatch(skyla_hip_context *ctx, const skyla_hip_pipeline *p,
+                            const uint32_t groups[3], const uint32_t *push, uint32_t n_push,
+                            uint32_t reps, double *ns_out) {
+  if (!ctx || !p || !groups || !ns_out || reps == 0)
+    return fail(SKYLA_HIP_E_ARG, "time_dispatch: bad argument");
+  if (n_push != p->push_words)
+    return fail(SKYLA_HIP_E_ARG, "time_dispatch: %s takes %u push words, got %u",
+                p->symbol.c_str(), p->push_words, n_push);
+  for (void *b : p->sets[0])
+    if (!b) return fail(SKYLA_HIP_E_STATE, "time_dispatch: %s is not bound", p->symbol.c_str());
+  HIP_TRY(hipSetDevice(ctx->device));
+  Command c;
+  c.kind = Command::Dispatch;
+  c.fn = p->fn;
+  c.threads = p->threads;
+  for (int i = 0; i < 3; i++) c.groups[i] = groups[i];
+  c.bufs = p->sets[0];
+  c.push.assign(push, push + n_push);
+  Events e;
+  int s = e.make(reps + 1);
+  if (s) return s;
+  HIP_TRY(hipEventRecord(e.ev[0], ctx->stream));
+  for (uint32_t i = 0; i < reps; i++) {
+    s = launch(ctx->stream, c);
+    if (s) return s;
+    HIP_TRY(hipEventRecord(e.ev[i + 1], ctx->stream));
+  }
+  HIP_TRY(hipStreamSynchronize(ctx->stream));
+  for (uint32_t i = 0; i < reps; i++) {
+    float ms = 0.0f;
+    HIP_TRY(hipEventElapsedTime(&ms, e.ev[i], e.ev[i + 1]));
+    ns_out[i] = (double)ms * 1e6;
+  }
+  return SKYLA_HIP_OK;
+}
+
+}  // extern "C"

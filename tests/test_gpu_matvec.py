@@ -1,0 +1,137 @@
+"""GPU parity of the decode matvec and the bit-exact dequantisation (through the C-ABI).
+
+Bar: dequantised weights bit-exact against the oracle (quant.rs restated); matvec within
+1e-2 relative L2 of the oracle's f32 Matrix::matvec (the kernels
+actually land near 1e-4, so a tighter 2e-3 regression guard is asserted too).
+"""
+import numpy as np
+import pytest
+
+from helpers import Setup, rel_l2
+from oracle import skyla_oracle as so
+from skyla_hip import engine as E
+from skyla_hip import synth
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-2
+GUARD = 2e-3   # what the f16-activation kernels must keep
+
+
+def _dequant_gpu(ctx, dtype, n_in, n_out, data):
+    s = Setup(ctx, [(dtype, n_in, n_out, data)], n_in, n_out, extra_f32=n_in * n_out)
+    try:
+        m = s.q[0]
+        ty = {E.DType.Q8_0: 0, E.DType.Q4K: 1, E.DType.Q6K: 2}[dtype]
+        p = ctx.create_pipeline("dequant", 3, 28, [ty])
+        p.bind_buffers([s.weights[0], s.weights[0], s.arena])
+        groups = n_out * n_in // 32
+        push = [m.off[0], m.off[1], m.off[2], m.off[3], n_in, n_out, s.extra_off]
+        rec = ctx.record(False, lambda r: r.dispatch(p, [-(-groups // 256), 1, 1], push))
+        ctx.replay(rec)
+        rec.free()
+        p.free()
+        s.arena.download()
+        return s.arena.as_f32()[s.extra_off: s.extra_off + n_in * n_out].copy()
+    finally:
+        s.free()
+
+
+@pytest.mark.parametrize("dtype,n_in,n_out", [
+    (E.DType.Q4K, 512, 48), (E.DType.Q6K, 512, 48), (E.DType.Q8_0, 96, 40), (E.DType.Q4K, 4096, 8),
+])
+def test_dequant_bit_exact(ctx, dtype, n_in, n_out):
+    data = synth.matrix("test-dequant", f"{dtype.name}", dtype, n_in, n_out)
+    got = _dequant_gpu(ctx, dtype, n_in, n_out, data)
+    want = so.dequantize(int(dtype), data, n_in * n_out)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+SMALL = [
+    (E.DType.Q4K, 256, 1), (E.DType.Q4K, 512, 37), (E.DType.Q4K, 2304, 64), (E.DType.Q4K, 768, 9),
+    (E.DType.Q6K, 256, 1), (E.DType.Q6K, 512, 37), (E.DType.Q6K, 2304, 64),
+    (E.DType.Q8_0, 32, 1), (E.DType.Q8_0, 96, 13), (E.DType.Q8_0, 1024, 70),
+]
+
+
+@pytest.mark.parametrize("dtype,n_in,n_out", SMALL)
+@pytest.mark.parametrize("accum", [False, True])
+def test_matvec_small(ctx, dtype, n_in, n_out, accum):
+    data = synth.matrix("test-matvec", f"{dtype.name}-{n_in}-{n_out}", dtype, n_in, n_out)
+    x = synth.activations("test-matvec", f"x-{n_in}", n_in)
+    y0 = synth.activations("test-matvec", f"y0-{n_out}", n_out) if accum else np.zeros(n_out, np.float32)
+    s = Setup(ctx, [(dtype, n_in, n_out, data)], n_in, n_out)
+    try:
+        s.set_x(x)
+        s.set_y(y0)
+        s.matvec(0, accum)
+        got = s.y(1, n_out)[0]
+    finally:
+        s.free()
+    want = so.matvec(int(dtype), data, n_in, n_out, x)
+    # ACCUM adds y0 on the GPU; judge the matvec part (y0 + dot may cancel)
+    err = rel_l2(got - y0, want)
+    assert err <= GUARD, err
+
+
+@pytest.mark.parametrize("tactic", [(1, 1), (1, 2), (2, 2), (2, 4), (4, 1), (4, 2), (4, 4), (8, 1), (8, 2)])
+def test_matvec_tactics(ctx, tactic):
+    """Every instantiated (waves, rows) tactic covers every row exactly once."""
+    n_in, n_out = 1024, 301
+    mats = [(E.DType.Q4K, n_in, n_out, synth.matrix("tac", "q4k", E.DType.Q4K, n_in, n_out)),
+            (E.DType.Q6K, n_in, n_out, synth.matrix("tac", "q6k", E.DType.Q6K, n_in, n_out)),
+            (E.DType.Q8_0, n_in, n_out, synth.matrix("tac", "q8", E.DType.Q8_0, n_in, n_out))]
+    x = synth.activations("tac", "x", n_in)
+    s = Setup(ctx, mats, n_in, n_out, kquant_tactic=tactic, q8_0_tactic=tactic)
+    try:
+        s.set_x(x)
+        for i, (dt, _, _, data) in enumerate(mats):
+            s.set_y(np.full(n_out, np.nan, np.float32))
+            s.matvec(i)
+            got = s.y(1, n_out)[0]
+            want = so.matvec(int(dt), data, n_in, n_out, x)
+            assert rel_l2(got, want) <= GUARD, (dt, tactic)
+    finally:
+        s.free()
+
+
+# config 2: the Qwen3-8B decode shapes
+QWEN3_8B = [
+    ("q", E.DType.Q4K, 4096, 4096), ("k", E.DType.Q4K, 4096, 1024), ("o", E.DType.Q4K, 4096, 4096),
+    ("gate", E.DType.Q4K, 4096, 12288), ("down", E.DType.Q6K, 12288, 4096),
+    ("down_q4k", E.DType.Q4K, 12288, 4096),
+]
+
+
+@pytest.mark.parametrize("name,dtype,n_in,n_out", QWEN3_8B)
+def test_matvec_qwen3_8b_shapes(ctx, name, dtype, n_in, n_out):
+    data = synth.matrix("qwen3-8b", name, dtype, n_in, n_out)
+    x = synth.activations("qwen3-8b", f"x-{n_in}", n_in)
+    s = Setup(ctx, [(dtype, n_in, n_out, data)], n_in, n_out)
+    try:
+        s.set_x(x)
+        s.matvec(0)
+        got = s.y(1, n_out)[0]
+    finally:
+        s.free()
+    want = so.matvec(int(dtype), data, n_in, n_out, x)
+    err = rel_l2(got, want)
+    assert err <= TOL and err <= GUARD, err
+
+
+def test_matvec_linearity_full_size(ctx):
+    """Size-independent property at the full gate shape: A(x1 + x2) = A x1 + A x2."""
+    dtype, n_in, n_out = E.DType.Q4K, 4096, 12288
+    data = synth.matrix("qwen3-8b", "gate", dtype, n_in, n_out)
+    x1 = synth.activations("lin", "x1", n_in)
+    x2 = synth.activations("lin", "x2", n_in)
+    s = Setup(ctx, [(dtype, n_in, n_out, data)], n_in, n_out)
+    try:
+        outs = []
+        for x in (x1, x2, x1 + x2):
+            s.set_x(x)
+            s.matvec(0)
+            outs.append(s.y(1, n_out)[0].astype(np.float64))
+    finally:
+        s.free()
+    assert rel_l2(outs[2], outs[0] + outs[1]) <= GUARD
