@@ -1,0 +1,339 @@
+#!/usr/bin/env python3
+"""Benchmark of Skyla's quantized weight path on one MI355X.
+
+Workload (the config the headline metric is quoted on): the decode
+matvecs of Qwen3-8B, per layer Q 4096->4096, K and V 4096->1024, O 4096->4096 (ACCUM),
+gate and up 4096->12288 (all Q4_K) and down 12288->4096 (Q6_K, ACCUM), for all 36 layers.
+Each layer has its own copy of the weights in HBM (4.37 GB in total, 17x the 256 MB
+Infinity Cache), so every step streams the weights from HBM as a real decode token does.
+One step = one token's pass over the 36 layers = one replay of a recording of 252
+dispatches, issued exactly as skyla-engine's Graph::matvec issues them.
+
+value = algorithmic bytes of the step / step time, where algorithmic bytes per matvec =
+weight bytes + 4 n_in + 4 n_out (+ 4 n_out more for ACCUM's read of y).  Inputs are
+resident in HBM before timing starts.
+
+Also reported: matvec-only decode tok/s (1 / step time), the dominant kernel's roofline
+(matvec_q4k; average launch duration from HIP events on the launch stream), a measured HBM
+stream-read probe, the prefill GEMM at M = 512 (config 3) as TFLOP/s, and the CPU oracle
+(restatement of skyla-ref Matrix::matvec) timed on this host over a bounded sample.
+
+  python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "skyla-kernel_amd"))
+sys.path.insert(0, ROOT)
+
+import numpy as np  # noqa: E402
+
+from skyla_hip import engine as E  # noqa: E402
+from skyla_hip import synth  # noqa: E402
+from skyla_hip.abi import Context  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, vendor peak
+MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense FP16 MFMA, vendor peak
+
+CONFIG = "qwen3-8b"
+N_LAYER = 36
+N_EMBD, N_FF, N_KV = 4096, 12288, 1024
+# (name, dtype, n_in, n_out, accum)
+LAYER = [
+    ("q", E.DType.Q4K, N_EMBD, N_EMBD, False),
+    ("k", E.DType.Q4K, N_EMBD, N_KV, False),
+    ("v", E.DType.Q4K, N_EMBD, N_KV, False),
+    ("o", E.DType.Q4K, N_EMBD, N_EMBD, True),
+    ("gate", E.DType.Q4K, N_EMBD, N_FF, False),
+    ("up", E.DType.Q4K, N_EMBD, N_FF, False),
+    ("down", E.DType.Q6K, N_FF, N_EMBD, True),
+]
+
+
+def algo_bytes(dtype, n_in, n_out, accum) -> int:
+    return n_out * E.row_bytes(dtype, n_in) + 4 * n_in + 4 * n_out + (4 * n_out if accum else 0)
+
+
+class DecodeWorkload:
+    """36 layers of config-2 matvecs, laid out by the engine's planner."""
+
+    def __init__(self, ctx: Context, n_layer: int = N_LAYER, tactic=None):
+        self.ctx = ctx
+        self.data = {name: synth.matrix(CONFIG, name, dt, n_in, n_out) for name, dt, n_in, n_out, _ in LAYER}
+        planner = E.Planner(ctx.max_buffer())
+        self.layers = []
+        for _ in range(n_layer):
+            self.layers.append({name: planner.matrix(dt, n_in, n_out, self.data[name])
+                                for name, dt, n_in, n_out, _ in LAYER})
+        self.weights = E.upload_weights(ctx, planner)
+        self.weight_bytes = sum(b.size for b in self.weights)
+        # activation regions: n (4096), attn (4096), x (4096), q/k/v, gate/up (12288)
+        s_e, s_f = N_EMBD, N_FF
+        self.off = {}
+        o = 64
+        for name, width in [("n", s_e), ("attn", s_e), ("x", s_e), ("q", s_e), ("k", N_KV), ("v", N_KV),
+                            ("gate", s_f), ("up", s_f)]:
+            self.off[name] = o
+            o += width
+        self.arena = ctx.alloc_host(o * 4)
+        f = self.arena.as_f32()
+        g = synth.rng(CONFIG, "activations")
+        f[64:] = g.standard_normal(o - 64, dtype=np.float32)
+        self.arena.as_u32()[2] = 1
+        self.arena.upload()
+        self.k = E.Kernels(ctx, self.weights, self.arena, kquant_tactic=tactic)
+        self.step_bytes = n_layer * sum(algo_bytes(dt, n_in, n_out, acc) for _, dt, n_in, n_out, acc in LAYER)
+
+    def _layer(self, g: E.Graph, lw, only=None):
+        a = self.off
+        io = {"q": ("n", "q"), "k": ("n", "k"), "v": ("n", "v"), "o": ("attn", "x"),
+              "gate": ("n", "gate"), "up": ("n", "up"), "down": ("gate", "x")}
+        stages = [["q", "k", "v"], ["o"], ["gate", "up"], ["down"]]
+        for st in stages:
+            for name in st:
+                if only is not None and name not in only:
+                    continue
+                acc = name in ("o", "down")
+                xi, yo = io[name]
+                g.matvec(lw[name], (a[xi], 0), (a[yo], 0), acc, False)
+            g.r.barrier()
+
+    def record(self, only=None, profile=False):
+        def body(r):
+            g = E.Graph(r, self.k, None, None, False)
+            for lw in self.layers:
+                self._layer(g, lw, only)
+            r.host_barrier()
+        return self.ctx.record(profile, body)
+
+    def bytes_of(self, only) -> int:
+        return len(self.layers) * sum(algo_bytes(dt, n_in, n_out, acc) for name, dt, n_in, n_out, acc in LAYER
+                                      if name in only)
+
+    def free(self):
+        for b in self.weights:
+            b.free()
+        self.arena.free()
+
+
+def time_replays(ctx: Context, rec, warmup: int, steps: int) -> tuple[float, list[float]]:
+    """Wall seconds for `steps` synchronous replays, and per-replay device ns (HIP events)."""
+    for _ in range(warmup):
+        ctx.replay(rec)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        ctx.replay(rec)
+    wall = time.perf_counter() - t0
+    dev = [ctx.replay_timed(rec) for _ in range(max(3, min(steps, 10)))]
+    return wall, dev
+
+
+def hbm_probe(ctx: Context, gib: float = 2.0) -> float:
+    """Stream-read bandwidth of the bandwidth kernel (bandwidth.comp) over `gib` GiB."""
+    n_bytes = int(gib * (1 << 30)) // 16 * 16
+    src = ctx.alloc_host(n_bytes)
+    dst = ctx.alloc_host(1 << 20)
+    p = ctx.create_pipeline("bandwidth", 2, 4, [256])
+    p.bind_buffers([src, dst])
+    n_vec4 = n_bytes // 16
+    groups = 256 * 8 * 4
+    ns = ctx.time_dispatch(p, [groups, 1, 1], [n_vec4], 12)
+    p.free()
+    src.free()
+    dst.free()
+    best = min(ns[2:])
+    return n_bytes / best  # bytes per ns == GB/s
+
+
+def prefill_gemm(ctx: Context, m_tok: int = 512) -> dict:
+    """Config 3: Q4_K 4096x4096 and gate 4096x12288 at M = 512 f16 activations."""
+    out = {}
+    for name, dt, n_in, n_out in [("q", E.DType.Q4K, N_EMBD, N_EMBD), ("gate", E.DType.Q4K, N_EMBD, N_FF),
+                                  ("down", E.DType.Q6K, N_FF, N_EMBD)]:
+        data = synth.matrix(CONFIG, name, dt, n_in, n_out)
+        planner = E.Planner(ctx.max_buffer())
+        copies = 4
+        ms = [planner.matrix(dt, n_in, n_out, data) for _ in range(copies)]
+        weights = E.upload_weights(ctx, planner)
+        s_in, s_out = n_in, n_out
+        half_off = 64
+        y_off = half_off + (s_in * m_tok) // 2 + 64
+        arena = ctx.alloc_host((y_off + s_out * m_tok + 64) * 4)
+        h = arena.host().view("<f2")
+        x = synth.activations("qwen3-8b-prefill", f"x-{m_tok}-{n_in}", (m_tok, n_in)).astype(np.float16)
+        h[2 * half_off: 2 * half_off + x.size] = x.reshape(-1)
+        arena.as_u32()[2] = m_tok
+        arena.upload()
+        k = E.Kernels(ctx, weights, arena)
+        z = -(-m_tok // E.MATMUL_TILE_COLS)
+
+        def body(r, k=k, ms=ms):
+            g = E.Graph(r, k, None, None, True)
+            for i in range(8):
+                m = ms[i % copies]
+                g.matvec(m, (2 * half_off, s_in), (y_off, s_out), False, True, groups_z=z)
+        rec = ctx.record(False, body)
+        for _ in range(3):
+            ctx.replay(rec)
+        dev = min(ctx.replay_timed(rec) for _ in range(5)) / 8
+        flops = 2.0 * m_tok * n_in * n_out
+        out[name] = {"us": round(dev / 1e3, 2), "tflops": round(flops / dev / 1e3, 1),
+                     "mfma_frac": round(flops / dev / 1e3 / MFMA_F16_PEAK_TFLOPS, 4)}
+        rec.free()
+        for b in weights:
+            b.free()
+        arena.free()
+    return out
+
+
+def cpu_baseline(w: DecodeWorkload, budget_s: float = 12.0) -> dict:
+    """skyla-ref Matrix::matvec restated in C (oracle/), timed on this host: layer passes of
+    the same 7 matvecs until about budget_s seconds have elapsed."""
+    from oracle import skyla_oracle as so
+
+    threads = so.available_parallelism()
+    xs = {n_in: synth.activations(CONFIG, f"cpu-x-{n_in}", n_in) for n_in in (N_EMBD, N_FF)}
+    layer_bytes = sum(algo_bytes(dt, n_in, n_out, acc) for _, dt, n_in, n_out, acc in LAYER)
+    passes, t0 = 0, time.perf_counter()
+    while True:
+        for name, dt, n_in, n_out, _ in LAYER:
+            so.matvec(int(dt), w.data[name], n_in, n_out, xs[n_in], threads)
+        passes += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or passes >= 100:
+            break
+    gbs = passes * layer_bytes / el / 1e9
+    return {"value": round(gbs, 2), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{passes} passes over one Qwen3-8B layer's 7 decode matvecs "
+                      f"({layer_bytes / 1e6:.1f} MB each), {el:.1f} s; oracle/skyla_oracle.c "
+                      f"sk_matvec = skyla-ref Matrix::matvec (one thread per core, row dequant + "
+                      f"sequential f32 dot), -O2",
+            "tok_s_equiv": round(gbs * 1e9 / w.step_bytes, 3)}
+
+
+def parity_check(w: DecodeWorkload) -> float:
+    """rel-L2 of the GPU q matvec of layer 0 against the oracle (same inputs)."""
+    from oracle import skyla_oracle as so
+
+    ctx = w.ctx
+    rec = ctx.record(False, lambda r: E.Graph(r, w.k, None, None, False).matvec(
+        w.layers[0]["q"], (w.off["n"], 0), (w.off["q"], 0), False, False))
+    ctx.replay(rec)
+    rec.free()
+    w.arena.download()
+    f = w.arena.as_f32()
+    x = f[w.off["n"]: w.off["n"] + N_EMBD].copy()
+    got = f[w.off["q"]: w.off["q"] + N_EMBD].astype(np.float64)
+    want = so.matvec(int(E.DType.Q4K), w.data["q"], N_EMBD, N_EMBD, x).astype(np.float64)
+    return float(np.linalg.norm(got - want) / np.linalg.norm(want))
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--layers", type=int, default=N_LAYER)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the config-3 GEMM figures")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: every box of this build has a single MI355X, and "
+              f"the path shards across GPUs only by design (see DESIGN.md); got --gpus {args.gpus}",
+              file=sys.stderr)
+        return 2
+
+    def log(msg):
+        print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+    ctx = Context.new(0)
+    log(f"device {ctx.device_name()}; building {args.layers}-layer decode workload")
+    w = DecodeWorkload(ctx, args.layers)
+    log(f"{w.weight_bytes / 1e9:.2f} GB of weights in {len(w.weights)} buffers")
+    step = w.record()
+    wall, dev = time_replays(ctx, step, args.warmup, args.steps)
+    ms_per_step = wall / args.steps * 1e3
+    gbs = w.step_bytes / (wall / args.steps) / 1e9
+    dev_ms = float(np.median(dev)) / 1e6
+    log(f"step {ms_per_step:.3f} ms wall, {dev_ms:.3f} ms device; {gbs:.0f} GB/s")
+
+    # dominant kernel: matvec_q4k (Q, K, V, O, gate, up); events around its launches only
+    q4k_names = ("q", "k", "v", "o", "gate", "up")
+    rq = w.record(only=q4k_names)
+    _, dq = time_replays(ctx, rq, 3, 5)
+    n_launch = len(rq)
+    q4k_ns = float(np.median(dq)) / n_launch
+    q4k_bytes = w.bytes_of(q4k_names) / n_launch
+    rq.free()
+    rd = w.record(only=("down",))
+    _, dd = time_replays(ctx, rd, 3, 5)
+    q6k_ns = float(np.median(dd)) / len(rd)
+    q6k_bytes = w.bytes_of(("down",)) / len(rd)
+    rd.free()
+    achieved = q4k_bytes / q4k_ns  # GB/s
+    log(f"matvec_q4k avg {q4k_ns / 1e3:.2f} us/launch, {achieved:.0f} GB/s; "
+        f"matvec_q6k avg {q6k_ns / 1e3:.2f} us, {q6k_bytes / q6k_ns:.0f} GB/s")
+
+    parity = parity_check(w)
+    log(f"parity (q, layer 0) rel-L2 {parity:.2e}")
+    probe = hbm_probe(ctx)
+    log(f"HBM stream-read probe {probe:.0f} GB/s")
+    prefill = None if args.no_prefill else prefill_gemm(ctx)
+    if prefill:
+        log(f"prefill GEMM M=512: {prefill}")
+    cpu = None if args.no_cpu else cpu_baseline(w, args.cpu_seconds)
+    if cpu:
+        log(f"cpu baseline {cpu['value']} GB/s on {cpu['cores']} threads")
+
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "matvec_q4k_qwen3_8b_decode_traffic.json")
+    if os.path.exists(tpath):
+        with open(tpath) as fh:
+            traffic = json.load(fh).get("bytes_per_launch")
+
+    line = {
+        "metric": "Q4_K matvec HBM GB/s (% of peak) + decode tok/s, Qwen3-8B shapes, 1 GPU",
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16xf16->f32 over Q4_K/Q6_K blocks",
+        "data": "synthetic: seeded GGUF Q4_K/Q6_K blocks and N(0,1) f32 activations (config 2)",
+        "config": {"workload": "config 2: Qwen3-8B decode matvecs x 36 layers (Q,K,V,O,gate,up Q4_K; "
+                               "down Q6_K), one HBM copy of the weights per layer",
+                   "layers": args.layers, "dispatches_per_step": len(step),
+                   "weight_bytes": w.weight_bytes, "algorithmic_bytes_per_step": w.step_bytes},
+        "pct_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1),
+        "decode_tok_s_matvec_only": round(1e3 / ms_per_step, 1),
+        "device_ms_per_step": round(dev_ms, 4),
+        "roofline": {"bound": "hbm", "kernel": "matvec_q4k", "achieved": round(achieved, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": traffic, "algorithmic_bytes_per_launch": round(q4k_bytes),
+                     "avg_launch_us": round(q4k_ns / 1e3, 3)},
+        "matvec_q6k": {"avg_launch_us": round(q6k_ns / 1e3, 3), "gbs": round(q6k_bytes / q6k_ns, 1)},
+        "hbm_probe_gbs": round(probe, 1),
+        "parity_rel_l2": parity,
+        "prefill_gemm_m512": prefill,
+        "cpu_baseline": cpu,
+    }
+    step.free()
+    w.free()
+    ctx.free()
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -208,52 +208,87 @@ SK_DEV void step_scale(const WStage<TYPE> &s, int t, uint32_t hh, f16x2 &scale, 
 }
 
 // Activations of one stage: TN tokens x nk k, read by 256 threads as 8-k items (token
-// n = item / 32, k group g = item % 32), converted to f16 and pair-permuted per 8.
-template <int TN>
+// n = item / 32, k group g = item % 32).  f32 inputs are kept as f32 until the store so
+// the range guard below can rescale them; f16 inputs are staged as they are.
+template <int TN, int XHALF>
 struct XStage {
   static constexpr int ITEMS = TN * (KC / 8) / 256;
-  uint4 v[ITEMS];
+  float4 a[XHALF ? 1 : ITEMS], b[XHALF ? 1 : ITEMS];
+  uint4 h[XHALF ? ITEMS : 1];
 };
 
 template <int TN, int XHALF>
-SK_DEV void load_x(XStage<TN> &xr, const void *xv, const uint32_t *xrow, uint32_t x_off,
+SK_DEV void load_x(XStage<TN, XHALF> &xr, const void *xv, const uint32_t *xrow, uint32_t x_off,
                    uint32_t x_stride, uint32_t kc, uint32_t nk) {
   const uint32_t tid = threadIdx.x;
 #pragma unroll
-  for (int it = 0; it < XStage<TN>::ITEMS; it++) {
+  for (int it = 0; it < XStage<TN, XHALF>::ITEMS; it++) {
     const uint32_t id = tid + 256 * it;
     const uint32_t n = id >> 5, g = id & 31;
-    uint4 out = make_uint4(0, 0, 0, 0);
-    if (8 * g < nk) {
-      const size_t base = (size_t)x_off + (size_t)xrow[n] * x_stride + kc + 8 * g;
-      if (XHALF) {
-        const uint4 v = *(const uint4 *)((const f16 *)xv + base);
-        // (x0,x1),(x2,x3) -> (x0,x2),(x1,x3)
-        out.x = __builtin_amdgcn_perm(v.y, v.x, 0x05040100u);
-        out.y = __builtin_amdgcn_perm(v.y, v.x, 0x07060302u);
-        out.z = __builtin_amdgcn_perm(v.w, v.z, 0x05040100u);
-        out.w = __builtin_amdgcn_perm(v.w, v.z, 0x07060302u);
-      } else {
+    const bool live = 8 * g < nk;
+    const size_t base = (size_t)x_off + (size_t)xrow[n] * x_stride + kc + 8 * g;
+    if constexpr (XHALF) {
+      uint4 v = make_uint4(0, 0, 0, 0);
+      if (live) v = *(const uint4 *)((const f16 *)xv + base);
+      xr.h[it] = v;
+    } else {
+      float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
+      if (live) {
         const float *xp = (const float *)xv + base;
-        const float4 a = *(const float4 *)xp, b = *(const float4 *)(xp + 4);
-        out.x = as_u32(pack_f16x2(a.x, a.z));
-        out.y = as_u32(pack_f16x2(a.y, a.w));
-        out.z = as_u32(pack_f16x2(b.x, b.z));
-        out.w = as_u32(pack_f16x2(b.y, b.w));
+        a = *(const float4 *)xp;
+        b = *(const float4 *)(xp + 4);
       }
+      xr.a[it] = a;
+      xr.b[it] = b;
     }
-    xr.v[it] = out;
   }
 }
 
-template <int TN>
-SK_DEV void store_x(f16 *lds, const XStage<TN> &xr) {
+// f16 range guard.  f16 tops out at 65504; GEMM inputs such as silu(g)*u can exceed it.
+// When any value of a token's 256-k stage reaches 2^15, that (token, stage) is staged as
+// x * 2^-e (e = exponent(max) - 14, exact) and the stage's products are scaled back by 2^e.
+// The per-wave ballot keeps the common case (no large value in the wave) on a fast path.
+// exps[n] receives e for each token, flags[wave] whether the wave rescaled anything.
+template <int TN, int XHALF>
+SK_DEV void store_x(f16 *lds, const XStage<TN, XHALF> &xr, int *exps, uint32_t *flags) {
   const uint32_t tid = threadIdx.x;
+  uint32_t any = 0;
 #pragma unroll
-  for (int it = 0; it < XStage<TN>::ITEMS; it++) {
+  for (int it = 0; it < XStage<TN, XHALF>::ITEMS; it++) {
     const uint32_t id = tid + 256 * it;
-    *(uint4 *)(lds + (id >> 5) * PITCH + 8 * (id & 31)) = xr.v[it];
+    uint4 out;
+    int e = 0;
+    if constexpr (XHALF) {
+      const uint4 v = xr.h[it];
+      // (x0,x1),(x2,x3) -> (x0,x2),(x1,x3)
+      out.x = __builtin_amdgcn_perm(v.y, v.x, 0x05040100u);
+      out.y = __builtin_amdgcn_perm(v.y, v.x, 0x07060302u);
+      out.z = __builtin_amdgcn_perm(v.w, v.z, 0x05040100u);
+      out.w = __builtin_amdgcn_perm(v.w, v.z, 0x07060302u);
+    } else {
+      float4 a = xr.a[it], b = xr.b[it];
+      const float m = fmaxf(fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))),
+                            fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w))));
+      const bool big = !(m < 32768.0f);  // NaN counts as big: keeps the slow path honest
+      if (__ballot(big) != 0) {
+        float tm = m;
+#pragma unroll
+        for (int d = 16; d >= 1; d >>= 1) tm = fmaxf(tm, __shfl_xor(tm, d, 32));
+        e = tm >= 32768.0f ? (int)((__builtin_bit_cast(uint32_t, tm) >> 23) & 255u) - 127 - 14 : 0;
+        const float sc = __builtin_ldexpf(1.0f, -e);
+        a = make_float4(a.x * sc, a.y * sc, a.z * sc, a.w * sc);
+        b = make_float4(b.x * sc, b.y * sc, b.z * sc, b.w * sc);
+        any = 1;
+      }
+      out.x = as_u32(pack_f16x2(a.x, a.z));
+      out.y = as_u32(pack_f16x2(a.y, a.w));
+      out.z = as_u32(pack_f16x2(b.x, b.z));
+      out.w = as_u32(pack_f16x2(b.y, b.w));
+    }
+    *(uint4 *)(lds + (id >> 5) * PITCH + 8 * (id & 31)) = out;
+    if ((id & 31) == 0) exps[id >> 5] = e;
   }
+  if ((tid & 63) == 0) flags[tid >> 6] = any;
 }
 
 template <int TYPE, int ACCUM, int MOE, int XHALF>
@@ -264,6 +299,8 @@ SK_DEV void matmul_body(const uint4 *__restrict__ w, const uint16_t *__restrict_
   __shared__ __attribute__((aligned(16))) f16 xs[2][TN * PITCH];
   __shared__ uint32_t xrow[TN];
   __shared__ uint32_t yrow[TN];
+  __shared__ int xexp[2][TN];
+  __shared__ uint32_t xflag[2][4];
 
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = tid & 63, wave = tid >> 6;
@@ -295,19 +332,20 @@ SK_DEV void matmul_body(const uint4 *__restrict__ w, const uint16_t *__restrict_
   const uint32_t n_stage = (p.n_in + KC - 1) / KC;
   WStage<TYPE> ws;
   {
-    XStage<TN> x0;
+    XStage<TN, XHALF> x0;
     load_x<TN, XHALF>(x0, x, xrow, p.x_off, p.x_stride, 0, min(p.n_in, (uint32_t)KC));
     load_stage<TYPE>(ws, w, wd, p, wrow, 0, min(p.n_in, (uint32_t)KC));
-    store_x<TN>(xs[0], x0);
+    store_x<TN, XHALF>(xs[0], x0, xexp[0], xflag[0]);
   }
   __syncthreads();
 
   for (uint32_t st = 0; st < n_stage; st++) {
     const uint32_t kc = st * KC;
     const uint32_t nk = min(p.n_in - kc, (uint32_t)KC);
-    const f16 *cur = xs[st & 1];
+    const uint32_t buf = st & 1;
+    const f16 *cur = xs[buf];
     WStage<TYPE> wn;
-    XStage<TN> xn;
+    XStage<TN, XHALF> xn;
     const bool more = st + 1 < n_stage;
     if (more) {
       const uint32_t kn = kc + KC;
@@ -315,22 +353,42 @@ SK_DEV void matmul_body(const uint4 *__restrict__ w, const uint16_t *__restrict_
       load_x<TN, XHALF>(xn, x, xrow, p.x_off, p.x_stride, kn, min(p.n_in - kn, (uint32_t)KC));
     }
     const int steps = (int)(nk >> 4);
+    const bool rescaled = (xflag[buf][0] | xflag[buf][1] | xflag[buf][2] | xflag[buf][3]) != 0;
+    auto run = [&](f32x16 *dst) {
 #pragma unroll
-    for (int t = 0; t < 16; t++) {
-      if (t < steps) {
-        f16x2 sc, nm;
-        step_scale<TYPE>(ws, t, hh, sc, nm);
-        const f16x8 wf = weight_frag<TYPE>(ws, t, hh, sc, nm);
-        const uint32_t ko = koff<TYPE>(t, hh);
+      for (int t = 0; t < 16; t++) {
+        if (t < steps) {
+          f16x2 sc, nm;
+          step_scale<TYPE>(ws, t, hh, sc, nm);
+          const f16x8 wf = weight_frag<TYPE>(ws, t, hh, sc, nm);
+          const uint32_t ko = koff<TYPE>(t, hh);
 #pragma unroll
-        for (int j = 0; j < NB; j++) {
-          const f16x8 xf = *(const f16x8 *)(cur + (32 * j + (lane & 31)) * PITCH + ko);
-          acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(xf, wf, acc[j], 0, 0, 0);
+          for (int j = 0; j < NB; j++) {
+            const f16x8 xf = *(const f16x8 *)(cur + (32 * j + (lane & 31)) * PITCH + ko);
+            dst[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(xf, wf, dst[j], 0, 0, 0);
+          }
         }
       }
+    };
+    if (!rescaled) {
+      run(acc);
+    } else {
+      f32x16 part[NB];
+#pragma unroll
+      for (int j = 0; j < NB; j++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) part[j][i] = 0.0f;
+      run(part);
+#pragma unroll
+      for (int j = 0; j < NB; j++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+          const uint32_t tok = 32 * j + 8 * (i >> 2) + 4 * hh + (i & 3);
+          acc[j][i] += __builtin_ldexpf(part[j][i], xexp[buf][tok]);
+        }
     }
     if (more) {
-      store_x<TN>(xs[(st + 1) & 1], xn);
+      store_x<TN, XHALF>(xs[buf ^ 1], xn, xexp[buf ^ 1], xflag[buf ^ 1]);
       ws = wn;
     }
     __syncthreads();

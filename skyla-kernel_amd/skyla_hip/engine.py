@@ -19,7 +19,8 @@ from .abi import Buffer, Context, Pipeline, Recorder
 # ---- backend.rs: the skyla-hip arm of `mod selected` ----------------------------------
 MATMUL_TILE_COLS = 64   # tokens per matmul workgroup (matmul.hip TN, dense)
 MOE_TILE_COLS = 32      # tokens per grouped-expert workgroup (matmul.hip TN, MOE)
-HALF_INPUTS = True      # prefill GEMM inputs staged as f16 by to_half
+HALF_INPUTS = False     # GEMM inputs stay f32: the matmul stages them to f16 itself, with a
+                        # range guard (activations such as silu(g)*u can exceed f16's 65504)
 HYBRID = False
 # per-backend matvec tactics (waves per workgroup, rows per wave); kernels.rs:10-14
 Q8_0_TACTIC = (4, 2)

@@ -83,18 +83,33 @@ class Setup:
             g.matvec(m, (self.x_off, 0), (self.y_off, 0), accum, False)
         self.run(body)
 
-    def matmul(self, i: int, n_tok: int, accum: bool = False, half: bool = True):
+    def matmul(self, i: int, n_tok: int, accum: bool = False):
+        """The engine's batched Graph::matvec (f32 or f16 inputs per HALF_INPUTS)."""
         m = self.q[i]
         z = -(-n_tok // E.MATMUL_TILE_COLS)
 
         def body(r):
             g = E.Graph(r, self.k, None, None, True)
-            if half:
-                x = (2 * self.half_off, self.s_in)
-            else:
-                x = (self.x_off, self.s_in)
+            x = (2 * self.half_off, self.s_in) if E.HALF_INPUTS else (self.x_off, self.s_in)
             g.matvec(m, x, (self.y_off, self.s_out), accum, True, groups_z=z)
         self.run(body)
+
+    def matmul_variant(self, i: int, n_tok: int, accum: bool, x_half: bool):
+        """A matmul pipeline built directly, with f16 (x_half) or f32 inputs."""
+        m = self.q[i]
+        ty = {E.DType.Q8_0: 0, E.DType.Q4K: 1, E.DType.Q6K: 2}[m.dtype]
+        spec = [ty, int(accum), 0] + ([1] if x_half else [])
+        p = self.ctx.create_pipeline("matmul", 5, 52, spec)
+        w = self.weights[m.buf]
+        p.bind_buffers([w, w, self.arena, self.arena, self.arena])
+        x_off = 2 * self.half_off if x_half else self.x_off
+        push = [m.off[0], m.off[1], m.off[2], m.off[3], x_off, self.y_off, m.n_in, m.n_out, self.s_in,
+                self.s_out, 0, 0, 1]
+        z = -(-n_tok // E.MATMUL_TILE_COLS)
+        try:
+            self.run(lambda r: r.dispatch(p, [-(-m.n_out // 128), 1, z], push))
+        finally:
+            p.free()
 
     def free(self):
         for b in self.weights:
