@@ -1,34 +1,33 @@
 // Decode matvec (M = 1) over raw Q4_K / Q6_K / Q8_0 blocks for gfx950.
 //
 // Contract (what skyla-engine dispatches, graph.rs:23-34 and graph/moe.rs:8-24):
-//   pipeline spec [WAVES, ACCUM, ROWS, MOE, LPR] (kernels.rs:92-97), workgroup = WAVES
-//   wave64s, each lane group of LPR lanes owns ROWS consecutive output rows, so one
-//   workgroup covers WAVES * ROWS * 64 / LPR rows and grid.x = ceil(n_out / that).
-//   MOE: grid.y = slot; the expert is ids[ids_off + slot] and rows are offset by
-//   expert * n_out (matvec_q4k.comp:68-71).  x and y move by x_stride / y_stride per slot.
-//   ACCUM adds into y (residual add for O and down).
+//   pipeline spec [WAVES, ACCUM, ROWS, MOE, LPR] (kernels.rs:92-97): a workgroup is WAVES
+//   wave64s; each group of LPR lanes owns ROWS consecutive output rows, so a workgroup covers
+//   RWG = WAVES * (64 / LPR) * ROWS rows and grid.x = ceil(n_out / RWG).  MOE: grid.y = slot,
+//   the expert is ids[ids_off + slot] and its rows start at expert * n_out
+//   (matvec_q4k.comp:68-71); x and y move by x_stride / y_stride per slot.  ACCUM adds into y.
 //
-// Inner loop (MI355X-specific):
-//   * one 16-byte coalesced load per row per lane per step (64 lanes read 1 KiB of a row
-//     contiguously), the loads of every row of the step issued before any math, and the
-//     next step's loads issued before the current step's math;
-//   * activations are read once per step and shared by the ROWS rows: converted to f16
-//     pairs (RNE) in the order the packed weights need them;
-//   * weights are never converted to float one by one: a quant is OR-ed into the
-//     mantissa of the f16 constant 1024.0 (0x6400), giving 1024+q exactly, and
-//     v_dot2_f32_f16 multiplies two of them by two activations with f32 accumulation.
-//     The accumulator starts at -1024 * sum(x) (the f16 activations' own sum), which
-//     cancels the offset.  High nibbles are taken in place as 1024+16q (no shift) and
-//     the group total is scaled by 1/16 afterwards.
-//   * the sub-block scales are applied once per 16 (Q4_K, Q6_K) or 16 (Q8_0) values
-//     per row, in f32;
-//   * one shuffle reduction per row at the end; lane 0 of each lane group writes.
-// Numerics: f16 activations (relative error 2^-11 per element) and f32 accumulation; the
-// result differs from the reference's f32 dot only by rounding, far inside the 1e-2
-// relative-L2 bar.
+// Budget that shapes the kernel: at 8 TB/s each of the 256 CUs must consume ~13 B/clk of
+// weights (~23 Q4_K values/clk) while it has 64 VALU lane-ops/clk and ~64 B/clk of L1.
+//   * Activations are staged once per workgroup in LDS as f16 pairs in the order the packed
+//     quants need them, with their per-16 sums, instead of every wave re-reading f32 x
+//     through L1 (4x the weight bytes at two rows per wave).
+//   * Each (row, super-block) header is decoded once per workgroup into f32 products
+//     d*sc and dmin*m (the reference's d0 / min0, quant.rs:60-61), so a lane's per-row work
+//     is the quant extraction, v_dot2 and four FMAs.
+//   * A quant is OR-ed into the mantissa of the f16 constant 1024.0 (0x6400), giving 1024+q
+//     exactly; v_dot2_f32_f16 multiplies two of them by two activations with f32
+//     accumulation, and the accumulator starts at -1024 * sum(x) to cancel the offset.  High
+//     nibbles are taken in place as 1024+16q (no shift) and their scale carries the 1/16.
+//   * Weight loads are 16 B per lane, 1 KiB contiguous per wave instruction, and the first
+//     step's loads are issued before the staging so they overlap it.
+// Numerics: f16 activations (relative rounding 2^-11) with f32 accumulation -- within 1e-4
+// relative L2 of the reference's f32 dot in practice, far inside the 1e-2 bar.
 #include "common.h"
 
 #define MAGIC 0x64006400u  // f16x2 {1024.0, 1024.0}
+
+namespace {
 
 struct MatvecPush2 {  // Q4_K and Q8_0 (9 words, graph.rs:30 / graph/moe.rs:251-255)
   uint32_t o0, o1, x_off, y_off, n_in, n_out, ids_off, x_stride, y_stride;
@@ -38,32 +37,38 @@ struct MatvecPush4 {  // Q6_K (11 words, graph.rs:29 / graph/moe.rs:252)
   uint32_t o0, o1, o2, o3, x_off, y_off, n_in, n_out, ids_off, x_stride, y_stride;
 };
 
-SK_DEV float4 ld_x4(const float *p) { return *(const float4 *)p; }
-
-// Converts 16 consecutive activations v[0..15] into the pair order of the packed quants:
-// for dword k of a 16-byte weight unit, pair02 = (v[4k], v[4k+2]), pair13 = (v[4k+1],
-// v[4k+3]).  Returns the sum of the f16 values (f32 accumulation).
-SK_DEV float x16_pairs(const float4 v[4], f16x2 p02[4], f16x2 p13[4]) {
-  const f16x2 one = {(f16)1.0f, (f16)1.0f};
-  float s = 0.0f;
-#pragma unroll
-  for (int k = 0; k < 4; k++) {
-    p02[k] = pack_f16x2(v[k].x, v[k].z);
-    p13[k] = pack_f16x2(v[k].y, v[k].w);
-    s = dot2(p02[k], one, s);
-    s = dot2(p13[k], one, s);
-  }
-  return s;
+// (a & m) | o as one v_and_or_b32 with register operands (the compiler otherwise splits it
+// in two, because gfx9 VOP3 encodings take no literal).
+SK_DEV uint32_t and_or(uint32_t a, uint32_t m, uint32_t o) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(m), "v"(o));
+  return r;
 }
 
-// Writes the reduced row results.  Lane 0 of each LPR group stores ROWS values.
+template <int CTRL>
+SK_DEV float dpp_f(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+
+// Sum over groups of LPR consecutive lanes; every lane gets its group's total.
+template <int LPR>
+SK_DEV float lane_sum(float v) {
+  v += dpp_f<0xb1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_f<0x4e>(v);   // quad_perm [2,3,0,1]
+  v += dpp_f<0x141>(v);  // row_half_mirror: the two quads of each 8
+  v += dpp_f<0x140>(v);  // row_mirror: the two halves of each 16
+  if (LPR >= 32) v += __shfl_xor(v, 16, 64);
+  if (LPR >= 64) v += __shfl_xor(v, 32, 64);
+  return v;
+}
+
 template <int ACCUM, int ROWS, int LPR>
 SK_DEV void store_rows(float *y, uint32_t y_off, uint32_t first, uint32_t n_out, uint32_t lane,
-                       float acc[ROWS]) {
+                       const float (&acc)[ROWS]) {
 #pragma unroll
   for (int r = 0; r < ROWS; r++) {
-    float total = group_sum<LPR>(acc[r]);
-    uint32_t row = first + r;
+    const float total = lane_sum<LPR>(acc[r]);
+    const uint32_t row = first + r;
     if (lane == 0 && row < n_out) {
       if (ACCUM)
         y[y_off + row] += total;
@@ -73,284 +78,482 @@ SK_DEV void store_rows(float *y, uint32_t y_off, uint32_t first, uint32_t n_out,
   }
 }
 
+SK_DEV uint32_t pk(float a, float b) { return as_u32(pack_f16x2(a, b)); }
+
+// Geometry shared by the three formats.
+template <int WAVES, int ROWS, int LPR>
+struct Geo {
+  static constexpr int SUBS = 64 / LPR;            // row groups per wave
+  static constexpr int RWG = WAVES * SUBS * ROWS;  // rows per workgroup
+  static constexpr int NT = 64 * WAVES;            // threads per workgroup
+  // super-blocks of activations staged per pass: keeps the decoded scales <= 32 KiB
+  static constexpr int CH_SUP = (512 / RWG) < 1 ? 1 : ((512 / RWG) > 32 ? 32 : (512 / RWG));
+  static constexpr int CH = CH_SUP * 256;          // values per pass
+};
+
 // ---------------------------------------------------------------------------------------
-// Q4_K: lane step = one 16-byte unit of qs (32 quants) per row.
-// Unit u of a row: super-block u/8, chunk c = (u%8)/2, half h = u%2.  Its low nibbles are
-// values 64c + 16h + [0,16) of sub-block 2c, its high nibbles values 64c + 32 + 16h +
-// [0,16) of sub-block 2c+1 (quant.rs:56-66).
+// Q4_K.  Lane step = one 16 B unit of qs: unit u of a row is super-block u/8, chunk
+// c = (u/2)%4, bytes 16(u%2) + [0,16) of that chunk's 32 -- low nibbles are values
+// 64c + 16(u%2) + [0,16) of sub-block 2c, high nibbles the same positions of sub-block 2c+1
+// (quant.rs:56-66).  LDS per pass: xq[0..3][unit] = the unit's 32 activations as f16 pairs in
+// the (0,2),(1,3) order of the packed quants (low-nibble half, then high), xs[unit] = their
+// two 16-value sums, and per (row, super-block, chunk) the products d*sc (x2: low and high
+// sub-block, 1/16 folded into the high one) and dmin*m (quant.rs:40-49, 60-61).
 // ---------------------------------------------------------------------------------------
 template <int WAVES, int ACCUM, int ROWS, int MOE, int LPR>
 SK_DEV void matvec_q4k_body(const uint4 *__restrict__ w, const float *x, float *y,
                             const uint32_t *ids, const MatvecPush2 &p) {
+  using G = Geo<WAVES, ROWS, LPR>;
+  __shared__ uint4 xq[4][G::CH / 32];  // component-major: lanes read consecutive 16 B
+  __shared__ float2 xs[G::CH / 32];
+  __shared__ float4 sc[G::RWG][G::CH_SUP][4];
+
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = (tid & 63) % LPR;
   const uint32_t sub = (tid & 63) / LPR;
-  const uint32_t wave = blockIdx.x * WAVES + (tid >> 6);
-  const uint32_t first = (wave * (64 / LPR) + sub) * ROWS;
-  if (LPR == 64 && first >= p.n_out) return;
+  const uint32_t row0 = blockIdx.x * G::RWG;
+  const uint32_t lrow0 = ((tid >> 6) * G::SUBS + sub) * ROWS;  // first row of this group in the WG
+  const uint32_t first = row0 + lrow0;
   const uint32_t slot = blockIdx.y;
   const uint32_t base = MOE ? ids[p.ids_off + slot] * p.n_out : 0;
-  const float *xs = x + p.x_off + slot * p.x_stride;
+  const float *xv = x + p.x_off + slot * p.x_stride;
   const uint32_t y_off = p.y_off + slot * p.y_stride;
-  const uint32_t units = p.n_in >> 5;
-  const uint32_t supers = p.n_in >> 8;
+  const uint32_t units = p.n_in >> 5, supers = p.n_in >> 8;
+  const uint32_t c = (lane >> 1) & 3;  // chunk of this lane's units (u % 8 == lane % 8)
+  const uint32_t MW = MAGIC, LO = 0x000f000fu, HI = 0x00f000f0u;
 
   const uint4 *qs[ROWS];
-  const uint4 *hd[ROWS];
 #pragma unroll
-  for (int r = 0; r < ROWS; r++) {
-    uint32_t row = base + min(first + r, p.n_out - 1);
-    qs[r] = w + p.o0 + row * units;
-    hd[r] = w + p.o1 + row * supers;
-  }
-
-  // Per-lane constants of the scale unpack (u % 8 == lane % 8 for every step).
-  const uint32_t c = (lane >> 1) & 3;
-  const uint32_t xlane = c * 64 + (lane & 1) * 16;
-  const uint32_t sh = (c & 1) * 16;
-  const bool hi = c >= 2;
-  const uint32_t mW = hi ? 0x0f0fu : 0u;
-  const uint32_t s2 = hi ? 2u : 0u;
-  const uint32_t mY = hi ? 0x3030u : 0x3f3fu;
+  for (int r = 0; r < ROWS; r++) qs[r] = w + p.o0 + (base + min(first + r, p.n_out - 1)) * units;
 
   float acc[ROWS];
 #pragma unroll
   for (int r = 0; r < ROWS; r++) acc[r] = 0.0f;
 
-  uint32_t u = lane;
-  uint4 q[ROWS], h[ROWS];
-  float4 xa[4], xb[4];
-  if (u < units) {
-#pragma unroll
-    for (int r = 0; r < ROWS; r++) {
-      q[r] = qs[r][u];
-      h[r] = hd[r][u >> 3];
-    }
-    const float *xp = xs + (u >> 3) * 256 + xlane;
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-      xa[k] = ld_x4(xp + 4 * k);
-      xb[k] = ld_x4(xp + 32 + 4 * k);
-    }
-  }
-  for (; u < units; u += LPR) {
-    const uint32_t un = u + LPR;
-    uint4 qn[ROWS], hn[ROWS];
-    float4 xan[4], xbn[4];
-    if (un < units) {
-#pragma unroll
-      for (int r = 0; r < ROWS; r++) {
-        qn[r] = qs[r][un];
-        hn[r] = hd[r][un >> 3];
-      }
-      const float *xp = xs + (un >> 3) * 256 + xlane;
+  for (uint32_t k0 = 0; k0 < p.n_in; k0 += G::CH) {
+    const uint32_t nk = min(p.n_in - k0, (uint32_t)G::CH);
+    const uint32_t u0 = k0 >> 5, nu = nk >> 5, s0 = k0 >> 8, ns = nk >> 8;
+    // Load order matters (loads complete in issue order): this thread's first staging
+    // loads go out first, then the first PF steps of weights, so the staging below waits
+    // only for its own data while the weight stream is already in flight.
+    auto x_unit = [&](uint32_t i, float4 (&a)[4], float4 (&b)[4]) {
+      const uint32_t u = u0 + i;
+      const float *xp = xv + (u >> 3) * 256 + ((u >> 1) & 3) * 64 + (u & 1) * 16;
 #pragma unroll
       for (int k = 0; k < 4; k++) {
-        xan[k] = ld_x4(xp + 4 * k);
-        xbn[k] = ld_x4(xp + 32 + 4 * k);
+        a[k] = *(const float4 *)(xp + 4 * k);
+        b[k] = *(const float4 *)(xp + 32 + 4 * k);
+      }
+    };
+    auto x_store = [&](uint32_t i, const float4 (&a)[4], const float4 (&b)[4]) {
+      uint32_t pa[8], pb[8];
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        pa[2 * k] = pk(a[k].x, a[k].z);
+        pa[2 * k + 1] = pk(a[k].y, a[k].w);
+        pb[2 * k] = pk(b[k].x, b[k].z);
+        pb[2 * k + 1] = pk(b[k].y, b[k].w);
+      }
+      const f16x2 one = {(f16)1.0f, (f16)1.0f};
+      float sa = 0.0f, sb = 0.0f;
+#pragma unroll
+      for (int k = 0; k < 8; k++) {
+        sa = dot2(as_f16x2(pa[k]), one, sa);
+        sb = dot2(as_f16x2(pb[k]), one, sb);
+      }
+      xq[0][i] = make_uint4(pa[0], pa[1], pa[2], pa[3]);
+      xq[1][i] = make_uint4(pa[4], pa[5], pa[6], pa[7]);
+      xq[2][i] = make_uint4(pb[0], pb[1], pb[2], pb[3]);
+      xq[3][i] = make_uint4(pb[4], pb[5], pb[6], pb[7]);
+      xs[i] = make_float2(sa, sb);
+    };
+    const uint32_t n_items = (uint32_t)G::RWG * ns;
+    auto h_load = [&](uint32_t i) -> uint4 {
+      const uint32_t lr = i / ns, s = i % ns;
+      const uint32_t row = base + min(row0 + lr, p.n_out - 1);
+      return w[p.o1 + row * supers + s0 + s];
+    };
+    auto h_store = [&](uint32_t i, const uint4 h) {
+      const uint32_t lr = i / ns, s = i % ns;
+      const float d = f16_bits_to_f32(h.x & 0xffffu);
+      const float dmin = f16_bits_to_f32(h.x >> 16);
+#pragma unroll
+      for (int cc = 0; cc < 4; cc++) {
+        uint32_t sc0, m0, sc1, m1;
+        q4k_scale_min(2 * cc, h.y, h.z, h.w, sc0, m0);
+        q4k_scale_min(2 * cc + 1, h.y, h.z, h.w, sc1, m1);
+        sc[lr][s][cc] = make_float4(d * (float)sc0, d * (float)sc1 * 0.0625f, dmin * (float)m0,
+                                    dmin * (float)m1);
+      }
+    };
+    if (k0 != 0) __syncthreads();  // the previous pass is done with the LDS
+    float4 xa[4], xb[4];
+    uint4 h0 = make_uint4(0, 0, 0, 0);
+    if (tid < nu) x_unit(tid, xa, xb);
+    if (tid < n_items) h0 = h_load(tid);
+    constexpr int PF = 4;  // weight steps in flight per lane
+    uint4 q[PF][ROWS];
+#pragma unroll
+    for (int j = 0; j < PF; j++) {
+      const uint32_t i = lane + j * LPR;
+      if (i < nu) {
+#pragma unroll
+        for (int r = 0; r < ROWS; r++) q[j][r] = qs[r][u0 + i];
       }
     }
+    if (tid < nu) x_store(tid, xa, xb);
+    if (tid < n_items) h_store(tid, h0);
+    for (uint32_t i = tid + G::NT; i < nu; i += G::NT) {
+      x_unit(i, xa, xb);
+      x_store(i, xa, xb);
+    }
+    for (uint32_t i = tid + G::NT; i < n_items; i += G::NT) h_store(i, h_load(i));
+    __syncthreads();
 
-    f16x2 a02[4], a13[4], b02[4], b13[4];
-    const float sum_a = x16_pairs(xa, a02, a13);
-    const float sum_b = x16_pairs(xb, b02, b13);
+    for (uint32_t j0 = 0; lane + j0 * LPR < nu; j0 += PF) {
 #pragma unroll
-    for (int r = 0; r < ROWS; r++) {
-      float sa = -1024.0f * sum_a;
-      float sb = -1024.0f * sum_b;
-      const uint32_t wd[4] = {q[r].x, q[r].y, q[r].z, q[r].w};
+      for (int j = 0; j < PF; j++) {
+        const uint32_t i = lane + (j0 + j) * LPR;
+        if (i < nu) {
+          const uint4 xa0 = xq[0][i], xa1 = xq[1][i], xb0 = xq[2][i], xb1 = xq[3][i];
+          const float2 xsum = xs[i];
+          const uint32_t pa[8] = {xa0.x, xa0.y, xa0.z, xa0.w, xa1.x, xa1.y, xa1.z, xa1.w};
+          const uint32_t pb[8] = {xb0.x, xb0.y, xb0.z, xb0.w, xb1.x, xb1.y, xb1.z, xb1.w};
+          const float na = -1024.0f * xsum.x, nb = -1024.0f * xsum.y;
+          const uint32_t s = i >> 3;
 #pragma unroll
-      for (int k = 0; k < 4; k++) {
-        const uint32_t w0 = wd[k];
-        const uint32_t w8 = w0 >> 8;
-        sa = dot2(as_f16x2((w0 & 0x000f000fu) | MAGIC), a02[k], sa);
-        sa = dot2(as_f16x2((w8 & 0x000f000fu) | MAGIC), a13[k], sa);
-        sb = dot2(as_f16x2((w0 & 0x00f000f0u) | MAGIC), b02[k], sb);
-        sb = dot2(as_f16x2((w8 & 0x00f000f0u) | MAGIC), b13[k], sb);
+          for (int r = 0; r < ROWS; r++) {
+            float sa = na, sb = nb;
+            const uint32_t wd[4] = {q[j][r].x, q[j][r].y, q[j][r].z, q[j][r].w};
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+              const uint32_t w0 = wd[k], w8 = w0 >> 8;
+              sa = dot2(as_f16x2(and_or(w0, LO, MW)), as_f16x2(pa[2 * k]), sa);
+              sa = dot2(as_f16x2(and_or(w8, LO, MW)), as_f16x2(pa[2 * k + 1]), sa);
+              sb = dot2(as_f16x2(and_or(w0, HI, MW)), as_f16x2(pb[2 * k]), sb);
+              sb = dot2(as_f16x2(and_or(w8, HI, MW)), as_f16x2(pb[2 * k + 1]), sb);
+            }
+            const float4 f = sc[lrow0 + r][s][c];
+            acc[r] = __builtin_fmaf(f.x, sa, acc[r]);
+            acc[r] = __builtin_fmaf(f.y, sb, acc[r]);
+            acc[r] = __builtin_fmaf(-f.z, xsum.x, acc[r]);
+            acc[r] = __builtin_fmaf(-f.w, xsum.y, acc[r]);
+          }
+          const uint32_t inext = i + PF * LPR;  // refill this slot PF steps ahead
+          if (inext < nu) {
+#pragma unroll
+            for (int r = 0; r < ROWS; r++) q[j][r] = qs[r][u0 + inext];
+          }
+        }
       }
-      // scales/mins j = 2c, 2c+1 (quant.rs:40-49), two bytes at a time
-      const uint32_t ys = h[r].y >> sh, zs = h[r].z >> sh, ws = h[r].w >> sh;
-      const uint32_t scv = (ws & mW) | ((ys >> s2) & mY);
-      const uint32_t mv = ((ws >> 4) & mW) | ((zs >> s2) & mY);
-      const float sc0 = (float)(scv & 0xffu), sc1 = (float)((scv >> 8) & 0xffu);
-      const float m0 = (float)(mv & 0xffu), m1 = (float)((mv >> 8) & 0xffu);
-      const float d = f16_bits_to_f32(h[r].x & 0xffffu);
-      const float dmin = f16_bits_to_f32(h[r].x >> 16);
-      const float t = sc0 * sa + (sc1 * 0.0625f) * sb;
-      const float mt = m0 * sum_a + m1 * sum_b;
-      acc[r] += d * t - dmin * mt;
-    }
-#pragma unroll
-    for (int r = 0; r < ROWS; r++) {
-      q[r] = qn[r];
-      h[r] = hn[r];
-    }
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-      xa[k] = xan[k];
-      xb[k] = xbn[k];
     }
   }
   store_rows<ACCUM, ROWS, LPR>(y, y_off, first, p.n_out, lane, acc);
 }
 
 // ---------------------------------------------------------------------------------------
-// Q6_K: lane step = 64 values of one super-block: u -> super-block u/4, half (u%4)/2,
-// li = u%2.  It reads 16 B of ql at l = 16 li (a), 16 B at l + 32 (b), 16 B of qh (h),
-// the 16 scale bytes and d.  Groups g = 0..3 are values 128 half + 32 g + 16 li + [0,16)
-// with scale sc[8 half + li + 2g] (quant.rs:72-87).
+// Q6_K.  Lane step = 64 values of one super-block: u -> super-block u/4, half hf = (u%4)/2,
+// li = u%2.  It reads 16 B of ql at l = 16 li (a), 16 B at l + 32 (b) and 16 B of qh.
+// Group g = 0..3 is values 128 hf + 32 g + 16 li + [0,16) with scale sc[8 hf + li + 2g]
+// (quant.rs:72-87).  Groups 0,1 are built as 1024+q, groups 2,3 as 1024+16q (q the stored
+// 6-bit value, quant = q - 32).
+// LDS per pass: xq[unit] = 32 f16 pairs (4 groups x 8), xs[unit] = the 4 group sums, and per
+// (row, super-block) and (hf, li): d*sc for the lane's 4 groups (1/16 folded into g = 2, 3).
 // ---------------------------------------------------------------------------------------
 template <int WAVES, int ACCUM, int ROWS, int MOE, int LPR>
 SK_DEV void matvec_q6k_body(const uint4 *__restrict__ w, const uint16_t *__restrict__ wd,
-                            const float *x, float *y, const uint32_t *ids,
-                            const MatvecPush4 &p) {
+                            const float *x, float *y, const uint32_t *ids, const MatvecPush4 &p) {
+  using G = Geo<WAVES, ROWS, LPR>;
+  __shared__ uint4 xq[8][G::CH / 64];  // component-major
+  __shared__ float4 xs[G::CH / 64];
+  __shared__ float4 sc[G::RWG][G::CH_SUP][4];
+
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = (tid & 63) % LPR;
   const uint32_t sub = (tid & 63) / LPR;
-  const uint32_t wave = blockIdx.x * WAVES + (tid >> 6);
-  const uint32_t first = (wave * (64 / LPR) + sub) * ROWS;
-  if (LPR == 64 && first >= p.n_out) return;
+  const uint32_t row0 = blockIdx.x * G::RWG;
+  const uint32_t lrow0 = ((tid >> 6) * G::SUBS + sub) * ROWS;
+  const uint32_t first = row0 + lrow0;
   const uint32_t slot = blockIdx.y;
   const uint32_t base = MOE ? ids[p.ids_off + slot] * p.n_out : 0;
-  const float *xs = x + p.x_off + slot * p.x_stride;
+  const float *xv = x + p.x_off + slot * p.x_stride;
   const uint32_t y_off = p.y_off + slot * p.y_stride;
-  const uint32_t units = p.n_in >> 6;
   const uint32_t supers = p.n_in >> 8;
+  const uint32_t li = lane & 1, hf = (lane >> 1) & 1;
+  const uint32_t MW = MAGIC, L4 = 0x000f000fu, H4 = 0x00f000f0u, LH = 0x00300030u, HH = 0x03000300u;
 
-  uint32_t rowbase[ROWS];
+  uint32_t rb[ROWS];
 #pragma unroll
-  for (int r = 0; r < ROWS; r++) rowbase[r] = (base + min(first + r, p.n_out - 1)) * supers;
-
-  const uint32_t li = lane & 1;
-  const uint32_t hf = (lane >> 1) & 1;
-  const uint32_t inner = hf * 4 + li;           // uint4 index of `a` inside the block's ql
-  const uint32_t xlane = hf * 128 + li * 16;    // first value of group 0
-  const uint32_t bsh = li * 8;                  // byte of sc inside the selected word
+  for (int r = 0; r < ROWS; r++) rb[r] = (base + min(first + r, p.n_out - 1)) * supers;
 
   float acc[ROWS];
 #pragma unroll
   for (int r = 0; r < ROWS; r++) acc[r] = 0.0f;
 
-  for (uint32_t u = lane; u < units; u += LPR) {
-    const uint32_t sb = u >> 2;
-    uint4 qa[ROWS], qb[ROWS], qh[ROWS], sc[ROWS];
-    uint32_t dd[ROWS];
+  for (uint32_t k0 = 0; k0 < p.n_in; k0 += G::CH) {
+    const uint32_t nk = min(p.n_in - k0, (uint32_t)G::CH);
+    const uint32_t u0 = k0 >> 6, nu = nk >> 6, s0 = k0 >> 8, ns = nk >> 8;
+    constexpr int PF = 2;
+    uint4 qa[PF][ROWS], qb[PF][ROWS], qh[PF][ROWS];
+    auto load = [&](uint32_t i, uint4 (&a)[ROWS], uint4 (&b)[ROWS], uint4 (&h)[ROWS]) {
+      const uint32_t u = u0 + i;
+      const uint32_t s = u >> 2;
 #pragma unroll
-    for (int r = 0; r < ROWS; r++) {
-      const uint32_t rs = rowbase[r] + sb;
-      qa[r] = w[p.o0 + rs * 8 + inner];
-      qb[r] = w[p.o0 + rs * 8 + inner + 2];
-      qh[r] = w[p.o1 + rs * 4 + hf * 2 + li];
-      sc[r] = w[p.o2 + rs];
-      dd[r] = wd[p.o3 + rs];
-    }
-    const float *xp = xs + sb * 256 + xlane;
-    float4 xv[4][4];
-#pragma unroll
-    for (int g = 0; g < 4; g++)
-#pragma unroll
-      for (int k = 0; k < 4; k++) xv[g][k] = ld_x4(xp + 32 * g + 4 * k);
-    f16x2 p02[4][4], p13[4][4];
-    float xsum[4];
-#pragma unroll
-    for (int g = 0; g < 4; g++) xsum[g] = x16_pairs(xv[g], p02[g], p13[g]);
-
-#pragma unroll
-    for (int r = 0; r < ROWS; r++) {
-      // groups 0,1 hold 1024+q, groups 2,3 hold 1024+16q; q is the stored 6-bit value
-      // and the quant is q-32: the starting values cancel both offsets.
-      float s0 = -1056.0f * xsum[0], s1 = -1056.0f * xsum[1];
-      float s2 = -1536.0f * xsum[2], s3 = -1536.0f * xsum[3];
-      const uint32_t av[4] = {qa[r].x, qa[r].y, qa[r].z, qa[r].w};
-      const uint32_t bv[4] = {qb[r].x, qb[r].y, qb[r].z, qb[r].w};
-      const uint32_t hv[4] = {qh[r].x, qh[r].y, qh[r].z, qh[r].w};
-#pragma unroll
-      for (int k = 0; k < 4; k++) {
-        const uint32_t a0 = av[k], b0 = bv[k], h0 = hv[k];
-        const uint32_t a8 = a0 >> 8, b8 = b0 >> 8, h8 = h0 >> 8;
-        const uint32_t h4 = h0 << 4, h2 = h0 << 2, h84 = h8 << 4, h82 = h8 << 2;
-        s0 = dot2(as_f16x2((a0 & 0x000f000fu) | MAGIC | (h4 & 0x00300030u)), p02[0][k], s0);
-        s0 = dot2(as_f16x2((a8 & 0x000f000fu) | MAGIC | (h84 & 0x00300030u)), p13[0][k], s0);
-        s1 = dot2(as_f16x2((b0 & 0x000f000fu) | MAGIC | (h2 & 0x00300030u)), p02[1][k], s1);
-        s1 = dot2(as_f16x2((b8 & 0x000f000fu) | MAGIC | (h82 & 0x00300030u)), p13[1][k], s1);
-        s2 = dot2(as_f16x2((a0 & 0x00f000f0u) | MAGIC | (h4 & 0x03000300u)), p02[2][k], s2);
-        s2 = dot2(as_f16x2((a8 & 0x00f000f0u) | MAGIC | (h84 & 0x03000300u)), p13[2][k], s2);
-        s3 = dot2(as_f16x2((b0 & 0x00f000f0u) | MAGIC | (h2 & 0x03000300u)), p02[3][k], s3);
-        s3 = dot2(as_f16x2((b8 & 0x00f000f0u) | MAGIC | (h82 & 0x03000300u)), p13[3][k], s3);
+      for (int r = 0; r < ROWS; r++) {
+        const uint32_t rs = rb[r] + s;
+        a[r] = w[p.o0 + rs * 8 + hf * 4 + li];
+        b[r] = w[p.o0 + rs * 8 + hf * 4 + 2 + li];
+        h[r] = w[p.o1 + rs * 4 + hf * 2 + li];
       }
-      const uint32_t w0 = hf ? sc[r].z : sc[r].x;
-      const uint32_t w1 = hf ? sc[r].w : sc[r].y;
-      const float c0 = (float)(int32_t)__builtin_amdgcn_sbfe(w0, bsh, 8);
-      const float c1 = (float)(int32_t)__builtin_amdgcn_sbfe(w0, bsh + 16, 8);
-      const float c2 = (float)(int32_t)__builtin_amdgcn_sbfe(w1, bsh, 8);
-      const float c3 = (float)(int32_t)__builtin_amdgcn_sbfe(w1, bsh + 16, 8);
-      const float t = c0 * s0 + c1 * s1 + 0.0625f * (c2 * s2 + c3 * s3);
-      acc[r] += f16_bits_to_f32(dd[r]) * t;
+    };
+    auto x_unit = [&](uint32_t i, float4 (&v)[16]) {
+      const uint32_t u = u0 + i;
+      const float *xp = xv + (u >> 2) * 256 + ((u >> 1) & 1) * 128 + (u & 1) * 16;
+#pragma unroll
+      for (int g = 0; g < 4; g++)
+#pragma unroll
+        for (int k = 0; k < 4; k++) v[4 * g + k] = *(const float4 *)(xp + 32 * g + 4 * k);
+    };
+    auto x_store = [&](uint32_t i, const float4 (&v)[16]) {
+      const f16x2 one = {(f16)1.0f, (f16)1.0f};
+      float4 sums;
+      float *sp = (float *)&sums;
+#pragma unroll
+      for (int g = 0; g < 4; g++) {
+        uint32_t pp[8];
+        float s = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+          const float4 e = v[4 * g + k];
+          pp[2 * k] = pk(e.x, e.z);
+          pp[2 * k + 1] = pk(e.y, e.w);
+          s = dot2(as_f16x2(pp[2 * k]), one, s);
+          s = dot2(as_f16x2(pp[2 * k + 1]), one, s);
+        }
+        xq[2 * g][i] = make_uint4(pp[0], pp[1], pp[2], pp[3]);
+        xq[2 * g + 1][i] = make_uint4(pp[4], pp[5], pp[6], pp[7]);
+        sp[g] = s;
+      }
+      xs[i] = sums;
+    };
+    const uint32_t n_items = (uint32_t)G::RWG * ns;
+    auto h_load = [&](uint32_t i, uint4 &sv, uint32_t &dv) {
+      const uint32_t lr = i / ns, s = i % ns;
+      const uint32_t rs = (base + min(row0 + lr, p.n_out - 1)) * supers + s0 + s;
+      sv = w[p.o2 + rs];
+      dv = wd[p.o3 + rs];
+    };
+    auto h_store = [&](uint32_t i, const uint4 sv, uint32_t dv) {
+      const uint32_t lr = i / ns, s = i % ns;
+      const float d = f16_bits_to_f32(dv);
+      const uint32_t sw[4] = {sv.x, sv.y, sv.z, sv.w};
+#pragma unroll
+      for (int lp = 0; lp < 4; lp++) {  // (hf, li) = (lp / 2, lp % 2)
+        float o[4];
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+          const uint32_t k = 8 * (lp >> 1) + (lp & 1) + 2 * g;
+          const int s8 = (int)(int8_t)((sw[k >> 2] >> (8 * (k & 3))) & 255u);
+          o[g] = d * (float)s8 * (g >= 2 ? 0.0625f : 1.0f);
+        }
+        sc[lr][s][lp] = make_float4(o[0], o[1], o[2], o[3]);
+      }
+    };
+    if (k0 != 0) __syncthreads();
+    float4 xv16[16];
+    uint4 sv0 = make_uint4(0, 0, 0, 0);
+    uint32_t dv0 = 0;
+    if (tid < nu) x_unit(tid, xv16);
+    if (tid < n_items) h_load(tid, sv0, dv0);
+#pragma unroll
+    for (int j = 0; j < PF; j++)
+      if (lane + j * LPR < nu) load(lane + j * LPR, qa[j], qb[j], qh[j]);
+    if (tid < nu) x_store(tid, xv16);
+    if (tid < n_items) h_store(tid, sv0, dv0);
+    for (uint32_t i = tid + G::NT; i < nu; i += G::NT) {
+      x_unit(i, xv16);
+      x_store(i, xv16);
+    }
+    for (uint32_t i = tid + G::NT; i < n_items; i += G::NT) {
+      h_load(i, sv0, dv0);
+      h_store(i, sv0, dv0);
+    }
+    __syncthreads();
+
+    for (uint32_t j0 = 0; lane + j0 * LPR < nu; j0 += PF) {
+#pragma unroll
+      for (int j = 0; j < PF; j++) {
+        const uint32_t i = lane + (j0 + j) * LPR;
+        if (i < nu) {
+          uint32_t px[32];
+#pragma unroll
+          for (int jj = 0; jj < 8; jj++) {
+            const uint4 v = xq[jj][i];
+            px[4 * jj] = v.x;
+            px[4 * jj + 1] = v.y;
+            px[4 * jj + 2] = v.z;
+            px[4 * jj + 3] = v.w;
+          }
+          const float4 xsum = xs[i];
+          const float i0 = -1056.0f * xsum.x, i1 = -1056.0f * xsum.y;
+          const float i2 = -1536.0f * xsum.z, i3 = -1536.0f * xsum.w;
+          const uint32_t s = i >> 2;
+#pragma unroll
+          for (int r = 0; r < ROWS; r++) {
+            float t0 = i0, t1 = i1, t2 = i2, t3 = i3;
+            const uint32_t av[4] = {qa[j][r].x, qa[j][r].y, qa[j][r].z, qa[j][r].w};
+            const uint32_t bv[4] = {qb[j][r].x, qb[j][r].y, qb[j][r].z, qb[j][r].w};
+            const uint32_t hv[4] = {qh[j][r].x, qh[j][r].y, qh[j][r].z, qh[j][r].w};
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+              const uint32_t a0 = av[k], b0 = bv[k], h0 = hv[k];
+              const uint32_t a8 = a0 >> 8, b8 = b0 >> 8, h8 = h0 >> 8;
+              const uint32_t h4 = h0 << 4, h2 = h0 << 2, h84 = h8 << 4, h82 = h8 << 2;
+              t0 = dot2(as_f16x2(and_or(h4, LH, and_or(a0, L4, MW))), as_f16x2(px[0 * 8 + 2 * k]), t0);
+              t0 = dot2(as_f16x2(and_or(h84, LH, and_or(a8, L4, MW))), as_f16x2(px[0 * 8 + 2 * k + 1]), t0);
+              t1 = dot2(as_f16x2(and_or(h2, LH, and_or(b0, L4, MW))), as_f16x2(px[1 * 8 + 2 * k]), t1);
+              t1 = dot2(as_f16x2(and_or(h82, LH, and_or(b8, L4, MW))), as_f16x2(px[1 * 8 + 2 * k + 1]), t1);
+              t2 = dot2(as_f16x2(and_or(h4, HH, and_or(a0, H4, MW))), as_f16x2(px[2 * 8 + 2 * k]), t2);
+              t2 = dot2(as_f16x2(and_or(h84, HH, and_or(a8, H4, MW))), as_f16x2(px[2 * 8 + 2 * k + 1]), t2);
+              t3 = dot2(as_f16x2(and_or(h2, HH, and_or(b0, H4, MW))), as_f16x2(px[3 * 8 + 2 * k]), t3);
+              t3 = dot2(as_f16x2(and_or(h82, HH, and_or(b8, H4, MW))), as_f16x2(px[3 * 8 + 2 * k + 1]), t3);
+            }
+            const float4 f = sc[lrow0 + r][s][hf * 2 + li];
+            acc[r] = __builtin_fmaf(f.x, t0, acc[r]);
+            acc[r] = __builtin_fmaf(f.y, t1, acc[r]);
+            acc[r] = __builtin_fmaf(f.z, t2, acc[r]);
+            acc[r] = __builtin_fmaf(f.w, t3, acc[r]);
+          }
+          const uint32_t inext = i + PF * LPR;
+          if (inext < nu) load(inext, qa[j], qb[j], qh[j]);
+        }
+      }
     }
   }
   store_rows<ACCUM, ROWS, LPR>(y, y_off, first, p.n_out, lane, acc);
 }
 
 // ---------------------------------------------------------------------------------------
-// Q8_0: lane step = 16 quants (half a block) per row; d is block u/2's f16 scale.
-// q as f16: (q ^ 0x80) is 0..255, so MAGIC | that = 1152 + q exactly.
+// Q8_0.  Lane step = 16 quants (half a block) of one row; the block scale d is staged per
+// (row, block) as f32.  q as f16: (q ^ 0x80) is 0..255, so MAGIC | that = 1152 + q.
+// LDS per pass: xq[unit] = 8 f16 pairs, xs[unit] = their sum, dd[row][block] = d.
 // ---------------------------------------------------------------------------------------
 template <int WAVES, int ACCUM, int ROWS, int MOE, int LPR>
 SK_DEV void matvec_q8_0_body(const uint4 *__restrict__ w, const uint16_t *__restrict__ wd,
-                             const float *x, float *y, const uint32_t *ids,
-                             const MatvecPush2 &p) {
+                             const float *x, float *y, const uint32_t *ids, const MatvecPush2 &p) {
+  using G = Geo<WAVES, ROWS, LPR>;
+  constexpr int NBLK = G::CH / 32;
+  __shared__ uint4 xq[2][G::CH / 16];  // component-major
+  __shared__ float xs[G::CH / 16];
+  __shared__ float dd[G::RWG][NBLK];
+
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = (tid & 63) % LPR;
   const uint32_t sub = (tid & 63) / LPR;
-  const uint32_t wave = blockIdx.x * WAVES + (tid >> 6);
-  const uint32_t first = (wave * (64 / LPR) + sub) * ROWS;
-  if (LPR == 64 && first >= p.n_out) return;
+  const uint32_t row0 = blockIdx.x * G::RWG;
+  const uint32_t lrow0 = ((tid >> 6) * G::SUBS + sub) * ROWS;
+  const uint32_t first = row0 + lrow0;
   const uint32_t slot = blockIdx.y;
   const uint32_t base = MOE ? ids[p.ids_off + slot] * p.n_out : 0;
-  const float *xs = x + p.x_off + slot * p.x_stride;
+  const float *xv = x + p.x_off + slot * p.x_stride;
   const uint32_t y_off = p.y_off + slot * p.y_stride;
-  const uint32_t chunks = p.n_in >> 4;
-  const uint32_t blocks = p.n_in >> 5;
+  const uint32_t chunks = p.n_in >> 4, blocks = p.n_in >> 5;
+  const uint32_t MW = MAGIC, M8 = 0x00ff00ffu;
 
-  uint32_t rq[ROWS], rd[ROWS];
+  const uint4 *qr[ROWS];
 #pragma unroll
-  for (int r = 0; r < ROWS; r++) {
-    const uint32_t row = base + min(first + r, p.n_out - 1);
-    rq[r] = p.o0 + row * chunks;
-    rd[r] = p.o1 + row * blocks;
-  }
+  for (int r = 0; r < ROWS; r++) qr[r] = w + p.o0 + (base + min(first + r, p.n_out - 1)) * chunks;
+
   float acc[ROWS];
 #pragma unroll
   for (int r = 0; r < ROWS; r++) acc[r] = 0.0f;
 
-  for (uint32_t c = lane; c < chunks; c += LPR) {
-    uint4 q[ROWS];
-    uint32_t dd[ROWS];
+  for (uint32_t k0 = 0; k0 < p.n_in; k0 += G::CH) {
+    const uint32_t nk = min(p.n_in - k0, (uint32_t)G::CH);
+    const uint32_t u0 = k0 >> 4, nu = nk >> 4, b0 = k0 >> 5, nb = nk >> 5;
+    auto x_unit = [&](uint32_t i, float4 (&v)[4]) {
+      const float *xp = xv + (u0 + i) * 16;
 #pragma unroll
-    for (int r = 0; r < ROWS; r++) {
-      q[r] = w[rq[r] + c];
-      dd[r] = wd[rd[r] + (c >> 1)];
-    }
-    float4 xv[4];
-#pragma unroll
-    for (int k = 0; k < 4; k++) xv[k] = ld_x4(xs + c * 16 + 4 * k);
-    f16x2 p02[4], p13[4];
-    const float xsum = x16_pairs(xv, p02, p13);
-#pragma unroll
-    for (int r = 0; r < ROWS; r++) {
-      float s = -1152.0f * xsum;
-      const uint32_t wv[4] = {q[r].x, q[r].y, q[r].z, q[r].w};
+      for (int k = 0; k < 4; k++) v[k] = *(const float4 *)(xp + 4 * k);
+    };
+    auto x_store = [&](uint32_t i, const float4 (&v)[4]) {
+      uint32_t pp[8];
+      const f16x2 one = {(f16)1.0f, (f16)1.0f};
+      float s = 0.0f;
 #pragma unroll
       for (int k = 0; k < 4; k++) {
-        const uint32_t b = wv[k] ^ 0x80808080u;
-        s = dot2(as_f16x2((b & 0x00ff00ffu) | MAGIC), p02[k], s);
-        s = dot2(as_f16x2(((b >> 8) & 0x00ff00ffu) | MAGIC), p13[k], s);
+        pp[2 * k] = pk(v[k].x, v[k].z);
+        pp[2 * k + 1] = pk(v[k].y, v[k].w);
+        s = dot2(as_f16x2(pp[2 * k]), one, s);
+        s = dot2(as_f16x2(pp[2 * k + 1]), one, s);
       }
-      acc[r] += f16_bits_to_f32(dd[r]) * s;
+      xq[0][i] = make_uint4(pp[0], pp[1], pp[2], pp[3]);
+      xq[1][i] = make_uint4(pp[4], pp[5], pp[6], pp[7]);
+      xs[i] = s;
+    };
+    const uint32_t n_items = (uint32_t)G::RWG * nb;
+    auto d_load = [&](uint32_t i) -> uint32_t {
+      const uint32_t lr = i / nb, bl = i % nb;
+      const uint32_t row = base + min(row0 + lr, p.n_out - 1);
+      return wd[p.o1 + row * blocks + b0 + bl];
+    };
+    if (k0 != 0) __syncthreads();
+    float4 xv4[4];
+    uint32_t dv0 = 0;
+    if (tid < nu) x_unit(tid, xv4);
+    if (tid < n_items) dv0 = d_load(tid);
+    constexpr int PF = 4;
+    uint4 q[PF][ROWS];
+#pragma unroll
+    for (int j = 0; j < PF; j++) {
+      const uint32_t i = lane + j * LPR;
+      if (i < nu) {
+#pragma unroll
+        for (int r = 0; r < ROWS; r++) q[j][r] = qr[r][u0 + i];
+      }
+    }
+    if (tid < nu) x_store(tid, xv4);
+    if (tid < n_items) dd[tid / nb][tid % nb] = f16_bits_to_f32(dv0);
+    for (uint32_t i = tid + G::NT; i < nu; i += G::NT) {
+      x_unit(i, xv4);
+      x_store(i, xv4);
+    }
+    for (uint32_t i = tid + G::NT; i < n_items; i += G::NT) dd[i / nb][i % nb] = f16_bits_to_f32(d_load(i));
+    __syncthreads();
+
+    for (uint32_t j0 = 0; lane + j0 * LPR < nu; j0 += PF) {
+#pragma unroll
+      for (int j = 0; j < PF; j++) {
+        const uint32_t i = lane + (j0 + j) * LPR;
+        if (i < nu) {
+          const uint4 x0 = xq[0][i], x1 = xq[1][i];
+          const uint32_t px[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+          const float bias = -1152.0f * xs[i];
+#pragma unroll
+          for (int r = 0; r < ROWS; r++) {
+            float s = bias;
+            const uint32_t wv[4] = {q[j][r].x, q[j][r].y, q[j][r].z, q[j][r].w};
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+              const uint32_t b = wv[k] ^ 0x80808080u;
+              s = dot2(as_f16x2(and_or(b, M8, MW)), as_f16x2(px[2 * k]), s);
+              s = dot2(as_f16x2(and_or(b >> 8, M8, MW)), as_f16x2(px[2 * k + 1]), s);
+            }
+            acc[r] = __builtin_fmaf(dd[lrow0 + r][i >> 1], s, acc[r]);
+          }
+          const uint32_t inext = i + PF * LPR;
+          if (inext < nu) {
+#pragma unroll
+            for (int r = 0; r < ROWS; r++) q[j][r] = qr[r][u0 + inext];
+          }
+        }
+      }
     }
   }
   store_rows<ACCUM, ROWS, LPR>(y, y_off, first, p.n_out, lane, acc);
 }
+
+}  // namespace
 
 // ---------------------------------------------------------------------------------------
 // Exported instantiations: symbol = <shader name>__<spec words joined by '_'>.

@@ -24,7 +24,7 @@ HALF_INPUTS = False     # GEMM inputs stay f32: the matmul stages them to f16 it
 HYBRID = False
 # per-backend matvec tactics (waves per workgroup, rows per wave); kernels.rs:10-14
 Q8_0_TACTIC = (4, 2)
-KQUANT_TACTIC = (2, 4)
+KQUANT_TACTIC = (4, 2)
 MATMUL_TILE_ROWS = 128
 EXPERT_LPR = (64, 32, 16)
 
