@@ -184,7 +184,8 @@ int skyla_hip_context_new(int device, skyla_hip_context **out) {
   if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
     return fail(SKYLA_HIP_E_DEVICE, "device %d is %s; this backend carries gfx950 code only",
                 device, prop.gcnArchName);
-  ctx->name = prop.name;
+  ctx->name = prop.name[0] ? prop.name : "AMD Instinct";
+  ctx->name += std::string(" (") + prop.gcnArchName + ", " + std::to_string(prop.multiProcessorCount) + " CUs)";
   ctx->warp = (uint32_t)prop.warpSize;
   HIP_TRY(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking));
   const unsigned char *images[] = {skyla_co_matvec, skyla_co_matmul, skyla_co_moe, skyla_co_util};
