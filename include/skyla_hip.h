@@ -57,10 +57,10 @@ uint32_t skyla_hip_subgroup_size(const skyla_hip_context *ctx);
 /* Context::max_buffer (weights.rs:62, arena.rs:149): 4 GiB, so u32 element offsets
  * of every binding type stay in range. */
 uint64_t skyla_hip_max_buffer(const skyla_hip_context *ctx);
-/* Context::device_name (engine.rs:71).  Writes a NUL-terminated name into out[cap]. */
+/* Context::device_name (skyla-vk/src/context.rs:169; engine.rs:71).  Writes a NUL-terminated name into out[cap]. */
 int skyla_hip_device_name(const skyla_hip_context *ctx, char *out, size_t cap);
 
-/* ---- Buffer (skyla-vk/src/buffer.rs:17-57, 65-73 alloc_host) ---- */
+/* ---- Buffer (skyla-vk/src/buffer.rs:6-35 Buffer; 49-62 max_buffer, alloc_host) ---- */
 
 /* Context::alloc_host: `size` bytes of HBM plus a host mirror the engine fills through
  * skyla_hip_buffer_host (Buffer::as_mut_slice / as_f32_mut / as_u32_mut).  HBM starts
@@ -83,7 +83,7 @@ void *skyla_hip_buffer_device(skyla_hip_buffer *buf);
 int skyla_hip_buffer_copy(skyla_hip_buffer *dst, uint64_t dst_off, const skyla_hip_buffer *src,
                           uint64_t src_off, uint64_t len);
 
-/* ---- Pipeline (skyla-vk/src/pipeline.rs:139-258; kernels.rs:60, 118-119) ---- */
+/* ---- Pipeline (skyla-vk/src/pipeline.rs:16-124; kernels.rs:60, 118-119) ---- */
 
 /* Context::create_pipeline_sets(shader, n_buffers, push_size, spec, n_sets).
  * `name` is the reference shader name (matvec_q4k, matvec_q6k, matvec_q8_0, matmul,
@@ -95,14 +95,14 @@ int skyla_hip_pipeline_new(skyla_hip_context *ctx, const char *name, uint32_t n_
                            uint32_t push_size, const uint32_t *spec, uint32_t n_spec,
                            uint32_t n_sets, skyla_hip_pipeline **out);
 void skyla_hip_pipeline_free(skyla_hip_pipeline *p);
-/* Pipeline::bind_set_buffers(set, buffers) (pipeline.rs:227-248); bind_buffers is set 0. */
+/* Pipeline::bind_set_buffers(set, buffers) (pipeline.rs:104-124); bind_buffers (:100) is set 0. */
 int skyla_hip_pipeline_bind(skyla_hip_pipeline *p, uint32_t set, skyla_hip_buffer *const *bufs,
                             uint32_t n);
 /* Threads per workgroup for this pipeline (the per-kernel shape table of
  * skyla-metal/src/pipeline.rs:14-24, made explicit). */
 int skyla_hip_pipeline_threads(const skyla_hip_pipeline *p, uint32_t out[3]);
 
-/* ---- Record / replay (skyla-vk/src/record.rs:293-393, 395-148) ---- */
+/* ---- Record / replay (skyla-vk/src/record.rs:8-57 Recording, Recorder; 83-148 record, replay, marks) ---- */
 
 /* Context::record(profile, f): begin, issue Recorder calls, end. */
 int skyla_hip_record_begin(skyla_hip_context *ctx, int profile, skyla_hip_recorder **out);

@@ -293,3 +293,44 @@ def test_softmax_silu_argmax():
     assert np.allclose(s, ref, rtol=1e-6)
     assert so.argmax(x) == 2                      # max_by keeps the last maximum
     assert abs(so.silu(1.5) - 1.5 / (1 + np.exp(-1.5))) < 1e-6
+
+
+# ---------------------------------------------------------------------------- off-path helpers
+def test_rmsnorm_closed_forms():
+    """ops.rs:1-16.  Constant x = c with eps = 0 gives r = 1/|c| exactly; a 3-4 pair gives
+    mean square 12.5; float64 agreement on random data (catches n-1, missing eps or sqrt)."""
+    w = np.linspace(-2, 2, 64).astype(np.float32)
+    got = so.rmsnorm(np.full(64, 2.0, np.float32), w, 0.0)
+    assert np.array_equal(got, w)                          # 2 * 0.5 * w, exact
+    got = so.rmsnorm(np.array([3.0, 4.0], np.float32), np.ones(2, np.float32), 0.0)
+    assert np.allclose(got, np.array([3.0, 4.0]) / np.sqrt(12.5), rtol=2e-7)
+    x = synth.rng("oracle", "rms").standard_normal(4096).astype(np.float32)
+    w = synth.rng("oracle", "rmsw").standard_normal(4096).astype(np.float32)
+    want = x.astype(np.float64) / np.sqrt(np.mean(x.astype(np.float64) ** 2) + 1e-6) * w
+    assert np.allclose(so.rmsnorm(x, w, 1e-6), want, rtol=1e-5, atol=1e-6)
+
+
+def test_quantize_q8_0_rounding_and_round_trip():
+    """quant.rs:91-101: d = amax/127 stored as f16, q = round-half-away(x/d) clamped to
+    +-127; ragged tails quantise the values they have; a zero block has d = 0."""
+    x = np.zeros(40, np.float32)
+    x[0], x[1], x[2], x[3] = 127.0, 2.5, -2.5, 0.49
+    x[32:] = [-8.0, 4.0, 0, 0, 0, 0, 0, 1.0]                # second, ragged block: amax 8
+    b = so.quantize_q8_0(x)
+    assert b.size == 2 * 34
+    assert b[:2].view("<f2")[0] == 1.0                     # d = 127/127
+    q = b[2:34].view(np.int8)
+    assert list(q[:4]) == [127, 3, -3, 0]                  # half away from zero
+    d2 = float(b[34:36].view("<f2")[0])
+    assert d2 == float(np.float16(8.0 / 127.0))
+    q2 = b[36:44].view(np.int8)
+    assert q2[0] == -127 and q2[1] == round(4.0 * (127.0 / 8.0))
+    assert not b[44:].any()                                # bytes past the tail untouched
+    z = so.quantize_q8_0(np.zeros(32, np.float32))
+    assert not z.any()
+    r = synth.rng("oracle", "q8rt").standard_normal(32 * 64).astype(np.float32)
+    back = so.dequantize(int(DType.Q8_0), so.quantize_q8_0(r), r.size)
+    d = np.abs(r.reshape(-1, 32)).max(1).astype(np.float64) / 127.0
+    d16 = d.astype(np.float16).astype(np.float64)           # the stored scale
+    bound = np.repeat(0.5 * d + 127.0 * np.abs(d16 - d), 32) * 1.001 + 1e-7
+    assert np.all(np.abs(back.astype(np.float64) - r) <= bound)
