@@ -306,16 +306,17 @@ def main() -> int:
 
     # dominant kernel: matvec_q4k (Q, K, V, O, gate, up); events around its launches only
     q4k_names = ("q", "k", "v", "o", "gate", "up")
+    # (a launch may carry several fused dispatches: q/k/v and gate/up each run as one)
     rq = w.record(only=q4k_names)
     _, dq = time_replays(ctx, rq, 3, 5)
-    n_launch = len(rq)
+    n_launch = rq.launches()
     q4k_ns = float(np.median(dq)) / n_launch
     q4k_bytes = w.bytes_of(q4k_names) / n_launch
     rq.free()
     rd = w.record(only=("down",))
     _, dd = time_replays(ctx, rd, 3, 5)
-    q6k_ns = float(np.median(dd)) / len(rd)
-    q6k_bytes = w.bytes_of(("down",)) / len(rd)
+    q6k_ns = float(np.median(dd)) / rd.launches()
+    q6k_bytes = w.bytes_of(("down",)) / rd.launches()
     rd.free()
     achieved = q4k_bytes / q4k_ns  # GB/s
     log(f"matvec_q4k avg {q4k_ns / 1e3:.2f} us/launch, {achieved:.0f} GB/s; "
@@ -332,11 +333,15 @@ def main() -> int:
     if cpu:
         log(f"cpu baseline {cpu['value']} GB/s on {cpu['cores']} threads")
 
+    # HBM bytes of the matvec_q4k launches of one layer, measured with rocprofv3 PMC
+    # (FETCH_SIZE / WRITE_SIZE scaled by known-size kernels), spread over this run's launches
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "matvec_q4k_qwen3_8b_decode_traffic.json")
     if os.path.exists(tpath):
         with open(tpath) as fh:
-            traffic = json.load(fh).get("bytes_per_launch")
+            per_layer = json.load(fh).get("bytes_per_layer")
+        if per_layer:
+            traffic = round(per_layer * args.layers / n_launch)
 
     line = {
         "metric": "Q4_K matvec HBM GB/s (% of peak) + decode tok/s, Qwen3-8B shapes, 1 GPU",
@@ -354,6 +359,7 @@ def main() -> int:
         "config": {"workload": "config 2: Qwen3-8B decode matvecs x 36 layers (Q,K,V,O,gate,up Q4_K; "
                                "down Q6_K), one HBM copy of the weights per layer",
                    "layers": args.layers, "dispatches_per_step": len(step),
+                   "launches_per_step": step.launches(),
                    "replay": "direct launches" if EAGER else "one HIP graph per step",
                    "weight_bytes": w.weight_bytes, "algorithmic_bytes_per_step": w.step_bytes},
         "pct_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1),
@@ -362,7 +368,7 @@ def main() -> int:
         "roofline": {"bound": "hbm", "kernel": "matvec_q4k", "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic, "algorithmic_bytes_per_launch": round(q4k_bytes),
-                     "avg_launch_us": round(q4k_ns / 1e3, 3)},
+                     "avg_launch_us": round(q4k_ns / 1e3, 3), "launches_per_layer": n_launch / args.layers},
         "matvec_q6k": {"avg_launch_us": round(q6k_ns / 1e3, 3), "gbs": round(q6k_bytes / q6k_ns, 1)},
         "hbm_probe_gbs": round(probe, 1),
         "parity_rel_l2": parity,

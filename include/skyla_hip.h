@@ -121,6 +121,12 @@ int skyla_hip_record_end(skyla_hip_recorder *r, skyla_hip_recording **out);
 void skyla_hip_recording_free(skyla_hip_recording *rec);
 /* Number of dispatches in a recording. */
 uint32_t skyla_hip_recording_len(const skyla_hip_recording *rec);
+/* Number of kernel launches a replay makes (no counterpart in the reference, whose
+ * Vulkan command buffer issues one dispatch per Recorder::dispatch).  Consecutive
+ * dispatches of one matvec pipeline with no barrier between them, which the engine's
+ * contract makes independent, are fused into one launch over their combined rows
+ * (at most 4; environment SKYLA_HIP_FUSE=0 turns this off).  Profilers see launches. */
+uint32_t skyla_hip_recording_launches(const skyla_hip_recording *rec);
 
 /* Context::replay: run the recording (as one HIP graph) and wait for it. */
 int skyla_hip_replay(skyla_hip_context *ctx, const skyla_hip_recording *rec);

@@ -51,6 +51,37 @@ SK_DEV float group_sum(float v) {
 SK_DEV uint32_t ctl_word(const uint32_t *ctl, uint32_t i) { return ctl[i]; }
 
 // ---------------------------------------------------------------------------------------
+// Segmented launch.  Dispatches of one pipeline that the engine records with no barrier
+// between them are independent (a barrier is how it orders them), so the runtime fuses up
+// to MAXSEG of them into one launch: grid.x is the sum of their grid.x, and block b runs
+// segment s = number of start[1..] <= b with its own push words, at block b - start[s].
+// A single dispatch is the one-segment case.  Unused starts are 0xffffffff.
+// ---------------------------------------------------------------------------------------
+constexpr int MAXSEG = 4;
+
+template <typename P>
+struct Segments {
+  uint32_t n;
+  uint32_t start[MAXSEG];
+  P p[MAXSEG];
+};
+
+template <typename P>
+SK_DEV uint32_t segment_of(const Segments<P> &m, uint32_t b) {
+  return (uint32_t)(b >= m.start[1]) + (uint32_t)(b >= m.start[2]) + (uint32_t)(b >= m.start[3]);
+}
+
+// push words of segment s (wave-uniform), selected without indexing the argument array
+template <typename P>
+SK_DEV P segment_push(const Segments<P> &m, uint32_t s) {
+  P r = m.p[0];
+  if (s == 1) r = m.p[1];
+  if (s == 2) r = m.p[2];
+  if (s == 3) r = m.p[3];
+  return r;
+}
+
+// ---------------------------------------------------------------------------------------
 // Bit-exact dequantisation of one 32-value group, in the reference's operation order.
 // FP contraction is switched off inside these bodies: Rust never fuses a*b-c.
 // ---------------------------------------------------------------------------------------

@@ -102,7 +102,7 @@ struct Geo {
 // ---------------------------------------------------------------------------------------
 template <int WAVES, int ACCUM, int ROWS, int MOE, int LPR>
 SK_DEV void matvec_q4k_body(const uint4 *__restrict__ w, const float *x, float *y,
-                            const uint32_t *ids, const MatvecPush2 &p) {
+                            const uint32_t *ids, const MatvecPush2 &p, uint32_t bx) {
   using G = Geo<WAVES, ROWS, LPR>;
   __shared__ uint4 xq[4][G::CH / 32];  // component-major: lanes read consecutive 16 B
   __shared__ float2 xs[G::CH / 32];
@@ -111,7 +111,7 @@ SK_DEV void matvec_q4k_body(const uint4 *__restrict__ w, const float *x, float *
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = (tid & 63) % LPR;
   const uint32_t sub = (tid & 63) / LPR;
-  const uint32_t row0 = blockIdx.x * G::RWG;
+  const uint32_t row0 = bx * G::RWG;
   const uint32_t lrow0 = ((tid >> 6) * G::SUBS + sub) * ROWS;  // first row of this group in the WG
   const uint32_t first = row0 + lrow0;
   const uint32_t slot = blockIdx.y;
@@ -262,7 +262,8 @@ SK_DEV void matvec_q4k_body(const uint4 *__restrict__ w, const float *x, float *
 // ---------------------------------------------------------------------------------------
 template <int WAVES, int ACCUM, int ROWS, int MOE, int LPR>
 SK_DEV void matvec_q6k_body(const uint4 *__restrict__ w, const uint16_t *__restrict__ wd,
-                            const float *x, float *y, const uint32_t *ids, const MatvecPush4 &p) {
+                            const float *x, float *y, const uint32_t *ids, const MatvecPush4 &p,
+                            uint32_t bx) {
   using G = Geo<WAVES, ROWS, LPR>;
   __shared__ uint4 xq[8][G::CH / 64];  // component-major
   __shared__ float4 xs[G::CH / 64];
@@ -271,7 +272,7 @@ SK_DEV void matvec_q6k_body(const uint4 *__restrict__ w, const uint16_t *__restr
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = (tid & 63) % LPR;
   const uint32_t sub = (tid & 63) / LPR;
-  const uint32_t row0 = blockIdx.x * G::RWG;
+  const uint32_t row0 = bx * G::RWG;
   const uint32_t lrow0 = ((tid >> 6) * G::SUBS + sub) * ROWS;
   const uint32_t first = row0 + lrow0;
   const uint32_t slot = blockIdx.y;
@@ -440,7 +441,8 @@ SK_DEV void matvec_q6k_body(const uint4 *__restrict__ w, const uint16_t *__restr
 // ---------------------------------------------------------------------------------------
 template <int WAVES, int ACCUM, int ROWS, int MOE, int LPR>
 SK_DEV void matvec_q8_0_body(const uint4 *__restrict__ w, const uint16_t *__restrict__ wd,
-                             const float *x, float *y, const uint32_t *ids, const MatvecPush2 &p) {
+                             const float *x, float *y, const uint32_t *ids, const MatvecPush2 &p,
+                             uint32_t bx) {
   using G = Geo<WAVES, ROWS, LPR>;
   constexpr int NBLK = G::CH / 32;
   __shared__ uint4 xq[2][G::CH / 16];  // component-major
@@ -450,7 +452,7 @@ SK_DEV void matvec_q8_0_body(const uint4 *__restrict__ w, const uint16_t *__rest
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = (tid & 63) % LPR;
   const uint32_t sub = (tid & 63) / LPR;
-  const uint32_t row0 = blockIdx.x * G::RWG;
+  const uint32_t row0 = bx * G::RWG;
   const uint32_t lrow0 = ((tid >> 6) * G::SUBS + sub) * ROWS;
   const uint32_t first = row0 + lrow0;
   const uint32_t slot = blockIdx.y;
@@ -556,24 +558,28 @@ SK_DEV void matvec_q8_0_body(const uint4 *__restrict__ w, const uint16_t *__rest
 }  // namespace
 
 // ---------------------------------------------------------------------------------------
-// Exported instantiations: symbol = <shader name>__<spec words joined by '_'>.
+// Exported instantiations: symbol = <shader name>__<spec words joined by '_'>.  Each takes
+// the push words as a segment table (Segments, common.h), which the runtime builds.
 // ---------------------------------------------------------------------------------------
 #define MV_Q4K(W, A, R, M, L)                                                                \
   extern "C" __global__ __launch_bounds__(64 * W) void matvec_q4k__##W##_##A##_##R##_##M##_##L( \
-      const uint4 *w, const float *x, float *y, const uint32_t *ids, MatvecPush2 p) {        \
-    matvec_q4k_body<W, A, R, M, L>(w, x, y, ids, p);                                         \
+      const uint4 *w, const float *x, float *y, const uint32_t *ids, Segments<MatvecPush2> m) { \
+    const uint32_t s = segment_of(m, blockIdx.x);                                            \
+    matvec_q4k_body<W, A, R, M, L>(w, x, y, ids, segment_push(m, s), blockIdx.x - m.start[s]); \
   }
 #define MV_Q6K(W, A, R, M, L)                                                                \
   extern "C" __global__ __launch_bounds__(64 * W) void matvec_q6k__##W##_##A##_##R##_##M##_##L( \
       const uint4 *w, const uint16_t *wd, const float *x, float *y, const uint32_t *ids,     \
-      MatvecPush4 p) {                                                                       \
-    matvec_q6k_body<W, A, R, M, L>(w, wd, x, y, ids, p);                                     \
+      Segments<MatvecPush4> m) {                                                             \
+    const uint32_t s = segment_of(m, blockIdx.x);                                            \
+    matvec_q6k_body<W, A, R, M, L>(w, wd, x, y, ids, segment_push(m, s), blockIdx.x - m.start[s]); \
   }
 #define MV_Q8_0(W, A, R, M, L)                                                                \
   extern "C" __global__ __launch_bounds__(64 * W) void matvec_q8_0__##W##_##A##_##R##_##M##_##L( \
       const uint4 *w, const uint16_t *wd, const float *x, float *y, const uint32_t *ids,      \
-      MatvecPush2 p) {                                                                        \
-    matvec_q8_0_body<W, A, R, M, L>(w, wd, x, y, ids, p);                                     \
+      Segments<MatvecPush2> m) {                                                              \
+    const uint32_t s = segment_of(m, blockIdx.x);                                             \
+    matvec_q8_0_body<W, A, R, M, L>(w, wd, x, y, ids, segment_push(m, s), blockIdx.x - m.start[s]); \
   }
 
 // dense (MOE = 0, LPR = 64) and expert (ACCUM = 0, MOE = 1, LPR in {64, 32, 16})

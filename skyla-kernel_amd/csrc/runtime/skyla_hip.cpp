@@ -10,12 +10,17 @@
 //     capturing the list on the context stream), so a decode step costs one submission
 //     instead of one per kernel; a profiled recording replays eagerly with a HIP event
 //     after every mark.
+//   * Dispatches the engine records with no barrier between them are independent.  Runs of
+//     such dispatches of one matvec pipeline (q/k/v, gate/up, an expert's gate/up) become
+//     one launch over their combined rows: each kernel launch on MI355X carries ~1.7 us of
+//     fixed cost and a ramp-up/drain, which dominate the small decode matrices.
 //   * Buffers are HBM allocations with a host mirror that the caller synchronises
 //     explicitly (the reference's buffers are host-coherent; a discrete GPU's are not).
 #include "../../../include/skyla_hip.h"
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -63,21 +68,22 @@ struct KernelInfo {
   uint32_t spec_len_min, spec_len_max;
   int threads_from_spec;  // -1: fixed 256; k >= 0: 64 * spec[k] (matvec waves) or spec[k]
   bool waves;
+  bool segmented;  // takes its push words as a segment table (kernels/common.h Segments)
 };
 
 const KernelInfo kKernels[] = {
-    {"matvec_q4k", 4, 9, 5, 5, 0, true},
-    {"matvec_q6k", 5, 11, 5, 5, 0, true},
-    {"matvec_q8_0", 5, 9, 5, 5, 0, true},
-    {"matmul", 5, 13, 3, 4, -1, false},
-    {"moe_logits", 3, 5, 0, 0, -1, false},
-    {"moe_route", 2, 5, 0, 0, -1, false},
-    {"moe_sort", 1, 5, 0, 0, -1, false},
-    {"moe_combine", 1, 6, 0, 0, -1, false},
-    {"silu_mul", 2, 4, 0, 0, -1, false},
-    {"to_half", 3, 6, 0, 0, -1, false},
-    {"bandwidth", 2, 1, 1, 1, 0, false},
-    {"dequant", 3, 7, 1, 1, -1, false},
+    {"matvec_q4k", 4, 9, 5, 5, 0, true, true},
+    {"matvec_q6k", 5, 11, 5, 5, 0, true, true},
+    {"matvec_q8_0", 5, 9, 5, 5, 0, true, true},
+    {"matmul", 5, 13, 3, 4, -1, false, false},
+    {"moe_logits", 3, 5, 0, 0, -1, false, false},
+    {"moe_route", 2, 5, 0, 0, -1, false, false},
+    {"moe_sort", 1, 5, 0, 0, -1, false, false},
+    {"moe_combine", 1, 6, 0, 0, -1, false, false},
+    {"silu_mul", 2, 4, 0, 0, -1, false, false},
+    {"to_half", 3, 6, 0, 0, -1, false, false},
+    {"bandwidth", 2, 1, 1, 1, 0, false, false},
+    {"dequant", 3, 7, 1, 1, -1, false, false},
 };
 
 const KernelInfo *find_kernel(const char *name) {
@@ -110,6 +116,7 @@ struct skyla_hip_pipeline {
   uint32_t n_buffers = 0;
   uint32_t push_words = 0;
   uint32_t threads = 256;
+  bool segmented = false;
   std::vector<std::vector<void *>> sets;
 };
 
@@ -119,19 +126,105 @@ struct Command {
   enum Kind { Dispatch, Barrier, Mark } kind;
   hipFunction_t fn = nullptr;
   uint32_t threads = 0;
+  bool segmented = false;
   uint32_t groups[3] = {0, 0, 0};
   std::vector<void *> bufs;
   std::vector<uint32_t> push;
   std::string label;
 };
 
-int launch(hipStream_t stream, const Command &c) {
+// One kernel launch (or a mark) of a recording.  `args` is the by-value argument after the
+// binding pointers: the push words, or for segmented kernels the segment table
+// {n, start[kMaxSeg], push[kMaxSeg][words]} of kernels/common.h.
+struct Launch {
+  bool mark = false;
+  hipFunction_t fn = nullptr;
+  uint32_t threads = 0;
+  uint32_t groups[3] = {0, 0, 0};
+  std::vector<void *> bufs;
+  std::vector<uint32_t> args;
+};
+
+constexpr uint32_t kMaxSeg = 4;  // MAXSEG in kernels/common.h
+
+// Packs consecutive dispatches of one segmented kernel into one launch.
+Launch pack(const Command *const *run, uint32_t n) {
+  Launch l;
+  const Command &a = *run[0];
+  l.fn = a.fn;
+  l.threads = a.threads;
+  l.bufs = a.bufs;
+  if (!a.segmented) {
+    for (int i = 0; i < 3; i++) l.groups[i] = a.groups[i];
+    l.args = a.push;
+    return l;
+  }
+  const size_t w = a.push.size();
+  l.args.assign(1 + kMaxSeg + kMaxSeg * w, 0u);
+  l.args[0] = n;
+  uint32_t x = 0;
+  for (uint32_t i = 0; i < kMaxSeg; i++) {
+    l.args[1 + i] = i < n ? x : 0xffffffffu;
+    if (i < n) {
+      std::copy(run[i]->push.begin(), run[i]->push.end(), l.args.begin() + 1 + kMaxSeg + i * w);
+      x += run[i]->groups[0];
+    }
+  }
+  l.groups[0] = x;
+  l.groups[1] = a.groups[1];
+  l.groups[2] = a.groups[2];
+  return l;
+}
+
+// Can dispatch c join a fused launch that starts with dispatch a and holds `x` blocks?
+// (Dispatches between two barriers are independent; same kernel, bindings and grid y/z.)
+bool fusable(const Command &a, const Command &c, uint64_t x) {
+  return a.segmented && c.kind == Command::Dispatch && c.fn == a.fn && c.bufs == a.bufs &&
+         c.threads == a.threads && c.groups[1] == a.groups[1] && c.groups[2] == a.groups[2] &&
+         x + c.groups[0] <= 0x7fffffffu;
+}
+
+// The launch list of a recording.  Barriers need no command of their own: launches on one
+// stream (and the nodes of a graph captured from it) run in order.  SKYLA_HIP_FUSE=0 keeps
+// one launch per dispatch.
+std::vector<Launch> build_launches(const std::vector<Command> &cmds) {
+  const char *env = std::getenv("SKYLA_HIP_FUSE");
+  const bool fuse = !(env && env[0] == '0');
+  std::vector<Launch> out;
+  for (size_t i = 0; i < cmds.size();) {
+    const Command &a = cmds[i];
+    if (a.kind == Command::Mark) {
+      Launch m;
+      m.mark = true;
+      out.push_back(std::move(m));
+      i++;
+      continue;
+    }
+    if (a.kind != Command::Dispatch) {
+      i++;
+      continue;
+    }
+    const Command *run[kMaxSeg] = {&a};
+    uint32_t n = 1;
+    uint64_t x = a.groups[0];
+    while (fuse && n < kMaxSeg && i + n < cmds.size() && fusable(a, cmds[i + n], x)) {
+      run[n] = &cmds[i + n];
+      x += cmds[i + n].groups[0];
+      n++;
+    }
+    out.push_back(pack(run, n));
+    i += n;
+  }
+  return out;
+}
+
+int launch(hipStream_t stream, const Launch &l) {
   // kernel parameters: binding pointers in order, then the push struct by value
   std::vector<void *> params;
-  params.reserve(c.bufs.size() + 1);
-  for (void *const &p : c.bufs) params.push_back(const_cast<void **>(&p));
-  params.push_back(const_cast<uint32_t *>(c.push.data()));
-  HIP_TRY(hipModuleLaunchKernel(c.fn, c.groups[0], c.groups[1], c.groups[2], c.threads, 1, 1, 0,
+  params.reserve(l.bufs.size() + 1);
+  for (void *const &p : l.bufs) params.push_back(const_cast<void **>(&p));
+  params.push_back(const_cast<uint32_t *>(l.args.data()));
+  HIP_TRY(hipModuleLaunchKernel(l.fn, l.groups[0], l.groups[1], l.groups[2], l.threads, 1, 1, 0,
                                 stream, params.data(), nullptr));
   return SKYLA_HIP_OK;
 }
@@ -151,6 +244,7 @@ struct skyla_hip_recording {
   skyla_hip_context *ctx = nullptr;
   bool profile = false;
   std::vector<Command> cmds;
+  std::vector<Launch> launches;
   hipGraphExec_t exec = nullptr;
   hipGraph_t graph = nullptr;
   std::vector<std::string> labels;
@@ -350,6 +444,7 @@ int skyla_hip_pipeline_new(skyla_hip_context *ctx, const char *name, uint32_t n_
   p->n_buffers = n_buffers;
   p->push_words = k->push_words;
   p->threads = threads;
+  p->segmented = k->segmented;
   p->sets.assign(n_sets, std::vector<void *>(n_buffers, nullptr));
   HIP_TRY(hipSetDevice(ctx->device));
   for (hipModule_t m : ctx->modules) {
@@ -438,6 +533,7 @@ int skyla_hip_record_dispatch(skyla_hip_recorder *r, const skyla_hip_pipeline *p
   c.kind = Command::Dispatch;
   c.fn = p->fn;
   c.threads = p->threads;
+  c.segmented = p->segmented;
   for (int i = 0; i < 3; i++) c.groups[i] = groups[i];
   c.bufs = p->sets[set];
   c.push.assign(push, push + n_push);
@@ -486,6 +582,7 @@ int skyla_hip_record_end(skyla_hip_recorder *r, skyla_hip_recording **out) {
   rec->cmds = std::move(r->cmds);
   for (const Command &c : rec->cmds)
     if (c.kind == Command::Mark) rec->labels.push_back(c.label);
+  rec->launches = build_launches(rec->cmds);
   rec->mark_ns.assign(rec->labels.size(), 0.0);
   if (!rec->profile && skyla_hip_recording_len(rec.get()) > 0) {
     // One graph for the whole recording, captured from the launch list on the stream.
@@ -493,8 +590,8 @@ int skyla_hip_record_end(skyla_hip_recorder *r, skyla_hip_recording **out) {
     HIP_TRY(hipSetDevice(ctx->device));
     HIP_TRY(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
     int s = SKYLA_HIP_OK;
-    for (const Command &c : rec->cmds)
-      if (c.kind == Command::Dispatch && (s = launch(ctx->stream, c)) != SKYLA_HIP_OK) break;
+    for (const Launch &l : rec->launches)
+      if (!l.mark && (s = launch(ctx->stream, l)) != SKYLA_HIP_OK) break;
     hipGraph_t graph = nullptr;
     hipError_t e = hipStreamEndCapture(ctx->stream, &graph);
     if (s != SKYLA_HIP_OK) {
@@ -533,6 +630,13 @@ uint32_t skyla_hip_recording_len(const skyla_hip_recording *rec) {
   return n;
 }
 
+uint32_t skyla_hip_recording_launches(const skyla_hip_recording *rec) {
+  if (!rec) return 0;
+  uint32_t n = 0;
+  for (const Launch &l : rec->launches) n += !l.mark;
+  return n;
+}
+
 namespace {
 
 // Launches a recording on the context stream.  With `events`, one event is recorded at
@@ -544,11 +648,11 @@ static int submit(skyla_hip_context *ctx, const skyla_hip_recording *rec, std::v
   }
   if (events) HIP_TRY(hipEventRecord((*events)[0], ctx->stream));
   size_t m = 1;
-  for (const Command &c : rec->cmds) {
-    if (c.kind == Command::Dispatch) {
-      int s = launch(ctx->stream, c);
+  for (const Launch &l : rec->launches) {
+    if (!l.mark) {
+      int s = launch(ctx->stream, l);
       if (s) return s;
-    } else if (c.kind == Command::Mark && events) {
+    } else if (events) {
       HIP_TRY(hipEventRecord((*events)[m++], ctx->stream));
     }
   }
@@ -641,15 +745,18 @@ int skyla_hip_time_dispatch(skyla_hip_context *ctx, const skyla_hip_pipeline *p,
   c.kind = Command::Dispatch;
   c.fn = p->fn;
   c.threads = p->threads;
+  c.segmented = p->segmented;
   for (int i = 0; i < 3; i++) c.groups[i] = groups[i];
   c.bufs = p->sets[0];
   c.push.assign(push, push + n_push);
+  const Command *one[1] = {&c};
+  const Launch l = pack(one, 1);
   Events e;
   int s = e.make(reps + 1);
   if (s) return s;
   HIP_TRY(hipEventRecord(e.ev[0], ctx->stream));
   for (uint32_t i = 0; i < reps; i++) {
-    s = launch(ctx->stream, c);
+    s = launch(ctx->stream, l);
     if (s) return s;
     HIP_TRY(hipEventRecord(e.ev[i + 1], ctx->stream));
   }

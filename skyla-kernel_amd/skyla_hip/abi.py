@@ -51,6 +51,7 @@ SIGNATURES = [
     ("skyla_hip_record_end", C.c_int, [_vp, C.POINTER(_vp)]),
     ("skyla_hip_recording_free", None, [_vp]),
     ("skyla_hip_recording_len", C.c_uint32, [_vp]),
+    ("skyla_hip_recording_launches", C.c_uint32, [_vp]),
     ("skyla_hip_replay", C.c_int, [_vp, _vp]),
     ("skyla_hip_replay_timed", C.c_int, [_vp, _vp, C.POINTER(C.c_double)]),
     ("skyla_hip_marks", C.c_int,
@@ -191,6 +192,10 @@ class Recording:
 
     def __len__(self) -> int:
         return _lib.skyla_hip_recording_len(self._h)
+
+    def launches(self) -> int:
+        """Kernel launches per replay (fused runs of independent dispatches count once)."""
+        return _lib.skyla_hip_recording_launches(self._h)
 
     def free(self) -> None:
         if self._h:
