@@ -607,3 +607,12 @@ SK_DEV void matvec_q8_0_body(const uint4 *__restrict__ w, const uint16_t *__rest
 MV_ALL_TACTICS(MV_Q4K)
 MV_ALL_TACTICS(MV_Q6K)
 MV_ALL_TACTICS(MV_Q8_0)
+
+// Dense variants with fewer lanes per row (more pipelined steps per lane) that the runtime
+// picks for large launches (skyla_hip.cpp, choose_variant).
+MV_Q4K(8, 0, 1, 0, 16)
+MV_Q4K(8, 1, 1, 0, 16)
+MV_Q6K(4, 0, 1, 0, 32)
+MV_Q6K(4, 1, 1, 0, 32)
+MV_Q6K(4, 0, 1, 0, 16)
+MV_Q6K(4, 1, 1, 0, 16)

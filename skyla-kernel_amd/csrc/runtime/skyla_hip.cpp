@@ -109,6 +109,19 @@ struct skyla_hip_buffer {
   uint64_t size = 0;
 };
 
+// Alternative gfx950 variants of a dense matvec pipeline (same push layout, different
+// rows per workgroup) and the launch sizes they serve best.  A launch of `rows` output
+// rows in total uses the first alternative whose min_rows <= rows.
+struct MatvecAlt {
+  hipFunction_t fn;
+  uint32_t rwg, threads;
+  uint64_t min_rows;
+};
+struct Retile {
+  uint32_t n_out_word;  // index of n_out in the push words
+  std::vector<MatvecAlt> alts;
+};
+
 struct skyla_hip_pipeline {
   skyla_hip_context *ctx = nullptr;
   std::string symbol;
@@ -117,6 +130,7 @@ struct skyla_hip_pipeline {
   uint32_t push_words = 0;
   uint32_t threads = 256;
   bool segmented = false;
+  std::shared_ptr<const Retile> retile;  // dense matvec pipelines only
   std::vector<std::vector<void *>> sets;
 };
 
@@ -127,6 +141,7 @@ struct Command {
   hipFunction_t fn = nullptr;
   uint32_t threads = 0;
   bool segmented = false;
+  std::shared_ptr<const Retile> retile;
   uint32_t groups[3] = {0, 0, 0};
   std::vector<void *> bufs;
   std::vector<uint32_t> push;
@@ -160,6 +175,22 @@ Launch pack(const Command *const *run, uint32_t n) {
     return l;
   }
   const size_t w = a.push.size();
+  // a dense matvec launch may run on the variant that suits its total size; the grid is
+  // then recomputed from each segment's n_out (every row is still computed exactly once)
+  const MatvecAlt *alt = nullptr;
+  if (a.retile) {
+    uint64_t rows = 0;
+    for (uint32_t i = 0; i < n; i++) rows += run[i]->push[a.retile->n_out_word];
+    for (const MatvecAlt &v : a.retile->alts)
+      if (rows >= v.min_rows) {
+        alt = &v;
+        break;
+      }
+  }
+  if (alt) {
+    l.fn = alt->fn;
+    l.threads = alt->threads;
+  }
   l.args.assign(1 + kMaxSeg + kMaxSeg * w, 0u);
   l.args[0] = n;
   uint32_t x = 0;
@@ -167,7 +198,7 @@ Launch pack(const Command *const *run, uint32_t n) {
     l.args[1 + i] = i < n ? x : 0xffffffffu;
     if (i < n) {
       std::copy(run[i]->push.begin(), run[i]->push.end(), l.args.begin() + 1 + kMaxSeg + i * w);
-      x += run[i]->groups[0];
+      x += alt ? (run[i]->push[a.retile->n_out_word] + alt->rwg - 1) / alt->rwg : run[i]->groups[0];
     }
   }
   l.groups[0] = x;
@@ -180,6 +211,7 @@ Launch pack(const Command *const *run, uint32_t n) {
 // (Dispatches between two barriers are independent; same kernel, bindings and grid y/z.)
 bool fusable(const Command &a, const Command &c, uint64_t x) {
   return a.segmented && c.kind == Command::Dispatch && c.fn == a.fn && c.bufs == a.bufs &&
+         c.retile == a.retile &&
          c.threads == a.threads && c.groups[1] == a.groups[1] && c.groups[2] == a.groups[2] &&
          x + c.groups[0] <= 0x7fffffffu;
 }
@@ -251,6 +283,56 @@ struct skyla_hip_recording {
   std::vector<double> mark_ns;
   bool replayed = false;
 };
+
+namespace {
+
+hipFunction_t find_function(skyla_hip_context *ctx, const std::string &sym) {
+  for (hipModule_t m : ctx->modules) {
+    hipFunction_t fn = nullptr;
+    if (hipModuleGetFunction(&fn, m, sym.c_str()) == hipSuccess && fn) return fn;
+  }
+  (void)hipGetLastError();  // lookups that missed leave a sticky error behind
+  return nullptr;
+}
+
+// Variant choice for dense matvec launches, from sweeps of the Qwen3-8B decode shapes on
+// MI355X (n_in 4096 and 12288): large launches gain from fewer lanes per row (more
+// pipelined load steps per lane); small ones from more rows per lane.  Each entry is
+// (min_rows, waves, rows, lanes per row).
+struct VariantRule {
+  const char *name;
+  uint32_t n_out_word;
+  struct { uint64_t min_rows; uint32_t waves, rows, lpr; } v[3];
+  int n;
+};
+const VariantRule kVariantRules[] = {
+    {"matvec_q4k", 5, {{6144, 8, 1, 16}, {0, 4, 2, 64}}, 2},
+    {"matvec_q6k", 7, {{12288, 4, 1, 16}, {0, 4, 1, 32}}, 2},
+};
+
+std::shared_ptr<const Retile> make_retile(skyla_hip_context *ctx, const char *name, const uint32_t *spec,
+                                          uint32_t n_spec) {
+  if (n_spec != 5 || spec[3] != 0) return nullptr;  // dense pipelines only (MOE = 0)
+  if (const char *env = std::getenv("SKYLA_HIP_RETILE"); env && env[0] == '0') return nullptr;
+  for (const VariantRule &r : kVariantRules) {
+    if (std::strcmp(r.name, name) != 0) continue;
+    auto t = std::make_shared<Retile>();
+    t->n_out_word = r.n_out_word;
+    for (int i = 0; i < r.n; i++) {
+      const auto &v = r.v[i];
+      const std::string sym = std::string(name) + "__" + std::to_string(v.waves) + "_" +
+                              std::to_string(spec[1]) + "_" + std::to_string(v.rows) + "_0_" +
+                              std::to_string(v.lpr);
+      hipFunction_t fn = find_function(ctx, sym);
+      if (!fn) return nullptr;  // keep the engine's variant if any alternative is missing
+      t->alts.push_back({fn, v.waves * v.rows * (64 / v.lpr), 64 * v.waves, v.min_rows});
+    }
+    return t;
+  }
+  return nullptr;
+}
+
+}  // namespace
 
 extern "C" {
 
@@ -457,6 +539,7 @@ int skyla_hip_pipeline_new(skyla_hip_context *ctx, const char *name, uint32_t n_
   (void)hipGetLastError();  // lookups that missed leave a sticky error behind
   if (!p->fn)
     return fail(SKYLA_HIP_E_NO_KERNEL, "no gfx950 kernel %s for this spec", sym.c_str());
+  p->retile = make_retile(ctx, name, spec, n_spec);
   int max_threads = 0;
   if (hipFuncGetAttribute(&max_threads, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, p->fn) ==
           hipSuccess &&
@@ -534,6 +617,7 @@ int skyla_hip_record_dispatch(skyla_hip_recorder *r, const skyla_hip_pipeline *p
   c.fn = p->fn;
   c.threads = p->threads;
   c.segmented = p->segmented;
+  c.retile = p->retile;
   for (int i = 0; i < 3; i++) c.groups[i] = groups[i];
   c.bufs = p->sets[set];
   c.push.assign(push, push + n_push);

@@ -92,3 +92,35 @@ def test_barrier_and_other_pipelines_split_runs(ctx):
             rec.free()
     finally:
         s.free()
+
+
+@pytest.mark.parametrize("dtype,n_in,n_out", [(E.DType.Q4K, 4096, 8192), (E.DType.Q6K, 12288, 512),
+                                              (E.DType.Q6K, 1024, 12288)])
+@pytest.mark.parametrize("accum", [False, True])
+def test_variant_choice_matches_requested_variant(ctx, dtype, n_in, n_out, accum):
+    """Large dense launches run on the variant the runtime picks for their size; the result
+    equals the engine-requested variant's up to f32 summation order, and the oracle."""
+    data = synth.matrix("test-fusion", f"retile-{dtype.name}-{n_in}-{n_out}", dtype, n_in, n_out)
+    x = synth.activations("test-fusion", f"rx-{n_in}", n_in)
+    y0 = synth.activations("test-fusion", f"ry-{n_out}", n_out)
+    got = {}
+    for retile in ("0", "1"):
+        old = os.environ.get("SKYLA_HIP_RETILE")
+        os.environ["SKYLA_HIP_RETILE"] = retile
+        try:
+            s = Setup(ctx, [(dtype, n_in, n_out, data)], n_in, n_out)
+        finally:
+            if old is None:
+                del os.environ["SKYLA_HIP_RETILE"]
+            else:
+                os.environ["SKYLA_HIP_RETILE"] = old
+        try:
+            s.set_x(x)
+            s.set_y(y0)
+            s.matvec(0, accum)
+            got[retile] = s.y(1, n_out)[0].astype(np.float64)
+        finally:
+            s.free()
+    assert rel_l2(got["1"], got["0"]) < 1e-5
+    want = so.matvec(int(dtype), data, n_in, n_out, x).astype(np.float64)
+    assert rel_l2(got["1"] - (y0 if accum else 0.0), want) < 2e-3
