@@ -136,7 +136,10 @@ SK_DEV f16x8 weight_frag(const WStage<TYPE> &s, int t, uint32_t hh, f16x2 scale,
   } else if constexpr (TYPE == 2) {
     // step t: half hf = t/8, group g = (t/2)%4, l0 = 16 (t%2) + 8 hh
     const int hf = t >> 3, g = (t >> 1) & 3;
-    const uint32_t l0 = 16 * (t & 1) + 8 * hh;  // byte offset inside the 32-byte run
+    // byte offsets inside the 32-byte runs for lane half 0; half 1 reads 8 bytes further.
+    // Both candidates use constant indices (t is unrolled) and the lane picks one, so the
+    // staged arrays stay in registers.
+    const uint32_t l0 = 16 * (t & 1);
     const uint32_t lbyte = hf * 64 + ((g & 1) ? 32 : 0) + l0;
     const uint32_t hbyte = hf * 32 + l0;
     auto word = [](const uint4 *v, uint32_t byte) -> uint32_t {
@@ -144,8 +147,10 @@ SK_DEV f16x8 weight_frag(const WStage<TYPE> &s, int t, uint32_t hh, f16x2 scale,
       const uint32_t k = (byte >> 2) & 3;
       return k == 0 ? q.x : (k == 1 ? q.y : (k == 2 ? q.z : q.w));
     };
-    const uint32_t l_0 = word(s.ql, lbyte), l_1 = word(s.ql, lbyte + 4);
-    const uint32_t h_0 = word(s.qh, hbyte), h_1 = word(s.qh, hbyte + 4);
+    const uint32_t l_0 = hh ? word(s.ql, lbyte + 8) : word(s.ql, lbyte);
+    const uint32_t l_1 = hh ? word(s.ql, lbyte + 12) : word(s.ql, lbyte + 4);
+    const uint32_t h_0 = hh ? word(s.qh, hbyte + 8) : word(s.qh, hbyte);
+    const uint32_t h_1 = hh ? word(s.qh, hbyte + 12) : word(s.qh, hbyte + 4);
     const uint32_t lmask = (g >= 2) ? 0x00f000f0u : 0x000f000fu;
     const uint32_t hmask = (g >= 2) ? 0x03000300u : 0x00300030u;
     const int hs = 4 - 2 * (g & 1);
@@ -410,18 +415,581 @@ SK_DEV void matmul_body(const uint4 *__restrict__ w, const uint16_t *__restrict_
   }
 }
 
+// ---------------------------------------------------------------------------------------
+// Dense prefill tile: 128 rows x 128 tokens (MATMUL_TILE_COLS = 128), eight waves of
+// 32 rows x 64 tokens (two per SIMD, so one wave's dequantisation overlaps the other's MFMAs).
+//   * Weights: a super-block (256 k) of raw blocks per lane, prefetched one super-block
+//     ahead; scale/min products decoded once per super-block; fragments dequantised per
+//     16-k step as in weight_frag.
+//   * Activations: 128-k chunks (eight steps) staged in LDS as f16; the next chunk's loads
+//     are in flight in registers while the current one runs on the matrix cores.
+//   * Tile order is XCD-aware (see below).
+//   * f16 range guard per (token, 128-k chunk): a chunk holding |x| >= 2^15 is staged as
+//     x * 2^-e (exact), and the wave scales its accumulators by 2^-e before that chunk's
+//     MFMAs and by 2^e after (exact for powers of two), so no extra registers are needed.
+// ---------------------------------------------------------------------------------------
+constexpr int TN2 = 128;            // tokens per tile
+constexpr int NT2 = 512;            // threads per dense workgroup (8 waves, 2 per SIMD)
+constexpr int KX = 128;             // k per activation chunk
+constexpr int PITCH2 = KX + 8;      // f16 per staged token row (16 B pad)
+
+// Per-lane scale/min of every step of a super-block, decoded once.
+template <int TYPE>
+struct StageScales;
+template <>
+struct StageScales<1> {
+  f16x2 sc[4], nm[4];
+  __device__ __forceinline__ void get(int t, f16x2 &s, f16x2 &m) const { s = sc[t >> 2]; m = nm[t >> 2]; }
+};
+template <>
+struct StageScales<2> {
+  f16x2 sc[16];
+  __device__ __forceinline__ void get(int t, f16x2 &s, f16x2 &m) const { s = sc[t]; m = splat((f16)0.0f); }
+};
+template <>
+struct StageScales<0> {
+  f16x2 sc[8];
+  __device__ __forceinline__ void get(int t, f16x2 &s, f16x2 &m) const { s = sc[t >> 1]; m = splat((f16)0.0f); }
+};
+
+template <int TYPE>
+SK_DEV void stage_scales(const WStage<TYPE> &s, uint32_t hh, StageScales<TYPE> &o) {
+  if constexpr (TYPE == 1) {
+#pragma unroll
+    for (int c = 0; c < 4; c++) step_scale<1>(s, 4 * c, hh, o.sc[c], o.nm[c]);
+  } else if constexpr (TYPE == 2) {
+#pragma unroll
+    for (int t = 0; t < 16; t++) {
+      f16x2 m;
+      step_scale<2>(s, t, hh, o.sc[t], m);
+    }
+  } else {
+#pragma unroll
+    for (int b = 0; b < 8; b++) {
+      f16x2 m;
+      step_scale<0>(s, 2 * b, hh, o.sc[b], m);
+    }
+  }
+}
+
+// One KX-k activation chunk of the tile as 8-value groups: group G = tid + 256 i is token
+// G / (KX/8), values 8 (G % (KX/8)) + [0, 8) of the chunk, so the lanes of one load
+// instruction read whole 512-byte runs of a few token rows (coalesced).
+constexpr int GPT = TN2 * KX / 8 / NT2;  // groups per thread
+constexpr int GPR = KX / 8;              // groups per token row (lanes sharing a token)
+template <int XHALF>
+struct XChunk {
+  float4 v[XHALF ? 1 : 2 * GPT];
+  uint4 h[XHALF ? GPT : 1];
+};
+
+template <int XHALF>
+SK_DEV void load_chunk(XChunk<XHALF> &c, const void *xv, const uint32_t *xrow, uint32_t x_off,
+                       uint32_t x_stride, uint32_t k0, uint32_t n_in) {
+#pragma unroll
+  for (int i = 0; i < GPT; i++) {
+    const uint32_t G = threadIdx.x + NT2 * i;
+    const uint32_t kb = k0 + 8 * (G % GPR);
+    // load unconditionally from a clamped, in-bounds address; values past n_in are zeroed
+    // when the chunk is stored (a select here would make the loads wait at once, and a
+    // predicated load is split into per-dword branches)
+    const size_t base = (size_t)x_off + (size_t)xrow[G / GPR] * x_stride + (kb < n_in ? kb : n_in - 8);
+    if constexpr (XHALF) {
+      c.h[i] = *(const uint4 *)((const f16 *)xv + base);
+    } else {
+      c.v[2 * i] = *(const float4 *)((const float *)xv + base);
+      c.v[2 * i + 1] = *(const float4 *)((const float *)xv + base + 4);
+    }
+  }
+}
+
+// Stores a chunk to LDS, pair-permuted as the weight fragments; returns whether this
+// wave rescaled any token.
+template <int XHALF>
+SK_DEV bool store_chunk(f16 *lds, XChunk<XHALF> &c, int *exps, uint32_t k0, uint32_t n_in) {
+  if (k0 + KX > n_in) {  // partial chunk (Q8_0 tail): zero the values past n_in
+#pragma unroll
+    for (int i = 0; i < GPT; i++) {
+      const bool live = k0 + 8 * ((threadIdx.x + NT2 * i) % GPR) < n_in;
+      if constexpr (XHALF) {
+        if (!live) c.h[i] = make_uint4(0, 0, 0, 0);
+      } else if (!live) {
+        c.v[2 * i] = make_float4(0.f, 0.f, 0.f, 0.f);
+        c.v[2 * i + 1] = make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    }
+  }
+  bool any = false;
+  if constexpr (!XHALF) {
+    float m = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 2 * GPT; i++)
+      m = fmaxf(m, fmaxf(fmaxf(fabsf(c.v[i].x), fabsf(c.v[i].y)), fmaxf(fabsf(c.v[i].z), fabsf(c.v[i].w))));
+    any = __ballot(!(m < 32768.0f)) != 0;  // NaN counts as big
+  }
+#pragma unroll
+  for (int i = 0; i < GPT; i++) {
+    const uint32_t G = threadIdx.x + NT2 * i;
+    const uint32_t n = G / GPR, kg = G % GPR;
+    uint4 o;
+    int e = 0;
+    if constexpr (XHALF) {
+      const uint4 v = c.h[i];
+      o.x = __builtin_amdgcn_perm(v.y, v.x, 0x05040100u);
+      o.y = __builtin_amdgcn_perm(v.y, v.x, 0x07060302u);
+      o.z = __builtin_amdgcn_perm(v.w, v.z, 0x05040100u);
+      o.w = __builtin_amdgcn_perm(v.w, v.z, 0x07060302u);
+    } else {
+      float4 a = c.v[2 * i], b = c.v[2 * i + 1];
+      if (any) {  // wave-uniform slow path: the token's max over its GPR lanes
+        float tm = fmaxf(fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))),
+                         fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w))));
+#pragma unroll
+        for (int d = GPR / 2; d >= 1; d >>= 1) tm = fmaxf(tm, __shfl_xor(tm, d, 64));
+        e = tm >= 32768.0f ? (int)((__builtin_bit_cast(uint32_t, tm) >> 23) & 255u) - 127 - 14 : 0;
+        const float sc = __builtin_ldexpf(1.0f, -e);
+        a = make_float4(a.x * sc, a.y * sc, a.z * sc, a.w * sc);
+        b = make_float4(b.x * sc, b.y * sc, b.z * sc, b.w * sc);
+      }
+      // values k0..k7 = a.xyzw b.xyzw -> pairs (0,2),(1,3),(4,6),(5,7)
+      o.x = as_u32(pack_f16x2(a.x, a.z));
+      o.y = as_u32(pack_f16x2(a.y, a.w));
+      o.z = as_u32(pack_f16x2(b.x, b.z));
+      o.w = as_u32(pack_f16x2(b.y, b.w));
+    }
+    *(uint4 *)(lds + n * PITCH2 + 8 * kg) = o;
+    if (kg == 0) exps[n] = e;
+  }
+  return any;
+}
+
+// K-quant weights of one 256-k stage, staged in LDS once per workgroup: the 128 rows'
+// raw block bytes are loaded with whole-line 16 B loads (8 or 13 lanes per row) and every
+// lane then reads the 8 bytes it dequantises per step from LDS.  Rows are PW bytes apart
+// (PW/4 odd multiple of 2 dwords), so the 32 rows a wave reads hit distinct bank pairs.
+template <int TYPE>
+struct WLds;
+template <>
+struct WLds<1> {  // Q4_K row: qs 128 | header 16
+  static constexpr uint32_t PW = 152;
+  uint4 q[2], hd;
+  SK_DEV void load(WLds &r, const uint4 *w, const MatmulPush &p, uint32_t row0, uint32_t sb, uint32_t tid) {
+    const uint32_t units = p.n_in >> 5, supers = p.n_in >> 8;
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      const uint32_t u = tid + NT2 * i, lr = u >> 3;
+      r.q[i] = w[p.o0 + min(row0 + lr, p.n_out - 1) * units + sb * 8 + (u & 7)];
+    }
+    if (tid < TM) r.hd = w[p.o1 + min(row0 + tid, p.n_out - 1) * supers + sb];
+  }
+  SK_DEV void store(const WLds &r, uint32_t *lds, uint32_t tid) {
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      const uint32_t u = tid + NT2 * i, lr = u >> 3;
+      uint2 *d = (uint2 *)(lds + (lr * PW + 16 * (u & 7)) / 4);
+      d[0] = make_uint2(r.q[i].x, r.q[i].y);
+      d[1] = make_uint2(r.q[i].z, r.q[i].w);
+    }
+    if (tid < TM) {
+      uint2 *d = (uint2 *)(lds + (tid * PW + 128) / 4);
+      d[0] = make_uint2(r.hd.x, r.hd.y);
+      d[1] = make_uint2(r.hd.z, r.hd.w);
+    }
+  }
+};
+template <>
+struct WLds<2> {  // Q6_K row: ql 128 | qh 64 | scales 16 | d 2
+  static constexpr uint32_t PW = 216;
+  uint4 ql[2], qh, sc;
+  uint32_t d;
+  SK_DEV void load(WLds &r, const uint4 *w, const uint16_t *wd, const MatmulPush &p, uint32_t row0,
+                   uint32_t sb, uint32_t tid) {
+    const uint32_t supers = p.n_in >> 8;
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      const uint32_t u = tid + NT2 * i, lr = u >> 3;
+      r.ql[i] = w[p.o0 + (min(row0 + lr, p.n_out - 1) * supers + sb) * 8 + (u & 7)];
+    }
+    {
+      const uint32_t lr = tid >> 2;
+      r.qh = w[p.o1 + (min(row0 + lr, p.n_out - 1) * supers + sb) * 4 + (tid & 3)];
+    }
+    const uint32_t lr = tid & (TM - 1);
+    const uint32_t rs = min(row0 + lr, p.n_out - 1) * supers + sb;
+    if (tid < TM) r.sc = w[p.o2 + rs];
+    else if (tid < 2 * TM) r.d = wd[p.o3 + rs];
+  }
+  SK_DEV void store(const WLds &r, uint32_t *lds, uint32_t tid) {
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      const uint32_t u = tid + NT2 * i, lr = u >> 3;
+      uint2 *d = (uint2 *)(lds + (lr * PW + 16 * (u & 7)) / 4);
+      d[0] = make_uint2(r.ql[i].x, r.ql[i].y);
+      d[1] = make_uint2(r.ql[i].z, r.ql[i].w);
+    }
+    {
+      const uint32_t lr = tid >> 2;
+      uint2 *d = (uint2 *)(lds + (lr * PW + 128 + 16 * (tid & 3)) / 4);
+      d[0] = make_uint2(r.qh.x, r.qh.y);
+      d[1] = make_uint2(r.qh.z, r.qh.w);
+    }
+    const uint32_t lr = tid & (TM - 1);
+    if (tid < TM) {
+      uint2 *d = (uint2 *)(lds + (lr * PW + 192) / 4);
+      d[0] = make_uint2(r.sc.x, r.sc.y);
+      d[1] = make_uint2(r.sc.z, r.sc.w);
+    } else if (tid < 2 * TM) {
+      lds[(lr * PW + 208) / 4] = r.d;
+    }
+  }
+};
+
+// Fragment of step t for lane half hh from the LDS row (same arithmetic as weight_frag).
+template <int TYPE>
+SK_DEV f16x8 lds_frag(const uint32_t *row, int t, uint32_t hh, f16x2 scale, f16x2 negmin) {
+  const uint32_t M = 0x64006400u;
+  if constexpr (TYPE == 1) {
+    const uint2 v = *(const uint2 *)(row + 2 * t);  // qs bytes [8t, 8t + 8)
+    const uint32_t mask = hh ? 0x00f000f0u : 0x000f000fu;
+    const f16x2 off = splat((f16)-1024.0f);
+    const uint32_t a = (v.x & mask) | M, b = ((v.x >> 8) & mask) | M;
+    const uint32_t e = (v.y & mask) | M, f = ((v.y >> 8) & mask) | M;
+    f16x2 w0 = __builtin_elementwise_fma(as_f16x2(a) + off, scale, negmin);
+    f16x2 w1 = __builtin_elementwise_fma(as_f16x2(b) + off, scale, negmin);
+    f16x2 w2 = __builtin_elementwise_fma(as_f16x2(e) + off, scale, negmin);
+    f16x2 w3 = __builtin_elementwise_fma(as_f16x2(f) + off, scale, negmin);
+    f16x8 r = {w0.x, w0.y, w1.x, w1.y, w2.x, w2.y, w3.x, w3.y};
+    return r;
+  } else {
+    const int hf = t >> 3, g = (t >> 1) & 3;
+    const uint32_t l0 = 16 * (t & 1) + 8 * hh;
+    const uint2 l = *(const uint2 *)(row + (hf * 64 + ((g & 1) ? 32 : 0) + l0) / 4);
+    const uint2 h = *(const uint2 *)(row + (128 + hf * 32 + l0) / 4);
+    const uint32_t lmask = (g >= 2) ? 0x00f000f0u : 0x000f000fu;
+    const uint32_t hmask = (g >= 2) ? 0x03000300u : 0x00300030u;
+    const int hs = 4 - 2 * (g & 1);
+    auto q6 = [&](uint32_t lv, uint32_t hv) -> uint32_t { return (lv & lmask) | M | ((hv << hs) & hmask); };
+    const f16x2 off = splat((g >= 2) ? (f16)-1536.0f : (f16)-1056.0f);
+    f16x2 w0 = (as_f16x2(q6(l.x, h.x)) + off) * scale;
+    f16x2 w1 = (as_f16x2(q6(l.x >> 8, h.x >> 8)) + off) * scale;
+    f16x2 w2 = (as_f16x2(q6(l.y, h.y)) + off) * scale;
+    f16x2 w3 = (as_f16x2(q6(l.y >> 8, h.y >> 8)) + off) * scale;
+    (void)negmin;
+    f16x8 r = {w0.x, w0.y, w1.x, w1.y, w2.x, w2.y, w3.x, w3.y};
+    return r;
+  }
+}
+
+// Stage scales of a lane from its LDS row (header / scales + d), as stage_scales.
+template <int TYPE>
+SK_DEV void lds_scales(const uint32_t *row, uint32_t hh, StageScales<TYPE> &o) {
+  WStage<TYPE> s;
+  if constexpr (TYPE == 1) {
+    const uint2 a = *(const uint2 *)(row + 32), b = *(const uint2 *)(row + 34);
+    s.hd = make_uint4(a.x, a.y, b.x, b.y);
+  } else {
+    const uint2 a = *(const uint2 *)(row + 48), b = *(const uint2 *)(row + 50);
+    s.sc = make_uint4(a.x, a.y, b.x, b.y);
+    s.d = row[52] & 0xffffu;
+  }
+  stage_scales<TYPE>(s, hh, o);
+}
+
+// Dense tile with LDS-staged K-quant weights (Q4_K, Q6_K); layout and activation path as
+// matmul_tile128.
+template <int TYPE, int ACCUM, int XHALF>
+SK_DEV void matmul_tile128_w(const uint4 *__restrict__ w, const uint16_t *__restrict__ wd, const void *x,
+                             float *y, const uint32_t *ctl, const MatmulPush &p) {
+  constexpr int NB = 2;
+  constexpr uint32_t PW = WLds<TYPE>::PW;
+  __shared__ __attribute__((aligned(16))) f16 xs[TN2 * PITCH2];
+  __shared__ __attribute__((aligned(16))) uint32_t wl[TM * PW / 4];
+  __shared__ uint32_t xrow[TN2];
+  __shared__ int xexp[TN2];
+  __shared__ uint32_t xflag[NT2 / 64];
+
+  const uint32_t tid = threadIdx.x;
+  const uint32_t lane = tid & 63, wave = tid >> 6;
+  const uint32_t hh = lane >> 5;
+  const uint32_t rb = wave & 3, tb = 2 * (wave >> 2);
+  const uint32_t gx = gridDim.x, gz = gridDim.z;
+  const uint32_t lin = blockIdx.x + gx * blockIdx.z;
+  const uint32_t row0 = (lin / gz) * TM;
+  const uint32_t n_all = ctl[2];
+  const uint32_t col0 = (lin % gz) * TN2;
+  if (col0 >= n_all) return;
+  const uint32_t n_tok = min(n_all - col0, (uint32_t)TN2);
+  if (tid < TN2) xrow[tid] = col0 + min(tid, n_tok - 1);
+  const uint32_t lrow = rb * 32 + (lane & 31);
+  const uint32_t my_row = row0 + lrow;
+  const uint32_t *wrow = wl + lrow * PW / 4;
+
+  f32x16 acc[NB];
+#pragma unroll
+  for (int j = 0; j < NB; j++)
+#pragma unroll
+    for (int i = 0; i < 16; i++) acc[j][i] = 0.0f;
+
+  const uint32_t n_stage = p.n_in / KC;
+  const uint32_t n_chunk = p.n_in / KX;
+  WLds<TYPE> wr;
+  if constexpr (TYPE == 1) wr.load(wr, w, p, row0, 0, tid);
+  else wr.load(wr, w, wd, p, row0, 0, tid);
+  __syncthreads();  // xrow
+  {
+    XChunk<XHALF> c0;
+    load_chunk<XHALF>(c0, x, xrow, p.x_off, p.x_stride, 0, p.n_in);
+    wr.store(wr, wl, tid);
+    const bool r = store_chunk<XHALF>(xs, c0, xexp, 0, p.n_in);
+    if (lane == 0) xflag[wave] = r;
+  }
+  __syncthreads();
+
+  uint32_t chunk = 0;
+  for (uint32_t st = 0; st < n_stage; st++) {
+    StageScales<TYPE> ss;
+    lds_scales<TYPE>(wrow, hh, ss);
+    const bool more = st + 1 < n_stage;
+    if (more) {
+      if constexpr (TYPE == 1) wr.load(wr, w, p, row0, st + 1, tid);
+      else wr.load(wr, w, wd, p, row0, st + 1, tid);
+    }
+#pragma unroll
+    for (int c4 = 0; c4 < KC / KX; c4++) {
+      XChunk<XHALF> xn;
+      const bool next = chunk + 1 < n_chunk;
+      if (next) load_chunk<XHALF>(xn, x, xrow, p.x_off, p.x_stride, (chunk + 1) * KX, p.n_in);
+      bool rescaled = false;
+#pragma unroll
+      for (int q = 0; q < NT2 / 64; q++) rescaled |= xflag[q] != 0;
+      if (rescaled) {
+#pragma unroll
+        for (int j = 0; j < NB; j++)
+#pragma unroll
+          for (int i = 0; i < 16; i++)
+            acc[j][i] = __builtin_ldexpf(acc[j][i], -xexp[32 * (tb + j) + 8 * (i >> 2) + 4 * hh + (i & 3)]);
+      }
+      constexpr int SPC = KX / 16;
+      f16x8 xf0[NB], xf1[NB], wf0, wf1;
+      auto frags = [&](int tt, f16x8(&xf)[NB], f16x8 &wf) {
+        const int t = SPC * c4 + tt;
+        f16x2 sc, nm;
+        ss.get(t, sc, nm);
+        wf = lds_frag<TYPE>(wrow, t, hh, sc, nm);
+        const uint32_t ko = koff<TYPE>(t, hh) - KX * c4;
+#pragma unroll
+        for (int j = 0; j < NB; j++) xf[j] = *(const f16x8 *)(xs + (32 * (tb + j) + (lane & 31)) * PITCH2 + ko);
+      };
+      frags(0, xf0, wf0);
+#pragma unroll
+      for (int tt = 0; tt < SPC; tt++) {
+        if (tt + 1 < SPC) {
+          if (tt & 1)
+            frags(tt + 1, xf0, wf0);
+          else
+            frags(tt + 1, xf1, wf1);
+        }
+#pragma unroll
+        for (int j = 0; j < NB; j++)
+          acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16((tt & 1) ? xf1[j] : xf0[j], (tt & 1) ? wf1 : wf0,
+                                                          acc[j], 0, 0, 0);
+      }
+      if (rescaled) {
+#pragma unroll
+        for (int j = 0; j < NB; j++)
+#pragma unroll
+          for (int i = 0; i < 16; i++)
+            acc[j][i] = __builtin_ldexpf(acc[j][i], xexp[32 * (tb + j) + 8 * (i >> 2) + 4 * hh + (i & 3)]);
+      }
+      __syncthreads();  // every wave is done with this chunk (and, at the stage end, the weights)
+      if (next) {
+        if (c4 == KC / KX - 1 && more) wr.store(wr, wl, tid);
+        const bool r = store_chunk<XHALF>(xs, xn, xexp, (chunk + 1) * KX, p.n_in);
+        if (lane == 0) xflag[wave] = r;
+        __syncthreads();
+      }
+      chunk++;
+    }
+  }
+
+  if (my_row < p.n_out) {
+#pragma unroll
+    for (int j = 0; j < NB; j++) {
+#pragma unroll
+      for (int i = 0; i < 16; i++) {
+        const uint32_t tok = 32 * (tb + j) + 8 * (i >> 2) + 4 * hh + (i & 3);
+        if (tok < n_tok) {
+          float *o = y + p.y_off + (size_t)(col0 + tok) * p.y_stride + my_row;
+          *o = ACCUM ? *o + acc[j][i] : acc[j][i];
+        }
+      }
+    }
+  }
+}
+
+template <int TYPE, int ACCUM, int XHALF>
+SK_DEV void matmul_tile128(const uint4 *__restrict__ w, const uint16_t *__restrict__ wd, const void *x,
+                           float *y, const uint32_t *ctl, const MatmulPush &p) {
+  // wave w: rows 32 (w % 4) + [0, 32), tokens 64 (w / 4) + [0, 64) of the tile; the two
+  // waves of a row block dequantise the same fragments (VALU) but share one weight stream
+  constexpr int NB = 2;
+  __shared__ __attribute__((aligned(16))) f16 xs[TN2 * PITCH2];
+  __shared__ uint32_t xrow[TN2];
+  __shared__ int xexp[TN2];
+  __shared__ uint32_t xflag[NT2 / 64];
+
+  const uint32_t tid = threadIdx.x;
+  const uint32_t lane = tid & 63, wave = tid >> 6;
+  const uint32_t hh = lane >> 5;
+  const uint32_t rb = wave & 3, tb = 2 * (wave >> 2);  // row block, first token block
+  // Tile order: blocks are dealt to the 8 XCDs round-robin by linear id, so consecutive ids
+  // take consecutive token tiles; every workgroup of an XCD then shares one token tile of
+  // activations in that XCD's L2 (the row tiles, read once per token tile, stream past).
+  const uint32_t gx = gridDim.x, gz = gridDim.z;
+  const uint32_t lin = blockIdx.x + gx * blockIdx.z;
+  const uint32_t row0 = (lin / gz) * TM;
+  const uint32_t n_all = ctl[2];
+  const uint32_t col0 = (lin % gz) * TN2;
+  if (col0 >= n_all) return;
+  const uint32_t n_tok = min(n_all - col0, (uint32_t)TN2);
+  if (tid < TN2) xrow[tid] = col0 + min(tid, n_tok - 1);
+  __syncthreads();
+
+  const uint32_t my_row = row0 + rb * 32 + (lane & 31);
+  const uint32_t wrow = min(my_row, p.n_out - 1);
+
+  f32x16 acc[NB];
+#pragma unroll
+  for (int j = 0; j < NB; j++)
+#pragma unroll
+    for (int i = 0; i < 16; i++) acc[j][i] = 0.0f;
+
+  const uint32_t n_stage = (p.n_in + KC - 1) / KC;
+  const uint32_t n_chunk = (p.n_in + KX - 1) / KX;
+  WStage<TYPE> ws;
+  load_stage<TYPE>(ws, w, wd, p, wrow, 0, min(p.n_in, (uint32_t)KC));
+  {
+    XChunk<XHALF> c0;
+    load_chunk<XHALF>(c0, x, xrow, p.x_off, p.x_stride, 0, p.n_in);
+    const bool r = store_chunk<XHALF>(xs, c0, xexp, 0, p.n_in);
+    if (lane == 0) xflag[wave] = r;
+  }
+  __syncthreads();
+
+  uint32_t chunk = 0;
+  for (uint32_t st = 0; st < n_stage; st++) {
+    const uint32_t kc = st * KC;
+    const uint32_t nk = min(p.n_in - kc, (uint32_t)KC);
+    StageScales<TYPE> ss;
+    stage_scales<TYPE>(ws, hh, ss);
+    WStage<TYPE> wn;
+    const bool more = st + 1 < n_stage;
+#pragma unroll
+    for (int c4 = 0; c4 < KC / KX; c4++) {
+      if ((uint32_t)(KX * c4) < nk) {
+        // the next chunk is loaded into registers while this one runs from LDS; the next
+        // super-block's weights are requested during the stage's last chunk, after it
+        XChunk<XHALF> xn;
+        const bool next = chunk + 1 < n_chunk;
+        if (next) load_chunk<XHALF>(xn, x, xrow, p.x_off, p.x_stride, (chunk + 1) * KX, p.n_in);
+        if (c4 == KC / KX - 1 && more) load_stage<TYPE>(wn, w, wd, p, wrow, kc + KC, min(p.n_in - kc - KC, (uint32_t)KC));
+        bool rescaled = false;
+#pragma unroll
+        for (int q = 0; q < NT2 / 64; q++) rescaled |= xflag[q] != 0;
+        const f16 *cur = xs;
+        if (rescaled) {  // acc *= 2^-e(token) before this chunk (exact)
+#pragma unroll
+          for (int j = 0; j < NB; j++)
+#pragma unroll
+            for (int i = 0; i < 16; i++)
+              acc[j][i] = __builtin_ldexpf(acc[j][i], -xexp[32 * (tb + j) + 8 * (i >> 2) + 4 * hh + (i & 3)]);
+        }
+        // Software-pipelined steps: the LDS reads and the dequantisation of step tt+1 are
+        // issued before the MFMAs of step tt, so their latency hides behind the matrix cores.
+        // K-quant stages are always whole (n_in % 256 == 0); Q8_0's last stage may be short.
+        constexpr int SPC = KX / 16;  // steps per chunk
+        const int nsteps = TYPE == 0 ? min(SPC, (int)(nk - KX * c4) / 16) : SPC;
+        f16x8 xf0[NB], xf1[NB], wf0, wf1;
+        auto frags = [&](int tt, f16x8(&xf)[NB], f16x8 &wf) {
+          const int t = SPC * c4 + tt;
+          f16x2 sc, nm;
+          ss.get(t, sc, nm);
+          wf = weight_frag<TYPE>(ws, t, hh, sc, nm);
+          const uint32_t ko = koff<TYPE>(t, hh) - KX * c4;
+#pragma unroll
+          for (int j = 0; j < NB; j++) xf[j] = *(const f16x8 *)(cur + (32 * (tb + j) + (lane & 31)) * PITCH2 + ko);
+        };
+        frags(0, xf0, wf0);
+#pragma unroll
+        for (int tt = 0; tt < SPC; tt++) {
+          if (tt < nsteps) {
+            if (tt + 1 < nsteps) {
+              if (tt & 1)
+                frags(tt + 1, xf0, wf0);
+              else
+                frags(tt + 1, xf1, wf1);
+            }
+#pragma unroll
+            for (int j = 0; j < NB; j++)
+              acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16((tt & 1) ? xf1[j] : xf0[j], (tt & 1) ? wf1 : wf0,
+                                                              acc[j], 0, 0, 0);
+          }
+        }
+        if (rescaled) {
+#pragma unroll
+          for (int j = 0; j < NB; j++)
+#pragma unroll
+            for (int i = 0; i < 16; i++)
+              acc[j][i] = __builtin_ldexpf(acc[j][i], xexp[32 * (tb + j) + 8 * (i >> 2) + 4 * hh + (i & 3)]);
+        }
+        __syncthreads();  // every wave is done with this chunk
+        if (next) {
+          const bool r = store_chunk<XHALF>(xs, xn, xexp, (chunk + 1) * KX, p.n_in);
+          if (lane == 0) xflag[wave] = r;
+          __syncthreads();
+        }
+        chunk++;
+      }
+    }
+    if (more) ws = wn;
+  }
+
+  if (my_row < p.n_out) {
+#pragma unroll
+    for (int j = 0; j < NB; j++) {
+#pragma unroll
+      for (int i = 0; i < 16; i++) {
+        const uint32_t tok = 32 * (tb + j) + 8 * (i >> 2) + 4 * hh + (i & 3);
+        if (tok < n_tok) {
+          float *o = y + p.y_off + (size_t)(col0 + tok) * p.y_stride + my_row;
+          *o = ACCUM ? *o + acc[j][i] : acc[j][i];
+        }
+      }
+    }
+  }
+}
+
 }  // namespace
 
+// Dense (MOE = 0) launches use the 128 x 128 tile; expert groups (MOE = 1) the 128 x 32 one.
+#define MM_BODY(T, A, M, H)                                                     \
+  if constexpr (M == 0 && T != 0)                                               \
+    matmul_tile128_w<T, A, H>(w, wd, x, y, ctl, p);                             \
+  else if constexpr (M == 0)                                                    \
+    matmul_tile128<T, A, H>(w, wd, x, y, ctl, p);                               \
+  else                                                                          \
+    matmul_body<T, A, M, H>(w, wd, x, y, ctl, p);
+
 #define MM(T, A, M)                                                                          \
-  extern "C" __global__ __launch_bounds__(256) void matmul__##T##_##A##_##M(                 \
+  extern "C" __global__ __launch_bounds__(M ? 256 : NT2) void matmul__##T##_##A##_##M(       \
       const uint4 *w, const uint16_t *wd, const float *x, float *y, const uint32_t *ctl,     \
       MatmulPush p) {                                                                        \
-    matmul_body<T, A, M, 0>(w, wd, x, y, ctl, p);                                            \
+    MM_BODY(T, A, M, 0)                                                                      \
   }                                                                                          \
-  extern "C" __global__ __launch_bounds__(256) void matmul__##T##_##A##_##M##_1(             \
+  extern "C" __global__ __launch_bounds__(M ? 256 : NT2) void matmul__##T##_##A##_##M##_1(   \
       const uint4 *w, const uint16_t *wd, const f16 *x, float *y, const uint32_t *ctl,       \
       MatmulPush p) {                                                                        \
-    matmul_body<T, A, M, 1>(w, wd, x, y, ctl, p);                                            \
+    MM_BODY(T, A, M, 1)                                                                      \
   }
 
 #define MM_TYPE(T) \

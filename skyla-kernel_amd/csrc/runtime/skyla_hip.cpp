@@ -520,6 +520,8 @@ int skyla_hip_pipeline_new(skyla_hip_context *ctx, const char *name, uint32_t n_
   uint32_t threads = 256;
   if (k->threads_from_spec >= 0)
     threads = k->waves ? 64 * spec[k->threads_from_spec] : spec[k->threads_from_spec];
+  // matmul: dense tiles (MOE = 0) run eight waves, expert groups four (matmul.hip)
+  if (std::strcmp(name, "matmul") == 0 && spec[2] == 0) threads = 512;
   auto p = std::make_unique<skyla_hip_pipeline>();
   p->ctx = ctx;
   p->symbol = sym;

@@ -17,7 +17,7 @@ import numpy as np
 from .abi import Buffer, Context, Pipeline, Recorder
 
 # ---- backend.rs: the skyla-hip arm of `mod selected` ----------------------------------
-MATMUL_TILE_COLS = 64   # tokens per matmul workgroup (matmul.hip TN, dense)
+MATMUL_TILE_COLS = 128   # tokens per matmul workgroup (matmul.hip TN, dense)
 MOE_TILE_COLS = 32      # tokens per grouped-expert workgroup (matmul.hip TN, MOE)
 HALF_INPUTS = False     # GEMM inputs stay f32: the matmul stages them to f16 itself, with a
                         # range guard (activations such as silu(g)*u can exceed f16's 65504)
