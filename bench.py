@@ -15,8 +15,9 @@ resident in HBM before timing starts.
 
 Also reported: matvec-only decode tok/s (1 / step time), the dominant kernel's roofline
 (matvec_q4k; average launch duration from HIP events on the launch stream), a measured HBM
-stream-read probe, the prefill GEMM at M = 512 (config 3) as TFLOP/s, and the CPU oracle
-(restatement of skyla-ref Matrix::matvec) timed on this host over a bounded sample.
+stream-read probe, the prefill GEMM at M = 512 (config 3) as TFLOP/s, the MoE layer of
+config 4 (decode token and 128-token prefill chunk), and the CPU oracle (restatement of
+skyla-ref Matrix::matvec) timed on this host over a bounded sample.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -222,6 +223,67 @@ def prefill_gemm(ctx: Context, m_tok: int = 512) -> dict:
     return out
 
 
+MOE_CFG = "qwen3-30b-a3b-moe"
+MOE_EMBD, MOE_FF, MOE_EXPERT, MOE_USED = 2048, 768, 128, 8
+
+
+def moe_layers(ctx: Context, n_layer: int = 12, n_tok: int = 128) -> dict:
+    """Config 4: Qwen3-30B-A3B-style MoE layer (128 experts, top-8, Q4_K gate/up/down of
+    2048x768 / 768x2048 per expert, f32 router), as skyla-engine's Graph::moe sequence
+    (graph/moe.rs:42-80), over `n_layer` distinct copies of the layer (4 GB at 12) so the
+    selected experts stream from HBM.  Decode: one token through the layers; prefill: one
+    128-token chunk.  Bytes per layer = distinct selected experts x 3 expert matrices +
+    the 1 MiB router (the algorithmic bytes of the MoE row)."""
+    c = E.Config(n_embd=MOE_EMBD, n_ff=64, n_expert=MOE_EXPERT, n_expert_used=MOE_USED, n_ff_expert=MOE_FF)
+    router = synth.router(MOE_CFG, "router", MOE_EXPERT, MOE_EMBD)
+    data = {name: synth.matrix(MOE_CFG, f"{name}_exps", E.DType.Q4K, n_in, n_out, MOE_EXPERT)
+            for name, n_in, n_out in [("gate", MOE_EMBD, MOE_FF), ("up", MOE_EMBD, MOE_FF), ("down", MOE_FF, MOE_EMBD)]}
+    p = E.Planner(ctx.max_buffer())
+    layers = []
+    for _ in range(n_layer):
+        layers.append((p.matrix(E.DType.Q4K, MOE_EMBD, MOE_FF, data["gate"]),
+                       p.matrix(E.DType.Q4K, MOE_EMBD, MOE_FF, data["up"]),
+                       p.matrix(E.DType.Q4K, MOE_FF, MOE_EMBD, data["down"]),
+                       p.table(router.reshape(-1))))
+    weights = E.upload_weights(ctx, p)
+    a = E.Arena(ctx, c)
+    k = E.Kernels(ctx, weights, a.buffer)
+    expert_bytes = 3 * MOE_FF * E.row_bytes(E.DType.Q4K, MOE_EMBD)  # gate + up + down of one expert
+    router_bytes = MOE_EXPERT * MOE_EMBD * 4
+    out = {"layers": n_layer, "weight_bytes": sum(b.size for b in weights)}
+    for mode, tokens in (("decode", 1), ("prefill", n_tok)):
+        f = a.f32()
+        g = synth.rng(MOE_CFG, f"bench-{mode}")
+        for t in range(tokens):
+            f[a.n + t * a.s_embd: a.n + t * a.s_embd + MOE_EMBD] = g.standard_normal(MOE_EMBD, dtype=np.float32)
+            f[a.x + t * a.s_embd: a.x + t * a.s_embd + MOE_EMBD] = 0.0
+        a.set_ctl(0, 0, tokens)
+        a.buffer.upload()
+
+        def body(r, batched=tokens > 1):
+            for gq, uq, dq, ro in layers:
+                E.Graph(r, k, a, c, batched).moe(gq, uq, dq, ro)
+        rec = ctx.record(EAGER, body)
+        ctx.replay(rec)
+        a.buffer.download()
+        ids = a.u32()[a.moe.ids: a.moe.ids + tokens * MOE_USED]
+        distinct = len(set(int(i) for i in ids))
+        for _ in range(3):
+            ctx.replay(rec)
+        ns = float(np.median([ctx.replay_timed(rec) for _ in range(7)]))
+        per_layer = ns / n_layer
+        moved = distinct * expert_bytes + router_bytes
+        flops = 2.0 * tokens * MOE_USED * 3 * MOE_EMBD * MOE_FF
+        out[mode] = {"tokens": tokens, "us_per_layer": round(per_layer / 1e3, 2), "distinct_experts": distinct,
+                     "algorithmic_bytes_per_layer": moved, "gbs": round(moved / per_layer, 1),
+                     "tflops": round(flops / per_layer / 1e3, 2), "launches_per_layer": rec.launches() / n_layer}
+        rec.free()
+    for b in weights:
+        b.free()
+    a.buffer.free()
+    return out
+
+
 def cpu_baseline(w: DecodeWorkload, budget_s: float = 15.0) -> dict:
     """skyla-ref Matrix::matvec restated in C (oracle/), timed on this host: layer passes of
     the same 7 matvecs until about budget_s seconds have elapsed."""
@@ -272,6 +334,7 @@ def main() -> int:
     ap.add_argument("--layers", type=int, default=N_LAYER)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--no-prefill", action="store_true", help="skip the config-3 GEMM figures")
+    ap.add_argument("--no-moe", action="store_true", help="skip the config-4 MoE figures")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--eager", action="store_true",
                     help="replay recordings as direct launches instead of one HIP graph")
@@ -329,6 +392,9 @@ def main() -> int:
     prefill = None if args.no_prefill else prefill_gemm(ctx)
     if prefill:
         log(f"prefill GEMM M=512: {prefill}")
+    moe = None if args.no_moe else moe_layers(ctx)
+    if moe:
+        log(f"MoE layer (config 4): {moe}")
     cpu = None if args.no_cpu else cpu_baseline(w, args.cpu_seconds)
     if cpu:
         log(f"cpu baseline {cpu['value']} GB/s on {cpu['cores']} threads")
@@ -373,6 +439,7 @@ def main() -> int:
         "hbm_probe_gbs": round(probe, 1),
         "parity_rel_l2": parity,
         "prefill_gemm_m512": prefill,
+        "moe_layer_config4": moe,
         "cpu_baseline": cpu,
     }
     step.free()
