@@ -191,15 +191,16 @@ SK_DEV void matvec_q4k_body(const uint4 *__restrict__ w, const float *x, float *
     uint4 h0 = make_uint4(0, 0, 0, 0);
     if (tid < nu) x_unit(tid, xa, xb);
     if (tid < n_items) h0 = h_load(tid);
+    // Weight loads are issued unconditionally (indices clamped in bounds): a load under a
+    // branch makes the compiler wait for every load in flight at each step, which would
+    // serialise the prefetch ring with the arithmetic.
     constexpr int PF = 4;  // weight steps in flight per lane
     uint4 q[PF][ROWS];
 #pragma unroll
     for (int j = 0; j < PF; j++) {
-      const uint32_t i = lane + j * LPR;
-      if (i < nu) {
+      const uint32_t i = min(lane + j * LPR, nu - 1);
 #pragma unroll
-        for (int r = 0; r < ROWS; r++) q[j][r] = qs[r][u0 + i];
-      }
+      for (int r = 0; r < ROWS; r++) q[j][r] = qs[r][u0 + i];
     }
     if (tid < nu) x_store(tid, xa, xb);
     if (tid < n_items) h_store(tid, h0);
@@ -239,12 +240,10 @@ SK_DEV void matvec_q4k_body(const uint4 *__restrict__ w, const float *x, float *
             acc[r] = __builtin_fmaf(-f.z, xsum.x, acc[r]);
             acc[r] = __builtin_fmaf(-f.w, xsum.y, acc[r]);
           }
-          const uint32_t inext = i + PF * LPR;  // refill this slot PF steps ahead
-          if (inext < nu) {
-#pragma unroll
-            for (int r = 0; r < ROWS; r++) q[j][r] = qs[r][u0 + inext];
-          }
         }
+        const uint32_t inext = min(i + PF * LPR, nu - 1);  // refill this slot PF steps ahead
+#pragma unroll
+        for (int r = 0; r < ROWS; r++) q[j][r] = qs[r][u0 + inext];
       }
     }
   }
@@ -367,8 +366,7 @@ SK_DEV void matvec_q6k_body(const uint4 *__restrict__ w, const uint16_t *__restr
     if (tid < nu) x_unit(tid, xv16);
     if (tid < n_items) h_load(tid, sv0, dv0);
 #pragma unroll
-    for (int j = 0; j < PF; j++)
-      if (lane + j * LPR < nu) load(lane + j * LPR, qa[j], qb[j], qh[j]);
+    for (int j = 0; j < PF; j++) load(min(lane + j * LPR, nu - 1), qa[j], qb[j], qh[j]);
     if (tid < nu) x_store(tid, xv16);
     if (tid < n_items) h_store(tid, sv0, dv0);
     for (uint32_t i = tid + G::NT; i < nu; i += G::NT) {
@@ -425,9 +423,8 @@ SK_DEV void matvec_q6k_body(const uint4 *__restrict__ w, const uint16_t *__restr
             acc[r] = __builtin_fmaf(f.z, t2, acc[r]);
             acc[r] = __builtin_fmaf(f.w, t3, acc[r]);
           }
-          const uint32_t inext = i + PF * LPR;
-          if (inext < nu) load(inext, qa[j], qb[j], qh[j]);
         }
+        load(min(i + PF * LPR, nu - 1), qa[j], qb[j], qh[j]);  // unconditional, as in Q4_K
       }
     }
   }
@@ -504,15 +501,13 @@ SK_DEV void matvec_q8_0_body(const uint4 *__restrict__ w, const uint16_t *__rest
     uint32_t dv0 = 0;
     if (tid < nu) x_unit(tid, xv4);
     if (tid < n_items) dv0 = d_load(tid);
-    constexpr int PF = 4;
+    constexpr int PF = 4;  // unconditional loads, as in Q4_K
     uint4 q[PF][ROWS];
 #pragma unroll
     for (int j = 0; j < PF; j++) {
-      const uint32_t i = lane + j * LPR;
-      if (i < nu) {
+      const uint32_t i = min(lane + j * LPR, nu - 1);
 #pragma unroll
-        for (int r = 0; r < ROWS; r++) q[j][r] = qr[r][u0 + i];
-      }
+      for (int r = 0; r < ROWS; r++) q[j][r] = qr[r][u0 + i];
     }
     if (tid < nu) x_store(tid, xv4);
     if (tid < n_items) dd[tid / nb][tid % nb] = f16_bits_to_f32(dv0);
@@ -543,12 +538,10 @@ SK_DEV void matvec_q8_0_body(const uint4 *__restrict__ w, const uint16_t *__rest
             }
             acc[r] = __builtin_fmaf(dd[lrow0 + r][i >> 1], s, acc[r]);
           }
-          const uint32_t inext = i + PF * LPR;
-          if (inext < nu) {
-#pragma unroll
-            for (int r = 0; r < ROWS; r++) q[j][r] = qr[r][u0 + inext];
-          }
         }
+        const uint32_t inext = min(i + PF * LPR, nu - 1);
+#pragma unroll
+        for (int r = 0; r < ROWS; r++) q[j][r] = qr[r][u0 + inext];
       }
     }
   }
