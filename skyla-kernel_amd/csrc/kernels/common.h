@@ -50,6 +50,21 @@ SK_DEV float group_sum(float v) {
 
 SK_DEV uint32_t ctl_word(const uint32_t *ctl, uint32_t i) { return ctl[i]; }
 
+// Buffer resource over [base, base + bytes) for raw buffer loads: a load whose offset is
+// past the end returns zero instead of touching memory (range checked per dword).  The
+// offset of a load is voffset (per lane) + soffset (wave-uniform), so a constant step of a
+// uniform loop goes in the scalar operand and costs no vector instruction.  Word 3 is the
+// gfx9 descriptor format (32-bit data, no swizzle).
+typedef __amdgpu_buffer_rsrc_t BufRes;
+SK_DEV BufRes buf_res(const void *base, uint64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0,
+                                           (int)(uint32_t)(bytes < 0xffffffffull ? bytes : 0xffffffffull),
+                                           0x00020000);
+}
+SK_DEV uint4 buf_load(BufRes r, uint32_t voffset, uint32_t soffset) {
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voffset, soffset, 0));
+}
+
 // ---------------------------------------------------------------------------------------
 // Segmented launch.  Dispatches of one pipeline that the engine records with no barrier
 // between them are independent (a barrier is how it orders them), so the runtime fuses up

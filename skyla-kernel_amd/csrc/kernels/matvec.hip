@@ -97,15 +97,40 @@ struct Geo {
 // 64c + 16(u%2) + [0,16) of sub-block 2c, high nibbles the same positions of sub-block 2c+1
 // (quant.rs:56-66).  LDS per pass: xq[0..3][unit] = the unit's 32 activations as f16 pairs in
 // the (0,2),(1,3) order of the packed quants (low-nibble half, then high), xs[unit] = their
-// two 16-value sums, and per (row, super-block, chunk) the products d*sc (x2: low and high
-// sub-block, 1/16 folded into the high one) and dmin*m (quant.rs:40-49, 60-61).
+// two 16-value sums, and per (row, super-block, chunk) four products of the header
+// (quant.rs:40-49, 60-61): d*sc_lo, d*sc_hi/16, and the terms that multiply the two sums,
+// 1024*d*sc_lo + dmin*m_lo and 64*d*sc_hi + dmin*m_hi (the 1024 cancels the f16 offset of
+// the packed quants, so a lane's dot products start from zero).
+//
+// Every lane of a workgroup runs the same number of steps S = ceil(units / LPR): units past
+// the pass hold zero activations and zero products, so they add exactly zero, and the loop
+// carries no per-lane guard.  Weights and headers are read through buffer resources that
+// end at the matrix (rows past n_out are clamped, reads past the end return zero), so the
+// ring's loads take their step offset in the scalar operand and need no address math.
+// Activations are staged by all threads, a quarter unit (8 floats) each, so no thread
+// holds more than 64 B of them in flight.
 // ---------------------------------------------------------------------------------------
+template <int WAVES, int ROWS, int LPR>
+struct GeoQ4 {
+  static constexpr int SUBS = 64 / LPR;
+  static constexpr int RWG = WAVES * SUBS * ROWS;
+  static constexpr int NT = 64 * WAVES;
+  static constexpr int CH_A = (512 / RWG) < 1 ? 1 : ((512 / RWG) > 32 ? 32 : (512 / RWG));
+  static constexpr int CH_B = CH_A > NT / 16 ? NT / 16 : CH_A;      // <= 64 B of x per thread
+  static constexpr int CH_SUP = CH_B < LPR / 8 ? LPR / 8 : CH_B;     // super-blocks per pass
+  static constexpr int CHU = CH_SUP * 8;                           // units per pass
+  // weight steps in flight: 16 VGPRs of ring, and no more steps than a 4096-value row has
+  static constexpr int PF = (ROWS >= 4 ? 1 : 4 / ROWS) > 128 / LPR ? 128 / LPR : (ROWS >= 4 ? 1 : 4 / ROWS);
+  static_assert(CHU % LPR == 0, "a full pass gives every lane the same number of steps");
+};
+
 template <int WAVES, int ACCUM, int ROWS, int MOE, int LPR>
 SK_DEV void matvec_q4k_body(const uint4 *__restrict__ w, const float *x, float *y,
                             const uint32_t *ids, const MatvecPush2 &p, uint32_t bx) {
-  using G = Geo<WAVES, ROWS, LPR>;
-  __shared__ uint4 xq[4][G::CH / 32];  // component-major: lanes read consecutive 16 B
-  __shared__ float2 xs[G::CH / 32];
+  using G = GeoQ4<WAVES, ROWS, LPR>;
+  constexpr int CHU = G::CHU, PF = G::PF;
+  __shared__ uint4 xq[4][CHU];  // component-major: lanes read consecutive 16 B
+  __shared__ float2 xs[CHU];
   __shared__ float4 sc[G::RWG][G::CH_SUP][4];
 
   const uint32_t tid = threadIdx.x;
@@ -122,130 +147,131 @@ SK_DEV void matvec_q4k_body(const uint4 *__restrict__ w, const float *x, float *
   const uint32_t c = (lane >> 1) & 3;  // chunk of this lane's units (u % 8 == lane % 8)
   const uint32_t MW = MAGIC, LO = 0x000f000fu, HI = 0x00f000f0u;
 
-  const uint4 *qs[ROWS];
+  const BufRes wq = buf_res(w + p.o0, (uint64_t)(base + p.n_out) * units * 16);
+  const BufRes wh = buf_res(w + p.o1, (uint64_t)(base + p.n_out) * supers * 16);
+  uint32_t voff[ROWS];
 #pragma unroll
-  for (int r = 0; r < ROWS; r++) qs[r] = w + p.o0 + (base + min(first + r, p.n_out - 1)) * units;
+  for (int r = 0; r < ROWS; r++) voff[r] = ((base + min(first + r, p.n_out - 1)) * units + lane) * 16;
 
   float acc[ROWS];
 #pragma unroll
   for (int r = 0; r < ROWS; r++) acc[r] = 0.0f;
 
-  for (uint32_t k0 = 0; k0 < p.n_in; k0 += G::CH) {
-    const uint32_t nk = min(p.n_in - k0, (uint32_t)G::CH);
+  for (uint32_t k0 = 0; k0 < p.n_in; k0 += CHU * 32) {
+    const uint32_t nk = min(p.n_in - k0, (uint32_t)CHU * 32);
     const uint32_t u0 = k0 >> 5, nu = nk >> 5, s0 = k0 >> 8, ns = nk >> 8;
-    // Load order matters (loads complete in issue order): this thread's first staging
-    // loads go out first, then the first PF steps of weights, so the staging below waits
-    // only for its own data while the weight stream is already in flight.
-    auto x_unit = [&](uint32_t i, float4 (&a)[4], float4 (&b)[4]) {
-      const uint32_t u = u0 + i;
-      const float *xp = xv + (u >> 3) * 256 + ((u >> 1) & 3) * 64 + (u & 1) * 16;
-#pragma unroll
-      for (int k = 0; k < 4; k++) {
-        a[k] = *(const float4 *)(xp + 4 * k);
-        b[k] = *(const float4 *)(xp + 32 + 4 * k);
-      }
-    };
-    auto x_store = [&](uint32_t i, const float4 (&a)[4], const float4 (&b)[4]) {
-      uint32_t pa[8], pb[8];
-#pragma unroll
-      for (int k = 0; k < 4; k++) {
-        pa[2 * k] = pk(a[k].x, a[k].z);
-        pa[2 * k + 1] = pk(a[k].y, a[k].w);
-        pb[2 * k] = pk(b[k].x, b[k].z);
-        pb[2 * k + 1] = pk(b[k].y, b[k].w);
-      }
-      const f16x2 one = {(f16)1.0f, (f16)1.0f};
-      float sa = 0.0f, sb = 0.0f;
-#pragma unroll
-      for (int k = 0; k < 8; k++) {
-        sa = dot2(as_f16x2(pa[k]), one, sa);
-        sb = dot2(as_f16x2(pb[k]), one, sb);
-      }
-      xq[0][i] = make_uint4(pa[0], pa[1], pa[2], pa[3]);
-      xq[1][i] = make_uint4(pa[4], pa[5], pa[6], pa[7]);
-      xq[2][i] = make_uint4(pb[0], pb[1], pb[2], pb[3]);
-      xq[3][i] = make_uint4(pb[4], pb[5], pb[6], pb[7]);
-      xs[i] = make_float2(sa, sb);
-    };
-    const uint32_t n_items = (uint32_t)G::RWG * ns;
-    auto h_load = [&](uint32_t i) -> uint4 {
-      const uint32_t lr = i / ns, s = i % ns;
-      const uint32_t row = base + min(row0 + lr, p.n_out - 1);
-      return w[p.o1 + row * supers + s0 + s];
-    };
-    auto h_store = [&](uint32_t i, const uint4 h) {
-      const uint32_t lr = i / ns, s = i % ns;
-      const float d = f16_bits_to_f32(h.x & 0xffffu);
-      const float dmin = f16_bits_to_f32(h.x >> 16);
-#pragma unroll
-      for (int cc = 0; cc < 4; cc++) {
-        uint32_t sc0, m0, sc1, m1;
-        q4k_scale_min(2 * cc, h.y, h.z, h.w, sc0, m0);
-        q4k_scale_min(2 * cc + 1, h.y, h.z, h.w, sc1, m1);
-        sc[lr][s][cc] = make_float4(d * (float)sc0, d * (float)sc1 * 0.0625f, dmin * (float)m0,
-                                    dmin * (float)m1);
-      }
-    };
     if (k0 != 0) __syncthreads();  // the previous pass is done with the LDS
-    float4 xa[4], xb[4];
-    uint4 h0 = make_uint4(0, 0, 0, 0);
-    if (tid < nu) x_unit(tid, xa, xb);
-    if (tid < n_items) h0 = h_load(tid);
-    // Weight loads are issued unconditionally (indices clamped in bounds): a load under a
-    // branch makes the compiler wait for every load in flight at each step, which would
-    // serialise the prefetch ring with the arithmetic.
-    constexpr int PF = 4;  // weight steps in flight per lane
+    // Load order matters (a wave's loads complete in issue order): activations, then
+    // headers, then the first PF weight steps, so staging waits only for its own data.
+    constexpr int XI = (4 * CHU + G::NT - 1) / G::NT;  // activation quarters per thread
+    float4 xa[XI][2];
+#pragma unroll
+    for (int j = 0; j < XI; j++) {
+      const uint32_t t = tid + j * G::NT, u = u0 + (t >> 2), qq = t & 3;
+      if (t < 4 * nu) {
+        const float *xp = xv + (u >> 3) * 256 + ((u >> 1) & 3) * 64 + (u & 1) * 16 + (qq >> 1) * 32 + (qq & 1) * 8;
+        xa[j][0] = *(const float4 *)xp;
+        xa[j][1] = *(const float4 *)(xp + 4);
+      }
+    }
+    constexpr int NH = G::RWG * G::CH_SUP, HI_T = (NH + G::NT - 1) / G::NT;  // header items
+    uint4 hd[HI_T];
+#pragma unroll
+    for (int j = 0; j < HI_T; j++) {
+      const uint32_t i = tid + j * G::NT, lr = i / G::CH_SUP, s = i % G::CH_SUP;
+      if (i < NH && s < ns) hd[j] = buf_load(wh, ((base + min(row0 + lr, p.n_out - 1)) * supers + s) * 16, s0 * 16);
+    }
     uint4 q[PF][ROWS];
 #pragma unroll
-    for (int j = 0; j < PF; j++) {
-      const uint32_t i = min(lane + j * LPR, nu - 1);
+    for (int j = 0; j < PF; j++)
 #pragma unroll
-      for (int r = 0; r < ROWS; r++) q[j][r] = qs[r][u0 + i];
-    }
-    if (tid < nu) x_store(tid, xa, xb);
-    if (tid < n_items) h_store(tid, h0);
-    for (uint32_t i = tid + G::NT; i < nu; i += G::NT) {
-      x_unit(i, xa, xb);
-      x_store(i, xa, xb);
-    }
-    for (uint32_t i = tid + G::NT; i < n_items; i += G::NT) h_store(i, h_load(i));
-    __syncthreads();
+      for (int r = 0; r < ROWS; r++) q[j][r] = buf_load(wq, voff[r], (u0 + j * LPR) * 16);
 
-    for (uint32_t j0 = 0; lane + j0 * LPR < nu; j0 += PF) {
+    // stage: item t = quarter t%4 of unit t/4 (values 0-7, 8-15 of the low-nibble half,
+    // then of the high half); the pair sums of quarters make the unit's two 16-value sums
 #pragma unroll
-      for (int j = 0; j < PF; j++) {
-        const uint32_t i = lane + (j0 + j) * LPR;
-        if (i < nu) {
-          const uint4 xa0 = xq[0][i], xa1 = xq[1][i], xb0 = xq[2][i], xb1 = xq[3][i];
-          const float2 xsum = xs[i];
-          const uint32_t pa[8] = {xa0.x, xa0.y, xa0.z, xa0.w, xa1.x, xa1.y, xa1.z, xa1.w};
-          const uint32_t pb[8] = {xb0.x, xb0.y, xb0.z, xb0.w, xb1.x, xb1.y, xb1.z, xb1.w};
-          const float na = -1024.0f * xsum.x, nb = -1024.0f * xsum.y;
-          const uint32_t s = i >> 3;
-#pragma unroll
-          for (int r = 0; r < ROWS; r++) {
-            float sa = na, sb = nb;
-            const uint32_t wd[4] = {q[j][r].x, q[j][r].y, q[j][r].z, q[j][r].w};
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-              const uint32_t w0 = wd[k], w8 = w0 >> 8;
-              sa = dot2(as_f16x2(and_or(w0, LO, MW)), as_f16x2(pa[2 * k]), sa);
-              sa = dot2(as_f16x2(and_or(w8, LO, MW)), as_f16x2(pa[2 * k + 1]), sa);
-              sb = dot2(as_f16x2(and_or(w0, HI, MW)), as_f16x2(pb[2 * k]), sb);
-              sb = dot2(as_f16x2(and_or(w8, HI, MW)), as_f16x2(pb[2 * k + 1]), sb);
-            }
-            const float4 f = sc[lrow0 + r][s][c];
-            acc[r] = __builtin_fmaf(f.x, sa, acc[r]);
-            acc[r] = __builtin_fmaf(f.y, sb, acc[r]);
-            acc[r] = __builtin_fmaf(-f.z, xsum.x, acc[r]);
-            acc[r] = __builtin_fmaf(-f.w, xsum.y, acc[r]);
-          }
-        }
-        const uint32_t inext = min(i + PF * LPR, nu - 1);  // refill this slot PF steps ahead
-#pragma unroll
-        for (int r = 0; r < ROWS; r++) q[j][r] = qs[r][u0 + inext];
+    for (int j = 0; j < XI; j++) {
+      const uint32_t t = tid + j * G::NT, u = t >> 2, qq = t & 3;
+      const bool live = t < 4 * nu;
+      const float4 a = live ? xa[j][0] : make_float4(0.f, 0.f, 0.f, 0.f);
+      const float4 b = live ? xa[j][1] : make_float4(0.f, 0.f, 0.f, 0.f);
+      const uint32_t h0 = pk(a.x, a.z), h1 = pk(a.y, a.w), h2 = pk(b.x, b.z), h3 = pk(b.y, b.w);
+      const f16x2 one = {(f16)1.0f, (f16)1.0f};
+      float sum = dot2(as_f16x2(h0), one, 0.0f);
+      sum = dot2(as_f16x2(h1), one, sum);
+      sum = dot2(as_f16x2(h2), one, sum);
+      sum = dot2(as_f16x2(h3), one, sum);
+      sum += dpp_f<0xb1>(sum);  // + the other quarter of the same half
+      if (t < 4 * CHU) {
+        xq[qq][u] = make_uint4(h0, h1, h2, h3);
+        if ((qq & 1) == 0) ((float *)&xs[u])[qq >> 1] = sum;
       }
     }
+    // decode: the 8 six-bit scales and mins as bytes of four words (quant.rs:40-49)
+#pragma unroll
+    for (int j = 0; j < HI_T; j++) {
+      const uint32_t i = tid + j * G::NT, lr = i / G::CH_SUP, s = i % G::CH_SUP;
+      if (i < NH && s >= ns) {
+#pragma unroll
+        for (int cc = 0; cc < 4; cc++) sc[lr][s][cc] = make_float4(0.f, 0.f, 0.f, 0.f);
+      } else if (i < NH) {
+        const uint4 h = hd[j];
+        const float d = f16_bits_to_f32(h.x & 0xffffu), dmin = f16_bits_to_f32(h.x >> 16);
+        const float d16 = d * 0.0625f, d1024 = d * 1024.0f, d64 = d * 64.0f;
+        const uint32_t sw[2] = {h.y & 0x3f3f3f3fu, (h.w & 0x0f0f0f0fu) | ((h.y >> 2) & 0x30303030u)};
+        const uint32_t mw[2] = {h.z & 0x3f3f3f3fu, ((h.w >> 4) & 0x0f0f0f0fu) | ((h.z >> 2) & 0x30303030u)};
+#pragma unroll
+        for (int cc = 0; cc < 4; cc++) {
+          const uint32_t sv = sw[cc >> 1] >> (16 * (cc & 1)), mv = mw[cc >> 1] >> (16 * (cc & 1));
+          const float s_lo = (float)(sv & 255u), s_hi = (float)((sv >> 8) & 255u);
+          const float m_lo = (float)(mv & 255u), m_hi = (float)((mv >> 8) & 255u);
+          sc[lr][s][cc] = make_float4(d * s_lo, d16 * s_hi, __builtin_fmaf(d1024, s_lo, dmin * m_lo),
+                                      __builtin_fmaf(d64, s_hi, dmin * m_hi));
+        }
+      }
+    }
+    __syncthreads();
+
+    const uint32_t S = (nu + LPR - 1) / LPR;
+    auto step = [&](uint32_t st, const uint4 (&qj)[ROWS]) {
+      const uint32_t i = lane + st * LPR;
+      const uint4 xa0 = xq[0][i], xa1 = xq[1][i], xb0 = xq[2][i], xb1 = xq[3][i];
+      const float2 xsum = xs[i];
+      const uint32_t pa[8] = {xa0.x, xa0.y, xa0.z, xa0.w, xa1.x, xa1.y, xa1.z, xa1.w};
+      const uint32_t pb[8] = {xb0.x, xb0.y, xb0.z, xb0.w, xb1.x, xb1.y, xb1.z, xb1.w};
+      const uint32_t s = (lane >> 3) + st * (LPR / 8);
+#pragma unroll
+      for (int r = 0; r < ROWS; r++) {
+        float sa = 0.0f, sb = 0.0f;
+        const uint32_t wd[4] = {qj[r].x, qj[r].y, qj[r].z, qj[r].w};
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+          const uint32_t w0 = wd[k], w8 = w0 >> 8;
+          sa = dot2(as_f16x2(and_or(w0, LO, MW)), as_f16x2(pa[2 * k]), sa);
+          sa = dot2(as_f16x2(and_or(w8, LO, MW)), as_f16x2(pa[2 * k + 1]), sa);
+          sb = dot2(as_f16x2(and_or(w0, HI, MW)), as_f16x2(pb[2 * k]), sb);
+          sb = dot2(as_f16x2(and_or(w8, HI, MW)), as_f16x2(pb[2 * k + 1]), sb);
+        }
+        const float4 f = sc[lrow0 + r][s][c];
+        acc[r] = __builtin_fmaf(f.x, sa, acc[r]);
+        acc[r] = __builtin_fmaf(f.y, sb, acc[r]);
+        acc[r] = __builtin_fmaf(-f.z, xsum.x, acc[r]);
+        acc[r] = __builtin_fmaf(-f.w, xsum.y, acc[r]);
+      }
+    };
+    uint32_t j0 = 0;
+    for (; j0 + PF < S; j0 += PF) {
+#pragma unroll
+      for (int j = 0; j < PF; j++) {
+        step(j0 + j, q[j]);
+#pragma unroll
+        for (int r = 0; r < ROWS; r++) q[j][r] = buf_load(wq, voff[r], (u0 + (j0 + j + PF) * LPR) * 16);
+        __builtin_amdgcn_sched_barrier(0);  // each refill right behind the step it replaces
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < PF; j++)
+      if (j0 + j < S) step(j0 + j, q[j]);
   }
   store_rows<ACCUM, ROWS, LPR>(y, y_off, first, p.n_out, lane, acc);
 }
@@ -554,8 +580,12 @@ SK_DEV void matvec_q8_0_body(const uint4 *__restrict__ w, const uint16_t *__rest
 // Exported instantiations: symbol = <shader name>__<spec words joined by '_'>.  Each takes
 // the push words as a segment table (Segments, common.h), which the runtime builds.
 // ---------------------------------------------------------------------------------------
+// Waves per SIMD the Q4_K kernels are register-budgeted for: eight-wave workgroups keep
+// three per CU (the LDS allows three), which caps them at 80 VGPRs.
+#define MV_Q4K_WPE(W, R) ((W) >= 8 && (R) == 1 ? 6 : 1)
 #define MV_Q4K(W, A, R, M, L)                                                                \
-  extern "C" __global__ __launch_bounds__(64 * W) void matvec_q4k__##W##_##A##_##R##_##M##_##L( \
+  extern "C" __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(MV_Q4K_WPE(W, R)))) \
+  void matvec_q4k__##W##_##A##_##R##_##M##_##L(                                                \
       const uint4 *w, const float *x, float *y, const uint32_t *ids, Segments<MatvecPush2> m) { \
     const uint32_t s = segment_of(m, blockIdx.x);                                            \
     matvec_q4k_body<W, A, R, M, L>(w, x, y, ids, segment_push(m, s), blockIdx.x - m.start[s]); \

@@ -296,9 +296,10 @@ hipFunction_t find_function(skyla_hip_context *ctx, const std::string &sym) {
 }
 
 // Variant choice for dense matvec launches, from sweeps of the Qwen3-8B decode shapes on
-// MI355X (n_in 4096 and 12288): large launches gain from fewer lanes per row (more
-// pipelined load steps per lane); small ones from more rows per lane.  Each entry is
-// (min_rows, waves, rows, lanes per row).
+// MI355X (n_in 4096 and 12288): eight-wave workgroups throughout; large launches gain from
+// fewer lanes per row (more pipelined load steps per lane, fewer workgroups staging the
+// activations), small ones from more workgroups.  Each entry is (min_rows, waves, rows,
+// lanes per row).
 struct VariantRule {
   const char *name;
   uint32_t n_out_word;
@@ -306,7 +307,7 @@ struct VariantRule {
   int n;
 };
 const VariantRule kVariantRules[] = {
-    {"matvec_q4k", 5, {{6144, 8, 1, 16}, {0, 4, 2, 64}}, 2},
+    {"matvec_q4k", 5, {{6144, 8, 1, 16}, {0, 8, 1, 64}}, 2},
     {"matvec_q6k", 7, {{12288, 4, 1, 16}, {0, 4, 1, 32}}, 2},
 };
 
