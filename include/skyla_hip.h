@@ -91,9 +91,10 @@ int skyla_hip_buffer_copy(skyla_hip_buffer *dst, uint64_t dst_off, const skyla_h
  * kernel is the gfx950 instantiation for `spec`; an unknown (name, spec) fails with
  * SKYLA_HIP_E_NO_KERNEL, as a shader that does not compile fails pipeline creation.
  * n_buffers and push_size must match the kernel's bindings and push struct.
- * A dense matvec pipeline (spec MOE = 0) may launch another compiled variant of the same
- * kernel (same bindings and push words, different rows per workgroup) chosen by the
- * launch's total rows, with the grid recomputed from each dispatch's n_out; every row is
+ * A matvec pipeline (dense rows, or Q4_K expert rows) may launch another compiled variant
+ * of the same kernel (same bindings and push words, different rows per workgroup) chosen
+ * by the launch's total rows, with grid.x recomputed from each dispatch's n_out (grid.y,
+ * the expert slots, is kept); every row is
  * still computed once, and results differ from the requested variant only by f32
  * summation order.  Environment SKYLA_HIP_RETILE=0 (read here) keeps the requested one. */
 int skyla_hip_pipeline_new(skyla_hip_context *ctx, const char *name, uint32_t n_buffers,

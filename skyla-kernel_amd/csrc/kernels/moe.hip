@@ -28,13 +28,9 @@ SK_DEV float key_value(uint32_t k) {
   return __builtin_bit_cast(float, b);
 }
 
-SK_DEV uint64_t wave_max_u64(uint64_t v) {
-#pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) {
-    const uint64_t o = __shfl_xor(v, d, 64);
-    v = o > v ? o : v;
-  }
-  return v;
+template <int CTRL>
+SK_DEV uint32_t dpp_u(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xf, 0xf, false);
 }
 
 }  // namespace
@@ -59,43 +55,62 @@ extern "C" __global__ __launch_bounds__(256) void moe_logits(const float *w, con
 }
 
 // moe_route (moe_route.comp:55-106): per token, n_used rounds of "largest logit, lowest
-// index on ties", then weights exp(v_k - v_0) / sum.  One workgroup per token, expert t
-// held by thread t (n_expert <= 256); tokens at or beyond ctl[2] do nothing.
-extern "C" __global__ __launch_bounds__(256) void moe_route(float *a, uint32_t *ids, RoutePush p) {
-  __shared__ uint64_t wave_best[2][4];
-  __shared__ float chosen_value[16];
-  __shared__ uint32_t chosen_index[16];
+// index on ties", then weights exp(v_k - v_0) / sum.  One wave per token: expert
+// e = lane + 64 j is held in key[j] (n_expert <= 256), a round is a lane maximum, a wave
+// maximum (DPP within rows of 16, then two shuffles) and a ballot for the lowest expert
+// holding it.  Lane k keeps round k's choice; the exponentials are computed in parallel
+// and summed in round order, as the reference does.  Tokens at or beyond ctl[2] do nothing.
+extern "C" __global__ __launch_bounds__(64) void moe_route(float *a, uint32_t *ids, RoutePush p) {
   const uint32_t tok = blockIdx.y;
   const uint32_t n_tok = __builtin_bit_cast(uint32_t, a[2]);
   if (tok >= n_tok) return;
-  const uint32_t t = threadIdx.x, wave = t >> 6;
+  const uint32_t t = threadIdx.x;
   const uint32_t n_used = min(p.n_used, 16u);
+  const uint32_t n_expert = min(p.n_expert, 256u);
   const uint32_t logits_off = p.logits_off + tok * p.n_expert;
-  // key = (value order, ~index): the u64 maximum is the largest value, lowest index
-  uint64_t key = 0;
-  if (t < p.n_expert) key = ((uint64_t)order_key(a[logits_off + t]) << 32) | (uint32_t)~t;
-  for (uint32_t k = 0; k < n_used; k++) {
-    const uint64_t m = wave_max_u64(key);
-    if ((t & 63) == 0) wave_best[k & 1][wave] = m;
-    __syncthreads();
-    uint64_t best = wave_best[k & 1][0];
+  // 0 marks "taken or absent"; a real key is >= 1 (only one NaN pattern maps to 0)
+  uint32_t key[4];
 #pragma unroll
-    for (int v = 1; v < 4; v++) best = wave_best[k & 1][v] > best ? wave_best[k & 1][v] : best;
-    const uint32_t idx = ~(uint32_t)best;
-    if (t == 0) {
-      chosen_value[k] = key_value((uint32_t)(best >> 32));
-      chosen_index[k] = idx;
-    }
-    if (t == idx) key = 0;
+  for (int j = 0; j < 4; j++) {
+    const uint32_t e = t + 64 * j;
+    key[j] = e < n_expert ? max(order_key(a[logits_off + e]), 1u) : 0u;
   }
-  __syncthreads();
-  if (t != 0) return;
-  const float largest = chosen_value[0];
-  float total = 0.0f;
-  for (uint32_t k = 0; k < n_used; k++) total += expf(chosen_value[k] - largest);
+  float chosen = 0.0f;
+  uint32_t chosen_idx = 0;
   for (uint32_t k = 0; k < n_used; k++) {
-    ids[p.ids_off + tok * p.n_used + k] = chosen_index[k];
-    a[p.weights_off + tok * p.n_used + k] = expf(chosen_value[k] - largest) / total;
+    uint32_t m = max(max(key[0], key[1]), max(key[2], key[3]));
+    m = max(m, dpp_u<0xb1>(m));   // quad_perm [1,0,3,2]
+    m = max(m, dpp_u<0x4e>(m));   // quad_perm [2,3,0,1]
+    m = max(m, dpp_u<0x141>(m));  // row_half_mirror
+    m = max(m, dpp_u<0x140>(m));  // row_mirror
+    m = max(m, (uint32_t)__shfl_xor((int)m, 16, 64));
+    m = max(m, (uint32_t)__shfl_xor((int)m, 32, 64));
+    // lowest expert index holding m: the smallest j with a holder, then the lowest lane
+    uint32_t idx = 0;
+    bool found = false;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const uint64_t holders = __ballot(key[j] == m);
+      if (!found && holders != 0) {
+        idx = (uint32_t)__builtin_ctzll(holders) + 64 * j;
+        found = true;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+      if (idx == t + 64 * j) key[j] = 0;
+    if (t == k) {
+      chosen = key_value(m);
+      chosen_idx = idx;
+    }
+  }
+  const float largest = __shfl(chosen, 0, 64);
+  const float e = expf(chosen - largest);
+  float total = 0.0f;
+  for (uint32_t k = 0; k < n_used; k++) total += __shfl(e, (int)k, 64);
+  if (t < n_used) {
+    ids[p.ids_off + tok * p.n_used + t] = chosen_idx;
+    a[p.weights_off + tok * p.n_used + t] = e / total;
   }
 }
 

@@ -130,7 +130,7 @@ struct skyla_hip_pipeline {
   uint32_t push_words = 0;
   uint32_t threads = 256;
   bool segmented = false;
-  std::shared_ptr<const Retile> retile;  // dense matvec pipelines only
+  std::shared_ptr<const Retile> retile;  // matvec pipelines with a variant rule
   std::vector<std::vector<void *>> sets;
 };
 
@@ -175,8 +175,8 @@ Launch pack(const Command *const *run, uint32_t n) {
     return l;
   }
   const size_t w = a.push.size();
-  // a dense matvec launch may run on the variant that suits its total size; the grid is
-  // then recomputed from each segment's n_out (every row is still computed exactly once)
+  // a matvec launch may run on the variant that suits its total size; grid.x is then
+  // recomputed from each segment's n_out (every row is still computed exactly once)
   const MatvecAlt *alt = nullptr;
   if (a.retile) {
     uint64_t rows = 0;
@@ -295,35 +295,38 @@ hipFunction_t find_function(skyla_hip_context *ctx, const std::string &sym) {
   return nullptr;
 }
 
-// Variant choice for dense matvec launches, from sweeps of the Qwen3-8B decode shapes on
-// MI355X (n_in 4096 and 12288): eight-wave workgroups throughout; large launches gain from
-// fewer lanes per row (more pipelined load steps per lane, fewer workgroups staging the
-// activations), small ones from more workgroups.  Each entry is (min_rows, waves, rows,
-// lanes per row).
+// Variant choice for matvec launches, from sweeps on MI355X.  Dense rows (Qwen3-8B decode
+// shapes, n_in 4096 and 12288): eight-wave workgroups; large launches gain from fewer lanes
+// per row (more pipelined load steps per lane, fewer workgroups staging the activations),
+// small ones from more workgroups.  Expert rows (MOE = 1, grid.y = slots; config-4 gate/up
+// n_in 2048 and down n_in 768 over 8 slots): 16 lanes per row, one row each, four waves.
+// Each entry is (min_rows, waves, rows, lanes per row); grid.x follows from n_out.
 struct VariantRule {
   const char *name;
+  uint32_t moe;
   uint32_t n_out_word;
   struct { uint64_t min_rows; uint32_t waves, rows, lpr; } v[3];
   int n;
 };
 const VariantRule kVariantRules[] = {
-    {"matvec_q4k", 5, {{6144, 8, 1, 16}, {0, 8, 1, 64}}, 2},
-    {"matvec_q6k", 7, {{12288, 4, 1, 16}, {0, 4, 1, 32}}, 2},
+    {"matvec_q4k", 0, 5, {{6144, 8, 1, 16}, {0, 8, 1, 64}}, 2},
+    {"matvec_q6k", 0, 7, {{12288, 4, 1, 16}, {0, 4, 1, 32}}, 2},
+    {"matvec_q4k", 1, 5, {{0, 4, 1, 16}}, 1},
 };
 
 std::shared_ptr<const Retile> make_retile(skyla_hip_context *ctx, const char *name, const uint32_t *spec,
                                           uint32_t n_spec) {
-  if (n_spec != 5 || spec[3] != 0) return nullptr;  // dense pipelines only (MOE = 0)
+  if (n_spec != 5) return nullptr;
   if (const char *env = std::getenv("SKYLA_HIP_RETILE"); env && env[0] == '0') return nullptr;
   for (const VariantRule &r : kVariantRules) {
-    if (std::strcmp(r.name, name) != 0) continue;
+    if (std::strcmp(r.name, name) != 0 || r.moe != spec[3]) continue;
     auto t = std::make_shared<Retile>();
     t->n_out_word = r.n_out_word;
     for (int i = 0; i < r.n; i++) {
       const auto &v = r.v[i];
       const std::string sym = std::string(name) + "__" + std::to_string(v.waves) + "_" +
-                              std::to_string(spec[1]) + "_" + std::to_string(v.rows) + "_0_" +
-                              std::to_string(v.lpr);
+                              std::to_string(spec[1]) + "_" + std::to_string(v.rows) + "_" +
+                              std::to_string(spec[3]) + "_" + std::to_string(v.lpr);
       hipFunction_t fn = find_function(ctx, sym);
       if (!fn) return nullptr;  // keep the engine's variant if any alternative is missing
       t->alts.push_back({fn, v.waves * v.rows * (64 / v.lpr), 64 * v.waves, v.min_rows});
@@ -523,6 +526,7 @@ int skyla_hip_pipeline_new(skyla_hip_context *ctx, const char *name, uint32_t n_
     threads = k->waves ? 64 * spec[k->threads_from_spec] : spec[k->threads_from_spec];
   // matmul: dense tiles (MOE = 0) run eight waves, expert groups four (matmul.hip)
   if (std::strcmp(name, "matmul") == 0 && spec[2] == 0) threads = 512;
+  if (std::strcmp(name, "moe_route") == 0) threads = 64;  // one wave per token
   auto p = std::make_unique<skyla_hip_pipeline>();
   p->ctx = ctx;
   p->symbol = sym;

@@ -7,6 +7,8 @@ skyla-ref/src/ffn.rs:58-76), for a decode token and a 128-token prefill chunk.  
 near-ties can legitimately flip the route between two summation orders, so the chain tests
 skip a token whose 8th and 9th logits are closer than 1e-5 (none do at these seeds).
 """
+import os
+
 import numpy as np
 import pytest
 
@@ -52,9 +54,11 @@ class MoeSetup:
         a.set_ctl(0, 0, n.shape[0])
         a.buffer.upload()
 
-    def run_moe(self, batched: bool):
+    def run_moe(self, batched: bool, kernels=None):
+        k = kernels or self.k
+
         def body(r):
-            E.Graph(r, self.k, self.a, self.c, batched).moe(self.qg, self.qu, self.qd, self.router_off)
+            E.Graph(r, k, self.a, self.c, batched).moe(self.qg, self.qu, self.qd, self.router_off)
         rec = self.ctx.record(False, body)
         self.ctx.replay(rec)
         rec.free()
@@ -234,3 +238,32 @@ def test_moe_prefill_chunk(ctx, moe):
     assert checked >= n_tok - 2
     assert max(errs) <= 5e-3, max(errs)
     assert rel_l2(np.concatenate(gots), np.concatenate(outs)) <= 2e-3
+
+
+def test_moe_decode_expert_variant_choice(ctx, moe):
+    """Expert launches run on the variant the runtime picks for them (four waves, 16 lanes
+    per row); the layer output equals the engine-requested variants' up to f32 summation
+    order, and the route is the same."""
+    n = synth.activations(CFG, "variant-n", (1, N_EMBD))
+    x0 = synth.activations(CFG, "variant-x", (1, N_EMBD))
+    assert not _near_tie(moe.router, n[0])
+    got, ids = {}, {}
+    for retile in ("0", "1"):
+        old = os.environ.get("SKYLA_HIP_RETILE")
+        os.environ["SKYLA_HIP_RETILE"] = retile
+        try:
+            k = E.Kernels(ctx, moe.weights, moe.a.buffer)
+        finally:
+            if old is None:
+                del os.environ["SKYLA_HIP_RETILE"]
+            else:
+                os.environ["SKYLA_HIP_RETILE"] = old
+        moe.load(n, x0)
+        moe.run_moe(batched=False, kernels=k)
+        a, m = moe.a, moe.a.moe
+        got[retile] = moe.rows(a.x, a.s_embd, 1, N_EMBD)[0].astype(np.float64) - x0[0]
+        ids[retile] = list(a.u32()[m.ids: m.ids + N_USED])
+    assert ids["1"] == ids["0"]
+    assert rel_l2(got["1"], got["0"]) < 1e-5
+    out, _, _ = _oracle_moe(moe, n[0])
+    assert rel_l2(got["1"], out) <= 2e-3
