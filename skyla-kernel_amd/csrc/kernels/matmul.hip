@@ -430,8 +430,10 @@ SK_DEV void matmul_body(const uint4 *__restrict__ w, const uint16_t *__restrict_
 // ---------------------------------------------------------------------------------------
 constexpr int TN2 = 128;            // tokens per tile
 constexpr int NT2 = 512;            // threads per dense workgroup (8 waves, 2 per SIMD)
-constexpr int KX = 128;             // k per activation chunk
-constexpr int PITCH2 = KX + 8;      // f16 per staged token row (16 B pad)
+constexpr int KX_W = 256;           // k per activation chunk: K-quant tiles (one super-block)
+constexpr int KX_Q8 = 128;          // k per activation chunk: Q8_0 tile (register weights)
+template <int KX>
+constexpr int pitch2() { return KX + 8; }  // f16 per staged token row (16 B pad)
 
 // Per-lane scale/min of every step of a super-block, decoded once.
 template <int TYPE>
@@ -472,50 +474,53 @@ SK_DEV void stage_scales(const WStage<TYPE> &s, uint32_t hh, StageScales<TYPE> &
   }
 }
 
-// One KX-k activation chunk of the tile as 8-value groups: group G = tid + 256 i is token
-// G / (KX/8), values 8 (G % (KX/8)) + [0, 8) of the chunk, so the lanes of one load
-// instruction read whole 512-byte runs of a few token rows (coalesced).
-constexpr int GPT = TN2 * KX / 8 / NT2;  // groups per thread
-constexpr int GPR = KX / 8;              // groups per token row (lanes sharing a token)
-template <int XHALF>
+// One KX-k activation chunk of the tile.  f32 inputs: item J = tid + 512 i is 4 values,
+// token J / (KX/4), values 4 (J % (KX/4)) + [0, 4) of the chunk, so a load instruction
+// reads whole token rows with 16 consecutive bytes per lane.  f16 inputs: item = 8 values
+// (16 B), token J / (KX/8).  Either way the LDS row holds pairs (0,2),(1,3) of every four
+// values, the order of the packed-quant extraction.
+template <int KX, int XHALF>
 struct XChunk {
-  float4 v[XHALF ? 1 : 2 * GPT];
-  uint4 h[XHALF ? GPT : 1];
+  static constexpr int PER = XHALF ? 8 : 4;              // values per item
+  static constexpr int IPT = TN2 * KX / PER / NT2;       // items per thread
+  static constexpr int IPR = KX / PER;                   // items per token row
+  float4 v[XHALF ? 1 : IPT];
+  uint4 h[XHALF ? IPT : 1];
 };
 
-template <int XHALF>
-SK_DEV void load_chunk(XChunk<XHALF> &c, const void *xv, const uint32_t *xrow, uint32_t x_off,
+template <int KX, int XHALF>
+SK_DEV void load_chunk(XChunk<KX, XHALF> &c, const void *xv, const uint32_t *xrow, uint32_t x_off,
                        uint32_t x_stride, uint32_t k0, uint32_t n_in) {
+  constexpr int IPT = XChunk<KX, XHALF>::IPT, IPR = XChunk<KX, XHALF>::IPR, PER = XChunk<KX, XHALF>::PER;
 #pragma unroll
-  for (int i = 0; i < GPT; i++) {
-    const uint32_t G = threadIdx.x + NT2 * i;
-    const uint32_t kb = k0 + 8 * (G % GPR);
+  for (int i = 0; i < IPT; i++) {
+    const uint32_t J = threadIdx.x + NT2 * i;
+    const uint32_t kb = k0 + PER * (J % IPR);
     // load unconditionally from a clamped, in-bounds address; values past n_in are zeroed
     // when the chunk is stored (a select here would make the loads wait at once, and a
     // predicated load is split into per-dword branches)
-    const size_t base = (size_t)x_off + (size_t)xrow[G / GPR] * x_stride + (kb < n_in ? kb : n_in - 8);
-    if constexpr (XHALF) {
+    const size_t base = (size_t)x_off + (size_t)xrow[J / IPR] * x_stride + (kb < n_in ? kb : n_in - PER);
+    if constexpr (XHALF)
       c.h[i] = *(const uint4 *)((const f16 *)xv + base);
-    } else {
-      c.v[2 * i] = *(const float4 *)((const float *)xv + base);
-      c.v[2 * i + 1] = *(const float4 *)((const float *)xv + base + 4);
-    }
+    else
+      c.v[i] = *(const float4 *)((const float *)xv + base);
   }
 }
 
 // Stores a chunk to LDS, pair-permuted as the weight fragments; returns whether this
 // wave rescaled any token.
-template <int XHALF>
-SK_DEV bool store_chunk(f16 *lds, XChunk<XHALF> &c, int *exps, uint32_t k0, uint32_t n_in) {
+template <int KX, int XHALF>
+SK_DEV bool store_chunk(f16 *lds, XChunk<KX, XHALF> &c, int *exps, uint32_t k0, uint32_t n_in) {
+  constexpr int IPT = XChunk<KX, XHALF>::IPT, IPR = XChunk<KX, XHALF>::IPR, PER = XChunk<KX, XHALF>::PER;
+  constexpr int PITCH2 = pitch2<KX>();
   if (k0 + KX > n_in) {  // partial chunk (Q8_0 tail): zero the values past n_in
 #pragma unroll
-    for (int i = 0; i < GPT; i++) {
-      const bool live = k0 + 8 * ((threadIdx.x + NT2 * i) % GPR) < n_in;
+    for (int i = 0; i < IPT; i++) {
+      const bool live = k0 + PER * ((threadIdx.x + NT2 * i) % IPR) < n_in;
       if constexpr (XHALF) {
         if (!live) c.h[i] = make_uint4(0, 0, 0, 0);
       } else if (!live) {
-        c.v[2 * i] = make_float4(0.f, 0.f, 0.f, 0.f);
-        c.v[2 * i + 1] = make_float4(0.f, 0.f, 0.f, 0.f);
+        c.v[i] = make_float4(0.f, 0.f, 0.f, 0.f);
       }
     }
   }
@@ -523,42 +528,39 @@ SK_DEV bool store_chunk(f16 *lds, XChunk<XHALF> &c, int *exps, uint32_t k0, uint
   if constexpr (!XHALF) {
     float m = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 2 * GPT; i++)
+    for (int i = 0; i < IPT; i++)
       m = fmaxf(m, fmaxf(fmaxf(fabsf(c.v[i].x), fabsf(c.v[i].y)), fmaxf(fabsf(c.v[i].z), fabsf(c.v[i].w))));
     any = __ballot(!(m < 32768.0f)) != 0;  // NaN counts as big
   }
 #pragma unroll
-  for (int i = 0; i < GPT; i++) {
-    const uint32_t G = threadIdx.x + NT2 * i;
-    const uint32_t n = G / GPR, kg = G % GPR;
-    uint4 o;
-    int e = 0;
+  for (int i = 0; i < IPT; i++) {
+    const uint32_t J = threadIdx.x + NT2 * i;
+    const uint32_t n = J / IPR, kq = J % IPR;
     if constexpr (XHALF) {
       const uint4 v = c.h[i];
+      uint4 o;
       o.x = __builtin_amdgcn_perm(v.y, v.x, 0x05040100u);
       o.y = __builtin_amdgcn_perm(v.y, v.x, 0x07060302u);
       o.z = __builtin_amdgcn_perm(v.w, v.z, 0x05040100u);
       o.w = __builtin_amdgcn_perm(v.w, v.z, 0x07060302u);
+      *(uint4 *)(lds + n * PITCH2 + 8 * kq) = o;
+      if (kq == 0) exps[n] = 0;
     } else {
-      float4 a = c.v[2 * i], b = c.v[2 * i + 1];
-      if (any) {  // wave-uniform slow path: the token's max over its GPR lanes
-        float tm = fmaxf(fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))),
-                         fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w))));
+      float4 a = c.v[i];
+      int e = 0;
+      if (any) {  // wave-uniform slow path: the token's max over its IPR lanes
+        float tm = fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w)));
 #pragma unroll
-        for (int d = GPR / 2; d >= 1; d >>= 1) tm = fmaxf(tm, __shfl_xor(tm, d, 64));
+        for (int d = IPR / 2; d >= 1; d >>= 1) tm = fmaxf(tm, __shfl_xor(tm, d, 64));
         e = tm >= 32768.0f ? (int)((__builtin_bit_cast(uint32_t, tm) >> 23) & 255u) - 127 - 14 : 0;
         const float sc = __builtin_ldexpf(1.0f, -e);
         a = make_float4(a.x * sc, a.y * sc, a.z * sc, a.w * sc);
-        b = make_float4(b.x * sc, b.y * sc, b.z * sc, b.w * sc);
       }
-      // values k0..k7 = a.xyzw b.xyzw -> pairs (0,2),(1,3),(4,6),(5,7)
-      o.x = as_u32(pack_f16x2(a.x, a.z));
-      o.y = as_u32(pack_f16x2(a.y, a.w));
-      o.z = as_u32(pack_f16x2(b.x, b.z));
-      o.w = as_u32(pack_f16x2(b.y, b.w));
+      // values k0..k3 = a.xyzw -> pairs (0,2),(1,3)
+      *(uint2 *)(lds + n * PITCH2 + 4 * kq) =
+          make_uint2(as_u32(pack_f16x2(a.x, a.z)), as_u32(pack_f16x2(a.y, a.w)));
+      if (kq == 0) exps[n] = e;
     }
-    *(uint4 *)(lds + n * PITCH2 + 8 * kg) = o;
-    if (kg == 0) exps[n] = e;
   }
   return any;
 }
@@ -701,6 +703,7 @@ template <int TYPE, int ACCUM, int XHALF>
 SK_DEV void matmul_tile128_w(const uint4 *__restrict__ w, const uint16_t *__restrict__ wd, const void *x,
                              float *y, const uint32_t *ctl, const MatmulPush &p) {
   constexpr int NB = 2;
+  constexpr int KX = KX_W, PITCH2 = pitch2<KX>();
   constexpr uint32_t PW = WLds<TYPE>::PW;
   __shared__ __attribute__((aligned(16))) f16 xs[TN2 * PITCH2];
   __shared__ __attribute__((aligned(16))) uint32_t wl[TM * PW / 4];
@@ -737,10 +740,10 @@ SK_DEV void matmul_tile128_w(const uint4 *__restrict__ w, const uint16_t *__rest
   else wr.load(wr, w, wd, p, row0, 0, tid);
   __syncthreads();  // xrow
   {
-    XChunk<XHALF> c0;
-    load_chunk<XHALF>(c0, x, xrow, p.x_off, p.x_stride, 0, p.n_in);
+    XChunk<KX, XHALF> c0;
+    load_chunk<KX, XHALF>(c0, x, xrow, p.x_off, p.x_stride, 0, p.n_in);
     wr.store(wr, wl, tid);
-    const bool r = store_chunk<XHALF>(xs, c0, xexp, 0, p.n_in);
+    const bool r = store_chunk<KX, XHALF>(xs, c0, xexp, 0, p.n_in);
     if (lane == 0) xflag[wave] = r;
   }
   __syncthreads();
@@ -756,9 +759,9 @@ SK_DEV void matmul_tile128_w(const uint4 *__restrict__ w, const uint16_t *__rest
     }
 #pragma unroll
     for (int c4 = 0; c4 < KC / KX; c4++) {
-      XChunk<XHALF> xn;
+      XChunk<KX, XHALF> xn;
       const bool next = chunk + 1 < n_chunk;
-      if (next) load_chunk<XHALF>(xn, x, xrow, p.x_off, p.x_stride, (chunk + 1) * KX, p.n_in);
+      if (next) load_chunk<KX, XHALF>(xn, x, xrow, p.x_off, p.x_stride, (chunk + 1) * KX, p.n_in);
       bool rescaled = false;
 #pragma unroll
       for (int q = 0; q < NT2 / 64; q++) rescaled |= xflag[q] != 0;
@@ -804,7 +807,7 @@ SK_DEV void matmul_tile128_w(const uint4 *__restrict__ w, const uint16_t *__rest
       __syncthreads();  // every wave is done with this chunk (and, at the stage end, the weights)
       if (next) {
         if (c4 == KC / KX - 1 && more) wr.store(wr, wl, tid);
-        const bool r = store_chunk<XHALF>(xs, xn, xexp, (chunk + 1) * KX, p.n_in);
+        const bool r = store_chunk<KX, XHALF>(xs, xn, xexp, (chunk + 1) * KX, p.n_in);
         if (lane == 0) xflag[wave] = r;
         __syncthreads();
       }
@@ -833,6 +836,7 @@ SK_DEV void matmul_tile128(const uint4 *__restrict__ w, const uint16_t *__restri
   // wave w: rows 32 (w % 4) + [0, 32), tokens 64 (w / 4) + [0, 64) of the tile; the two
   // waves of a row block dequantise the same fragments (VALU) but share one weight stream
   constexpr int NB = 2;
+  constexpr int KX = KX_Q8, PITCH2 = pitch2<KX>();
   __shared__ __attribute__((aligned(16))) f16 xs[TN2 * PITCH2];
   __shared__ uint32_t xrow[TN2];
   __shared__ int xexp[TN2];
@@ -869,9 +873,9 @@ SK_DEV void matmul_tile128(const uint4 *__restrict__ w, const uint16_t *__restri
   WStage<TYPE> ws;
   load_stage<TYPE>(ws, w, wd, p, wrow, 0, min(p.n_in, (uint32_t)KC));
   {
-    XChunk<XHALF> c0;
-    load_chunk<XHALF>(c0, x, xrow, p.x_off, p.x_stride, 0, p.n_in);
-    const bool r = store_chunk<XHALF>(xs, c0, xexp, 0, p.n_in);
+    XChunk<KX, XHALF> c0;
+    load_chunk<KX, XHALF>(c0, x, xrow, p.x_off, p.x_stride, 0, p.n_in);
+    const bool r = store_chunk<KX, XHALF>(xs, c0, xexp, 0, p.n_in);
     if (lane == 0) xflag[wave] = r;
   }
   __syncthreads();
@@ -889,9 +893,9 @@ SK_DEV void matmul_tile128(const uint4 *__restrict__ w, const uint16_t *__restri
       if ((uint32_t)(KX * c4) < nk) {
         // the next chunk is loaded into registers while this one runs from LDS; the next
         // super-block's weights are requested during the stage's last chunk, after it
-        XChunk<XHALF> xn;
+        XChunk<KX, XHALF> xn;
         const bool next = chunk + 1 < n_chunk;
-        if (next) load_chunk<XHALF>(xn, x, xrow, p.x_off, p.x_stride, (chunk + 1) * KX, p.n_in);
+        if (next) load_chunk<KX, XHALF>(xn, x, xrow, p.x_off, p.x_stride, (chunk + 1) * KX, p.n_in);
         if (c4 == KC / KX - 1 && more) load_stage<TYPE>(wn, w, wd, p, wrow, kc + KC, min(p.n_in - kc - KC, (uint32_t)KC));
         bool rescaled = false;
 #pragma unroll
@@ -944,7 +948,7 @@ SK_DEV void matmul_tile128(const uint4 *__restrict__ w, const uint16_t *__restri
         }
         __syncthreads();  // every wave is done with this chunk
         if (next) {
-          const bool r = store_chunk<XHALF>(xs, xn, xexp, (chunk + 1) * KX, p.n_in);
+          const bool r = store_chunk<KX, XHALF>(xs, xn, xexp, (chunk + 1) * KX, p.n_in);
           if (lane == 0) xflag[wave] = r;
           __syncthreads();
         }
