@@ -479,22 +479,23 @@ SK_DEV void stage_scales(const WStage<TYPE> &s, uint32_t hh, StageScales<TYPE> &
 // reads whole token rows with 16 consecutive bytes per lane.  f16 inputs: item = 8 values
 // (16 B), token J / (KX/8).  Either way the LDS row holds pairs (0,2),(1,3) of every four
 // values, the order of the packed-quant extraction.
-template <int KX, int XHALF>
+template <int KX, int XHALF, int NT>
 struct XChunk {
   static constexpr int PER = XHALF ? 8 : 4;              // values per item
-  static constexpr int IPT = TN2 * KX / PER / NT2;       // items per thread
+  static constexpr int IPT = TN2 * KX / PER / NT;        // items per thread
   static constexpr int IPR = KX / PER;                   // items per token row
   float4 v[XHALF ? 1 : IPT];
   uint4 h[XHALF ? IPT : 1];
 };
 
-template <int KX, int XHALF>
-SK_DEV void load_chunk(XChunk<KX, XHALF> &c, const void *xv, const uint32_t *xrow, uint32_t x_off,
+template <int KX, int XHALF, int NT>
+SK_DEV void load_chunk(XChunk<KX, XHALF, NT> &c, const void *xv, const uint32_t *xrow, uint32_t x_off,
                        uint32_t x_stride, uint32_t k0, uint32_t n_in) {
-  constexpr int IPT = XChunk<KX, XHALF>::IPT, IPR = XChunk<KX, XHALF>::IPR, PER = XChunk<KX, XHALF>::PER;
+  using C = XChunk<KX, XHALF, NT>;
+  constexpr int IPT = C::IPT, IPR = C::IPR, PER = C::PER;
 #pragma unroll
   for (int i = 0; i < IPT; i++) {
-    const uint32_t J = threadIdx.x + NT2 * i;
+    const uint32_t J = threadIdx.x + NT * i;
     const uint32_t kb = k0 + PER * (J % IPR);
     // load unconditionally from a clamped, in-bounds address; values past n_in are zeroed
     // when the chunk is stored (a select here would make the loads wait at once, and a
@@ -509,14 +510,15 @@ SK_DEV void load_chunk(XChunk<KX, XHALF> &c, const void *xv, const uint32_t *xro
 
 // Stores a chunk to LDS, pair-permuted as the weight fragments; returns whether this
 // wave rescaled any token.
-template <int KX, int XHALF>
-SK_DEV bool store_chunk(f16 *lds, XChunk<KX, XHALF> &c, int *exps, uint32_t k0, uint32_t n_in) {
-  constexpr int IPT = XChunk<KX, XHALF>::IPT, IPR = XChunk<KX, XHALF>::IPR, PER = XChunk<KX, XHALF>::PER;
+template <int KX, int XHALF, int NT>
+SK_DEV bool store_chunk(f16 *lds, XChunk<KX, XHALF, NT> &c, int *exps, uint32_t k0, uint32_t n_in) {
+  using C = XChunk<KX, XHALF, NT>;
+  constexpr int IPT = C::IPT, IPR = C::IPR, PER = C::PER;
   constexpr int PITCH2 = pitch2<KX>();
   if (k0 + KX > n_in) {  // partial chunk (Q8_0 tail): zero the values past n_in
 #pragma unroll
     for (int i = 0; i < IPT; i++) {
-      const bool live = k0 + PER * ((threadIdx.x + NT2 * i) % IPR) < n_in;
+      const bool live = k0 + PER * ((threadIdx.x + NT * i) % IPR) < n_in;
       if constexpr (XHALF) {
         if (!live) c.h[i] = make_uint4(0, 0, 0, 0);
       } else if (!live) {
@@ -534,7 +536,7 @@ SK_DEV bool store_chunk(f16 *lds, XChunk<KX, XHALF> &c, int *exps, uint32_t k0, 
   }
 #pragma unroll
   for (int i = 0; i < IPT; i++) {
-    const uint32_t J = threadIdx.x + NT2 * i;
+    const uint32_t J = threadIdx.x + NT * i;
     const uint32_t n = J / IPR, kq = J % IPR;
     if constexpr (XHALF) {
       const uint4 v = c.h[i];
@@ -569,25 +571,27 @@ SK_DEV bool store_chunk(f16 *lds, XChunk<KX, XHALF> &c, int *exps, uint32_t k0, 
 // raw block bytes are loaded with whole-line 16 B loads (8 or 13 lanes per row) and every
 // lane then reads the 8 bytes it dequantises per step from LDS.  Rows are PW bytes apart
 // (PW/4 odd multiple of 2 dwords), so the 32 rows a wave reads hit distinct bank pairs.
-template <int TYPE>
+// NT threads share the loads (NT >= 256).
+template <int TYPE, int NT>
 struct WLds;
-template <>
-struct WLds<1> {  // Q4_K row: qs 128 | header 16
+template <int NT>
+struct WLds<1, NT> {  // Q4_K row: qs 128 | header 16
   static constexpr uint32_t PW = 152;
-  uint4 q[2], hd;
+  static constexpr int QI = TM * 8 / NT;  // qs units per thread
+  uint4 q[QI], hd;
   SK_DEV void load(WLds &r, const uint4 *w, const MatmulPush &p, uint32_t row0, uint32_t sb, uint32_t tid) {
     const uint32_t units = p.n_in >> 5, supers = p.n_in >> 8;
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
-      const uint32_t u = tid + NT2 * i, lr = u >> 3;
+    for (int i = 0; i < QI; i++) {
+      const uint32_t u = tid + NT * i, lr = u >> 3;
       r.q[i] = w[p.o0 + min(row0 + lr, p.n_out - 1) * units + sb * 8 + (u & 7)];
     }
     if (tid < TM) r.hd = w[p.o1 + min(row0 + tid, p.n_out - 1) * supers + sb];
   }
   SK_DEV void store(const WLds &r, uint32_t *lds, uint32_t tid) {
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
-      const uint32_t u = tid + NT2 * i, lr = u >> 3;
+    for (int i = 0; i < QI; i++) {
+      const uint32_t u = tid + NT * i, lr = u >> 3;
       uint2 *d = (uint2 *)(lds + (lr * PW + 16 * (u & 7)) / 4);
       d[0] = make_uint2(r.q[i].x, r.q[i].y);
       d[1] = make_uint2(r.q[i].z, r.q[i].w);
@@ -599,22 +603,24 @@ struct WLds<1> {  // Q4_K row: qs 128 | header 16
     }
   }
 };
-template <>
-struct WLds<2> {  // Q6_K row: ql 128 | qh 64 | scales 16 | d 2
+template <int NT>
+struct WLds<2, NT> {  // Q6_K row: ql 128 | qh 64 | scales 16 | d 2
   static constexpr uint32_t PW = 216;
-  uint4 ql[2], qh, sc;
+  static constexpr int LI = TM * 8 / NT, HI = TM * 4 / NT;  // ql / qh units per thread
+  uint4 ql[LI], qh[HI], sc;
   uint32_t d;
   SK_DEV void load(WLds &r, const uint4 *w, const uint16_t *wd, const MatmulPush &p, uint32_t row0,
                    uint32_t sb, uint32_t tid) {
     const uint32_t supers = p.n_in >> 8;
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
-      const uint32_t u = tid + NT2 * i, lr = u >> 3;
+    for (int i = 0; i < LI; i++) {
+      const uint32_t u = tid + NT * i, lr = u >> 3;
       r.ql[i] = w[p.o0 + (min(row0 + lr, p.n_out - 1) * supers + sb) * 8 + (u & 7)];
     }
-    {
-      const uint32_t lr = tid >> 2;
-      r.qh = w[p.o1 + (min(row0 + lr, p.n_out - 1) * supers + sb) * 4 + (tid & 3)];
+#pragma unroll
+    for (int i = 0; i < HI; i++) {
+      const uint32_t u = tid + NT * i, lr = u >> 2;
+      r.qh[i] = w[p.o1 + (min(row0 + lr, p.n_out - 1) * supers + sb) * 4 + (u & 3)];
     }
     const uint32_t lr = tid & (TM - 1);
     const uint32_t rs = min(row0 + lr, p.n_out - 1) * supers + sb;
@@ -623,17 +629,18 @@ struct WLds<2> {  // Q6_K row: ql 128 | qh 64 | scales 16 | d 2
   }
   SK_DEV void store(const WLds &r, uint32_t *lds, uint32_t tid) {
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
-      const uint32_t u = tid + NT2 * i, lr = u >> 3;
+    for (int i = 0; i < LI; i++) {
+      const uint32_t u = tid + NT * i, lr = u >> 3;
       uint2 *d = (uint2 *)(lds + (lr * PW + 16 * (u & 7)) / 4);
       d[0] = make_uint2(r.ql[i].x, r.ql[i].y);
       d[1] = make_uint2(r.ql[i].z, r.ql[i].w);
     }
-    {
-      const uint32_t lr = tid >> 2;
-      uint2 *d = (uint2 *)(lds + (lr * PW + 128 + 16 * (tid & 3)) / 4);
-      d[0] = make_uint2(r.qh.x, r.qh.y);
-      d[1] = make_uint2(r.qh.z, r.qh.w);
+#pragma unroll
+    for (int i = 0; i < HI; i++) {
+      const uint32_t u = tid + NT * i, lr = u >> 2;
+      uint2 *d = (uint2 *)(lds + (lr * PW + 128 + 16 * (u & 3)) / 4);
+      d[0] = make_uint2(r.qh[i].x, r.qh[i].y);
+      d[1] = make_uint2(r.qh[i].z, r.qh[i].w);
     }
     const uint32_t lr = tid & (TM - 1);
     if (tid < TM) {
@@ -697,29 +704,44 @@ SK_DEV void lds_scales(const uint32_t *row, uint32_t hh, StageScales<TYPE> &o) {
   stage_scales<TYPE>(s, hh, o);
 }
 
-// Dense tile with LDS-staged K-quant weights (Q4_K, Q6_K); layout and activation path as
-// matmul_tile128.
-template <int TYPE, int ACCUM, int XHALF>
+// Dense tile with LDS-staged K-quant weights (Q4_K, Q6_K), 128 rows x 128 tokens.
+//   NW = 8: waves of 32 rows x 64 tokens (two per SIMD), 256-k activation chunks.
+//   NW = 4: waves of 32 rows x all 128 tokens, 128-k chunks: each dequantised weight
+//     fragment feeds four MFMAs instead of two (half the VALU per MFMA) and the ~54 KB of
+//     LDS lets two workgroups share a CU.
+// K split: with S > 1, grid.z = token tiles x S and workgroup (row tile, token tile, split)
+// runs its share of the super-blocks.  Each writes its f32 partial tile to `ws` with
+// coherent (sc1) stores, drains them, and counts itself in cnt[tile]; the last of the S
+// sums the partials in split order (deterministic) and writes y, then resets the count
+// for the next launch.  No workgroup ever waits for another.
+template <int TYPE, int ACCUM, int XHALF, int NW>
 SK_DEV void matmul_tile128_w(const uint4 *__restrict__ w, const uint16_t *__restrict__ wd, const void *x,
-                             float *y, const uint32_t *ctl, const MatmulPush &p) {
-  constexpr int NB = 2;
-  constexpr int KX = KX_W, PITCH2 = pitch2<KX>();
-  constexpr uint32_t PW = WLds<TYPE>::PW;
+                             float *y, const uint32_t *ctl, const MatmulPush &p, float *ws = nullptr,
+                             uint32_t *cnt = nullptr, uint32_t S = 1) {
+  constexpr int NT = 64 * NW;
+  constexpr int NB = NW == 8 ? 2 : 4;  // 32-token blocks per wave
+  constexpr int KX = NW == 8 ? KX_W : 128, PITCH2 = pitch2<KX>();
+  constexpr uint32_t PW = WLds<TYPE, NT>::PW;
   __shared__ __attribute__((aligned(16))) f16 xs[TN2 * PITCH2];
   __shared__ __attribute__((aligned(16))) uint32_t wl[TM * PW / 4];
   __shared__ uint32_t xrow[TN2];
   __shared__ int xexp[TN2];
-  __shared__ uint32_t xflag[NT2 / 64];
+  __shared__ uint32_t xflag[NW];
+  __shared__ uint32_t last;
 
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = tid & 63, wave = tid >> 6;
   const uint32_t hh = lane >> 5;
-  const uint32_t rb = wave & 3, tb = 2 * (wave >> 2);
-  const uint32_t gx = gridDim.x, gz = gridDim.z;
+  const uint32_t rb = NW == 8 ? (wave & 3) : wave, tb = NW == 8 ? 2 * (wave >> 2) : 0;
+  // Tile order: workgroups are dealt to the 8 XCDs round-robin by linear id, and
+  // consecutive ids take consecutive token tiles (then splits), so the workgroups of one
+  // XCD share a token tile's activations in that XCD's L2.
+  const uint32_t gx = gridDim.x, gz = gridDim.z, Z = gz / S;
   const uint32_t lin = blockIdx.x + gx * blockIdx.z;
-  const uint32_t row0 = (lin / gz) * TM;
+  const uint32_t rt = lin / gz, rem = lin % gz, tt = rem % Z, sp = rem / Z;
+  const uint32_t row0 = rt * TM;
   const uint32_t n_all = ctl[2];
-  const uint32_t col0 = (lin % gz) * TN2;
+  const uint32_t col0 = tt * TN2;
   if (col0 >= n_all) return;
   const uint32_t n_tok = min(n_all - col0, (uint32_t)TN2);
   if (tid < TN2) xrow[tid] = col0 + min(tid, n_tok - 1);
@@ -733,17 +755,20 @@ SK_DEV void matmul_tile128_w(const uint4 *__restrict__ w, const uint16_t *__rest
 #pragma unroll
     for (int i = 0; i < 16; i++) acc[j][i] = 0.0f;
 
-  const uint32_t n_stage = p.n_in / KC;
-  const uint32_t n_chunk = p.n_in / KX;
-  WLds<TYPE> wr;
-  if constexpr (TYPE == 1) wr.load(wr, w, p, row0, 0, tid);
-  else wr.load(wr, w, wd, p, row0, 0, tid);
+  const uint32_t n_stage_all = p.n_in / KC;
+  const uint32_t st0 = sp * n_stage_all / S, st1 = (sp + 1) * n_stage_all / S;
+  const uint32_t n_stage = st1 - st0;
+  const uint32_t n_chunk = n_stage * (KC / KX);
+  const uint32_t kbase = st0 * KC;
+  WLds<TYPE, NT> wr;
+  if constexpr (TYPE == 1) wr.load(wr, w, p, row0, st0, tid);
+  else wr.load(wr, w, wd, p, row0, st0, tid);
   __syncthreads();  // xrow
   {
-    XChunk<KX, XHALF> c0;
-    load_chunk<KX, XHALF>(c0, x, xrow, p.x_off, p.x_stride, 0, p.n_in);
+    XChunk<KX, XHALF, NT> c0;
+    load_chunk<KX, XHALF, NT>(c0, x, xrow, p.x_off, p.x_stride, kbase, p.n_in);
     wr.store(wr, wl, tid);
-    const bool r = store_chunk<KX, XHALF>(xs, c0, xexp, 0, p.n_in);
+    const bool r = store_chunk<KX, XHALF, NT>(xs, c0, xexp, kbase, p.n_in);
     if (lane == 0) xflag[wave] = r;
   }
   __syncthreads();
@@ -754,17 +779,17 @@ SK_DEV void matmul_tile128_w(const uint4 *__restrict__ w, const uint16_t *__rest
     lds_scales<TYPE>(wrow, hh, ss);
     const bool more = st + 1 < n_stage;
     if (more) {
-      if constexpr (TYPE == 1) wr.load(wr, w, p, row0, st + 1, tid);
-      else wr.load(wr, w, wd, p, row0, st + 1, tid);
+      if constexpr (TYPE == 1) wr.load(wr, w, p, row0, st0 + st + 1, tid);
+      else wr.load(wr, w, wd, p, row0, st0 + st + 1, tid);
     }
 #pragma unroll
     for (int c4 = 0; c4 < KC / KX; c4++) {
-      XChunk<KX, XHALF> xn;
+      XChunk<KX, XHALF, NT> xn;
       const bool next = chunk + 1 < n_chunk;
-      if (next) load_chunk<KX, XHALF>(xn, x, xrow, p.x_off, p.x_stride, (chunk + 1) * KX, p.n_in);
+      if (next) load_chunk<KX, XHALF, NT>(xn, x, xrow, p.x_off, p.x_stride, kbase + (chunk + 1) * KX, p.n_in);
       bool rescaled = false;
 #pragma unroll
-      for (int q = 0; q < NT2 / 64; q++) rescaled |= xflag[q] != 0;
+      for (int q = 0; q < NW; q++) rescaled |= xflag[q] != 0;
       if (rescaled) {
 #pragma unroll
         for (int j = 0; j < NB; j++)
@@ -774,8 +799,8 @@ SK_DEV void matmul_tile128_w(const uint4 *__restrict__ w, const uint16_t *__rest
       }
       constexpr int SPC = KX / 16;
       f16x8 xf0[NB], xf1[NB], wf0, wf1;
-      auto frags = [&](int tt, f16x8(&xf)[NB], f16x8 &wf) {
-        const int t = SPC * c4 + tt;
+      auto frags = [&](int ts, f16x8(&xf)[NB], f16x8 &wf) {
+        const int t = SPC * c4 + ts;
         f16x2 sc, nm;
         ss.get(t, sc, nm);
         wf = lds_frag<TYPE>(wrow, t, hh, sc, nm);
@@ -785,16 +810,16 @@ SK_DEV void matmul_tile128_w(const uint4 *__restrict__ w, const uint16_t *__rest
       };
       frags(0, xf0, wf0);
 #pragma unroll
-      for (int tt = 0; tt < SPC; tt++) {
-        if (tt + 1 < SPC) {
-          if (tt & 1)
-            frags(tt + 1, xf0, wf0);
+      for (int ts = 0; ts < SPC; ts++) {
+        if (ts + 1 < SPC) {
+          if (ts & 1)
+            frags(ts + 1, xf0, wf0);
           else
-            frags(tt + 1, xf1, wf1);
+            frags(ts + 1, xf1, wf1);
         }
 #pragma unroll
         for (int j = 0; j < NB; j++)
-          acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16((tt & 1) ? xf1[j] : xf0[j], (tt & 1) ? wf1 : wf0,
+          acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16((ts & 1) ? xf1[j] : xf0[j], (ts & 1) ? wf1 : wf0,
                                                           acc[j], 0, 0, 0);
       }
       if (rescaled) {
@@ -807,12 +832,43 @@ SK_DEV void matmul_tile128_w(const uint4 *__restrict__ w, const uint16_t *__rest
       __syncthreads();  // every wave is done with this chunk (and, at the stage end, the weights)
       if (next) {
         if (c4 == KC / KX - 1 && more) wr.store(wr, wl, tid);
-        const bool r = store_chunk<KX, XHALF>(xs, xn, xexp, (chunk + 1) * KX, p.n_in);
+        const bool r = store_chunk<KX, XHALF, NT>(xs, xn, xexp, kbase + (chunk + 1) * KX, p.n_in);
         if (lane == 0) xflag[wave] = r;
         __syncthreads();
       }
       chunk++;
     }
+  }
+
+  if (S > 1) {
+    const uint32_t tile = rt * Z + tt;
+    constexpr uint32_t PART = NW * NB * 16 * 64;  // floats of one partial tile
+    float *mine = ws + (size_t)(tile * S + sp) * PART + wave * (NB * 16 * 64);
+#pragma unroll
+    for (int j = 0; j < NB; j++)
+#pragma unroll
+      for (int i = 0; i < 16; i++)
+        __hip_atomic_store(mine + (j * 16 + i) * 64 + lane, acc[j][i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);  // the coherent stores are done before the count
+    __syncthreads();
+    if (tid == 0) last = __hip_atomic_fetch_add(&cnt[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == S - 1;
+    __syncthreads();
+    if (!last) return;
+#pragma unroll
+    for (int j = 0; j < NB; j++)
+#pragma unroll
+      for (int i = 0; i < 16; i++) {
+        float t = 0.0f;
+        for (uint32_t q = 0; q < S; q++) {
+          const float v = q == sp ? acc[j][i]
+                                  : __hip_atomic_load(ws + (size_t)(tile * S + q) * PART + wave * (NB * 16 * 64) +
+                                                          (j * 16 + i) * 64 + lane,
+                                                      __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          t = q == 0 ? v : t + v;
+        }
+        acc[j][i] = t;
+      }
+    if (tid == 0) __hip_atomic_store(&cnt[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 
   if (my_row < p.n_out) {
@@ -873,9 +929,9 @@ SK_DEV void matmul_tile128(const uint4 *__restrict__ w, const uint16_t *__restri
   WStage<TYPE> ws;
   load_stage<TYPE>(ws, w, wd, p, wrow, 0, min(p.n_in, (uint32_t)KC));
   {
-    XChunk<KX, XHALF> c0;
-    load_chunk<KX, XHALF>(c0, x, xrow, p.x_off, p.x_stride, 0, p.n_in);
-    const bool r = store_chunk<KX, XHALF>(xs, c0, xexp, 0, p.n_in);
+    XChunk<KX, XHALF, NT2> c0;
+    load_chunk<KX, XHALF, NT2>(c0, x, xrow, p.x_off, p.x_stride, 0, p.n_in);
+    const bool r = store_chunk<KX, XHALF, NT2>(xs, c0, xexp, 0, p.n_in);
     if (lane == 0) xflag[wave] = r;
   }
   __syncthreads();
@@ -893,9 +949,9 @@ SK_DEV void matmul_tile128(const uint4 *__restrict__ w, const uint16_t *__restri
       if ((uint32_t)(KX * c4) < nk) {
         // the next chunk is loaded into registers while this one runs from LDS; the next
         // super-block's weights are requested during the stage's last chunk, after it
-        XChunk<KX, XHALF> xn;
+        XChunk<KX, XHALF, NT2> xn;
         const bool next = chunk + 1 < n_chunk;
-        if (next) load_chunk<KX, XHALF>(xn, x, xrow, p.x_off, p.x_stride, (chunk + 1) * KX, p.n_in);
+        if (next) load_chunk<KX, XHALF, NT2>(xn, x, xrow, p.x_off, p.x_stride, (chunk + 1) * KX, p.n_in);
         if (c4 == KC / KX - 1 && more) load_stage<TYPE>(wn, w, wd, p, wrow, kc + KC, min(p.n_in - kc - KC, (uint32_t)KC));
         bool rescaled = false;
 #pragma unroll
@@ -948,7 +1004,7 @@ SK_DEV void matmul_tile128(const uint4 *__restrict__ w, const uint16_t *__restri
         }
         __syncthreads();  // every wave is done with this chunk
         if (next) {
-          const bool r = store_chunk<KX, XHALF>(xs, xn, xexp, (chunk + 1) * KX, p.n_in);
+          const bool r = store_chunk<KX, XHALF, NT2>(xs, xn, xexp, (chunk + 1) * KX, p.n_in);
           if (lane == 0) xflag[wave] = r;
           __syncthreads();
         }
@@ -978,7 +1034,7 @@ SK_DEV void matmul_tile128(const uint4 *__restrict__ w, const uint16_t *__restri
 // Dense (MOE = 0) launches use the 128 x 128 tile; expert groups (MOE = 1) the 128 x 32 one.
 #define MM_BODY(T, A, M, H)                                                     \
   if constexpr (M == 0 && T != 0)                                               \
-    matmul_tile128_w<T, A, H>(w, wd, x, y, ctl, p);                             \
+    matmul_tile128_w<T, A, H, 8>(w, wd, x, y, ctl, p);                          \
   else if constexpr (M == 0)                                                    \
     matmul_tile128<T, A, H>(w, wd, x, y, ctl, p);                               \
   else                                                                          \
@@ -1005,3 +1061,25 @@ SK_DEV void matmul_tile128(const uint4 *__restrict__ w, const uint16_t *__restri
 MM_TYPE(0)
 MM_TYPE(1)
 MM_TYPE(2)
+
+// Runtime-internal dense K-quant variants (not engine symbols): NW = 4 or 8 waves, with a
+// K split over workspace `ws` and counters `cnt` (zeroed once; each launch leaves them zero).
+#define MMX(T, A, H, XT)                                                                          \
+  extern "C" __global__ __launch_bounds__(256) void matmul_w4__##T##_##A##_##H(                   \
+      const uint4 *w, const uint16_t *wd, const XT *x, float *y, const uint32_t *ctl,             \
+      MatmulPush p, float *ws, uint32_t *cnt, uint32_t S) {                                       \
+    matmul_tile128_w<T, A, H, 4>(w, wd, x, y, ctl, p, ws, cnt, S);                                \
+  }                                                                                               \
+  extern "C" __global__ __launch_bounds__(512) void matmul_w8__##T##_##A##_##H(                   \
+      const uint4 *w, const uint16_t *wd, const XT *x, float *y, const uint32_t *ctl,             \
+      MatmulPush p, float *ws, uint32_t *cnt, uint32_t S) {                                       \
+    matmul_tile128_w<T, A, H, 8>(w, wd, x, y, ctl, p, ws, cnt, S);                                \
+  }
+MMX(1, 0, 0, float)
+MMX(1, 1, 0, float)
+MMX(1, 0, 1, f16)
+MMX(1, 1, 1, f16)
+MMX(2, 0, 0, float)
+MMX(2, 1, 0, float)
+MMX(2, 0, 1, f16)
+MMX(2, 1, 1, f16)

@@ -131,6 +131,8 @@ struct skyla_hip_pipeline {
   uint32_t threads = 256;
   bool segmented = false;
   std::shared_ptr<const Retile> retile;  // matvec pipelines with a variant rule
+  hipFunction_t split_fn = nullptr;      // dense K-quant matmul: the K-split variant
+  uint32_t split_threads = 0;
   std::vector<std::vector<void *>> sets;
 };
 
@@ -142,6 +144,8 @@ struct Command {
   uint32_t threads = 0;
   bool segmented = false;
   std::shared_ptr<const Retile> retile;
+  hipFunction_t split_fn = nullptr;
+  uint32_t split_threads = 0;
   uint32_t groups[3] = {0, 0, 0};
   std::vector<void *> bufs;
   std::vector<uint32_t> push;
@@ -158,9 +162,31 @@ struct Launch {
   uint32_t groups[3] = {0, 0, 0};
   std::vector<void *> bufs;
   std::vector<uint32_t> args;
+  // K split (matmul): S > 1 appends (workspace, counters, S) to the kernel arguments
+  uint32_t split = 0;
+  uint64_t ws_bytes = 0;  // partial tiles
+  uint32_t n_cnt = 0;     // per-tile counters
+  void *ws = nullptr;
+  void *cnt = nullptr;
 };
 
 constexpr uint32_t kMaxSeg = 4;  // MAXSEG in kernels/common.h
+constexpr uint64_t kSplitTileBytes = 128 * 128 * 4;  // one f32 partial tile (kernels/matmul.hip)
+
+// K split of a dense K-quant matmul launch (matmul.hip, matmul_tile128_w): launches of at
+// most 128 tiles of 128 x 128 leave CUs idle (the tile keeps one workgroup per CU), so
+// their super-blocks are split over up to 256 workgroups, keeping at least 4 per split.
+// Measured on MI355X at M = 512: 4096 x 4096 68.6 -> 53.0 us, 4096 x 12288 191.6 -> 119.3 us.
+uint32_t split_of(const Command &a) {
+  if (!a.split_fn || a.push.size() < 7) return 1;
+  const uint64_t tiles = (uint64_t)a.groups[0] * a.groups[1] * a.groups[2];
+  const uint32_t n_stage = a.push[6] / 256;  // MatmulPush.n_in
+  if (tiles == 0 || tiles > 128) return 1;
+  uint32_t S = (uint32_t)(256 / tiles);
+  S = std::min(S, n_stage / 4);
+  S = std::min(S, 8u);
+  return S < 2 ? 1 : S;
+}
 
 // Packs consecutive dispatches of one segmented kernel into one launch.
 Launch pack(const Command *const *run, uint32_t n) {
@@ -172,6 +198,15 @@ Launch pack(const Command *const *run, uint32_t n) {
   if (!a.segmented) {
     for (int i = 0; i < 3; i++) l.groups[i] = a.groups[i];
     l.args = a.push;
+    const uint32_t S = split_of(a);
+    if (S > 1) {
+      l.fn = a.split_fn;
+      l.threads = a.split_threads;
+      l.groups[2] = a.groups[2] * S;
+      l.split = S;
+      l.n_cnt = a.groups[0] * a.groups[2];
+      l.ws_bytes = (uint64_t)l.n_cnt * S * kSplitTileBytes;
+    }
     return l;
   }
   const size_t w = a.push.size();
@@ -256,8 +291,45 @@ int launch(hipStream_t stream, const Launch &l) {
   params.reserve(l.bufs.size() + 1);
   for (void *const &p : l.bufs) params.push_back(const_cast<void **>(&p));
   params.push_back(const_cast<uint32_t *>(l.args.data()));
+  if (l.split) {
+    params.push_back(const_cast<void **>(&l.ws));
+    params.push_back(const_cast<void **>(&l.cnt));
+    params.push_back(const_cast<uint32_t *>(&l.split));
+  }
   HIP_TRY(hipModuleLaunchKernel(l.fn, l.groups[0], l.groups[1], l.groups[2], l.threads, 1, 1, 0,
                                 stream, params.data(), nullptr));
+  return SKYLA_HIP_OK;
+}
+
+// Gives the K-split launches of a list their workspace: one device allocation (partial
+// tiles, then per-tile counters) sized for the largest, shared by all of them since the
+// launches of a list run one after another on one stream.  The counters are zeroed here,
+// outside any graph capture, and every launch leaves them zero.  *owned receives the
+// allocation (nullptr when no launch splits).
+int bind_workspace(std::vector<Launch> &ls, void **owned) {
+  *owned = nullptr;
+  uint64_t ws = 0, n_cnt = 0;
+  for (const Launch &l : ls)
+    if (l.split) {
+      ws = std::max(ws, l.ws_bytes);
+      n_cnt = std::max<uint64_t>(n_cnt, l.n_cnt);
+    }
+  if (!ws) return SKYLA_HIP_OK;
+  const uint64_t cnt_off = (ws + 255) & ~(uint64_t)255;
+  void *mem = nullptr;
+  HIP_TRY(hipMalloc(&mem, cnt_off + n_cnt * 4));
+  hipError_t e = hipMemset((char *)mem + cnt_off, 0, n_cnt * 4);
+  if (e == hipSuccess) e = hipDeviceSynchronize();
+  if (e != hipSuccess) {
+    hipFree(mem);
+    return fail(SKYLA_HIP_E_DEVICE, "K-split workspace: %s", hipGetErrorString(e));
+  }
+  for (Launch &l : ls)
+    if (l.split) {
+      l.ws = mem;
+      l.cnt = (char *)mem + cnt_off;
+    }
+  *owned = mem;
   return SKYLA_HIP_OK;
 }
 
@@ -277,6 +349,7 @@ struct skyla_hip_recording {
   bool profile = false;
   std::vector<Command> cmds;
   std::vector<Launch> launches;
+  void *workspace = nullptr;  // K-split partials and counters of the launches
   hipGraphExec_t exec = nullptr;
   hipGraph_t graph = nullptr;
   std::vector<std::string> labels;
@@ -547,6 +620,17 @@ int skyla_hip_pipeline_new(skyla_hip_context *ctx, const char *name, uint32_t n_
   if (!p->fn)
     return fail(SKYLA_HIP_E_NO_KERNEL, "no gfx950 kernel %s for this spec", sym.c_str());
   p->retile = make_retile(ctx, name, spec, n_spec);
+  // dense K-quant matmul (TYPE 1/2, MOE 0): its K-split variant, used for launches with few
+  // tiles (split_of); SKYLA_HIP_SPLITK=0 keeps every launch on the engine's kernel
+  if (std::strcmp(name, "matmul") == 0 && n_spec >= 3 && (spec[0] == 1 || spec[0] == 2) && spec[2] == 0) {
+    const char *env = std::getenv("SKYLA_HIP_SPLITK");
+    if (!(env && env[0] == '0')) {
+      const std::string ssym = "matmul_w8__" + std::to_string(spec[0]) + "_" + std::to_string(spec[1]) + "_" +
+                               std::to_string(n_spec == 4 ? spec[3] : 0);
+      p->split_fn = find_function(ctx, ssym);
+      p->split_threads = 512;
+    }
+  }
   int max_threads = 0;
   if (hipFuncGetAttribute(&max_threads, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, p->fn) ==
           hipSuccess &&
@@ -625,6 +709,8 @@ int skyla_hip_record_dispatch(skyla_hip_recorder *r, const skyla_hip_pipeline *p
   c.threads = p->threads;
   c.segmented = p->segmented;
   c.retile = p->retile;
+  c.split_fn = p->split_fn;
+  c.split_threads = p->split_threads;
   for (int i = 0; i < 3; i++) c.groups[i] = groups[i];
   c.bufs = p->sets[set];
   c.push.assign(push, push + n_push);
@@ -675,6 +761,8 @@ int skyla_hip_record_end(skyla_hip_recorder *r, skyla_hip_recording **out) {
     if (c.kind == Command::Mark) rec->labels.push_back(c.label);
   rec->launches = build_launches(rec->cmds);
   rec->mark_ns.assign(rec->labels.size(), 0.0);
+  HIP_TRY(hipSetDevice(rec->ctx->device));
+  if (int s = bind_workspace(rec->launches, &rec->workspace)) return s;
   if (!rec->profile && skyla_hip_recording_len(rec.get()) > 0) {
     // One graph for the whole recording, captured from the launch list on the stream.
     skyla_hip_context *ctx = rec->ctx;
@@ -711,6 +799,7 @@ void skyla_hip_recording_free(skyla_hip_recording *rec) {
   hipStreamSynchronize(rec->ctx->stream);
   if (rec->exec) hipGraphExecDestroy(rec->exec);
   if (rec->graph) hipGraphDestroy(rec->graph);
+  if (rec->workspace) hipFree(rec->workspace);
   delete rec;
 }
 
@@ -837,11 +926,23 @@ int skyla_hip_time_dispatch(skyla_hip_context *ctx, const skyla_hip_pipeline *p,
   c.fn = p->fn;
   c.threads = p->threads;
   c.segmented = p->segmented;
+  c.retile = p->retile;
+  c.split_fn = p->split_fn;
+  c.split_threads = p->split_threads;
   for (int i = 0; i < 3; i++) c.groups[i] = groups[i];
   c.bufs = p->sets[0];
   c.push.assign(push, push + n_push);
   const Command *one[1] = {&c};
-  const Launch l = pack(one, 1);
+  std::vector<Launch> ls{pack(one, 1)};
+  void *workspace = nullptr;
+  if (int s = bind_workspace(ls, &workspace)) return s;
+  struct FreeWs {
+    void *p;
+    ~FreeWs() {
+      if (p) hipFree(p);
+    }
+  } free_ws{workspace};
+  const Launch &l = ls[0];
   Events e;
   int s = e.make(reps + 1);
   if (s) return s;
