@@ -479,19 +479,19 @@ SK_DEV void stage_scales(const WStage<TYPE> &s, uint32_t hh, StageScales<TYPE> &
 // reads whole token rows with 16 consecutive bytes per lane.  f16 inputs: item = 8 values
 // (16 B), token J / (KX/8).  Either way the LDS row holds pairs (0,2),(1,3) of every four
 // values, the order of the packed-quant extraction.
-template <int KX, int XHALF, int NT>
+template <int KX, int XHALF, int NT, int TN = TN2>
 struct XChunk {
   static constexpr int PER = XHALF ? 8 : 4;              // values per item
-  static constexpr int IPT = TN2 * KX / PER / NT;        // items per thread
+  static constexpr int IPT = TN * KX / PER / NT;         // items per thread
   static constexpr int IPR = KX / PER;                   // items per token row
   float4 v[XHALF ? 1 : IPT];
   uint4 h[XHALF ? IPT : 1];
 };
 
-template <int KX, int XHALF, int NT>
-SK_DEV void load_chunk(XChunk<KX, XHALF, NT> &c, const void *xv, const uint32_t *xrow, uint32_t x_off,
+template <int KX, int XHALF, int NT, int TN>
+SK_DEV void load_chunk(XChunk<KX, XHALF, NT, TN> &c, const void *xv, const uint32_t *xrow, uint32_t x_off,
                        uint32_t x_stride, uint32_t k0, uint32_t n_in) {
-  using C = XChunk<KX, XHALF, NT>;
+  using C = XChunk<KX, XHALF, NT, TN>;
   constexpr int IPT = C::IPT, IPR = C::IPR, PER = C::PER;
 #pragma unroll
   for (int i = 0; i < IPT; i++) {
@@ -510,9 +510,9 @@ SK_DEV void load_chunk(XChunk<KX, XHALF, NT> &c, const void *xv, const uint32_t 
 
 // Stores a chunk to LDS, pair-permuted as the weight fragments; returns whether this
 // wave rescaled any token.
-template <int KX, int XHALF, int NT>
-SK_DEV bool store_chunk(f16 *lds, XChunk<KX, XHALF, NT> &c, int *exps, uint32_t k0, uint32_t n_in) {
-  using C = XChunk<KX, XHALF, NT>;
+template <int KX, int XHALF, int NT, int TN>
+SK_DEV bool store_chunk(f16 *lds, XChunk<KX, XHALF, NT, TN> &c, int *exps, uint32_t k0, uint32_t n_in) {
+  using C = XChunk<KX, XHALF, NT, TN>;
   constexpr int IPT = C::IPT, IPR = C::IPR, PER = C::PER;
   constexpr int PITCH2 = pitch2<KX>();
   if (k0 + KX > n_in) {  // partial chunk (Q8_0 tail): zero the values past n_in
@@ -579,14 +579,15 @@ struct WLds<1, NT> {  // Q4_K row: qs 128 | header 16
   static constexpr uint32_t PW = 152;
   static constexpr int QI = TM * 8 / NT;  // qs units per thread
   uint4 q[QI], hd;
-  SK_DEV void load(WLds &r, const uint4 *w, const MatmulPush &p, uint32_t row0, uint32_t sb, uint32_t tid) {
+  SK_DEV void load(WLds &r, const uint4 *w, const MatmulPush &p, uint32_t row0, uint32_t sb, uint32_t tid,
+                   uint32_t base = 0) {
     const uint32_t units = p.n_in >> 5, supers = p.n_in >> 8;
 #pragma unroll
     for (int i = 0; i < QI; i++) {
       const uint32_t u = tid + NT * i, lr = u >> 3;
-      r.q[i] = w[p.o0 + min(row0 + lr, p.n_out - 1) * units + sb * 8 + (u & 7)];
+      r.q[i] = w[p.o0 + (base + min(row0 + lr, p.n_out - 1)) * units + sb * 8 + (u & 7)];
     }
-    if (tid < TM) r.hd = w[p.o1 + min(row0 + tid, p.n_out - 1) * supers + sb];
+    if (tid < TM) r.hd = w[p.o1 + (base + min(row0 + tid, p.n_out - 1)) * supers + sb];
   }
   SK_DEV void store(const WLds &r, uint32_t *lds, uint32_t tid) {
 #pragma unroll
@@ -610,20 +611,20 @@ struct WLds<2, NT> {  // Q6_K row: ql 128 | qh 64 | scales 16 | d 2
   uint4 ql[LI], qh[HI], sc;
   uint32_t d;
   SK_DEV void load(WLds &r, const uint4 *w, const uint16_t *wd, const MatmulPush &p, uint32_t row0,
-                   uint32_t sb, uint32_t tid) {
+                   uint32_t sb, uint32_t tid, uint32_t base = 0) {
     const uint32_t supers = p.n_in >> 8;
 #pragma unroll
     for (int i = 0; i < LI; i++) {
       const uint32_t u = tid + NT * i, lr = u >> 3;
-      r.ql[i] = w[p.o0 + (min(row0 + lr, p.n_out - 1) * supers + sb) * 8 + (u & 7)];
+      r.ql[i] = w[p.o0 + ((base + min(row0 + lr, p.n_out - 1)) * supers + sb) * 8 + (u & 7)];
     }
 #pragma unroll
     for (int i = 0; i < HI; i++) {
       const uint32_t u = tid + NT * i, lr = u >> 2;
-      r.qh[i] = w[p.o1 + (min(row0 + lr, p.n_out - 1) * supers + sb) * 4 + (u & 3)];
+      r.qh[i] = w[p.o1 + ((base + min(row0 + lr, p.n_out - 1)) * supers + sb) * 4 + (u & 3)];
     }
     const uint32_t lr = tid & (TM - 1);
-    const uint32_t rs = min(row0 + lr, p.n_out - 1) * supers + sb;
+    const uint32_t rs = (base + min(row0 + lr, p.n_out - 1)) * supers + sb;
     if (tid < TM) r.sc = w[p.o2 + rs];
     else if (tid < 2 * TM) r.d = wd[p.o3 + rs];
   }
@@ -714,18 +715,20 @@ SK_DEV void lds_scales(const uint32_t *row, uint32_t hh, StageScales<TYPE> &o) {
 // coherent (sc1) stores, drains them, and counts itself in cnt[tile]; the last of the S
 // sums the partials in split order (deterministic) and writes y, then resets the count
 // for the next launch.  No workgroup ever waits for another.
-template <int TYPE, int ACCUM, int XHALF, int NW>
+template <int TYPE, int ACCUM, int XHALF, int NW, int TN = TN2, int MOE = 0>
 SK_DEV void matmul_tile128_w(const uint4 *__restrict__ w, const uint16_t *__restrict__ wd, const void *x,
                              float *y, const uint32_t *ctl, const MatmulPush &p, float *ws = nullptr,
                              uint32_t *cnt = nullptr, uint32_t S = 1) {
+  static_assert(NW == 4 || TN == TN2, "eight waves split a 128-token tile");
   constexpr int NT = 64 * NW;
-  constexpr int NB = NW == 8 ? 2 : 4;  // 32-token blocks per wave
-  constexpr int KX = NW == 8 ? KX_W : 128, PITCH2 = pitch2<KX>();
+  constexpr int NB = NW == 8 ? 2 : TN / 32;  // 32-token blocks per wave
+  constexpr int KX = (NW == 8 || TN < TN2) ? KX_W : 128, PITCH2 = pitch2<KX>();
   constexpr uint32_t PW = WLds<TYPE, NT>::PW;
-  __shared__ __attribute__((aligned(16))) f16 xs[TN2 * PITCH2];
+  __shared__ __attribute__((aligned(16))) f16 xs[TN * PITCH2];
   __shared__ __attribute__((aligned(16))) uint32_t wl[TM * PW / 4];
-  __shared__ uint32_t xrow[TN2];
-  __shared__ int xexp[TN2];
+  __shared__ uint32_t xrow[TN];
+  __shared__ uint32_t yrow[TN];
+  __shared__ int xexp[TN];
   __shared__ uint32_t xflag[NW];
   __shared__ uint32_t last;
 
@@ -736,15 +739,26 @@ SK_DEV void matmul_tile128_w(const uint4 *__restrict__ w, const uint16_t *__rest
   // Tile order: workgroups are dealt to the 8 XCDs round-robin by linear id, and
   // consecutive ids take consecutive token tiles (then splits), so the workgroups of one
   // XCD share a token tile's activations in that XCD's L2.
+  // Expert groups (MOE): grid.y = expert e, whose group of (count, start) = table[e] tokens
+  // is listed in list[]; tile z takes group tokens [z TN, z TN + TN), token i being slot
+  // s = list[start + i] that reads x row s / x_div and writes y row s (matmul.comp:124-150).
   const uint32_t gx = gridDim.x, gz = gridDim.z, Z = gz / S;
   const uint32_t lin = blockIdx.x + gx * blockIdx.z;
-  const uint32_t rt = lin / gz, rem = lin % gz, tt = rem % Z, sp = rem / Z;
+  const uint32_t rt = MOE ? blockIdx.x : lin / gz, rem = lin % gz;
+  const uint32_t tt = MOE ? blockIdx.z : rem % Z, sp = MOE ? 0 : rem / Z;
+  const uint32_t e = MOE ? blockIdx.y : 0;
+  const uint32_t base = MOE ? e * p.n_out : 0;
   const uint32_t row0 = rt * TM;
-  const uint32_t n_all = ctl[2];
-  const uint32_t col0 = tt * TN2;
+  const uint32_t n_all = MOE ? ctl[p.table_off + 2 * e] : ctl[2];
+  const uint32_t col0 = tt * TN;
   if (col0 >= n_all) return;
-  const uint32_t n_tok = min(n_all - col0, (uint32_t)TN2);
-  if (tid < TN2) xrow[tid] = col0 + min(tid, n_tok - 1);
+  const uint32_t n_tok = min(n_all - col0, (uint32_t)TN);
+  if (tid < TN) {
+    const uint32_t i = min(tid, n_tok - 1);
+    const uint32_t slot = MOE ? ctl[p.list_off + ctl[p.table_off + 2 * e + 1] + col0 + i] : col0 + i;
+    xrow[tid] = MOE ? slot / p.x_div : slot;
+    yrow[tid] = slot;
+  }
   const uint32_t lrow = rb * 32 + (lane & 31);
   const uint32_t my_row = row0 + lrow;
   const uint32_t *wrow = wl + lrow * PW / 4;
@@ -761,14 +775,14 @@ SK_DEV void matmul_tile128_w(const uint4 *__restrict__ w, const uint16_t *__rest
   const uint32_t n_chunk = n_stage * (KC / KX);
   const uint32_t kbase = st0 * KC;
   WLds<TYPE, NT> wr;
-  if constexpr (TYPE == 1) wr.load(wr, w, p, row0, st0, tid);
-  else wr.load(wr, w, wd, p, row0, st0, tid);
+  if constexpr (TYPE == 1) wr.load(wr, w, p, row0, st0, tid, base);
+  else wr.load(wr, w, wd, p, row0, st0, tid, base);
   __syncthreads();  // xrow
   {
-    XChunk<KX, XHALF, NT> c0;
-    load_chunk<KX, XHALF, NT>(c0, x, xrow, p.x_off, p.x_stride, kbase, p.n_in);
+    XChunk<KX, XHALF, NT, TN> c0;
+    load_chunk<KX, XHALF, NT, TN>(c0, x, xrow, p.x_off, p.x_stride, kbase, p.n_in);
     wr.store(wr, wl, tid);
-    const bool r = store_chunk<KX, XHALF, NT>(xs, c0, xexp, kbase, p.n_in);
+    const bool r = store_chunk<KX, XHALF, NT, TN>(xs, c0, xexp, kbase, p.n_in);
     if (lane == 0) xflag[wave] = r;
   }
   __syncthreads();
@@ -779,14 +793,14 @@ SK_DEV void matmul_tile128_w(const uint4 *__restrict__ w, const uint16_t *__rest
     lds_scales<TYPE>(wrow, hh, ss);
     const bool more = st + 1 < n_stage;
     if (more) {
-      if constexpr (TYPE == 1) wr.load(wr, w, p, row0, st0 + st + 1, tid);
-      else wr.load(wr, w, wd, p, row0, st0 + st + 1, tid);
+      if constexpr (TYPE == 1) wr.load(wr, w, p, row0, st0 + st + 1, tid, base);
+      else wr.load(wr, w, wd, p, row0, st0 + st + 1, tid, base);
     }
 #pragma unroll
     for (int c4 = 0; c4 < KC / KX; c4++) {
-      XChunk<KX, XHALF, NT> xn;
+      XChunk<KX, XHALF, NT, TN> xn;
       const bool next = chunk + 1 < n_chunk;
-      if (next) load_chunk<KX, XHALF, NT>(xn, x, xrow, p.x_off, p.x_stride, kbase + (chunk + 1) * KX, p.n_in);
+      if (next) load_chunk<KX, XHALF, NT, TN>(xn, x, xrow, p.x_off, p.x_stride, kbase + (chunk + 1) * KX, p.n_in);
       bool rescaled = false;
 #pragma unroll
       for (int q = 0; q < NW; q++) rescaled |= xflag[q] != 0;
@@ -832,7 +846,7 @@ SK_DEV void matmul_tile128_w(const uint4 *__restrict__ w, const uint16_t *__rest
       __syncthreads();  // every wave is done with this chunk (and, at the stage end, the weights)
       if (next) {
         if (c4 == KC / KX - 1 && more) wr.store(wr, wl, tid);
-        const bool r = store_chunk<KX, XHALF, NT>(xs, xn, xexp, kbase + (chunk + 1) * KX, p.n_in);
+        const bool r = store_chunk<KX, XHALF, NT, TN>(xs, xn, xexp, kbase + (chunk + 1) * KX, p.n_in);
         if (lane == 0) xflag[wave] = r;
         __syncthreads();
       }
@@ -878,7 +892,7 @@ SK_DEV void matmul_tile128_w(const uint4 *__restrict__ w, const uint16_t *__rest
       for (int i = 0; i < 16; i++) {
         const uint32_t tok = 32 * (tb + j) + 8 * (i >> 2) + 4 * hh + (i & 3);
         if (tok < n_tok) {
-          float *o = y + p.y_off + (size_t)(col0 + tok) * p.y_stride + my_row;
+          float *o = y + p.y_off + (size_t)yrow[tok] * p.y_stride + my_row;
           *o = ACCUM ? *o + acc[j][i] : acc[j][i];
         }
       }
@@ -1031,12 +1045,15 @@ SK_DEV void matmul_tile128(const uint4 *__restrict__ w, const uint16_t *__restri
 
 }  // namespace
 
-// Dense (MOE = 0) launches use the 128 x 128 tile; expert groups (MOE = 1) the 128 x 32 one.
+// Dense (MOE = 0) launches use the 128 x 128 tile; expert groups (MOE = 1) 128 x 32 tiles
+// (K-quants: LDS-staged weights, four waves of 32 rows; Q8_0: register weights).
 #define MM_BODY(T, A, M, H)                                                     \
   if constexpr (M == 0 && T != 0)                                               \
     matmul_tile128_w<T, A, H, 8>(w, wd, x, y, ctl, p);                          \
   else if constexpr (M == 0)                                                    \
     matmul_tile128<T, A, H>(w, wd, x, y, ctl, p);                               \
+  else if constexpr (T != 0)                                                    \
+    matmul_tile128_w<T, A, H, 4, 32, 1>(w, wd, x, y, ctl, p);                   \
   else                                                                          \
     matmul_body<T, A, M, H>(w, wd, x, y, ctl, p);
 
