@@ -332,35 +332,30 @@ SK_DEV void matvec_q6k_body(const uint4 *__restrict__ w, const uint16_t *__restr
         h[r] = w[p.o1 + rs * 4 + hf * 2 + li];
       }
     };
-    auto x_unit = [&](uint32_t i, float4 (&v)[16]) {
-      const uint32_t u = u0 + i;
-      const float *xp = xv + (u >> 2) * 256 + ((u >> 1) & 1) * 128 + (u & 1) * 16;
+    // activation item t = group t%4 of unit t/4: 16 values (4 x 16 B) that become 8 f16
+    // pairs and one 16-value sum (16 VGPRs in flight per item, not a whole unit's 64)
+    const uint32_t n_xi = 4 * nu;
+    auto x_item = [&](uint32_t t, float4 (&v)[4]) {
+      const uint32_t u = u0 + (t >> 2), g = t & 3;
+      const float *xp = xv + (u >> 2) * 256 + ((u >> 1) & 1) * 128 + (u & 1) * 16 + 32 * g;
 #pragma unroll
-      for (int g = 0; g < 4; g++)
-#pragma unroll
-        for (int k = 0; k < 4; k++) v[4 * g + k] = *(const float4 *)(xp + 32 * g + 4 * k);
+      for (int k = 0; k < 4; k++) v[k] = *(const float4 *)(xp + 4 * k);
     };
-    auto x_store = [&](uint32_t i, const float4 (&v)[16]) {
+    auto x_store = [&](uint32_t t, const float4 (&v)[4]) {
+      const uint32_t i = t >> 2, g = t & 3;
       const f16x2 one = {(f16)1.0f, (f16)1.0f};
-      float4 sums;
-      float *sp = (float *)&sums;
+      uint32_t pp[8];
+      float s = 0.0f;
 #pragma unroll
-      for (int g = 0; g < 4; g++) {
-        uint32_t pp[8];
-        float s = 0.0f;
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-          const float4 e = v[4 * g + k];
-          pp[2 * k] = pk(e.x, e.z);
-          pp[2 * k + 1] = pk(e.y, e.w);
-          s = dot2(as_f16x2(pp[2 * k]), one, s);
-          s = dot2(as_f16x2(pp[2 * k + 1]), one, s);
-        }
-        xq[2 * g][i] = make_uint4(pp[0], pp[1], pp[2], pp[3]);
-        xq[2 * g + 1][i] = make_uint4(pp[4], pp[5], pp[6], pp[7]);
-        sp[g] = s;
+      for (int k = 0; k < 4; k++) {
+        pp[2 * k] = pk(v[k].x, v[k].z);
+        pp[2 * k + 1] = pk(v[k].y, v[k].w);
+        s = dot2(as_f16x2(pp[2 * k]), one, s);
+        s = dot2(as_f16x2(pp[2 * k + 1]), one, s);
       }
-      xs[i] = sums;
+      xq[2 * g][i] = make_uint4(pp[0], pp[1], pp[2], pp[3]);
+      xq[2 * g + 1][i] = make_uint4(pp[4], pp[5], pp[6], pp[7]);
+      ((float *)&xs[i])[g] = s;
     };
     const uint32_t n_items = (uint32_t)G::RWG * ns;
     auto h_load = [&](uint32_t i, uint4 &sv, uint32_t &dv) {
@@ -386,18 +381,18 @@ SK_DEV void matvec_q6k_body(const uint4 *__restrict__ w, const uint16_t *__restr
       }
     };
     if (k0 != 0) __syncthreads();
-    float4 xv16[16];
+    float4 xv4[4];
     uint4 sv0 = make_uint4(0, 0, 0, 0);
     uint32_t dv0 = 0;
-    if (tid < nu) x_unit(tid, xv16);
+    if (tid < n_xi) x_item(tid, xv4);
     if (tid < n_items) h_load(tid, sv0, dv0);
 #pragma unroll
     for (int j = 0; j < PF; j++) load(min(lane + j * LPR, nu - 1), qa[j], qb[j], qh[j]);
-    if (tid < nu) x_store(tid, xv16);
+    if (tid < n_xi) x_store(tid, xv4);
     if (tid < n_items) h_store(tid, sv0, dv0);
-    for (uint32_t i = tid + G::NT; i < nu; i += G::NT) {
-      x_unit(i, xv16);
-      x_store(i, xv16);
+    for (uint32_t t = tid + G::NT; t < n_xi; t += G::NT) {
+      x_item(t, xv4);
+      x_store(t, xv4);
     }
     for (uint32_t i = tid + G::NT; i < n_items; i += G::NT) {
       h_load(i, sv0, dv0);
@@ -410,47 +405,42 @@ SK_DEV void matvec_q6k_body(const uint4 *__restrict__ w, const uint16_t *__restr
       for (int j = 0; j < PF; j++) {
         const uint32_t i = lane + (j0 + j) * LPR;
         if (i < nu) {
-          uint32_t px[32];
-#pragma unroll
-          for (int jj = 0; jj < 8; jj++) {
-            const uint4 v = xq[jj][i];
-            px[4 * jj] = v.x;
-            px[4 * jj + 1] = v.y;
-            px[4 * jj + 2] = v.z;
-            px[4 * jj + 3] = v.w;
-          }
           const float4 xsum = xs[i];
-          const float i0 = -1056.0f * xsum.x, i1 = -1056.0f * xsum.y;
-          const float i2 = -1536.0f * xsum.z, i3 = -1536.0f * xsum.w;
+          const float ib[4] = {-1056.0f * xsum.x, -1056.0f * xsum.y, -1536.0f * xsum.z, -1536.0f * xsum.w};
           const uint32_t s = i >> 2;
 #pragma unroll
           for (int r = 0; r < ROWS; r++) {
-            float t0 = i0, t1 = i1, t2 = i2, t3 = i3;
-            const uint32_t av[4] = {qa[j][r].x, qa[j][r].y, qa[j][r].z, qa[j][r].w};
-            const uint32_t bv[4] = {qb[j][r].x, qb[j][r].y, qb[j][r].z, qb[j][r].w};
-            const uint32_t hv[4] = {qh[j][r].x, qh[j][r].y, qh[j][r].z, qh[j][r].w};
+            float t[4];
+            // group g: quants from ql half a (g even) or b (g odd), low nibbles for g < 2 and
+            // high for g >= 2; qh bits 2g, 2g+1 land on bits 4-5 (g < 2) or 8-9 of each lane.
+            // One group's operands are live at a time (157 -> 108 VGPRs).
 #pragma unroll
-            for (int k = 0; k < 4; k++) {
-              const uint32_t a0 = av[k], b0 = bv[k], h0 = hv[k];
-              const uint32_t a8 = a0 >> 8, b8 = b0 >> 8, h8 = h0 >> 8;
-              const uint32_t h4 = h0 << 4, h2 = h0 << 2, h84 = h8 << 4, h82 = h8 << 2;
-              t0 = dot2(as_f16x2(and_or(h4, LH, and_or(a0, L4, MW))), as_f16x2(px[0 * 8 + 2 * k]), t0);
-              t0 = dot2(as_f16x2(and_or(h84, LH, and_or(a8, L4, MW))), as_f16x2(px[0 * 8 + 2 * k + 1]), t0);
-              t1 = dot2(as_f16x2(and_or(h2, LH, and_or(b0, L4, MW))), as_f16x2(px[1 * 8 + 2 * k]), t1);
-              t1 = dot2(as_f16x2(and_or(h82, LH, and_or(b8, L4, MW))), as_f16x2(px[1 * 8 + 2 * k + 1]), t1);
-              t2 = dot2(as_f16x2(and_or(h4, HH, and_or(a0, H4, MW))), as_f16x2(px[2 * 8 + 2 * k]), t2);
-              t2 = dot2(as_f16x2(and_or(h84, HH, and_or(a8, H4, MW))), as_f16x2(px[2 * 8 + 2 * k + 1]), t2);
-              t3 = dot2(as_f16x2(and_or(h2, HH, and_or(b0, H4, MW))), as_f16x2(px[3 * 8 + 2 * k]), t3);
-              t3 = dot2(as_f16x2(and_or(h82, HH, and_or(b8, H4, MW))), as_f16x2(px[3 * 8 + 2 * k + 1]), t3);
+            for (int g = 0; g < 4; g++) {
+              const uint4 x0 = xq[2 * g][i], x1 = xq[2 * g + 1][i];
+              const uint32_t px[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+              const uint4 qv = (g & 1) ? qb[j][r] : qa[j][r];
+              const uint32_t wv[4] = {qv.x, qv.y, qv.z, qv.w};
+              const uint32_t hv[4] = {qh[j][r].x, qh[j][r].y, qh[j][r].z, qh[j][r].w};
+              const uint32_t QM = g < 2 ? L4 : H4, HM = g < 2 ? LH : HH, SH = (g & 1) ? 2 : 4;
+              float tg = ib[g];
+#pragma unroll
+              for (int k = 0; k < 4; k++) {
+                const uint32_t w0 = wv[k], w8 = w0 >> 8, h0 = hv[k] << SH, h8 = (hv[k] >> 8) << SH;
+                tg = dot2(as_f16x2(and_or(h0, HM, and_or(w0, QM, MW))), as_f16x2(px[2 * k]), tg);
+                tg = dot2(as_f16x2(and_or(h8, HM, and_or(w8, QM, MW))), as_f16x2(px[2 * k + 1]), tg);
+              }
+              t[g] = tg;
+              __builtin_amdgcn_sched_barrier(0);
             }
             const float4 f = sc[lrow0 + r][s][hf * 2 + li];
-            acc[r] = __builtin_fmaf(f.x, t0, acc[r]);
-            acc[r] = __builtin_fmaf(f.y, t1, acc[r]);
-            acc[r] = __builtin_fmaf(f.z, t2, acc[r]);
-            acc[r] = __builtin_fmaf(f.w, t3, acc[r]);
+            acc[r] = __builtin_fmaf(f.x, t[0], acc[r]);
+            acc[r] = __builtin_fmaf(f.y, t[1], acc[r]);
+            acc[r] = __builtin_fmaf(f.z, t[2], acc[r]);
+            acc[r] = __builtin_fmaf(f.w, t[3], acc[r]);
           }
         }
         load(min(i + PF * LPR, nu - 1), qa[j], qb[j], qh[j]);  // unconditional, as in Q4_K
+        __builtin_amdgcn_sched_barrier(0);  // each refill right behind the step it replaces
       }
     }
   }
@@ -637,5 +627,7 @@ MV_Q4K(8, 0, 1, 0, 16)
 MV_Q4K(8, 1, 1, 0, 16)
 MV_Q6K(4, 0, 1, 0, 32)
 MV_Q6K(4, 1, 1, 0, 32)
+MV_Q6K(8, 0, 1, 0, 32)
+MV_Q6K(8, 1, 1, 0, 32)
 MV_Q6K(4, 0, 1, 0, 16)
 MV_Q6K(4, 1, 1, 0, 16)

@@ -355,6 +355,16 @@ struct skyla_hip_recording {
   std::vector<std::string> labels;
   std::vector<double> mark_ns;
   bool replayed = false;
+  // device resources go with the recording, also when record_end fails half-way
+  ~skyla_hip_recording() {
+    if (ctx) {
+      hipSetDevice(ctx->device);
+      hipStreamSynchronize(ctx->stream);
+    }
+    if (exec) hipGraphExecDestroy(exec);
+    if (graph) hipGraphDestroy(graph);
+    if (workspace) hipFree(workspace);
+  }
 };
 
 namespace {
@@ -369,9 +379,10 @@ hipFunction_t find_function(skyla_hip_context *ctx, const std::string &sym) {
 }
 
 // Variant choice for matvec launches, from sweeps on MI355X.  Dense rows (Qwen3-8B decode
-// shapes, n_in 4096 and 12288): eight-wave workgroups; large launches gain from fewer lanes
-// per row (more pipelined load steps per lane, fewer workgroups staging the activations),
-// small ones from more workgroups.  Expert rows (MOE = 1, grid.y = slots; config-4 gate/up
+// shapes, n_in 4096 and 12288): eight-wave workgroups (four for Q6_K launches of 12288 rows
+// or more); large launches gain from fewer lanes per row (more pipelined load steps per
+// lane, fewer workgroups staging the activations), small ones from more workgroups.
+// Q6_K 12288 -> 4096 (the down projection): 11.4 us on (8, 1, 32), 11.7 us on (4, 1, 32).  Expert rows (MOE = 1, grid.y = slots; config-4 gate/up
 // n_in 2048 and down n_in 768 over 8 slots): 16 lanes per row, one row each, four waves.
 // Each entry is (min_rows, waves, rows, lanes per row); grid.x follows from n_out.
 struct VariantRule {
@@ -383,7 +394,7 @@ struct VariantRule {
 };
 const VariantRule kVariantRules[] = {
     {"matvec_q4k", 0, 5, {{6144, 8, 1, 16}, {0, 8, 1, 64}}, 2},
-    {"matvec_q6k", 0, 7, {{12288, 4, 1, 16}, {0, 4, 1, 32}}, 2},
+    {"matvec_q6k", 0, 7, {{12288, 4, 1, 16}, {0, 8, 1, 32}}, 2},
     {"matvec_q4k", 1, 5, {{0, 4, 1, 16}}, 1},
 };
 
@@ -793,15 +804,7 @@ int skyla_hip_record_end(skyla_hip_recorder *r, skyla_hip_recording **out) {
   return SKYLA_HIP_OK;
 }
 
-void skyla_hip_recording_free(skyla_hip_recording *rec) {
-  if (!rec) return;
-  hipSetDevice(rec->ctx->device);
-  hipStreamSynchronize(rec->ctx->stream);
-  if (rec->exec) hipGraphExecDestroy(rec->exec);
-  if (rec->graph) hipGraphDestroy(rec->graph);
-  if (rec->workspace) hipFree(rec->workspace);
-  delete rec;
-}
+void skyla_hip_recording_free(skyla_hip_recording *rec) { delete rec; }
 
 uint32_t skyla_hip_recording_len(const skyla_hip_recording *rec) {
   if (!rec) return 0;

@@ -2,6 +2,9 @@
 self-contained arenas."""
 from __future__ import annotations
 
+import contextlib
+import os
+
 import numpy as np
 
 from skyla_hip import engine as E
@@ -16,6 +19,21 @@ def rel_l2(got: np.ndarray, want: np.ndarray) -> float:
 
 def pad64(n: int) -> int:
     return -(-n // 64) * 64
+
+
+@contextlib.contextmanager
+def env(**kw):
+    """Runtime switches (SKYLA_HIP_*) read when a pipeline is created or a recording ends."""
+    old = {k: os.environ.get(k) for k in kw}
+    os.environ.update({k: str(v) for k, v in kw.items()})
+    try:
+        yield
+    finally:
+        for k, v in old.items():
+            if v is None:
+                del os.environ[k]
+            else:
+                os.environ[k] = v
 
 
 class Setup:
