@@ -54,6 +54,64 @@ extern "C" __global__ __launch_bounds__(256) void moe_logits(const float *w, con
   if (tid == 0) logits[p.logits_off + tok * gridDim.x + e] = part[0] + part[1] + part[2] + part[3];
 }
 
+// moe_logits_t: the runtime's form of moe_logits for a batch (same logits, another grid and
+// summation order).  Workgroup (g, h) computes the LG x LG block of experts LG g + [0, LG)
+// and tokens LG h + [0, LG): each lane accumulates all LG x LG dot products over its own
+// float4 columns (the four waves take interleaved column ranges), the 64 sums are spread
+// one per lane by a halving exchange across the wave, and the four waves' sums are added
+// in wave order.  Per workgroup that reads 2 LG rows once instead of one expert row and
+// one token row per (expert, token): ~32 MB of L2 traffic at 128 x 128 x 2048 instead of
+// ~256 MB, which bounded the one-workgroup-per-logit form.
+constexpr uint32_t LG = 8;
+extern "C" __global__ __launch_bounds__(256) void moe_logits_t(const float *w, const float *a,
+                                                                float *logits, LogitsPush p,
+                                                                uint32_t n_expert, uint32_t n_tok) {
+  __shared__ float part[4][64];
+  const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint32_t e0 = blockIdx.x * LG, t0 = blockIdx.y * LG;
+  const uint32_t n4 = p.n_embd / 4;
+  const float4 *xr[LG], *rr[LG];
+#pragma unroll
+  for (uint32_t i = 0; i < LG; i++) {
+    xr[i] = (const float4 *)(a + p.x_off + min(t0 + i, n_tok - 1) * p.x_stride);
+    rr[i] = (const float4 *)(w + p.router_off + min(e0 + i, n_expert - 1) * p.n_embd);
+  }
+  float v[LG * LG];  // v[LG ti + ei]
+#pragma unroll
+  for (uint32_t j = 0; j < LG * LG; j++) v[j] = 0.0f;
+  for (uint32_t c = wave * 64 + lane; c < n4; c += 256) {
+    float4 xv[LG], rv[LG];
+#pragma unroll
+    for (uint32_t i = 0; i < LG; i++) {
+      xv[i] = xr[i][c];
+      rv[i] = rr[i][c];
+    }
+#pragma unroll
+    for (uint32_t ti = 0; ti < LG; ti++)
+#pragma unroll
+      for (uint32_t ei = 0; ei < LG; ei++)
+        v[LG * ti + ei] += xv[ti].x * rv[ei].x + xv[ti].y * rv[ei].y + xv[ti].z * rv[ei].z + xv[ti].w * rv[ei].w;
+  }
+  // halving exchange: after the step of distance d, lane l holds the sums of the outputs
+  // whose index has l's bits >= d; lane l ends with output l
+#pragma unroll
+  for (uint32_t d = 32, n = 64; d >= 1; d >>= 1, n >>= 1) {
+    const bool upper = (lane & d) != 0;
+#pragma unroll
+    for (uint32_t j = 0; j < n / 2; j++) {
+      const float keep = upper ? v[j + n / 2] : v[j], send = upper ? v[j] : v[j + n / 2];
+      v[j] = keep + __shfl_xor(send, (int)d, 64);
+    }
+  }
+  part[wave][lane] = v[0];
+  __syncthreads();
+  if (threadIdx.x < 64) {
+    const uint32_t tok = t0 + lane / LG, e = e0 + lane % LG;
+    const float sum = ((part[0][lane] + part[1][lane]) + part[2][lane]) + part[3][lane];
+    if (tok < n_tok && e < n_expert) logits[p.logits_off + tok * n_expert + e] = sum;
+  }
+}
+
 // moe_route (moe_route.comp:55-106): per token, n_used rounds of "largest logit, lowest
 // index on ties", then weights exp(v_k - v_0) / sum.  One wave per token: expert
 // e = lane + 64 j is held in key[j] (n_expert <= 256), a round is a lane maximum, a wave
@@ -117,19 +175,28 @@ extern "C" __global__ __launch_bounds__(64) void moe_route(float *a, uint32_t *i
 // moe_sort (moe_sort.comp:21-55): slot s = tok * n_used + k is routed to ids[s].  Writes
 // table[2e] = count, table[2e+1] = start (exclusive scan in expert order) and list[start +
 // rank] = s with rank = number of earlier slots of the same expert (stable).  One
-// workgroup; the ranking runs on wave 0, 64 slots at a time, using ballots to find the
-// lanes that share an expert.
+// workgroup; the ids are read once into LDS (the list writes go to the same arena, so
+// reads from it could not be hoisted past them), and the ranking runs on wave 0, 64 slots
+// at a time, using ballots to find the lanes that share an expert.
 extern "C" __global__ __launch_bounds__(256) void moe_sort(uint32_t *a, SortPush p) {
   __shared__ uint32_t count[256];
   __shared__ uint32_t next[256];
+  __shared__ uint32_t sid[MAX_SLOTS];
   const uint32_t t = threadIdx.x;
   const uint32_t n = min(a[2] * p.n_used, MAX_SLOTS);
   const uint32_t n_expert = min(p.n_expert, 256u);
   count[t] = 0;
+  uint32_t mine[MAX_SLOTS / 256];
+#pragma unroll
+  for (uint32_t j = 0; j < MAX_SLOTS / 256; j++) {
+    const uint32_t i = t + 256 * j;
+    mine[j] = i < n ? a[p.ids_off + i] : 0xffffffffu;
+  }
   __syncthreads();
-  for (uint32_t i = t; i < n; i += 256) {
-    const uint32_t e = a[p.ids_off + i];
-    if (e < n_expert) atomicAdd(&count[e], 1u);
+#pragma unroll
+  for (uint32_t j = 0; j < MAX_SLOTS / 256; j++) {
+    sid[t + 256 * j] = mine[j];
+    if (mine[j] < n_expert) atomicAdd(&count[mine[j]], 1u);
   }
   __syncthreads();
   if (t < 64) {
@@ -161,7 +228,7 @@ extern "C" __global__ __launch_bounds__(256) void moe_sort(uint32_t *a, SortPush
     for (uint32_t base = 0; base < n; base += 64) {
       const uint32_t i = base + t;
       const bool live = i < n;
-      const uint32_t e = live ? a[p.ids_off + i] : 0xffffffffu;
+      const uint32_t e = live ? sid[i] : 0xffffffffu;
       const bool ok = live && e < n_expert;
       // lanes with the same expert: intersect the ballots of all 8 expert bits
       uint64_t same = __ballot(ok);

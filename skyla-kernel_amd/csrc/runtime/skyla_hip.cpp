@@ -133,6 +133,8 @@ struct skyla_hip_pipeline {
   std::shared_ptr<const Retile> retile;  // matvec pipelines with a variant rule
   hipFunction_t split_fn = nullptr;      // dense K-quant matmul: the K-split variant
   uint32_t split_threads = 0;
+  hipFunction_t tok_fn = nullptr;        // batched form: a tok_per_wg x tok_per_wg block of
+  uint32_t tok_per_wg = 0;               // grid.x and grid.y per workgroup
   std::vector<std::vector<void *>> sets;
 };
 
@@ -146,6 +148,8 @@ struct Command {
   std::shared_ptr<const Retile> retile;
   hipFunction_t split_fn = nullptr;
   uint32_t split_threads = 0;
+  hipFunction_t tok_fn = nullptr;
+  uint32_t tok_per_wg = 0;
   uint32_t groups[3] = {0, 0, 0};
   std::vector<void *> bufs;
   std::vector<uint32_t> push;
@@ -168,6 +172,7 @@ struct Launch {
   uint32_t n_cnt = 0;     // per-tile counters
   void *ws = nullptr;
   void *cnt = nullptr;
+  std::vector<uint32_t> extra;  // trailing by-value u32 arguments (batched forms: the token count)
 };
 
 constexpr uint32_t kMaxSeg = 4;  // MAXSEG in kernels/common.h
@@ -198,6 +203,12 @@ Launch pack(const Command *const *run, uint32_t n) {
   if (!a.segmented) {
     for (int i = 0; i < 3; i++) l.groups[i] = a.groups[i];
     l.args = a.push;
+    if (a.tok_fn && a.groups[1] > 1) {  // grid (x, y) = (experts, tokens): blocks of both
+      l.fn = a.tok_fn;
+      l.groups[0] = (a.groups[0] + a.tok_per_wg - 1) / a.tok_per_wg;
+      l.groups[1] = (a.groups[1] + a.tok_per_wg - 1) / a.tok_per_wg;
+      l.extra = {a.groups[0], a.groups[1]};
+    }
     const uint32_t S = split_of(a);
     if (S > 1) {
       l.fn = a.split_fn;
@@ -296,6 +307,7 @@ int launch(hipStream_t stream, const Launch &l) {
     params.push_back(const_cast<void **>(&l.cnt));
     params.push_back(const_cast<uint32_t *>(&l.split));
   }
+  for (const uint32_t &v : l.extra) params.push_back(const_cast<uint32_t *>(&v));
   HIP_TRY(hipModuleLaunchKernel(l.fn, l.groups[0], l.groups[1], l.groups[2], l.threads, 1, 1, 0,
                                 stream, params.data(), nullptr));
   return SKYLA_HIP_OK;
@@ -631,6 +643,11 @@ int skyla_hip_pipeline_new(skyla_hip_context *ctx, const char *name, uint32_t n_
   if (!p->fn)
     return fail(SKYLA_HIP_E_NO_KERNEL, "no gfx950 kernel %s for this spec", sym.c_str());
   p->retile = make_retile(ctx, name, spec, n_spec);
+  // router logits of a batch: 8 x 8 (expert, token) blocks per workgroup (moe.hip, moe_logits_t)
+  if (std::strcmp(name, "moe_logits") == 0) {
+    p->tok_fn = find_function(ctx, "moe_logits_t");
+    p->tok_per_wg = 8;
+  }
   // dense K-quant matmul (TYPE 1/2, MOE 0): its K-split variant, used for launches with few
   // tiles (split_of); SKYLA_HIP_SPLITK=0 keeps every launch on the engine's kernel
   if (std::strcmp(name, "matmul") == 0 && n_spec >= 3 && (spec[0] == 1 || spec[0] == 2) && spec[2] == 0) {
@@ -722,6 +739,8 @@ int skyla_hip_record_dispatch(skyla_hip_recorder *r, const skyla_hip_pipeline *p
   c.retile = p->retile;
   c.split_fn = p->split_fn;
   c.split_threads = p->split_threads;
+  c.tok_fn = p->tok_fn;
+  c.tok_per_wg = p->tok_per_wg;
   for (int i = 0; i < 3; i++) c.groups[i] = groups[i];
   c.bufs = p->sets[set];
   c.push.assign(push, push + n_push);
@@ -932,6 +951,8 @@ int skyla_hip_time_dispatch(skyla_hip_context *ctx, const skyla_hip_pipeline *p,
   c.retile = p->retile;
   c.split_fn = p->split_fn;
   c.split_threads = p->split_threads;
+  c.tok_fn = p->tok_fn;
+  c.tok_per_wg = p->tok_per_wg;
   for (int i = 0; i < 3; i++) c.groups[i] = groups[i];
   c.bufs = p->sets[0];
   c.push.assign(push, push + n_push);

@@ -92,6 +92,39 @@ def _dispatch(ctx, p, groups, push):
     rec.free()
 
 
+@pytest.mark.parametrize("n_embd,n_tok", [(2048, 1), (2048, 37), (2048, 128), (2560, 21)])
+def test_logits_kernel_batches(ctx, n_embd, n_tok):
+    """Router logits for a decode token and for ragged batches (the runtime runs batches
+    16 tokens per workgroup; 2560 values take the re-read path for rows past 2048): each
+    logit within f32 summation-order error of an f64 reference, and nothing written for
+    tokens past the batch."""
+    router = synth.router(CFG, f"router-{n_embd}", N_EXPERT, n_embd)
+    x = synth.activations(CFG, f"logits-x-{n_embd}-{n_tok}", (n_tok, n_embd))
+    p = E.Planner(ctx.max_buffer())
+    roff = p.table(router.reshape(-1))
+    weights = E.upload_weights(ctx, p)
+    x_off, lg_off = 64, 64 + n_tok * n_embd
+    size = (lg_off + (n_tok + 16) * N_EXPERT + 64) * 4
+    arena = ctx.alloc_host(size)
+    try:
+        f = arena.as_f32()
+        f[x_off: x_off + x.size] = x.reshape(-1)
+        f[lg_off: lg_off + (n_tok + 16) * N_EXPERT] = -7.0
+        arena.upload()
+        k = E.Kernels(ctx, weights, arena)
+        _dispatch(ctx, k.logits, [N_EXPERT, n_tok, 1], [x_off, roff, lg_off, n_embd, n_embd])
+        arena.download()
+        got = arena.as_f32()[lg_off: lg_off + (n_tok + 16) * N_EXPERT].reshape(n_tok + 16, N_EXPERT)
+        want = x.astype(np.float64) @ router.astype(np.float64).T
+        bound = 1e-5 * (np.abs(x).astype(np.float64) @ np.abs(router).astype(np.float64).T)
+        assert np.all(np.abs(got[:n_tok] - want) <= bound)
+        assert np.all(got[n_tok:] == -7.0)
+    finally:
+        arena.free()
+        for b in weights:
+            b.free()
+
+
 def test_route_kernel_ties_and_order(ctx, moe):
     a, m = moe.a, moe.a.moe
     n_tok = 128
