@@ -237,6 +237,55 @@ void sk_rmsnorm(const float *x, const float *w, uint64_t n, float eps, float *ou
     for (uint64_t i = 0; i < n; i++) out[i] = x[i] * r * w[i];
 }
 
+/* ops.rs:8-16 rmsnorm_inplace: x *= r * w (note the grouping, unlike rmsnorm) */
+void sk_rmsnorm_inplace(float *x, const float *w, uint64_t n, float eps) {
+    float ss = -0.0f;
+    for (uint64_t i = 0; i < n; i++) ss += x[i] * x[i];
+    float ms = ss / (float)n;
+    float r = 1.0f / sqrtf(ms + eps);
+    for (uint64_t i = 0; i < n; i++) x[i] *= r * w[i];
+}
+
+/* rope.rs:36-40 frequencies without scaling (no YaRN): theta^(-2i / d), i < d / 2 */
+void sk_rope_freqs(uint64_t head_dim, float theta, float *out) {
+    float d = (float)head_dim;
+    for (uint64_t i = 0; i < head_dim / 2; i++) out[i] = powf(theta, -2.0f * (float)i / d);
+}
+
+/* rope.rs:60-68 rope_neox over x[0..n): pairs (i, i + n/2) rotated by pos * freqs[i] */
+void sk_rope_neox(float *x, uint64_t n, uint64_t pos, const float *freqs, float mscale) {
+    uint64_t half = n / 2;
+    for (uint64_t i = 0; i < half; i++) {
+        float ang = (float)pos * freqs[i];
+        float sn = sinf(ang) * mscale, cs = cosf(ang) * mscale;
+        float a = x[i], b = x[i + half];
+        x[i] = a * cs - b * sn;
+        x[i + half] = a * sn + b * cs;
+    }
+}
+
+/* model.rs:150-169, the attention of every head over the f32 cache of n_pos positions
+ * (no output gate): scores = q.k * (1 / sqrt(hd)), softmax, o = sum_p w_p v_p in position
+ * order from 0.  scores holds n_pos floats of scratch. */
+void sk_attention(const float *q, const float *k_cache, const float *v_cache, uint64_t n_pos,
+                  uint64_t n_head, uint64_t n_head_kv, uint64_t hd, float *scores, float *out) {
+    uint64_t kv_dim = n_head_kv * hd, n_rep = n_head / n_head_kv;
+    float scale = 1.0f / sqrtf((float)hd);
+    for (uint64_t h = 0; h < n_head; h++) {
+        uint64_t base = (h / n_rep) * hd;
+        const float *qh = q + h * hd;
+        for (uint64_t p = 0; p < n_pos; p++) scores[p] = sk_dot(qh, k_cache + p * kv_dim + base, hd) * scale;
+        sk_softmax(scores, n_pos);
+        float *oh = out + h * hd;
+        for (uint64_t d = 0; d < hd; d++) oh[d] = 0.0f;
+        for (uint64_t p = 0; p < n_pos; p++) {
+            const float *vp = v_cache + p * kv_dim + base;
+            float w = scores[p];
+            for (uint64_t d = 0; d < hd; d++) oh[d] += w * vp[d];
+        }
+    }
+}
+
 /* ops.rs:18-26 */
 void sk_softmax(float *x, uint64_t n) {
     float max = -INFINITY;

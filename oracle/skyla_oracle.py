@@ -72,6 +72,14 @@ def lib() -> C.CDLL:
                                      C.c_uint64, C.c_uint64, C.c_uint64, _f, _f, _u32, _f, C.c_uint32]
         l.sk_moe_sort.restype = C.c_int
         l.sk_moe_sort.argtypes = [_u32, C.c_uint64, C.c_uint32, _u32, _u32]
+        l.sk_rmsnorm_inplace.restype = None
+        l.sk_rmsnorm_inplace.argtypes = [_f, _f, C.c_uint64, C.c_float]
+        l.sk_rope_freqs.restype = None
+        l.sk_rope_freqs.argtypes = [C.c_uint64, C.c_float, _f]
+        l.sk_rope_neox.restype = None
+        l.sk_rope_neox.argtypes = [_f, C.c_uint64, C.c_uint64, _f, C.c_float]
+        l.sk_attention.restype = None
+        l.sk_attention.argtypes = [_f, _f, _f, C.c_uint64, C.c_uint64, C.c_uint64, C.c_uint64, _f, _f]
         l.sk_available_parallelism.restype = C.c_uint32
         l.sk_available_parallelism.argtypes = []
         _lib = l
@@ -217,6 +225,63 @@ def moe_sort(ids: np.ndarray, n_expert: int):
     lst = np.zeros(ids.size, np.uint32)
     _check(lib().sk_moe_sort(_p(ids, _u32), ids.size, n_expert, _p(table, _u32), _p(lst, _u32)), "moe_sort")
     return table.reshape(n_expert, 2), lst
+
+
+def rmsnorm_inplace(x: np.ndarray, w, eps) -> None:
+    """ops.rs:8-16 rmsnorm_inplace (x *= r * w) on a contiguous float32 array."""
+    assert x.dtype == np.float32 and x.flags.c_contiguous
+    w = np.ascontiguousarray(w, np.float32)
+    lib().sk_rmsnorm_inplace(_p(x, _f), _p(w, _f), x.size, eps)
+
+
+def rope_freqs(head_dim: int, theta: float) -> np.ndarray:
+    """rope.rs:36-40 frequencies (no scaling)."""
+    out = np.zeros(head_dim // 2, np.float32)
+    lib().sk_rope_freqs(head_dim, theta, _p(out, _f))
+    return out
+
+
+def rope_neox(x: np.ndarray, pos: int, freqs: np.ndarray, mscale: float = 1.0) -> None:
+    """rope.rs:60-68 rope_neox in place on a contiguous float32 array."""
+    assert x.dtype == np.float32 and x.flags.c_contiguous
+    freqs = np.ascontiguousarray(freqs, np.float32)
+    lib().sk_rope_neox(_p(x, _f), x.size, pos, _p(freqs, _f), mscale)
+
+
+def attention(q: np.ndarray, k_cache: np.ndarray, v_cache: np.ndarray, n_pos: int, n_head: int,
+              n_head_kv: int, hd: int) -> np.ndarray:
+    """model.rs:150-169: every head's softmax attention over n_pos cached positions."""
+    q = np.ascontiguousarray(q, np.float32)
+    k_cache = np.ascontiguousarray(k_cache, np.float32)
+    v_cache = np.ascontiguousarray(v_cache, np.float32)
+    scores = np.zeros(max(n_pos, 1), np.float32)
+    out = np.zeros(n_head * hd, np.float32)
+    lib().sk_attention(_p(q, _f), _p(k_cache, _f), _p(v_cache, _f), n_pos, n_head, n_head_kv, hd,
+                       _p(scores, _f), _p(out, _f))
+    return out
+
+
+def kv_quantize_q8(y: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """The GPU backend's q8 KV store (skyla-shaders/shaders/qkv_prep.comp:40-65): per 32
+    consecutive values s = max|y| / 127 in f32, q = round(y / s) with the f32 quotient (ties to
+    even; GLSL leaves the tie direction to the implementation), 0 where s = 0; the scale is
+    stored as f16.  Returns (q int8, scales f16), one scale per 32 values."""
+    y = np.ascontiguousarray(y, np.float32)
+    blocks = y.reshape(-1, 32)
+    s32 = (np.abs(blocks).max(1) / np.float32(127.0)).astype(np.float32)
+    safe = np.where(s32 > 0, s32, np.float32(1.0)).astype(np.float32)
+    q = np.where(s32[:, None] > 0, np.rint(blocks / safe[:, None]), 0).astype(np.int8)
+    return q.reshape(y.shape), s32.astype(np.float16)
+
+
+def kv_stored(y: np.ndarray, q8: bool) -> np.ndarray:
+    """What the attention reads back for a cache row stored by qkv_prep.comp:48-65 (and
+    read by attention.comp): f16(y), or q * f16 scale."""
+    y = np.ascontiguousarray(y, np.float32)
+    if not q8:
+        return y.astype(np.float16).astype(np.float32)
+    q, s = kv_quantize_q8(y)
+    return (q.reshape(-1, 32).astype(np.float32) * s.astype(np.float32)[:, None]).reshape(y.shape)
 
 
 def available_parallelism() -> int:

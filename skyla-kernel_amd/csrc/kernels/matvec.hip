@@ -80,6 +80,41 @@ SK_DEV void store_rows(float *y, uint32_t y_off, uint32_t first, uint32_t n_out,
 
 SK_DEV uint32_t pk(float a, float b) { return as_u32(pack_f16x2(a, b)); }
 
+// Range guard of the f16 activation staging.  A pass's activations are staged as f16, whose
+// range ends at 65504, while the reference multiplies f32 activations (matvec_q4k.comp,
+// matvec_q6k.comp, matvec_q8_0.comp) and inputs such as silu(g) * u reach 1e5-1e6.  Each
+// wave notes in its LDS word the largest |x| >= 2^15 it staged (as float bits, which order
+// like the values for x >= 0; a NaN counts as inf); lane 0 clears the word first, and one
+// wave's LDS operations complete in issue order, so only lanes holding such a value pay for
+// an LDS atomic.  A pass holding |x| >= 2^15 (or a NaN / inf, which no scaling helps) is staged
+// again as x * 2^-e, e = exponent(max) - 14, and the rows' accumulators are scaled by 2^-e
+// before that pass's steps and by 2^e after: exact powers of two, so the result is the
+// unscaled sum up to the f16 rounding of the scaled values.  Passes without large values
+// (all of them in practice) take the unscaled staging as is.
+SK_DEV float abs_max4(float4 v) { return fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))); }
+
+SK_DEV void guard_note(uint32_t *wmax, float m) {
+  uint32_t *slot = wmax + (threadIdx.x >> 6);
+  if ((threadIdx.x & 63) == 0) *slot = 0u;
+  if (!(m < 32768.0f)) atomicMax(slot, m == m ? __builtin_bit_cast(uint32_t, m) : 0x7f800000u);
+}
+
+// after the barrier that ends the staging: the pass's exponent (0: no scaling)
+template <int WAVES>
+SK_DEV int guard_exp(const uint32_t *wmax) {
+  uint32_t m = 0u;
+#pragma unroll
+  for (int w = 0; w < WAVES; w++) m = max(m, wmax[w]);
+  const int e = m == 0u || m >= 0x7f800000u ? 0 : (int)(m >> 23) - 127 - 14;
+  return __builtin_amdgcn_readfirstlane(e);  // the same in every lane: keep it scalar
+}
+
+template <int ROWS>
+SK_DEV void scale_rows(float (&acc)[ROWS], int e) {
+#pragma unroll
+  for (int r = 0; r < ROWS; r++) acc[r] = __builtin_ldexpf(acc[r], e);
+}
+
 // Geometry shared by the three formats.
 template <int WAVES, int ROWS, int LPR>
 struct Geo {
@@ -132,6 +167,7 @@ SK_DEV void matvec_q4k_body(const uint4 *__restrict__ w, const float *x, float *
   __shared__ uint4 xq[4][CHU];  // component-major: lanes read consecutive 16 B
   __shared__ float2 xs[CHU];
   __shared__ float4 sc[G::RWG][G::CH_SUP][4];
+  __shared__ uint32_t wmax[WAVES];
 
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = (tid & 63) % LPR;
@@ -165,15 +201,19 @@ SK_DEV void matvec_q4k_body(const uint4 *__restrict__ w, const float *x, float *
     // headers, then the first PF weight steps, so staging waits only for its own data.
     constexpr int XI = (4 * CHU + G::NT - 1) / G::NT;  // activation quarters per thread
     float4 xa[XI][2];
+    auto load_x = [&]() {
 #pragma unroll
-    for (int j = 0; j < XI; j++) {
-      const uint32_t t = tid + j * G::NT, u = u0 + (t >> 2), qq = t & 3;
-      if (t < 4 * nu) {
-        const float *xp = xv + (u >> 3) * 256 + ((u >> 1) & 3) * 64 + (u & 1) * 16 + (qq >> 1) * 32 + (qq & 1) * 8;
-        xa[j][0] = *(const float4 *)xp;
-        xa[j][1] = *(const float4 *)(xp + 4);
+      for (int j = 0; j < XI; j++) {
+        const uint32_t t = tid + j * G::NT, u = u0 + (t >> 2), qq = t & 3;
+        xa[j][0] = xa[j][1] = make_float4(0.f, 0.f, 0.f, 0.f);  // every path defines them
+        if (t < 4 * nu) {
+          const float *xp = xv + (u >> 3) * 256 + ((u >> 1) & 3) * 64 + (u & 1) * 16 + (qq >> 1) * 32 + (qq & 1) * 8;
+          xa[j][0] = *(const float4 *)xp;
+          xa[j][1] = *(const float4 *)(xp + 4);
+        }
       }
-    }
+    };
+    load_x();
     constexpr int NH = G::RWG * G::CH_SUP, HI_T = (NH + G::NT - 1) / G::NT;  // header items
     uint4 hd[HI_T];
 #pragma unroll
@@ -189,24 +229,32 @@ SK_DEV void matvec_q4k_body(const uint4 *__restrict__ w, const float *x, float *
 
     // stage: item t = quarter t%4 of unit t/4 (values 0-7, 8-15 of the low-nibble half,
     // then of the high half); the pair sums of quarters make the unit's two 16-value sums
+    auto stage_x = [&](float scale) -> float {
+      float big = 0.0f;  // largest |x| staged
 #pragma unroll
-    for (int j = 0; j < XI; j++) {
-      const uint32_t t = tid + j * G::NT, u = t >> 2, qq = t & 3;
-      const bool live = t < 4 * nu;
-      const float4 a = live ? xa[j][0] : make_float4(0.f, 0.f, 0.f, 0.f);
-      const float4 b = live ? xa[j][1] : make_float4(0.f, 0.f, 0.f, 0.f);
-      const uint32_t h0 = pk(a.x, a.z), h1 = pk(a.y, a.w), h2 = pk(b.x, b.z), h3 = pk(b.y, b.w);
-      const f16x2 one = {(f16)1.0f, (f16)1.0f};
-      float sum = dot2(as_f16x2(h0), one, 0.0f);
-      sum = dot2(as_f16x2(h1), one, sum);
-      sum = dot2(as_f16x2(h2), one, sum);
-      sum = dot2(as_f16x2(h3), one, sum);
-      sum += dpp_f<0xb1>(sum);  // + the other quarter of the same half
-      if (t < 4 * CHU) {
-        xq[qq][u] = make_uint4(h0, h1, h2, h3);
-        if ((qq & 1) == 0) ((float *)&xs[u])[qq >> 1] = sum;
+      for (int j = 0; j < XI; j++) {
+        const uint32_t t = tid + j * G::NT, u = t >> 2, qq = t & 3;
+        float4 a = xa[j][0], b = xa[j][1];
+        big = fmaxf(big, fmaxf(abs_max4(a), abs_max4(b)));
+        if (scale != 1.0f) {
+          a = make_float4(a.x * scale, a.y * scale, a.z * scale, a.w * scale);
+          b = make_float4(b.x * scale, b.y * scale, b.z * scale, b.w * scale);
+        }
+        const uint32_t h0 = pk(a.x, a.z), h1 = pk(a.y, a.w), h2 = pk(b.x, b.z), h3 = pk(b.y, b.w);
+        const f16x2 one = {(f16)1.0f, (f16)1.0f};
+        float sum = dot2(as_f16x2(h0), one, 0.0f);
+        sum = dot2(as_f16x2(h1), one, sum);
+        sum = dot2(as_f16x2(h2), one, sum);
+        sum = dot2(as_f16x2(h3), one, sum);
+        sum += dpp_f<0xb1>(sum);  // + the other quarter of the same half
+        if (t < 4 * CHU) {
+          xq[qq][u] = make_uint4(h0, h1, h2, h3);
+          if ((qq & 1) == 0) ((float *)&xs[u])[qq >> 1] = sum;
+        }
       }
-    }
+      return big;
+    };
+    guard_note(wmax, stage_x(1.0f));
     // decode: the 8 six-bit scales and mins as bytes of four words (quant.rs:40-49)
 #pragma unroll
     for (int j = 0; j < HI_T; j++) {
@@ -231,6 +279,13 @@ SK_DEV void matvec_q4k_body(const uint4 *__restrict__ w, const float *x, float *
       }
     }
     __syncthreads();
+    const int e = guard_exp<WAVES>(wmax);
+    if (e) {  // rare: the pass again at x * 2^-e
+      load_x();
+      stage_x(__builtin_ldexpf(1.0f, -e));
+      __syncthreads();
+      scale_rows(acc, -e);
+    }
 
     const uint32_t S = (nu + LPR - 1) / LPR;
     auto step = [&](uint32_t st, const uint4 (&qj)[ROWS]) {
@@ -272,6 +327,7 @@ SK_DEV void matvec_q4k_body(const uint4 *__restrict__ w, const float *x, float *
 #pragma unroll
     for (int j = 0; j < PF; j++)
       if (j0 + j < S) step(j0 + j, q[j]);
+    if (e) scale_rows(acc, e);
   }
   store_rows<ACCUM, ROWS, LPR>(y, y_off, first, p.n_out, lane, acc);
 }
@@ -293,6 +349,7 @@ SK_DEV void matvec_q6k_body(const uint4 *__restrict__ w, const uint16_t *__restr
   __shared__ uint4 xq[8][G::CH / 64];  // component-major
   __shared__ float4 xs[G::CH / 64];
   __shared__ float4 sc[G::RWG][G::CH_SUP][4];
+  __shared__ uint32_t wmax[WAVES];
 
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = (tid & 63) % LPR;
@@ -341,15 +398,19 @@ SK_DEV void matvec_q6k_body(const uint4 *__restrict__ w, const uint16_t *__restr
 #pragma unroll
       for (int k = 0; k < 4; k++) v[k] = *(const float4 *)(xp + 4 * k);
     };
-    auto x_store = [&](uint32_t t, const float4 (&v)[4]) {
+    float big = 0.0f;  // largest |x| this thread staged
+    auto x_store = [&](uint32_t t, const float4 (&v)[4], float scale) {
       const uint32_t i = t >> 2, g = t & 3;
       const f16x2 one = {(f16)1.0f, (f16)1.0f};
       uint32_t pp[8];
       float s = 0.0f;
 #pragma unroll
       for (int k = 0; k < 4; k++) {
-        pp[2 * k] = pk(v[k].x, v[k].z);
-        pp[2 * k + 1] = pk(v[k].y, v[k].w);
+        big = fmaxf(big, abs_max4(v[k]));
+        const float4 e = scale != 1.0f ? make_float4(v[k].x * scale, v[k].y * scale, v[k].z * scale, v[k].w * scale)
+                                       : v[k];
+        pp[2 * k] = pk(e.x, e.z);
+        pp[2 * k + 1] = pk(e.y, e.w);
         s = dot2(as_f16x2(pp[2 * k]), one, s);
         s = dot2(as_f16x2(pp[2 * k + 1]), one, s);
       }
@@ -388,17 +449,27 @@ SK_DEV void matvec_q6k_body(const uint4 *__restrict__ w, const uint16_t *__restr
     if (tid < n_items) h_load(tid, sv0, dv0);
 #pragma unroll
     for (int j = 0; j < PF; j++) load(min(lane + j * LPR, nu - 1), qa[j], qb[j], qh[j]);
-    if (tid < n_xi) x_store(tid, xv4);
+    if (tid < n_xi) x_store(tid, xv4, 1.0f);
     if (tid < n_items) h_store(tid, sv0, dv0);
     for (uint32_t t = tid + G::NT; t < n_xi; t += G::NT) {
       x_item(t, xv4);
-      x_store(t, xv4);
+      x_store(t, xv4, 1.0f);
     }
     for (uint32_t i = tid + G::NT; i < n_items; i += G::NT) {
       h_load(i, sv0, dv0);
       h_store(i, sv0, dv0);
     }
+    guard_note(wmax, big);
     __syncthreads();
+    const int e = guard_exp<WAVES>(wmax);
+    if (e) {  // rare: the pass again at x * 2^-e
+      for (uint32_t t = tid; t < n_xi; t += G::NT) {
+        x_item(t, xv4);
+        x_store(t, xv4, __builtin_ldexpf(1.0f, -e));
+      }
+      __syncthreads();
+      scale_rows(acc, -e);
+    }
 
     for (uint32_t j0 = 0; lane + j0 * LPR < nu; j0 += PF) {
 #pragma unroll
@@ -443,6 +514,7 @@ SK_DEV void matvec_q6k_body(const uint4 *__restrict__ w, const uint16_t *__restr
         __builtin_amdgcn_sched_barrier(0);  // each refill right behind the step it replaces
       }
     }
+    if (e) scale_rows(acc, e);
   }
   store_rows<ACCUM, ROWS, LPR>(y, y_off, first, p.n_out, lane, acc);
 }
@@ -461,6 +533,7 @@ SK_DEV void matvec_q8_0_body(const uint4 *__restrict__ w, const uint16_t *__rest
   __shared__ uint4 xq[2][G::CH / 16];  // component-major
   __shared__ float xs[G::CH / 16];
   __shared__ float dd[G::RWG][NBLK];
+  __shared__ uint32_t wmax[WAVES];
 
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = (tid & 63) % LPR;
@@ -491,14 +564,18 @@ SK_DEV void matvec_q8_0_body(const uint4 *__restrict__ w, const uint16_t *__rest
 #pragma unroll
       for (int k = 0; k < 4; k++) v[k] = *(const float4 *)(xp + 4 * k);
     };
-    auto x_store = [&](uint32_t i, const float4 (&v)[4]) {
+    float big = 0.0f;  // largest |x| this thread staged
+    auto x_store = [&](uint32_t i, const float4 (&v)[4], float scale) {
       uint32_t pp[8];
       const f16x2 one = {(f16)1.0f, (f16)1.0f};
       float s = 0.0f;
 #pragma unroll
       for (int k = 0; k < 4; k++) {
-        pp[2 * k] = pk(v[k].x, v[k].z);
-        pp[2 * k + 1] = pk(v[k].y, v[k].w);
+        big = fmaxf(big, abs_max4(v[k]));
+        const float4 e = scale != 1.0f ? make_float4(v[k].x * scale, v[k].y * scale, v[k].z * scale, v[k].w * scale)
+                                       : v[k];
+        pp[2 * k] = pk(e.x, e.z);
+        pp[2 * k + 1] = pk(e.y, e.w);
         s = dot2(as_f16x2(pp[2 * k]), one, s);
         s = dot2(as_f16x2(pp[2 * k + 1]), one, s);
       }
@@ -525,14 +602,24 @@ SK_DEV void matvec_q8_0_body(const uint4 *__restrict__ w, const uint16_t *__rest
 #pragma unroll
       for (int r = 0; r < ROWS; r++) q[j][r] = qr[r][u0 + i];
     }
-    if (tid < nu) x_store(tid, xv4);
+    if (tid < nu) x_store(tid, xv4, 1.0f);
     if (tid < n_items) dd[tid / nb][tid % nb] = f16_bits_to_f32(dv0);
     for (uint32_t i = tid + G::NT; i < nu; i += G::NT) {
       x_unit(i, xv4);
-      x_store(i, xv4);
+      x_store(i, xv4, 1.0f);
     }
     for (uint32_t i = tid + G::NT; i < n_items; i += G::NT) dd[i / nb][i % nb] = f16_bits_to_f32(d_load(i));
+    guard_note(wmax, big);
     __syncthreads();
+    const int e = guard_exp<WAVES>(wmax);
+    if (e) {  // rare: the pass again at x * 2^-e
+      for (uint32_t i = tid; i < nu; i += G::NT) {
+        x_unit(i, xv4);
+        x_store(i, xv4, __builtin_ldexpf(1.0f, -e));
+      }
+      __syncthreads();
+      scale_rows(acc, -e);
+    }
 
     for (uint32_t j0 = 0; lane + j0 * LPR < nu; j0 += PF) {
 #pragma unroll
@@ -560,6 +647,7 @@ SK_DEV void matvec_q8_0_body(const uint4 *__restrict__ w, const uint16_t *__rest
         for (int r = 0; r < ROWS; r++) q[j][r] = qr[r][u0 + inext];
       }
     }
+    if (e) scale_rows(acc, e);
   }
   store_rows<ACCUM, ROWS, LPR>(y, y_off, first, p.n_out, lane, acc);
 }

@@ -48,6 +48,37 @@ BW(1024)
 // Push: o0..o3 region offsets (as the matmul push), n_in, n_rows, y_off.
 struct DequantPush { uint32_t o0, o1, o2, o3, n_in, n_rows, y_off; };
 
+// The 32 values of group gi (32-value groups in row order) of row `row`; returns the index
+// of the first value within the row.
+template <int TYPE>
+SK_DEV uint32_t dequant_group(const uint4 *w, const uint16_t *wd, uint32_t o0, uint32_t o1, uint32_t o2,
+                              uint32_t o3, uint32_t n_in, uint32_t row, uint32_t gi, float o[32]) {
+  if (TYPE == 1) {
+    const uint32_t sb = gi >> 3, sub = gi & 7;
+    const uint32_t rs = row * (n_in >> 8) + sb;
+    const uint4 *qs = w + o0 + rs * 8 + (sub >> 1) * 2;
+    dequant_q4k_sub(w[o1 + rs], qs[0], qs[1], sub, o);
+    return sb * 256 + (sub >> 1) * 64 + (sub & 1) * 32;
+  } else if (TYPE == 2) {
+    const uint32_t sb = gi >> 3, hf = (gi >> 2) & 1, g = gi & 3;
+    const uint32_t rs = row * (n_in >> 8) + sb;
+    uint4 ql[4], qh[2];
+    for (int i = 0; i < 4; i++) ql[i] = w[o0 + rs * 8 + hf * 4 + i];
+    for (int i = 0; i < 2; i++) qh[i] = w[o1 + rs * 4 + hf * 2 + i];
+    dequant_q6k_group(ql, qh, w[o2 + rs], f16_bits_to_f32(wd[o3 + rs]), hf, g, o);
+    return sb * 256 + hf * 128 + g * 32;
+  } else {
+    const uint4 *q = w + o0 + row * (n_in >> 4) + gi * 2;
+    dequant_q8_0_block(q[0], q[1], f16_bits_to_f32(wd[o1 + row * (n_in >> 5) + gi]), o);
+    return gi * 32;
+  }
+}
+
+SK_DEV void store32(float *dst, const float o[32]) {
+#pragma unroll
+  for (int i = 0; i < 8; i++) ((float4 *)dst)[i] = make_float4(o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]);
+}
+
 template <int TYPE>
 SK_DEV void dequant_body(const uint4 *w, const uint16_t *wd, float *y, DequantPush p) {
   const uint32_t groups = p.n_in >> 5;
@@ -55,30 +86,37 @@ SK_DEV void dequant_body(const uint4 *w, const uint16_t *wd, float *y, DequantPu
   if (gid >= groups * p.n_rows) return;
   const uint32_t row = gid / groups, gi = gid % groups;
   float o[32];
-  uint32_t first;
-  if (TYPE == 1) {
-    const uint32_t sb = gi >> 3, sub = gi & 7;
-    const uint32_t rs = row * (p.n_in >> 8) + sb;
-    const uint4 *qs = w + p.o0 + rs * 8 + (sub >> 1) * 2;
-    dequant_q4k_sub(w[p.o1 + rs], qs[0], qs[1], sub, o);
-    first = sb * 256 + (sub >> 1) * 64 + (sub & 1) * 32;
-  } else if (TYPE == 2) {
-    const uint32_t sb = gi >> 3, hf = (gi >> 2) & 1, g = gi & 3;
-    const uint32_t rs = row * (p.n_in >> 8) + sb;
-    uint4 ql[4], qh[2];
-    for (int i = 0; i < 4; i++) ql[i] = w[p.o0 + rs * 8 + hf * 4 + i];
-    for (int i = 0; i < 2; i++) qh[i] = w[p.o1 + rs * 4 + hf * 2 + i];
-    dequant_q6k_group(ql, qh, w[p.o2 + rs], f16_bits_to_f32(wd[p.o3 + rs]), hf, g, o);
-    first = sb * 256 + hf * 128 + g * 32;
-  } else {
-    const uint4 *q = w + p.o0 + row * (p.n_in >> 4) + gi * 2;
-    dequant_q8_0_block(q[0], q[1], f16_bits_to_f32(wd[p.o1 + row * groups + gi]), o);
-    first = gi * 32;
-  }
-  float4 *dst = (float4 *)(y + p.y_off + (size_t)row * p.n_in + first);
-#pragma unroll
-  for (int i = 0; i < 8; i++) dst[i] = make_float4(o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]);
+  const uint32_t first = dequant_group<TYPE>(w, wd, p.o0, p.o1, p.o2, p.o3, p.n_in, row, gi, o);
+  store32(y + p.y_off + (size_t)row * p.n_in + first, o);
 }
+
+// embed: the activation rows of a chunk's tokens from the HBM copy of token_embd.  The
+// reference dequantises the rows on the host and writes them into the mapped arena
+// (engine.rs:100-117, skyla_gguf::dequantize); here the engine writes only the token ids
+// (u32, at ids_off of the arena) and this gathers and dequantises row ids[tok] into
+// a[x_off + tok * stride ..] for tok < ctl[2], with the same bit-exact arithmetic as
+// dequant.  One thread per 32-value group; grid [ceil(n_embd / 32 / 256), tokens, 1].
+// spec [TYPE]; push: o0..o3 of the matrix, n_embd, ids_off, x_off, stride.
+struct EmbedPush { uint32_t o0, o1, o2, o3, n_embd, ids_off, x_off, stride; };
+
+template <int TYPE>
+SK_DEV void embed_body(const uint4 *w, const uint16_t *wd, float *a, const uint32_t *ctl, EmbedPush p) {
+  const uint32_t tok = blockIdx.y, gi = blockIdx.x * 256 + threadIdx.x;
+  if (tok >= ctl[2] || gi >= (p.n_embd >> 5)) return;
+  const uint32_t row = ctl[p.ids_off + tok];
+  float o[32];
+  const uint32_t first = dequant_group<TYPE>(w, wd, p.o0, p.o1, p.o2, p.o3, p.n_embd, row, gi, o);
+  store32(a + p.x_off + tok * p.stride + first, o);
+}
+
+#define EMB(T)                                                                               \
+  extern "C" __global__ __launch_bounds__(256) void embed__##T(                                \
+      const uint4 *w, const uint16_t *wd, float *a, const uint32_t *ctl, EmbedPush p) {       \
+    embed_body<T>(w, wd, a, ctl, p);                                                         \
+  }
+EMB(0)
+EMB(1)
+EMB(2)
 
 #define DQ(T)                                                                                \
   extern "C" __global__ __launch_bounds__(256) void dequant__##T(const uint4 *w,              \

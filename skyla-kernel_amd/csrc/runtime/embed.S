@@ -14,4 +14,5 @@ EMBED(skyla_co_matvec, "matvec.hsaco")
 EMBED(skyla_co_matmul, "matmul.hsaco")
 EMBED(skyla_co_moe, "moe.hsaco")
 EMBED(skyla_co_util, "util.hsaco")
+EMBED(skyla_co_attention, "attention.hsaco")
     .section .note.GNU-stack,"",@progbits

@@ -34,6 +34,7 @@ extern "C" const unsigned char skyla_co_matvec[], skyla_co_matvec_end[];
 extern "C" const unsigned char skyla_co_matmul[], skyla_co_matmul_end[];
 extern "C" const unsigned char skyla_co_moe[], skyla_co_moe_end[];
 extern "C" const unsigned char skyla_co_util[], skyla_co_util_end[];
+extern "C" const unsigned char skyla_co_attention[], skyla_co_attention_end[];
 
 namespace {
 
@@ -66,9 +67,10 @@ struct KernelInfo {
   uint32_t n_buffers;
   uint32_t push_words;
   uint32_t spec_len_min, spec_len_max;
-  int threads_from_spec;  // -1: fixed 256; k >= 0: 64 * spec[k] (matvec waves) or spec[k]
+  int threads_from_spec;  // -1: fixed (`threads`); k >= 0: 64 * spec[k] (matvec waves) or spec[k]
   bool waves;
   bool segmented;  // takes its push words as a segment table (kernels/common.h Segments)
+  uint32_t threads = 256;
 };
 
 const KernelInfo kKernels[] = {
@@ -77,13 +79,20 @@ const KernelInfo kKernels[] = {
     {"matvec_q8_0", 5, 9, 5, 5, 0, true, true},
     {"matmul", 5, 13, 3, 4, -1, false, false},
     {"moe_logits", 3, 5, 0, 0, -1, false, false},
-    {"moe_route", 2, 5, 0, 0, -1, false, false},
+    {"moe_route", 2, 5, 0, 0, -1, false, false, 64},  // one wave per token
     {"moe_sort", 1, 5, 0, 0, -1, false, false},
     {"moe_combine", 1, 6, 0, 0, -1, false, false},
     {"silu_mul", 2, 4, 0, 0, -1, false, false},
     {"to_half", 3, 6, 0, 0, -1, false, false},
     {"bandwidth", 2, 1, 1, 1, 0, false, false},
     {"dequant", 3, 7, 1, 1, -1, false, false},
+    // the decode step around the matvecs (kernels/attention.hip; kernels.rs:186-193)
+    {"rmsnorm", 3, 6, 0, 0, -1, false, false},
+    {"qkv_prep", 5, 16, 5, 5, -1, false, false, 64},       // one wave per (head, token)
+    {"attention", 5, 11, 6, 6, -1, false, false, 64},      // one wave per (kv head, split, token)
+    {"attention_merge", 2, 6, 2, 2, -1, false, false, 128},
+    {"take_last", 2, 4, 0, 0, -1, false, false},
+    {"embed", 4, 8, 1, 1, -1, false, false},  // token rows from the HBM token_embd (util.hip)
 };
 
 const KernelInfo *find_kernel(const char *name) {
@@ -464,7 +473,8 @@ int skyla_hip_context_new(int device, skyla_hip_context **out) {
   ctx->name += std::string(" (") + prop.gcnArchName + ", " + std::to_string(prop.multiProcessorCount) + " CUs)";
   ctx->warp = (uint32_t)prop.warpSize;
   HIP_TRY(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking));
-  const unsigned char *images[] = {skyla_co_matvec, skyla_co_matmul, skyla_co_moe, skyla_co_util};
+  const unsigned char *images[] = {skyla_co_matvec, skyla_co_matmul, skyla_co_moe, skyla_co_util,
+                                   skyla_co_attention};
   for (const unsigned char *img : images) {
     hipModule_t m = nullptr;
     hipError_t le = hipModuleLoadData(&m, img);
@@ -617,12 +627,11 @@ int skyla_hip_pipeline_new(skyla_hip_context *ctx, const char *name, uint32_t n_
   if (std::strcmp(name, "matmul") == 0 && n_spec == 4 && spec[3] == 0) n_key = 3;
   std::string sym = name;
   for (uint32_t i = 0; i < n_key; i++) sym += (i ? "_" : "__") + std::to_string(spec[i]);
-  uint32_t threads = 256;
+  uint32_t threads = k->threads;
   if (k->threads_from_spec >= 0)
     threads = k->waves ? 64 * spec[k->threads_from_spec] : spec[k->threads_from_spec];
   // matmul: dense tiles (MOE = 0) run eight waves, expert groups four (matmul.hip)
   if (std::strcmp(name, "matmul") == 0 && spec[2] == 0) threads = 512;
-  if (std::strcmp(name, "moe_route") == 0) threads = 64;  // one wave per token
   auto p = std::make_unique<skyla_hip_pipeline>();
   p->ctx = ctx;
   p->symbol = sym;

@@ -195,7 +195,8 @@ class Kernels:
     """kernels.rs:139-233, restricted to the pipelines of the quantized weight path."""
 
     def __init__(self, ctx: Context, weights: Sequence[Buffer], a: Buffer,
-                 kquant_tactic=None, q8_0_tactic=None):
+                 kquant_tactic=None, q8_0_tactic=None, kv: Buffer | None = None, c: Config | None = None,
+                 precision: KvPrecision | None = None, embd_dtype: DType | None = None):
         if ctx.subgroup_size != 64:
             raise ValueError(f"no kernels for subgroup size {ctx.subgroup_size} (need 64)")
         lanes = 64
@@ -220,6 +221,31 @@ class Kernels:
         self.combine = build("moe_combine", [a], 24)
         self.sort = build("moe_sort", [a], 20)
         self.to_half = build("to_half", [a, a, a], 24) if HALF_INPUTS else None
+        if kv is None:
+            return
+        # the rest of the decode step (kernels.rs:186-193); heads are 128 wide, no gate
+        if c.head_dim != 128 or c.n_head % c.n_head_kv or c.n_head // c.n_head_kv not in (1, 2, 4, 8):
+            raise ValueError(f"no attention kernels for head_dim {c.head_dim}, "
+                             f"{c.n_head}/{c.n_head_kv} heads")
+        pr = KvPrecision(precision)
+        k8, v8 = int(pr.keys_q8), int(pr.values_q8)
+
+        def build_spec(name, bufs, push, spec):
+            p = ctx.create_pipeline(name, len(bufs), push, spec)
+            p.bind_buffers(bufs)
+            return p
+
+        self.rmsnorm = build("rmsnorm", [w0, a, a], 24)
+        self.qkv = build_spec("qkv_prep", [w0, a, a, kv, kv], 64, [k8, v8, c.head_dim, c.head_dim, 0])
+        self.attention = build_spec("attention", [a, a, kv, kv, kv], 44,
+                                    [c.n_head // c.n_head_kv, ATTENTION_CHUNK, k8, v8, c.head_dim, c.head_dim])
+        self.merge = build_spec("attention_merge", [a, a], 24, [c.head_dim, 0])
+        self.take_last = build("take_last", [a, a], 16)
+        # token rows gathered from the HBM token_embd, one binding set per weight buffer
+        ty = {DType.Q8_0: 0, DType.Q4K: 1, DType.Q6K: 2}[DType(embd_dtype)]
+        self.embed = ctx.create_pipeline_sets("embed", 4, 32, [ty], len(weights))
+        for i, wb in enumerate(weights):
+            self.embed.bind_set_buffers(i, [wb, wb, a, a])
 
     def matvec(self, dtype: DType, batched: bool) -> Matvec:
         s = self.batch if batched else self.decode
@@ -229,7 +255,8 @@ class Kernels:
 # ---- arena.rs ----------------------------------------------------------------------------
 @dataclasses.dataclass
 class Config:
-    """The fields of skyla_ref::Config (skyla-ref/src/lib.rs:17-37) the path reads."""
+    """The fields of skyla_ref::Config (skyla-ref/src/lib.rs:17-37) the path reads (the
+    plain attention layout: no RoPE scaling, n_rot = head_dim, no output gate)."""
     n_embd: int
     n_ff: int = 0
     n_head: int = 1
@@ -240,6 +267,91 @@ class Config:
     n_expert_used: int = 0
     n_ff_expert: int = 0
     eps: float = 1e-6
+    n_layer: int = 0
+    rope_theta: float = 1e6
+    rope_mscale: float = 1.0
+
+
+_libm = None
+
+
+def rope_frequencies(c: Config) -> np.ndarray:
+    """rope.rs:36-40 without scaling: theta^(-2i / head_dim), with the f32 exponent and the
+    C library's powf that Rust's f32::powf calls."""
+    global _libm
+    if _libm is None:
+        import ctypes
+        import ctypes.util
+        _libm = ctypes.CDLL(ctypes.util.find_library("m"))
+        _libm.powf.restype = ctypes.c_float
+        _libm.powf.argtypes = [ctypes.c_float, ctypes.c_float]
+    d = np.float32(c.head_dim)
+    out = [_libm.powf(np.float32(c.rope_theta), np.float32(-2.0) * np.float32(i) / d) for i in range(c.head_dim // 2)]
+    return np.asarray(out, np.float32)
+
+
+# ---- kv.rs -------------------------------------------------------------------------------
+class KvPrecision(IntEnum):
+    """kv.rs:1-16."""
+    F16 = 0
+    Q8 = 1
+    F16_KEYS_Q8_VALUES = 2
+
+    @property
+    def keys_q8(self) -> bool:
+        return self == KvPrecision.Q8
+
+    @property
+    def values_q8(self) -> bool:
+        return self != KvPrecision.F16
+
+
+class KvLayout:
+    """kv.rs:18-88: keys of every cached layer, then values, then the f16 scales of the
+    8-bit halves; offsets in units of the view that reads them (f16 or i8 entries, f16
+    scales)."""
+
+    def __init__(self, precision: KvPrecision, layers: Sequence[bool], max_ctx: int, kv_dim: int):
+        self.precision = KvPrecision(precision)
+        n, self.slots = 0, []
+        for cached in layers:
+            n += int(cached)
+            self.slots.append(max(n - 1, 0))
+        self.n_layer = n
+        self.per_layer = max_ctx * kv_dim
+
+    @staticmethod
+    def _width(q8: bool) -> int:
+        return 1 if q8 else 2
+
+    def keys_bytes(self) -> int:
+        return self.n_layer * self.per_layer * self._width(self.precision.keys_q8)
+
+    def values_bytes(self) -> int:
+        return self.n_layer * self.per_layer * self._width(self.precision.values_q8)
+
+    def scales_per_layer(self) -> int:
+        return self.per_layer // 32
+
+    def bytes(self) -> int:
+        scaled = int(self.precision.keys_q8) + int(self.precision.values_q8)
+        return self.keys_bytes() + self.values_bytes() + scaled * self.n_layer * self.scales_per_layer() * 2
+
+    def keys(self, layer: int) -> int:
+        return self.slots[layer] * self.per_layer
+
+    def values(self, layer: int) -> int:
+        return self.keys_bytes() // self._width(self.precision.values_q8) + self.slots[layer] * self.per_layer
+
+    def _scales_base(self) -> int:
+        return (self.keys_bytes() + self.values_bytes()) // 2
+
+    def key_scales(self, layer: int) -> int:
+        return self._scales_base() + self.slots[layer] * self.scales_per_layer()
+
+    def value_scales(self, layer: int) -> int:
+        skip = int(self.precision.keys_q8) * self.n_layer * self.scales_per_layer()
+        return self._scales_base() + skip + self.slots[layer] * self.scales_per_layer()
 
 
 def _next64(n: int) -> int:
@@ -260,10 +372,13 @@ class MoeRegions:
 
 
 class Arena:
-    """arena.rs:82-113 without the KV cache and recurrent-state regions: fixed f32
-    offsets after 64 control words, BATCH rows per batched region."""
+    """arena.rs:82-181 without the recurrent-state regions: fixed f32 offsets after 64
+    control words, BATCH rows per batched region, and (with a precision) the KV cache
+    buffer of kv.rs.  One region more than the reference: `tokens`, the u32 ids of the
+    chunk, which the embed kernel gathers rows for (the reference dequantises them on the
+    host into x, engine.rs:100-117)."""
 
-    def __init__(self, ctx: Context, c: Config, max_ctx: int = 64):
+    def __init__(self, ctx: Context, c: Config, max_ctx: int = 64, precision: KvPrecision | None = None):
         self.size = 64
         n_split = -(-max_ctx // ATTENTION_CHUNK)
 
@@ -298,8 +413,17 @@ class Arena:
         widest = max([_next64(w) * BATCH for w in (c.n_embd, c.n_head * c.head_dim, c.n_ff)]
                      + [stride * slots])
         self.half = single(widest // 2 + 64)
+        self.tokens = single(BATCH)
         self.buffer = ctx.alloc_host(self.size * 4)
         self.n_split = n_split
+        self.max_ctx = max_ctx
+        self.kv_layout, self.kv = None, None
+        if precision is not None:
+            self.kv_layout = KvLayout(precision, [True] * c.n_layer, max_ctx, c.n_head_kv * c.head_dim)
+            if self.kv_layout.bytes() > ctx.max_buffer():
+                raise ValueError(f"KV cache for {max_ctx} tokens needs {self.kv_layout.bytes() >> 20} MiB, "
+                                 "above the allocation cap")
+            self.kv = ctx.alloc_host(max(16, self.kv_layout.bytes()))
 
     def f32(self):
         return self.buffer.as_f32()
@@ -412,3 +536,226 @@ class Graph:
         xg = self.input((a.gate, a.s_ff), c.n_ff, 1)
         self.matvec(down, xg, (a.x, a.s_embd), True, bt)
         self.stage("matvec down")
+
+    # ---- the rest of graph.rs: norms, attention, a layer ----------------------------
+    def rmsnorm(self, x: int, w: int, y: int, tokens: int) -> None:
+        """graph.rs:48-52."""
+        c = self.c
+        push = [x, w, y, c.n_embd, f32_bits(c.eps), self.a.s_embd]
+        self.r.dispatch(self.k.rmsnorm, [1, tokens, 1], push)
+
+    def embed(self, m: QMatrix) -> None:
+        """The chunk's token rows into x (the reference's host-side Engine::load,
+        engine.rs:100-117, as a gather from the HBM token_embd)."""
+        a, c = self.a, self.c
+        o = m.off
+        push = [o[0], o[1], o[2], o[3], c.n_embd, a.tokens, a.x, a.s_embd]
+        self.r.dispatch_set(self.k.embed, m.buf, [-(-(c.n_embd // 32) // 256), self.b, 1], push)
+        self.stage("embed")
+
+    def attention(self, l: int, at: "AttnWeights", rope: int) -> None:
+        """graph.rs:59-113: q/k/v matvecs, QK-norm + RoPE + KV write, split-K attention,
+        merge, o (+= x)."""
+        a, c, bt = self.a, self.c, self.batched
+        xn = self.input((a.n, a.s_embd), c.n_embd, 1)
+        self.matvec(at.wq, xn, (a.q, a.s_q), False, bt)
+        self.matvec(at.wk, xn, (a.k, a.s_kv), False, bt)
+        self.matvec(at.wv, xn, (a.v, a.s_kv), False, bt)
+        self.stage("matvec qkv")
+        self.qk_rope(l, at.q_norm, at.k_norm, rope)
+        self.attend(l)
+        xa = self.input((a.attn, a.s_attn), c.n_head * c.head_dim, 1)
+        self.matvec(at.wo, xa, (a.x, a.s_embd), True, bt)
+        self.stage("matvec o")
+
+    def qk_rope(self, l: int, q_norm: int, k_norm: int, rope: int) -> None:
+        """graph.rs:67-88: QK-norm + RoPE of q (in place) and k, and k, v into layer l's cache."""
+        a, c, kv = self.a, self.c, self.a.kv_layout
+        push = [a.q, a.k, a.v, q_norm, k_norm, kv.keys(l), kv.values(l), c.n_head, c.n_head_kv,
+                f32_bits(c.eps), rope, f32_bits(c.rope_mscale), a.s_q, a.s_kv, kv.key_scales(l),
+                kv.value_scales(l)]
+        self.r.dispatch(self.k.qkv, [c.n_head + 2 * c.n_head_kv, self.b, 1], push)
+        self.stage("qk norm + rope")
+
+    def attend(self, l: int) -> None:
+        """graph.rs:89-109: split-K attention over layer l's cache, then the merge into attn."""
+        a, c, kv = self.a, self.c, self.a.kv_layout
+        scale = np.float32(1.0) / np.sqrt(np.float32(c.head_dim))
+        push = [a.q, a.part, kv.keys(l), kv.values(l), c.n_head_kv, a.n_split, f32_bits(scale), a.s_q,
+                a.s_part, kv.key_scales(l), kv.value_scales(l)]
+        self.r.dispatch(self.k.attention, [c.n_head_kv, a.n_split, self.b], push)
+        self.stage("attention")
+        push = [a.part, a.attn, a.n_split, ATTENTION_CHUNK, a.s_part, a.s_attn]
+        self.r.dispatch(self.k.merge, [c.n_head, self.b, 1], push)
+        self.stage("attention merge")
+
+    def layer(self, l: int, lw: "LayerWeights", rope: int) -> None:
+        """graph.rs:150-185."""
+        a, b = self.a, self.b
+        self.rmsnorm(a.x, lw.attn_norm, a.n, b)
+        self.stage("rmsnorm")
+        self.attention(l, lw.attn, rope)
+        self.rmsnorm(a.x, lw.ffn_norm, a.n, b)
+        self.stage("rmsnorm")
+        if lw.router is not None:
+            self.moe(lw.gate, lw.up, lw.down, lw.router)
+        else:
+            self.dense_ffn(lw.gate, lw.up, lw.down)
+
+
+def f32_bits(v: float) -> int:
+    """f32::to_bits of a push word."""
+    return int(np.array([v], dtype=np.float32).view(np.uint32)[0])
+
+
+# ---- weights.rs --------------------------------------------------------------------------
+@dataclasses.dataclass
+class AttnWeights:
+    q_norm: int
+    k_norm: int
+    wq: QMatrix
+    wk: QMatrix
+    wv: QMatrix
+    wo: QMatrix
+
+
+@dataclasses.dataclass
+class LayerWeights:
+    attn_norm: int
+    ffn_norm: int
+    attn: AttnWeights
+    gate: QMatrix
+    up: QMatrix
+    down: QMatrix
+    router: int | None = None
+
+
+@dataclasses.dataclass
+class Weights:
+    buffers: list
+    output: QMatrix
+    embd: QMatrix
+    out_norm: int
+    rope: int
+    layers: list
+
+
+def load_weights(ctx: Context, model: dict, c: Config) -> Weights:
+    """weights.rs:58-144 for the dense attention layout (and MoE FFNs), from a tensor map:
+    name -> f32 array (norms, router) or (dtype, n_in, n_out, raw GGUF blocks[, n_expert]).
+    Tables (RoPE frequencies, norms, routers) go first in buffer 0, as the planner puts them.
+    token_embd is also laid out for the GPU embedding gather; a tied model (no
+    output.weight) uses that one copy as its output head, as weights.rs:133-136 does."""
+    p = Planner(ctx.max_buffer())
+    rope = p.table(rope_frequencies(c))
+    out_norm = p.table(model["output_norm.weight"])
+    moe = c.n_expert > 0
+    norms = []
+    for i in range(c.n_layer):
+        n = lambda s: f"blk.{i}.{s}.weight"  # noqa: E731
+        norms.append((p.table(model[n("attn_norm")]), p.table(model[n("ffn_norm")]),
+                      p.table(model[n("attn_q_norm")]), p.table(model[n("attn_k_norm")]),
+                      p.table(model[n("ffn_gate_inp")]) if moe else None))
+
+    def mat(name):  # expert tensors hold n_expert matrices of n_out rows (QMatrix.n_out per expert)
+        t = model[name]
+        return p.matrix(t[0], t[1], t[2], t[3])
+
+    embd = mat("token_embd.weight")
+    output = mat("output.weight") if "output.weight" in model else embd
+    layers = []
+    ffn = (lambda s: f"{s}_exps") if moe else (lambda s: s)
+    for i, (attn_norm, ffn_norm, q_norm, k_norm, router) in enumerate(norms):
+        n = lambda s: f"blk.{i}.{s}.weight"  # noqa: E731
+        at = AttnWeights(q_norm, k_norm, mat(n("attn_q")), mat(n("attn_k")), mat(n("attn_v")), mat(n("attn_output")))
+        gate, up, down = (mat(n(ffn(s))) for s in ("ffn_gate", "ffn_up", "ffn_down"))
+        layers.append(LayerWeights(attn_norm, ffn_norm, at, gate, up, down, router))
+    return Weights(upload_weights(ctx, p), output, embd, out_norm, rope, layers)
+
+
+# ---- graph.rs::record, engine.rs ---------------------------------------------------------
+def record(ctx: Context, k: Kernels, w: Weights, a: Arena, c: Config, batched: bool, profile: bool = False):
+    """graph.rs:199-233: the decode step (one token) or a prefill chunk (BATCH rows, ctl[2]
+    of them live), ending in the output head over the last row."""
+    def body(r: Recorder) -> None:
+        g = Graph(r, k, a, c, batched)
+        g.embed(w.embd)
+        for l, lw in enumerate(w.layers):
+            g.layer(l, lw, w.rope)
+        src = a.x
+        if batched:
+            n = c.n_embd
+            r.dispatch(k.take_last, [-(-n // 256), 1, 1], [a.x, a.last, n, a.s_embd])
+            g.stage("take last")
+            src = a.last
+        g.rmsnorm(src, w.out_norm, a.last, 1)
+        g.stage("rmsnorm")
+        g.matvec(w.output, (a.last, 0), (a.logits, 0), False, False)
+        r.host_barrier()
+        r.mark("matvec output")
+    return ctx.record(profile, body)
+
+
+class Engine:
+    """engine.rs:12-152 over the HIP backend: weights, arena (with the KV cache), kernels,
+    and the decode and prefill recordings; step() and prefill() return the logits of the
+    last token."""
+
+    def __init__(self, ctx: Context, model: dict, c: Config, max_ctx: int,
+                 precision: KvPrecision = KvPrecision.F16_KEYS_Q8_VALUES, profile: bool = False):
+        self.ctx, self.c = ctx, c
+        self.weights = load_weights(ctx, model, c)
+        self.arena = Arena(ctx, c, max_ctx, precision)
+        self.kernels = Kernels(ctx, self.weights.buffers, self.arena.buffer, kv=self.arena.kv, c=c,
+                               precision=precision, embd_dtype=self.weights.embd.dtype)
+        self.decode = record(ctx, self.kernels, self.weights, self.arena, c, False, profile)
+        self.prefill_rec = record(ctx, self.kernels, self.weights, self.arena, c, True, profile)
+        self.pos = 0
+
+    def reset(self) -> None:
+        self.pos = 0
+
+    def load(self, tokens) -> None:
+        """engine.rs:98-124: the chunk's token ids and the control words."""
+        a = self.arena
+        if self.pos + len(tokens) > a.max_ctx:
+            raise ValueError(f"context full ({a.max_ctx} tokens)")
+        if len(tokens) > BATCH or any(int(t) >= self.c.n_vocab for t in tokens):
+            raise ValueError("token outside the vocabulary or chunk longer than BATCH")
+        u = a.u32()
+        u[a.tokens: a.tokens + len(tokens)] = np.asarray(tokens, np.uint32)
+        u[0], u[1], u[2] = int(tokens[0]), self.pos, len(tokens)
+        a.buffer.upload(0, 64 * 4)
+        a.buffer.upload(a.tokens * 4, len(tokens) * 4)
+
+    def logits(self) -> np.ndarray:
+        a = self.arena
+        a.buffer.download(a.logits * 4, self.c.n_vocab * 4)
+        return a.f32()[a.logits: a.logits + self.c.n_vocab].copy()
+
+    def step(self, token: int) -> np.ndarray:
+        """engine.rs:137-142."""
+        self.load([token])
+        self.ctx.replay(self.decode)
+        self.pos += 1
+        return self.logits()
+
+    def prefill(self, tokens) -> np.ndarray:
+        """engine.rs:144-152: BATCH-token chunks."""
+        if len(tokens) == 0:
+            raise ValueError("prefill needs at least one token")
+        for i in range(0, len(tokens), BATCH):
+            chunk = tokens[i: i + BATCH]
+            self.load(chunk)
+            self.ctx.replay(self.prefill_rec)
+            self.pos += len(chunk)
+        return self.logits()
+
+    def free(self) -> None:
+        for rec in (self.decode, self.prefill_rec):
+            rec.free()
+        for b in self.weights.buffers:
+            b.free()
+        if self.arena.kv is not None:
+            self.arena.kv.free()
+        self.arena.buffer.free()

@@ -68,3 +68,66 @@ def activations(config: str, name: str, shape) -> np.ndarray:
 
 def router(config: str, name: str, n_expert: int, n_embd: int) -> np.ndarray:
     return (rng(config, name).standard_normal(size=(n_expert, n_embd), dtype=np.float32) * np.float32(0.02))
+
+
+# ---- whole models (BASELINE.json configs 1 and 5) ---------------------------------------
+def qwen3_config(name: str):
+    """Config 1: Qwen3-0.6B (hidden 1024, 28 layers, 16 / 8 heads of 128, FFN 3072, vocab
+    151936, RoPE theta 1e6, eps 1e-6).  Config 5: Qwen3-8B (hidden 4096, 36 layers, 32 / 8
+    heads, FFN 12288).  "tiny": the same layout at test size."""
+    from .engine import Config
+    if name == "qwen3-0.6b":
+        return Config(n_embd=1024, n_ff=3072, n_head=16, n_head_kv=8, head_dim=128, n_vocab=151936, n_layer=28)
+    if name == "qwen3-8b":
+        return Config(n_embd=4096, n_ff=12288, n_head=32, n_head_kv=8, head_dim=128, n_vocab=151936, n_layer=36)
+    if name == "tiny":
+        return Config(n_embd=512, n_ff=1024, n_head=4, n_head_kv=2, head_dim=128, n_vocab=2048, n_layer=3)
+    raise ValueError(f"unknown model {name}")
+
+
+def qwen3(config: str, c, quant: str = "q8_0", norms: str = "ones") -> dict:
+    """Tensor map of a dense Qwen3 model with seeded random weights (the names of the GGUF
+    tensors, model.rs:33-60, weights.rs:58-144): name -> f32 array for norms, or
+    (dtype, n_in, n_out, raw GGUF blocks) for matrices.
+      quant "q8_0": every matrix Q8_0 and the head tied to token_embd (config 1).
+      quant "q4_k_m": token_embd and attention/gate/up Q4_K, ffn_down Q6_K in even layers and
+        Q4_K in odd ones, output head Q6_K (config 5).
+      norms "ones": f32 1.0 (config 1); "random": U[0.5, 1.5], which also exercises the
+        norm weights."""
+    def norm(name, n):
+        if norms == "ones":
+            return np.ones(n, np.float32)
+        return rng(config, name).uniform(0.5, 1.5, size=n).astype(np.float32)
+
+    def mat(name, dt, n_in, n_out):
+        return (DType(dt), n_in, n_out, matrix(config, name, dt, n_in, n_out))
+
+    q8 = quant == "q8_0"
+    base = DType.Q8_0 if q8 else DType.Q4K
+    hd = c.head_dim
+    t = {"token_embd.weight": mat("token_embd.weight", base, c.n_embd, c.n_vocab),
+         "output_norm.weight": norm("output_norm.weight", c.n_embd)}
+    if not q8:
+        t["output.weight"] = mat("output.weight", DType.Q6K, c.n_embd, c.n_vocab)
+    for i in range(c.n_layer):
+        n = lambda s: f"blk.{i}.{s}.weight"  # noqa: E731
+        down = base if q8 or i % 2 else DType.Q6K
+        t.update({
+            n("attn_norm"): norm(n("attn_norm"), c.n_embd),
+            n("ffn_norm"): norm(n("ffn_norm"), c.n_embd),
+            n("attn_q_norm"): norm(n("attn_q_norm"), hd),
+            n("attn_k_norm"): norm(n("attn_k_norm"), hd),
+            n("attn_q"): mat(n("attn_q"), base, c.n_embd, c.n_head * hd),
+            n("attn_k"): mat(n("attn_k"), base, c.n_embd, c.n_head_kv * hd),
+            n("attn_v"): mat(n("attn_v"), base, c.n_embd, c.n_head_kv * hd),
+            n("attn_output"): mat(n("attn_output"), base, c.n_head * hd, c.n_embd),
+            n("ffn_gate"): mat(n("ffn_gate"), base, c.n_embd, c.n_ff),
+            n("ffn_up"): mat(n("ffn_up"), base, c.n_embd, c.n_ff),
+            n("ffn_down"): mat(n("ffn_down"), down, c.n_ff, c.n_embd),
+        })
+    return t
+
+
+def prompt(config: str, n: int, n_vocab: int) -> list[int]:
+    """Config 1's prompt: n token ids uniform in [0, n_vocab)."""
+    return [int(v) for v in rng(config, "prompt").integers(0, n_vocab, size=n)]

@@ -135,3 +135,29 @@ def test_matvec_linearity_full_size(ctx):
     finally:
         s.free()
     assert rel_l2(outs[2], outs[0] + outs[1]) <= GUARD
+
+
+@pytest.mark.parametrize("dtype,n_in,n_out", [
+    (E.DType.Q4K, 4096, 301), (E.DType.Q4K, 12288, 4096), (E.DType.Q6K, 2304, 64),
+    (E.DType.Q6K, 12288, 4096), (E.DType.Q8_0, 1024, 70), (E.DType.Q8_0, 3072, 301),
+])
+def test_matvec_large_activations(ctx, dtype, n_in, n_out):
+    """Activations past the f16 range (silu(gate) * up reaches 1e5-1e6 in real checkpoints;
+    the reference multiplies them in f32): the kernels' staging guard rescales the passes
+    that hold them by a power of two, the others stay as they are."""
+    data = synth.matrix("test-big", f"{dtype.name}-{n_in}-{n_out}", dtype, n_in, n_out)
+    x = synth.activations("test-big", f"x-{n_in}", n_in)
+    x[: n_in // 3] *= np.float32(3e5)
+    x[n_in // 2] = np.float32(-1.5e6)
+    x[n_in - 1] = np.float32(70000.0)
+    s = Setup(ctx, [(dtype, n_in, n_out, data)], n_in, n_out)
+    try:
+        s.set_x(x)
+        s.matvec(0)
+        got = s.y(1, n_out)[0]
+    finally:
+        s.free()
+    want = so.matvec(int(dtype), data, n_in, n_out, x)
+    assert np.isfinite(got).all()
+    err = rel_l2(got, want)
+    assert err <= GUARD, err
