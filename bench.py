@@ -16,7 +16,8 @@ resident in HBM before timing starts.
 Also reported: matvec-only decode tok/s (1 / step time), the dominant kernel's roofline
 (matvec_q4k; average launch duration from HIP events on the launch stream), a measured HBM
 stream-read probe, the prefill GEMM at M = 512 (config 3) as TFLOP/s, the MoE layer of
-config 4 (decode token and 128-token prefill chunk), and the CPU oracle (restatement of
+config 4 (decode token and 128-token prefill chunk), the end-to-end Qwen3-8B Q4_K_M decode
+of config 5 at KV contexts 1024 and 16384 (tok/s), and the CPU oracle (restatement of
 skyla-ref Matrix::matvec) timed on this host over a bounded sample.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W]
@@ -284,6 +285,52 @@ def moe_layers(ctx: Context, n_layer: int = 12, n_tok: int = 128) -> dict:
     return out
 
 
+def decode_config5(ctx: Context, contexts=(1024, 16384), steps: int = 20, warmup: int = 3) -> dict:
+    """Config 5: the full Qwen3-8B Q4_K_M decode step (embedding gather, 36 layers of
+    RMSNorm, q/k/v, QK-norm + RoPE + KV write, attention over the cache, o, gate/up, SiLU,
+    down, then the output norm and the 151936-row Q6_K head), with the KV cache (f16 keys,
+    8-bit values) pre-filled with N(0,1) rows to each context length.  tok/s is end to end
+    as Engine::step runs it: control words up, one graph replay, the logits back and the
+    greedy argmax on the host.  The 36 layers hold copies of one seeded layer (two for
+    ffn_down's Q6_K / Q4_K halves), each its own HBM copy."""
+    c = synth.qwen3_config("qwen3-8b")
+    t = synth.qwen3("qwen3-8b-q4_k_m", c, "q4_k_m", "ones", shared_layers=True)
+    max_ctx = max(contexts) + warmup + steps + 8
+    eng = E.Engine(ctx, t, c, max_ctx, E.KvPrecision.F16_KEYS_Q8_VALUES)
+    try:
+        a, kvl = eng.arena, eng.arena.kv_layout
+        kv_dim = c.n_head_kv * c.head_dim
+        synth.fill_kv(kvl, a.kv.host(), max(contexts), kv_dim, "qwen3-8b-q4_k_m")
+        a.kv.upload()
+        mats = [v for k, v in t.items() if isinstance(v, tuple) and k != "token_embd.weight"]
+        weight_bytes = sum(m[2] * E.row_bytes(m[0], m[1]) for m in mats) + E.row_bytes(E.DType.Q4K, c.n_embd)
+        per_pos = c.n_layer * (kv_dim * 2 + kv_dim + kv_dim // 32 * 2)  # f16 K, i8 V, f16 V scales
+        out = {"model": "Qwen3-8B Q4_K_M (36 layers, Q6_K head and even-layer ffn_down)",
+               "kv": "f16 keys, 8-bit values", "weight_bytes_per_token": weight_bytes,
+               "launches_per_token": eng.decode.launches()}
+        for n_ctx in contexts:
+            tok = 0
+            eng.pos = n_ctx
+            for _ in range(warmup):
+                tok = int(np.argmax(eng.step(tok)))
+            eng.pos = n_ctx
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                tok = int(np.argmax(eng.step(tok)))
+            wall = (time.perf_counter() - t0) / steps
+            eng.pos = n_ctx
+            eng.load([tok])
+            dev = float(np.median([ctx.replay_timed(eng.decode) for _ in range(5)])) / 1e9
+            nbytes = weight_bytes + n_ctx * per_pos
+            out[f"ctx{n_ctx}"] = {"tok_s": round(1.0 / wall, 1), "ms_per_token": round(wall * 1e3, 3),
+                                  "device_ms_per_token": round(dev * 1e3, 3),
+                                  "kv_bytes_read": n_ctx * per_pos,
+                                  "gbs_device": round(nbytes / dev / 1e9, 1)}
+        return out
+    finally:
+        eng.free()
+
+
 def cpu_baseline(w: DecodeWorkload, budget_s: float = 15.0) -> dict:
     """skyla-ref Matrix::matvec restated in C (oracle/), timed on this host: layer passes of
     the same 7 matvecs until about budget_s seconds have elapsed."""
@@ -335,6 +382,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--no-prefill", action="store_true", help="skip the config-3 GEMM figures")
     ap.add_argument("--no-moe", action="store_true", help="skip the config-4 MoE figures")
+    ap.add_argument("--no-e2e", action="store_true", help="skip the config-5 end-to-end decode figures")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--eager", action="store_true",
                     help="replay recordings as direct launches instead of one HIP graph")
@@ -395,6 +443,9 @@ def main() -> int:
     moe = None if args.no_moe else moe_layers(ctx)
     if moe:
         log(f"MoE layer (config 4): {moe}")
+    e2e = None if args.no_e2e else decode_config5(ctx)
+    if e2e:
+        log(f"end-to-end decode (config 5): {e2e}")
     cpu = None if args.no_cpu else cpu_baseline(w, args.cpu_seconds)
     if cpu:
         log(f"cpu baseline {cpu['value']} GB/s on {cpu['cores']} threads")
@@ -440,6 +491,7 @@ def main() -> int:
         "parity_rel_l2": parity,
         "prefill_gemm_m512": prefill,
         "moe_layer_config4": moe,
+        "decode_e2e_config5": e2e,
         "cpu_baseline": cpu,
     }
     step.free()

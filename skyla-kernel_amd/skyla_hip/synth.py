@@ -85,7 +85,7 @@ def qwen3_config(name: str):
     raise ValueError(f"unknown model {name}")
 
 
-def qwen3(config: str, c, quant: str = "q8_0", norms: str = "ones") -> dict:
+def qwen3(config: str, c, quant: str = "q8_0", norms: str = "ones", shared_layers: bool = False) -> dict:
     """Tensor map of a dense Qwen3 model with seeded random weights (the names of the GGUF
     tensors, model.rs:33-60, weights.rs:58-144): name -> f32 array for norms, or
     (dtype, n_in, n_out, raw GGUF blocks) for matrices.
@@ -93,14 +93,24 @@ def qwen3(config: str, c, quant: str = "q8_0", norms: str = "ones") -> dict:
       quant "q4_k_m": token_embd and attention/gate/up Q4_K, ffn_down Q6_K in even layers and
         Q4_K in odd ones, output head Q6_K (config 5).
       norms "ones": f32 1.0 (config 1); "random": U[0.5, 1.5], which also exercises the
-        norm weights."""
+        norm weights.
+    shared_layers: every layer's matrices are the seeded ones of layer 0 (ffn_down: of layer
+      0 or 1, by its type), which the loader still lays out as a copy per layer; the bench
+      uses it to build a 5 GB model in seconds with the same HBM traffic."""
     def norm(name, n):
         if norms == "ones":
             return np.ones(n, np.float32)
         return rng(config, name).uniform(0.5, 1.5, size=n).astype(np.float32)
 
+    made = {}
+
     def mat(name, dt, n_in, n_out):
-        return (DType(dt), n_in, n_out, matrix(config, name, dt, n_in, n_out))
+        if shared_layers and name.startswith("blk."):
+            i = int(name.split(".")[1])
+            name = name.replace(f"blk.{i}.", f"blk.{i % 2 if 'ffn_down' in name else 0}.", 1)
+        if name not in made:
+            made[name] = (DType(dt), n_in, n_out, matrix(config, name, dt, n_in, n_out))
+        return made[name]
 
     q8 = quant == "q8_0"
     base = DType.Q8_0 if q8 else DType.Q4K
@@ -126,6 +136,31 @@ def qwen3(config: str, c, quant: str = "q8_0", norms: str = "ones") -> dict:
             n("ffn_down"): mat(n("ffn_down"), down, c.n_ff, c.n_embd),
         })
     return t
+
+
+def fill_kv(layout, kv_host: np.ndarray, n_pos: int, kv_dim: int, config: str) -> None:
+    """Positions [0, n_pos) of every layer's cache, in the host mirror of the KV buffer,
+    with seeded N(0,1) keys and values stored at the layout's precision (f16 rows, or 8-bit
+    rows with one f16 scale max|y| / 127 per 32 values, as the KV write kernel stores them).
+    One layer's rows are drawn and copied into every layer."""
+    g = rng(config, "kv")
+    pr = layout.precision
+    for keys, q8 in ((True, pr.keys_q8), (False, pr.values_q8)):
+        y = g.standard_normal(size=(n_pos * kv_dim // 32, 32), dtype=np.float32)
+        if q8:
+            s = (np.abs(y).max(1) / np.float32(127.0)).astype(np.float32)
+            q = np.rint(y / s[:, None]).astype(np.int8).reshape(-1)
+            sh = s.astype(np.float16)
+        else:
+            h = y.reshape(-1).astype(np.float16)
+        for l in range(len(layout.slots)):
+            off = layout.keys(l) if keys else layout.values(l)
+            if q8:
+                kv_host.view(np.int8)[off: off + q.size] = q
+                so = layout.key_scales(l) if keys else layout.value_scales(l)
+                kv_host.view("<f2")[so: so + sh.size] = sh
+            else:
+                kv_host.view("<f2")[off: off + h.size] = h
 
 
 def prompt(config: str, n: int, n_vocab: int) -> list[int]:

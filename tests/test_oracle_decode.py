@@ -139,3 +139,22 @@ def test_kv_quantize_q8_closed_forms():
     assert (np.abs(back - blocks) <= bound).all()
     # f16 rows: round to nearest even of the f16 format
     assert np.array_equal(so.kv_stored(y, False), y.astype(np.float16).astype(np.float32))
+
+
+def test_fill_kv_rows_per_layer():
+    """synth.fill_kv (the bench's N(0,1) pre-fill): every layer's first n_pos rows hold the same
+    f16 keys and 8-bit values; each 32-value block's largest quant is +-127; about N(0,1)."""
+    layout = E.KvLayout(E.KvPrecision.F16_KEYS_Q8_VALUES, [True] * 3, 96, 256)
+    host = np.zeros(layout.bytes(), np.uint8)
+    synth.fill_kv(layout, host, 64, 256, "test-fill")
+    n = 64 * 256
+    keys = [host.view("<f2")[layout.keys(l): layout.keys(l) + n].astype(np.float32) for l in range(3)]
+    vals = [host.view(np.int8)[layout.values(l): layout.values(l) + n] for l in range(3)]
+    scl = [host.view("<f2")[layout.value_scales(l): layout.value_scales(l) + n // 32] for l in range(3)]
+    assert all(np.array_equal(keys[0], k) for k in keys) and all(np.array_equal(vals[0], v) for v in vals)
+    assert np.array_equal(np.abs(vals[0].reshape(-1, 32).astype(np.int32)).max(1), np.full(n // 32, 127))
+    v = vals[0].reshape(-1, 32).astype(np.float32) * scl[0].astype(np.float32)[:, None]
+    for x in (keys[0], v.reshape(-1)):
+        assert abs(float(x.mean())) < 0.05 and abs(float(x.std()) - 1.0) < 0.05
+    # rows past n_pos stay untouched
+    assert not host.view("<f2")[layout.keys(0) + n: layout.keys(0) + 96 * 256].any()
