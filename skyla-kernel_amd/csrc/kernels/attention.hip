@@ -5,8 +5,8 @@
 // Contract (bindings, push words, grids) as the engine dispatches them:
 //   rmsnorm          [W, A, C]            6 words  grid [1, tokens, 1]
 //   qkv_prep         [W, A, C, KV, KV8]  16 words  grid [n_head + 2 n_kv, tokens, 1]
-//   attention        [A, C, KV, KV8, KVS] 11 words grid [n_kv, n_split, tokens]
-//   attention_merge  [A, C]               6 words  grid [n_head, tokens, 1]
+//   attention        [A, C, KV, KV8, KVS] 11 words grid [n_kv, n_split, tokens], 256 threads
+//   attention_merge  [A, C]               6 words  grid [n_head, tokens, 1], 1024 threads
 //   take_last        [A, C]               4 words  grid [ceil(n / 256), 1, 1]
 // W is a weight buffer (f32 tables: norm weights, RoPE frequencies), A the f32 arena and C
 // its u32 view (ctl[1] = position of the first token, ctl[2] = token count), KV the cache
@@ -120,93 +120,181 @@ SK_DEV float load_kv(const f16 *kv, const int8_t *kv8, uint32_t cache, uint32_t 
     return (float)kv8[at] * (float)kv[scales + pos * (kv_dim / 32) + kvh * 4 + d / 32];
 }
 
-// One wave per (kv head, split of CHUNK positions, token).  The N_REP query heads that share
-// the kv head are held in LDS (scaled).  Scores: lane p takes position split * CHUNK + p and
-// dots its key row with every query head.  The chunk's softmax numerators e_p = exp(s_p - m)
-// then weight the value rows, lane d owning output elements d and d + 64.  The partial
-// (m, l = sum e_p, acc = sum e_p v_p) goes to the part region for attention_merge; it is the
-// same quantity as the reference's running (m, l, acc) over the chunk (attention.comp:83-97).
+// One workgroup of four waves per (kv head, split of CHUNK positions, token); every load of
+// the split is issued up front.  Scores: thread t takes a quarter (32 dims) of the key row
+// of position t / 4 and dots it with the N_REP query heads that share the kv head (held in
+// LDS, scaled); the four quarters meet in a quad shuffle.  The chunk's softmax numerators
+// e_p = exp(s_p - m) go through LDS to the value phase, where thread t weights 8 dims
+// (8 (t % 16) ...) of the value rows of positions 4 (t / 16) ... 4 (t / 16) + 3; the 16
+// position groups are then summed in LDS.  The partial (m, l = sum e_p, acc = sum e_p v_p)
+// goes to the part region for attention_merge; it is the same quantity as the reference's
+// running (m, l, acc) over the chunk (attention.comp:83-97).  Positions past the token's
+// own are masked (e = 0) and read a live row instead, so no load leaves the cache.
 template <int N_REP, int K8, int V8>
 SK_DEV void attention_body(float *a, const uint32_t *ctl, const f16 *kv, const int8_t *kv8, const AttnPush &p) {
+  constexpr int HG = N_REP < 4 ? N_REP : 4;  // heads per value reduction round
   __shared__ float qs[N_REP][HD];
+  __shared__ float es[N_REP][CHUNK];
+  __shared__ float wm[4][N_REP], wl[4][N_REP];
+  __shared__ float4 vp[16][HG * HD / 4];
   const uint32_t kvh = blockIdx.x, split = blockIdx.y, tok = blockIdx.z;
   const uint32_t n_pos = ctl[1] + tok + 1;
   if (tok >= ctl[2] || split * CHUNK >= n_pos) return;
-  const uint32_t lane = threadIdx.x, kv_dim = p.n_kv * HD;
-  const uint32_t q_base = p.q_off + tok * p.q_stride;
+  const uint32_t t = threadIdx.x, wave = t >> 6, kv_dim = p.n_kv * HD;
+  const uint32_t begin = split * CHUNK, cnt = min(CHUNK, n_pos - begin);
+
+  // keys: position kp, dims [32 kc, 32 kc + 32)
+  const uint32_t kp = t >> 2, kc = t & 3, kpos = begin + min(kp, cnt - 1);
+  uint4 kr[4];
+  float ksc = 1.0f;
+  if constexpr (!K8) {
+    const uint4 *src = (const uint4 *)(kv + p.kc_off + kpos * kv_dim + kvh * HD + 32 * kc);
+#pragma unroll
+    for (int i = 0; i < 4; i++) kr[i] = src[i];
+  } else {
+    const uint4 *src = (const uint4 *)(kv8 + p.kc_off + kpos * kv_dim + kvh * HD + 32 * kc);
+    kr[0] = src[0];
+    kr[1] = src[1];
+    ksc = (float)kv[p.ks_off + kpos * (kv_dim / 32) + kvh * 4 + kc];  // one block per quarter
+  }
+  // values: dims [8 vg, 8 vg + 8) of positions 4 vq + [0, 4)
+  const uint32_t vg = t & 15, vq = t >> 4;
+  uint4 vr[4];
+  float vsc[4];
+#pragma unroll
+  for (int q = 0; q < 4; q++) {
+    const uint32_t vpos = begin + min(4 * vq + q, cnt - 1);
+    if constexpr (!V8) {
+      vr[q] = *(const uint4 *)(kv + p.vc_off + vpos * kv_dim + kvh * HD + 8 * vg);
+      vsc[q] = 1.0f;
+    } else {
+      const uint2 r = *(const uint2 *)(kv8 + p.vc_off + vpos * kv_dim + kvh * HD + 8 * vg);
+      vr[q] = make_uint4(r.x, r.y, 0u, 0u);
+      vsc[q] = (float)kv[p.vs_off + vpos * (kv_dim / 32) + kvh * 4 + (vg >> 2)];
+    }
+  }
+  // the query heads of this kv head, scaled
+  const uint32_t q_base = p.q_off + tok * p.q_stride + kvh * N_REP * HD;
+  for (uint32_t i = t; i < N_REP * HD; i += 256) qs[i / HD][i % HD] = a[q_base + i] * p.scale;
+  __syncthreads();
+
+  float k[32];
+  if constexpr (!K8) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const uint32_t wd[4] = {kr[i].x, kr[i].y, kr[i].z, kr[i].w};
+#pragma unroll
+      for (int h = 0; h < 4; h++) {
+        const f16x2 v = as_f16x2(wd[h]);
+        k[8 * i + 2 * h] = (float)v.x;
+        k[8 * i + 2 * h + 1] = (float)v.y;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      const uint32_t wd[4] = {kr[i].x, kr[i].y, kr[i].z, kr[i].w};
+#pragma unroll
+      for (int b = 0; b < 16; b++) k[16 * i + b] = (float)(int8_t)((wd[b >> 2] >> (8 * (b & 3))) & 255u) * ksc;
+    }
+  }
+  const bool live = kp < cnt;
+  float e[N_REP];
 #pragma unroll
   for (int j = 0; j < N_REP; j++) {
-    const uint32_t qb = q_base + (kvh * N_REP + j) * HD;
-    qs[j][lane] = a[qb + lane] * p.scale;
-    qs[j][lane + 64] = a[qb + lane + 64] * p.scale;
+    const float4 *qv = (const float4 *)&qs[j][32 * kc];
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const float4 qq = qv[i];
+      s = __builtin_fmaf(qq.x, k[4 * i], s);
+      s = __builtin_fmaf(qq.y, k[4 * i + 1], s);
+      s = __builtin_fmaf(qq.z, k[4 * i + 2], s);
+      s = __builtin_fmaf(qq.w, k[4 * i + 3], s);
+    }
+    s += __shfl_xor(s, 1, 64);
+    s += __shfl_xor(s, 2, 64);
+    e[j] = live ? s : -INFINITY;
+    const float m = wave_max(e[j]);
+    if ((t & 63) == 0) wm[wave][j] = m;
   }
   __syncthreads();
-  const uint32_t begin = split * CHUNK, cnt = min(CHUNK, n_pos - begin);
-  const bool live = lane < cnt;
-  const uint32_t pos = begin + (live ? lane : 0);
-  float s[N_REP];
-#pragma unroll
-  for (int j = 0; j < N_REP; j++) s[j] = 0.0f;
-  for (uint32_t d0 = 0; d0 < HD; d0 += 8) {
-    float k[8];
-    if constexpr (!K8) {
-      const uint4 raw = *(const uint4 *)(kv + p.kc_off + pos * kv_dim + kvh * HD + d0);
-      const uint32_t wd[4] = {raw.x, raw.y, raw.z, raw.w};
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const f16x2 h = as_f16x2(wd[i]);
-        k[2 * i] = (float)h.x;
-        k[2 * i + 1] = (float)h.y;
-      }
-    } else {
-      const uint2 raw = *(const uint2 *)(kv8 + p.kc_off + pos * kv_dim + kvh * HD + d0);
-      const float sc = (float)kv[p.ks_off + pos * (kv_dim / 32) + kvh * 4 + d0 / 32];
-      const uint32_t wd[2] = {raw.x, raw.y};
-#pragma unroll
-      for (int i = 0; i < 8; i++) k[i] = (float)(int8_t)((wd[i >> 2] >> (8 * (i & 3))) & 255u) * sc;
-    }
-#pragma unroll
-    for (int j = 0; j < N_REP; j++)
-#pragma unroll
-      for (int i = 0; i < 8; i++) s[j] = __builtin_fmaf(qs[j][d0 + i], k[i], s[j]);
-  }
-  float e[N_REP], m[N_REP], l[N_REP];
+  float mx[N_REP];
 #pragma unroll
   for (int j = 0; j < N_REP; j++) {
-    m[j] = wave_max(live ? s[j] : -INFINITY);
-    e[j] = live ? expf(s[j] - m[j]) : 0.0f;
-    l[j] = wave_sum(e[j]);
+    mx[j] = fmaxf(fmaxf(wm[0][j], wm[1][j]), fmaxf(wm[2][j], wm[3][j]));
+    e[j] = live ? expf(e[j] - mx[j]) : 0.0f;
+    if (kc == 0) es[j][kp] = e[j];
+    const float l = wave_sum(kc == 0 ? e[j] : 0.0f);
+    if ((t & 63) == 0) wl[wave][j] = l;
   }
-  float acc0[N_REP], acc1[N_REP];
+  __syncthreads();
+
+  float v[4][8];
 #pragma unroll
-  for (int j = 0; j < N_REP; j++) acc0[j] = acc1[j] = 0.0f;
-  for (uint32_t q = 0; q < cnt; q++) {
-    const float v0 = load_kv<V8>(kv, kv8, p.vc_off, p.vs_off, kv_dim, begin + q, kvh, lane);
-    const float v1 = load_kv<V8>(kv, kv8, p.vc_off, p.vs_off, kv_dim, begin + q, kvh, lane + 64);
+  for (int q = 0; q < 4; q++) {
+    if constexpr (!V8) {
+      const uint32_t wd[4] = {vr[q].x, vr[q].y, vr[q].z, vr[q].w};
 #pragma unroll
-    for (int j = 0; j < N_REP; j++) {
-      const float ep = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, e[j]), (int)q));
-      acc0[j] = __builtin_fmaf(ep, v0, acc0[j]);
-      acc1[j] = __builtin_fmaf(ep, v1, acc1[j]);
+      for (int h = 0; h < 4; h++) {
+        const f16x2 x = as_f16x2(wd[h]);
+        v[q][2 * h] = (float)x.x;
+        v[q][2 * h + 1] = (float)x.y;
+      }
+    } else {
+      const uint32_t wd[2] = {vr[q].x, vr[q].y};
+#pragma unroll
+      for (int b = 0; b < 8; b++) v[q][b] = (float)(int8_t)((wd[b >> 2] >> (8 * (b & 3))) & 255u) * vsc[q];
     }
   }
   const uint32_t part_base = p.part_off + tok * p.part_stride;
 #pragma unroll
-  for (int j = 0; j < N_REP; j++) {
-    const uint32_t base = part_base + ((kvh * N_REP + j) * p.n_split + split) * PART;
-    if (lane == 0) {
-      a[base] = m[j];
-      a[base + 1] = l[j];
+  for (int h0 = 0; h0 < N_REP; h0 += HG) {
+    if (h0 != 0) __syncthreads();  // the previous round's sums are read
+#pragma unroll
+    for (int j = 0; j < HG; j++) {
+      float acc[8];
+#pragma unroll
+      for (int i = 0; i < 8; i++) acc[i] = 0.0f;
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const float ep = es[h0 + j][4 * vq + q];
+#pragma unroll
+        for (int i = 0; i < 8; i++) acc[i] = __builtin_fmaf(ep, v[q][i], acc[i]);
+      }
+      vp[vq][(j * HD + 8 * vg) / 4] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+      vp[vq][(j * HD + 8 * vg) / 4 + 1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
     }
-    a[base + 2 + lane] = acc0[j];
-    a[base + 2 + lane + 64] = acc1[j];
+    __syncthreads();
+    for (uint32_t o = t; o < HG * HD; o += 256) {
+      float sum = 0.0f;
+#pragma unroll
+      for (int g = 0; g < 16; g++) sum += ((const float *)vp[g])[o];
+      const uint32_t j = h0 + o / HD;
+      a[part_base + ((kvh * N_REP + j) * p.n_split + split) * PART + 2 + o % HD] = sum;
+    }
+  }
+  if (t < N_REP) {
+    const uint32_t base = part_base + ((kvh * N_REP + t) * p.n_split + split) * PART;
+    float l = 0.0f, m = 0.0f;
+#pragma unroll
+    for (int j = 0; j < N_REP; j++)
+      if ((uint32_t)j == t) {
+        m = mx[j];
+        l = ((wl[0][j] + wl[1][j]) + wl[2][j]) + wl[3][j];
+      }
+    a[base] = m;
+    a[base + 1] = l;
   }
 }
 
 }  // namespace
 
 // rmsnorm (rmsnorm.comp; ops.rs:1-16): y = x * r * w, r = 1 / sqrt(mean(x^2) + eps), per
-// token below ctl[2].  256 threads; partial sums of squares per wave, added in wave order.
+// token below ctl[2].  256 threads; rows of at most 4096 floats at 16-byte aligned offsets
+// (every arena row and norm table) are read once as float4, all loads in flight together,
+// and kept in registers for the scaling; other rows take a plain loop.  Partial sums of
+// squares per wave, added in wave order.
 extern "C" __global__ __launch_bounds__(256) void rmsnorm(const float *w, float *a, const uint32_t *ctl,
                                                            NormPush p) {
 #pragma clang fp contract(off)
@@ -214,6 +302,35 @@ extern "C" __global__ __launch_bounds__(256) void rmsnorm(const float *w, float 
   const uint32_t tok = blockIdx.y, t = threadIdx.x;
   if (tok >= ctl[2]) return;
   const uint32_t x = p.x_off + tok * p.stride, y = p.y_off + tok * p.stride;
+  if (((x | y | p.w_off | p.n) & 3u) == 0 && p.n <= 4096) {
+    const uint32_t n4 = p.n >> 2;
+    float4 xv[4], wv[4];
+    float ss = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const uint32_t i = t + 256 * k;
+      xv[k] = wv[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (i < n4) {
+        xv[k] = ((const float4 *)(a + x))[i];
+        wv[k] = ((const float4 *)(w + p.w_off))[i];
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 4; k++) ss += ((xv[k].x * xv[k].x + xv[k].y * xv[k].y) + xv[k].z * xv[k].z) + xv[k].w * xv[k].w;
+    ss = wave_sum(ss);
+    if ((t & 63) == 0) part[t >> 6] = ss;
+    __syncthreads();
+    const float total = ((part[0] + part[1]) + part[2]) + part[3];
+    const float r = 1.0f / sqrtf(total / (float)p.n + p.eps);
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const uint32_t i = t + 256 * k;
+      if (i < n4)
+        ((float4 *)(a + y))[i] = make_float4(xv[k].x * r * wv[k].x, xv[k].y * r * wv[k].y, xv[k].z * r * wv[k].z,
+                                             xv[k].w * r * wv[k].w);
+    }
+    return;
+  }
   float ss = 0.0f;
   for (uint32_t i = t; i < p.n; i += 256) {
     const float v = a[x + i];
@@ -241,7 +358,7 @@ QKV(1, 1)
 
 // attention (attention.comp): spec [N_REP, CHUNK, K_Q8, V_Q8, head_dim, q_head].
 #define ATTN(R, K8, V8)                                                                          \
-  extern "C" __global__ __launch_bounds__(64) void attention__##R##_64_##K8##_##V8##_128_128(    \
+  extern "C" __global__ __launch_bounds__(256) void attention__##R##_64_##K8##_##V8##_128_128(   \
       float *a, const uint32_t *ctl, const f16 *kv, const int8_t *kv8, const f16 *kvs, AttnPush p) { \
     (void)kvs;                                                                                   \
     attention_body<R, K8, V8>(a, ctl, kv, kv8, p);                                               \
@@ -252,24 +369,58 @@ ATTN_REP(0, 1)
 ATTN_REP(1, 1)
 
 // attention_merge (attention_merge.comp): o = sum_s w_s acc_s / sum_s w_s l_s with
-// w_s = exp(m_s - max m) over the splits that hold positions, in split order.  Spec
-// [head_dim, gated] = [128, 0].
-extern "C" __global__ __launch_bounds__(128) void attention_merge__128_0(float *a, const uint32_t *ctl,
-                                                                          MergePush p) {
-  const uint32_t h = blockIdx.x, tok = blockIdx.y, t = threadIdx.x;
+// w_s = exp(m_s - max m) over the splits that hold positions.  Spec [head_dim, gated] =
+// [128, 0].  One workgroup of 1024 threads per (head, token): the weights go to LDS, then
+// thread t sums dims 2 (t % 64) + {0, 1} over the splits s = t / 64 (mod 16), every split's
+// load in flight at once, and the 16 groups are added in LDS.
+constexpr uint32_t MAX_SPLITS = 4096;  // 262144 positions; the engine's arena stays below
+
+extern "C" __global__ __launch_bounds__(1024) void attention_merge__128_0(float *a, const uint32_t *ctl,
+                                                                           MergePush p) {
+  __shared__ float wts[MAX_SPLITS];
+  __shared__ float red[16];
+  __shared__ float2 sums[16][HD / 2];
+  const uint32_t h = blockIdx.x, tok = blockIdx.y, t = threadIdx.x, wave = t >> 6;
   if (tok >= ctl[2]) return;
-  const uint32_t used = (ctl[1] + tok + p.chunk) / p.chunk;
+  const uint32_t used = min(min((ctl[1] + tok + p.chunk) / p.chunk, p.n_split), MAX_SPLITS);
   const uint32_t first = p.part_off + tok * p.part_stride + h * p.n_split * PART;
-  float big = -1e30f;
-  for (uint32_t s = 0; s < used; s++) big = fmaxf(big, a[first + s * PART]);
-  float total = 0.0f, o = 0.0f;
-  for (uint32_t s = 0; s < used; s++) {
-    const uint32_t base = first + s * PART;
-    const float wgt = expf(a[base] - big);
-    total += wgt * a[base + 1];
-    o += wgt * a[base + 2 + t];
+  float big = -INFINITY;
+  for (uint32_t s = t; s < used; s += 1024) big = fmaxf(big, a[first + s * PART]);
+  big = wave_max(big);
+  if ((t & 63) == 0) red[wave] = big;
+  __syncthreads();
+  big = red[0];
+#pragma unroll
+  for (int w = 1; w < 16; w++) big = fmaxf(big, red[w]);
+  __syncthreads();  // red is reused
+  float total = 0.0f;
+  for (uint32_t s = t; s < used; s += 1024) {
+    const float wgt = expf(a[first + s * PART] - big);
+    wts[s] = wgt;
+    total = __builtin_fmaf(wgt, a[first + s * PART + 1], total);
   }
-  a[p.o_off + tok * p.o_stride + h * HD + t] = o / total;
+  total = wave_sum(total);
+  if ((t & 63) == 0) red[wave] = total;
+  __syncthreads();
+  total = 0.0f;
+#pragma unroll
+  for (int w = 0; w < 16; w++) total += red[w];
+  const uint32_t dp = t & 63;
+  float2 acc = make_float2(0.0f, 0.0f);
+#pragma unroll 8
+  for (uint32_t s = wave; s < used; s += 16) {
+    const float2 v = *(const float2 *)(a + first + s * PART + 2 + 2 * dp);
+    acc.x = __builtin_fmaf(wts[s], v.x, acc.x);
+    acc.y = __builtin_fmaf(wts[s], v.y, acc.y);
+  }
+  sums[wave][dp] = acc;
+  __syncthreads();
+  if (t < HD) {
+    float o = 0.0f;
+#pragma unroll
+    for (int g = 0; g < 16; g++) o += ((const float *)sums[g])[t];
+    a[p.o_off + tok * p.o_stride + h * HD + t] = o / total;
+  }
 }
 
 // take_last (take_last.comp): the last token row of a chunk, for the output head.

@@ -30,6 +30,7 @@ EXPERT_LPR = (64, 32, 16)
 
 # arena.rs:6-7
 ATTENTION_CHUNK = 64
+MAX_SPLITS = 4096       # splits the attention merge weighs in LDS (kernels/attention.hip)
 BATCH = 128
 
 
@@ -381,6 +382,8 @@ class Arena:
     def __init__(self, ctx: Context, c: Config, max_ctx: int = 64, precision: KvPrecision | None = None):
         self.size = 64
         n_split = -(-max_ctx // ATTENTION_CHUNK)
+        if n_split > MAX_SPLITS:
+            raise ValueError(f"max_ctx {max_ctx} above {MAX_SPLITS * ATTENTION_CHUNK} positions (the merge's split table)")
 
         def batched(width):
             stride = _next64(width)

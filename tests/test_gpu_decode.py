@@ -62,12 +62,16 @@ class Bench:
         self.a.buffer.free()
 
 
-def _cfg():
-    return E.Config(n_embd=512, n_ff=1024, n_head=4, n_head_kv=2, head_dim=128, n_vocab=16, n_layer=2)
+def _cfg(n_embd=512, n_head=4, n_head_kv=2):
+    return E.Config(n_embd=n_embd, n_ff=1024, n_head=n_head, n_head_kv=n_head_kv, head_dim=128, n_vocab=16,
+                    n_layer=2)
 
 
-def test_rmsnorm_matches_oracle(ctx):
-    c = _cfg()
+@pytest.mark.parametrize("n_embd", [512, 1056, 8192])
+def test_rmsnorm_matches_oracle(ctx, n_embd):
+    """Rows of 512 and 1056 (the float4 path, full and ragged) and 8192 (above the
+    registers' 4096) against ops.rs rmsnorm."""
+    c = _cfg(n_embd)
     g = np.random.default_rng(1)
     w = g.uniform(0.5, 1.5, c.n_embd).astype(np.float32)
     b = Bench(ctx, c, P.F16, {"w": w})
@@ -155,14 +159,16 @@ def test_qkv_prep_matches_oracle(ctx, precision):
 
 
 @pytest.mark.parametrize("precision", list(P))
-@pytest.mark.parametrize("n_pos", [1, 64, 65, 190])
-def test_attention_matches_oracle(ctx, precision, n_pos):
+@pytest.mark.parametrize("n_pos", [1, 5, 64, 65, 190, 4100])
+@pytest.mark.parametrize("heads", [(4, 2), (4, 4), (8, 2), (8, 1)])
+def test_attention_matches_oracle(ctx, precision, n_pos, heads):
     """Split-K attention + merge over positions [0, ctl[1] + t] for two tokens, against the
     oracle's attention over the same (dequantised) cache entries; 190 positions span three
-    splits, 64 / 65 the split boundary."""
-    c = _cfg()
+    splits, 64 / 65 the split boundary, 4100 sixty-five splits (more than the merge's 16
+    split groups); 1, 2, 4 and 8 query heads per kv head."""
+    c = _cfg(512, *heads)
     g = np.random.default_rng(3 + n_pos)
-    b = Bench(ctx, c, precision, {"one": np.ones(128, np.float32)})
+    b = Bench(ctx, c, precision, {"one": np.ones(128, np.float32)}, max_ctx=max(256, n_pos))
     try:
         a, kvl, kv_dim = b.a, b.a.kv_layout, c.n_head_kv * 128
         K = (g.standard_normal((n_pos, kv_dim)) * 2).astype(np.float32)
@@ -189,7 +195,9 @@ def test_attention_matches_oracle(ctx, precision, n_pos):
         for t in range(n_tok):
             m = n_pos - n_tok + t + 1
             want = so.attention(q[t], Kd[:m].reshape(-1), Vd[:m].reshape(-1), m, c.n_head, c.n_head_kv, 128)
-            assert rel_l2(got[t], want) < 2e-6, (t, m)
+            # both sides round each of m terms in f32: the oracle sequentially, the kernel
+            # in split partials, so the allowance grows like sqrt(m) past a few hundred
+            assert rel_l2(got[t], want) < 1e-6 * max(2.0, np.sqrt(m) / 16), (t, m)
     finally:
         b.free()
 
