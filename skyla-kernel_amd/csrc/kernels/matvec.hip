@@ -37,6 +37,17 @@ struct MatvecPush4 {  // Q6_K (11 words, graph.rs:29 / graph/moe.rs:252)
   uint32_t o0, o1, o2, o3, x_off, y_off, n_in, n_out, ids_off, x_stride, y_stride;
 };
 
+// The fused forms (matvec_*_silu, matvec_*_norm) append two words: the offset of the
+// second activation vector (the up rows, or the RMSNorm weights) and the norm's eps.
+struct MatvecPush2F {
+  uint32_t o0, o1, x_off, y_off, n_in, n_out, ids_off, x_stride, y_stride, aux_off;
+  float eps;
+};
+struct MatvecPush4F {
+  uint32_t o0, o1, o2, o3, x_off, y_off, n_in, n_out, ids_off, x_stride, y_stride, aux_off;
+  float eps;
+};
+
 // (a & m) | o as one v_and_or_b32 with register operands (the compiler otherwise splits it
 // in two, because gfx9 VOP3 encodings take no literal).
 SK_DEV uint32_t and_or(uint32_t a, uint32_t m, uint32_t o) {
@@ -115,6 +126,52 @@ SK_DEV void scale_rows(float (&acc)[ROWS], int e) {
   for (int r = 0; r < ROWS; r++) acc[r] = __builtin_ldexpf(acc[r], e);
 }
 
+// Fused activation forms.  MODE 1 (SiLU; silu_mul.comp:15-23) stages x / (1 + e^-x) * aux:
+// the down projection reads the gate and up rows itself.  MODE 2 (RMSNorm; rmsnorm.comp,
+// ops.rs:1-16) stages x * aux (the norm weights) and adds x^2 to ss; the row's
+// r = 1 / sqrt(sum / n_in + eps) multiplies the sums before they are stored, since every
+// output is linear in the staged vector.  Every workgroup reads the whole x anyway, so each
+// computes the same sum of squares itself (in the same order) and no separate launch runs.
+template <int MODE>
+SK_DEV float4 fuse4(float4 v, float4 aux, float &ss) {
+#pragma clang fp contract(off)
+  if constexpr (MODE == 1) {
+    v.x = v.x / (1.0f + expf(-v.x)) * aux.x;
+    v.y = v.y / (1.0f + expf(-v.y)) * aux.y;
+    v.z = v.z / (1.0f + expf(-v.z)) * aux.z;
+    v.w = v.w / (1.0f + expf(-v.w)) * aux.w;
+  } else if constexpr (MODE == 2) {
+    ss += ((v.x * v.x + v.y * v.y) + v.z * v.z) + v.w * v.w;
+    v = make_float4(v.x * aux.x, v.y * aux.y, v.z * aux.z, v.w * aux.w);
+  }
+  return v;
+}
+
+// MODE 2: the pass's sums of squares, one per 16 lanes, into wss before the staging
+// barrier; after it every thread adds all of them in the same order.
+template <int MODE, int WAVES>
+SK_DEV void norm_note(float *wss, float ssp) {
+  if constexpr (MODE == 2) {
+    const float v = lane_sum<16>(ssp);
+    if ((threadIdx.x & 15) == 0) wss[threadIdx.x >> 4] = v;
+  }
+}
+template <int MODE, int WAVES>
+SK_DEV void norm_take(const float *wss, float &ss) {
+  if constexpr (MODE == 2) {
+#pragma unroll
+    for (int i = 0; i < 4 * WAVES; i++) ss += wss[i];
+  }
+}
+template <int MODE, int ROWS, typename P>
+SK_DEV void norm_apply(float (&acc)[ROWS], float ss, const P &p) {
+  if constexpr (MODE == 2) {
+    const float r = 1.0f / sqrtf(ss / (float)p.n_in + p.eps);
+#pragma unroll
+    for (int i = 0; i < ROWS; i++) acc[i] *= r;
+  }
+}
+
 // Geometry shared by the three formats.
 template <int WAVES, int ROWS, int LPR>
 struct Geo {
@@ -159,15 +216,16 @@ struct GeoQ4 {
   static_assert(CHU % LPR == 0, "a full pass gives every lane the same number of steps");
 };
 
-template <int WAVES, int ACCUM, int ROWS, int MOE, int LPR>
+template <int WAVES, int ACCUM, int ROWS, int MOE, int LPR, int MODE = 0, typename P = MatvecPush2>
 SK_DEV void matvec_q4k_body(const uint4 *__restrict__ w, const float *x, float *y,
-                            const uint32_t *ids, const MatvecPush2 &p, uint32_t bx) {
+                            const uint32_t *ids, const P &p, uint32_t bx) {
   using G = GeoQ4<WAVES, ROWS, LPR>;
   constexpr int CHU = G::CHU, PF = G::PF;
   __shared__ uint4 xq[4][CHU];  // component-major: lanes read consecutive 16 B
   __shared__ float2 xs[CHU];
   __shared__ float4 sc[G::RWG][G::CH_SUP][4];
   __shared__ uint32_t wmax[WAVES];
+  __shared__ float wss[MODE == 2 ? 4 * WAVES : 1];
 
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = (tid & 63) % LPR;
@@ -178,6 +236,9 @@ SK_DEV void matvec_q4k_body(const uint4 *__restrict__ w, const float *x, float *
   const uint32_t slot = blockIdx.y;
   const uint32_t base = MOE ? ids[p.ids_off + slot] * p.n_out : 0;
   const float *xv = x + p.x_off + slot * p.x_stride;
+  const float *av = x;  // MODE != 0: the second vector, indexed as xv
+  if constexpr (MODE != 0) av = x + p.aux_off + (MODE == 1 ? slot * p.x_stride : 0);
+  float ss = 0.0f;      // MODE 2: sum of x^2 over the passes so far
   const uint32_t y_off = p.y_off + slot * p.y_stride;
   const uint32_t units = p.n_in >> 5, supers = p.n_in >> 8;
   const uint32_t c = (lane >> 1) & 3;  // chunk of this lane's units (u % 8 == lane % 8)
@@ -200,16 +261,21 @@ SK_DEV void matvec_q4k_body(const uint4 *__restrict__ w, const float *x, float *
     // Load order matters (a wave's loads complete in issue order): activations, then
     // headers, then the first PF weight steps, so staging waits only for its own data.
     constexpr int XI = (4 * CHU + G::NT - 1) / G::NT;  // activation quarters per thread
-    float4 xa[XI][2];
+    float4 xa[XI][2], xu[MODE ? XI : 1][2];
     auto load_x = [&]() {
 #pragma unroll
       for (int j = 0; j < XI; j++) {
         const uint32_t t = tid + j * G::NT, u = u0 + (t >> 2), qq = t & 3;
         xa[j][0] = xa[j][1] = make_float4(0.f, 0.f, 0.f, 0.f);  // every path defines them
+        if constexpr (MODE != 0) xu[j][0] = xu[j][1] = make_float4(0.f, 0.f, 0.f, 0.f);
         if (t < 4 * nu) {
-          const float *xp = xv + (u >> 3) * 256 + ((u >> 1) & 3) * 64 + (u & 1) * 16 + (qq >> 1) * 32 + (qq & 1) * 8;
-          xa[j][0] = *(const float4 *)xp;
-          xa[j][1] = *(const float4 *)(xp + 4);
+          const uint32_t at = (u >> 3) * 256 + ((u >> 1) & 3) * 64 + (u & 1) * 16 + (qq >> 1) * 32 + (qq & 1) * 8;
+          xa[j][0] = *(const float4 *)(xv + at);
+          xa[j][1] = *(const float4 *)(xv + at + 4);
+          if constexpr (MODE != 0) {
+            xu[j][0] = *(const float4 *)(av + at);
+            xu[j][1] = *(const float4 *)(av + at + 4);
+          }
         }
       }
     };
@@ -229,12 +295,19 @@ SK_DEV void matvec_q4k_body(const uint4 *__restrict__ w, const float *x, float *
 
     // stage: item t = quarter t%4 of unit t/4 (values 0-7, 8-15 of the low-nibble half,
     // then of the high half); the pair sums of quarters make the unit's two 16-value sums
+    float ssp = 0.0f;  // MODE 2: this pass's sum of x^2 (first staging only)
     auto stage_x = [&](float scale) -> float {
       float big = 0.0f;  // largest |x| staged
 #pragma unroll
       for (int j = 0; j < XI; j++) {
         const uint32_t t = tid + j * G::NT, u = t >> 2, qq = t & 3;
         float4 a = xa[j][0], b = xa[j][1];
+        if constexpr (MODE != 0) {
+          float sq = 0.0f;
+          a = fuse4<MODE>(a, xu[j][0], sq);
+          b = fuse4<MODE>(b, xu[j][1], sq);
+          if (scale == 1.0f) ssp += sq;
+        }
         big = fmaxf(big, fmaxf(abs_max4(a), abs_max4(b)));
         if (scale != 1.0f) {
           a = make_float4(a.x * scale, a.y * scale, a.z * scale, a.w * scale);
@@ -255,6 +328,7 @@ SK_DEV void matvec_q4k_body(const uint4 *__restrict__ w, const float *x, float *
       return big;
     };
     guard_note(wmax, stage_x(1.0f));
+    norm_note<MODE, WAVES>(wss, ssp);
     // decode: the 8 six-bit scales and mins as bytes of four words (quant.rs:40-49)
 #pragma unroll
     for (int j = 0; j < HI_T; j++) {
@@ -279,6 +353,7 @@ SK_DEV void matvec_q4k_body(const uint4 *__restrict__ w, const float *x, float *
       }
     }
     __syncthreads();
+    norm_take<MODE, WAVES>(wss, ss);
     const int e = guard_exp<WAVES>(wmax);
     if (e) {  // rare: the pass again at x * 2^-e
       load_x();
@@ -329,6 +404,7 @@ SK_DEV void matvec_q4k_body(const uint4 *__restrict__ w, const float *x, float *
       if (j0 + j < S) step(j0 + j, q[j]);
     if (e) scale_rows(acc, e);
   }
+  norm_apply<MODE>(acc, ss, p);
   store_rows<ACCUM, ROWS, LPR>(y, y_off, first, p.n_out, lane, acc);
 }
 
@@ -341,15 +417,16 @@ SK_DEV void matvec_q4k_body(const uint4 *__restrict__ w, const float *x, float *
 // LDS per pass: xq[unit] = 32 f16 pairs (4 groups x 8), xs[unit] = the 4 group sums, and per
 // (row, super-block) and (hf, li): d*sc for the lane's 4 groups (1/16 folded into g = 2, 3).
 // ---------------------------------------------------------------------------------------
-template <int WAVES, int ACCUM, int ROWS, int MOE, int LPR>
+template <int WAVES, int ACCUM, int ROWS, int MOE, int LPR, int MODE = 0, typename P = MatvecPush4>
 SK_DEV void matvec_q6k_body(const uint4 *__restrict__ w, const uint16_t *__restrict__ wd,
-                            const float *x, float *y, const uint32_t *ids, const MatvecPush4 &p,
+                            const float *x, float *y, const uint32_t *ids, const P &p,
                             uint32_t bx) {
   using G = Geo<WAVES, ROWS, LPR>;
   __shared__ uint4 xq[8][G::CH / 64];  // component-major
   __shared__ float4 xs[G::CH / 64];
   __shared__ float4 sc[G::RWG][G::CH_SUP][4];
   __shared__ uint32_t wmax[WAVES];
+  __shared__ float wss[MODE == 2 ? 4 * WAVES : 1];
 
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = (tid & 63) % LPR;
@@ -360,6 +437,9 @@ SK_DEV void matvec_q6k_body(const uint4 *__restrict__ w, const uint16_t *__restr
   const uint32_t slot = blockIdx.y;
   const uint32_t base = MOE ? ids[p.ids_off + slot] * p.n_out : 0;
   const float *xv = x + p.x_off + slot * p.x_stride;
+  const float *av = x;  // MODE != 0: the second vector, indexed as xv
+  if constexpr (MODE != 0) av = x + p.aux_off + (MODE == 1 ? slot * p.x_stride : 0);
+  float ss = 0.0f;
   const uint32_t y_off = p.y_off + slot * p.y_stride;
   const uint32_t supers = p.n_in >> 8;
   const uint32_t li = lane & 1, hf = (lane >> 1) & 1;
@@ -392,23 +472,30 @@ SK_DEV void matvec_q6k_body(const uint4 *__restrict__ w, const uint16_t *__restr
     // activation item t = group t%4 of unit t/4: 16 values (4 x 16 B) that become 8 f16
     // pairs and one 16-value sum (16 VGPRs in flight per item, not a whole unit's 64)
     const uint32_t n_xi = 4 * nu;
+    float4 xu4[MODE ? 4 : 1];
     auto x_item = [&](uint32_t t, float4 (&v)[4]) {
       const uint32_t u = u0 + (t >> 2), g = t & 3;
-      const float *xp = xv + (u >> 2) * 256 + ((u >> 1) & 1) * 128 + (u & 1) * 16 + 32 * g;
+      const uint32_t at = (u >> 2) * 256 + ((u >> 1) & 1) * 128 + (u & 1) * 16 + 32 * g;
 #pragma unroll
-      for (int k = 0; k < 4; k++) v[k] = *(const float4 *)(xp + 4 * k);
+      for (int k = 0; k < 4; k++) v[k] = *(const float4 *)(xv + at + 4 * k);
+      if constexpr (MODE != 0) {
+#pragma unroll
+        for (int k = 0; k < 4; k++) xu4[k] = *(const float4 *)(av + at + 4 * k);
+      }
     };
     float big = 0.0f;  // largest |x| this thread staged
+    float ssp = 0.0f;  // MODE 2: this pass's sum of x^2 (first staging only)
     auto x_store = [&](uint32_t t, const float4 (&v)[4], float scale) {
       const uint32_t i = t >> 2, g = t & 3;
       const f16x2 one = {(f16)1.0f, (f16)1.0f};
       uint32_t pp[8];
-      float s = 0.0f;
+      float s = 0.0f, sq = 0.0f;
 #pragma unroll
       for (int k = 0; k < 4; k++) {
-        big = fmaxf(big, abs_max4(v[k]));
-        const float4 e = scale != 1.0f ? make_float4(v[k].x * scale, v[k].y * scale, v[k].z * scale, v[k].w * scale)
-                                       : v[k];
+        float4 f = v[k];
+        if constexpr (MODE != 0) f = fuse4<MODE>(f, xu4[k], sq);
+        big = fmaxf(big, abs_max4(f));
+        const float4 e = scale != 1.0f ? make_float4(f.x * scale, f.y * scale, f.z * scale, f.w * scale) : f;
         pp[2 * k] = pk(e.x, e.z);
         pp[2 * k + 1] = pk(e.y, e.w);
         s = dot2(as_f16x2(pp[2 * k]), one, s);
@@ -417,6 +504,7 @@ SK_DEV void matvec_q6k_body(const uint4 *__restrict__ w, const uint16_t *__restr
       xq[2 * g][i] = make_uint4(pp[0], pp[1], pp[2], pp[3]);
       xq[2 * g + 1][i] = make_uint4(pp[4], pp[5], pp[6], pp[7]);
       ((float *)&xs[i])[g] = s;
+      if (scale == 1.0f) ssp += sq;
     };
     const uint32_t n_items = (uint32_t)G::RWG * ns;
     auto h_load = [&](uint32_t i, uint4 &sv, uint32_t &dv) {
@@ -460,7 +548,9 @@ SK_DEV void matvec_q6k_body(const uint4 *__restrict__ w, const uint16_t *__restr
       h_store(i, sv0, dv0);
     }
     guard_note(wmax, big);
+    norm_note<MODE, WAVES>(wss, ssp);
     __syncthreads();
+    norm_take<MODE, WAVES>(wss, ss);
     const int e = guard_exp<WAVES>(wmax);
     if (e) {  // rare: the pass again at x * 2^-e
       for (uint32_t t = tid; t < n_xi; t += G::NT) {
@@ -516,6 +606,7 @@ SK_DEV void matvec_q6k_body(const uint4 *__restrict__ w, const uint16_t *__restr
     }
     if (e) scale_rows(acc, e);
   }
+  norm_apply<MODE>(acc, ss, p);
   store_rows<ACCUM, ROWS, LPR>(y, y_off, first, p.n_out, lane, acc);
 }
 
@@ -524,9 +615,9 @@ SK_DEV void matvec_q6k_body(const uint4 *__restrict__ w, const uint16_t *__restr
 // (row, block) as f32.  q as f16: (q ^ 0x80) is 0..255, so MAGIC | that = 1152 + q.
 // LDS per pass: xq[unit] = 8 f16 pairs, xs[unit] = their sum, dd[row][block] = d.
 // ---------------------------------------------------------------------------------------
-template <int WAVES, int ACCUM, int ROWS, int MOE, int LPR>
+template <int WAVES, int ACCUM, int ROWS, int MOE, int LPR, int MODE = 0, typename P = MatvecPush2>
 SK_DEV void matvec_q8_0_body(const uint4 *__restrict__ w, const uint16_t *__restrict__ wd,
-                             const float *x, float *y, const uint32_t *ids, const MatvecPush2 &p,
+                             const float *x, float *y, const uint32_t *ids, const P &p,
                              uint32_t bx) {
   using G = Geo<WAVES, ROWS, LPR>;
   constexpr int NBLK = G::CH / 32;
@@ -534,6 +625,7 @@ SK_DEV void matvec_q8_0_body(const uint4 *__restrict__ w, const uint16_t *__rest
   __shared__ float xs[G::CH / 16];
   __shared__ float dd[G::RWG][NBLK];
   __shared__ uint32_t wmax[WAVES];
+  __shared__ float wss[MODE == 2 ? 4 * WAVES : 1];
 
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = (tid & 63) % LPR;
@@ -544,6 +636,9 @@ SK_DEV void matvec_q8_0_body(const uint4 *__restrict__ w, const uint16_t *__rest
   const uint32_t slot = blockIdx.y;
   const uint32_t base = MOE ? ids[p.ids_off + slot] * p.n_out : 0;
   const float *xv = x + p.x_off + slot * p.x_stride;
+  const float *av = x;  // MODE != 0: the second vector, indexed as xv
+  if constexpr (MODE != 0) av = x + p.aux_off + (MODE == 1 ? slot * p.x_stride : 0);
+  float ss = 0.0f;
   const uint32_t y_off = p.y_off + slot * p.y_stride;
   const uint32_t chunks = p.n_in >> 4, blocks = p.n_in >> 5;
   const uint32_t MW = MAGIC, M8 = 0x00ff00ffu;
@@ -559,21 +654,28 @@ SK_DEV void matvec_q8_0_body(const uint4 *__restrict__ w, const uint16_t *__rest
   for (uint32_t k0 = 0; k0 < p.n_in; k0 += G::CH) {
     const uint32_t nk = min(p.n_in - k0, (uint32_t)G::CH);
     const uint32_t u0 = k0 >> 4, nu = nk >> 4, b0 = k0 >> 5, nb = nk >> 5;
+    float4 xu4[MODE ? 4 : 1];
     auto x_unit = [&](uint32_t i, float4 (&v)[4]) {
-      const float *xp = xv + (u0 + i) * 16;
+      const uint32_t at = (u0 + i) * 16;
 #pragma unroll
-      for (int k = 0; k < 4; k++) v[k] = *(const float4 *)(xp + 4 * k);
+      for (int k = 0; k < 4; k++) v[k] = *(const float4 *)(xv + at + 4 * k);
+      if constexpr (MODE != 0) {
+#pragma unroll
+        for (int k = 0; k < 4; k++) xu4[k] = *(const float4 *)(av + at + 4 * k);
+      }
     };
     float big = 0.0f;  // largest |x| this thread staged
+    float ssp = 0.0f;  // MODE 2: this pass's sum of x^2 (first staging only)
     auto x_store = [&](uint32_t i, const float4 (&v)[4], float scale) {
       uint32_t pp[8];
       const f16x2 one = {(f16)1.0f, (f16)1.0f};
-      float s = 0.0f;
+      float s = 0.0f, sq = 0.0f;
 #pragma unroll
       for (int k = 0; k < 4; k++) {
-        big = fmaxf(big, abs_max4(v[k]));
-        const float4 e = scale != 1.0f ? make_float4(v[k].x * scale, v[k].y * scale, v[k].z * scale, v[k].w * scale)
-                                       : v[k];
+        float4 f = v[k];
+        if constexpr (MODE != 0) f = fuse4<MODE>(f, xu4[k], sq);
+        big = fmaxf(big, abs_max4(f));
+        const float4 e = scale != 1.0f ? make_float4(f.x * scale, f.y * scale, f.z * scale, f.w * scale) : f;
         pp[2 * k] = pk(e.x, e.z);
         pp[2 * k + 1] = pk(e.y, e.w);
         s = dot2(as_f16x2(pp[2 * k]), one, s);
@@ -582,6 +684,7 @@ SK_DEV void matvec_q8_0_body(const uint4 *__restrict__ w, const uint16_t *__rest
       xq[0][i] = make_uint4(pp[0], pp[1], pp[2], pp[3]);
       xq[1][i] = make_uint4(pp[4], pp[5], pp[6], pp[7]);
       xs[i] = s;
+      if (scale == 1.0f) ssp += sq;
     };
     const uint32_t n_items = (uint32_t)G::RWG * nb;
     auto d_load = [&](uint32_t i) -> uint32_t {
@@ -610,7 +713,9 @@ SK_DEV void matvec_q8_0_body(const uint4 *__restrict__ w, const uint16_t *__rest
     }
     for (uint32_t i = tid + G::NT; i < n_items; i += G::NT) dd[i / nb][i % nb] = f16_bits_to_f32(d_load(i));
     guard_note(wmax, big);
+    norm_note<MODE, WAVES>(wss, ssp);
     __syncthreads();
+    norm_take<MODE, WAVES>(wss, ss);
     const int e = guard_exp<WAVES>(wmax);
     if (e) {  // rare: the pass again at x * 2^-e
       for (uint32_t i = tid; i < nu; i += G::NT) {
@@ -649,6 +754,7 @@ SK_DEV void matvec_q8_0_body(const uint4 *__restrict__ w, const uint16_t *__rest
     }
     if (e) scale_rows(acc, e);
   }
+  norm_apply<MODE>(acc, ss, p);
   store_rows<ACCUM, ROWS, LPR>(y, y_off, first, p.n_out, lane, acc);
 }
 
@@ -708,6 +814,46 @@ SK_DEV void matvec_q8_0_body(const uint4 *__restrict__ w, const uint16_t *__rest
 MV_ALL_TACTICS(MV_Q4K)
 MV_ALL_TACTICS(MV_Q6K)
 MV_ALL_TACTICS(MV_Q8_0)
+
+// Fused forms (MODE 1 = SiLU of the gate rows times the up rows, the down projection;
+// MODE 2 = RMSNorm, the projections that read a normed residual), dense rows only.
+#define MV_Q4K_F(SUF, MODE, W, A, R, L)                                                       \
+  extern "C" __global__ __launch_bounds__(64 * W) void matvec_q4k_##SUF##__##W##_##A##_##R##_0_##L(                                            \
+      const uint4 *w, const float *x, float *y, const uint32_t *ids, Segments<MatvecPush2F> m) { \
+    const uint32_t s = segment_of(m, blockIdx.x);                                            \
+    matvec_q4k_body<W, A, R, 0, L, MODE>(w, x, y, ids, segment_push(m, s), blockIdx.x - m.start[s]); \
+  }
+#define MV_Q6K_F(SUF, MODE, W, A, R, L)                                                       \
+  extern "C" __global__ __launch_bounds__(64 * W) void matvec_q6k_##SUF##__##W##_##A##_##R##_0_##L( \
+      const uint4 *w, const uint16_t *wd, const float *x, float *y, const uint32_t *ids,     \
+      Segments<MatvecPush4F> m) {                                                            \
+    const uint32_t s = segment_of(m, blockIdx.x);                                            \
+    matvec_q6k_body<W, A, R, 0, L, MODE>(w, wd, x, y, ids, segment_push(m, s), blockIdx.x - m.start[s]); \
+  }
+#define MV_Q8_0_F(SUF, MODE, W, A, R, L)                                                      \
+  extern "C" __global__ __launch_bounds__(64 * W) void matvec_q8_0_##SUF##__##W##_##A##_##R##_0_##L( \
+      const uint4 *w, const uint16_t *wd, const float *x, float *y, const uint32_t *ids,     \
+      Segments<MatvecPush2F> m) {                                                            \
+    const uint32_t s = segment_of(m, blockIdx.x);                                            \
+    matvec_q8_0_body<W, A, R, 0, L, MODE>(w, wd, x, y, ids, segment_push(m, s), blockIdx.x - m.start[s]); \
+  }
+// the engine's default tactic (4 waves, 2 rows, 64 lanes) and the runtime's size variants;
+// the norm forms write (ACCUM 0: q, k, v, gate, up, the head), the SiLU forms accumulate
+// (the down projection adds into the residual)
+MV_Q4K_F(norm, 2, 4, 0, 2, 64)
+MV_Q4K_F(norm, 2, 8, 0, 1, 16)
+MV_Q4K_F(norm, 2, 8, 0, 1, 64)
+MV_Q4K_F(silu, 1, 4, 1, 2, 64)
+MV_Q4K_F(silu, 1, 8, 1, 1, 16)
+MV_Q4K_F(silu, 1, 8, 1, 1, 64)
+MV_Q6K_F(norm, 2, 4, 0, 2, 64)
+MV_Q6K_F(norm, 2, 4, 0, 1, 16)
+MV_Q6K_F(norm, 2, 8, 0, 1, 32)
+MV_Q6K_F(silu, 1, 4, 1, 2, 64)
+MV_Q6K_F(silu, 1, 4, 1, 1, 16)
+MV_Q6K_F(silu, 1, 8, 1, 1, 32)
+MV_Q8_0_F(norm, 2, 4, 0, 2, 64)
+MV_Q8_0_F(silu, 1, 4, 1, 2, 64)
 
 // Dense variants with fewer lanes per row (more pipelined steps per lane) that the runtime
 // picks for large launches (skyla_hip.cpp, choose_variant).

@@ -77,6 +77,13 @@ const KernelInfo kKernels[] = {
     {"matvec_q4k", 4, 9, 5, 5, 0, true, true},
     {"matvec_q6k", 5, 11, 5, 5, 0, true, true},
     {"matvec_q8_0", 5, 9, 5, 5, 0, true, true},
+    // fused forms (kernels/matvec.hip): + the second vector's offset and eps
+    {"matvec_q4k_norm", 4, 11, 5, 5, 0, true, true},
+    {"matvec_q4k_silu", 4, 11, 5, 5, 0, true, true},
+    {"matvec_q6k_norm", 5, 13, 5, 5, 0, true, true},
+    {"matvec_q6k_silu", 5, 13, 5, 5, 0, true, true},
+    {"matvec_q8_0_norm", 5, 11, 5, 5, 0, true, true},
+    {"matvec_q8_0_silu", 5, 11, 5, 5, 0, true, true},
     {"matmul", 5, 13, 3, 4, -1, false, false},
     {"moe_logits", 3, 5, 0, 0, -1, false, false},
     {"moe_route", 2, 5, 0, 0, -1, false, false, 64},  // one wave per token
@@ -417,6 +424,11 @@ const VariantRule kVariantRules[] = {
     {"matvec_q4k", 0, 5, {{6144, 8, 1, 16}, {0, 8, 1, 64}}, 2},
     {"matvec_q6k", 0, 7, {{12288, 4, 1, 16}, {0, 8, 1, 32}}, 2},
     {"matvec_q4k", 1, 5, {{0, 4, 1, 16}}, 1},
+    // the fused forms take the same variants (they are compiled for exactly these)
+    {"matvec_q4k_norm", 0, 5, {{6144, 8, 1, 16}, {0, 8, 1, 64}}, 2},
+    {"matvec_q4k_silu", 0, 5, {{6144, 8, 1, 16}, {0, 8, 1, 64}}, 2},
+    {"matvec_q6k_norm", 0, 7, {{12288, 4, 1, 16}, {0, 8, 1, 32}}, 2},
+    {"matvec_q6k_silu", 0, 7, {{12288, 4, 1, 16}, {0, 8, 1, 32}}, 2},
 };
 
 std::shared_ptr<const Retile> make_retile(skyla_hip_context *ctx, const char *name, const uint32_t *spec,

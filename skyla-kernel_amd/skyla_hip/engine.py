@@ -192,12 +192,23 @@ def _matvec(ctx: Context, shader: str, dual_view: bool, push: int, matmul_type, 
     return Matvec(pipelines, experts, lanes, rpg)
 
 
+def _fused(ctx: Context, shader: str, dual_view: bool, push: int, tactic, accum: int,
+           weights: Sequence[Buffer], a: Buffer) -> Matvec:
+    """A fused decode matvec (matvec_*_norm / matvec_*_silu): the plain kernel's spec and
+    bindings, two push words more (the second vector's offset, eps); one accum form."""
+    waves, rows = tactic
+    p = ctx.create_pipeline_sets(shader, 4 + int(dual_view), push, [waves, accum, rows, 0, 64], len(weights))
+    for i, w in enumerate(weights):
+        p.bind_set_buffers(i, [w] + ([w] if dual_view else []) + [a, a, a])
+    return Matvec([p, p], [], 64, waves * rows)
+
+
 class Kernels:
     """kernels.rs:139-233, restricted to the pipelines of the quantized weight path."""
 
     def __init__(self, ctx: Context, weights: Sequence[Buffer], a: Buffer,
                  kquant_tactic=None, q8_0_tactic=None, kv: Buffer | None = None, c: Config | None = None,
-                 precision: KvPrecision | None = None, embd_dtype: DType | None = None):
+                 precision: KvPrecision | None = None, embd_dtype: DType | None = None, fuse: str = "none"):
         if ctx.subgroup_size != 64:
             raise ValueError(f"no kernels for subgroup size {ctx.subgroup_size} (need 64)")
         lanes = 64
@@ -210,6 +221,19 @@ class Kernels:
             _matvec(ctx, "matvec_q6k", True, 44, None, kq, lanes, weights, a),
         ]
         self.batch = [_matvec(ctx, "matmul", True, 52, t, (0, 0), lanes, weights, a) for t in (0, 1, 2)]
+        # decode matvecs with the RMSNorm before them / the SiLU gate folded in (compiled for the
+        # default tactics only)
+        self.norm = self.silu_mv = None
+        self.fuse = fuse
+        if fuse != "none":
+            if kq != KQUANT_TACTIC or q8 != Q8_0_TACTIC:
+                raise ValueError("the fused decode matvecs exist for the default tactics only")
+            self.norm = [_fused(ctx, "matvec_q8_0_norm", True, 44, q8, 0, weights, a),
+                         _fused(ctx, "matvec_q4k_norm", False, 44, kq, 0, weights, a),
+                         _fused(ctx, "matvec_q6k_norm", True, 52, kq, 0, weights, a)]
+            self.silu_mv = [_fused(ctx, "matvec_q8_0_silu", True, 44, q8, 1, weights, a),
+                            _fused(ctx, "matvec_q4k_silu", False, 44, kq, 1, weights, a),
+                            _fused(ctx, "matvec_q6k_silu", True, 52, kq, 1, weights, a)]
 
         def build(name, bufs, push):
             p = ctx.create_pipeline(name, len(bufs), push, [])
@@ -248,8 +272,11 @@ class Kernels:
         for i, wb in enumerate(weights):
             self.embed.bind_set_buffers(i, [wb, wb, a, a])
 
-    def matvec(self, dtype: DType, batched: bool) -> Matvec:
-        s = self.batch if batched else self.decode
+    def matvec(self, dtype: DType, batched: bool, form: str | None = None) -> Matvec:
+        if batched:
+            s = self.batch
+        else:
+            s = self.decode if form is None else {"norm": self.norm, "silu": self.silu_mv}[form]
         return {DType.Q4K: s[1], DType.Q6K: s[2]}.get(DType(dtype), s[0])
 
 
@@ -417,6 +444,10 @@ class Arena:
                      + [stride * slots])
         self.half = single(widest // 2 + 64)
         self.tokens = single(BATCH)
+        # the RMSNorm weights the fused decode matvecs read beside x: per layer the attention
+        # and FFN norms, then the output norm (filled by Engine from the weight tables)
+        self.s_norm, self.n_layer = _next64(c.n_embd), c.n_layer
+        self.norms = single(self.s_norm * (2 * c.n_layer + 1)) if c.n_layer else None
         self.buffer = ctx.alloc_host(self.size * 4)
         self.n_split = n_split
         self.max_ctx = max_ctx
@@ -434,6 +465,12 @@ class Arena:
     def u32(self):
         return self.buffer.as_u32()
 
+    def norm(self, layer: int, ffn: bool = False) -> int:
+        """Offset of a layer's attention (ffn False) or FFN norm weights in the norms region;
+        layer -1 is the output norm."""
+        slot = 2 * self.n_layer if layer < 0 else 2 * layer + int(ffn)
+        return self.norms + self.s_norm * slot
+
     def set_ctl(self, first_token: int, pos: int, n_tokens: int) -> None:
         """Engine::load's control words (engine.rs:119-123)."""
         u = self.u32()
@@ -447,14 +484,24 @@ class Graph:
     def __init__(self, r: Recorder, k: Kernels, a: Arena, c: Config, batched: bool):
         self.r, self.k, self.a, self.c, self.batched = r, k, a, c, batched
         self.b = BATCH if batched else 1
+        # decode with the fused matvecs (Kernels.fuse): "qkv" folds the attention norm into
+        # q/k/v; "all" also the FFN norm into gate/up, the SiLU into down and the output norm
+        # into the head
+        fuse = getattr(k, "fuse", "none")
+        on = not batched and fuse != "none" and a is not None and a.norms is not None
+        self.fused = on
+        self.fused_all = on and fuse == "all"
 
     def stage(self, label: str) -> None:
         self.r.barrier()
         self.r.mark(label)
 
-    def matvec(self, m: QMatrix, x, y, accum: bool, batched: bool, groups_z: int | None = None) -> None:
-        """graph.rs:23-34."""
-        mv = self.k.matvec(m.dtype, batched)
+    def matvec(self, m: QMatrix, x, y, accum: bool, batched: bool, groups_z: int | None = None,
+               form: str | None = None, aux: int = 0) -> None:
+        """graph.rs:23-34.  `form` "norm" / "silu" (decode only) dispatches the fused kernel:
+        x is the raw residual (norm, `aux` = the norm weights) or the gate rows (silu, `aux` =
+        the up rows)."""
+        mv = self.k.matvec(m.dtype, batched, form)
         groups = -(-m.n_out // mv.rows_per_group)
         o = m.off
         if batched:
@@ -463,6 +510,8 @@ class Graph:
             push = [o[0], o[1], o[2], o[3], x[0], y[0], m.n_in, m.n_out, 0, 0, 0]
         else:
             push = [o[0], o[1], x[0], y[0], m.n_in, m.n_out, 0, 0, 0]
+        if form is not None:
+            push += [aux, f32_bits(self.c.eps if form == "norm" else 0.0)]
         cols = (groups_z if groups_z is not None else BATCH // MATMUL_TILE_COLS) if batched else 1
         self.r.dispatch_set(mv.pipeline(accum), m.buf, [groups, 1, cols], push)
 
@@ -527,9 +576,17 @@ class Graph:
                         [a.x, m.down, m.weights, n_embd, a.s_embd, used])
         self.stage("moe combine")
 
-    def dense_ffn(self, gate: QMatrix, up: QMatrix, down: QMatrix) -> None:
+    def dense_ffn(self, gate: QMatrix, up: QMatrix, down: QMatrix, l: int = 0) -> None:
         """graph.rs:174-184 (after the ffn rmsnorm): gate, up -> silu -> down (+= x)."""
         a, c, b, bt = self.a, self.c, self.b, self.batched
+        if self.fused_all:  # the FFN norm folded into gate and up, the SiLU into down (decode)
+            f = dict(form="norm", aux=a.norm(l, True))
+            self.matvec(gate, (a.x, a.s_embd), (a.gate, a.s_ff), False, False, **f)
+            self.matvec(up, (a.x, a.s_embd), (a.up, a.s_ff), False, False, **f)
+            self.stage("matvec gate+up")
+            self.matvec(down, (a.gate, a.s_ff), (a.x, a.s_embd), True, False, form="silu", aux=a.up)
+            self.stage("matvec down")
+            return
         xn = self.input((a.n, a.s_embd), c.n_embd, 1)
         self.matvec(gate, xn, (a.gate, a.s_ff), False, bt)
         self.matvec(up, xn, (a.up, a.s_ff), False, bt)
@@ -560,10 +617,15 @@ class Graph:
         """graph.rs:59-113: q/k/v matvecs, QK-norm + RoPE + KV write, split-K attention,
         merge, o (+= x)."""
         a, c, bt = self.a, self.c, self.batched
-        xn = self.input((a.n, a.s_embd), c.n_embd, 1)
-        self.matvec(at.wq, xn, (a.q, a.s_q), False, bt)
-        self.matvec(at.wk, xn, (a.k, a.s_kv), False, bt)
-        self.matvec(at.wv, xn, (a.v, a.s_kv), False, bt)
+        if self.fused:  # the attention norm folded into q, k, v (x is the raw residual)
+            f = dict(form="norm", aux=a.norm(l))
+            for wm, out in ((at.wq, (a.q, a.s_q)), (at.wk, (a.k, a.s_kv)), (at.wv, (a.v, a.s_kv))):
+                self.matvec(wm, (a.x, a.s_embd), out, False, False, **f)
+        else:
+            xn = self.input((a.n, a.s_embd), c.n_embd, 1)
+            self.matvec(at.wq, xn, (a.q, a.s_q), False, bt)
+            self.matvec(at.wk, xn, (a.k, a.s_kv), False, bt)
+            self.matvec(at.wv, xn, (a.v, a.s_kv), False, bt)
         self.stage("matvec qkv")
         self.qk_rope(l, at.q_norm, at.k_norm, rope)
         self.attend(l)
@@ -595,15 +657,18 @@ class Graph:
     def layer(self, l: int, lw: "LayerWeights", rope: int) -> None:
         """graph.rs:150-185."""
         a, b = self.a, self.b
-        self.rmsnorm(a.x, lw.attn_norm, a.n, b)
-        self.stage("rmsnorm")
+        if not self.fused:
+            self.rmsnorm(a.x, lw.attn_norm, a.n, b)
+            self.stage("rmsnorm")
         self.attention(l, lw.attn, rope)
-        self.rmsnorm(a.x, lw.ffn_norm, a.n, b)
-        self.stage("rmsnorm")
-        if lw.router is not None:
+        moe = lw.router is not None
+        if not self.fused_all or moe:
+            self.rmsnorm(a.x, lw.ffn_norm, a.n, b)
+            self.stage("rmsnorm")
+        if moe:
             self.moe(lw.gate, lw.up, lw.down, lw.router)
         else:
-            self.dense_ffn(lw.gate, lw.up, lw.down)
+            self.dense_ffn(lw.gate, lw.up, lw.down, l)
 
 
 def f32_bits(v: float) -> int:
@@ -691,9 +756,12 @@ def record(ctx: Context, k: Kernels, w: Weights, a: Arena, c: Config, batched: b
             r.dispatch(k.take_last, [-(-n // 256), 1, 1], [a.x, a.last, n, a.s_embd])
             g.stage("take last")
             src = a.last
-        g.rmsnorm(src, w.out_norm, a.last, 1)
-        g.stage("rmsnorm")
-        g.matvec(w.output, (a.last, 0), (a.logits, 0), False, False)
+        if g.fused_all:
+            g.matvec(w.output, (src, 0), (a.logits, 0), False, False, form="norm", aux=a.norm(-1))
+        else:
+            g.rmsnorm(src, w.out_norm, a.last, 1)
+            g.stage("rmsnorm")
+            g.matvec(w.output, (a.last, 0), (a.logits, 0), False, False)
         r.host_barrier()
         r.mark("matvec output")
     return ctx.record(profile, body)
@@ -705,12 +773,29 @@ class Engine:
     last token."""
 
     def __init__(self, ctx: Context, model: dict, c: Config, max_ctx: int,
-                 precision: KvPrecision = KvPrecision.F16_KEYS_Q8_VALUES, profile: bool = False):
+                 precision: KvPrecision = KvPrecision.F16_KEYS_Q8_VALUES, profile: bool = False,
+                 fuse: str = "qkv"):
+        """fuse (decode step only; prefill keeps the separate launches): "qkv" folds the
+        attention RMSNorm into the q/k/v matvecs; "all" also folds the FFN norm into gate/up,
+        the SiLU gate into the down projection and the output norm into the head; "none"
+        keeps graph.rs's launches.  Measured on MI355X (config 5, 1k context) "qkv" saves a
+        launch per layer for 1.3 us more in the q/k/v launch, while "all" is slower than
+        "none": each of the down (+8 to 14 us) and head (+44 us) matvec workgroups repeats
+        the elementwise work and its loads, and the fused forms hold more registers."""
         self.ctx, self.c = ctx, c
         self.weights = load_weights(ctx, model, c)
         self.arena = Arena(ctx, c, max_ctx, precision)
+        a = self.arena
+        if fuse != "none":
+            f = a.f32()
+            for l in range(c.n_layer):
+                for ffn, name in ((False, "attn_norm"), (True, "ffn_norm")):
+                    o = a.norm(l, ffn)
+                    f[o: o + c.n_embd] = model[f"blk.{l}.{name}.weight"]
+            f[a.norm(-1): a.norm(-1) + c.n_embd] = model["output_norm.weight"]
+            a.buffer.upload(a.norms * 4, a.s_norm * (2 * c.n_layer + 1) * 4)
         self.kernels = Kernels(ctx, self.weights.buffers, self.arena.buffer, kv=self.arena.kv, c=c,
-                               precision=precision, embd_dtype=self.weights.embd.dtype)
+                               precision=precision, embd_dtype=self.weights.embd.dtype, fuse=fuse)
         self.decode = record(ctx, self.kernels, self.weights, self.arena, c, False, profile)
         self.prefill_rec = record(ctx, self.kernels, self.weights, self.arena, c, True, profile)
         self.pos = 0

