@@ -327,3 +327,22 @@ def test_config1_qwen3_06b_greedy(ctx, precision):
         assert worst < (1e-2 if precision == P.F16 else 2e-2), worst
     finally:
         eng.free()
+
+
+def test_engine_from_gguf_file(ctx, tmp_path):
+    """A model written to a GGUF file and loaded back (gguf.py: reader.rs, Config::from_gguf)
+    decodes exactly as the same tensors handed over in memory."""
+    from skyla_hip import gguf as G
+    c = synth.qwen3_config("tiny")
+    tensors = synth.qwen3(f"{CFG}-gguf", c, "q4_k_m", "random")
+    path = str(tmp_path / "tiny.gguf")
+    G.write_model(path, "qwen3", c, tensors)
+    g = G.Gguf(path)
+    c2, t2 = G.config_from_gguf(g), G.tensors_from_gguf(g)
+    e1, e2 = E.Engine(ctx, tensors, c, 32), E.Engine(ctx, t2, c2, 32)
+    try:
+        for tok in (5, 77, 1999):
+            assert np.array_equal(e1.step(tok), e2.step(tok))
+    finally:
+        e1.free()
+        e2.free()
