@@ -121,9 +121,10 @@ SK_DEV float load_kv(const f16 *kv, const int8_t *kv8, uint32_t cache, uint32_t 
 }
 
 // One workgroup of four waves per (kv head, split of CHUNK positions, token); every load of
-// the split is issued up front.  Scores: thread t takes a quarter (32 dims) of the key row
-// of position t / 4 and dots it with the N_REP query heads that share the kv head (held in
-// LDS, scaled); the four quarters meet in a quad shuffle.  The chunk's softmax numerators
+// the split is issued up front.  Scores: thread t takes dims 8 (t % 16) ... of the key rows
+// of positions t / 16 + 16 k (k < 4), so 16 lanes read one row's whole cache lines, and
+// dots them with the N_REP query heads that share the kv head (held in LDS, scaled); the
+// 16 partial dots of a row meet in a DPP sum.  The chunk's softmax numerators
 // e_p = exp(s_p - m) go through LDS to the value phase, where thread t weights 8 dims
 // (8 (t % 16) ...) of the value rows of positions 4 (t / 16) ... 4 (t / 16) + 3; the 16
 // position groups are then summed in LDS.  The partial (m, l = sum e_p, acc = sum e_p v_p)
@@ -143,19 +144,22 @@ SK_DEV void attention_body(float *a, const uint32_t *ctl, const f16 *kv, const i
   const uint32_t t = threadIdx.x, wave = t >> 6, kv_dim = p.n_kv * HD;
   const uint32_t begin = split * CHUNK, cnt = min(CHUNK, n_pos - begin);
 
-  // keys: position kp, dims [32 kc, 32 kc + 32)
-  const uint32_t kp = t >> 2, kc = t & 3, kpos = begin + min(kp, cnt - 1);
+  // keys: dims [8 kd, 8 kd + 8) of positions kg + 16 k, k < 4 (16 lanes cover a row: every
+  // load instruction reads whole cache lines)
+  const uint32_t kd = t & 15, kg = t >> 4;
   uint4 kr[4];
-  float ksc = 1.0f;
-  if constexpr (!K8) {
-    const uint4 *src = (const uint4 *)(kv + p.kc_off + kpos * kv_dim + kvh * HD + 32 * kc);
+  float ksc[4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) kr[i] = src[i];
-  } else {
-    const uint4 *src = (const uint4 *)(kv8 + p.kc_off + kpos * kv_dim + kvh * HD + 32 * kc);
-    kr[0] = src[0];
-    kr[1] = src[1];
-    ksc = (float)kv[p.ks_off + kpos * (kv_dim / 32) + kvh * 4 + kc];  // one block per quarter
+  for (int k = 0; k < 4; k++) {
+    const uint32_t kpos = begin + min(kg + 16 * k, cnt - 1);
+    if constexpr (!K8) {
+      kr[k] = *(const uint4 *)(kv + p.kc_off + kpos * kv_dim + kvh * HD + 8 * kd);
+      ksc[k] = 1.0f;
+    } else {
+      const uint2 r = *(const uint2 *)(kv8 + p.kc_off + kpos * kv_dim + kvh * HD + 8 * kd);
+      kr[k] = make_uint4(r.x, r.y, 0u, 0u);
+      ksc[k] = (float)kv[p.ks_off + kpos * (kv_dim / 32) + kvh * 4 + (kd >> 2)];
+    }
   }
   // values: dims [8 vg, 8 vg + 8) of positions 4 vq + [0, 4)
   const uint32_t vg = t & 15, vq = t >> 4;
@@ -178,44 +182,47 @@ SK_DEV void attention_body(float *a, const uint32_t *ctl, const f16 *kv, const i
   for (uint32_t i = t; i < N_REP * HD; i += 256) qs[i / HD][i % HD] = a[q_base + i] * p.scale;
   __syncthreads();
 
-  float k[32];
-  if constexpr (!K8) {
+  float sc[4][N_REP];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const uint32_t wd[4] = {kr[i].x, kr[i].y, kr[i].z, kr[i].w};
+  for (int k = 0; k < 4; k++) {
+    float key[8];
+    if constexpr (!K8) {
+      const uint32_t wd[4] = {kr[k].x, kr[k].y, kr[k].z, kr[k].w};
 #pragma unroll
       for (int h = 0; h < 4; h++) {
         const f16x2 v = as_f16x2(wd[h]);
-        k[8 * i + 2 * h] = (float)v.x;
-        k[8 * i + 2 * h + 1] = (float)v.y;
+        key[2 * h] = (float)v.x;
+        key[2 * h + 1] = (float)v.y;
       }
+    } else {
+      const uint32_t wd[2] = {kr[k].x, kr[k].y};
+#pragma unroll
+      for (int b = 0; b < 8; b++) key[b] = (float)(int8_t)((wd[b >> 2] >> (8 * (b & 3))) & 255u) * ksc[k];
     }
-  } else {
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
-      const uint32_t wd[4] = {kr[i].x, kr[i].y, kr[i].z, kr[i].w};
-#pragma unroll
-      for (int b = 0; b < 16; b++) k[16 * i + b] = (float)(int8_t)((wd[b >> 2] >> (8 * (b & 3))) & 255u) * ksc;
+    for (int j = 0; j < N_REP; j++) {
+      const float4 q0 = *(const float4 *)&qs[j][8 * kd], q1 = *(const float4 *)&qs[j][8 * kd + 4];
+      float s = 0.0f;
+      s = __builtin_fmaf(q0.x, key[0], s);
+      s = __builtin_fmaf(q0.y, key[1], s);
+      s = __builtin_fmaf(q0.z, key[2], s);
+      s = __builtin_fmaf(q0.w, key[3], s);
+      s = __builtin_fmaf(q1.x, key[4], s);
+      s = __builtin_fmaf(q1.y, key[5], s);
+      s = __builtin_fmaf(q1.z, key[6], s);
+      s = __builtin_fmaf(q1.w, key[7], s);
+      sc[k][j] = lane_sum<16>(s);  // the row's dot, in all 16 lanes
     }
   }
-  const bool live = kp < cnt;
-  float e[N_REP];
 #pragma unroll
   for (int j = 0; j < N_REP; j++) {
-    const float4 *qv = (const float4 *)&qs[j][32 * kc];
-    float s = 0.0f;
+    float m = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-      const float4 qq = qv[i];
-      s = __builtin_fmaf(qq.x, k[4 * i], s);
-      s = __builtin_fmaf(qq.y, k[4 * i + 1], s);
-      s = __builtin_fmaf(qq.z, k[4 * i + 2], s);
-      s = __builtin_fmaf(qq.w, k[4 * i + 3], s);
+    for (int k = 0; k < 4; k++) {
+      if (kg + 16 * k >= cnt) sc[k][j] = -INFINITY;
+      m = fmaxf(m, sc[k][j]);
     }
-    s += __shfl_xor(s, 1, 64);
-    s += __shfl_xor(s, 2, 64);
-    e[j] = live ? s : -INFINITY;
-    const float m = wave_max(e[j]);
+    m = wave_max(m);
     if ((t & 63) == 0) wm[wave][j] = m;
   }
   __syncthreads();
@@ -223,9 +230,14 @@ SK_DEV void attention_body(float *a, const uint32_t *ctl, const f16 *kv, const i
 #pragma unroll
   for (int j = 0; j < N_REP; j++) {
     mx[j] = fmaxf(fmaxf(wm[0][j], wm[1][j]), fmaxf(wm[2][j], wm[3][j]));
-    e[j] = live ? expf(e[j] - mx[j]) : 0.0f;
-    if (kc == 0) es[j][kp] = e[j];
-    const float l = wave_sum(kc == 0 ? e[j] : 0.0f);
+    float l = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const float e = kg + 16 * k < cnt ? expf(sc[k][j] - mx[j]) : 0.0f;
+      if (kd == 0) es[j][kg + 16 * k] = e;
+      l += e;
+    }
+    l = wave_sum(kd == 0 ? l : 0.0f);
     if ((t & 63) == 0) wl[wave][j] = l;
   }
   __syncthreads();

@@ -48,6 +48,24 @@ SK_DEV float group_sum(float v) {
   return v;
 }
 
+template <int CTRL>
+SK_DEV float dpp_f(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+
+// Sum over groups of LPR consecutive lanes (16, 32 or 64) through DPP row operations (and
+// one or two cross-row shuffles); every lane gets its group's total.
+template <int LPR>
+SK_DEV float lane_sum(float v) {
+  v += dpp_f<0xb1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_f<0x4e>(v);   // quad_perm [2,3,0,1]
+  v += dpp_f<0x141>(v);  // row_half_mirror: the two quads of each 8
+  v += dpp_f<0x140>(v);  // row_mirror: the two halves of each 16
+  if (LPR >= 32) v += __shfl_xor(v, 16, 64);
+  if (LPR >= 64) v += __shfl_xor(v, 32, 64);
+  return v;
+}
+
 SK_DEV uint32_t ctl_word(const uint32_t *ctl, uint32_t i) { return ctl[i]; }
 
 // Buffer resource over [base, base + bytes) for raw buffer loads: a load whose offset is
