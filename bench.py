@@ -296,7 +296,7 @@ def decode_config5(ctx: Context, contexts=(1024, 16384), steps: int = 20, warmup
     c = synth.qwen3_config("qwen3-8b")
     t = synth.qwen3("qwen3-8b-q4_k_m", c, "q4_k_m", "ones", shared_layers=True)
     max_ctx = max(contexts) + warmup + steps + 8
-    eng = E.Engine(ctx, t, c, max_ctx, E.KvPrecision.F16_KEYS_Q8_VALUES)
+    eng = E.Engine(ctx, t, c, max_ctx, E.KvPrecision.F16_KEYS_Q8_VALUES, profile=EAGER)
     try:
         a, kvl = eng.arena, eng.arena.kv_layout
         kv_dim = c.n_head_kv * c.head_dim
@@ -383,6 +383,9 @@ def main() -> int:
     ap.add_argument("--no-prefill", action="store_true", help="skip the config-3 GEMM figures")
     ap.add_argument("--no-moe", action="store_true", help="skip the config-4 MoE figures")
     ap.add_argument("--no-e2e", action="store_true", help="skip the config-5 end-to-end decode figures")
+    ap.add_argument("--e2e-only", type=str, default=None, metavar="CTX[,CTX]",
+                    help="run only the config-5 end-to-end decode at these KV context lengths and print "
+                         "its figures (for kernel traces of the whole decode step)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--eager", action="store_true",
                     help="replay recordings as direct launches instead of one HIP graph")
@@ -403,6 +406,11 @@ def main() -> int:
     ctx = Context.new(0)
     if args.calibrate:
         print(json.dumps(calibrate(ctx)))
+        ctx.free()
+        return 0
+    if args.e2e_only:
+        e2e = decode_config5(ctx, tuple(int(v) for v in args.e2e_only.split(",")))
+        print(json.dumps({"decode_e2e_config5": e2e}))
         ctx.free()
         return 0
     log(f"device {ctx.device_name()}; building {args.layers}-layer decode workload")
