@@ -7,6 +7,8 @@
 //   qkv_prep         [W, A, C, KV, KV8]  16 words  grid [n_head + 2 n_kv, tokens, 1]
 //   attention        [A, C, KV, KV8, KVS] 11 words grid [n_kv, n_split, tokens], 256 threads
 //   attention_merge  [A, C]               6 words  grid [n_head, tokens, 1], 1024 threads
+//   attention_prep   [W, A, C, KV, KV8]  17 words  grid [n_kv, n_split, 1], 256 threads:
+//                    qkv_prep + attention of a single-token step
 //   take_last        [A, C]               4 words  grid [ceil(n / 256), 1, 1]
 // W is a weight buffer (f32 tables: norm weights, RoPE frequencies), A the f32 arena and C
 // its u32 view (ctl[1] = position of the first token, ctl[2] = token count), KV the cache
@@ -40,6 +42,16 @@ struct AttnPush {
   uint32_t q_stride, part_stride, ks_off, vs_off;
 };
 struct MergePush { uint32_t part_off, o_off, n_split, chunk, part_stride, o_stride; };
+// attention_prep: qkv_prep's and attention's words for a single-token step (17 words)
+struct PrepPush {
+  uint32_t q_off, k_off, v_off, qn_off, kn_off, kc_off, vc_off, n_kv;
+  float eps;
+  uint32_t rope_off;
+  float mscale;
+  uint32_t ks_off, vs_off, part_off, n_split;
+  float scale;
+  uint32_t part_stride;
+};
 struct LastPush { uint32_t src_off, dst_off, n, stride; };
 
 SK_DEV float wave_sum(float v) { return group_sum<64>(v); }
@@ -58,24 +70,55 @@ SK_DEV float block_max(float v) {
   return v;
 }
 
-// Writes y0 (element t) and y1 (element t + 64) of one head's cache row.
+// Writes y0 (element t) and y1 (element t + 64) of one head's cache row.  With `raw`, the
+// stored row also goes to LDS as the cache holds it (128 f16, or 128 i8 and the four block
+// scales in `sc`), for a reader in the same workgroup.
 template <int Q8>
 SK_DEV void store_kv(f16 *kv, int8_t *kv8, uint32_t cache, uint32_t scales, uint32_t kv_dim, uint32_t pos,
-                     uint32_t head, uint32_t t, float y0, float y1) {
+                     uint32_t head, uint32_t t, float y0, float y1, uint32_t *raw = nullptr,
+                     float *sc = nullptr) {
   const uint32_t dst = cache + pos * kv_dim + head * HD;
   if constexpr (!Q8) {
-    kv[dst + t] = (f16)y0;
-    kv[dst + t + 64] = (f16)y1;
+    const f16 h0 = (f16)y0, h1 = (f16)y1;
+    kv[dst + t] = h0;
+    kv[dst + t + 64] = h1;
+    if (raw) {
+      ((f16 *)raw)[t] = h0;
+      ((f16 *)raw)[t + 64] = h1;
+    }
   } else {
     const float s0 = block_max(y0) / 127.0f, s1 = block_max(y1) / 127.0f;
-    kv8[dst + t] = (int8_t)(s0 > 0.0f ? __builtin_rintf(y0 / s0) : 0.0f);
-    kv8[dst + t + 64] = (int8_t)(s1 > 0.0f ? __builtin_rintf(y1 / s1) : 0.0f);
+    const int8_t q0 = (int8_t)(s0 > 0.0f ? __builtin_rintf(y0 / s0) : 0.0f);
+    const int8_t q1 = (int8_t)(s1 > 0.0f ? __builtin_rintf(y1 / s1) : 0.0f);
+    kv8[dst + t] = q0;
+    kv8[dst + t + 64] = q1;
     if ((t & 31) == 0) {
       const uint32_t sd = scales + pos * (kv_dim / 32) + head * 4 + t / 32;
       kv[sd] = (f16)s0;
       kv[sd + 2] = (f16)s1;
     }
+    if (raw) {
+      ((int8_t *)raw)[t] = q0;
+      ((int8_t *)raw)[t + 64] = q1;
+      if ((t & 31) == 0) {
+        sc[t / 32] = (float)(f16)s0;
+        sc[t / 32 + 2] = (float)(f16)s1;
+      }
+    }
   }
+}
+
+// QK-norm (rmsnorm.comp over one 128-wide head, weights at nw) and NeoX RoPE (rope.rs:60-68)
+// of the pair (element t, element t + 64), one wave per head.
+SK_DEV void norm_rope(const float *w, uint32_t nw, uint32_t rope_off, float eps, float mscale, uint32_t pos,
+                      uint32_t t, float x0, float x1, float &y0, float &y1) {
+#pragma clang fp contract(off)
+  const float r = 1.0f / sqrtf(wave_sum(x0 * x0 + x1 * x1) / (float)HD + eps);
+  const float n0 = x0 * r * w[nw + t], n1 = x1 * r * w[nw + t + 64];
+  const float angle = (float)pos * w[rope_off + t];
+  const float c = cosf(angle) * mscale, s = sinf(angle) * mscale;
+  y0 = n0 * c - n1 * s;
+  y1 = n0 * s + n1 * c;
 }
 
 template <int K8, int V8>
@@ -94,13 +137,8 @@ SK_DEV void qkv_body(const float *w, float *a, const uint32_t *ctl, f16 *kv, int
   const uint32_t head = is_q ? h : h - p.n_head;
   const uint32_t src = (is_q ? p.q_off + tok * p.q_stride : p.k_off + tok * p.kv_stride) + head * HD;
   const uint32_t nw = is_q ? p.qn_off : p.kn_off;
-  const float x0 = a[src + t], x1 = a[src + t + 64];
-  const float r = 1.0f / sqrtf(wave_sum(x0 * x0 + x1 * x1) / (float)HD + p.eps);
-  const float n0 = x0 * r * w[nw + t], n1 = x1 * r * w[nw + t + 64];
-  // NeoX rotation of the pair (t, t + 64) by pos * freq[t] (rope.rs:60-68)
-  const float angle = (float)pos * w[p.rope_off + t];
-  const float c = cosf(angle) * p.mscale, s = sinf(angle) * p.mscale;
-  const float y0 = n0 * c - n1 * s, y1 = n0 * s + n1 * c;
+  float y0, y1;
+  norm_rope(w, nw, p.rope_off, p.eps, p.mscale, pos, t, a[src + t], a[src + t + 64], y0, y1);
   if (is_q) {
     a[src + t] = y0;
     a[src + t + 64] = y1;
@@ -131,10 +169,20 @@ SK_DEV float load_kv(const f16 *kv, const int8_t *kv8, uint32_t cache, uint32_t 
 // goes to the part region for attention_merge; it is the same quantity as the reference's
 // running (m, l, acc) over the chunk (attention.comp:83-97).  Positions past the token's
 // own are masked (e = 0) and read a live row instead, so no load leaves the cache.
-template <int N_REP, int K8, int V8>
-SK_DEV void attention_body(float *a, const uint32_t *ctl, const f16 *kv, const int8_t *kv8, const AttnPush &p) {
+//
+// PREP (attention_prep, single-token steps): qkv_prep folded in.  Each workgroup norms and
+// rotates its own query heads from the raw q rows (one wave per head, the same arithmetic
+// as qkv_prep), and the workgroup whose split holds the new position writes that
+// position's key and value rows to the cache as qkv_prep would, keeping the stored bytes
+// in LDS: its threads take them from there in place of the rows they loaded from the cache
+// before the write (the new row and the masked slots clamped to it).
+template <int N_REP, int K8, int V8, bool PREP = false>
+SK_DEV void attention_body(const float *w, float *a, const uint32_t *ctl, f16 *kv, int8_t *kv8, const AttnPush &p,
+                           const PrepPush *pp) {
   constexpr int HG = N_REP < 4 ? N_REP : 4;  // heads per value reduction round
   __shared__ float qs[N_REP][HD];
+  __shared__ __attribute__((aligned(16))) uint32_t nk[PREP ? 64 : 1], nv[PREP ? 64 : 1];
+  __shared__ float nks[PREP ? 4 : 1], nvs[PREP ? 4 : 1];
   __shared__ float es[N_REP][CHUNK];
   __shared__ float wm[4][N_REP], wl[4][N_REP];
   __shared__ float4 vp[16][HG * HD / 4];
@@ -179,8 +227,58 @@ SK_DEV void attention_body(float *a, const uint32_t *ctl, const f16 *kv, const i
   }
   // the query heads of this kv head, scaled
   const uint32_t q_base = p.q_off + tok * p.q_stride + kvh * N_REP * HD;
-  for (uint32_t i = t; i < N_REP * HD; i += 256) qs[i / HD][i % HD] = a[q_base + i] * p.scale;
+  if constexpr (PREP) {
+    const uint32_t pos = ctl[1], lane = t & 63;
+    for (uint32_t j = wave; j < (uint32_t)N_REP; j += 4) {
+      float y0, y1;
+      norm_rope(w, pp->qn_off, pp->rope_off, pp->eps, pp->mscale, pos, lane, a[q_base + j * HD + lane],
+                a[q_base + j * HD + lane + 64], y0, y1);
+      qs[j][lane] = y0 * p.scale;
+      qs[j][lane + 64] = y1 * p.scale;
+    }
+    if (pos / CHUNK == split) {
+      if (wave == 0) {
+        float y0, y1;
+        const uint32_t src = pp->k_off + kvh * HD;
+        norm_rope(w, pp->kn_off, pp->rope_off, pp->eps, pp->mscale, pos, lane, a[src + lane], a[src + lane + 64], y0,
+                  y1);
+        store_kv<K8>(kv, kv8, p.kc_off, p.ks_off, kv_dim, pos, kvh, lane, y0, y1, nk, nks);
+      } else if (wave == 1) {
+        const uint32_t src = pp->v_off + kvh * HD;
+        store_kv<V8>(kv, kv8, p.vc_off, p.vs_off, kv_dim, pos, kvh, lane, a[src + lane], a[src + lane + 64], nv, nvs);
+      }
+    }
+  } else {
+    for (uint32_t i = t; i < N_REP * HD; i += 256) qs[i / HD][i % HD] = a[q_base + i] * p.scale;
+  }
   __syncthreads();
+  if constexpr (PREP) {
+    if (ctl[1] / CHUNK == split) {  // the new row (pl = cnt - 1) and the masked slots clamped to it
+      const uint32_t pl = cnt - 1;
+#pragma unroll
+      for (int k = 0; k < 4; k++)
+        if (kg + 16 * k >= pl) {
+          if constexpr (!K8) {
+            kr[k] = ((const uint4 *)nk)[kd];
+          } else {
+            const uint2 u = ((const uint2 *)nk)[kd];
+            kr[k] = make_uint4(u.x, u.y, 0u, 0u);
+            ksc[k] = nks[kd >> 2];
+          }
+        }
+#pragma unroll
+      for (int q = 0; q < 4; q++)
+        if (4 * vq + q >= pl) {
+          if constexpr (!V8) {
+            vr[q] = ((const uint4 *)nv)[vg];
+          } else {
+            const uint2 u = ((const uint2 *)nv)[vg];
+            vr[q] = make_uint4(u.x, u.y, 0u, 0u);
+            vsc[q] = nvs[vg >> 2];
+          }
+        }
+    }
+  }
 
   float sc[4][N_REP];
 #pragma unroll
@@ -373,7 +471,13 @@ QKV(1, 1)
   extern "C" __global__ __launch_bounds__(256) void attention__##R##_64_##K8##_##V8##_128_128(   \
       float *a, const uint32_t *ctl, const f16 *kv, const int8_t *kv8, const f16 *kvs, AttnPush p) { \
     (void)kvs;                                                                                   \
-    attention_body<R, K8, V8>(a, ctl, kv, kv8, p);                                               \
+    attention_body<R, K8, V8>(nullptr, a, ctl, const_cast<f16 *>(kv), const_cast<int8_t *>(kv8), p, nullptr); \
+  }                                                                                              \
+  extern "C" __global__ __launch_bounds__(256) void attention_prep__##R##_64_##K8##_##V8##_128_128( \
+      const float *w, float *a, const uint32_t *ctl, f16 *kv, int8_t *kv8, PrepPush pp) {        \
+    const AttnPush p = {pp.q_off, pp.part_off, pp.kc_off, pp.vc_off, pp.n_kv, pp.n_split,         \
+                        pp.scale, 0u, pp.part_stride, pp.ks_off, pp.vs_off};                     \
+    attention_body<R, K8, V8, true>(w, a, ctl, kv, kv8, p, &pp);                                 \
   }
 #define ATTN_REP(K8, V8) ATTN(1, K8, V8) ATTN(2, K8, V8) ATTN(4, K8, V8) ATTN(8, K8, V8)
 ATTN_REP(0, 0)

@@ -265,6 +265,11 @@ class Kernels:
         self.attention = build_spec("attention", [a, a, kv, kv, kv], 44,
                                     [c.n_head // c.n_head_kv, ATTENTION_CHUNK, k8, v8, c.head_dim, c.head_dim])
         self.merge = build_spec("attention_merge", [a, a], 24, [c.head_dim, 0])
+        # single-token steps: qkv_prep folded into the attention (kernels/attention.hip)
+        self.attn_prep = None
+        if self.fuse != "none":
+            self.attn_prep = build_spec("attention_prep", [w0, a, a, kv, kv], 68,
+                                        [c.n_head // c.n_head_kv, ATTENTION_CHUNK, k8, v8, c.head_dim, c.head_dim])
         self.take_last = build("take_last", [a, a], 16)
         # token rows gathered from the HBM token_embd, one binding set per weight buffer
         ty = {DType.Q8_0: 0, DType.Q4K: 1, DType.Q6K: 2}[DType(embd_dtype)]
@@ -627,8 +632,11 @@ class Graph:
             self.matvec(at.wk, xn, (a.k, a.s_kv), False, bt)
             self.matvec(at.wv, xn, (a.v, a.s_kv), False, bt)
         self.stage("matvec qkv")
-        self.qk_rope(l, at.q_norm, at.k_norm, rope)
-        self.attend(l)
+        if self.fused and self.k.attn_prep is not None:
+            self.attend_prep(l, at.q_norm, at.k_norm, rope)
+        else:
+            self.qk_rope(l, at.q_norm, at.k_norm, rope)
+            self.attend(l)
         xa = self.input((a.attn, a.s_attn), c.n_head * c.head_dim, 1)
         self.matvec(at.wo, xa, (a.x, a.s_embd), True, bt)
         self.stage("matvec o")
@@ -641,6 +649,21 @@ class Graph:
                 kv.value_scales(l)]
         self.r.dispatch(self.k.qkv, [c.n_head + 2 * c.n_head_kv, self.b, 1], push)
         self.stage("qk norm + rope")
+
+    def attend_prep(self, l: int, q_norm: int, k_norm: int, rope: int) -> None:
+        """qk_rope and attend of a single-token step as one launch (attention_prep), then the
+        merge.  The step's q, k, v rows are raw: each workgroup norms and rotates its query
+        heads, the one holding the new position writes its key and value."""
+        a, c, kv = self.a, self.c, self.a.kv_layout
+        scale = np.float32(1.0) / np.sqrt(np.float32(c.head_dim))
+        push = [a.q, a.k, a.v, q_norm, k_norm, kv.keys(l), kv.values(l), c.n_head_kv, f32_bits(c.eps), rope,
+                f32_bits(c.rope_mscale), kv.key_scales(l), kv.value_scales(l), a.part, a.n_split, f32_bits(scale),
+                a.s_part]
+        self.r.dispatch(self.k.attn_prep, [c.n_head_kv, a.n_split, 1], push)
+        self.stage("attention (+ qk norm, rope, kv write)")
+        push = [a.part, a.attn, a.n_split, ATTENTION_CHUNK, a.s_part, a.s_attn]
+        self.r.dispatch(self.k.merge, [c.n_head, 1, 1], push)
+        self.stage("attention merge")
 
     def attend(self, l: int) -> None:
         """graph.rs:89-109: split-K attention over layer l's cache, then the merge into attn."""

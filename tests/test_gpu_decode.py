@@ -28,7 +28,7 @@ CFG = "test-decode"
 class Bench:
     """Tables + a small embedding matrix, arena with KV cache, and the kernels."""
 
-    def __init__(self, ctx, c, precision, tables, max_ctx=256, embd=None):
+    def __init__(self, ctx, c, precision, tables, max_ctx=256, embd=None, fuse="none"):
         self.ctx, self.c = ctx, c
         p = E.Planner(ctx.max_buffer())
         self.off = {k: p.table(v) for k, v in tables.items()}
@@ -37,7 +37,7 @@ class Bench:
         self.weights = E.upload_weights(ctx, p)
         self.a = E.Arena(ctx, c, max_ctx, precision)
         self.k = E.Kernels(ctx, self.weights, self.a.buffer, kv=self.a.kv, c=c, precision=precision,
-                           embd_dtype=dt)
+                           embd_dtype=dt, fuse=fuse)
 
     def run(self, body, batched=True):
         rec = self.ctx.record(False, lambda r: body(E.Graph(r, self.k, self.a, self.c, batched)))
@@ -346,3 +346,49 @@ def test_engine_from_gguf_file(ctx, tmp_path):
     finally:
         e1.free()
         e2.free()
+
+
+@pytest.mark.parametrize("precision", list(P))
+@pytest.mark.parametrize("pos0", [0, 37, 64, 130])
+@pytest.mark.parametrize("heads", [(4, 2), (8, 1), (4, 4)])
+def test_attention_prep_equals_qkv_prep_then_attention(ctx, precision, pos0, heads):
+    """attention_prep (one token: qkv_prep folded into the attention) leaves the same cache
+    bytes and the same attention output, bit for bit, as qkv_prep then attention; the new
+    position first in its split (64, 130 - 128 = 2) and alone (0)."""
+    c = _cfg(512, *heads)
+    g = np.random.default_rng(7 + pos0)
+    qn, kn = g.uniform(0.5, 1.5, 128).astype(np.float32), g.uniform(0.5, 1.5, 128).astype(np.float32)
+    tables = {"qn": qn, "kn": kn, "rope": E.rope_frequencies(c)}
+    b = Bench(ctx, c, precision, tables, fuse="qkv")
+    try:
+        a = b.a
+        kv_host = a.kv.host()
+        kv_host[:] = g.integers(0, 256, kv_host.size, dtype=np.uint8)
+        kv_host.view("<f2")[:] = g.standard_normal(kv_host.size // 2).astype(np.float16)  # finite rows
+        kv0 = kv_host.copy()
+        q = (g.standard_normal(c.n_head * 128) * 3).astype(np.float32)
+        k = (g.standard_normal(c.n_head_kv * 128) * 3).astype(np.float32)
+        v = g.standard_normal(c.n_head_kv * 128).astype(np.float32)
+        outs = []
+        for fused in (False, True):
+            kv_host[:] = kv0
+            a.kv.upload()
+            b.put_rows(a.q, a.s_q, q[None])
+            b.put_rows(a.k, a.s_kv, k[None])
+            b.put_rows(a.v, a.s_kv, v[None])
+            a.set_ctl(0, pos0, 1)
+            a.buffer.upload()
+            if fused:
+                b.run(lambda gr: gr.attend_prep(1, b.off["qn"], b.off["kn"], b.off["rope"]), batched=False)
+            else:
+                b.run(lambda gr: (gr.qk_rope(1, b.off["qn"], b.off["kn"], b.off["rope"]), gr.attend(1)),
+                      batched=False)
+            a.buffer.download()
+            a.kv.download()
+            outs.append((b.rows(a.attn, a.s_attn, 1, c.n_head * 128)[0].copy(), a.kv.host().copy()))
+        (o0, kv_a), (o1, kv_b) = outs
+        assert np.array_equal(kv_a, kv_b)
+        assert np.isfinite(o1).all()
+        assert np.array_equal(o0.view(np.uint32), o1.view(np.uint32))
+    finally:
+        b.free()
