@@ -184,7 +184,7 @@ SK_DEV void attention_body(const float *w, float *a, const uint32_t *ctl, f16 *k
   __shared__ __attribute__((aligned(16))) uint32_t nk[PREP ? 64 : 1], nv[PREP ? 64 : 1];
   __shared__ float nks[PREP ? 4 : 1], nvs[PREP ? 4 : 1];
   __shared__ float es[N_REP][CHUNK];
-  __shared__ float wm[4][N_REP], wl[4][N_REP];
+  __shared__ float wm[4][N_REP];
   __shared__ float4 vp[16][HG * HD / 4];
   const uint32_t kvh = blockIdx.x, split = blockIdx.y, tok = blockIdx.z;
   const uint32_t n_pos = ctl[1] + tok + 1;
@@ -312,6 +312,8 @@ SK_DEV void attention_body(const float *w, float *a, const uint32_t *ctl, f16 *k
       sc[k][j] = lane_sum<16>(s);  // the row's dot, in all 16 lanes
     }
   }
+  // The 16 lanes of a group hold the same 4 x N_REP scores, so the wave maximum needs only
+  // the two cross-group steps, and each lane then exponentiates its own share of them.
 #pragma unroll
   for (int j = 0; j < N_REP; j++) {
     float m = -INFINITY;
@@ -320,25 +322,37 @@ SK_DEV void attention_body(const float *w, float *a, const uint32_t *ctl, f16 *k
       if (kg + 16 * k >= cnt) sc[k][j] = -INFINITY;
       m = fmaxf(m, sc[k][j]);
     }
-    m = wave_max(m);
+    m = fmaxf(m, __shfl_xor(m, 16, 64));
+    m = fmaxf(m, __shfl_xor(m, 32, 64));
     if ((t & 63) == 0) wm[wave][j] = m;
   }
   __syncthreads();
   float mx[N_REP];
 #pragma unroll
-  for (int j = 0; j < N_REP; j++) {
-    mx[j] = fmaxf(fmaxf(wm[0][j], wm[1][j]), fmaxf(wm[2][j], wm[3][j]));
-    float l = 0.0f;
+  for (int j = 0; j < N_REP; j++) mx[j] = fmaxf(fmaxf(wm[0][j], wm[1][j]), fmaxf(wm[2][j], wm[3][j]));
+  constexpr int NS = 4 * N_REP;  // scores of a lane group: (position k, head j) = (i / N_REP, i % N_REP)
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
-      const float e = kg + 16 * k < cnt ? expf(sc[k][j] - mx[j]) : 0.0f;
-      if (kd == 0) es[j][kg + 16 * k] = e;
-      l += e;
+  for (int i0 = 0; i0 < NS; i0 += 16) {
+    const int i = i0 + (int)kd;
+    if (i < NS) {
+      float s = -INFINITY, m = 0.0f;
+#pragma unroll
+      for (int u = i0; u < (i0 + 16 < NS ? i0 + 16 : NS); u++)
+        if (u == i) {
+          s = sc[u / N_REP][u % N_REP];
+          m = mx[u % N_REP];
+        }
+      const uint32_t pk = kg + 16 * (uint32_t)(i / N_REP);
+      es[i % N_REP][pk] = pk < cnt ? expf(s - m) : 0.0f;
     }
-    l = wave_sum(kd == 0 ? l : 0.0f);
-    if ((t & 63) == 0) wl[wave][j] = l;
   }
   __syncthreads();
+  // l = sum of the split's e per head: wave 0 adds the LDS rows while the others go on
+  float lrow[N_REP];
+  if (wave == 0) {
+#pragma unroll
+    for (int j = 0; j < N_REP; j++) lrow[j] = wave_sum(es[j][t]);
+  }
 
   float v[4][8];
 #pragma unroll
@@ -391,7 +405,7 @@ SK_DEV void attention_body(const float *w, float *a, const uint32_t *ctl, f16 *k
     for (int j = 0; j < N_REP; j++)
       if ((uint32_t)j == t) {
         m = mx[j];
-        l = ((wl[0][j] + wl[1][j]) + wl[2][j]) + wl[3][j];
+        l = lrow[j];
       }
     a[base] = m;
     a[base + 1] = l;
