@@ -319,7 +319,7 @@ def decode_config5(ctx: Context, contexts=(1024, 16384), steps: int = 20, warmup
                 tok = int(np.argmax(eng.step(tok)))
             wall = (time.perf_counter() - t0) / steps
             eng.pos = n_ctx
-            eng.load([tok])
+            eng.load([tok], batched=False)
             dev = float(np.median([ctx.replay_timed(eng.decode) for _ in range(5)])) / 1e9
             nbytes = weight_bytes + n_ctx * per_pos
             out[f"ctx{n_ctx}"] = {"tok_s": round(1.0 / wall, 1), "ms_per_token": round(wall * 1e3, 3),

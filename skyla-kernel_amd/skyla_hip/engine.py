@@ -614,7 +614,10 @@ class Graph:
         engine.rs:100-117, as a gather from the HBM token_embd)."""
         a, c = self.a, self.c
         o = m.off
-        push = [o[0], o[1], o[2], o[3], c.n_embd, a.tokens, a.x, a.s_embd]
+        # a single-token step reads its id from ctl[0] (the first token, engine.rs:119-123),
+        # so Engine.step uploads the control words only
+        ids = a.tokens if self.batched else 0
+        push = [o[0], o[1], o[2], o[3], c.n_embd, ids, a.x, a.s_embd]
         self.r.dispatch_set(self.k.embed, m.buf, [-(-(c.n_embd // 32) // 256), self.b, 1], push)
         self.stage("embed")
 
@@ -826,8 +829,9 @@ class Engine:
     def reset(self) -> None:
         self.pos = 0
 
-    def load(self, tokens) -> None:
-        """engine.rs:98-124: the chunk's token ids and the control words."""
+    def load(self, tokens, batched: bool = True) -> None:
+        """engine.rs:98-124: the chunk's token ids and the control words (a single-token
+        step's id travels in ctl[0] only)."""
         a = self.arena
         if self.pos + len(tokens) > a.max_ctx:
             raise ValueError(f"context full ({a.max_ctx} tokens)")
@@ -837,7 +841,8 @@ class Engine:
         u[a.tokens: a.tokens + len(tokens)] = np.asarray(tokens, np.uint32)
         u[0], u[1], u[2] = int(tokens[0]), self.pos, len(tokens)
         a.buffer.upload(0, 64 * 4)
-        a.buffer.upload(a.tokens * 4, len(tokens) * 4)
+        if batched:
+            a.buffer.upload(a.tokens * 4, len(tokens) * 4)
 
     def logits(self) -> np.ndarray:
         a = self.arena
@@ -846,7 +851,7 @@ class Engine:
 
     def step(self, token: int) -> np.ndarray:
         """engine.rs:137-142."""
-        self.load([token])
+        self.load([token], batched=False)
         self.ctx.replay(self.decode)
         self.pos += 1
         return self.logits()
