@@ -59,6 +59,7 @@ int fail(int code, const char *fmt, ...) {
 
 constexpr uint64_t kMaxBuffer = 4ull << 30;  // keeps u32 element offsets valid
 constexpr uint32_t kMaxMarks = 2048;          // skyla-vk/src/record.rs:6
+constexpr uint64_t kMaxPinned = 1ull << 30;   // host mirrors pinned up to this size
 
 // Bindings, push words and workgroup shape of every kernel the engine creates
 // (kernels.rs:170-205; workgroup shapes as skyla-metal/src/pipeline.rs:14-24).
@@ -119,10 +120,24 @@ struct skyla_hip_context {
   uint32_t warp = 64;
 };
 
+struct HostFree {
+  bool pinned;
+  HostFree(bool p = false) : pinned(p) {}
+  void operator()(unsigned char *p) const {
+    if (pinned)
+      (void)hipHostFree(p);
+    else
+      delete[] p;
+  }
+};
+
 struct skyla_hip_buffer {
   skyla_hip_context *ctx = nullptr;
   void *dev = nullptr;
-  std::unique_ptr<unsigned char[]> host;
+  // host mirror: pinned (hipHostMalloc) up to kMaxPinned bytes, so the per-step copies
+  // (control words up, logits down) are direct DMA; larger mirrors (weights, copied once)
+  // are pageable
+  std::unique_ptr<unsigned char[], HostFree> host;
   uint64_t size = 0;
 };
 
@@ -561,7 +576,13 @@ void *skyla_hip_buffer_host(skyla_hip_buffer *buf) {
     return nullptr;
   }
   if (!buf->host) {
-    buf->host.reset(new (std::nothrow) unsigned char[buf->size]);
+    void *pinned = nullptr;
+    if (buf->size <= kMaxPinned && hipHostMalloc(&pinned, buf->size, hipHostMallocDefault) == hipSuccess) {
+      buf->host = std::unique_ptr<unsigned char[], HostFree>((unsigned char *)pinned, HostFree(true));
+    } else {
+      (void)hipGetLastError();  // a refused pinned allocation falls back to pageable memory
+      buf->host.reset(new (std::nothrow) unsigned char[buf->size]);
+    }
     if (!buf->host) {
       fail(SKYLA_HIP_E_OOM, "buffer_host: cannot allocate %llu host bytes",
            (unsigned long long)buf->size);
