@@ -43,6 +43,10 @@ struct MatvecPush2F {
   uint32_t o0, o1, x_off, y_off, n_in, n_out, ids_off, x_stride, y_stride, aux_off;
   float eps;
 };
+// matvec_q4k_glu: the gate matrix's regions, then the up matrix's (11 words)
+struct MatvecPushGlu {
+  uint32_t o0, o1, x_off, y_off, n_in, n_out, ids_off, x_stride, y_stride, u0, u1;
+};
 struct MatvecPush4F {
   uint32_t o0, o1, o2, o3, x_off, y_off, n_in, n_out, ids_off, x_stride, y_stride, aux_off;
   float eps;
@@ -209,25 +213,38 @@ SK_DEV void matvec_q4k_body(const uint4 *__restrict__ w, const float *x, float *
   __shared__ float4 sc[G::RWG][G::CH_SUP][4];
   __shared__ uint32_t wmax[WAVES];
   __shared__ float wss[MODE == 2 ? 4 * WAVES : 1];
+  // MODE 3 (gate and up in one launch): the first half of the waves computes gate rows,
+  // the second half the up rows of the same outputs, and the store writes silu(g) * u
+  constexpr bool PAIR = MODE == 3, AUX = MODE == 1 || MODE == 2;
+  constexpr int OUT = PAIR ? G::RWG / 2 : G::RWG;  // outputs per workgroup
+  __shared__ float ush[PAIR ? OUT : 1];
 
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = (tid & 63) % LPR;
   const uint32_t sub = (tid & 63) / LPR;
-  const uint32_t row0 = bx * G::RWG;
-  const uint32_t lrow0 = ((tid >> 6) * G::SUBS + sub) * ROWS;  // first row of this group in the WG
+  const uint32_t row0 = bx * OUT;
+  const uint32_t wv = tid >> 6;
+  const bool second = PAIR && wv >= (uint32_t)WAVES / 2;
+  const uint32_t lrow0 = ((PAIR ? wv % (WAVES / 2) : wv) * G::SUBS + sub) * ROWS;  // first row of this group
+  const uint32_t hrow0 = (second ? OUT : 0) + lrow0;  // its header rows in LDS
   const uint32_t first = row0 + lrow0;
   const uint32_t slot = blockIdx.y;
   const uint32_t base = MOE ? ids[p.ids_off + slot] * p.n_out : 0;
   const float *xv = x + p.x_off + slot * p.x_stride;
-  const float *av = x;  // MODE != 0: the second vector, indexed as xv
-  if constexpr (MODE != 0) av = x + p.aux_off + (MODE == 1 ? slot * p.x_stride : 0);
+  const float *av = x;  // MODE 1, 2: the second vector, indexed as xv
+  if constexpr (AUX) av = x + p.aux_off + (MODE == 1 ? slot * p.x_stride : 0);
   float ss = 0.0f;      // MODE 2: sum of x^2 over the passes so far
   const uint32_t y_off = p.y_off + slot * p.y_stride;
   const uint32_t units = p.n_in >> 5, supers = p.n_in >> 8;
   const uint32_t c = (lane >> 1) & 3;  // chunk of this lane's units (u % 8 == lane % 8)
   const uint32_t MW = MAGIC, LO = 0x000f000fu, HI = 0x00f000f0u;
 
-  const BufRes wq = buf_res(w + p.o0, (uint64_t)(base + p.n_out) * units * 16);
+  uint32_t mo0 = p.o0, mo1 = p.o1;  // this wave's matrix
+  if constexpr (PAIR) {
+    mo0 = __builtin_amdgcn_readfirstlane(second ? p.u0 : p.o0);
+    mo1 = __builtin_amdgcn_readfirstlane(second ? p.u1 : p.o1);
+  }
+  const BufRes wq = buf_res(w + mo0, (uint64_t)(base + p.n_out) * units * 16);
   const BufRes wh = buf_res(w + p.o1, (uint64_t)(base + p.n_out) * supers * 16);
   uint32_t voff[ROWS];
 #pragma unroll
@@ -244,18 +261,18 @@ SK_DEV void matvec_q4k_body(const uint4 *__restrict__ w, const float *x, float *
     // Load order matters (a wave's loads complete in issue order): activations, then
     // headers, then the first PF weight steps, so staging waits only for its own data.
     constexpr int XI = (4 * CHU + G::NT - 1) / G::NT;  // activation quarters per thread
-    float4 xa[XI][2], xu[MODE ? XI : 1][2];
+    float4 xa[XI][2], xu[AUX ? XI : 1][2];
     auto load_x = [&]() {
 #pragma unroll
       for (int j = 0; j < XI; j++) {
         const uint32_t t = tid + j * G::NT, u = u0 + (t >> 2), qq = t & 3;
         xa[j][0] = xa[j][1] = make_float4(0.f, 0.f, 0.f, 0.f);  // every path defines them
-        if constexpr (MODE != 0) xu[j][0] = xu[j][1] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if constexpr (AUX) xu[j][0] = xu[j][1] = make_float4(0.f, 0.f, 0.f, 0.f);
         if (t < 4 * nu) {
           const uint32_t at = (u >> 3) * 256 + ((u >> 1) & 3) * 64 + (u & 1) * 16 + (qq >> 1) * 32 + (qq & 1) * 8;
           xa[j][0] = *(const float4 *)(xv + at);
           xa[j][1] = *(const float4 *)(xv + at + 4);
-          if constexpr (MODE != 0) {
+          if constexpr (AUX) {
             xu[j][0] = *(const float4 *)(av + at);
             xu[j][1] = *(const float4 *)(av + at + 4);
           }
@@ -268,7 +285,12 @@ SK_DEV void matvec_q4k_body(const uint4 *__restrict__ w, const float *x, float *
 #pragma unroll
     for (int j = 0; j < HI_T; j++) {
       const uint32_t i = tid + j * G::NT, lr = i / G::CH_SUP, s = i % G::CH_SUP;
-      if (i < NH && s < ns) hd[j] = buf_load(wh, ((base + min(row0 + lr, p.n_out - 1)) * supers + s) * 16, s0 * 16);
+      if constexpr (PAIR) {  // rows [0, OUT) of the gate, then the same rows of up
+        if (i < NH && s < ns)
+          hd[j] = w[(lr >= (uint32_t)OUT ? p.u1 : p.o1) + min(row0 + lr % OUT, p.n_out - 1) * supers + s0 + s];
+      } else {
+        if (i < NH && s < ns) hd[j] = buf_load(wh, ((base + min(row0 + lr, p.n_out - 1)) * supers + s) * 16, s0 * 16);
+      }
     }
     uint4 q[PF][ROWS];
 #pragma unroll
@@ -285,7 +307,7 @@ SK_DEV void matvec_q4k_body(const uint4 *__restrict__ w, const float *x, float *
       for (int j = 0; j < XI; j++) {
         const uint32_t t = tid + j * G::NT, u = t >> 2, qq = t & 3;
         float4 a = xa[j][0], b = xa[j][1];
-        if constexpr (MODE != 0) {
+        if constexpr (AUX) {
           float sq = 0.0f;
           a = fuse4<MODE>(a, xu[j][0], sq);
           b = fuse4<MODE>(b, xu[j][1], sq);
@@ -365,7 +387,7 @@ SK_DEV void matvec_q4k_body(const uint4 *__restrict__ w, const float *x, float *
           sb = dot2(as_f16x2(and_or(w0, HI, MW)), as_f16x2(pb[2 * k]), sb);
           sb = dot2(as_f16x2(and_or(w8, HI, MW)), as_f16x2(pb[2 * k + 1]), sb);
         }
-        const float4 f = sc[lrow0 + r][s][c];
+        const float4 f = sc[hrow0 + r][s][c];
         acc[r] = __builtin_fmaf(f.x, sa, acc[r]);
         acc[r] = __builtin_fmaf(f.y, sb, acc[r]);
         acc[r] = __builtin_fmaf(-f.z, xsum.x, acc[r]);
@@ -388,7 +410,24 @@ SK_DEV void matvec_q4k_body(const uint4 *__restrict__ w, const float *x, float *
     if (e) scale_rows(acc, e);
   }
   norm_apply<MODE>(acc, ss, p);
-  store_rows<ACCUM, ROWS, LPR>(y, y_off, first, p.n_out, lane, acc);
+  if constexpr (PAIR) {
+    float tot[ROWS];
+#pragma unroll
+    for (int r = 0; r < ROWS; r++) {
+      tot[r] = lane_sum<LPR>(acc[r]);
+      if (second && lane == 0) ush[lrow0 + r] = tot[r];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < ROWS; r++)
+      if (!second && lane == 0 && first + r < p.n_out) {
+#pragma clang fp contract(off)
+        const float g = tot[r];
+        y[y_off + first + r] = g / (1.0f + expf(-g)) * ush[lrow0 + r];  // silu_mul.comp:15-23
+      }
+  } else {
+    store_rows<ACCUM, ROWS, LPR>(y, y_off, first, p.n_out, lane, acc);
+  }
 }
 
 // ---------------------------------------------------------------------------------------
@@ -837,6 +876,16 @@ MV_Q6K_F(silu, 1, 4, 1, 1, 16)
 MV_Q6K_F(silu, 1, 8, 1, 1, 32)
 MV_Q8_0_F(norm, 2, 4, 0, 2, 64)
 MV_Q8_0_F(silu, 1, 4, 1, 2, 64)
+// gate and up of a decode token in one launch, writing silu(gate) * up (MODE 3): half the
+// waves take gate rows, half the same rows of up, so a workgroup outputs RWG / 2 values
+#define MV_Q4K_GLU(W, R, L)                                                                    \
+  extern "C" __global__ __launch_bounds__(64 * W) void matvec_q4k_glu__##W##_0_##R##_0_##L(      \
+      const uint4 *w, const float *x, float *y, const uint32_t *ids, Segments<MatvecPushGlu> m) { \
+    const uint32_t s = segment_of(m, blockIdx.x);                                            \
+    matvec_q4k_body<W, 0, R, 0, L, 3>(w, x, y, ids, segment_push(m, s), blockIdx.x - m.start[s]); \
+  }
+MV_Q4K_GLU(8, 1, 16)
+MV_Q4K_GLU(8, 1, 64)
 
 // Dense variants with fewer lanes per row (more pipelined steps per lane) that the runtime
 // picks for large launches (skyla_hip.cpp, choose_variant).

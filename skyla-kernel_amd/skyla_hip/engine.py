@@ -223,7 +223,7 @@ class Kernels:
         self.batch = [_matvec(ctx, "matmul", True, 52, t, (0, 0), lanes, weights, a) for t in (0, 1, 2)]
         # decode matvecs with the RMSNorm before them / the SiLU gate folded in (compiled for the
         # default tactics only)
-        self.norm = self.silu_mv = None
+        self.norm = self.silu_mv = self.glu = None
         self.fuse = fuse
         if fuse != "none":
             if kq != KQUANT_TACTIC or q8 != Q8_0_TACTIC:
@@ -234,6 +234,11 @@ class Kernels:
             self.silu_mv = [_fused(ctx, "matvec_q8_0_silu", True, 44, q8, 1, weights, a),
                             _fused(ctx, "matvec_q4k_silu", False, 44, kq, 1, weights, a),
                             _fused(ctx, "matvec_q6k_silu", True, 52, kq, 1, weights, a)]
+            # Q4_K gate and up in one launch writing silu(gate) * up: eight waves, half on
+            # each matrix, 16 lanes per row, 16 outputs per workgroup
+            self.glu = ctx.create_pipeline_sets("matvec_q4k_glu", 4, 44, [8, 0, 1, 0, 16], len(weights))
+            for i, wb in enumerate(weights):
+                self.glu.bind_set_buffers(i, [wb, a, a, a])
 
         def build(name, bufs, push):
             p = ctx.create_pipeline(name, len(bufs), push, [])
@@ -584,6 +589,16 @@ class Graph:
     def dense_ffn(self, gate: QMatrix, up: QMatrix, down: QMatrix, l: int = 0) -> None:
         """graph.rs:174-184 (after the ffn rmsnorm): gate, up -> silu -> down (+= x)."""
         a, c, b, bt = self.a, self.c, self.b, self.batched
+        if (self.fused and not self.fused_all and self.k.glu is not None and gate.dtype == up.dtype == DType.Q4K
+                and gate.buf == up.buf and (gate.n_in, gate.n_out) == (up.n_in, up.n_out)):
+            # gate and up in one launch that writes silu(gate) * up: no silu_mul launch
+            g, u = gate.off, up.off
+            push = [g[0], g[1], a.n, a.gate, gate.n_in, gate.n_out, 0, 0, 0, u[0], u[1]]
+            self.r.dispatch_set(self.k.glu, gate.buf, [-(-gate.n_out // 16), 1, 1], push)
+            self.stage("matvec gate+up (silu)")
+            self.matvec(down, (a.gate, a.s_ff), (a.x, a.s_embd), True, False)
+            self.stage("matvec down")
+            return
         if self.fused_all:  # the FFN norm folded into gate and up, the SiLU into down (decode)
             f = dict(form="norm", aux=a.norm(l, True))
             self.matvec(gate, (a.x, a.s_embd), (a.gate, a.s_ff), False, False, **f)

@@ -7,7 +7,7 @@ actually land near 1e-4, so a tighter 2e-3 regression guard is asserted too).
 import numpy as np
 import pytest
 
-from helpers import Setup, env, rel_l2
+from helpers import Setup, env, pad64, rel_l2
 from oracle import skyla_oracle as so
 from skyla_hip import engine as E
 from skyla_hip import synth
@@ -207,3 +207,43 @@ def test_fused_matvec_forms(ctx, dtype, n_in, n_out, form, retile):
     assert np.isfinite(got).all()
     err = rel_l2(got - y0, want)
     assert err <= GUARD, err
+
+
+@pytest.mark.parametrize("n_in,n_out", [(4096, 12288), (1024, 1536), (2048, 100)])
+def test_glu_pair_equals_gate_up_then_silu(ctx, n_in, n_out):
+    """matvec_q4k_glu (gate and up in one launch writing silu(gate) * up) against the two
+    matvecs and silu_mul on the same device: bit for bit where both run the 16-lane rows."""
+    g = synth.matrix("test-glu", f"gate-{n_in}-{n_out}", E.DType.Q4K, n_in, n_out)
+    u = synth.matrix("test-glu", f"up-{n_in}-{n_out}", E.DType.Q4K, n_in, n_out)
+    x = synth.activations("test-glu", f"x-{n_in}", n_in)
+    s = Setup(ctx, [(E.DType.Q4K, n_in, n_out, g), (E.DType.Q4K, n_in, n_out, u)], n_in, n_out,
+              extra_f32=2 * pad64(n_out))
+    k = E.Kernels(ctx, s.weights, s.arena, fuse="qkv")
+    try:
+        s.set_x(x)
+        gq, uq = s.q
+        assert gq.buf == uq.buf
+        go, uo = s.extra_off, s.extra_off + pad64(n_out)
+
+        def fused(r):
+            push = [gq.off[0], gq.off[1], s.x_off, s.y_off, n_in, n_out, 0, 0, 0, uq.off[0], uq.off[1]]
+            r.dispatch_set(k.glu, gq.buf, [-(-n_out // 16), 1, 1], push)
+
+        def plain(r):
+            gr = E.Graph(r, k, None, E.Config(n_embd=n_in), False)
+            gr.matvec(gq, (s.x_off, 0), (go, 0), False, False)
+            gr.matvec(uq, (s.x_off, 0), (uo, 0), False, False)
+            r.barrier()
+            r.dispatch(k.silu, [-(-n_out // 256), 1, 1], [go, uo, n_out, 0])
+        s.run(fused)
+        s.run(plain)
+        s.arena.download()
+        f = s.arena.as_f32()
+        got, want = f[s.y_off: s.y_off + n_out].copy(), f[go: go + n_out].copy()
+    finally:
+        s.free()
+    assert np.isfinite(got).all()
+    if 2 * n_out >= 6144:  # the plain gate+up launch runs the same (8, 1, 16) variant
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    else:                  # another lane split of the same sums
+        assert rel_l2(got, want) <= 1e-5
