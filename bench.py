@@ -396,7 +396,8 @@ def main() -> int:
     EAGER = args.eager
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: every box of this build has a single MI355X, and "
-              f"the path shards across GPUs only by design (see DESIGN.md); got --gpus {args.gpus}",
+              f"the path shards across GPUs only by design (rows of the dense matrices, experts of the MoE); "
+              f"got --gpus {args.gpus}",
               file=sys.stderr)
         return 2
 
