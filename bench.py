@@ -291,8 +291,9 @@ def decode_config5(ctx: Context, contexts=(1024, 16384), steps: int = 20, warmup
     down, then the output norm and the 151936-row Q6_K head), with the KV cache (f16 keys,
     8-bit values) pre-filled with N(0,1) rows to each context length.  tok/s is end to end
     as Engine::step runs it: control words up, one graph replay, the logits back and the
-    greedy argmax on the host.  The 36 layers hold copies of one seeded layer (two for
-    ffn_down's Q6_K / Q4_K halves), each its own HBM copy."""
+    greedy argmax on the host.  Also a 512-token prefill from position 0 (four 128-token
+    chunks).  The 36 layers hold copies of one seeded layer (two for ffn_down's Q6_K / Q4_K
+    halves), each its own HBM copy."""
     c = synth.qwen3_config("qwen3-8b")
     t = synth.qwen3("qwen3-8b-q4_k_m", c, "q4_k_m", "ones", shared_layers=True)
     max_ctx = max(contexts) + warmup + steps + 8
@@ -326,6 +327,19 @@ def decode_config5(ctx: Context, contexts=(1024, 16384), steps: int = 20, warmup
                                   "device_ms_per_token": round(dev * 1e3, 3),
                                   "kv_bytes_read": n_ctx * per_pos,
                                   "gbs_device": round(nbytes / dev / 1e9, 1)}
+        # prefill: a 512-token prompt from position 0 as Engine::prefill runs it (four
+        # 128-token chunks, each one graph replay of the batched recording)
+        prompt = [int(v) for v in synth.rng("qwen3-8b-q4_k_m", "prompt").integers(0, c.n_vocab, 512)]
+        eng.reset()
+        eng.prefill(prompt[:128])  # warm-up
+        times = []
+        for _ in range(3):
+            eng.reset()
+            t0 = time.perf_counter()
+            eng.prefill(prompt)
+            times.append(time.perf_counter() - t0)
+        pt = float(np.median(times))
+        out["prefill512"] = {"tok_s": round(512 / pt, 1), "ms": round(pt * 1e3, 2), "chunks": 4}
         return out
     finally:
         eng.free()

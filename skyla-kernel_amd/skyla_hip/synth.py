@@ -92,6 +92,8 @@ def qwen3(config: str, c, quant: str = "q8_0", norms: str = "ones", shared_layer
       quant "q8_0": every matrix Q8_0 and the head tied to token_embd (config 1).
       quant "q4_k_m": token_embd and attention/gate/up Q4_K, ffn_down Q6_K in even layers and
         Q4_K in odd ones, output head Q6_K (config 5).
+      quant "q4_k_m_mixed": as q4_k_m with attn_v also Q6_K in even layers, as llama.cpp's
+        Q4_K_M mixes them (q, k and v then differ in type within a layer).
       norms "ones": f32 1.0 (config 1); "random": U[0.5, 1.5], which also exercises the
         norm weights.
     shared_layers: every layer's matrices are the seeded ones of layer 0 (ffn_down: of layer
@@ -122,6 +124,7 @@ def qwen3(config: str, c, quant: str = "q8_0", norms: str = "ones", shared_layer
     for i in range(c.n_layer):
         n = lambda s: f"blk.{i}.{s}.weight"  # noqa: E731
         down = base if q8 or i % 2 else DType.Q6K
+        v_type = DType.Q6K if quant == "q4_k_m_mixed" and i % 2 == 0 else base
         t.update({
             n("attn_norm"): norm(n("attn_norm"), c.n_embd),
             n("ffn_norm"): norm(n("ffn_norm"), c.n_embd),
@@ -129,7 +132,7 @@ def qwen3(config: str, c, quant: str = "q8_0", norms: str = "ones", shared_layer
             n("attn_k_norm"): norm(n("attn_k_norm"), hd),
             n("attn_q"): mat(n("attn_q"), base, c.n_embd, c.n_head * hd),
             n("attn_k"): mat(n("attn_k"), base, c.n_embd, c.n_head_kv * hd),
-            n("attn_v"): mat(n("attn_v"), base, c.n_embd, c.n_head_kv * hd),
+            n("attn_v"): mat(n("attn_v"), v_type, c.n_embd, c.n_head_kv * hd),
             n("attn_output"): mat(n("attn_output"), base, c.n_head * hd, c.n_embd),
             n("ffn_gate"): mat(n("ffn_gate"), base, c.n_embd, c.n_ff),
             n("ffn_up"): mat(n("ffn_up"), base, c.n_embd, c.n_ff),

@@ -230,12 +230,16 @@ NEAR = 2e-2  # oracle top-2 margin, relative to the logits' std, below which a f
 
 
 @pytest.mark.parametrize("fuse", ["none", "qkv", "all"])
-@pytest.mark.parametrize("quant", ["q8_0", "q4_k_m"])
+@pytest.mark.parametrize("quant", ["q8_0", "q4_k_m", "q4_k_m_mixed"])
 @pytest.mark.parametrize("precision", [P.F16, P.F16_KEYS_Q8_VALUES])
 def test_decode_top1_against_oracle(ctx, quant, precision, fuse):
-    """32 greedy steps of a 3-layer model, with each of the decode graph's fusion levels."""
+    """32 greedy steps of a 3-layer model, with each of the decode graph's fusion levels.
+    q4_k_m_mixed is the q4_k_m model's seeded weights with attn_v Q6_K in even layers (q, k
+    and v of one layer in two types).  Seeded apart, that layout drew an ill-conditioned
+    model: FFN activations of 1e6, and 2.5e-4 of noise on its stored k/v rows moved the
+    oracle's own logits by up to 97%, so no rounding-level bound could hold."""
     c = synth.qwen3_config("tiny")
-    tensors = synth.qwen3(f"{CFG}-{quant}", c, quant, "random")
+    tensors = synth.qwen3(f"{CFG}-{'q4_k_m' if quant == 'q4_k_m_mixed' else quant}", c, quant, "random")
     oracle = Model(c, tensors, (precision.keys_q8, precision.values_q8))
     eng = E.Engine(ctx, tensors, c, 64, precision, fuse=fuse)
     try:

@@ -49,7 +49,8 @@ def test_dequant_bit_exact(ctx, dtype, n_in, n_out):
 
 SMALL = [
     (E.DType.Q4K, 256, 1), (E.DType.Q4K, 512, 37), (E.DType.Q4K, 2304, 64), (E.DType.Q4K, 768, 9),
-    (E.DType.Q6K, 256, 1), (E.DType.Q6K, 512, 37), (E.DType.Q6K, 2304, 64),
+    (E.DType.Q6K, 256, 1), (E.DType.Q6K, 512, 37), (E.DType.Q6K, 2304, 64), (E.DType.Q6K, 512, 256),
+    (E.DType.Q6K, 512, 1024), (E.DType.Q6K, 1024, 256),
     (E.DType.Q8_0, 32, 1), (E.DType.Q8_0, 96, 13), (E.DType.Q8_0, 1024, 70),
 ]
 
