@@ -345,6 +345,36 @@ def decode_config5(ctx: Context, contexts=(1024, 16384), steps: int = 20, warmup
         eng.free()
 
 
+def decode_config1(ctx: Context, steps: int = 64, warmup: int = 3) -> dict:
+    """Config 1: Qwen3-0.6B with every matrix Q8_0 and the output head tied to token_embd
+    (28 layers, 151936-row head), KV f16 keys and 8-bit values: the 16-token prompt through
+    Engine::prefill, then greedy decode steps timed end to end as Engine::step runs them.
+    The 28 layers hold copies of one seeded layer, each its own HBM copy."""
+    c = synth.qwen3_config("qwen3-0.6b")
+    t = synth.qwen3("qwen3-0.6b-q8_0", c, "q8_0", "ones", shared_layers=True)
+    prompt = synth.prompt("qwen3-0.6b-q8_0", 16, c.n_vocab)
+    eng = E.Engine(ctx, t, c, len(prompt) + warmup + steps + 8, E.KvPrecision.F16_KEYS_Q8_VALUES, profile=EAGER)
+    try:
+        mats = [v for v in t.values() if isinstance(v, tuple)]
+        weight_bytes = sum(m[2] * E.row_bytes(m[0], m[1]) for m in mats)  # the head is token_embd
+        tok = int(np.argmax(eng.prefill(prompt)))
+        for _ in range(warmup):
+            tok = int(np.argmax(eng.step(tok)))
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            tok = int(np.argmax(eng.step(tok)))
+        wall = (time.perf_counter() - t0) / steps
+        eng.load([tok], batched=False)
+        dev = float(np.median([ctx.replay_timed(eng.decode) for _ in range(5)])) / 1e9
+        return {"model": "Qwen3-0.6B Q8_0 (28 layers, head tied to token_embd)", "kv": "f16 keys, 8-bit values",
+                "prompt": len(prompt), "steps": steps, "weight_bytes_per_token": weight_bytes,
+                "launches_per_token": eng.decode.launches(), "tok_s": round(1.0 / wall, 1),
+                "ms_per_token": round(wall * 1e3, 3), "device_ms_per_token": round(dev * 1e3, 3),
+                "gbs_device": round(weight_bytes / dev / 1e9, 1)}
+    finally:
+        eng.free()
+
+
 def cpu_baseline(w: DecodeWorkload, budget_s: float = 15.0) -> dict:
     """skyla-ref Matrix::matvec restated in C (oracle/), timed on this host: layer passes of
     the same 7 matvecs until about budget_s seconds have elapsed."""
@@ -425,7 +455,7 @@ def main() -> int:
         return 0
     if args.e2e_only:
         e2e = decode_config5(ctx, tuple(int(v) for v in args.e2e_only.split(",")))
-        print(json.dumps({"decode_e2e_config5": e2e}))
+        print(json.dumps({"decode_e2e_config5": e2e, "decode_e2e_config1": decode_config1(ctx)}))
         ctx.free()
         return 0
     log(f"device {ctx.device_name()}; building {args.layers}-layer decode workload")
@@ -467,8 +497,10 @@ def main() -> int:
     if moe:
         log(f"MoE layer (config 4): {moe}")
     e2e = None if args.no_e2e else decode_config5(ctx)
+    e2e1 = None if args.no_e2e else decode_config1(ctx)
     if e2e:
         log(f"end-to-end decode (config 5): {e2e}")
+        log(f"end-to-end decode (config 1): {e2e1}")
     cpu = None if args.no_cpu else cpu_baseline(w, args.cpu_seconds)
     if cpu:
         log(f"cpu baseline {cpu['value']} GB/s on {cpu['cores']} threads")
@@ -515,6 +547,7 @@ def main() -> int:
         "prefill_gemm_m512": prefill,
         "moe_layer_config4": moe,
         "decode_e2e_config5": e2e,
+        "decode_e2e_config1": e2e1,
         "cpu_baseline": cpu,
     }
     step.free()
