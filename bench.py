@@ -43,6 +43,7 @@ from skyla_hip.abi import Context  # noqa: E402
 # Recordings replay as one HIP graph; with --eager they replay as direct launches of the
 # same launch list (the runtime's profiled-recording path), for tools that trace launches.
 EAGER = False
+FUSE = "qkv"  # the decode graph's fusion level in the end-to-end runs (Engine fuse)
 
 HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, vendor peak
 MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense FP16 MFMA, vendor peak
@@ -297,7 +298,7 @@ def decode_config5(ctx: Context, contexts=(1024, 16384), steps: int = 20, warmup
     c = synth.qwen3_config("qwen3-8b")
     t = synth.qwen3("qwen3-8b-q4_k_m", c, "q4_k_m", "ones", shared_layers=True)
     max_ctx = max(contexts) + warmup + steps + 8
-    eng = E.Engine(ctx, t, c, max_ctx, E.KvPrecision.F16_KEYS_Q8_VALUES, profile=EAGER)
+    eng = E.Engine(ctx, t, c, max_ctx, E.KvPrecision.F16_KEYS_Q8_VALUES, profile=EAGER, fuse=FUSE)
     try:
         a, kvl = eng.arena, eng.arena.kv_layout
         kv_dim = c.n_head_kv * c.head_dim
@@ -435,9 +436,11 @@ def main() -> int:
                     help="replay recordings as direct launches instead of one HIP graph")
     ap.add_argument("--calibrate", action="store_true",
                     help="run only the two known-size kernels that scale rocprofv3 FETCH_SIZE/WRITE_SIZE")
+    ap.add_argument("--fuse", choices=["none", "qkv", "ffn", "all"], default="qkv",
+                    help="the decode graph's fusion level in the end-to-end runs")
     args = ap.parse_args()
-    global EAGER
-    EAGER = args.eager
+    global EAGER, FUSE
+    EAGER, FUSE = args.eager, args.fuse
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: every box of this build has a single MI355X, and "
               f"the path shards across GPUs only by design (rows of the dense matrices, experts of the MoE); "

@@ -47,6 +47,11 @@ struct MatvecPush2F {
 struct MatvecPushGlu {
   uint32_t o0, o1, x_off, y_off, n_in, n_out, ids_off, x_stride, y_stride, u0, u1;
 };
+// matvec_q4k_glun: matvec_q4k_glu's words, then the norm weights and eps (13 words)
+struct MatvecPushGluN {
+  uint32_t o0, o1, x_off, y_off, n_in, n_out, ids_off, x_stride, y_stride, u0, u1, aux_off;
+  float eps;
+};
 struct MatvecPush4F {
   uint32_t o0, o1, o2, o3, x_off, y_off, n_in, n_out, ids_off, x_stride, y_stride, aux_off;
   float eps;
@@ -127,7 +132,7 @@ SK_DEV float4 fuse4(float4 v, float4 aux, float &ss) {
     v.y = v.y / (1.0f + expf(-v.y)) * aux.y;
     v.z = v.z / (1.0f + expf(-v.z)) * aux.z;
     v.w = v.w / (1.0f + expf(-v.w)) * aux.w;
-  } else if constexpr (MODE == 2) {
+  } else if constexpr (MODE == 2 || MODE == 4) {
     ss += ((v.x * v.x + v.y * v.y) + v.z * v.z) + v.w * v.w;
     v = make_float4(v.x * aux.x, v.y * aux.y, v.z * aux.z, v.w * aux.w);
   }
@@ -138,21 +143,21 @@ SK_DEV float4 fuse4(float4 v, float4 aux, float &ss) {
 // barrier; after it every thread adds all of them in the same order.
 template <int MODE, int WAVES>
 SK_DEV void norm_note(float *wss, float ssp) {
-  if constexpr (MODE == 2) {
+  if constexpr (MODE == 2 || MODE == 4) {
     const float v = lane_sum<16>(ssp);
     if ((threadIdx.x & 15) == 0) wss[threadIdx.x >> 4] = v;
   }
 }
 template <int MODE, int WAVES>
 SK_DEV void norm_take(const float *wss, float &ss) {
-  if constexpr (MODE == 2) {
+  if constexpr (MODE == 2 || MODE == 4) {
 #pragma unroll
     for (int i = 0; i < 4 * WAVES; i++) ss += wss[i];
   }
 }
 template <int MODE, int ROWS, typename P>
 SK_DEV void norm_apply(float (&acc)[ROWS], float ss, const P &p) {
-  if constexpr (MODE == 2) {
+  if constexpr (MODE == 2 || MODE == 4) {
     const float r = 1.0f / sqrtf(ss / (float)p.n_in + p.eps);
 #pragma unroll
     for (int i = 0; i < ROWS; i++) acc[i] *= r;
@@ -212,10 +217,12 @@ SK_DEV void matvec_q4k_body(const uint4 *__restrict__ w, const float *x, float *
   __shared__ float2 xs[CHU];
   __shared__ float4 sc[G::RWG][G::CH_SUP][4];
   __shared__ uint32_t wmax[WAVES];
-  __shared__ float wss[MODE == 2 ? 4 * WAVES : 1];
+  __shared__ float wss[MODE == 2 || MODE == 4 ? 4 * WAVES : 1];
   // MODE 3 (gate and up in one launch): the first half of the waves computes gate rows,
-  // the second half the up rows of the same outputs, and the store writes silu(g) * u
-  constexpr bool PAIR = MODE == 3, AUX = MODE == 1 || MODE == 2;
+  // the second half the up rows of the same outputs, and the store writes silu(g) * u.
+  // MODE 4: MODE 3 with the FFN RMSNorm folded in as MODE 2 folds it (x * w staged, r
+  // applied to the gate and up sums before the SiLU)
+  constexpr bool PAIR = MODE == 3 || MODE == 4, AUX = MODE == 1 || MODE == 2 || MODE == 4;
   constexpr int OUT = PAIR ? G::RWG / 2 : G::RWG;  // outputs per workgroup
   __shared__ float ush[PAIR ? OUT : 1];
 
@@ -886,6 +893,14 @@ MV_Q8_0_F(silu, 1, 4, 1, 2, 64)
   }
 MV_Q4K_GLU(8, 1, 16)
 MV_Q4K_GLU(8, 1, 64)
+// the same with the FFN RMSNorm folded in (MODE 4): x is the raw residual
+#define MV_Q4K_GLUN(W, R, L)                                                                   \
+  extern "C" __global__ __launch_bounds__(64 * W) void matvec_q4k_glun__##W##_0_##R##_0_##L(     \
+      const uint4 *w, const float *x, float *y, const uint32_t *ids, Segments<MatvecPushGluN> m) { \
+    const uint32_t s = segment_of(m, blockIdx.x);                                            \
+    matvec_q4k_body<W, 0, R, 0, L, 4>(w, x, y, ids, segment_push(m, s), blockIdx.x - m.start[s]); \
+  }
+MV_Q4K_GLUN(8, 1, 16)
 
 // Dense variants with fewer lanes per row (more pipelined steps per lane) that the runtime
 // picks for large launches (skyla_hip.cpp, choose_variant).

@@ -86,6 +86,7 @@ const KernelInfo kKernels[] = {
     {"matvec_q8_0_norm", 5, 11, 5, 5, 0, true, true},
     {"matvec_q8_0_silu", 5, 11, 5, 5, 0, true, true},
     {"matvec_q4k_glu", 4, 11, 5, 5, 0, true, true},  // gate + up -> silu(gate) * up
+    {"matvec_q4k_glun", 4, 13, 5, 5, 0, true, true},  // the same after the FFN RMSNorm
     {"matmul", 5, 13, 3, 4, -1, false, false},
     {"moe_logits", 3, 5, 0, 0, -1, false, false},
     {"moe_route", 2, 5, 0, 0, -1, false, false, 64},  // one wave per token

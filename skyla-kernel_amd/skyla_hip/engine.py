@@ -223,7 +223,7 @@ class Kernels:
         self.batch = [_matvec(ctx, "matmul", True, 52, t, (0, 0), lanes, weights, a) for t in (0, 1, 2)]
         # decode matvecs with the RMSNorm before them / the SiLU gate folded in (compiled for the
         # default tactics only)
-        self.norm = self.silu_mv = self.glu = None
+        self.norm = self.silu_mv = self.glu = self.glu_norm = None
         self.fuse = fuse
         if fuse != "none":
             if kq != KQUANT_TACTIC or q8 != Q8_0_TACTIC:
@@ -237,8 +237,11 @@ class Kernels:
             # Q4_K gate and up in one launch writing silu(gate) * up: eight waves, half on
             # each matrix, 16 lanes per row, 16 outputs per workgroup
             self.glu = ctx.create_pipeline_sets("matvec_q4k_glu", 4, 44, [8, 0, 1, 0, 16], len(weights))
+            # ... and the same launch with the FFN RMSNorm folded in (fuse "ffn")
+            self.glu_norm = ctx.create_pipeline_sets("matvec_q4k_glun", 4, 52, [8, 0, 1, 0, 16], len(weights))
             for i, wb in enumerate(weights):
                 self.glu.bind_set_buffers(i, [wb, a, a, a])
+                self.glu_norm.bind_set_buffers(i, [wb, a, a, a])
 
         def build(name, bufs, push):
             p = ctx.create_pipeline(name, len(bufs), push, [])
@@ -495,11 +498,12 @@ class Graph:
         self.r, self.k, self.a, self.c, self.batched = r, k, a, c, batched
         self.b = BATCH if batched else 1
         # decode with the fused matvecs (Kernels.fuse): "qkv" folds the attention norm into
-        # q/k/v; "all" also the FFN norm into gate/up, the SiLU into down and the output norm
-        # into the head
+        # q/k/v; "ffn" also the FFN norm into the Q4_K gate/up pair; "all" the FFN norm into
+        # gate/up, the SiLU into down and the output norm into the head
         fuse = getattr(k, "fuse", "none")
         on = not batched and fuse != "none" and a is not None and a.norms is not None
         self.fused = on
+        self.fused_ffn = on and fuse == "ffn"
         self.fused_all = on and fuse == "all"
 
     def stage(self, label: str) -> None:
@@ -586,15 +590,25 @@ class Graph:
                         [a.x, m.down, m.weights, n_embd, a.s_embd, used])
         self.stage("moe combine")
 
+    def glu_pair(self, gate: QMatrix, up: QMatrix) -> bool:
+        """A decode step's Q4_K gate and up of one shape and buffer run as one launch."""
+        return (self.fused and not self.fused_all and self.k.glu is not None and gate.dtype == up.dtype == DType.Q4K
+                and gate.buf == up.buf and (gate.n_in, gate.n_out) == (up.n_in, up.n_out))
+
     def dense_ffn(self, gate: QMatrix, up: QMatrix, down: QMatrix, l: int = 0) -> None:
         """graph.rs:174-184 (after the ffn rmsnorm): gate, up -> silu -> down (+= x)."""
         a, c, b, bt = self.a, self.c, self.b, self.batched
-        if (self.fused and not self.fused_all and self.k.glu is not None and gate.dtype == up.dtype == DType.Q4K
-                and gate.buf == up.buf and (gate.n_in, gate.n_out) == (up.n_in, up.n_out)):
+        if self.glu_pair(gate, up):
             # gate and up in one launch that writes silu(gate) * up: no silu_mul launch
+            # ("ffn": from the raw residual, with the FFN norm folded in: no rmsnorm launch)
             g, u = gate.off, up.off
             push = [g[0], g[1], a.n, a.gate, gate.n_in, gate.n_out, 0, 0, 0, u[0], u[1]]
-            self.r.dispatch_set(self.k.glu, gate.buf, [-(-gate.n_out // 16), 1, 1], push)
+            kern = self.k.glu
+            if self.fused_ffn:
+                push[2] = a.x
+                push += [a.norm(l, True), f32_bits(c.eps)]
+                kern = self.k.glu_norm
+            self.r.dispatch_set(kern, gate.buf, [-(-gate.n_out // 16), 1, 1], push)
             self.stage("matvec gate+up (silu)")
             self.matvec(down, (a.gate, a.s_ff), (a.x, a.s_embd), True, False)
             self.stage("matvec down")
@@ -703,7 +717,8 @@ class Graph:
             self.stage("rmsnorm")
         self.attention(l, lw.attn, rope)
         moe = lw.router is not None
-        if not self.fused_all or moe:
+        norm_folded = self.fused_all or (self.fused_ffn and self.glu_pair(lw.gate, lw.up))
+        if not norm_folded or moe:
             self.rmsnorm(a.x, lw.ffn_norm, a.n, b)
             self.stage("rmsnorm")
         if moe:
@@ -817,12 +832,15 @@ class Engine:
                  precision: KvPrecision = KvPrecision.F16_KEYS_Q8_VALUES, profile: bool = False,
                  fuse: str = "qkv"):
         """fuse (decode step only; prefill keeps the separate launches): "qkv" folds the
-        attention RMSNorm into the q/k/v matvecs; "all" also folds the FFN norm into gate/up,
-        the SiLU gate into the down projection and the output norm into the head; "none"
-        keeps graph.rs's launches.  Measured on MI355X (config 5, 1k context) "qkv" saves a
-        launch per layer for 1.3 us more in the q/k/v launch, while "all" is slower than
-        "none": each of the down (+8 to 14 us) and head (+44 us) matvec workgroups repeats
-        the elementwise work and its loads, and the fused forms hold more registers."""
+        attention RMSNorm into the q/k/v matvecs; "ffn" also the FFN norm into the Q4_K
+        gate/up pair; "all" folds the FFN norm into gate/up, the SiLU gate into the down
+        projection and the output norm into the head; "none" keeps graph.rs's launches.
+        Measured on MI355X (config 5, 1k context) "qkv" saves a launch per layer for 1.3 us
+        more in the q/k/v launch; "ffn" saves one more launch per layer, but its pair launch
+        (94 VGPRs against 75: two workgroups per CU instead of three) is slower by as much
+        (477.8 against 477.6 tok/s); "all" is slower than "none": each of the down (+8 to
+        14 us) and head (+44 us) matvec workgroups repeats the elementwise work and its
+        loads, and the fused forms hold more registers."""
         self.ctx, self.c = ctx, c
         self.weights = load_weights(ctx, model, c)
         self.arena = Arena(ctx, c, max_ctx, precision)

@@ -229,7 +229,7 @@ def test_embed_gathers_rows_bit_exact(ctx, dt):
 NEAR = 2e-2  # oracle top-2 margin, relative to the logits' std, below which a flip is noise
 
 
-@pytest.mark.parametrize("fuse", ["none", "qkv", "all"])
+@pytest.mark.parametrize("fuse", ["none", "qkv", "ffn", "all"])
 @pytest.mark.parametrize("quant", ["q8_0", "q4_k_m", "q4_k_m_mixed"])
 @pytest.mark.parametrize("precision", [P.F16, P.F16_KEYS_Q8_VALUES])
 def test_decode_top1_against_oracle(ctx, quant, precision, fuse):

@@ -210,6 +210,41 @@ def test_fused_matvec_forms(ctx, dtype, n_in, n_out, form, retile):
     assert err <= GUARD, err
 
 
+@pytest.mark.parametrize("big", [False, True])
+@pytest.mark.parametrize("n_in,n_out", [(4096, 12288), (1024, 1536), (2048, 100)])
+def test_glu_norm_pair_against_oracle(ctx, n_in, n_out, big):
+    """matvec_q4k_glun (the gate/up pair with the FFN RMSNorm folded in, from the raw
+    residual) against the oracle's rmsnorm, the two Matrix::matvec and silu * up; `big`
+    puts an eighth of the residual past f16 (3e4 to 1e5), so the staging guard rescales
+    the passes that hold it."""
+    g = synth.matrix("test-glu", f"gate-{n_in}-{n_out}", E.DType.Q4K, n_in, n_out)
+    u = synth.matrix("test-glu", f"up-{n_in}-{n_out}", E.DType.Q4K, n_in, n_out)
+    rg = synth.rng("test-glu", f"norm-{n_in}-{big}")
+    x = (rg.standard_normal(n_in) * 3).astype(np.float32)
+    if big:
+        x[: n_in // 8] *= np.float32(3e4)
+    w = rg.uniform(0.5, 1.5, n_in).astype(np.float32)
+    eps = 1e-6
+    s = Setup(ctx, [(E.DType.Q4K, n_in, n_out, g), (E.DType.Q4K, n_in, n_out, u)], n_in, n_out, extra_f32=n_in)
+    k = E.Kernels(ctx, s.weights, s.arena, fuse="ffn")
+    try:
+        s.arena.as_f32()[s.extra_off: s.extra_off + n_in] = w
+        s.set_x(x)
+        gq, uq = s.q
+        push = [gq.off[0], gq.off[1], s.x_off, s.y_off, n_in, n_out, 0, 0, 0, uq.off[0], uq.off[1], s.extra_off,
+                E.f32_bits(eps)]
+        s.run(lambda r: r.dispatch_set(k.glu_norm, gq.buf, [-(-n_out // 16), 1, 1], push))
+        got = s.y(1, n_out)[0]
+    finally:
+        s.free()
+    n = so.rmsnorm(x, w, np.float32(eps))
+    gg = so.matvec(int(E.DType.Q4K), g, n_in, n_out, n).astype(np.float64)
+    uu = so.matvec(int(E.DType.Q4K), u, n_in, n_out, n).astype(np.float64)
+    want = gg / (1.0 + np.exp(-gg)) * uu
+    assert np.isfinite(got).all()
+    assert rel_l2(got, want) <= GUARD, rel_l2(got, want)
+
+
 @pytest.mark.parametrize("n_in,n_out", [(4096, 12288), (1024, 1536), (2048, 100)])
 def test_glu_pair_equals_gate_up_then_silu(ctx, n_in, n_out):
     """matvec_q4k_glu (gate and up in one launch writing silu(gate) * up) against the two
