@@ -30,6 +30,7 @@ EXPERT_LPR = (64, 32, 16)
 
 # arena.rs:6-7
 ATTENTION_CHUNK = 64
+FUSE_LEVELS = ("none", "qkv", "ffn", "all")  # the decode graph's fusion levels (Engine fuse)
 MAX_SPLITS = 4096       # splits the attention merge weighs in LDS (kernels/attention.hip)
 BATCH = 128
 
@@ -224,6 +225,8 @@ class Kernels:
         # decode matvecs with the RMSNorm before them / the SiLU gate folded in (compiled for the
         # default tactics only)
         self.norm = self.silu_mv = self.glu = self.glu_norm = None
+        if fuse not in FUSE_LEVELS:
+            raise ValueError(f"fuse {fuse!r}: one of {', '.join(FUSE_LEVELS)}")
         self.fuse = fuse
         if fuse != "none":
             if kq != KQUANT_TACTIC or q8 != Q8_0_TACTIC:
