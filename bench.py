@@ -529,7 +529,7 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f16xf16->f32 over Q4_K/Q6_K blocks",
+        "dtype": "f32: exact integer quants x f32 activations, f32 accumulate (Q4_K/Q6_K blocks)",
         "data": "synthetic: seeded GGUF Q4_K/Q6_K blocks and N(0,1) f32 activations (config 2)",
         "config": {"workload": "config 2: Qwen3-8B decode matvecs x 36 layers (Q,K,V,O,gate,up Q4_K; "
                                "down Q6_K), one HBM copy of the weights per layer",

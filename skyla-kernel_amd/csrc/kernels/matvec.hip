@@ -9,31 +9,28 @@
 //
 // Budget that shapes the kernel: at 8 TB/s each of the 256 CUs must consume ~13 B/clk of
 // weights (~23 Q4_K values/clk) while it has 64 VALU lane-ops/clk and ~64 B/clk of L1.
-//   * Activations are staged once per workgroup in LDS as f16 pairs in the order the packed
-//     quants need them, with their per-16 sums, instead of every wave re-reading f32 x
-//     through L1 (4x the weight bytes at two rows per wave).
+//   * Activations are staged once per workgroup in LDS as f32, in the order the packed
+//     quants need them, with their per-16 sums, instead of every wave re-reading x
+//     through L1.
 //   * Each (row, super-block) header is decoded once per workgroup into f32 products
 //     d*sc and dmin*m (the reference's d0 / min0, quant.rs:60-61), so a lane's per-row work
-//     is the quant extraction, v_dot2 and four FMAs.
-//   * A quant is OR-ed into the mantissa of the f16 constant 1024.0 (0x6400), giving 1024+q
-//     exactly; v_dot2_f32_f16 multiplies two of them by two activations with f32
-//     accumulation, and the accumulator starts at -1024 * sum(x) to cancel the offset.  High
-//     nibbles are taken in place as 1024+16q (no shift) and their scale carries the 1/16.
+//     is the quant extraction, one FMA per value and four FMAs per unit.
+//   * Arithmetic is the reference's: f32 activations times exact integer quants in f32
+//     (matvec_q4k.comp:84-100).  Four quants sit in the bytes of a masked word and
+//     v_cvt_f32_ubyte0..3 turns each into an exact f32; high nibbles are taken in place as
+//     16q (no shift) and their scale carries the 1/16.  Each lane sums value * quant in
+//     f32 FMAs, so the result differs from the reference's f32 dot only in summation order.
 //   * Weight loads are 16 B per lane, 1 KiB contiguous per wave instruction, and the first
 //     step's loads are issued before the staging so they overlap it.
-// Numerics: f16 activations (relative rounding 2^-11) with f32 accumulation -- within 1e-4
-// relative L2 of the reference's f32 dot in practice, far inside the 1e-2 bar.
 #include "common.h"
-
-#define MAGIC 0x64006400u  // f16x2 {1024.0, 1024.0}
 
 namespace {
 
-struct MatvecPush2 {  // Q4_K and Q8_0 (9 words, graph.rs:30 / graph/moe.rs:251-255)
+struct MatvecPush2 {  // Q4_K and Q8_0 (9 words, graph.rs:30 / graph/moe.rs:8-24)
   uint32_t o0, o1, x_off, y_off, n_in, n_out, ids_off, x_stride, y_stride;
 };
 
-struct MatvecPush4 {  // Q6_K (11 words, graph.rs:29 / graph/moe.rs:252)
+struct MatvecPush4 {  // Q6_K (11 words, graph.rs:29 / graph/moe.rs:8-24)
   uint32_t o0, o1, o2, o3, x_off, y_off, n_in, n_out, ids_off, x_stride, y_stride;
 };
 
@@ -57,14 +54,6 @@ struct MatvecPush4F {
   float eps;
 };
 
-// (a & m) | o as one v_and_or_b32 with register operands (the compiler otherwise splits it
-// in two, because gfx9 VOP3 encodings take no literal).
-SK_DEV uint32_t and_or(uint32_t a, uint32_t m, uint32_t o) {
-  uint32_t r;
-  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(m), "v"(o));
-  return r;
-}
-
 template <int ACCUM, int ROWS, int LPR>
 SK_DEV void store_rows(float *y, uint32_t y_off, uint32_t first, uint32_t n_out, uint32_t lane,
                        const float (&acc)[ROWS]) {
@@ -81,42 +70,27 @@ SK_DEV void store_rows(float *y, uint32_t y_off, uint32_t first, uint32_t n_out,
   }
 }
 
-SK_DEV uint32_t pk(float a, float b) { return as_u32(pack_f16x2(a, b)); }
-
-// Range guard of the f16 activation staging.  A pass's activations are staged as f16, whose
-// range ends at 65504, while the reference multiplies f32 activations (matvec_q4k.comp,
-// matvec_q6k.comp, matvec_q8_0.comp) and inputs such as silu(g) * u reach 1e5-1e6.  Each
-// wave notes in its LDS word the largest |x| >= 2^15 it staged (as float bits, which order
-// like the values for x >= 0; a NaN counts as inf); lane 0 clears the word first, and one
-// wave's LDS operations complete in issue order, so only lanes holding such a value pay for
-// an LDS atomic.  A pass holding |x| >= 2^15 (or a NaN / inf, which no scaling helps) is staged
-// again as x * 2^-e, e = exponent(max) - 14, and the rows' accumulators are scaled by 2^-e
-// before that pass's steps and by 2^e after: exact powers of two, so the result is the
-// unscaled sum up to the f16 rounding of the scaled values.  Passes without large values
-// (all of them in practice) take the unscaled staging as is.
-SK_DEV float abs_max4(float4 v) { return fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))); }
-
-SK_DEV void guard_note(uint32_t *wmax, float m) {
-  uint32_t *slot = wmax + (threadIdx.x >> 6);
-  if ((threadIdx.x & 63) == 0) *slot = 0u;
-  if (!(m < 32768.0f)) atomicMax(slot, m == m ? __builtin_bit_cast(uint32_t, m) : 0x7f800000u);
+// s + sum over the four bytes b of word v of f32(b) * x[b], in byte order.  The byte
+// conversions are v_cvt_f32_ubyte0..3 (exact for 0..255).
+SK_DEV float fma_bytes(uint32_t v, float4 x, float s) {
+  s = __builtin_fmaf((float)(v & 255u), x.x, s);
+  s = __builtin_fmaf((float)((v >> 8) & 255u), x.y, s);
+  s = __builtin_fmaf((float)((v >> 16) & 255u), x.z, s);
+  s = __builtin_fmaf((float)(v >> 24), x.w, s);
+  return s;
 }
 
-// after the barrier that ends the staging: the pass's exponent (0: no scaling)
-template <int WAVES>
-SK_DEV int guard_exp(const uint32_t *wmax) {
-  uint32_t m = 0u;
-#pragma unroll
-  for (int w = 0; w < WAVES; w++) m = max(m, wmax[w]);
-  const int e = m == 0u || m >= 0x7f800000u ? 0 : (int)(m >> 23) - 127 - 14;
-  return __builtin_amdgcn_readfirstlane(e);  // the same in every lane: keep it scalar
+// sum of the 16 products of the masked bytes of q (word k holds values 4k..4k+3) with x,
+// starting from s
+SK_DEV float fma_bytes16(uint4 q, uint32_t mask, const float4 (&x)[4], float s) {
+  s = fma_bytes(q.x & mask, x[0], s);
+  s = fma_bytes(q.y & mask, x[1], s);
+  s = fma_bytes(q.z & mask, x[2], s);
+  s = fma_bytes(q.w & mask, x[3], s);
+  return s;
 }
 
-template <int ROWS>
-SK_DEV void scale_rows(float (&acc)[ROWS], int e) {
-#pragma unroll
-  for (int r = 0; r < ROWS; r++) acc[r] = __builtin_ldexpf(acc[r], e);
-}
+SK_DEV float sum4(float4 v) { return (v.x + v.y) + (v.z + v.w); }
 
 // Fused activation forms.  MODE 1 (SiLU; silu_mul.comp:15-23) stages x / (1 + e^-x) * aux:
 // the down projection reads the gate and up rows itself.  MODE 2 (RMSNorm; rmsnorm.comp,
@@ -164,27 +138,16 @@ SK_DEV void norm_apply(float (&acc)[ROWS], float ss, const P &p) {
   }
 }
 
-// Geometry shared by the three formats.
-template <int WAVES, int ROWS, int LPR>
-struct Geo {
-  static constexpr int SUBS = 64 / LPR;            // row groups per wave
-  static constexpr int RWG = WAVES * SUBS * ROWS;  // rows per workgroup
-  static constexpr int NT = 64 * WAVES;            // threads per workgroup
-  // super-blocks of activations staged per pass: keeps the decoded scales <= 32 KiB
-  static constexpr int CH_SUP = (512 / RWG) < 1 ? 1 : ((512 / RWG) > 32 ? 32 : (512 / RWG));
-  static constexpr int CH = CH_SUP * 256;          // values per pass
-};
-
 // ---------------------------------------------------------------------------------------
 // Q4_K.  Lane step = one 16 B unit of qs: unit u of a row is super-block u/8, chunk
 // c = (u/2)%4, bytes 16(u%2) + [0,16) of that chunk's 32 -- low nibbles are values
 // 64c + 16(u%2) + [0,16) of sub-block 2c, high nibbles the same positions of sub-block 2c+1
-// (quant.rs:56-66).  LDS per pass: xq[0..3][unit] = the unit's 32 activations as f16 pairs in
-// the (0,2),(1,3) order of the packed quants (low-nibble half, then high), xs[unit] = their
+// (quant.rs:56-66).  LDS per pass: xf[0..3][unit] = the 16 activations of the low-nibble
+// values, xf[4..7][unit] those of the high nibbles (f32, 4 per component), xs[unit] = their
 // two 16-value sums, and per (row, super-block, chunk) four products of the header
-// (quant.rs:40-49, 60-61): d*sc_lo, d*sc_hi/16, and the terms that multiply the two sums,
-// 1024*d*sc_lo + dmin*m_lo and 64*d*sc_hi + dmin*m_hi (the 1024 cancels the f16 offset of
-// the packed quants, so a lane's dot products start from zero).
+// (quant.rs:40-49, 60-61): d*sc_lo, d*sc_hi/16, dmin*m_lo and dmin*m_hi.  A unit adds
+//   d*sc_lo * sum(q_lo x) + d*sc_hi/16 * sum(16 q_hi x) - dmin*m_lo * sum(x_lo) - dmin*m_hi * sum(x_hi)
+// which is the reference's sum of ((d sc) q - dmin m) x regrouped.
 //
 // Every lane of a workgroup runs the same number of steps S = ceil(units / LPR): units past
 // the pass hold zero activations and zero products, so they add exactly zero, and the loop
@@ -213,10 +176,9 @@ SK_DEV void matvec_q4k_body(const uint4 *__restrict__ w, const float *x, float *
                             const uint32_t *ids, const P &p, uint32_t bx) {
   using G = GeoQ4<WAVES, ROWS, LPR>;
   constexpr int CHU = G::CHU, PF = G::PF;
-  __shared__ uint4 xq[4][CHU];  // component-major: lanes read consecutive 16 B
+  __shared__ float4 xf[8][CHU];  // component-major: lanes read consecutive 16 B
   __shared__ float2 xs[CHU];
   __shared__ float4 sc[G::RWG][G::CH_SUP][4];
-  __shared__ uint32_t wmax[WAVES];
   __shared__ float wss[MODE == 2 || MODE == 4 ? 4 * WAVES : 1];
   // MODE 3 (gate and up in one launch): the first half of the waves computes gate rows,
   // the second half the up rows of the same outputs, and the store writes silu(g) * u.
@@ -244,13 +206,13 @@ SK_DEV void matvec_q4k_body(const uint4 *__restrict__ w, const float *x, float *
   const uint32_t y_off = p.y_off + slot * p.y_stride;
   const uint32_t units = p.n_in >> 5, supers = p.n_in >> 8;
   const uint32_t c = (lane >> 1) & 3;  // chunk of this lane's units (u % 8 == lane % 8)
-  const uint32_t MW = MAGIC, LO = 0x000f000fu, HI = 0x00f000f0u;
 
   uint32_t mo0 = p.o0, mo1 = p.o1;  // this wave's matrix
   if constexpr (PAIR) {
     mo0 = __builtin_amdgcn_readfirstlane(second ? p.u0 : p.o0);
     mo1 = __builtin_amdgcn_readfirstlane(second ? p.u1 : p.o1);
   }
+  (void)mo1;
   const BufRes wq = buf_res(w + mo0, (uint64_t)(base + p.n_out) * units * 16);
   const BufRes wh = buf_res(w + p.o1, (uint64_t)(base + p.n_out) * supers * 16);
   uint32_t voff[ROWS];
@@ -269,24 +231,21 @@ SK_DEV void matvec_q4k_body(const uint4 *__restrict__ w, const float *x, float *
     // headers, then the first PF weight steps, so staging waits only for its own data.
     constexpr int XI = (4 * CHU + G::NT - 1) / G::NT;  // activation quarters per thread
     float4 xa[XI][2], xu[AUX ? XI : 1][2];
-    auto load_x = [&]() {
 #pragma unroll
-      for (int j = 0; j < XI; j++) {
-        const uint32_t t = tid + j * G::NT, u = u0 + (t >> 2), qq = t & 3;
-        xa[j][0] = xa[j][1] = make_float4(0.f, 0.f, 0.f, 0.f);  // every path defines them
-        if constexpr (AUX) xu[j][0] = xu[j][1] = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (t < 4 * nu) {
-          const uint32_t at = (u >> 3) * 256 + ((u >> 1) & 3) * 64 + (u & 1) * 16 + (qq >> 1) * 32 + (qq & 1) * 8;
-          xa[j][0] = *(const float4 *)(xv + at);
-          xa[j][1] = *(const float4 *)(xv + at + 4);
-          if constexpr (AUX) {
-            xu[j][0] = *(const float4 *)(av + at);
-            xu[j][1] = *(const float4 *)(av + at + 4);
-          }
+    for (int j = 0; j < XI; j++) {
+      const uint32_t t = tid + j * G::NT, u = u0 + (t >> 2), qq = t & 3;
+      xa[j][0] = xa[j][1] = make_float4(0.f, 0.f, 0.f, 0.f);  // every path defines them
+      if constexpr (AUX) xu[j][0] = xu[j][1] = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (t < 4 * nu) {
+        const uint32_t at = (u >> 3) * 256 + ((u >> 1) & 3) * 64 + (u & 1) * 16 + (qq >> 1) * 32 + (qq & 1) * 8;
+        xa[j][0] = *(const float4 *)(xv + at);
+        xa[j][1] = *(const float4 *)(xv + at + 4);
+        if constexpr (AUX) {
+          xu[j][0] = *(const float4 *)(av + at);
+          xu[j][1] = *(const float4 *)(av + at + 4);
         }
       }
-    };
-    load_x();
+    }
     constexpr int NH = G::RWG * G::CH_SUP, HI_T = (NH + G::NT - 1) / G::NT;  // header items
     uint4 hd[HI_T];
 #pragma unroll
@@ -307,39 +266,23 @@ SK_DEV void matvec_q4k_body(const uint4 *__restrict__ w, const float *x, float *
 
     // stage: item t = quarter t%4 of unit t/4 (values 0-7, 8-15 of the low-nibble half,
     // then of the high half); the pair sums of quarters make the unit's two 16-value sums
-    float ssp = 0.0f;  // MODE 2: this pass's sum of x^2 (first staging only)
-    auto stage_x = [&](float scale) -> float {
-      float big = 0.0f;  // largest |x| staged
+    float ssp = 0.0f;  // MODE 2: this pass's sum of x^2
 #pragma unroll
-      for (int j = 0; j < XI; j++) {
-        const uint32_t t = tid + j * G::NT, u = t >> 2, qq = t & 3;
-        float4 a = xa[j][0], b = xa[j][1];
-        if constexpr (AUX) {
-          float sq = 0.0f;
-          a = fuse4<MODE>(a, xu[j][0], sq);
-          b = fuse4<MODE>(b, xu[j][1], sq);
-          if (scale == 1.0f) ssp += sq;
-        }
-        big = fmaxf(big, fmaxf(abs_max4(a), abs_max4(b)));
-        if (scale != 1.0f) {
-          a = make_float4(a.x * scale, a.y * scale, a.z * scale, a.w * scale);
-          b = make_float4(b.x * scale, b.y * scale, b.z * scale, b.w * scale);
-        }
-        const uint32_t h0 = pk(a.x, a.z), h1 = pk(a.y, a.w), h2 = pk(b.x, b.z), h3 = pk(b.y, b.w);
-        const f16x2 one = {(f16)1.0f, (f16)1.0f};
-        float sum = dot2(as_f16x2(h0), one, 0.0f);
-        sum = dot2(as_f16x2(h1), one, sum);
-        sum = dot2(as_f16x2(h2), one, sum);
-        sum = dot2(as_f16x2(h3), one, sum);
-        sum += dpp_f<0xb1>(sum);  // + the other quarter of the same half
-        if (t < 4 * CHU) {
-          xq[qq][u] = make_uint4(h0, h1, h2, h3);
-          if ((qq & 1) == 0) ((float *)&xs[u])[qq >> 1] = sum;
-        }
+    for (int j = 0; j < XI; j++) {
+      const uint32_t t = tid + j * G::NT, u = t >> 2, qq = t & 3;
+      float4 a = xa[j][0], b = xa[j][1];
+      if constexpr (AUX) {
+        a = fuse4<MODE>(a, xu[j][0], ssp);
+        b = fuse4<MODE>(b, xu[j][1], ssp);
       }
-      return big;
-    };
-    guard_note(wmax, stage_x(1.0f));
+      float sum = sum4(a) + sum4(b);
+      sum += dpp_f<0xb1>(sum);  // + the other quarter of the same half
+      if (t < 4 * CHU) {
+        xf[(qq >> 1) * 4 + (qq & 1) * 2][u] = a;
+        xf[(qq >> 1) * 4 + (qq & 1) * 2 + 1][u] = b;
+        if ((qq & 1) == 0) ((float *)&xs[u])[qq >> 1] = sum;
+      }
+    }
     norm_note<MODE, WAVES>(wss, ssp);
     // decode: the 8 six-bit scales and mins as bytes of four words (quant.rs:40-49)
 #pragma unroll
@@ -351,7 +294,7 @@ SK_DEV void matvec_q4k_body(const uint4 *__restrict__ w, const float *x, float *
       } else if (i < NH) {
         const uint4 h = hd[j];
         const float d = f16_bits_to_f32(h.x & 0xffffu), dmin = f16_bits_to_f32(h.x >> 16);
-        const float d16 = d * 0.0625f, d1024 = d * 1024.0f, d64 = d * 64.0f;
+        const float d16 = d * 0.0625f;
         const uint32_t sw[2] = {h.y & 0x3f3f3f3fu, (h.w & 0x0f0f0f0fu) | ((h.y >> 2) & 0x30303030u)};
         const uint32_t mw[2] = {h.z & 0x3f3f3f3fu, ((h.w >> 4) & 0x0f0f0f0fu) | ((h.z >> 2) & 0x30303030u)};
 #pragma unroll
@@ -359,44 +302,34 @@ SK_DEV void matvec_q4k_body(const uint4 *__restrict__ w, const float *x, float *
           const uint32_t sv = sw[cc >> 1] >> (16 * (cc & 1)), mv = mw[cc >> 1] >> (16 * (cc & 1));
           const float s_lo = (float)(sv & 255u), s_hi = (float)((sv >> 8) & 255u);
           const float m_lo = (float)(mv & 255u), m_hi = (float)((mv >> 8) & 255u);
-          sc[lr][s][cc] = make_float4(d * s_lo, d16 * s_hi, __builtin_fmaf(d1024, s_lo, dmin * m_lo),
-                                      __builtin_fmaf(d64, s_hi, dmin * m_hi));
+          sc[lr][s][cc] = make_float4(d * s_lo, d16 * s_hi, dmin * m_lo, dmin * m_hi);
         }
       }
     }
     __syncthreads();
     norm_take<MODE, WAVES>(wss, ss);
-    const int e = guard_exp<WAVES>(wmax);
-    if (e) {  // rare: the pass again at x * 2^-e
-      load_x();
-      stage_x(__builtin_ldexpf(1.0f, -e));
-      __syncthreads();
-      scale_rows(acc, -e);
-    }
 
     const uint32_t S = (nu + LPR - 1) / LPR;
     auto step = [&](uint32_t st, const uint4 (&qj)[ROWS]) {
       const uint32_t i = lane + st * LPR;
-      const uint4 xa0 = xq[0][i], xa1 = xq[1][i], xb0 = xq[2][i], xb1 = xq[3][i];
-      const float2 xsum = xs[i];
-      const uint32_t pa[8] = {xa0.x, xa0.y, xa0.z, xa0.w, xa1.x, xa1.y, xa1.z, xa1.w};
-      const uint32_t pb[8] = {xb0.x, xb0.y, xb0.z, xb0.w, xb1.x, xb1.y, xb1.z, xb1.w};
       const uint32_t s = (lane >> 3) + st * (LPR / 8);
+      float sa[ROWS], sb[ROWS];
+      {
+        const float4 xl[4] = {xf[0][i], xf[1][i], xf[2][i], xf[3][i]};
+#pragma unroll
+        for (int r = 0; r < ROWS; r++) sa[r] = fma_bytes16(qj[r], 0x0f0f0f0fu, xl, 0.0f);
+      }
+      {
+        const float4 xh[4] = {xf[4][i], xf[5][i], xf[6][i], xf[7][i]};
+#pragma unroll
+        for (int r = 0; r < ROWS; r++) sb[r] = fma_bytes16(qj[r], 0xf0f0f0f0u, xh, 0.0f);
+      }
+      const float2 xsum = xs[i];
 #pragma unroll
       for (int r = 0; r < ROWS; r++) {
-        float sa = 0.0f, sb = 0.0f;
-        const uint32_t wd[4] = {qj[r].x, qj[r].y, qj[r].z, qj[r].w};
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-          const uint32_t w0 = wd[k], w8 = w0 >> 8;
-          sa = dot2(as_f16x2(and_or(w0, LO, MW)), as_f16x2(pa[2 * k]), sa);
-          sa = dot2(as_f16x2(and_or(w8, LO, MW)), as_f16x2(pa[2 * k + 1]), sa);
-          sb = dot2(as_f16x2(and_or(w0, HI, MW)), as_f16x2(pb[2 * k]), sb);
-          sb = dot2(as_f16x2(and_or(w8, HI, MW)), as_f16x2(pb[2 * k + 1]), sb);
-        }
         const float4 f = sc[hrow0 + r][s][c];
-        acc[r] = __builtin_fmaf(f.x, sa, acc[r]);
-        acc[r] = __builtin_fmaf(f.y, sb, acc[r]);
+        acc[r] = __builtin_fmaf(f.x, sa[r], acc[r]);
+        acc[r] = __builtin_fmaf(f.y, sb[r], acc[r]);
         acc[r] = __builtin_fmaf(-f.z, xsum.x, acc[r]);
         acc[r] = __builtin_fmaf(-f.w, xsum.y, acc[r]);
       }
@@ -414,7 +347,6 @@ SK_DEV void matvec_q4k_body(const uint4 *__restrict__ w, const float *x, float *
 #pragma unroll
     for (int j = 0; j < PF; j++)
       if (j0 + j < S) step(j0 + j, q[j]);
-    if (e) scale_rows(acc, e);
   }
   norm_apply<MODE>(acc, ss, p);
   if constexpr (PAIR) {
@@ -441,27 +373,36 @@ SK_DEV void matvec_q4k_body(const uint4 *__restrict__ w, const float *x, float *
 // Q6_K.  Lane step = 64 values of one super-block: u -> super-block u/4, half hf = (u%4)/2,
 // li = u%2.  It reads 16 B of ql at l = 16 li (a), 16 B at l + 32 (b) and 16 B of qh.
 // Group g = 0..3 is values 128 hf + 32 g + 16 li + [0,16) with scale sc[8 hf + li + 2g]
-// (quant.rs:72-87).  Groups 0,1 are built as 1024+q, groups 2,3 as 1024+16q (q the stored
-// 6-bit value, quant = q - 32).
-// LDS per pass: xq[unit] = 32 f16 pairs (4 groups x 8), xs[unit] = the 4 group sums, and per
-// (row, super-block) and (hf, li): d*sc for the lane's 4 groups (1/16 folded into g = 2, 3).
+// (quant.rs:72-87).  Each word of a group is rebuilt as four bytes q = nibble | 2 high bits
+// << 4 (the stored 6-bit value; the quant is q - 32), converted exactly to f32 and
+// multiplied with f32 activations; the group sum starts at -32 * sum(x).
+// LDS per pass: xf[4g + k][unit] = activations 4k..4k+3 of group g (f32), xs[unit] = the 4
+// group sums, and per (row, super-block) and (hf, li): d*sc for the lane's 4 groups.
 // ---------------------------------------------------------------------------------------
+template <int WAVES, int ROWS, int LPR>
+struct GeoQ6 {
+  static constexpr int RWG = WAVES * (64 / LPR) * ROWS;  // rows per workgroup
+  static constexpr int NT = 64 * WAVES;
+  // super-blocks of activations per pass: 16 KiB of f32 activations and <= 16 KiB of scales
+  static constexpr int CH_SUP = (256 / RWG) < 1 ? 1 : ((256 / RWG) > 16 ? 16 : (256 / RWG));
+  static constexpr int CH = CH_SUP * 256;          // values per pass
+};
+
 template <int WAVES, int ACCUM, int ROWS, int MOE, int LPR, int MODE = 0, typename P = MatvecPush4>
 SK_DEV void matvec_q6k_body(const uint4 *__restrict__ w, const uint16_t *__restrict__ wd,
                             const float *x, float *y, const uint32_t *ids, const P &p,
                             uint32_t bx) {
-  using G = Geo<WAVES, ROWS, LPR>;
-  __shared__ uint4 xq[8][G::CH / 64];  // component-major
+  using G = GeoQ6<WAVES, ROWS, LPR>;
+  __shared__ float4 xf[16][G::CH / 64];  // component-major
   __shared__ float4 xs[G::CH / 64];
   __shared__ float4 sc[G::RWG][G::CH_SUP][4];
-  __shared__ uint32_t wmax[WAVES];
   __shared__ float wss[MODE == 2 ? 4 * WAVES : 1];
 
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = (tid & 63) % LPR;
   const uint32_t sub = (tid & 63) / LPR;
   const uint32_t row0 = bx * G::RWG;
-  const uint32_t lrow0 = ((tid >> 6) * G::SUBS + sub) * ROWS;
+  const uint32_t lrow0 = ((tid >> 6) * (64 / LPR) + sub) * ROWS;
   const uint32_t first = row0 + lrow0;
   const uint32_t slot = blockIdx.y;
   const uint32_t base = MOE ? ids[p.ids_off + slot] * p.n_out : 0;
@@ -472,7 +413,6 @@ SK_DEV void matvec_q6k_body(const uint4 *__restrict__ w, const uint16_t *__restr
   const uint32_t y_off = p.y_off + slot * p.y_stride;
   const uint32_t supers = p.n_in >> 8;
   const uint32_t li = lane & 1, hf = (lane >> 1) & 1;
-  const uint32_t MW = MAGIC, L4 = 0x000f000fu, H4 = 0x00f000f0u, LH = 0x00300030u, HH = 0x03000300u;
 
   uint32_t rb[ROWS];
 #pragma unroll
@@ -498,8 +438,7 @@ SK_DEV void matvec_q6k_body(const uint4 *__restrict__ w, const uint16_t *__restr
         h[r] = w[p.o1 + rs * 4 + hf * 2 + li];
       }
     };
-    // activation item t = group t%4 of unit t/4: 16 values (4 x 16 B) that become 8 f16
-    // pairs and one 16-value sum (16 VGPRs in flight per item, not a whole unit's 64)
+    // activation item t = group t%4 of unit t/4: 16 values (4 x 16 B) and their sum
     const uint32_t n_xi = 4 * nu;
     float4 xu4[MODE ? 4 : 1];
     auto x_item = [&](uint32_t t, float4 (&v)[4]) {
@@ -512,28 +451,16 @@ SK_DEV void matvec_q6k_body(const uint4 *__restrict__ w, const uint16_t *__restr
         for (int k = 0; k < 4; k++) xu4[k] = *(const float4 *)(av + at + 4 * k);
       }
     };
-    float big = 0.0f;  // largest |x| this thread staged
-    float ssp = 0.0f;  // MODE 2: this pass's sum of x^2 (first staging only)
-    auto x_store = [&](uint32_t t, const float4 (&v)[4], float scale) {
+    float ssp = 0.0f;  // MODE 2: this pass's sum of x^2
+    auto x_store = [&](uint32_t t, float4 (&v)[4]) {
       const uint32_t i = t >> 2, g = t & 3;
-      const f16x2 one = {(f16)1.0f, (f16)1.0f};
-      uint32_t pp[8];
-      float s = 0.0f, sq = 0.0f;
+      if constexpr (MODE != 0) {
 #pragma unroll
-      for (int k = 0; k < 4; k++) {
-        float4 f = v[k];
-        if constexpr (MODE != 0) f = fuse4<MODE>(f, xu4[k], sq);
-        big = fmaxf(big, abs_max4(f));
-        const float4 e = scale != 1.0f ? make_float4(f.x * scale, f.y * scale, f.z * scale, f.w * scale) : f;
-        pp[2 * k] = pk(e.x, e.z);
-        pp[2 * k + 1] = pk(e.y, e.w);
-        s = dot2(as_f16x2(pp[2 * k]), one, s);
-        s = dot2(as_f16x2(pp[2 * k + 1]), one, s);
+        for (int k = 0; k < 4; k++) v[k] = fuse4<MODE>(v[k], xu4[k], ssp);
       }
-      xq[2 * g][i] = make_uint4(pp[0], pp[1], pp[2], pp[3]);
-      xq[2 * g + 1][i] = make_uint4(pp[4], pp[5], pp[6], pp[7]);
-      ((float *)&xs[i])[g] = s;
-      if (scale == 1.0f) ssp += sq;
+#pragma unroll
+      for (int k = 0; k < 4; k++) xf[4 * g + k][i] = v[k];
+      ((float *)&xs[i])[g] = (sum4(v[0]) + sum4(v[1])) + (sum4(v[2]) + sum4(v[3]));
     };
     const uint32_t n_items = (uint32_t)G::RWG * ns;
     auto h_load = [&](uint32_t i, uint4 &sv, uint32_t &dv) {
@@ -553,7 +480,7 @@ SK_DEV void matvec_q6k_body(const uint4 *__restrict__ w, const uint16_t *__restr
         for (int g = 0; g < 4; g++) {
           const uint32_t k = 8 * (lp >> 1) + (lp & 1) + 2 * g;
           const int s8 = (int)(int8_t)((sw[k >> 2] >> (8 * (k & 3))) & 255u);
-          o[g] = d * (float)s8 * (g >= 2 ? 0.0625f : 1.0f);
+          o[g] = d * (float)s8;
         }
         sc[lr][s][lp] = make_float4(o[0], o[1], o[2], o[3]);
       }
@@ -566,29 +493,19 @@ SK_DEV void matvec_q6k_body(const uint4 *__restrict__ w, const uint16_t *__restr
     if (tid < n_items) h_load(tid, sv0, dv0);
 #pragma unroll
     for (int j = 0; j < PF; j++) load(min(lane + j * LPR, nu - 1), qa[j], qb[j], qh[j]);
-    if (tid < n_xi) x_store(tid, xv4, 1.0f);
+    if (tid < n_xi) x_store(tid, xv4);
     if (tid < n_items) h_store(tid, sv0, dv0);
     for (uint32_t t = tid + G::NT; t < n_xi; t += G::NT) {
       x_item(t, xv4);
-      x_store(t, xv4, 1.0f);
+      x_store(t, xv4);
     }
     for (uint32_t i = tid + G::NT; i < n_items; i += G::NT) {
       h_load(i, sv0, dv0);
       h_store(i, sv0, dv0);
     }
-    guard_note(wmax, big);
     norm_note<MODE, WAVES>(wss, ssp);
     __syncthreads();
     norm_take<MODE, WAVES>(wss, ss);
-    const int e = guard_exp<WAVES>(wmax);
-    if (e) {  // rare: the pass again at x * 2^-e
-      for (uint32_t t = tid; t < n_xi; t += G::NT) {
-        x_item(t, xv4);
-        x_store(t, xv4, __builtin_ldexpf(1.0f, -e));
-      }
-      __syncthreads();
-      scale_rows(acc, -e);
-    }
 
     for (uint32_t j0 = 0; lane + j0 * LPR < nu; j0 += PF) {
 #pragma unroll
@@ -596,28 +513,26 @@ SK_DEV void matvec_q6k_body(const uint4 *__restrict__ w, const uint16_t *__restr
         const uint32_t i = lane + (j0 + j) * LPR;
         if (i < nu) {
           const float4 xsum = xs[i];
-          const float ib[4] = {-1056.0f * xsum.x, -1056.0f * xsum.y, -1536.0f * xsum.z, -1536.0f * xsum.w};
+          const float ib[4] = {-32.0f * xsum.x, -32.0f * xsum.y, -32.0f * xsum.z, -32.0f * xsum.w};
           const uint32_t s = i >> 2;
 #pragma unroll
           for (int r = 0; r < ROWS; r++) {
             float t[4];
             // group g: quants from ql half a (g even) or b (g odd), low nibbles for g < 2 and
-            // high for g >= 2; qh bits 2g, 2g+1 land on bits 4-5 (g < 2) or 8-9 of each lane.
-            // One group's operands are live at a time (157 -> 108 VGPRs).
+            // high for g >= 2; qh bits 2g, 2g+1 of each byte moved to bits 4-5.  One group's
+            // operands are live at a time.
 #pragma unroll
             for (int g = 0; g < 4; g++) {
-              const uint4 x0 = xq[2 * g][i], x1 = xq[2 * g + 1][i];
-              const uint32_t px[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+              const float4 xg[4] = {xf[4 * g][i], xf[4 * g + 1][i], xf[4 * g + 2][i], xf[4 * g + 3][i]};
               const uint4 qv = (g & 1) ? qb[j][r] : qa[j][r];
-              const uint32_t wv[4] = {qv.x, qv.y, qv.z, qv.w};
+              const uint32_t wv4[4] = {qv.x, qv.y, qv.z, qv.w};
               const uint32_t hv[4] = {qh[j][r].x, qh[j][r].y, qh[j][r].z, qh[j][r].w};
-              const uint32_t QM = g < 2 ? L4 : H4, HM = g < 2 ? LH : HH, SH = (g & 1) ? 2 : 4;
               float tg = ib[g];
 #pragma unroll
               for (int k = 0; k < 4; k++) {
-                const uint32_t w0 = wv[k], w8 = w0 >> 8, h0 = hv[k] << SH, h8 = (hv[k] >> 8) << SH;
-                tg = dot2(as_f16x2(and_or(h0, HM, and_or(w0, QM, MW))), as_f16x2(px[2 * k]), tg);
-                tg = dot2(as_f16x2(and_or(h8, HM, and_or(w8, QM, MW))), as_f16x2(px[2 * k + 1]), tg);
+                const uint32_t lo = g < 2 ? wv4[k] : wv4[k] >> 4;
+                const uint32_t hb = g == 0 ? hv[k] << 4 : g == 1 ? hv[k] << 2 : g == 2 ? hv[k] : hv[k] >> 2;
+                tg = fma_bytes((lo & 0x0f0f0f0fu) | (hb & 0x30303030u), xg[k], tg);
               }
               t[g] = tg;
               __builtin_amdgcn_sched_barrier(0);
@@ -633,7 +548,6 @@ SK_DEV void matvec_q6k_body(const uint4 *__restrict__ w, const uint16_t *__restr
         __builtin_amdgcn_sched_barrier(0);  // each refill right behind the step it replaces
       }
     }
-    if (e) scale_rows(acc, e);
   }
   norm_apply<MODE>(acc, ss, p);
   store_rows<ACCUM, ROWS, LPR>(y, y_off, first, p.n_out, lane, acc);
@@ -641,26 +555,35 @@ SK_DEV void matvec_q6k_body(const uint4 *__restrict__ w, const uint16_t *__restr
 
 // ---------------------------------------------------------------------------------------
 // Q8_0.  Lane step = 16 quants (half a block) of one row; the block scale d is staged per
-// (row, block) as f32.  q as f16: (q ^ 0x80) is 0..255, so MAGIC | that = 1152 + q.
-// LDS per pass: xq[unit] = 8 f16 pairs, xs[unit] = their sum, dd[row][block] = d.
+// (row, block) as f32.  q ^ 0x80 is q + 128 as a byte (0..255), converted exactly to f32;
+// the unit's sum starts at -128 * sum(x), then takes d.
+// LDS per pass: xf[k][unit] = activations 4k..4k+3 (f32), xs[unit] = their sum,
+// dd[row][block] = d.
 // ---------------------------------------------------------------------------------------
+template <int WAVES, int ROWS, int LPR>
+struct GeoQ8 {
+  static constexpr int RWG = WAVES * (64 / LPR) * ROWS;  // rows per workgroup
+  static constexpr int NT = 64 * WAVES;
+  // values per pass: 32 KiB of f32 activations and <= 32 KiB of block scales
+  static constexpr int CH = (8192 * 8 / RWG) > 8192 ? 8192 : (8192 * 8 / RWG);
+};
+
 template <int WAVES, int ACCUM, int ROWS, int MOE, int LPR, int MODE = 0, typename P = MatvecPush2>
 SK_DEV void matvec_q8_0_body(const uint4 *__restrict__ w, const uint16_t *__restrict__ wd,
                              const float *x, float *y, const uint32_t *ids, const P &p,
                              uint32_t bx) {
-  using G = Geo<WAVES, ROWS, LPR>;
+  using G = GeoQ8<WAVES, ROWS, LPR>;
   constexpr int NBLK = G::CH / 32;
-  __shared__ uint4 xq[2][G::CH / 16];  // component-major
+  __shared__ float4 xf[4][G::CH / 16];  // component-major
   __shared__ float xs[G::CH / 16];
   __shared__ float dd[G::RWG][NBLK];
-  __shared__ uint32_t wmax[WAVES];
   __shared__ float wss[MODE == 2 ? 4 * WAVES : 1];
 
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = (tid & 63) % LPR;
   const uint32_t sub = (tid & 63) / LPR;
   const uint32_t row0 = bx * G::RWG;
-  const uint32_t lrow0 = ((tid >> 6) * G::SUBS + sub) * ROWS;
+  const uint32_t lrow0 = ((tid >> 6) * (64 / LPR) + sub) * ROWS;
   const uint32_t first = row0 + lrow0;
   const uint32_t slot = blockIdx.y;
   const uint32_t base = MOE ? ids[p.ids_off + slot] * p.n_out : 0;
@@ -670,7 +593,6 @@ SK_DEV void matvec_q8_0_body(const uint4 *__restrict__ w, const uint16_t *__rest
   float ss = 0.0f;
   const uint32_t y_off = p.y_off + slot * p.y_stride;
   const uint32_t chunks = p.n_in >> 4, blocks = p.n_in >> 5;
-  const uint32_t MW = MAGIC, M8 = 0x00ff00ffu;
 
   const uint4 *qr[ROWS];
 #pragma unroll
@@ -693,27 +615,15 @@ SK_DEV void matvec_q8_0_body(const uint4 *__restrict__ w, const uint16_t *__rest
         for (int k = 0; k < 4; k++) xu4[k] = *(const float4 *)(av + at + 4 * k);
       }
     };
-    float big = 0.0f;  // largest |x| this thread staged
-    float ssp = 0.0f;  // MODE 2: this pass's sum of x^2 (first staging only)
-    auto x_store = [&](uint32_t i, const float4 (&v)[4], float scale) {
-      uint32_t pp[8];
-      const f16x2 one = {(f16)1.0f, (f16)1.0f};
-      float s = 0.0f, sq = 0.0f;
+    float ssp = 0.0f;  // MODE 2: this pass's sum of x^2
+    auto x_store = [&](uint32_t i, float4 (&v)[4]) {
+      if constexpr (MODE != 0) {
 #pragma unroll
-      for (int k = 0; k < 4; k++) {
-        float4 f = v[k];
-        if constexpr (MODE != 0) f = fuse4<MODE>(f, xu4[k], sq);
-        big = fmaxf(big, abs_max4(f));
-        const float4 e = scale != 1.0f ? make_float4(f.x * scale, f.y * scale, f.z * scale, f.w * scale) : f;
-        pp[2 * k] = pk(e.x, e.z);
-        pp[2 * k + 1] = pk(e.y, e.w);
-        s = dot2(as_f16x2(pp[2 * k]), one, s);
-        s = dot2(as_f16x2(pp[2 * k + 1]), one, s);
+        for (int k = 0; k < 4; k++) v[k] = fuse4<MODE>(v[k], xu4[k], ssp);
       }
-      xq[0][i] = make_uint4(pp[0], pp[1], pp[2], pp[3]);
-      xq[1][i] = make_uint4(pp[4], pp[5], pp[6], pp[7]);
-      xs[i] = s;
-      if (scale == 1.0f) ssp += sq;
+#pragma unroll
+      for (int k = 0; k < 4; k++) xf[k][i] = v[k];
+      xs[i] = (sum4(v[0]) + sum4(v[1])) + (sum4(v[2]) + sum4(v[3]));
     };
     const uint32_t n_items = (uint32_t)G::RWG * nb;
     auto d_load = [&](uint32_t i) -> uint32_t {
@@ -734,45 +644,31 @@ SK_DEV void matvec_q8_0_body(const uint4 *__restrict__ w, const uint16_t *__rest
 #pragma unroll
       for (int r = 0; r < ROWS; r++) q[j][r] = qr[r][u0 + i];
     }
-    if (tid < nu) x_store(tid, xv4, 1.0f);
+    if (tid < nu) x_store(tid, xv4);
     if (tid < n_items) dd[tid / nb][tid % nb] = f16_bits_to_f32(dv0);
     for (uint32_t i = tid + G::NT; i < nu; i += G::NT) {
       x_unit(i, xv4);
-      x_store(i, xv4, 1.0f);
+      x_store(i, xv4);
     }
     for (uint32_t i = tid + G::NT; i < n_items; i += G::NT) dd[i / nb][i % nb] = f16_bits_to_f32(d_load(i));
-    guard_note(wmax, big);
     norm_note<MODE, WAVES>(wss, ssp);
     __syncthreads();
     norm_take<MODE, WAVES>(wss, ss);
-    const int e = guard_exp<WAVES>(wmax);
-    if (e) {  // rare: the pass again at x * 2^-e
-      for (uint32_t i = tid; i < nu; i += G::NT) {
-        x_unit(i, xv4);
-        x_store(i, xv4, __builtin_ldexpf(1.0f, -e));
-      }
-      __syncthreads();
-      scale_rows(acc, -e);
-    }
 
     for (uint32_t j0 = 0; lane + j0 * LPR < nu; j0 += PF) {
 #pragma unroll
       for (int j = 0; j < PF; j++) {
         const uint32_t i = lane + (j0 + j) * LPR;
         if (i < nu) {
-          const uint4 x0 = xq[0][i], x1 = xq[1][i];
-          const uint32_t px[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-          const float bias = -1152.0f * xs[i];
+          const float4 xk[4] = {xf[0][i], xf[1][i], xf[2][i], xf[3][i]};
+          const float bias = -128.0f * xs[i];
 #pragma unroll
           for (int r = 0; r < ROWS; r++) {
             float s = bias;
-            const uint32_t wv[4] = {q[j][r].x, q[j][r].y, q[j][r].z, q[j][r].w};
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-              const uint32_t b = wv[k] ^ 0x80808080u;
-              s = dot2(as_f16x2(and_or(b, M8, MW)), as_f16x2(px[2 * k]), s);
-              s = dot2(as_f16x2(and_or(b >> 8, M8, MW)), as_f16x2(px[2 * k + 1]), s);
-            }
+            s = fma_bytes(q[j][r].x ^ 0x80808080u, xk[0], s);
+            s = fma_bytes(q[j][r].y ^ 0x80808080u, xk[1], s);
+            s = fma_bytes(q[j][r].z ^ 0x80808080u, xk[2], s);
+            s = fma_bytes(q[j][r].w ^ 0x80808080u, xk[3], s);
             acc[r] = __builtin_fmaf(dd[lrow0 + r][i >> 1], s, acc[r]);
           }
         }
@@ -781,7 +677,6 @@ SK_DEV void matvec_q8_0_body(const uint4 *__restrict__ w, const uint16_t *__rest
         for (int r = 0; r < ROWS; r++) q[j][r] = qr[r][u0 + inext];
       }
     }
-    if (e) scale_rows(acc, e);
   }
   norm_apply<MODE>(acc, ss, p);
   store_rows<ACCUM, ROWS, LPR>(y, y_off, first, p.n_out, lane, acc);

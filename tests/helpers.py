@@ -17,6 +17,22 @@ def rel_l2(got: np.ndarray, want: np.ndarray) -> float:
     return float(np.linalg.norm(got - want) / max(np.linalg.norm(want), 1e-30))
 
 
+# Floor of the f32 bar: a plain f32 reordering of a short dot product can land much closer
+# to the oracle than one of 4096 terms by chance.
+F32_FLOOR = 2e-6
+
+
+def f32_reorder_bar(dtype, data, n_in: int, n_out: int, x, want) -> float:
+    """Twice the relative L2 distance between a plain f32 reordering of the same product
+    (numpy's float32 W @ x over the oracle's dequantised rows: blocked BLAS sums) and the
+    oracle's sequential f32 dot (matrix.rs:50-53), floored at F32_FLOOR.  A kernel that
+    multiplies f32 activations by the exact quants in f32 lands inside it."""
+    from oracle import skyla_oracle as so
+
+    w = so.dequantize(int(dtype), data, n_in * n_out).reshape(n_out, n_in)
+    return max(2.0 * rel_l2(w @ np.asarray(x, np.float32), want), F32_FLOOR)
+
+
 def pad64(n: int) -> int:
     return -(-n // 64) * 64
 

@@ -5,10 +5,9 @@ and its merge, the embedding gather), then end to end: the engine's decode of se
 Qwen3 models against skyla-ref's Model (oracle/model.py), teacher-forced on the oracle's
 greedy tokens, with no top-1 disagreement (north_star).  The oracle stores its KV cache the
 way the reference's GPU backend does for the precision under test (qkv_prep.comp:48-65:
-f16 rows or q8 blocks); the GPU path still stages the matvec activations as f16 where the
-reference multiplies f32 (about 2e-3 relative on the logits), so a step whose oracle top-2
-margin is below that noise (NEAR) may legitimately flip: such steps are counted and must
-stay rare, not failed one by one.
+f16 rows or q8 blocks).  Every step's top-1 is compared: the tests print the number of
+disagreements, the smallest oracle top-2 margin met and the worst logits distance, and
+assert that no step disagrees.
 """
 import numpy as np
 import pytest
@@ -226,7 +225,26 @@ def test_embed_gathers_rows_bit_exact(ctx, dt):
         b.free()
 
 
-NEAR = 2e-2  # oracle top-2 margin, relative to the logits' std, below which a flip is noise
+class Top1:
+    """Top-1 bookkeeping of a teacher-forced decode: disagreements, the smallest oracle top-2
+    margin (relative to the logits' std) and the worst logits relative L2."""
+
+    def __init__(self):
+        self.flips, self.steps, self.worst, self.margin = 0, 0, 0.0, np.inf
+        self.last = None
+
+    def judge(self, gl, ol):
+        self.steps += 1
+        self.worst = max(self.worst, rel_l2(gl, ol))
+        top = np.argsort(ol)[::-1][:2]
+        self.margin = min(self.margin, float((ol[top[0]] - ol[top[1]]) / ol.std()))
+        self.flips += int(np.argmax(gl)) != so.argmax(ol)
+        self.last = so.argmax(ol)
+
+    def report(self, what):
+        print(f"{what}: {self.steps} steps, top-1 disagreements {self.flips}, smallest oracle "
+              f"top-2 margin {self.margin:.2e} std, worst logits rel-L2 {self.worst:.2e}")
+
 
 
 @pytest.mark.parametrize("fuse", ["none", "qkv", "ffn", "all"])
@@ -243,22 +261,14 @@ def test_decode_top1_against_oracle(ctx, quant, precision, fuse):
     oracle = Model(c, tensors, (precision.keys_q8, precision.values_q8))
     eng = E.Engine(ctx, tensors, c, 64, precision, fuse=fuse)
     try:
-        bad = near = 0
-        worst = 0.0
+        t = Top1()
         tok = synth.prompt(CFG, 1, c.n_vocab)[0]
         for _ in range(32):                      # 32 greedy steps, teacher-forced
-            gl, ol = eng.step(tok), oracle.forward(tok)
-            worst = max(worst, rel_l2(gl, ol))
-            top = np.argsort(ol)[::-1][:2]
-            if int(np.argmax(gl)) != int(top[0]):
-                if ol[top[0]] - ol[top[1]] < NEAR * ol.std():
-                    near += 1
-                else:
-                    bad += 1
-            tok = so.argmax(ol)
-        assert bad == 0, (bad, near, worst)
-        assert near <= 1, near
-        assert worst < 2e-2, worst
+            t.judge(eng.step(tok), oracle.forward(tok))
+            tok = t.last
+        t.report(f"tiny {quant} {precision.name} fuse={fuse}")
+        assert t.flips == 0, t.flips
+        assert t.worst < 1e-3, t.worst
     finally:
         eng.free()
 
@@ -288,47 +298,52 @@ def test_prefill_then_decode_against_oracle(ctx):
         eng.free()
 
 
+# Oracle top-2 margin (relative to the logits' std) under which a prompt that went through
+# the f16-operand prefill GEMM may flip with 8-bit values: fixed, not scaled by the error.
+NEAR = 2e-2
+
+
+@pytest.mark.parametrize("prompt_path", ["step", "prefill"])
 @pytest.mark.parametrize("precision", [P.F16, P.F16_KEYS_Q8_VALUES])
-def test_config1_qwen3_06b_greedy(ctx, precision):
+def test_config1_qwen3_06b_greedy(ctx, precision, prompt_path):
     """Config 1 (Qwen3-0.6B, Q8_0 weights, tied head, norms 1.0): the 16-token prompt of
-    uniform ids through Engine::prefill, then 64 greedy decode steps, both sides fed the
-    oracle's tokens; no top-1 disagreement outside near-ties.  With 8-bit values the two
-    sides round their cache from slightly different v rows (the GPU's matvec stages f16),
-    and a value that lands on the other side of a quantisation step moves by max|v| / 127:
-    the logits then differ by about 1.5% relative L2, so a flip also counts as a near-tie
-    when the oracle's top-2 margin is within four times that step's measured noise."""
+    uniform ids, then 64 greedy decode steps, both sides fed the oracle's tokens.
+
+    prompt_path "step": the prompt token by token through the decode graph, as skyla-ref's
+    CPU model takes it; every matvec multiplies f32 activations in f32, and no step of the
+    65 may disagree.  "prefill": the prompt through Engine::prefill, whose batched GEMM
+    multiplies f16 operands as the reference's matmul.comp does (about 1e-3 relative on its
+    k/v rows); with f16 keys and values no step may disagree either.  With 8-bit values a
+    value that the GEMM's rounding moves across a quantisation step moves by max|v| / 127,
+    which puts about 1% relative L2 on the logits: a disagreement is then allowed only at
+    a step whose oracle top-2 margin is below NEAR, at most one, and all are reported."""
     c = synth.qwen3_config("qwen3-0.6b")
     tensors = synth.qwen3("qwen3-0.6b-q8_0", c, "q8_0", "ones")
     prompt = synth.prompt("qwen3-0.6b-q8_0", 16, c.n_vocab)
     oracle = Model(c, tensors, (precision.keys_q8, precision.values_q8))
     eng = E.Engine(ctx, tensors, c, 96, precision)
     try:
-        bad = near = 0
-        worst = 0.0
-
-        def judge(gl, ol):
-            nonlocal bad, near, worst
-            err = rel_l2(gl, ol)
-            worst = max(worst, err)
-            top = np.argsort(ol)[::-1][:2]
-            if int(np.argmax(gl)) != int(top[0]):
-                if ol[top[0]] - ol[top[1]] < max(NEAR, 4 * err) * ol.std():
-                    near += 1
-                else:
-                    bad += 1
-
-        gl = eng.prefill(prompt)
-        for t in prompt:
-            ol = oracle.forward(t)
-        judge(gl, ol)
+        t = Top1()
+        if prompt_path == "prefill":
+            gl = eng.prefill(prompt)
+            for tok in prompt:
+                ol = oracle.forward(tok)
+            t.judge(gl, ol)
+        else:
+            for tok in prompt[:-1]:
+                eng.step(tok)
+                oracle.forward(tok)
+            t.judge(eng.step(prompt[-1]), oracle.forward(prompt[-1]))
         for _ in range(64):
-            tok = so.argmax(ol)
-            gl, ol = eng.step(tok), oracle.forward(tok)
-            judge(gl, ol)
+            t.judge(eng.step(t.last), oracle.forward(t.last))
+        t.report(f"config 1 {precision.name} prompt by {prompt_path}")
         assert eng.pos == oracle.pos == 80
-        assert bad == 0, (bad, near, worst)
-        assert near <= 3, near
-        assert worst < (1e-2 if precision == P.F16 else 2e-2), worst
+        if prompt_path == "prefill" and precision.values_q8:
+            assert t.flips <= 1 and (t.flips == 0 or t.margin < NEAR), (t.flips, t.margin)
+            assert t.worst < 2e-2, t.worst
+        else:
+            assert t.flips == 0, (t.flips, t.margin)
+            assert t.worst < (1e-3 if prompt_path == "step" else 1e-2), t.worst
     finally:
         eng.free()
 

@@ -1,13 +1,15 @@
 """GPU parity of the decode matvec and the bit-exact dequantisation (through the C-ABI).
 
 Bar: dequantised weights bit-exact against the oracle (quant.rs restated); matvec within
-1e-2 relative L2 of the oracle's f32 Matrix::matvec (the kernels
-actually land near 1e-4, so a tighter 2e-3 regression guard is asserted too).
+1e-2 relative L2 of the oracle's f32 Matrix::matvec and, since
+the kernels multiply f32 activations by the exact quants in f32 as the reference does,
+within twice what a plain f32 reordering of the same product gives (f32_reorder_bar,
+about 1.5e-6 to 2.5e-6 at the Qwen3-8B shapes).
 """
 import numpy as np
 import pytest
 
-from helpers import Setup, env, pad64, rel_l2
+from helpers import F32_FLOOR, Setup, env, f32_reorder_bar, pad64, rel_l2
 from oracle import skyla_oracle as so
 from skyla_hip import engine as E
 from skyla_hip import synth
@@ -15,7 +17,7 @@ from skyla_hip import synth
 pytestmark = pytest.mark.gpu
 
 TOL = 1e-2
-GUARD = 2e-3   # what the f16-activation kernels must keep
+F32 = 1e-5     # f32 arithmetic, where the product is composed with other f32 work (norm, SiLU)
 
 
 def _dequant_gpu(ctx, dtype, n_in, n_out, data):
@@ -72,7 +74,8 @@ def test_matvec_small(ctx, dtype, n_in, n_out, accum):
     want = so.matvec(int(dtype), data, n_in, n_out, x)
     # ACCUM adds y0 on the GPU; judge the matvec part (y0 + dot may cancel)
     err = rel_l2(got - y0, want)
-    assert err <= GUARD, err
+    bar = f32_reorder_bar(dtype, data, n_in, n_out, x, want) + (4e-7 if accum else 0.0)
+    assert err <= bar, (err, bar)
 
 
 @pytest.mark.parametrize("tactic", [(1, 1), (1, 2), (2, 2), (2, 4), (4, 1), (4, 2), (4, 4), (8, 1), (8, 2)])
@@ -91,7 +94,7 @@ def test_matvec_tactics(ctx, tactic):
             s.matvec(i)
             got = s.y(1, n_out)[0]
             want = so.matvec(int(dt), data, n_in, n_out, x)
-            assert rel_l2(got, want) <= GUARD, (dt, tactic)
+            assert rel_l2(got, want) <= f32_reorder_bar(dt, data, n_in, n_out, x, want), (dt, tactic)
     finally:
         s.free()
 
@@ -117,7 +120,9 @@ def test_matvec_qwen3_8b_shapes(ctx, name, dtype, n_in, n_out):
         s.free()
     want = so.matvec(int(dtype), data, n_in, n_out, x)
     err = rel_l2(got, want)
-    assert err <= TOL and err <= GUARD, err
+    bar = f32_reorder_bar(dtype, data, n_in, n_out, x, want)
+    print(f"{name}: rel-L2 {err:.3e}, plain f32 reordering bar {bar:.3e}")
+    assert err <= TOL and err <= bar, (err, bar)
 
 
 def test_matvec_linearity_full_size(ctx):
@@ -135,7 +140,7 @@ def test_matvec_linearity_full_size(ctx):
             outs.append(s.y(1, n_out)[0].astype(np.float64))
     finally:
         s.free()
-    assert rel_l2(outs[2], outs[0] + outs[1]) <= GUARD
+    assert rel_l2(outs[2], outs[0] + outs[1]) <= 4 * F32_FLOOR
 
 
 @pytest.mark.parametrize("dtype,n_in,n_out", [
@@ -143,9 +148,8 @@ def test_matvec_linearity_full_size(ctx):
     (E.DType.Q6K, 12288, 4096), (E.DType.Q8_0, 1024, 70), (E.DType.Q8_0, 3072, 301),
 ])
 def test_matvec_large_activations(ctx, dtype, n_in, n_out):
-    """Activations past the f16 range (silu(gate) * up reaches 1e5-1e6 in real checkpoints;
-    the reference multiplies them in f32): the kernels' staging guard rescales the passes
-    that hold them by a power of two, the others stay as they are."""
+    """Activations past the f16 range (silu(gate) * up reaches 1e5-1e6 in real checkpoints):
+    multiplied in f32, as the reference does, with the same f32 bar."""
     data = synth.matrix("test-big", f"{dtype.name}-{n_in}-{n_out}", dtype, n_in, n_out)
     x = synth.activations("test-big", f"x-{n_in}", n_in)
     x[: n_in // 3] *= np.float32(3e5)
@@ -161,7 +165,7 @@ def test_matvec_large_activations(ctx, dtype, n_in, n_out):
     want = so.matvec(int(dtype), data, n_in, n_out, x)
     assert np.isfinite(got).all()
     err = rel_l2(got, want)
-    assert err <= GUARD, err
+    assert err <= f32_reorder_bar(dtype, data, n_in, n_out, x, want), err
 
 
 FUSED = [(E.DType.Q4K, 4096, 301), (E.DType.Q4K, 4096, 6144), (E.DType.Q4K, 12288, 4096),
@@ -185,7 +189,7 @@ def test_fused_matvec_forms(ctx, dtype, n_in, n_out, form, retile):
         y0 = np.zeros(n_out, np.float32)
     else:
         aux = g.standard_normal(n_in).astype(np.float32)
-        aux[: n_in // 8] *= np.float32(2e4)   # past f16: the staging guard rescales those passes
+        aux[: n_in // 8] *= np.float32(2e4)   # silu(g) * u past the f16 range, as in real checkpoints
         y0 = g.standard_normal(n_out).astype(np.float32)
     c = E.Config(n_embd=n_in, eps=1e-6)
     with env(SKYLA_HIP_RETILE=retile):
@@ -207,7 +211,7 @@ def test_fused_matvec_forms(ctx, dtype, n_in, n_out, form, retile):
     want = so.matvec(int(dtype), data, n_in, n_out, xin)
     assert np.isfinite(got).all()
     err = rel_l2(got - y0, want)
-    assert err <= GUARD, err
+    assert err <= F32, err
 
 
 @pytest.mark.parametrize("big", [False, True])
@@ -215,8 +219,7 @@ def test_fused_matvec_forms(ctx, dtype, n_in, n_out, form, retile):
 def test_glu_norm_pair_against_oracle(ctx, n_in, n_out, big):
     """matvec_q4k_glun (the gate/up pair with the FFN RMSNorm folded in, from the raw
     residual) against the oracle's rmsnorm, the two Matrix::matvec and silu * up; `big`
-    puts an eighth of the residual past f16 (3e4 to 1e5), so the staging guard rescales
-    the passes that hold it."""
+    puts an eighth of the residual past the f16 range (3e4 to 1e5)."""
     g = synth.matrix("test-glu", f"gate-{n_in}-{n_out}", E.DType.Q4K, n_in, n_out)
     u = synth.matrix("test-glu", f"up-{n_in}-{n_out}", E.DType.Q4K, n_in, n_out)
     rg = synth.rng("test-glu", f"norm-{n_in}-{big}")
@@ -242,7 +245,7 @@ def test_glu_norm_pair_against_oracle(ctx, n_in, n_out, big):
     uu = so.matvec(int(E.DType.Q4K), u, n_in, n_out, n).astype(np.float64)
     want = gg / (1.0 + np.exp(-gg)) * uu
     assert np.isfinite(got).all()
-    assert rel_l2(got, want) <= GUARD, rel_l2(got, want)
+    assert rel_l2(got, want) <= F32, rel_l2(got, want)
 
 
 @pytest.mark.parametrize("n_in,n_out", [(4096, 12288), (1024, 1536), (2048, 100)])

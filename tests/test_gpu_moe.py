@@ -18,6 +18,8 @@ from skyla_hip import engine as E
 from skyla_hip import synth
 
 pytestmark = pytest.mark.gpu
+# decode: f32 matvecs composed with f32 SiLU and combine; prefill: f16-input GEMMs
+F32 = 1e-5
 
 CFG = "qwen3-30b-a3b-moe"
 N_EMBD, N_FF_EXP, N_EXPERT, N_USED = 2048, 768, 128, 8
@@ -241,7 +243,7 @@ def test_moe_decode_token(ctx, moe):
     assert list(a.u32()[m.ids: m.ids + N_USED]) == list(ids)
     assert np.allclose(a.f32()[m.weights: m.weights + N_USED], w, rtol=1e-5)
     got = moe.rows(a.x, a.s_embd, 1, N_EMBD)[0] - x0[0]
-    assert rel_l2(got, out) <= 2e-3
+    assert rel_l2(got, out) <= F32, rel_l2(got, out)  # expert matvecs in f32, as the reference
 
 
 def test_moe_prefill_chunk(ctx, moe):
@@ -299,4 +301,4 @@ def test_moe_decode_expert_variant_choice(ctx, moe):
     assert ids["1"] == ids["0"]
     assert rel_l2(got["1"], got["0"]) < 1e-5
     out, _, _ = _oracle_moe(moe, n[0])
-    assert rel_l2(got["1"], out) <= 2e-3
+    assert rel_l2(got["1"], out) <= F32
