@@ -70,14 +70,24 @@ SK_DEV void store_rows(float *y, uint32_t y_off, uint32_t first, uint32_t n_out,
   }
 }
 
-// s + sum over the four bytes b of word v of f32(b) * x[b], in byte order.  The byte
-// conversions are v_cvt_f32_ubyte0..3 (exact for 0..255).
+// s + sum over the four bytes b of word v of f32(b) * x[b], in byte order: four
+// v_cvt_f32_ubyte0..3 (exact for 0..255) and four FMAs.
 SK_DEV float fma_bytes(uint32_t v, float4 x, float s) {
   s = __builtin_fmaf((float)(v & 255u), x.x, s);
   s = __builtin_fmaf((float)((v >> 8) & 255u), x.y, s);
   s = __builtin_fmaf((float)((v >> 16) & 255u), x.z, s);
   s = __builtin_fmaf((float)(v >> 24), x.w, s);
   return s;
+}
+
+// A mask constant the compiler cannot see through, held in an SGPR.  With a visible
+// constant such as 0x0f0f0f0f the compiler knows which bits of the masked word are zero
+// and extracts each byte with its own v_bfe_u32 before a v_cvt_f32_ubyte0 (two VALU per
+// quant), instead of one v_and_b32 per word and v_cvt_f32_ubyte0..3 (one per quant).
+SK_DEV uint32_t opaque_mask(uint32_t c) {
+  uint32_t r;
+  asm volatile("s_mov_b32 %0, %1" : "=s"(r) : "i"(c));
+  return r;
 }
 
 // sum of the 16 products of the masked bytes of q (word k holds values 4k..4k+3) with x,
@@ -206,6 +216,7 @@ SK_DEV void matvec_q4k_body(const uint4 *__restrict__ w, const float *x, float *
   const uint32_t y_off = p.y_off + slot * p.y_stride;
   const uint32_t units = p.n_in >> 5, supers = p.n_in >> 8;
   const uint32_t c = (lane >> 1) & 3;  // chunk of this lane's units (u % 8 == lane % 8)
+  const uint32_t LO4 = opaque_mask(0x0f0f0f0fu), HI4 = opaque_mask(0xf0f0f0f0u);
 
   uint32_t mo0 = p.o0, mo1 = p.o1;  // this wave's matrix
   if constexpr (PAIR) {
@@ -317,12 +328,12 @@ SK_DEV void matvec_q4k_body(const uint4 *__restrict__ w, const float *x, float *
       {
         const float4 xl[4] = {xf[0][i], xf[1][i], xf[2][i], xf[3][i]};
 #pragma unroll
-        for (int r = 0; r < ROWS; r++) sa[r] = fma_bytes16(qj[r], 0x0f0f0f0fu, xl, 0.0f);
+        for (int r = 0; r < ROWS; r++) sa[r] = fma_bytes16(qj[r], LO4, xl, 0.0f);
       }
       {
         const float4 xh[4] = {xf[4][i], xf[5][i], xf[6][i], xf[7][i]};
 #pragma unroll
-        for (int r = 0; r < ROWS; r++) sb[r] = fma_bytes16(qj[r], 0xf0f0f0f0u, xh, 0.0f);
+        for (int r = 0; r < ROWS; r++) sb[r] = fma_bytes16(qj[r], HI4, xh, 0.0f);
       }
       const float2 xsum = xs[i];
 #pragma unroll
@@ -370,6 +381,164 @@ SK_DEV void matvec_q4k_body(const uint4 *__restrict__ w, const float *x, float *
 }
 
 // ---------------------------------------------------------------------------------------
+// Q4_K, K-split form for n_in = 4096 (the Qwen3-8B q, k, v, o, gate and up rows).  The
+// workgroup's eight waves split every row it owns by super-blocks: wave w takes units
+// 16w .. 16w+15 (super-blocks 2w, 2w+1), lane l the unit 16w + l%16 of the rows of its slot
+// l/16.  A lane's 32 activations are therefore the same for every row it touches: they are
+// loaded once, into registers, with their two 16-value sums, and no activation goes
+// through LDS.  A row-group is 4 slots x RPL rows; its weights (one 16 B unit per lane and
+// row) and headers (16 B per row and super-block) are loaded one group ahead of the
+// arithmetic.  Each wave decodes its own headers into the products d*sc_lo, d*sc_hi/16,
+// dmin*m_lo and dmin*m_hi (quant.rs:40-49, 60-61) in a region of LDS that only it touches,
+// so no workgroup barrier is needed there; a lane's unit sum is reduced over its 16 lanes
+// with DPP, and the eight waves' partial rows meet in LDS once, at the end, added in wave
+// order.
+// MODE 2 (RMSNorm folded in: x * w in the registers, the totals scaled by r) and MODE 3
+// (gate and up of the same outputs in one launch: slots 0, 1 take gate rows, 2, 3 the same
+// rows of up, and the store writes silu(gate) * up) as in the forms above.
+// ---------------------------------------------------------------------------------------
+template <int ACCUM, int RPL, int NG, int MODE = 0, typename P = MatvecPush2>
+SK_DEV void matvec_q4k_ks_body(const uint4 *__restrict__ w, const float *x, float *y, const P &p,
+                               uint32_t bx) {
+  constexpr bool PAIR = MODE == 3;
+  constexpr int RG = 4 * RPL;             // rows per row-group
+  constexpr int OG = PAIR ? RG / 2 : RG;  // outputs per row-group
+  constexpr int OUT = OG * NG;            // outputs per workgroup
+  constexpr int CPL = RG / 8;             // header chunks each lane decodes per row-group
+  static_assert(RG % 8 == 0 && CPL >= 1 && CPL <= 4, "two headers per row, 64 lanes");
+  __shared__ float4 hp[8][RG][2][4];      // per wave: row, super-block, chunk
+  __shared__ float part[8][RG * NG];
+  __shared__ float wss[MODE == 2 ? 8 : 1];
+
+  const uint32_t tid = threadIdx.x, wv = tid >> 6, l = tid & 63;
+  const uint32_t ul = l & 15, slot = l >> 4;
+  const uint32_t unit = wv * 16 + ul;  // of the row's 128
+  const uint32_t sbl = ul >> 3;        // the unit's super-block is 2 wv + sbl
+  const uint32_t c = (unit >> 1) & 3;  // its chunk
+  const uint32_t LO4 = opaque_mask(0x0f0f0f0fu), HI4 = opaque_mask(0xf0f0f0f0u);
+  const uint32_t out0 = bx * OUT;
+
+  // row (clamped) and matrix regions of (group g, slot s, row r of the slot)
+  auto row_of = [&](uint32_t g, uint32_t s, uint32_t r) -> uint32_t {
+    const uint32_t o = out0 + g * OG + (PAIR ? (s & 1) : s) * RPL + r;
+    return min(o, p.n_out - 1);
+  };
+  auto regions = [&](uint32_t s, uint32_t &q_off, uint32_t &h_off) {
+    q_off = p.o0;
+    h_off = p.o1;
+    if constexpr (PAIR) {
+      if (s >= 2) {
+        q_off = p.u0;
+        h_off = p.u1;
+      }
+    }
+  };
+  uint32_t qo, ho;
+  regions(slot, qo, ho);
+  // the header this lane decodes: h = (l * CPL) / 4, chunks (l * CPL) % 4 + [0, CPL)
+  const uint32_t hh = (l * CPL) >> 2, hc0 = (l * CPL) & 3;
+  const uint32_t h_rl = hh >> 1, h_sb = hh & 1;  // its row of the group and super-block
+  uint32_t hqo, hho;
+  regions(h_rl / RPL, hqo, hho);
+  (void)hqo;
+
+  auto load_group = [&](uint32_t g, uint4 (&q)[RPL], uint4 &h) {
+    h = w[hho + (size_t)row_of(g, h_rl / RPL, h_rl % RPL) * 16 + 2 * wv + h_sb];
+#pragma unroll
+    for (int r = 0; r < RPL; r++) q[r] = w[qo + (size_t)row_of(g, slot, r) * 128 + unit];
+  };
+
+  // activations first: they are what every row waits on
+  const uint32_t at = (unit >> 3) * 256 + c * 64 + (unit & 1) * 16;
+  const float *xv = x + p.x_off;
+  float4 xl[4], xh[4];
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    xl[k] = *(const float4 *)(xv + at + 4 * k);
+    xh[k] = *(const float4 *)(xv + at + 32 + 4 * k);
+  }
+  uint4 qc[RPL], hc;
+  load_group(0, qc, hc);
+  if constexpr (MODE == 2) {  // x * w (the norm weights sit at aux_off), and sum(x^2)
+    const float *wn = x + p.aux_off;
+    float sq = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const float4 a = *(const float4 *)(wn + at + 4 * k), b = *(const float4 *)(wn + at + 32 + 4 * k);
+      xl[k] = fuse4<2>(xl[k], a, sq);
+      xh[k] = fuse4<2>(xh[k], b, sq);
+    }
+    sq = lane_sum<16>(slot == 0 ? sq : 0.0f);  // each value once: slot 0's lanes
+    if (l == 0) wss[wv] = sq;
+  }
+  const float sl = (sum4(xl[0]) + sum4(xl[1])) + (sum4(xl[2]) + sum4(xl[3]));
+  const float sh = (sum4(xh[0]) + sum4(xh[1])) + (sum4(xh[2]) + sum4(xh[3]));
+
+#pragma unroll
+  for (int g = 0; g < NG; g++) {
+    uint4 qn[RPL], hn;
+    if (g + 1 < NG) load_group(g + 1, qn, hn);
+    // decode this group's headers into the wave's products
+    {
+      const float d = f16_bits_to_f32(hc.x & 0xffffu), dmin = f16_bits_to_f32(hc.x >> 16);
+      const float d16 = d * 0.0625f;
+      const uint32_t sw[2] = {hc.y & 0x3f3f3f3fu, (hc.w & 0x0f0f0f0fu) | ((hc.y >> 2) & 0x30303030u)};
+      const uint32_t mw[2] = {hc.z & 0x3f3f3f3fu, ((hc.w >> 4) & 0x0f0f0f0fu) | ((hc.z >> 2) & 0x30303030u)};
+#pragma unroll
+      for (int i = 0; i < CPL; i++) {
+        const uint32_t cc = hc0 + i;
+        const uint32_t sv = (cc < 2 ? sw[0] : sw[1]) >> (16 * (cc & 1));
+        const uint32_t mv = (cc < 2 ? mw[0] : mw[1]) >> (16 * (cc & 1));
+        hp[wv][h_rl][h_sb][cc] = make_float4(d * (float)(sv & 255u), d16 * (float)((sv >> 8) & 255u),
+                                             dmin * (float)(mv & 255u), dmin * (float)((mv >> 8) & 255u));
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < RPL; r++) {
+      const float sa = fma_bytes16(qc[r], LO4, xl, 0.0f);
+      const float sb = fma_bytes16(qc[r], HI4, xh, 0.0f);
+      const float4 f = hp[wv][slot * RPL + r][sbl][c];
+      float v = f.x * sa;
+      v = __builtin_fmaf(f.y, sb, v);
+      v = __builtin_fmaf(-f.z, sl, v);
+      v = __builtin_fmaf(-f.w, sh, v);
+      v = lane_sum<16>(v);
+      if (ul == 0) part[wv][g * RG + slot * RPL + r] = v;
+    }
+    if (g + 1 < NG) {
+#pragma unroll
+      for (int r = 0; r < RPL; r++) qc[r] = qn[r];
+      hc = hn;
+    }
+  }
+  __syncthreads();
+  if (tid < (uint32_t)OUT && out0 + tid < p.n_out) {
+    const uint32_t g = tid / OG, o = tid % OG;
+    float t = 0.0f, u = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      t += part[i][g * RG + o];
+      if constexpr (PAIR) u += part[i][g * RG + 2 * RPL + o];
+    }
+    if constexpr (MODE == 2) {
+      float s2 = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 8; i++) s2 += wss[i];
+      t *= 1.0f / sqrtf(s2 / (float)p.n_in + p.eps);
+    }
+    const uint32_t yo = p.y_off + out0 + tid;
+    if constexpr (PAIR) {
+#pragma clang fp contract(off)
+      y[yo] = t / (1.0f + expf(-t)) * u;  // silu_mul.comp:15-23
+    } else if (ACCUM) {
+      y[yo] += t;
+    } else {
+      y[yo] = t;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------
 // Q6_K.  Lane step = 64 values of one super-block: u -> super-block u/4, half hf = (u%4)/2,
 // li = u%2.  It reads 16 B of ql at l = 16 li (a), 16 B at l + 32 (b) and 16 B of qh.
 // Group g = 0..3 is values 128 hf + 32 g + 16 li + [0,16) with scale sc[8 hf + li + 2g]
@@ -413,6 +582,7 @@ SK_DEV void matvec_q6k_body(const uint4 *__restrict__ w, const uint16_t *__restr
   const uint32_t y_off = p.y_off + slot * p.y_stride;
   const uint32_t supers = p.n_in >> 8;
   const uint32_t li = lane & 1, hf = (lane >> 1) & 1;
+  const uint32_t LO4 = opaque_mask(0x0f0f0f0fu), H2 = opaque_mask(0x30303030u);
 
   uint32_t rb[ROWS];
 #pragma unroll
@@ -532,7 +702,7 @@ SK_DEV void matvec_q6k_body(const uint4 *__restrict__ w, const uint16_t *__restr
               for (int k = 0; k < 4; k++) {
                 const uint32_t lo = g < 2 ? wv4[k] : wv4[k] >> 4;
                 const uint32_t hb = g == 0 ? hv[k] << 4 : g == 1 ? hv[k] << 2 : g == 2 ? hv[k] : hv[k] >> 2;
-                tg = fma_bytes((lo & 0x0f0f0f0fu) | (hb & 0x30303030u), xg[k], tg);
+                tg = fma_bytes((lo & LO4) | (hb & H2), xg[k], tg);
               }
               t[g] = tg;
               __builtin_amdgcn_sched_barrier(0);
@@ -593,6 +763,7 @@ SK_DEV void matvec_q8_0_body(const uint4 *__restrict__ w, const uint16_t *__rest
   float ss = 0.0f;
   const uint32_t y_off = p.y_off + slot * p.y_stride;
   const uint32_t chunks = p.n_in >> 4, blocks = p.n_in >> 5;
+  const uint32_t SG = opaque_mask(0x80808080u);
 
   const uint4 *qr[ROWS];
 #pragma unroll
@@ -665,10 +836,10 @@ SK_DEV void matvec_q8_0_body(const uint4 *__restrict__ w, const uint16_t *__rest
 #pragma unroll
           for (int r = 0; r < ROWS; r++) {
             float s = bias;
-            s = fma_bytes(q[j][r].x ^ 0x80808080u, xk[0], s);
-            s = fma_bytes(q[j][r].y ^ 0x80808080u, xk[1], s);
-            s = fma_bytes(q[j][r].z ^ 0x80808080u, xk[2], s);
-            s = fma_bytes(q[j][r].w ^ 0x80808080u, xk[3], s);
+            s = fma_bytes(q[j][r].x ^ SG, xk[0], s);
+            s = fma_bytes(q[j][r].y ^ SG, xk[1], s);
+            s = fma_bytes(q[j][r].z ^ SG, xk[2], s);
+            s = fma_bytes(q[j][r].w ^ SG, xk[3], s);
             acc[r] = __builtin_fmaf(dd[lrow0 + r][i >> 1], s, acc[r]);
           }
         }
@@ -807,3 +978,36 @@ MV_Q6K(8, 0, 1, 0, 32)
 MV_Q6K(8, 1, 1, 0, 32)
 MV_Q6K(4, 0, 1, 0, 16)
 MV_Q6K(4, 1, 1, 0, 16)
+
+// K-split Q4_K form for n_in = 4096 (matvec_q4k_ks_body): RPL rows per slot, NG row-groups
+// per workgroup; the runtime picks it for dense Q4_K launches whose rows all have n_in 4096.
+#define MV_Q4K_KS(A, R, G)                                                                   \
+  extern "C" __global__ __launch_bounds__(512) void matvec_q4k_ks__##A##_##R##_##G(           \
+      const uint4 *w, const float *x, float *y, const uint32_t *ids, Segments<MatvecPush2> m) { \
+    const uint32_t s = segment_of(m, blockIdx.x);                                            \
+    (void)ids;                                                                               \
+    matvec_q4k_ks_body<A, R, G>(w, x, y, segment_push(m, s), blockIdx.x - m.start[s]);       \
+  }
+#define MV_Q4K_KS_NORM(R, G)                                                                 \
+  extern "C" __global__ __launch_bounds__(512) void matvec_q4k_ks_norm__0_##R##_##G(          \
+      const uint4 *w, const float *x, float *y, const uint32_t *ids, Segments<MatvecPush2F> m) { \
+    const uint32_t s = segment_of(m, blockIdx.x);                                            \
+    (void)ids;                                                                               \
+    matvec_q4k_ks_body<0, R, G, 2>(w, x, y, segment_push(m, s), blockIdx.x - m.start[s]);    \
+  }
+#define MV_Q4K_KS_GLU(R, G)                                                                  \
+  extern "C" __global__ __launch_bounds__(512) void matvec_q4k_ks_glu__0_##R##_##G(           \
+      const uint4 *w, const float *x, float *y, const uint32_t *ids, Segments<MatvecPushGlu> m) { \
+    const uint32_t s = segment_of(m, blockIdx.x);                                            \
+    (void)ids;                                                                               \
+    matvec_q4k_ks_body<0, R, G, 3>(w, x, y, segment_push(m, s), blockIdx.x - m.start[s]);    \
+  }
+#define MV_Q4K_KS_ALL(R, G) MV_Q4K_KS(0, R, G) MV_Q4K_KS(1, R, G) MV_Q4K_KS_NORM(R, G) MV_Q4K_KS_GLU(R, G)
+MV_Q4K_KS_ALL(2, 1)
+MV_Q4K_KS_ALL(2, 2)
+MV_Q4K_KS_ALL(4, 1)
+MV_Q4K_KS_ALL(4, 2)
+MV_Q4K_KS_ALL(4, 3)
+MV_Q4K_KS_ALL(4, 6)
+MV_Q4K_KS_ALL(8, 1)
+MV_Q4K_KS_ALL(8, 3)

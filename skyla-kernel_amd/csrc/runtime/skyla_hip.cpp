@@ -148,11 +148,14 @@ struct skyla_hip_buffer {
 // rows in total uses the first alternative whose min_rows <= rows.
 struct MatvecAlt {
   hipFunction_t fn;
-  uint32_t rwg, threads;
+  uint32_t rwg, threads;  // outputs per workgroup, threads per workgroup
   uint64_t min_rows;
+  uint32_t n_in_req = 0;              // nonzero: every segment's n_in must equal it
+  uint64_t max_rows = ~uint64_t{0};   // and the launch at most this many rows
 };
 struct Retile {
-  uint32_t n_out_word;  // index of n_out in the push words
+  uint32_t n_out_word;     // index of n_out in the push words
+  uint32_t n_in_word = 4;  // index of n_in
   std::vector<MatvecAlt> alts;
 };
 
@@ -261,11 +264,15 @@ Launch pack(const Command *const *run, uint32_t n) {
   if (a.retile) {
     uint64_t rows = 0;
     for (uint32_t i = 0; i < n; i++) rows += run[i]->push[a.retile->n_out_word];
-    for (const MatvecAlt &v : a.retile->alts)
-      if (rows >= v.min_rows) {
+    for (const MatvecAlt &v : a.retile->alts) {
+      if (rows < v.min_rows || rows > v.max_rows) continue;
+      bool fits = true;
+      for (uint32_t i = 0; i < n && v.n_in_req; i++) fits &= run[i]->push[a.retile->n_in_word] == v.n_in_req;
+      if (fits) {
         alt = &v;
         break;
       }
+    }
   }
   if (alt) {
     l.fn = alt->fn;
@@ -449,26 +456,74 @@ const VariantRule kVariantRules[] = {
     {"matvec_q6k_silu", 0, 7, {{12288, 4, 1, 16}, {0, 8, 1, 32}}, 2},
 };
 
+// K-split Q4_K forms for launches whose rows all have n_in = 4096 (matvec.hip,
+// matvec_q4k_ks_body): (rows per slot, row-groups per workgroup) by launch size, from sweeps
+// on MI355X.  A workgroup of 512 threads covers 4 * rpl * ng rows (half as many outputs for
+// the gate/up pair).  Config-2 launches (us, K-split 4 x 1 against the LDS-staged forms):
+// q+k+v 6.50 / 6.71, o 5.28 / 6.13, gate+up 13.33 / 13.04 -- so launches of 16384 rows or
+// more (gate+up; 8192 outputs of the pair) stay on the LDS-staged forms.  SKYLA_HIP_KS=0
+// keeps the LDS-staged forms everywhere; SKYLA_HIP_KS=R_G forces one shape (for sweeps).
+struct KsRule {
+  uint64_t min_rows, max_rows;  // rows of the launch (outputs for the gate/up pair)
+  uint32_t rpl, ng;
+};
+const KsRule kKsRules[] = {{0, 16383, 4, 1}};
+const KsRule kKsPairRules[] = {{0, 8191, 4, 1}};
+
+void add_ks(skyla_hip_context *ctx, const char *name, const uint32_t *spec, Retile &t) {
+  const char *env = std::getenv("SKYLA_HIP_KS");
+  if (env && env[0] == '0') return;
+  std::string ks;
+  bool pair = false;
+  if (std::strcmp(name, "matvec_q4k") == 0 && spec[3] == 0)
+    ks = "matvec_q4k_ks__" + std::to_string(spec[1]);
+  else if (std::strcmp(name, "matvec_q4k_norm") == 0 && spec[1] == 0)
+    ks = "matvec_q4k_ks_norm__0";
+  else if (std::strcmp(name, "matvec_q4k_glu") == 0)
+    ks = "matvec_q4k_ks_glu__0", pair = true;
+  else
+    return;
+  std::vector<KsRule> rules(pair ? std::begin(kKsPairRules) : std::begin(kKsRules),
+                            pair ? std::end(kKsPairRules) : std::end(kKsRules));
+  uint32_t fr = 0, fg = 0;
+  if (env && std::sscanf(env, "%u_%u", &fr, &fg) == 2) rules = {{0, ~uint64_t{0}, fr, fg}};
+  std::vector<MatvecAlt> alts;
+  for (const KsRule &r : rules) {
+    hipFunction_t fn = find_function(ctx, ks + "_" + std::to_string(r.rpl) + "_" + std::to_string(r.ng));
+    if (!fn) return;  // all or nothing
+    alts.push_back({fn, (pair ? 2u : 4u) * r.rpl * r.ng, 512, r.min_rows, 4096, r.max_rows});
+  }
+  t.alts.insert(t.alts.end(), alts.begin(), alts.end());
+}
+
 std::shared_ptr<const Retile> make_retile(skyla_hip_context *ctx, const char *name, const uint32_t *spec,
                                           uint32_t n_spec) {
   if (n_spec != 5) return nullptr;
   if (const char *env = std::getenv("SKYLA_HIP_RETILE"); env && env[0] == '0') return nullptr;
+  auto t = std::make_shared<Retile>();
+  t->n_out_word = 5;
+  add_ks(ctx, name, spec, *t);
   for (const VariantRule &r : kVariantRules) {
     if (std::strcmp(r.name, name) != 0 || r.moe != spec[3]) continue;
-    auto t = std::make_shared<Retile>();
     t->n_out_word = r.n_out_word;
+    std::vector<MatvecAlt> alts;
     for (int i = 0; i < r.n; i++) {
       const auto &v = r.v[i];
       const std::string sym = std::string(name) + "__" + std::to_string(v.waves) + "_" +
                               std::to_string(spec[1]) + "_" + std::to_string(v.rows) + "_" +
                               std::to_string(spec[3]) + "_" + std::to_string(v.lpr);
       hipFunction_t fn = find_function(ctx, sym);
-      if (!fn) return nullptr;  // keep the engine's variant if any alternative is missing
-      t->alts.push_back({fn, v.waves * v.rows * (64 / v.lpr), 64 * v.waves, v.min_rows});
+      if (!fn) {  // keep the engine's variant if any alternative is missing
+        alts.clear();
+        break;
+      }
+      alts.push_back({fn, v.waves * v.rows * (64 / v.lpr), 64 * v.waves, v.min_rows});
     }
-    return t;
+    t->alts.insert(t->alts.end(), alts.begin(), alts.end());
+    break;
   }
-  return nullptr;
+  if (t->alts.empty()) return nullptr;
+  return t;
 }
 
 }  // namespace

@@ -343,7 +343,9 @@ def test_config1_qwen3_06b_greedy(ctx, precision, prompt_path):
             assert t.worst < 2e-2, t.worst
         else:
             assert t.flips == 0, (t.flips, t.margin)
-            assert t.worst < (1e-3 if prompt_path == "step" else 1e-2), t.worst
+            # 8-bit values: a v value the ~1e-6 matvec differences move across a
+            # quantisation step moves by max|v| / 127 (a few of 2.3 million per run)
+            assert t.worst < (1e-2 if prompt_path == "prefill" else 5e-3 if precision.values_q8 else 1e-3), t.worst
     finally:
         eng.free()
 

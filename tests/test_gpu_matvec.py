@@ -248,7 +248,7 @@ def test_glu_norm_pair_against_oracle(ctx, n_in, n_out, big):
     assert rel_l2(got, want) <= F32, rel_l2(got, want)
 
 
-@pytest.mark.parametrize("n_in,n_out", [(4096, 12288), (1024, 1536), (2048, 100)])
+@pytest.mark.parametrize("n_in,n_out", [(4096, 12288), (4096, 4096), (1024, 1536), (2048, 100)])
 def test_glu_pair_equals_gate_up_then_silu(ctx, n_in, n_out):
     """matvec_q4k_glu (gate and up in one launch writing silu(gate) * up) against the two
     matvecs and silu_mul on the same device: bit for bit where both run the 16-lane rows."""
@@ -282,7 +282,48 @@ def test_glu_pair_equals_gate_up_then_silu(ctx, n_in, n_out):
     finally:
         s.free()
     assert np.isfinite(got).all()
-    if 2 * n_out >= 6144:  # the plain gate+up launch runs the same (8, 1, 16) variant
+    if 2 * n_out >= 6144:  # the plain gate+up launch runs the same variant (K-split, or 8, 1, 16)
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
     else:                  # another lane split of the same sums
         assert rel_l2(got, want) <= 1e-5
+
+
+KS_SHAPES = ["2_1", "2_2", "4_1", "4_2", "4_3", "4_6", "8_1", "8_3"]
+
+
+@pytest.mark.parametrize("shape", KS_SHAPES)
+@pytest.mark.parametrize("accum", [False, True])
+def test_ks_shapes_against_oracle(ctx, shape, accum):
+    """Every compiled shape of the K-split Q4_K form (n_in = 4096; SKYLA_HIP_KS forces one)
+    over three fused segments whose row counts are not multiples of its workgroup (q, k, v
+    of 4096 + 333 + 1), ACCUM on and off, against the oracle at the f32 bar; rows past
+    n_out stay untouched."""
+    n_in, outs = 4096, [4096, 333, 1]
+    datas = [synth.matrix("test-ks", f"{i}-{n}", E.DType.Q4K, n_in, n) for i, n in enumerate(outs)]
+    x = synth.activations("test-ks", "x", n_in)
+    with env(SKYLA_HIP_KS=shape):
+        s = Setup(ctx, [(E.DType.Q4K, n_in, n, d) for n, d in zip(outs, datas)], n_in, max(outs), rows=len(outs))
+    try:
+        y0 = synth.activations("test-ks", "y0", (len(outs), s.s_out))
+        s.set_x(x)
+        s.set_y(y0)
+
+        def body(r):
+            g = E.Graph(r, s.k, None, None, False)
+            for i, m in enumerate(s.q):
+                g.matvec(m, (s.x_off, 0), (s.y_off + i * s.s_out, 0), accum, False)
+        rec = ctx.record(False, body)
+        try:
+            assert rec.launches() == 1           # the three dispatches run as one launch
+            ctx.replay(rec)
+        finally:
+            rec.free()
+        got = s.y(len(outs), s.s_out)
+    finally:
+        s.free()
+    for i, (n, d) in enumerate(zip(outs, datas)):
+        want = so.matvec(int(E.DType.Q4K), d, n_in, n, x)
+        part = got[i, :n].astype(np.float64) - (y0[i, :n] if accum else 0.0)
+        bar = f32_reorder_bar(E.DType.Q4K, d, n_in, n, x, want) + (4e-7 if accum else 0.0)
+        assert rel_l2(part, want) <= bar, (shape, i, rel_l2(part, want), bar)
+        assert np.array_equal(got[i, n:], y0[i, n:])        # rows past n_out untouched
