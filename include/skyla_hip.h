@@ -152,6 +152,19 @@ int skyla_hip_time_dispatch(skyla_hip_context *ctx, const skyla_hip_pipeline *p,
                             const uint32_t groups[3], const uint32_t *push, uint32_t n_push,
                             uint32_t reps, double *ns_out);
 
+/* No counterpart in the reference.  For callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc): one
+ * dispatch of set 0 of `p`, as skyla_hip_time_dispatch makes with reps = 1, untimed and
+ * synchronous, with no hipMalloc, hipFree or other allocating call.  The one kernel family
+ * that needs a workspace, the K split of a dense K-quant matmul, takes its partial tiles
+ * and counters from a static device array of this context's matmul code object (256 f32
+ * tiles of 128 x 128 and 1024 counters: 16 MiB + 4 KiB) instead of a workspace of its
+ * own; a launch needing more fails with SKYLA_HIP_E_OOM.  Every call on one context shares
+ * that array: calls that overlap (several host threads, or work still queued on the
+ * context stream by another caller) race. */
+int skyla_hip_dispatch_noalloc(skyla_hip_context *ctx, const skyla_hip_pipeline *p,
+                               const uint32_t groups[3], const uint32_t *push, uint32_t n_push);
+
 #ifdef __cplusplus
 }
 #endif

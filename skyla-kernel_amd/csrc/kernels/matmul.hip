@@ -1100,3 +1100,22 @@ MMX(2, 0, 0, float)
 MMX(2, 1, 0, float)
 MMX(2, 0, 1, f16)
 MMX(2, 1, 1, f16)
+
+// Workspace of skyla_hip_dispatch_noalloc, the entry point that allocates nothing: the K
+// split's f32 partial tiles (SCRATCH_TILES of 128 x 128), then its per-tile arrival
+// counters (SCRATCH_COUNTERS).  A K-split launch holds at most 256 partial tiles (row tiles
+// x token tiles x S <= 256, skyla_hip.cpp split_of) and 128 counters.  Each loaded copy of
+// this code object (one per context, so one per device) owns its array until it is
+// unloaded.  Kernels never name it: the runtime looks its device address up once per
+// context and passes that as the `ws` and `cnt` arguments, as it passes its own workspace.
+#define SCRATCH_TILES 256
+#define SCRATCH_COUNTERS 1024
+__device__ __attribute__((used)) __align__(256) unsigned char
+    scratch[SCRATCH_TILES * 128 * 128 * 4 + SCRATCH_COUNTERS * 4];
+
+// p[0, n) = v: clears the counters before an allocation-free launch (a kernel, not
+// hipMemsetAsync, so that a caller may capture it into a HIP graph)
+extern "C" __global__ __launch_bounds__(256) void fill_u32(uint32_t *p, uint32_t n, uint32_t v) {
+  const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+  if (i < n) p[i] = v;
+}

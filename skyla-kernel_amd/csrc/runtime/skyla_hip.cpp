@@ -114,12 +114,22 @@ const KernelInfo *find_kernel(const char *name) {
 
 }  // namespace
 
+// Layout of the static workspace `scratch` in the matmul code object (kernels/matmul.hip):
+// SCRATCH_TILES f32 tiles of 128 x 128, then SCRATCH_COUNTERS u32 counters.
+constexpr uint64_t kScratchTiles = 256;
+constexpr uint64_t kScratchCounters = 1024;
+
 struct skyla_hip_context {
   int device = 0;
   hipStream_t stream = nullptr;
   std::vector<hipModule_t> modules;
   std::string name;
   uint32_t warp = 64;
+  // device address of this context's copy of `scratch` (looked up once, at context_new),
+  // its size, and the fill kernel that clears its counters
+  char *scratch = nullptr;
+  size_t scratch_bytes = 0;
+  hipFunction_t fill_u32 = nullptr;
 };
 
 struct HostFree {
@@ -568,6 +578,28 @@ int skyla_hip_context_new(int device, skyla_hip_context **out) {
       return fail(SKYLA_HIP_E_DEVICE, "hipModuleLoadData: %s", hipGetErrorString(le));
     }
     ctx->modules.push_back(m);
+  }
+  // The allocation-free dispatch's workspace: the `scratch` array of the matmul code object
+  // as loaded for this device.  The code objects are loaded with hipModuleLoadData rather
+  // than registered with the runtime, so the module API's lookup (hipModuleGetGlobal) is
+  // the one that resolves its address; host code uses only this pointer, never the name.
+  {
+    hipDeviceptr_t dp = nullptr;
+    size_t bytes = 0;
+    hipError_t ge = hipModuleGetGlobal(&dp, &bytes, ctx->modules[1], "scratch");
+    if (ge != hipSuccess || !dp || bytes < kScratchTiles * 128 * 128 * 4 + kScratchCounters * 4) {
+      (void)hipGetLastError();
+      skyla_hip_context_free(ctx.release());
+      return fail(SKYLA_HIP_E_DEVICE, "hipModuleGetGlobal(scratch): %s (%zu bytes)", hipGetErrorString(ge), bytes);
+    }
+    ctx->scratch = static_cast<char *>(dp);
+    ctx->scratch_bytes = bytes;
+    hipError_t fe = hipModuleGetFunction(&ctx->fill_u32, ctx->modules[1], "fill_u32");
+    if (fe != hipSuccess || !ctx->fill_u32) {
+      (void)hipGetLastError();
+      skyla_hip_context_free(ctx.release());
+      return fail(SKYLA_HIP_E_DEVICE, "hipModuleGetFunction(fill_u32): %s", hipGetErrorString(fe));
+    }
   }
   *out = ctx.release();
   return SKYLA_HIP_OK;
@@ -1082,6 +1114,54 @@ int skyla_hip_time_dispatch(skyla_hip_context *ctx, const skyla_hip_pipeline *p,
     HIP_TRY(hipEventElapsedTime(&ms, e.ev[i], e.ev[i + 1]));
     ns_out[i] = (double)ms * 1e6;
   }
+  return SKYLA_HIP_OK;
+}
+
+int skyla_hip_dispatch_noalloc(skyla_hip_context *ctx, const skyla_hip_pipeline *p, const uint32_t groups[3],
+                               const uint32_t *push, uint32_t n_push) {
+  if (!ctx || !p || !groups || (n_push && !push)) return fail(SKYLA_HIP_E_ARG, "dispatch_noalloc: bad argument");
+  if (p->ctx != ctx) return fail(SKYLA_HIP_E_ARG, "dispatch_noalloc: pipeline of another context");
+  if (n_push != p->push_words)
+    return fail(SKYLA_HIP_E_ARG, "dispatch_noalloc: %s takes %u push words, got %u", p->symbol.c_str(),
+                p->push_words, n_push);
+  for (void *b : p->sets[0])
+    if (!b) return fail(SKYLA_HIP_E_STATE, "dispatch_noalloc: %s is not bound", p->symbol.c_str());
+  if (!ctx->scratch || !ctx->fill_u32) return fail(SKYLA_HIP_E_STATE, "dispatch_noalloc: no scratch on this context");
+  HIP_TRY(hipSetDevice(ctx->device));
+  Command c;
+  c.kind = Command::Dispatch;
+  c.fn = p->fn;
+  c.threads = p->threads;
+  c.segmented = p->segmented;
+  c.retile = p->retile;
+  c.split_fn = p->split_fn;
+  c.split_threads = p->split_threads;
+  c.tok_fn = p->tok_fn;
+  c.tok_per_wg = p->tok_per_wg;
+  for (int i = 0; i < 3; i++) c.groups[i] = groups[i];
+  c.bufs = p->sets[0];
+  c.push.assign(push, push + n_push);
+  const Command *one[1] = {&c};
+  Launch l = pack(one, 1);
+  if (l.split) {  // the K split's partials and counters live in the static scratch array
+    const uint64_t tile_cap = kScratchTiles * kSplitTileBytes;
+    if (l.ws_bytes > tile_cap || l.n_cnt > kScratchCounters)
+      return fail(SKYLA_HIP_E_OOM,
+                  "dispatch_noalloc: %s needs %llu B of partial tiles and %u counters; the static scratch holds "
+                  "%llu B and %llu",
+                  p->symbol.c_str(), (unsigned long long)l.ws_bytes, l.n_cnt, (unsigned long long)tile_cap,
+                  (unsigned long long)kScratchCounters);
+    l.ws = ctx->scratch;
+    l.cnt = ctx->scratch + tile_cap;
+    // counters start at zero: every K-split launch leaves them so, but the array keeps
+    // whatever the last call on this device left
+    void *cp = l.cnt;
+    uint32_t n = l.n_cnt, zero = 0;
+    void *fp[] = {&cp, &n, &zero};
+    HIP_TRY(hipModuleLaunchKernel(ctx->fill_u32, (n + 255) / 256, 1, 1, 256, 1, 1, 0, ctx->stream, fp, nullptr));
+  }
+  if (int s = launch(ctx->stream, l)) return s;
+  HIP_TRY(hipStreamSynchronize(ctx->stream));
   return SKYLA_HIP_OK;
 }
 

@@ -58,6 +58,7 @@ SIGNATURES = [
      [_vp, _vp, C.POINTER(C.c_char_p), C.POINTER(C.c_double), C.c_uint32, _u32p]),
     ("skyla_hip_time_dispatch", C.c_int,
      [_vp, _vp, _u32p, _u32p, C.c_uint32, C.c_uint32, C.POINTER(C.c_double)]),
+    ("skyla_hip_dispatch_noalloc", C.c_int, [_vp, _vp, _u32p, _u32p, C.c_uint32]),
 ]
 
 _lib = None
@@ -277,6 +278,11 @@ class Context:
         out = (C.c_double * reps)()
         _check(_lib.skyla_hip_time_dispatch(self._h, p._h, _u32s(groups), _u32s(push), len(push), reps, out))
         return list(out)
+
+    def dispatch_noalloc(self, p: Pipeline, groups: Sequence[int], push: Sequence[int]) -> None:
+        """One synchronous dispatch that allocates no device memory (a K-split matmul takes
+        the context's static scratch array; see include/skyla_hip.h)."""
+        _check(_lib.skyla_hip_dispatch_noalloc(self._h, p._h, _u32s(groups), _u32s(push), len(push)))
 
     def free(self) -> None:
         if self._h:
