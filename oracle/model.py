@@ -3,9 +3,11 @@ INFRASTRUCTURE ONLY.
 
 The decode step of the reference's CPU model, composed from the C restatements in
 skyla_oracle.c: Matrix::row / matvec, rmsnorm, rmsnorm_inplace, rope_neox, the attention of
-model.rs:150-169 and ffn::swiglu, with the f32 KV cache the reference keeps.  Element-wise
-additions are numpy float32 (one IEEE rounding each, as Rust's).  No RoPE scaling, no
-output gate, no recurrent layers: the dense layouts of the Qwen3 decode configurations.
+model.rs:150-169 and the two arms of Ffn::forward (ffn.rs:58-76: swiglu, or route then the
+weighted sum of the selected experts' swiglu for a qwen3moe layer), with the f32 KV cache
+the reference keeps.  Element-wise additions are numpy float32 (one IEEE rounding each, as
+Rust's).  No RoPE scaling, no output gate, no recurrent layers: the attention layouts of
+the Qwen3 decode configurations.
 
 `kv_store` selects the cache the attention reads: None keeps the reference CPU model's f32
 rows (model.rs:140-148); a pair (keys_q8, values_q8) stores every key and value row as the
@@ -30,6 +32,16 @@ class Model:
         self.k_cache = [[] for _ in range(self.c.n_layer)]
         self.v_cache = [[] for _ in range(self.c.n_layer)]
         self.pos = 0
+
+    def load_cache(self, keys: np.ndarray, values: np.ndarray) -> None:
+        """A pre-filled context: positions [0, n) of every layer's cache hold the rows
+        keys / values [n, kv_dim] (as the attention reads them back), and the next forward
+        runs at position n."""
+        n = keys.shape[0]
+        for l in range(self.c.n_layer):
+            self.k_cache[l] = [np.ascontiguousarray(keys, np.float32).reshape(-1)]
+            self.v_cache[l] = [np.ascontiguousarray(values, np.float32).reshape(-1)]
+        self.pos = n
 
     def _mv(self, name: str, x: np.ndarray) -> np.ndarray:
         dt, n_in, n_out, data = self.t[name][:4]
@@ -64,8 +76,15 @@ class Model:
             n = so.rmsnorm(x, self.t[name("attn_norm")], c.eps)
             x = x + self._attention(l, n)
             n = so.rmsnorm(x, self.t[name("ffn_norm")], c.eps)
-            g, u, d = (self.t[name(s)] for s in ("ffn_gate", "ffn_up", "ffn_down"))
-            x = x + so.swiglu(int(g[0]), g[3], int(u[0]), u[3], int(d[0]), d[3], c.n_embd, c.n_ff, n)
+            if c.n_expert:  # Ffn::Moe (ffn.rs:64-75)
+                g, u, d = (self.t[name(s)] for s in ("ffn_gate_exps", "ffn_up_exps", "ffn_down_exps"))
+                out, _, _ = so.moe_forward(self.t[name("ffn_gate_inp")], int(g[0]), g[3], int(u[0]), u[3],
+                                           int(d[0]), d[3], c.n_embd, c.n_ff_expert, c.n_expert,
+                                           c.n_expert_used, n)
+                x = x + out
+            else:           # Ffn::Dense
+                g, u, d = (self.t[name(s)] for s in ("ffn_gate", "ffn_up", "ffn_down"))
+                x = x + so.swiglu(int(g[0]), g[3], int(u[0]), u[3], int(d[0]), d[3], c.n_embd, c.n_ff, n)
         x = so.rmsnorm(x, self.t["output_norm.weight"], c.eps)
         out = self.t.get("output.weight", self.t["token_embd.weight"])
         self.pos += 1

@@ -91,7 +91,9 @@ class Planner:
         return off
 
     def table(self, data: np.ndarray) -> int:
-        data = np.ascontiguousarray(data, dtype="<f4")
+        """An f32 table (norm weights, RoPE frequencies, a [n_expert][n_embd] router) in
+        buffer 0, row-major."""
+        data = np.ascontiguousarray(data, dtype="<f4").reshape(-1)
         off = self._alloc(0, data.size * 4)
         self.tables.append((off, data))
         return off // 4

@@ -82,6 +82,9 @@ def qwen3_config(name: str):
         return Config(n_embd=4096, n_ff=12288, n_head=32, n_head_kv=8, head_dim=128, n_vocab=151936, n_layer=36)
     if name == "tiny":
         return Config(n_embd=512, n_ff=1024, n_head=4, n_head_kv=2, head_dim=128, n_vocab=2048, n_layer=3)
+    if name == "tiny-moe":  # qwen3moe at test size: 16 experts, top 4, expert FFN 256
+        return Config(n_embd=512, n_ff=1024, n_head=4, n_head_kv=2, head_dim=128, n_vocab=2048, n_layer=2,
+                      n_expert=16, n_expert_used=4, n_ff_expert=256)
     raise ValueError(f"unknown model {name}")
 
 
@@ -137,6 +140,44 @@ def qwen3(config: str, c, quant: str = "q8_0", norms: str = "ones", shared_layer
             n("ffn_gate"): mat(n("ffn_gate"), base, c.n_embd, c.n_ff),
             n("ffn_up"): mat(n("ffn_up"), base, c.n_embd, c.n_ff),
             n("ffn_down"): mat(n("ffn_down"), down, c.n_ff, c.n_embd),
+        })
+    return t
+
+
+def qwen3moe(config: str, c, norms: str = "random") -> dict:
+    """Tensor map of a qwen3moe model (config 4's layer inside the dense attention layout of
+    model.rs): attention and token_embd Q4_K, output head Q6_K, and per layer an f32 router
+    ffn_gate_inp ~ N(0, 0.02) of [n_expert][n_embd] with expert tensors ffn_{gate,up,down}_exps
+    in Q4_K, (dtype, n_in, n_out per expert, raw blocks of n_expert matrices, n_expert)
+    (weights.rs:82-84, ffn.rs:48-54)."""
+    def norm(name, n):
+        if norms == "ones":
+            return np.ones(n, np.float32)
+        return rng(config, name).uniform(0.5, 1.5, size=n).astype(np.float32)
+
+    def mat(name, dt, n_in, n_out, n_expert=1):
+        entry = (DType(dt), n_in, n_out, matrix(config, name, dt, n_in, n_out, n_expert))
+        return entry + (n_expert,) if n_expert > 1 else entry
+
+    hd, e = c.head_dim, c.n_expert
+    t = {"token_embd.weight": mat("token_embd.weight", DType.Q4K, c.n_embd, c.n_vocab),
+         "output_norm.weight": norm("output_norm.weight", c.n_embd),
+         "output.weight": mat("output.weight", DType.Q6K, c.n_embd, c.n_vocab)}
+    for i in range(c.n_layer):
+        n = lambda s: f"blk.{i}.{s}.weight"  # noqa: E731
+        t.update({
+            n("attn_norm"): norm(n("attn_norm"), c.n_embd),
+            n("ffn_norm"): norm(n("ffn_norm"), c.n_embd),
+            n("attn_q_norm"): norm(n("attn_q_norm"), hd),
+            n("attn_k_norm"): norm(n("attn_k_norm"), hd),
+            n("attn_q"): mat(n("attn_q"), DType.Q4K, c.n_embd, c.n_head * hd),
+            n("attn_k"): mat(n("attn_k"), DType.Q4K, c.n_embd, c.n_head_kv * hd),
+            n("attn_v"): mat(n("attn_v"), DType.Q4K, c.n_embd, c.n_head_kv * hd),
+            n("attn_output"): mat(n("attn_output"), DType.Q4K, c.n_head * hd, c.n_embd),
+            n("ffn_gate_inp"): router(config, n("ffn_gate_inp"), e, c.n_embd),
+            n("ffn_gate_exps"): mat(n("ffn_gate_exps"), DType.Q4K, c.n_embd, c.n_ff_expert, e),
+            n("ffn_up_exps"): mat(n("ffn_up_exps"), DType.Q4K, c.n_embd, c.n_ff_expert, e),
+            n("ffn_down_exps"): mat(n("ffn_down_exps"), DType.Q4K, c.n_ff_expert, c.n_embd, e),
         })
     return t
 

@@ -413,3 +413,90 @@ def test_attention_prep_equals_qkv_prep_then_attention(ctx, precision, pos0, hea
         assert np.array_equal(o0.view(np.uint32), o1.view(np.uint32))
     finally:
         b.free()
+
+
+def _stored_rows(kvl, kv_host, n_pos, kv_dim):
+    """Layer 0's first n_pos cache rows as the attention reads them back (f16 keys; 8-bit
+    values times their f16 scale), from the host mirror synth.fill_kv wrote."""
+    pr = kvl.precision
+    assert not pr.keys_q8 and pr.values_q8
+    k = kv_host.view("<f2")[kvl.keys(0): kvl.keys(0) + n_pos * kv_dim].astype(np.float32)
+    q = kv_host.view(np.int8)[kvl.values(0): kvl.values(0) + n_pos * kv_dim].astype(np.float32)
+    sc = kv_host.view("<f2")[kvl.value_scales(0): kvl.value_scales(0) + n_pos * kv_dim // 32].astype(np.float32)
+    v = (q.reshape(-1, 32) * sc[:, None]).reshape(n_pos, kv_dim)
+    return k.reshape(n_pos, kv_dim), v
+
+
+def test_config5_qwen3_8b_prefilled_contexts(ctx):
+    """Config 5 at full size: the 36-layer Qwen3-8B Q4_K_M decode step (Q6_K head and
+    even-layer ffn_down, every layer its own HBM copy of layer 0 / 1's seeded matrices) with
+    the f16-key / 8-bit-value cache pre-filled with N(0,1) rows to 16384 positions (256
+    splits of 64 merged) and then to 1024, three teacher-forced steps at each, against the
+    oracle Model holding the same stored rows: top-1 equal at every step, logits within
+    2e-2 relative L2 (engine.rs:137-152, arena.rs:83-181, kv.rs:33-88)."""
+    c = synth.qwen3_config("qwen3-8b")
+    t = synth.qwen3("qwen3-8b-q4_k_m", c, "q4_k_m", "ones", shared_layers=True)
+    kv_dim = c.n_head_kv * c.head_dim
+    eng = E.Engine(ctx, t, c, 16384 + 8, P.F16_KEYS_Q8_VALUES)
+    try:
+        kvl, kv_host = eng.arena.kv_layout, eng.arena.kv.host()
+        synth.fill_kv(kvl, kv_host, 16384, kv_dim, "qwen3-8b-q4_k_m")
+        eng.arena.kv.upload()
+        keys, values = _stored_rows(kvl, kv_host, 16384, kv_dim)
+        # 16384 first: the 1024 case's steps overwrite positions 1024..1026 of the fill
+        for n_ctx in (16384, 1024):
+            oracle = Model(c, t, (False, True))
+            oracle.load_cache(keys[:n_ctx], values[:n_ctx])
+            eng.pos = n_ctx
+            top = Top1()
+            tok = synth.prompt("qwen3-8b-q4_k_m", 1, c.n_vocab)[0]
+            for _ in range(3):
+                top.judge(eng.step(tok), oracle.forward(tok))
+                tok = top.last
+            top.report(f"config 5 at {n_ctx} positions")
+            assert eng.pos == oracle.pos == n_ctx + 3
+            assert top.flips == 0, (n_ctx, top.flips, top.margin)
+            assert top.worst < 2e-2, (n_ctx, top.worst)
+    finally:
+        eng.free()
+
+
+@pytest.mark.parametrize("precision", [P.F16, P.F16_KEYS_Q8_VALUES])
+def test_moe_model_from_gguf_against_oracle(ctx, tmp_path, precision):
+    """A qwen3moe model (16 experts, top 4, expert FFN 256, f32 routers) written to a GGUF
+    file, read back (reader.rs, Config::from_gguf) and decoded through the engine's MoE
+    layer (graph/moe.rs:42-80 inside graph.rs:158-185) against the oracle Model's Ffn::Moe
+    arm (ffn.rs:58-76 from model.rs:113-114): 24 greedy steps teacher-forced, no top-1
+    disagreement; then a 40-token prompt through Engine::prefill (the grouped GEMMs)."""
+    from skyla_hip import gguf as G
+    c = synth.qwen3_config("tiny-moe")
+    tensors = synth.qwen3moe(f"{CFG}-moe", c)
+    path = str(tmp_path / "tiny-moe.gguf")
+    G.write_model(path, "qwen3moe", c, tensors)
+    g = G.Gguf(path)
+    c2, t2 = G.config_from_gguf(g), G.tensors_from_gguf(g)
+    assert (c2.n_expert, c2.n_expert_used, c2.n_ff_expert, c2.n_layer) == (16, 4, 256, 2)
+    assert t2["blk.0.ffn_gate_exps.weight"][4] == 16 and t2["blk.1.ffn_gate_inp.weight"].shape == (16, c.n_embd)
+    oracle = Model(c2, t2, (precision.keys_q8, precision.values_q8))
+    eng = E.Engine(ctx, t2, c2, 96, precision)
+    try:
+        top = Top1()
+        tok = synth.prompt(f"{CFG}-moe", 1, c.n_vocab)[0]
+        for _ in range(24):
+            top.judge(eng.step(tok), oracle.forward(tok))
+            tok = top.last
+        top.report(f"qwen3moe {precision.name}")
+        assert top.flips == 0, (top.flips, top.margin)
+        assert top.worst < 1e-3, top.worst
+        eng.reset()
+        oracle.reset()
+        prompt = synth.prompt(f"{CFG}-moe-prefill", 40, c.n_vocab)
+        gl = eng.prefill(prompt)
+        for t_ in prompt:
+            ol = oracle.forward(t_)
+        err = rel_l2(gl, ol)
+        print(f"qwen3moe {precision.name} 40-token prefill: logits rel-L2 {err:.2e}")
+        assert int(np.argmax(gl)) == so.argmax(ol)
+        assert err < 2e-2, err
+    finally:
+        eng.free()
