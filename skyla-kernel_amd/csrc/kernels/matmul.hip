@@ -32,7 +32,7 @@ constexpr int TM = 128;        // rows per workgroup
 constexpr int KC = 256;        // k per LDS stage (one K-quant super-block)
 constexpr int PITCH = KC + 8;  // f16 per staged token row (16 B pad: conflict-free b128)
 
-struct MatmulPush {  // 13 words (graph.rs:28, graph/moe.rs:264-266)
+struct MatmulPush {  // 13 words (graph.rs:27-32, graph/moe.rs:26-40)
   uint32_t o0, o1, o2, o3, x_off, y_off, n_in, n_out, x_stride, y_stride, table_off, list_off,
       x_div;
 };
@@ -863,9 +863,14 @@ SK_DEV void matmul_tile128_w(const uint4 *__restrict__ w, const uint16_t *__rest
 #pragma unroll
       for (int i = 0; i < 16; i++)
         __hip_atomic_store(mine + (j * 16 + i) * 64 + lane, acc[j][i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __builtin_amdgcn_s_waitcnt(0);  // the coherent stores are done before the count
+    __builtin_amdgcn_s_waitcnt(0);  // each wave's partial stores complete before the barrier
     __syncthreads();
-    if (tid == 0) last = __hip_atomic_fetch_add(&cnt[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == S - 1;
+    // Release at agent scope: the count is made after this workgroup's partial stores are
+    // visible device-wide (buffer_wbl2 sc1 and a wait, by one thread).  The last workgroup
+    // reads the partials with agent-scope atomic loads, which go to the coherence point past
+    // the XCD's L2, so it needs no acquire-side L2 invalidate (that was the 2x cost of a
+    // full __threadfence here).
+    if (tid == 0) last = __hip_atomic_fetch_add(&cnt[tile], 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT) == S - 1;
     __syncthreads();
     if (!last) return;
 #pragma unroll

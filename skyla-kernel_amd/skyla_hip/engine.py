@@ -33,6 +33,9 @@ ATTENTION_CHUNK = 64
 FUSE_LEVELS = ("none", "qkv", "ffn", "all")  # the decode graph's fusion levels (Engine fuse)
 MAX_SPLITS = 4096       # splits the attention merge weighs in LDS (kernels/attention.hip)
 BATCH = 128
+# What the MoE kernels hold (moe.hip): moe_route keeps 4 logits per lane of one wave and
+# picks at most 16; moe_sort ranks at most 1024 slots (moe_sort.comp:15).
+MOE_MAX_EXPERTS, MOE_MAX_USED, MOE_MAX_SLOTS = 256, 16, 1024
 
 
 class DType(IntEnum):
@@ -140,7 +143,8 @@ class Planner:
 
 
 def upload_weights(ctx: Context, planner: Planner) -> list[Buffer]:
-    """Weights::load (weights.rs:245-254) plus the explicit upload a discrete GPU needs."""
+    """The buffer fill of Weights::load (weights.rs:127-136) plus the explicit upload a
+    discrete GPU needs."""
     bufs = []
     for i in range(len(planner.sizes)):
         b = ctx.alloc_host(max(16, planner.buffer_size(i)))
@@ -152,7 +156,8 @@ def upload_weights(ctx: Context, planner: Planner) -> list[Buffer]:
 
 # ---- kernels.rs ------------------------------------------------------------------------
 class Matvec:
-    """kernels.rs:55-60, 235-252."""
+    """kernels.rs:51-90 (the pipelines of one format) and 196-213 (pipeline, grouped,
+    experts)."""
 
     def __init__(self, pipelines, experts, lanes, rows_per_group):
         self.pipelines, self.experts_, self.lanes, self.rows_per_group = pipelines, experts, lanes, rows_per_group
@@ -207,7 +212,8 @@ def _fused(ctx: Context, shader: str, dual_view: bool, push: int, tactic, accum:
 
 
 class Kernels:
-    """kernels.rs:139-233, restricted to the pipelines of the quantized weight path."""
+    """Kernels::new (kernels.rs:101-184), restricted to the pipelines of the quantized
+    weight path."""
 
     def __init__(self, ctx: Context, weights: Sequence[Buffer], a: Buffer,
                  kquant_tactic=None, q8_0_tactic=None, kv: Buffer | None = None, c: Config | None = None,
@@ -454,6 +460,15 @@ class Arena:
         self.logits = single(c.n_vocab)
         stride = _next64(c.n_ff_expert)
         slots = c.n_expert_used * BATCH
+        if c.n_expert:  # the limits of the MoE kernels (moe.hip), checked before any launch
+            if c.n_expert > MOE_MAX_EXPERTS:
+                raise ValueError(f"{c.n_expert} experts: moe_route and moe_sort take at most {MOE_MAX_EXPERTS}")
+            if not 1 <= c.n_expert_used <= min(MOE_MAX_USED, c.n_expert):
+                raise ValueError(f"{c.n_expert_used} experts per token: moe_route picks 1 to "
+                                 f"{min(MOE_MAX_USED, c.n_expert)}")
+            if slots > MOE_MAX_SLOTS:
+                raise ValueError(f"{c.n_expert_used} experts x {BATCH} tokens = {slots} slots: moe_sort sorts at "
+                                 f"most {MOE_MAX_SLOTS} (moe_sort.comp:15)")
         self.moe = MoeRegions(
             logits=single(c.n_expert * BATCH), ids=single(slots), weights=single(slots),
             gate=single(stride * slots), up=single(stride * slots), down=single(self.s_embd * slots),

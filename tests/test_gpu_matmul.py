@@ -76,7 +76,7 @@ def test_matmul_range_guard_large_activations(ctx):
 
 
 @pytest.mark.parametrize("name,dtype,n_in,n_out", [
-    ("q", E.DType.Q4K, 4096, 4096), ("down", E.DType.Q6K, 12288, 4096),
+    ("q", E.DType.Q4K, 4096, 4096), ("gate", E.DType.Q4K, 4096, 12288), ("down", E.DType.Q6K, 12288, 4096),
 ])
 def test_matmul_config3(ctx, name, dtype, n_in, n_out):
     """Config 3: M = 512 tokens at the Qwen3-8B shapes (f16 activations N(0,1))."""

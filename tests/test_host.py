@@ -221,3 +221,16 @@ def test_arena_layout_follows_arena_rs():
     assert a.s_ff == 12288 and a.s_kv == 1024
     assert a.logits == a.last + 4096
     assert a.buffer == a.size * 4
+
+
+@pytest.mark.parametrize("n_expert,n_used,msg", [(257, 8, "experts: moe_route"), (128, 17, "per token"),
+                                                 (8, 9, "per token"), (64, 0, "per token"),
+                                                 (128, 9, "slots")])
+def test_arena_rejects_moe_past_kernel_limits(n_expert, n_used, msg):
+    """moe_route holds 256 logits and picks at most 16 experts; moe_sort ranks at most 1024
+    slots (8 experts x the 128-token chunk): the arena refuses such a model before anything
+    is allocated or launched, instead of the kernels clamping silently."""
+    c = E.Config(n_embd=256, n_ff=256, n_head=2, n_head_kv=1, n_vocab=64, n_layer=1,
+                 n_expert=n_expert, n_expert_used=n_used, n_ff_expert=256)
+    with pytest.raises(ValueError, match=msg):
+        E.Arena(None, c, 64)
