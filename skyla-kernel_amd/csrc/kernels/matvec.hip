@@ -49,6 +49,11 @@ struct MatvecPushGluN {
   uint32_t o0, o1, x_off, y_off, n_in, n_out, ids_off, x_stride, y_stride, u0, u1, aux_off;
   float eps;
 };
+// matvec_q4k_ecomb: an expert matvec's words, then moe_combine's residual offset, routing
+// weights offset and experts per token (12 words)
+struct MatvecPushComb {
+  uint32_t o0, o1, x_off, y_off, n_in, n_out, ids_off, x_stride, y_stride, res_off, w_off, n_used;
+};
 struct MatvecPush4F {
   uint32_t o0, o1, o2, o3, x_off, y_off, n_in, n_out, ids_off, x_stride, y_stride, aux_off;
   float eps;
@@ -183,7 +188,7 @@ struct GeoQ4 {
 
 template <int WAVES, int ACCUM, int ROWS, int MOE, int LPR, int MODE = 0, typename P = MatvecPush2>
 SK_DEV void matvec_q4k_body(const uint4 *__restrict__ w, const float *x, float *y,
-                            const uint32_t *ids, const P &p, uint32_t bx) {
+                            const uint32_t *ids, const P &p, uint32_t bx, uint32_t *cnt = nullptr) {
   using G = GeoQ4<WAVES, ROWS, LPR>;
   constexpr int CHU = G::CHU, PF = G::PF;
   __shared__ float4 xf[8][CHU];  // component-major: lanes read consecutive 16 B
@@ -193,7 +198,12 @@ SK_DEV void matvec_q4k_body(const uint4 *__restrict__ w, const float *x, float *
   // MODE 3 (gate and up in one launch): the first half of the waves computes gate rows,
   // the second half the up rows of the same outputs, and the store writes silu(g) * u.
   // MODE 4: MODE 3 with the FFN RMSNorm folded in as MODE 2 folds it (x * w staged, r
-  // applied to the gate and up sums before the SiLU)
+  // applied to the gate and up sums before the SiLU).
+  // MODE 5 (an expert down projection with moe_combine after it, MOE = 1): each slot's rows
+  // are stored with agent-scope (coherent) stores, which complete before the workgroup
+  // counts itself in cnt[bx]; the last of the grid.y slots to arrive reads the other slots'
+  // rows with agent-scope loads, adds sum_s w_s * y_s to the residual for those rows in
+  // moe_combine's order (moe_combine.comp:16-27), and resets the count.
   constexpr bool PAIR = MODE == 3 || MODE == 4, AUX = MODE == 1 || MODE == 2 || MODE == 4;
   constexpr int OUT = PAIR ? G::RWG / 2 : G::RWG;  // outputs per workgroup
   __shared__ float ush[PAIR ? OUT : 1];
@@ -264,7 +274,7 @@ SK_DEV void matvec_q4k_body(const uint4 *__restrict__ w, const float *x, float *
       const uint32_t i = tid + j * G::NT, lr = i / G::CH_SUP, s = i % G::CH_SUP;
       if constexpr (PAIR) {  // rows [0, OUT) of the gate, then the same rows of up
         if (i < NH && s < ns)
-          hd[j] = w[(lr >= (uint32_t)OUT ? p.u1 : p.o1) + min(row0 + lr % OUT, p.n_out - 1) * supers + s0 + s];
+          hd[j] = w[(lr >= (uint32_t)OUT ? p.u1 : p.o1) + (base + min(row0 + lr % OUT, p.n_out - 1)) * supers + s0 + s];
       } else {
         if (i < NH && s < ns) hd[j] = buf_load(wh, ((base + min(row0 + lr, p.n_out - 1)) * supers + s) * 16, s0 * 16);
       }
@@ -375,6 +385,32 @@ SK_DEV void matvec_q4k_body(const uint4 *__restrict__ w, const float *x, float *
         const float g = tot[r];
         y[y_off + first + r] = g / (1.0f + expf(-g)) * ush[lrow0 + r];  // silu_mul.comp:15-23
       }
+  } else if constexpr (MODE == 5) {
+    __shared__ bool last;
+#pragma unroll
+    for (int r = 0; r < ROWS; r++) {
+      const float total = lane_sum<LPR>(acc[r]);
+      if (lane == 0 && first + r < p.n_out)
+        __hip_atomic_store(y + y_off + first + r, total, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // each wave's coherent stores complete before the barrier
+    __syncthreads();
+    if (tid == 0) last = __hip_atomic_fetch_add(&cnt[bx], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.y - 1;
+    __syncthreads();
+    if (!last) return;
+    for (uint32_t t = tid; t < (uint32_t)G::RWG; t += G::NT) {
+#pragma clang fp contract(off)
+      const uint32_t row = row0 + t;
+      if (row >= p.n_out) continue;
+      float sum = 0.0f;
+      for (uint32_t s = 0; s < p.n_used; s++) {
+        const float ys = __hip_atomic_load(y + p.y_off + s * p.y_stride + row, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+        sum += y[p.w_off + s] * ys;
+      }
+      y[p.res_off + row] += sum;
+    }
+    if (tid == 0) __hip_atomic_store(&cnt[bx], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   } else {
     store_rows<ACCUM, ROWS, LPR>(y, y_off, first, p.n_out, lane, acc);
   }
@@ -1011,3 +1047,17 @@ MV_Q4K_KS_ALL(4, 3)
 MV_Q4K_KS_ALL(4, 6)
 MV_Q4K_KS_ALL(8, 1)
 MV_Q4K_KS_ALL(8, 3)
+
+// MoE decode forms the runtime substitutes for engine dispatch pairs (skyla_hip.cpp,
+// fuse_moe): an expert's gate and up with silu_mul after them (MODE 3 over the slot grid),
+// and an expert down projection with moe_combine after it (MODE 5, counters in `cnt`).
+extern "C" __global__ __launch_bounds__(256) void matvec_q4k_glu__4_0_1_1_16(
+    const uint4 *w, const float *x, float *y, const uint32_t *ids, Segments<MatvecPushGlu> m) {
+  const uint32_t s = segment_of(m, blockIdx.x);
+  matvec_q4k_body<4, 0, 1, 1, 16, 3>(w, x, y, ids, segment_push(m, s), blockIdx.x - m.start[s]);
+}
+extern "C" __global__ __launch_bounds__(256) void matvec_q4k_ecomb__4_1_16(
+    const uint4 *w, const float *x, float *y, const uint32_t *ids, Segments<MatvecPushComb> m, uint32_t *cnt) {
+  const uint32_t s = segment_of(m, blockIdx.x);
+  matvec_q4k_body<4, 0, 1, 1, 16, 5>(w, x, y, ids, segment_push(m, s), blockIdx.x - m.start[s], cnt);
+}

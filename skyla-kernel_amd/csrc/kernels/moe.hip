@@ -15,6 +15,11 @@ struct SortPush { uint32_t ids_off, table_off, list_off, n_expert, n_used; };
 struct CombinePush { uint32_t x_off, y_off, weights_off, n, stride, n_used; };
 struct SiluPush { uint32_t g_off, u_off, n, stride; };
 struct HalfPush { uint32_t src_off, dst_off, n, src_stride, dst_stride, per_token; };
+// moe_logits_route: moe_logits's words, then moe_route's (one by-value argument)
+struct LogitsRoutePush {
+  LogitsPush lp;
+  RoutePush rp;
+};
 
 // Monotone u32 key of a float with -0 folded onto +0 (so equal values tie exactly as the
 // float comparisons of moe_route.comp:66-81 do).
@@ -118,11 +123,12 @@ extern "C" __global__ __launch_bounds__(256) void moe_logits_t(const float *w, c
 // maximum (DPP within rows of 16, then two shuffles) and a ballot for the lowest expert
 // holding it.  Lane k keeps round k's choice; the exponentials are computed in parallel
 // and summed in round order, as the reference does.  Tokens at or beyond ctl[2] do nothing.
-extern "C" __global__ __launch_bounds__(64) void moe_route(float *a, uint32_t *ids, RoutePush p) {
-  const uint32_t tok = blockIdx.y;
-  const uint32_t n_tok = __builtin_bit_cast(uint32_t, a[2]);
-  if (tok >= n_tok) return;
-  const uint32_t t = threadIdx.x;
+namespace {
+// moe_route's selection for token `tok` on one wave (lane t).  COHERENT reads the logits with
+// agent-scope loads (written by other workgroups of the same launch).
+template <bool COHERENT>
+SK_DEV void route_token(const float *a, float *aw, uint32_t *ids, const RoutePush &p, uint32_t tok,
+                        uint32_t t) {
   const uint32_t n_used = min(p.n_used, 16u);
   const uint32_t n_expert = min(p.n_expert, 256u);
   const uint32_t logits_off = p.logits_off + tok * p.n_expert;
@@ -131,7 +137,11 @@ extern "C" __global__ __launch_bounds__(64) void moe_route(float *a, uint32_t *i
 #pragma unroll
   for (int j = 0; j < 4; j++) {
     const uint32_t e = t + 64 * j;
-    key[j] = e < n_expert ? max(order_key(a[logits_off + e]), 1u) : 0u;
+    float v = 0.0f;
+    if (e < n_expert)
+      v = COHERENT ? __hip_atomic_load(a + logits_off + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                   : a[logits_off + e];
+    key[j] = e < n_expert ? max(order_key(v), 1u) : 0u;
   }
   float chosen = 0.0f;
   uint32_t chosen_idx = 0;
@@ -168,8 +178,56 @@ extern "C" __global__ __launch_bounds__(64) void moe_route(float *a, uint32_t *i
   for (uint32_t k = 0; k < n_used; k++) total += __shfl(e, (int)k, 64);
   if (t < n_used) {
     ids[p.ids_off + tok * p.n_used + t] = chosen_idx;
-    a[p.weights_off + tok * p.n_used + t] = e / total;
+    aw[p.weights_off + tok * p.n_used + t] = e / total;
   }
+}
+}  // namespace
+
+extern "C" __global__ __launch_bounds__(64) void moe_route(float *a, uint32_t *ids, RoutePush p) {
+  const uint32_t tok = blockIdx.y;
+  const uint32_t n_tok = __builtin_bit_cast(uint32_t, a[2]);
+  if (tok >= n_tok) return;
+  route_token<false>(a, a, ids, p, tok, threadIdx.x);
+}
+
+// moe_logits then moe_route of one decode token in one launch (the runtime fuses the pair
+// when the engine records them back to back; no counterpart kernel in the reference).
+// Grid [n_expert, 1, 1]: each workgroup computes its logit exactly as moe_logits does and
+// stores it with an agent-scope (coherent, sc1) store, waits for it to complete and counts
+// the workgroup in cnt[0]; the last of the n_expert workgroups reads every logit back with
+// agent-scope loads (served past the XCD's L2, so no invalidate is needed), runs
+// moe_route's selection on its first wave and resets the counter.  Same logits, ids and
+// weights, bit for bit, as the two launches.  (An agent-scope release on the count writes
+// back the XCD's L2 from every workgroup: 33.5 against 26.5 us per config-4 layer.)
+extern "C" __global__ __launch_bounds__(256) void moe_logits_route(const float *w, float *a, uint32_t *ids,
+                                                                    LogitsRoutePush p, uint32_t *cnt) {
+  const LogitsPush &lp = p.lp;
+  const RoutePush &rp = p.rp;
+  __shared__ float part[4];
+  __shared__ bool last;
+  const uint32_t e = blockIdx.x, tid = threadIdx.x;
+  const float4 *row = (const float4 *)(w + lp.router_off + e * lp.n_embd);
+  const float4 *x = (const float4 *)(a + lp.x_off);
+  float s = 0.0f;
+  for (uint32_t i = tid; i < lp.n_embd / 4; i += 256) {
+    const float4 r = row[i], v = x[i];
+    s += r.x * v.x + r.y * v.y + r.z * v.z + r.w * v.w;
+  }
+  s = group_sum<64>(s);
+  if ((tid & 63) == 0) part[tid >> 6] = s;
+  __syncthreads();
+  if (tid == 0) {
+    __hip_atomic_store(a + lp.logits_off + e, part[0] + part[1] + part[2] + part[3], __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);  // the coherent store is done before the count
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    last = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
+  }
+  __syncthreads();
+  if (!last || tid >= 64) return;
+  const uint32_t n_tok = __builtin_bit_cast(uint32_t, a[2]);
+  if (n_tok > 0) route_token<true>(a, a, ids, rp, 0, tid);
+  if (tid == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // moe_sort (moe_sort.comp:21-55): slot s = tok * n_used + k is routed to ids[s].  Writes

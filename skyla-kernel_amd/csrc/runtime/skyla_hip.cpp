@@ -182,6 +182,9 @@ struct skyla_hip_pipeline {
   uint32_t split_threads = 0;
   hipFunction_t tok_fn = nullptr;        // batched form: a tok_per_wg x tok_per_wg block of
   uint32_t tok_per_wg = 0;               // grid.x and grid.y per workgroup
+  std::string name;                      // shader name
+  hipFunction_t moe_fn = nullptr;        // MoE decode forms (fuse_moe): moe_logits -> moe_logits_route,
+  hipFunction_t moe_fn2 = nullptr;       // Q4_K experts -> the gate/up pair, and the down + combine form
   std::vector<std::vector<void *>> sets;
 };
 
@@ -197,6 +200,9 @@ struct Command {
   uint32_t split_threads = 0;
   hipFunction_t tok_fn = nullptr;
   uint32_t tok_per_wg = 0;
+  std::string name;                 // the pipeline's shader name
+  hipFunction_t moe_fn = nullptr, moe_fn2 = nullptr;
+  uint32_t n_cnt = 0;               // fused MoE forms: self-resetting counters the kernel takes
   uint32_t groups[3] = {0, 0, 0};
   std::vector<void *> bufs;
   std::vector<uint32_t> push;
@@ -220,6 +226,7 @@ struct Launch {
   void *ws = nullptr;
   void *cnt = nullptr;
   std::vector<uint32_t> extra;  // trailing by-value u32 arguments (batched forms: the token count)
+  bool cnt_arg = false;         // fused MoE forms: a trailing counter pointer (n_cnt counters)
 };
 
 constexpr uint32_t kMaxSeg = 4;  // MAXSEG in kernels/common.h
@@ -247,6 +254,10 @@ Launch pack(const Command *const *run, uint32_t n) {
   l.fn = a.fn;
   l.threads = a.threads;
   l.bufs = a.bufs;
+  if (a.n_cnt) {  // the kernel takes a trailing counter pointer (fused MoE forms)
+    l.cnt_arg = true;
+    l.n_cnt = a.n_cnt;
+  }
   if (!a.segmented) {
     for (int i = 0; i < 3; i++) l.groups[i] = a.groups[i];
     l.args = a.push;
@@ -307,16 +318,119 @@ Launch pack(const Command *const *run, uint32_t n) {
 // Can dispatch c join a fused launch that starts with dispatch a and holds `x` blocks?
 // (Dispatches between two barriers are independent; same kernel, bindings and grid y/z.)
 bool fusable(const Command &a, const Command &c, uint64_t x) {
-  return a.segmented && c.kind == Command::Dispatch && c.fn == a.fn && c.bufs == a.bufs &&
+  return a.segmented && !a.n_cnt && c.kind == Command::Dispatch && c.fn == a.fn && c.bufs == a.bufs &&
          c.retile == a.retile &&
          c.threads == a.threads && c.groups[1] == a.groups[1] && c.groups[2] == a.groups[2] &&
          x + c.groups[0] <= 0x7fffffffu;
 }
 
+// Index of the next dispatch after i, skipping barriers; cmds.size() if a mark (a profiled
+// stage boundary) or the end comes first.
+size_t next_dispatch(const std::vector<Command> &cmds, size_t i) {
+  for (size_t j = i + 1; j < cmds.size(); j++) {
+    if (cmds[j].kind == Command::Barrier) continue;
+    return cmds[j].kind == Command::Dispatch ? j : cmds.size();
+  }
+  return cmds.size();
+}
+
+// MoE decode forms.  graph/moe.rs:42-80 records a decode token's MoE layer as six
+// dependent dispatches (logits, route, gate + up, silu, down, combine), and each launch on
+// MI355X costs ~2.3 us before any work.  Three pairs can become one launch each, computing
+// the same values bit for bit (tests/test_gpu_moe.py compares every form with the six
+// launches):
+//   1: moe_logits then moe_route (one token)      -> moe_logits_route
+//   2: a Q4_K expert gate and up then silu_mul    -> matvec_q4k_glu__4_0_1_1_16 (writes
+//      silu(gate) * up where silu_mul leaves it; the up rows are not stored)
+//   4: a Q4_K expert down then moe_combine        -> matvec_q4k_ecomb__4_1_16
+// The expert forms take the launch shape the runtime's variant rule gives expert matvecs
+// (four waves, one row, 16 lanes per row), so each row sums exactly as it would alone.
+// Config-4 decode, us per layer (graph replay, MI355X): six launches 26.3; form 2 24.4;
+// form 1 27.1 and form 4 26.3 -- those two hand their results from workgroup to workgroup
+// inside the launch (a coherent store, its completion, a device-scope count, coherent
+// reads), which costs as much as the launch boundary it removes -- so only form 2 is on.
+// SKYLA_HIP_MOEFUSE selects the forms as a bit mask (0 keeps the six launches).
+constexpr unsigned kMoeFormsDefault = 2;
+std::vector<Command> fuse_moe(const std::vector<Command> &cmds) {
+  const char *env = std::getenv("SKYLA_HIP_MOEFUSE");
+  const unsigned forms = env ? (unsigned)std::strtoul(env, nullptr, 0) : kMoeFormsDefault;
+  if (!forms) return cmds;
+  std::vector<Command> out;
+  out.reserve(cmds.size());
+  for (size_t i = 0; i < cmds.size();) {
+    const Command &a = cmds[i];
+    if ((forms & 1) && a.kind == Command::Dispatch && a.moe_fn && a.name == "moe_logits" && a.groups[1] == 1 &&
+        a.groups[2] == 1) {
+      const size_t j = next_dispatch(cmds, i);
+      if (j < cmds.size() && cmds[j].name == "moe_route" && cmds[j].groups[0] == 1 && cmds[j].groups[1] == 1 &&
+          cmds[j].groups[2] == 1 && cmds[j].push[0] == a.push[2]) {
+        Command f = a;
+        f.fn = a.moe_fn;
+        f.name = "moe_logits_route";
+        f.tok_fn = nullptr;
+        f.bufs = {a.bufs[0], a.bufs[1], cmds[j].bufs[1]};
+        f.push.insert(f.push.end(), cmds[j].push.begin(), cmds[j].push.end());
+        f.n_cnt = 1;
+        out.push_back(std::move(f));
+        i = j + 1;
+        continue;
+      }
+    }
+    // expert matvec push: o0, o1, x_off, y_off, n_in, n_out, ids_off, x_stride, y_stride
+    if (a.kind == Command::Dispatch && a.moe_fn && a.name == "matvec_q4k" && a.push.size() == 9) {
+      const size_t jb = i + 1 < cmds.size() ? i + 1 : cmds.size();
+      if ((forms & 2) && jb < cmds.size()) {
+        const Command &b = cmds[jb];
+        const size_t j = next_dispatch(cmds, jb);
+        if (b.kind == Command::Dispatch && b.fn == a.fn && b.bufs == a.bufs && b.groups[1] == a.groups[1] &&
+            b.groups[2] == 1 && a.groups[2] == 1 && b.push[2] == a.push[2] && b.push[4] == a.push[4] &&
+            b.push[5] == a.push[5] && b.push[6] == a.push[6] && b.push[7] == a.push[7] && b.push[8] == a.push[8] &&
+            j < cmds.size() && cmds[j].name == "silu_mul" && cmds[j].groups[1] == 1 && cmds[j].push[0] == a.push[3] &&
+            cmds[j].push[1] == b.push[3] && cmds[j].push[3] == 0 &&
+            cmds[j].push[2] == a.groups[1] * a.push[8] && a.push[8] >= a.push[5]) {
+          Command f = a;
+          f.fn = a.moe_fn;
+          f.name = "matvec_q4k_glu";
+          f.threads = 256;
+          f.retile = nullptr;
+          f.groups[0] = (a.push[5] + 7) / 8;
+          f.push.push_back(b.push[0]);
+          f.push.push_back(b.push[1]);
+          out.push_back(std::move(f));
+          i = j + 1;
+          continue;
+        }
+      }
+      const size_t j = next_dispatch(cmds, i);
+      if ((forms & 4) && a.moe_fn2 && j < cmds.size() && cmds[j].name == "moe_combine" && cmds[j].groups[1] == 1 &&
+          a.groups[2] == 1 && cmds[j].push[1] == a.push[3] && cmds[j].push[4] == a.push[8] &&
+          cmds[j].push[3] == a.push[5] && cmds[j].push[5] == a.groups[1]) {
+        Command f = a;
+        f.fn = a.moe_fn2;
+        f.name = "matvec_q4k_ecomb";
+        f.threads = 256;
+        f.retile = nullptr;
+        f.groups[0] = (a.push[5] + 15) / 16;
+        f.push.push_back(cmds[j].push[0]);
+        f.push.push_back(cmds[j].push[2]);
+        f.push.push_back(cmds[j].push[5]);
+        f.n_cnt = f.groups[0];
+        out.push_back(std::move(f));
+        i = j + 1;
+        continue;
+      }
+    }
+    out.push_back(a);
+    i++;
+  }
+  return out;
+}
+
 // The launch list of a recording.  Barriers need no command of their own: launches on one
 // stream (and the nodes of a graph captured from it) run in order.  SKYLA_HIP_FUSE=0 keeps
 // one launch per dispatch.
-std::vector<Launch> build_launches(const std::vector<Command> &cmds) {
+std::vector<Launch> build_launches(const std::vector<Command> &recorded) {
+  const std::vector<Command> cmds = fuse_moe(recorded);
   const char *env = std::getenv("SKYLA_HIP_FUSE");
   const bool fuse = !(env && env[0] == '0');
   std::vector<Launch> out;
@@ -359,6 +473,7 @@ int launch(hipStream_t stream, const Launch &l) {
     params.push_back(const_cast<uint32_t *>(&l.split));
   }
   for (const uint32_t &v : l.extra) params.push_back(const_cast<uint32_t *>(&v));
+  if (l.cnt_arg) params.push_back(const_cast<void **>(&l.cnt));
   HIP_TRY(hipModuleLaunchKernel(l.fn, l.groups[0], l.groups[1], l.groups[2], l.threads, 1, 1, 0,
                                 stream, params.data(), nullptr));
   return SKYLA_HIP_OK;
@@ -373,11 +488,11 @@ int bind_workspace(std::vector<Launch> &ls, void **owned) {
   *owned = nullptr;
   uint64_t ws = 0, n_cnt = 0;
   for (const Launch &l : ls)
-    if (l.split) {
+    if (l.split || l.cnt_arg) {
       ws = std::max(ws, l.ws_bytes);
       n_cnt = std::max<uint64_t>(n_cnt, l.n_cnt);
     }
-  if (!ws) return SKYLA_HIP_OK;
+  if (!ws && !n_cnt) return SKYLA_HIP_OK;
   const uint64_t cnt_off = (ws + 255) & ~(uint64_t)255;
   void *mem = nullptr;
   HIP_TRY(hipMalloc(&mem, cnt_off + n_cnt * 4));
@@ -388,7 +503,7 @@ int bind_workspace(std::vector<Launch> &ls, void **owned) {
     return fail(SKYLA_HIP_E_DEVICE, "K-split workspace: %s", hipGetErrorString(e));
   }
   for (Launch &l : ls)
-    if (l.split) {
+    if (l.split || l.cnt_arg) {
       l.ws = mem;
       l.cnt = (char *)mem + cnt_off;
     }
@@ -775,6 +890,15 @@ int skyla_hip_pipeline_new(skyla_hip_context *ctx, const char *name, uint32_t n_
   if (!p->fn)
     return fail(SKYLA_HIP_E_NO_KERNEL, "no gfx950 kernel %s for this spec", sym.c_str());
   p->retile = make_retile(ctx, name, spec, n_spec);
+  p->name = name;
+  // MoE decode forms (fuse_moe): the router pair, and Q4_K expert matvecs whose launches the
+  // variant rule puts on (4, 1, 16)
+  if (std::strcmp(name, "moe_logits") == 0) p->moe_fn = find_function(ctx, "moe_logits_route");
+  if (std::strcmp(name, "matvec_q4k") == 0 && n_spec == 5 && spec[1] == 0 && spec[3] == 1 && p->retile &&
+      p->retile->alts.size() == 1 && p->retile->alts[0].rwg == 16 && p->retile->alts[0].threads == 256) {
+    p->moe_fn = find_function(ctx, "matvec_q4k_glu__4_0_1_1_16");
+    p->moe_fn2 = find_function(ctx, "matvec_q4k_ecomb__4_1_16");
+  }
   // router logits of a batch: 8 x 8 (expert, token) blocks per workgroup (moe.hip, moe_logits_t)
   if (std::strcmp(name, "moe_logits") == 0) {
     p->tok_fn = find_function(ctx, "moe_logits_t");
@@ -873,6 +997,9 @@ int skyla_hip_record_dispatch(skyla_hip_recorder *r, const skyla_hip_pipeline *p
   c.split_threads = p->split_threads;
   c.tok_fn = p->tok_fn;
   c.tok_per_wg = p->tok_per_wg;
+  c.name = p->name;
+  c.moe_fn = p->moe_fn;
+  c.moe_fn2 = p->moe_fn2;
   for (int i = 0; i < 3; i++) c.groups[i] = groups[i];
   c.bufs = p->sets[set];
   c.push.assign(push, push + n_push);

@@ -302,3 +302,43 @@ def test_moe_decode_expert_variant_choice(ctx, moe):
     assert rel_l2(got["1"], got["0"]) < 1e-5
     out, _, _ = _oracle_moe(moe, n[0])
     assert rel_l2(got["1"], out) <= F32
+
+
+@pytest.mark.parametrize("forms,n_launch", [("7", 3), ("2", 5), ("1", 5), ("4", 5)])
+@pytest.mark.parametrize("seed", ["fuse-a", "fuse-b"])
+def test_moe_decode_fused_forms_equal_six_launches(ctx, moe, seed, forms, n_launch):
+    """The runtime's MoE decode forms (bit 1: logits + route, 2: the experts' gate + up +
+    SiLU, 4: down + combine; 2 is the default) against the engine's six dispatches launched
+    one by one (SKYLA_HIP_MOEFUSE=0): the same ids, routing weights, logits and residual,
+    bit for bit."""
+    n = synth.activations(CFG, f"{seed}-n", (1, N_EMBD))
+    x0 = synth.activations(CFG, f"{seed}-x", (1, N_EMBD))
+    got, launches = {}, {}
+    for fuse in (forms, "0"):
+        old = os.environ.get("SKYLA_HIP_MOEFUSE")
+        os.environ["SKYLA_HIP_MOEFUSE"] = fuse
+        try:
+            moe.load(n, x0)
+
+            def body(r):
+                E.Graph(r, moe.k, moe.a, moe.c, False).moe(moe.qg, moe.qu, moe.qd, moe.router_off)
+            rec = ctx.record(False, body)
+            launches[fuse] = rec.launches()
+            ctx.replay(rec)
+            rec.free()
+        finally:
+            if old is None:
+                del os.environ["SKYLA_HIP_MOEFUSE"]
+            else:
+                os.environ["SKYLA_HIP_MOEFUSE"] = old
+        moe.a.buffer.download()
+        a, m = moe.a, moe.a.moe
+        got[fuse] = (a.u32()[m.ids: m.ids + N_USED].copy(), a.f32()[m.weights: m.weights + N_USED].copy(),
+                     a.f32()[m.logits: m.logits + N_EXPERT].copy(), moe.rows(a.x, a.s_embd, 1, N_EMBD)[0].copy())
+    assert (launches[forms], launches["0"]) == (n_launch, 6)
+    for g1, g0 in zip(got[forms], got["0"]):
+        assert np.array_equal(g1.view(np.uint32), g0.view(np.uint32))
+    out, ids, _ = _oracle_moe(moe, n[0])
+    if not _near_tie(moe.router, n[0]):
+        assert list(got[forms][0]) == list(ids)
+        assert rel_l2(got[forms][3] - x0[0], out) <= F32
