@@ -434,6 +434,8 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--eager", action="store_true",
                     help="replay recordings as direct launches instead of one HIP graph")
+    ap.add_argument("--gemm-only", action="store_true",
+                    help="only the config-3 prefill GEMMs (for hardware-counter runs)")
     ap.add_argument("--calibrate", action="store_true",
                     help="run only the two known-size kernels that scale rocprofv3 FETCH_SIZE/WRITE_SIZE")
     ap.add_argument("--fuse", choices=["none", "qkv", "ffn", "all"], default="qkv",
@@ -454,6 +456,10 @@ def main() -> int:
     ctx = Context.new(0)
     if args.calibrate:
         print(json.dumps(calibrate(ctx)))
+        ctx.free()
+        return 0
+    if args.gemm_only:
+        print(json.dumps({"prefill_gemm_m512": prefill_gemm(ctx)}))
         ctx.free()
         return 0
     if args.e2e_only:
