@@ -68,6 +68,41 @@ SK_DEV float lane_sum(float v) {
 
 SK_DEV uint32_t ctl_word(const uint32_t *ctl, uint32_t i) { return ctl[i]; }
 
+// ---------------------------------------------------------------------------------------
+// f32 products of exact integer quants (the decode matvecs, matvec.hip and chain.hip).
+// ---------------------------------------------------------------------------------------
+// s + sum over the four bytes b of word v of f32(b) * x[b], in byte order: four
+// v_cvt_f32_ubyte0..3 (exact for 0..255) and four FMAs.
+SK_DEV float fma_bytes(uint32_t v, float4 x, float s) {
+  s = __builtin_fmaf((float)(v & 255u), x.x, s);
+  s = __builtin_fmaf((float)((v >> 8) & 255u), x.y, s);
+  s = __builtin_fmaf((float)((v >> 16) & 255u), x.z, s);
+  s = __builtin_fmaf((float)(v >> 24), x.w, s);
+  return s;
+}
+
+// A mask constant the compiler cannot see through, held in an SGPR.  With a visible
+// constant such as 0x0f0f0f0f the compiler knows which bits of the masked word are zero
+// and extracts each byte with its own v_bfe_u32 before a v_cvt_f32_ubyte0 (two VALU per
+// quant), instead of one v_and_b32 per word and v_cvt_f32_ubyte0..3 (one per quant).
+SK_DEV uint32_t opaque_mask(uint32_t c) {
+  uint32_t r;
+  asm volatile("s_mov_b32 %0, %1" : "=s"(r) : "i"(c));
+  return r;
+}
+
+// sum of the 16 products of the masked bytes of q (word k holds values 4k..4k+3) with x,
+// starting from s
+SK_DEV float fma_bytes16(uint4 q, uint32_t mask, const float4 (&x)[4], float s) {
+  s = fma_bytes(q.x & mask, x[0], s);
+  s = fma_bytes(q.y & mask, x[1], s);
+  s = fma_bytes(q.z & mask, x[2], s);
+  s = fma_bytes(q.w & mask, x[3], s);
+  return s;
+}
+
+SK_DEV float sum4(float4 v) { return (v.x + v.y) + (v.z + v.w); }
+
 // Buffer resource over [base, base + bytes) for raw buffer loads: a load whose offset is
 // past the end returns zero instead of touching memory (range checked per dword).  The
 // offset of a load is voffset (per lane) + soffset (wave-uniform), so a constant step of a

@@ -75,37 +75,6 @@ SK_DEV void store_rows(float *y, uint32_t y_off, uint32_t first, uint32_t n_out,
   }
 }
 
-// s + sum over the four bytes b of word v of f32(b) * x[b], in byte order: four
-// v_cvt_f32_ubyte0..3 (exact for 0..255) and four FMAs.
-SK_DEV float fma_bytes(uint32_t v, float4 x, float s) {
-  s = __builtin_fmaf((float)(v & 255u), x.x, s);
-  s = __builtin_fmaf((float)((v >> 8) & 255u), x.y, s);
-  s = __builtin_fmaf((float)((v >> 16) & 255u), x.z, s);
-  s = __builtin_fmaf((float)(v >> 24), x.w, s);
-  return s;
-}
-
-// A mask constant the compiler cannot see through, held in an SGPR.  With a visible
-// constant such as 0x0f0f0f0f the compiler knows which bits of the masked word are zero
-// and extracts each byte with its own v_bfe_u32 before a v_cvt_f32_ubyte0 (two VALU per
-// quant), instead of one v_and_b32 per word and v_cvt_f32_ubyte0..3 (one per quant).
-SK_DEV uint32_t opaque_mask(uint32_t c) {
-  uint32_t r;
-  asm volatile("s_mov_b32 %0, %1" : "=s"(r) : "i"(c));
-  return r;
-}
-
-// sum of the 16 products of the masked bytes of q (word k holds values 4k..4k+3) with x,
-// starting from s
-SK_DEV float fma_bytes16(uint4 q, uint32_t mask, const float4 (&x)[4], float s) {
-  s = fma_bytes(q.x & mask, x[0], s);
-  s = fma_bytes(q.y & mask, x[1], s);
-  s = fma_bytes(q.z & mask, x[2], s);
-  s = fma_bytes(q.w & mask, x[3], s);
-  return s;
-}
-
-SK_DEV float sum4(float4 v) { return (v.x + v.y) + (v.z + v.w); }
 
 // Fused activation forms.  MODE 1 (SiLU; silu_mul.comp:15-23) stages x / (1 + e^-x) * aux:
 // the down projection reads the gate and up rows itself.  MODE 2 (RMSNorm; rmsnorm.comp,

@@ -17,6 +17,7 @@
 //   * Buffers are HBM allocations with a host mirror that the caller synchronises
 //     explicitly (the reference's buffers are host-coherent; a discrete GPU's are not).
 #include "../../../include/skyla_hip.h"
+#include "../kernels/chain_table.h"
 
 #include <hip/hip_runtime.h>
 
@@ -35,6 +36,7 @@ extern "C" const unsigned char skyla_co_matmul[], skyla_co_matmul_end[];
 extern "C" const unsigned char skyla_co_moe[], skyla_co_moe_end[];
 extern "C" const unsigned char skyla_co_util[], skyla_co_util_end[];
 extern "C" const unsigned char skyla_co_attention[], skyla_co_attention_end[];
+extern "C" const unsigned char skyla_co_chain[], skyla_co_chain_end[];
 
 namespace {
 
@@ -130,6 +132,10 @@ struct skyla_hip_context {
   char *scratch = nullptr;
   size_t scratch_bytes = 0;
   hipFunction_t fill_u32 = nullptr;
+  // chained decode matvecs (chain.hip): the kernel, and its grid (one workgroup per CU);
+  // null when a workgroup cannot be resident on every CU at once
+  hipFunction_t chain_fn = nullptr;
+  uint32_t n_cu = 0;
 };
 
 struct HostFree {
@@ -185,6 +191,8 @@ struct skyla_hip_pipeline {
   std::string name;                      // shader name
   hipFunction_t moe_fn = nullptr;        // MoE decode forms (fuse_moe): moe_logits -> moe_logits_route,
   hipFunction_t moe_fn2 = nullptr;       // Q4_K experts -> the gate/up pair, and the down + combine form
+  uint32_t chain_kind = 0;               // dense matvecs matvec_chain can run (CHAIN_*), and
+  uint32_t chain_accum = 0;              // whether they accumulate
   std::vector<std::vector<void *>> sets;
 };
 
@@ -202,6 +210,7 @@ struct Command {
   uint32_t tok_per_wg = 0;
   std::string name;                 // the pipeline's shader name
   hipFunction_t moe_fn = nullptr, moe_fn2 = nullptr;
+  uint32_t chain_kind = 0, chain_accum = 0;
   uint32_t n_cnt = 0;               // fused MoE forms: self-resetting counters the kernel takes
   uint32_t groups[3] = {0, 0, 0};
   std::vector<void *> bufs;
@@ -227,6 +236,14 @@ struct Launch {
   void *cnt = nullptr;
   std::vector<uint32_t> extra;  // trailing by-value u32 arguments (batched forms: the token count)
   bool cnt_arg = false;         // fused MoE forms: a trailing counter pointer (n_cnt counters)
+  // a dense matvec launch matvec_chain can run as one of its stages (stage_ok), that stage;
+  // and for a chain launch its arguments (stage table, stage count, synchronisation words)
+  bool stage_ok = false;
+  ChainStage stage{};
+  bool chain = false;
+  uint64_t chain_table = 0;
+  uint32_t chain_n = 0;
+  void *chain_sync = nullptr;
 };
 
 constexpr uint32_t kMaxSeg = 4;  // MAXSEG in kernels/common.h
@@ -245,6 +262,53 @@ uint32_t split_of(const Command &a) {
   S = std::min(S, n_stage / 4);
   S = std::min(S, 8u);
   return S < 2 ? 1 : S;
+}
+
+// The matvec_chain stage (chain_table.h) of a launch of n dispatches of one dense matvec
+// pipeline, if the chain computes that shape: Q4_K with n_in 4096 or Q6_K with n_in 12288,
+// one token (grid y = z = 1), every segment reading the same activations at a 16-byte
+// aligned offset, and every region inside the first 4 GiB - 256 B of the weights buffer.
+bool chain_stage(const Command *const *run, uint32_t n, ChainStage &st) {
+  const Command &a = *run[0];
+  if (!a.chain_kind || a.groups[1] != 1 || a.groups[2] != 1 || n == 0 || n > 4) return false;
+  const bool q4 = a.chain_kind == CHAIN_Q4K_4096;
+  const size_t words = q4 ? 9 : 11;
+  if (a.push.size() != words || a.bufs.size() != (q4 ? 4u : 5u)) return false;
+  if (!q4 && a.bufs[0] != a.bufs[1]) return false;  // ql/qh/scales and d read one buffer
+  st = ChainStage{};
+  st.kind = a.chain_kind;
+  st.accum = a.chain_accum;
+  st.n_seg = n;
+  st.w = (uint64_t)(uintptr_t)a.bufs[0];
+  st.x = (uint64_t)(uintptr_t)a.bufs[q4 ? 1 : 2];
+  st.y = (uint64_t)(uintptr_t)a.bufs[q4 ? 2 : 3];
+  const uint32_t rows = q4 ? 8 : 2, n_in = q4 ? 4096 : 12288;
+  uint64_t records = 0, chunks = 0;
+  for (uint32_t i = 0; i < n; i++) {
+    const std::vector<uint32_t> &p = run[i]->push;
+    const uint32_t x_off = p[q4 ? 2 : 4], y_off = p[q4 ? 3 : 5], in = p[q4 ? 4 : 6], out = p[q4 ? 5 : 7];
+    if (in != n_in || out == 0 || x_off % 4 != 0 || (i && x_off != st.x_off)) return false;
+    st.x_off = x_off;
+    ChainSeg &sg = st.seg[i];
+    for (int k = 0; k < 4; k++) sg.o[k] = (q4 && k >= 2) ? 0 : p[k];
+    if (!q4 && sg.o[3] % 8 != 0) return false;  // d rows start 16-byte aligned
+    sg.n_out = out;
+    sg.y_off = y_off;
+    chunks += (out + rows - 1) / rows;
+    sg.g_end = (uint32_t)chunks;
+    const uint64_t nb = out;
+    if (q4) {
+      records = std::max({records, 16 * ((uint64_t)sg.o[0] + nb * 128), 16 * ((uint64_t)sg.o[1] + nb * 16)});
+    } else {
+      records = std::max({records, 16 * ((uint64_t)sg.o[0] + nb * 384), 16 * ((uint64_t)sg.o[1] + nb * 192),
+                          16 * ((uint64_t)sg.o[2] + nb * 48), 2 * ((uint64_t)sg.o[3] + nb * 48)});
+    }
+  }
+  if (records > 0xffffff00ull || chunks > 0x7fffffffull) return false;
+  for (uint32_t i = n; i < 4; i++) st.seg[i].g_end = 0xffffffffu;  // no chunk is past them
+  st.n_chunks = (uint32_t)chunks;
+  st.w_records = (uint32_t)records;
+  return true;
 }
 
 // Packs consecutive dispatches of one segmented kernel into one launch.
@@ -312,6 +376,7 @@ Launch pack(const Command *const *run, uint32_t n) {
   l.groups[0] = x;
   l.groups[1] = a.groups[1];
   l.groups[2] = a.groups[2];
+  l.stage_ok = chain_stage(run, n, l.stage);
   return l;
 }
 
@@ -462,6 +527,12 @@ std::vector<Launch> build_launches(const std::vector<Command> &recorded) {
 }
 
 int launch(hipStream_t stream, const Launch &l) {
+  if (l.chain) {  // matvec_chain(table, n_stages, sync)
+    void *cp[] = {const_cast<uint64_t *>(&l.chain_table), const_cast<uint32_t *>(&l.chain_n),
+                  const_cast<void **>(&l.chain_sync)};
+    HIP_TRY(hipModuleLaunchKernel(l.fn, l.groups[0], 1, 1, l.threads, 1, 1, 0, stream, cp, nullptr));
+    return SKYLA_HIP_OK;
+  }
   // kernel parameters: binding pointers in order, then the push struct by value
   std::vector<void *> params;
   params.reserve(l.bufs.size() + 1);
@@ -528,6 +599,7 @@ struct skyla_hip_recording {
   std::vector<Command> cmds;
   std::vector<Launch> launches;
   void *workspace = nullptr;  // K-split partials and counters of the launches
+  void *chain_mem = nullptr;  // matvec_chain stage tables and synchronisation words
   hipGraphExec_t exec = nullptr;
   hipGraph_t graph = nullptr;
   std::vector<std::string> labels;
@@ -542,6 +614,7 @@ struct skyla_hip_recording {
     if (exec) hipGraphExecDestroy(exec);
     if (graph) hipGraphDestroy(graph);
     if (workspace) hipFree(workspace);
+    if (chain_mem) hipFree(chain_mem);
   }
 };
 
@@ -554,6 +627,66 @@ hipFunction_t find_function(skyla_hip_context *ctx, const std::string &sym) {
   }
   (void)hipGetLastError();  // lookups that missed leave a sticky error behind
   return nullptr;
+}
+
+// Chained decode matvecs (chain.hip).  A run of two or more consecutive launches that
+// matvec_chain can run as stages (chain_stage) becomes one launch of one workgroup per CU,
+// which streams the weights of all of them through LDS and meets at a grid barrier between
+// stages, instead of paying a launch and a ramp per stage.  The stage tables of a recording
+// and the chain's synchronisation words share one device allocation (*owned), cleared here,
+// outside any graph capture; every chain launch leaves the words as it found them.
+// Measured on MI355X it is slower than the launches it replaces (config-2 step 1.78 ms
+// against 1.33 ms): a grid barrier between dependent stages costs 4-6 us (the last
+// workgroup's stores, its count, the others' polls, all past the XCDs' L2s), more than a
+// launch boundary, and the per-chunk workgroup barrier keeps the waves in lockstep.  So it
+// is off unless SKYLA_HIP_CHAIN=1.
+int chain_launches(skyla_hip_context *ctx, std::vector<Launch> &ls, void **owned) {
+  *owned = nullptr;
+  const char *env = std::getenv("SKYLA_HIP_CHAIN");
+  if (!ctx->chain_fn || !(env && env[0] == '1')) return SKYLA_HIP_OK;
+  std::vector<std::pair<size_t, size_t>> runs;  // [begin, end) of each run
+  for (size_t i = 0; i < ls.size();) {
+    size_t j = i;
+    while (j < ls.size() && !ls[j].mark && ls[j].stage_ok) j++;
+    if (j - i >= 2) runs.push_back({i, j});
+    i = j > i ? j : i + 1;
+  }
+  if (runs.empty()) return SKYLA_HIP_OK;
+  std::vector<ChainStage> table;
+  for (const auto &r : runs)
+    for (size_t i = r.first; i < r.second; i++) table.push_back(ls[i].stage);
+  const size_t sync_bytes = 256, bytes = sync_bytes + table.size() * sizeof(ChainStage);
+  void *mem = nullptr;
+  HIP_TRY(hipMalloc(&mem, bytes));
+  hipError_t e = hipMemset(mem, 0, sync_bytes);
+  if (e == hipSuccess) e = hipMemcpy((char *)mem + sync_bytes, table.data(), table.size() * sizeof(ChainStage),
+                                     hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipDeviceSynchronize();
+  if (e != hipSuccess) {
+    hipFree(mem);
+    return fail(SKYLA_HIP_E_DEVICE, "chain tables: %s", hipGetErrorString(e));
+  }
+  std::vector<Launch> out;
+  size_t next = 0, t = 0;
+  for (const auto &r : runs) {
+    for (; next < r.first; next++) out.push_back(std::move(ls[next]));
+    Launch c;
+    c.fn = ctx->chain_fn;
+    c.threads = CHAIN_THREADS;
+    c.groups[0] = ctx->n_cu;
+    c.groups[1] = c.groups[2] = 1;
+    c.chain = true;
+    c.chain_table = (uint64_t)(uintptr_t)((char *)mem + sync_bytes + t * sizeof(ChainStage));
+    c.chain_n = (uint32_t)(r.second - r.first);
+    c.chain_sync = mem;
+    t += c.chain_n;
+    out.push_back(std::move(c));
+    next = r.second;
+  }
+  for (; next < ls.size(); next++) out.push_back(std::move(ls[next]));
+  ls = std::move(out);
+  *owned = mem;
+  return SKYLA_HIP_OK;
 }
 
 // Variant choice for matvec launches, from sweeps on MI355X.  Dense rows (Qwen3-8B decode
@@ -684,7 +817,7 @@ int skyla_hip_context_new(int device, skyla_hip_context **out) {
   ctx->warp = (uint32_t)prop.warpSize;
   HIP_TRY(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking));
   const unsigned char *images[] = {skyla_co_matvec, skyla_co_matmul, skyla_co_moe, skyla_co_util,
-                                   skyla_co_attention};
+                                   skyla_co_attention, skyla_co_chain};
   for (const unsigned char *img : images) {
     hipModule_t m = nullptr;
     hipError_t le = hipModuleLoadData(&m, img);
@@ -715,6 +848,18 @@ int skyla_hip_context_new(int device, skyla_hip_context **out) {
       skyla_hip_context_free(ctx.release());
       return fail(SKYLA_HIP_E_DEVICE, "hipModuleGetFunction(fill_u32): %s", hipGetErrorString(fe));
     }
+  }
+  // matvec_chain waits at grid barriers, so it runs only if one workgroup fits on every CU
+  // at once: the grid is one workgroup per CU and the kernel's occupancy must allow one
+  {
+    hipFunction_t fn = find_function(ctx.get(), "matvec_chain");
+    int per_cu = 0;
+    if (fn && hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, CHAIN_THREADS, 0) == hipSuccess &&
+        per_cu >= 1 && prop.multiProcessorCount > 0) {
+      ctx->chain_fn = fn;
+      ctx->n_cu = (uint32_t)prop.multiProcessorCount;
+    }
+    (void)hipGetLastError();
   }
   *out = ctx.release();
   return SKYLA_HIP_OK;
@@ -899,6 +1044,12 @@ int skyla_hip_pipeline_new(skyla_hip_context *ctx, const char *name, uint32_t n_
     p->moe_fn = find_function(ctx, "matvec_q4k_glu__4_0_1_1_16");
     p->moe_fn2 = find_function(ctx, "matvec_q4k_ecomb__4_1_16");
   }
+  // dense decode matvecs matvec_chain can run (the shape is checked per launch)
+  if (n_spec == 5 && spec[3] == 0 && ctx->chain_fn) {
+    if (std::strcmp(name, "matvec_q4k") == 0) p->chain_kind = CHAIN_Q4K_4096;
+    if (std::strcmp(name, "matvec_q6k") == 0) p->chain_kind = CHAIN_Q6K_12288;
+    p->chain_accum = spec[1] != 0;
+  }
   // router logits of a batch: 8 x 8 (expert, token) blocks per workgroup (moe.hip, moe_logits_t)
   if (std::strcmp(name, "moe_logits") == 0) {
     p->tok_fn = find_function(ctx, "moe_logits_t");
@@ -1000,6 +1151,8 @@ int skyla_hip_record_dispatch(skyla_hip_recorder *r, const skyla_hip_pipeline *p
   c.name = p->name;
   c.moe_fn = p->moe_fn;
   c.moe_fn2 = p->moe_fn2;
+  c.chain_kind = p->chain_kind;
+  c.chain_accum = p->chain_accum;
   for (int i = 0; i < 3; i++) c.groups[i] = groups[i];
   c.bufs = p->sets[set];
   c.push.assign(push, push + n_push);
@@ -1052,6 +1205,7 @@ int skyla_hip_record_end(skyla_hip_recorder *r, skyla_hip_recording **out) {
   rec->mark_ns.assign(rec->labels.size(), 0.0);
   HIP_TRY(hipSetDevice(rec->ctx->device));
   if (int s = bind_workspace(rec->launches, &rec->workspace)) return s;
+  if (int s = chain_launches(rec->ctx, rec->launches, &rec->chain_mem)) return s;
   if (!rec->profile && skyla_hip_recording_len(rec.get()) > 0) {
     // One graph for the whole recording, captured from the launch list on the stream.
     skyla_hip_context *ctx = rec->ctx;
@@ -1134,6 +1288,26 @@ struct Events {
 
 }  // namespace
 
+}  // extern "C"
+
+namespace {
+// SKYLA_HIP_CHAIN_CHECK=1: after each replay, fail if a chain launch of the recording timed
+// out at its grid barrier (its workgroups were not all resident; the outputs are wrong) or
+// left its arrival count set.
+int chain_check(const skyla_hip_recording *rec) {
+  const char *env = std::getenv("SKYLA_HIP_CHAIN_CHECK");
+  if (!rec->chain_mem || !(env && env[0] == '1')) return SKYLA_HIP_OK;
+  uint32_t words[CHAIN_SYNC_WORDS] = {0, 0};
+  HIP_TRY(hipMemcpy(words, rec->chain_mem, sizeof words, hipMemcpyDeviceToHost));
+  if (words[0] != 0 || words[1] != 0)
+    return fail(SKYLA_HIP_E_DEVICE, "matvec_chain: grid barrier state %u / time-out %u after a replay", words[0],
+                words[1]);
+  return SKYLA_HIP_OK;
+}
+}  // namespace
+
+extern "C" {
+
 int skyla_hip_replay(skyla_hip_context *ctx, const skyla_hip_recording *rec) {
   if (!ctx || !rec) return fail(SKYLA_HIP_E_ARG, "replay: bad argument");
   if (rec->ctx != ctx) return fail(SKYLA_HIP_E_ARG, "replay: recording of another context");
@@ -1142,7 +1316,7 @@ int skyla_hip_replay(skyla_hip_context *ctx, const skyla_hip_recording *rec) {
     int s = submit(ctx, rec, nullptr);
     if (s) return s;
     HIP_TRY(hipStreamSynchronize(ctx->stream));
-    return SKYLA_HIP_OK;
+    return chain_check(rec);
   }
   Events e;
   int s = e.make(rec->labels.size() + 1);
@@ -1157,7 +1331,7 @@ int skyla_hip_replay(skyla_hip_context *ctx, const skyla_hip_recording *rec) {
     mut->mark_ns[i] = (double)ms * 1e6;
   }
   mut->replayed = true;
-  return SKYLA_HIP_OK;
+  return chain_check(rec);
 }
 
 int skyla_hip_replay_timed(skyla_hip_context *ctx, const skyla_hip_recording *rec, double *ns) {
