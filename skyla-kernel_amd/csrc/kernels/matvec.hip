@@ -544,6 +544,179 @@ SK_DEV void matvec_q4k_ks_body(const uint4 *__restrict__ w, const float *x, floa
 }
 
 // ---------------------------------------------------------------------------------------
+// Q4_K on the matrix cores, n_in = 4096 (matvec_q4k_mf__A_G): the K-split geometry of
+// matvec_q4k_ks_body -- wave w takes super-blocks 2w and 2w + 1 of 16 rows at a time, the
+// eight wave partials meet in LDS and are added in wave order -- with the products on
+// v_mfma_f32_16x16x32_f16, D[m][n] = sum over 32 values k of A[m][k] B[k][n]:
+//   A = the exact integer q * sc (4-bit quant times its 6-bit sub-block scale: at most 945,
+//       an exact f16), made from the packed nibbles with one and-or per pair (0x6400 | q is
+//       the f16 1024 + q; 0x6400 | 16 q is 1024 + 16 q) and one packed f16 FMA,
+//       (1024 + q) sc - 1024 sc or (1024 + 16 q) sc / 16 - 64 sc, rounded once from q sc;
+//   B column 0 = x_hi = f16(x 2^e), column 1 = x_lo = f16(x 2^e - x_hi) (the other columns
+//       are not read back); 2^e puts the wave's largest |x| in [2^13, 2^14), so x_hi + x_lo
+//       holds x to 2^-22 of itself (or 2^-38 of the wave's largest) and nothing overflows.
+// A super-block's row sum is then d (D[m][0] + D[m][1]) 2^-e, less the minimum terms
+// dmin * sum_j m_j * (sum of x over sub-block j) in f32 (quant.rs:56-66, regrouped as the
+// f32 forms do).  9 VALU instructions per 8 values instead of ~20.
+//
+// Lane (m = l % 16, kg = l / 16) loads bytes [16 kg, +16) and [64 + 16 kg, +16) of row m's
+// 128 qs bytes of each super-block: its words 0..3 lie in chunk kg / 2, words 4..7 in chunk
+// 2 + kg / 2 (chunk c: 32 bytes holding the low nibbles of sub-block 2c and the high
+// nibbles of sub-block 2c + 1).  Word j is the lane's A for step j of the super-block, its
+// eight values in A's element order: the low nibbles of bytes 0 and 2, their high nibbles,
+// then the same of bytes 1 and 3.  Lane (n, kg) of B holds the activations of the same
+// positions, staged once per workgroup through LDS (bq) in that order.
+// ---------------------------------------------------------------------------------------
+typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+typedef _Float16 h8v __attribute__((ext_vector_type(8)));
+typedef float f4v __attribute__((ext_vector_type(4)));
+
+// the two f16 constants that turn a nibble pair into q * sc: low nibbles (1024 + q) and
+// high nibbles (1024 + 16 q)
+struct NibScale {
+  h2v lo_mul, lo_add, hi_mul, hi_add;
+};
+SK_DEV NibScale nib_scale(uint32_t sc_lo, uint32_t sc_hi) {
+  const _Float16 a = (_Float16)(float)sc_lo, b = (_Float16)((float)sc_hi * 0.0625f);
+  const _Float16 c = (_Float16)(-1024.0f * (float)sc_lo), d = (_Float16)(-64.0f * (float)sc_hi);
+  return {h2v{a, a}, h2v{c, c}, h2v{b, b}, h2v{d, d}};
+}
+// A of one word: its eight values times their sub-block scales, exact
+SK_DEV h8v nib_a(uint32_t w, const NibScale &k, uint32_t M1, uint32_t M2, uint32_t F) {
+  const uint32_t t = w >> 8;
+  const h2v p0 = __builtin_elementwise_fma(__builtin_bit_cast(h2v, (w & M1) | F), k.lo_mul, k.lo_add);
+  const h2v p1 = __builtin_elementwise_fma(__builtin_bit_cast(h2v, (w & M2) | F), k.hi_mul, k.hi_add);
+  const h2v p2 = __builtin_elementwise_fma(__builtin_bit_cast(h2v, (t & M1) | F), k.lo_mul, k.lo_add);
+  const h2v p3 = __builtin_elementwise_fma(__builtin_bit_cast(h2v, (t & M2) | F), k.hi_mul, k.hi_add);
+  return h8v{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+}
+
+template <int ACCUM, int NG, typename P = MatvecPush2>
+SK_DEV void matvec_q4k_mf_body(const uint4 *__restrict__ w, const float *x, float *y, const P &p, uint32_t bx) {
+  constexpr int OUT = 16 * NG;
+  __shared__ uint4 bq[8][2][2][8][4];  // per wave: [column][super-block][step][kg], 8 f16 each
+  __shared__ float xsum[8][16];        // per wave: its 16 sub-block sums of x
+  __shared__ float cs[8][2][16];       // per wave: D[m][0] + D[m][1] per (super-block, row)
+  __shared__ float part[8][OUT];
+
+  const uint32_t tid = threadIdx.x, wv = tid >> 6, l = tid & 63;
+  const uint32_t m = l & 15, kg = l >> 4, h = kg >> 1;
+  const uint32_t out0 = bx * OUT;
+  // masks in SGPRs, the exponent bits in a VGPR: v_and_or_b32 reads one scalar operand
+  const uint32_t M1 = opaque_mask(0x000f000fu), M2 = opaque_mask(0x00f000f0u);
+  uint32_t F;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(F) : "i"(0x64006400));
+
+  uint4 q[2][2][2], hd[2][2];  // [buffer][super-block][half] qs, [buffer][super-block] header
+  auto load_group = [&](uint32_t g, uint32_t b) {
+    const uint32_t r = min(out0 + g * 16 + m, p.n_out - 1);
+#pragma unroll
+    for (int s = 0; s < 2; s++) {
+      const uint32_t sb = 2 * wv + s;
+      q[b][s][0] = w[p.o0 + (size_t)r * 128 + sb * 8 + kg];
+      q[b][s][1] = w[p.o0 + (size_t)r * 128 + sb * 8 + 4 + kg];
+      hd[b][s] = w[p.o1 + (size_t)r * 16 + sb];
+    }
+  };
+
+  // the wave's 512 activations: lane l holds values 8 l .. 8 l + 7 (super-block l / 32)
+  const float *xv = x + p.x_off + 512 * wv;
+  const float4 a0 = *(const float4 *)(xv + 8 * l), a1 = *(const float4 *)(xv + 8 * l + 4);
+  load_group(0, 0);
+  {
+    const float va[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+    float mx = 0.0f, sm = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 8; t++) {
+      mx = fmaxf(mx, fabsf(va[t]));
+      sm += va[t];
+    }
+    // sub-block sums (32 values = 4 lanes) and the wave's largest |x|
+    sm += __shfl_xor(sm, 1, 64);
+    sm += __shfl_xor(sm, 2, 64);
+    if ((l & 3) == 0) xsum[wv][l >> 2] = sm;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) mx = fmaxf(mx, __shfl_xor(mx, d, 64));
+    const int e = 14 - __builtin_amdgcn_frexp_expf(mx);
+    // hi / lo halves into B order: value v of a super-block -> chunk c = v / 64, high half
+    // hf, position p = v % 32 rounded down to 4, byte r = v % 4 -> (kg, step, element)
+    const uint32_t s = l >> 5, v0 = 8 * (l & 31);
+    const uint32_t c = v0 >> 6, hf = (v0 >> 5) & 1;
+    _Float16 *bh = (_Float16 *)&bq[wv][0][s][0][0], *bl = (_Float16 *)&bq[wv][1][s][0][0];
+#pragma unroll
+    for (int t = 0; t < 8; t++) {
+      const uint32_t pp = (v0 & 24) + (t & 4), r = t & 3;
+      const uint32_t kgv = 2 * (c & 1) + (pp >> 4), j = 4 * (c >> 1) + ((pp >> 2) & 3);
+      const uint32_t el = (r & 1) * 4 + hf * 2 + (r >> 1);
+      const float xs = __builtin_ldexpf(va[t], e);
+      const _Float16 hi = (_Float16)xs;
+      const _Float16 lo = (_Float16)(xs - (float)hi);
+      bh[(j * 4 + kgv) * 8 + el] = hi;
+      bl[(j * 4 + kgv) * 8 + el] = lo;
+    }
+    cs[wv][0][0] = __builtin_bit_cast(float, e);  // the wave's scale exponent, read back below
+  }
+  const int e = __builtin_bit_cast(int, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, cs[wv][0][0])));
+  // this lane's minimum sums: chunk kg of each super-block (sub-blocks 2 kg, 2 kg + 1)
+  const float xa0 = xsum[wv][2 * kg], xb0 = xsum[wv][2 * kg + 1];
+  const float xa1 = xsum[wv][8 + 2 * kg], xb1 = xsum[wv][8 + 2 * kg + 1];
+  const uint32_t bcol = m == 1 ? 1u : 0u;  // B lanes of column 0 and 1 (others: any values)
+
+#pragma unroll
+  for (int g = 0; g < NG; g++) {
+    const int b = g & 1;
+    if (g + 1 < NG) load_group(g + 1, b ^ 1);
+    float dsb[2], bias = 0.0f;
+#pragma unroll
+    for (int s = 0; s < 2; s++) {
+      const uint4 hc = hd[b][s];
+      const float d = f16_bits_to_f32(hc.x & 0xffffu), dmin = f16_bits_to_f32(hc.x >> 16);
+      const uint32_t sw0 = hc.y & 0x3f3f3f3fu, sw1 = (hc.w & 0x0f0f0f0fu) | ((hc.y >> 2) & 0x30303030u);
+      const uint32_t mw0 = hc.z & 0x3f3f3f3fu, mw1 = ((hc.w >> 4) & 0x0f0f0f0fu) | ((hc.z >> 2) & 0x30303030u);
+      // scales of chunks kg / 2 (words 0..3) and 2 + kg / 2 (words 4..7)
+      const NibScale k0 = nib_scale((sw0 >> (16 * h)) & 255u, (sw0 >> (16 * h + 8)) & 255u);
+      const NibScale k1 = nib_scale((sw1 >> (16 * h)) & 255u, (sw1 >> (16 * h + 8)) & 255u);
+      // minimum terms of chunk kg
+      const uint32_t mv = (kg < 2 ? mw0 : mw1) >> (16 * (kg & 1));
+      const float xa = s ? xa1 : xa0, xb = s ? xb1 : xb0;
+      bias = __builtin_fmaf(dmin, __builtin_fmaf((float)(mv & 255u), xa, (float)((mv >> 8) & 255u) * xb), bias);
+      dsb[s] = d;
+      const uint32_t wd[8] = {q[b][s][0].x, q[b][s][0].y, q[b][s][0].z, q[b][s][0].w,
+                              q[b][s][1].x, q[b][s][1].y, q[b][s][1].z, q[b][s][1].w};
+      f4v acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        const h8v bv = __builtin_bit_cast(h8v, bq[wv][bcol][s][j][kg]);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(nib_a(wd[j], j < 4 ? k0 : k1, M1, M2, F), bv, acc, 0, 0, 0);
+      }
+      // D[4 kg + i][m] in lane (m, kg): columns 0 and 1 are lanes 16 kg and 16 kg + 1
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const float v = acc[i] + dpp_f<0xb1>(acc[i]);  // + the neighbouring column
+        if (m == 0) cs[wv][s][4 * kg + i] = v;
+      }
+    }
+    bias += __shfl_xor(bias, 16, 64);
+    bias += __shfl_xor(bias, 32, 64);
+    if (kg == 0) {
+      const float t = __builtin_fmaf(dsb[1], cs[wv][1][m], dsb[0] * cs[wv][0][m]);
+      part[wv][g * 16 + m] = __builtin_ldexpf(t, -e) - bias;
+    }
+  }
+  __syncthreads();
+  if (tid < (uint32_t)OUT && out0 + tid < p.n_out) {
+    float t = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) t += part[i][tid];
+    const uint32_t yo = p.y_off + out0 + tid;
+    if (ACCUM)
+      y[yo] += t;
+    else
+      y[yo] = t;
+  }
+}
+
+// ---------------------------------------------------------------------------------------
 // Q6_K.  Lane step = 64 values of one super-block: u -> super-block u/4, half hf = (u%4)/2,
 // li = u%2.  It reads 16 B of ql at l = 16 li (a), 16 B at l + 32 (b) and 16 B of qh.
 // Group g = 0..3 is values 128 hf + 32 g + 16 li + [0,16) with scale sc[8 hf + li + 2g]
@@ -1016,6 +1189,22 @@ MV_Q4K_KS_ALL(4, 3)
 MV_Q4K_KS_ALL(4, 6)
 MV_Q4K_KS_ALL(8, 1)
 MV_Q4K_KS_ALL(8, 3)
+
+// Q4_K on the matrix cores for n_in = 4096 (matvec_q4k_mf_body): NG groups of 16 rows per
+// workgroup
+#define MV_Q4K_MF(A, G)                                                                      \
+  extern "C" __global__ __launch_bounds__(512) void matvec_q4k_mf__##A##_##G(                  \
+      const uint4 *w, const float *x, float *y, const uint32_t *ids, Segments<MatvecPush2> m) { \
+    const uint32_t s = segment_of(m, blockIdx.x);                                            \
+    (void)ids;                                                                               \
+    matvec_q4k_mf_body<A, G>(w, x, y, segment_push(m, s), blockIdx.x - m.start[s]);          \
+  }
+MV_Q4K_MF(0, 1)
+MV_Q4K_MF(1, 1)
+MV_Q4K_MF(0, 2)
+MV_Q4K_MF(1, 2)
+MV_Q4K_MF(0, 4)
+MV_Q4K_MF(1, 4)
 
 // MoE decode forms the runtime substitutes for engine dispatch pairs (skyla_hip.cpp,
 // fuse_moe): an expert's gate and up with silu_mul after them (MODE 3 over the slot grid),

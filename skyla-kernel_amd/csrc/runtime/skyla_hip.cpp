@@ -729,6 +729,19 @@ const KsRule kKsRules[] = {{0, 16383, 4, 1}};
 const KsRule kKsPairRules[] = {{0, 8191, 4, 1}};
 
 void add_ks(skyla_hip_context *ctx, const char *name, const uint32_t *spec, Retile &t) {
+  // SKYLA_HIP_MF=G: plain Q4_K launches with n_in = 4096 on the matrix-core form
+  // (matvec_q4k_mf_body), G groups of 16 rows per workgroup.  Off by default: on MI355X it
+  // measured no faster than the f32 forms (config-2 kernel trace: q+k+v 6.27 against 6.45
+  // us, o 6.41 against 5.25, gate+up 14.00 against 13.41) -- these launches are bound by
+  // their loads' latency, not by the VALU the matrix cores take over.
+  if (const char *mf = std::getenv("SKYLA_HIP_MF");
+      mf && mf[0] != '0' && std::strcmp(name, "matvec_q4k") == 0 && spec[3] == 0) {
+    const unsigned g = (unsigned)std::strtoul(mf, nullptr, 10);
+    if (hipFunction_t fn = find_function(ctx, "matvec_q4k_mf__" + std::to_string(spec[1]) + "_" + std::to_string(g))) {
+      t.alts.push_back({fn, 16 * g, 512, 0, 4096});
+      return;
+    }
+  }
   const char *env = std::getenv("SKYLA_HIP_KS");
   if (env && env[0] == '0') return;
   std::string ks;

@@ -327,3 +327,63 @@ def test_ks_shapes_against_oracle(ctx, shape, accum):
         bar = f32_reorder_bar(E.DType.Q4K, d, n_in, n, x, want) + (4e-7 if accum else 0.0)
         assert rel_l2(part, want) <= bar, (shape, i, rel_l2(part, want), bar)
         assert np.array_equal(got[i, n:], y0[i, n:])        # rows past n_out untouched
+
+
+@pytest.mark.parametrize("groups", ["1", "2", "4"])
+@pytest.mark.parametrize("accum", [False, True])
+def test_mf_shapes_against_oracle(ctx, groups, accum):
+    """The matrix-core Q4_K form (n_in = 4096; SKYLA_HIP_MF=G puts every plain Q4_K launch on
+    it with G groups of 16 rows per workgroup): three fused segments whose row counts are not
+    multiples of its workgroup, ACCUM on and off, against the oracle at the f32 bar; rows past
+    n_out stay untouched."""
+    n_in, outs = 4096, [4096, 333, 1]
+    datas = [synth.matrix("test-mf", f"{i}-{n}", E.DType.Q4K, n_in, n) for i, n in enumerate(outs)]
+    x = synth.activations("test-mf", "x", n_in)
+    with env(SKYLA_HIP_MF=groups):
+        s = Setup(ctx, [(E.DType.Q4K, n_in, n, d) for n, d in zip(outs, datas)], n_in, max(outs), rows=len(outs))
+    try:
+        y0 = synth.activations("test-mf", "y0", (len(outs), s.s_out))
+        s.set_x(x)
+        s.set_y(y0)
+
+        def body(r):
+            g = E.Graph(r, s.k, None, None, False)
+            for i, m in enumerate(s.q):
+                g.matvec(m, (s.x_off, 0), (s.y_off + i * s.s_out, 0), accum, False)
+        rec = ctx.record(False, body)
+        try:
+            assert rec.launches() == 1
+            ctx.replay(rec)
+        finally:
+            rec.free()
+        got = s.y(len(outs), s.s_out)
+    finally:
+        s.free()
+    for i, (n, d) in enumerate(zip(outs, datas)):
+        want = so.matvec(int(E.DType.Q4K), d, n_in, n, x)
+        part = got[i, :n].astype(np.float64) - (y0[i, :n] if accum else 0.0)
+        bar = f32_reorder_bar(E.DType.Q4K, d, n_in, n, x, want) + (4e-7 if accum else 0.0)
+        assert rel_l2(part, want) <= bar, (groups, i, rel_l2(part, want), bar)
+        assert np.array_equal(got[i, n:], y0[i, n:])
+
+
+@pytest.mark.parametrize("scale", [1e-30, 1e-4, 1.0, 3e4, 1e30])
+def test_mf_activation_range(ctx, scale):
+    """The matrix-core form splits x into f16 halves after a power-of-two scale per wave:
+    activations far outside the f16 range, and a vector mixing magnitudes 2^-20 .. 1 (each
+    wave's largest sets its scale), stay within the f32 bar."""
+    n_in, n_out = 4096, 512
+    d = synth.matrix("test-mf", "range", E.DType.Q4K, n_in, n_out)
+    g = synth.rng("test-mf", "range-x")
+    x = (g.standard_normal(n_in) * np.exp2(-20.0 * g.random(n_in)) * scale).astype(np.float32)
+    with env(SKYLA_HIP_MF="1"):
+        s = Setup(ctx, [(E.DType.Q4K, n_in, n_out, d)], n_in, n_out)
+    try:
+        s.set_x(x)
+        s.matvec(0)
+        got = s.y(1, n_out)[0]
+    finally:
+        s.free()
+    want = so.matvec(int(E.DType.Q4K), d, n_in, n_out, x)
+    assert np.all(np.isfinite(got))
+    assert rel_l2(got, want) <= f32_reorder_bar(E.DType.Q4K, d, n_in, n_out, x, want), rel_l2(got, want)
