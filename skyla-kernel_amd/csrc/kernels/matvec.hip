@@ -23,6 +23,7 @@
 //   * Weight loads are 16 B per lane, 1 KiB contiguous per wave instruction, and the first
 //     step's loads are issued before the staging so they overlap it.
 #include "common.h"
+#include "route.h"
 
 namespace {
 
@@ -43,6 +44,11 @@ struct MatvecPush2F {
 // matvec_q4k_glu: the gate matrix's regions, then the up matrix's (11 words)
 struct MatvecPushGlu {
   uint32_t o0, o1, x_off, y_off, n_in, n_out, ids_off, x_stride, y_stride, u0, u1;
+};
+// matvec_q4k_glur: matvec_q4k_glu's words, then moe_route's (16 words)
+struct MatvecPushGluR {
+  MatvecPushGlu g;
+  RoutePush r;
 };
 // matvec_q4k_glun: matvec_q4k_glu's words, then the norm weights and eps (13 words)
 struct MatvecPushGluN {
@@ -540,6 +546,123 @@ SK_DEV void matvec_q4k_ks_body(const uint4 *__restrict__ w, const float *x, floa
     } else {
       y[yo] = t;
     }
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// A decode token's expert down projections and moe_combine in one launch
+// (matvec_q4k_dcomb__8): graph/moe.rs:42-80 runs the down projections as the expert matvec
+// over grid.y = n_used slots (four waves, one row, 16 lanes per row -- the runtime's
+// variant for expert rows) and then moe_combine.  Here a workgroup owns DR rows for every
+// slot, so no workgroup waits for another:
+//   * each slot's activations are staged and each (slot, row) header decoded in LDS exactly
+//     as matvec_q4k_body stages them (zero past n_in, zero products past the last
+//     super-block), and every (slot, row) is summed by 16 lanes in that kernel's step
+//     order and reduced with the same DPP pattern, so each slot's row is bit-identical to
+//     the expert matvec's;
+//   * the rows' weighted sum is added to the residual in moe_combine's order
+//     (moe_combine.comp:16-27), so the residual is bit-identical to the two launches;
+//   * all the workgroup's weights are in flight at once: 16 groups of 16 lanes, group g
+//     taking slot g % 8 and rows g / 8, g / 8 + 2, ...  (n_used <= 8, n_in <= 1024).
+// The per-slot down rows are not written (nothing after moe_combine reads them).
+// ---------------------------------------------------------------------------------------
+template <int DR>
+SK_DEV void matvec_q4k_dcomb_body(const uint4 *__restrict__ w, float *a, const uint32_t *ids,
+                                  const MatvecPushComb &p, uint32_t bx) {
+  constexpr int SLOTS = 8, CHU = 32, CH_SUP = CHU / 8, LPR = 16, S = CHU / LPR;
+  static_assert(DR % 2 == 0, "two row sets per slot");
+  __shared__ float4 xf[SLOTS][8][CHU];
+  __shared__ float2 xs[SLOTS][CHU];
+  __shared__ float4 sc[SLOTS][DR][CH_SUP][4];
+  __shared__ float tot[SLOTS][DR];
+  const uint32_t tid = threadIdx.x;
+  const uint32_t units = p.n_in >> 5, supers = p.n_in >> 8;
+  const uint32_t row0 = bx * DR;
+  const uint32_t LO4 = opaque_mask(0x0f0f0f0fu), HI4 = opaque_mask(0xf0f0f0f0u);
+
+  // this lane's weights: group gi (slot gs, rows gr, gr + 2, ..), lane L of its 16
+  const uint32_t gi = tid >> 4, L = tid & 15, gs = gi % SLOTS, gr = gi / SLOTS;
+  const bool live = gs < p.n_used;
+  const uint32_t gbase = live ? ids[p.ids_off + gs] * p.n_out : 0;
+  uint4 q[DR / 2][S];
+#pragma unroll
+  for (int k = 0; k < DR / 2; k++) {
+    const uint32_t row = min(row0 + gr + 2 * k, p.n_out - 1);
+#pragma unroll
+    for (int st = 0; st < S; st++) {
+      const uint32_t i = L + st * LPR;
+      q[k][st] = make_uint4(0, 0, 0, 0);  // past n_in: multiplied by zero activations
+      if (live && i < units) q[k][st] = w[p.o0 + (size_t)(gbase + row) * units + i];
+    }
+  }
+  // stage every slot's activations (items: slot, unit, quarter) and decode the headers
+#pragma unroll
+  for (int j = 0; j < SLOTS * 4 * CHU / 256; j++) {
+    const uint32_t t = tid + 256 * j, sl = t / (4 * CHU), tt = t % (4 * CHU), u = tt >> 2, qq = tt & 3;
+    float4 va = make_float4(0.f, 0.f, 0.f, 0.f), vb = va;
+    if (sl < p.n_used && u < units) {
+      const float *xv = a + p.x_off + sl * p.x_stride;
+      const uint32_t at = (u >> 3) * 256 + ((u >> 1) & 3) * 64 + (u & 1) * 16 + (qq >> 1) * 32 + (qq & 1) * 8;
+      va = *(const float4 *)(xv + at);
+      vb = *(const float4 *)(xv + at + 4);
+    }
+    float sum = sum4(va) + sum4(vb);
+    sum += dpp_f<0xb1>(sum);  // + the other quarter of the same half
+    xf[sl][(qq >> 1) * 4 + (qq & 1) * 2][u] = va;
+    xf[sl][(qq >> 1) * 4 + (qq & 1) * 2 + 1][u] = vb;
+    if ((qq & 1) == 0) ((float *)&xs[sl][u])[qq >> 1] = sum;
+  }
+  for (uint32_t i = tid; i < (uint32_t)(SLOTS * DR * CH_SUP); i += 256) {
+    const uint32_t sl = i / (DR * CH_SUP), lr = (i / CH_SUP) % DR, sb = i % CH_SUP;
+    if (sl >= p.n_used || sb >= supers) {
+#pragma unroll
+      for (int cc = 0; cc < 4; cc++) sc[sl][lr][sb][cc] = make_float4(0.f, 0.f, 0.f, 0.f);
+      continue;
+    }
+    const uint32_t base = ids[p.ids_off + sl] * p.n_out;
+    const uint4 h = w[p.o1 + (size_t)(base + min(row0 + lr, p.n_out - 1)) * supers + sb];
+    const float d = f16_bits_to_f32(h.x & 0xffffu), dmin = f16_bits_to_f32(h.x >> 16);
+    const float d16 = d * 0.0625f;
+    const uint32_t sw[2] = {h.y & 0x3f3f3f3fu, (h.w & 0x0f0f0f0fu) | ((h.y >> 2) & 0x30303030u)};
+    const uint32_t mw[2] = {h.z & 0x3f3f3f3fu, ((h.w >> 4) & 0x0f0f0f0fu) | ((h.z >> 2) & 0x30303030u)};
+#pragma unroll
+    for (int cc = 0; cc < 4; cc++) {
+      const uint32_t sv = sw[cc >> 1] >> (16 * (cc & 1)), mv = mw[cc >> 1] >> (16 * (cc & 1));
+      const float s_lo = (float)(sv & 255u), s_hi = (float)((sv >> 8) & 255u);
+      const float m_lo = (float)(mv & 255u), m_hi = (float)((mv >> 8) & 255u);
+      sc[sl][lr][sb][cc] = make_float4(d * s_lo, d16 * s_hi, dmin * m_lo, dmin * m_hi);
+    }
+  }
+  __syncthreads();
+  // the expert matvec's steps: unit i = L + 16 st, super-block i / 8, chunk (L / 2) % 4
+  const uint32_t c = (L >> 1) & 3;
+#pragma unroll
+  for (int k = 0; k < DR / 2; k++) {
+    const uint32_t lr = gr + 2 * k;
+    float acc = 0.0f;
+#pragma unroll
+    for (int st = 0; st < S; st++) {
+      const uint32_t i = L + st * LPR, sb = (L >> 3) + st * (LPR / 8);
+      const float4 xl[4] = {xf[gs][0][i], xf[gs][1][i], xf[gs][2][i], xf[gs][3][i]};
+      const float sa = fma_bytes16(q[k][st], LO4, xl, 0.0f);
+      const float4 xh[4] = {xf[gs][4][i], xf[gs][5][i], xf[gs][6][i], xf[gs][7][i]};
+      const float sb2 = fma_bytes16(q[k][st], HI4, xh, 0.0f);
+      const float2 xsum = xs[gs][i];
+      const float4 f = sc[gs][lr][sb][c];
+      acc = __builtin_fmaf(f.x, sa, acc);
+      acc = __builtin_fmaf(f.y, sb2, acc);
+      acc = __builtin_fmaf(-f.z, xsum.x, acc);
+      acc = __builtin_fmaf(-f.w, xsum.y, acc);
+    }
+    const float total = lane_sum<LPR>(acc);
+    if (L == 0) tot[gs][lr] = total;
+  }
+  __syncthreads();
+  if (tid < (uint32_t)DR && row0 + tid < p.n_out) {
+#pragma clang fp contract(off)
+    float sum = 0.0f;
+    for (uint32_t s = 0; s < p.n_used; s++) sum += a[p.w_off + s] * tot[s][tid];
+    a[p.res_off + row0 + tid] += sum;
   }
 }
 
@@ -1213,6 +1336,37 @@ extern "C" __global__ __launch_bounds__(256) void matvec_q4k_glu__4_0_1_1_16(
     const uint4 *w, const float *x, float *y, const uint32_t *ids, Segments<MatvecPushGlu> m) {
   const uint32_t s = segment_of(m, blockIdx.x);
   matvec_q4k_body<4, 0, 1, 1, 16, 3>(w, x, y, ids, segment_push(m, s), blockIdx.x - m.start[s]);
+}
+// moe_route then the experts' gate + up + silu of one decode token in one launch: wave 0 of
+// every workgroup runs moe_route's selection (route.h) on the logits, so each workgroup
+// knows its slot's expert without waiting for another; workgroup (0, 0) also stores the
+// ids and routing weights for the launches after it.  Same ids, weights and outputs, bit
+// for bit, as moe_route then matvec_q4k_glu__4_0_1_1_16.
+extern "C" __global__ __launch_bounds__(256) void matvec_q4k_glur__4_0_1_1_16(
+    const uint4 *w, const float *x, float *y, uint32_t *ids, Segments<MatvecPushGluR> m) {
+  __shared__ uint32_t sid[16];
+  __shared__ float swt[16];
+  const MatvecPushGluR pp = m.p[0];
+  if (threadIdx.x < 64) {
+    RoutePush rp = pp.r;
+    rp.ids_off = 0;
+    rp.weights_off = 0;
+    route_token<false>(y, swt, sid, rp, 0, threadIdx.x);
+    if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x < min(pp.r.n_used, 16u)) {
+      ids[pp.r.ids_off + threadIdx.x] = sid[threadIdx.x];
+      y[pp.r.weights_off + threadIdx.x] = swt[threadIdx.x];
+    }
+  }
+  __syncthreads();
+  MatvecPushGlu g = pp.g;
+  g.ids_off = 0;
+  matvec_q4k_body<4, 0, 1, 1, 16, 3>(w, x, y, sid, g, blockIdx.x);
+}
+// an expert down projection and moe_combine for one token, no handoff (matvec_q4k_dcomb_body)
+extern "C" __global__ __launch_bounds__(256) void matvec_q4k_dcomb__8(
+    const uint4 *w, const float *x, float *y, const uint32_t *ids, Segments<MatvecPushComb> m) {
+  (void)x;  // the arena is bound as x, y and ids; y is its writable view
+  matvec_q4k_dcomb_body<8>(w, y, ids, m.p[0], blockIdx.x);
 }
 extern "C" __global__ __launch_bounds__(256) void matvec_q4k_ecomb__4_1_16(
     const uint4 *w, const float *x, float *y, const uint32_t *ids, Segments<MatvecPushComb> m, uint32_t *cnt) {

@@ -4,13 +4,13 @@
 // indices (arena.rs:85-113).  The arena's control words are ctl[0] = first token,
 // ctl[1] = position, ctl[2] = token count (engine.rs:119-123).
 #include "common.h"
+#include "route.h"
 
 namespace {
 
 constexpr uint32_t MAX_SLOTS = 1024;  // moe_sort.comp:15 (BATCH * n_used <= 1024)
 
 struct LogitsPush { uint32_t x_off, router_off, logits_off, n_embd, x_stride; };
-struct RoutePush { uint32_t logits_off, ids_off, weights_off, n_expert, n_used; };
 struct SortPush { uint32_t ids_off, table_off, list_off, n_expert, n_used; };
 struct CombinePush { uint32_t x_off, y_off, weights_off, n, stride, n_used; };
 struct SiluPush { uint32_t g_off, u_off, n, stride; };
@@ -20,23 +20,6 @@ struct LogitsRoutePush {
   LogitsPush lp;
   RoutePush rp;
 };
-
-// Monotone u32 key of a float with -0 folded onto +0 (so equal values tie exactly as the
-// float comparisons of moe_route.comp:66-81 do).
-SK_DEV uint32_t order_key(float v) {
-  const uint32_t b = __builtin_bit_cast(uint32_t, v + 0.0f);
-  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-}
-
-SK_DEV float key_value(uint32_t k) {
-  const uint32_t b = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
-  return __builtin_bit_cast(float, b);
-}
-
-template <int CTRL>
-SK_DEV uint32_t dpp_u(uint32_t v) {
-  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xf, 0xf, false);
-}
 
 }  // namespace
 
@@ -117,72 +100,7 @@ extern "C" __global__ __launch_bounds__(256) void moe_logits_t(const float *w, c
   }
 }
 
-// moe_route (moe_route.comp:55-106): per token, n_used rounds of "largest logit, lowest
-// index on ties", then weights exp(v_k - v_0) / sum.  One wave per token: expert
-// e = lane + 64 j is held in key[j] (n_expert <= 256), a round is a lane maximum, a wave
-// maximum (DPP within rows of 16, then two shuffles) and a ballot for the lowest expert
-// holding it.  Lane k keeps round k's choice; the exponentials are computed in parallel
-// and summed in round order, as the reference does.  Tokens at or beyond ctl[2] do nothing.
-namespace {
-// moe_route's selection for token `tok` on one wave (lane t).  COHERENT reads the logits with
-// agent-scope loads (written by other workgroups of the same launch).
-template <bool COHERENT>
-SK_DEV void route_token(const float *a, float *aw, uint32_t *ids, const RoutePush &p, uint32_t tok,
-                        uint32_t t) {
-  const uint32_t n_used = min(p.n_used, 16u);
-  const uint32_t n_expert = min(p.n_expert, 256u);
-  const uint32_t logits_off = p.logits_off + tok * p.n_expert;
-  // 0 marks "taken or absent"; a real key is >= 1 (only one NaN pattern maps to 0)
-  uint32_t key[4];
-#pragma unroll
-  for (int j = 0; j < 4; j++) {
-    const uint32_t e = t + 64 * j;
-    float v = 0.0f;
-    if (e < n_expert)
-      v = COHERENT ? __hip_atomic_load(a + logits_off + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                   : a[logits_off + e];
-    key[j] = e < n_expert ? max(order_key(v), 1u) : 0u;
-  }
-  float chosen = 0.0f;
-  uint32_t chosen_idx = 0;
-  for (uint32_t k = 0; k < n_used; k++) {
-    uint32_t m = max(max(key[0], key[1]), max(key[2], key[3]));
-    m = max(m, dpp_u<0xb1>(m));   // quad_perm [1,0,3,2]
-    m = max(m, dpp_u<0x4e>(m));   // quad_perm [2,3,0,1]
-    m = max(m, dpp_u<0x141>(m));  // row_half_mirror
-    m = max(m, dpp_u<0x140>(m));  // row_mirror
-    m = max(m, (uint32_t)__shfl_xor((int)m, 16, 64));
-    m = max(m, (uint32_t)__shfl_xor((int)m, 32, 64));
-    // lowest expert index holding m: the smallest j with a holder, then the lowest lane
-    uint32_t idx = 0;
-    bool found = false;
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const uint64_t holders = __ballot(key[j] == m);
-      if (!found && holders != 0) {
-        idx = (uint32_t)__builtin_ctzll(holders) + 64 * j;
-        found = true;
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < 4; j++)
-      if (idx == t + 64 * j) key[j] = 0;
-    if (t == k) {
-      chosen = key_value(m);
-      chosen_idx = idx;
-    }
-  }
-  const float largest = __shfl(chosen, 0, 64);
-  const float e = expf(chosen - largest);
-  float total = 0.0f;
-  for (uint32_t k = 0; k < n_used; k++) total += __shfl(e, (int)k, 64);
-  if (t < n_used) {
-    ids[p.ids_off + tok * p.n_used + t] = chosen_idx;
-    aw[p.weights_off + tok * p.n_used + t] = e / total;
-  }
-}
-}  // namespace
-
+// moe_route: one wave per token; tokens at or beyond ctl[2] do nothing.
 extern "C" __global__ __launch_bounds__(64) void moe_route(float *a, uint32_t *ids, RoutePush p) {
   const uint32_t tok = blockIdx.y;
   const uint32_t n_tok = __builtin_bit_cast(uint32_t, a[2]);

@@ -190,7 +190,9 @@ struct skyla_hip_pipeline {
   uint32_t tok_per_wg = 0;               // grid.x and grid.y per workgroup
   std::string name;                      // shader name
   hipFunction_t moe_fn = nullptr;        // MoE decode forms (fuse_moe): moe_logits -> moe_logits_route,
-  hipFunction_t moe_fn2 = nullptr;       // Q4_K experts -> the gate/up pair, and the down + combine form
+  hipFunction_t moe_fn2 = nullptr;       // Q4_K experts -> the gate/up pair, and the down + combine forms
+  hipFunction_t moe_fn3 = nullptr;
+  hipFunction_t moe_fn4 = nullptr;       // the gate/up pair that routes for itself
   uint32_t chain_kind = 0;               // dense matvecs matvec_chain can run (CHAIN_*), and
   uint32_t chain_accum = 0;              // whether they accumulate
   std::vector<std::vector<void *>> sets;
@@ -209,7 +211,7 @@ struct Command {
   hipFunction_t tok_fn = nullptr;
   uint32_t tok_per_wg = 0;
   std::string name;                 // the pipeline's shader name
-  hipFunction_t moe_fn = nullptr, moe_fn2 = nullptr;
+  hipFunction_t moe_fn = nullptr, moe_fn2 = nullptr, moe_fn3 = nullptr, moe_fn4 = nullptr;
   uint32_t chain_kind = 0, chain_accum = 0;
   uint32_t n_cnt = 0;               // fused MoE forms: self-resetting counters the kernel takes
   uint32_t groups[3] = {0, 0, 0};
@@ -401,21 +403,60 @@ size_t next_dispatch(const std::vector<Command> &cmds, size_t i) {
 
 // MoE decode forms.  graph/moe.rs:42-80 records a decode token's MoE layer as six
 // dependent dispatches (logits, route, gate + up, silu, down, combine), and each launch on
-// MI355X costs ~2.3 us before any work.  Three pairs can become one launch each, computing
-// the same values bit for bit (tests/test_gpu_moe.py compares every form with the six
-// launches):
+// MI355X costs ~2.3 us before any work.  The runtime can replace runs of them with one
+// launch each, computing the same values bit for bit (tests/test_gpu_moe.py compares every
+// form with the six launches):
 //   1: moe_logits then moe_route (one token)      -> moe_logits_route
 //   2: a Q4_K expert gate and up then silu_mul    -> matvec_q4k_glu__4_0_1_1_16 (writes
 //      silu(gate) * up where silu_mul leaves it; the up rows are not stored)
+//  16: moe_route, then form 2's three dispatches   -> matvec_q4k_glur__4_0_1_1_16 (every
+//      workgroup runs the route selection itself, so it needs no other's result)
 //   4: a Q4_K expert down then moe_combine        -> matvec_q4k_ecomb__4_1_16
-// The expert forms take the launch shape the runtime's variant rule gives expert matvecs
-// (four waves, one row, 16 lanes per row), so each row sums exactly as it would alone.
-// Config-4 decode, us per layer (graph replay, MI355X): six launches 26.3; form 2 24.4;
-// form 1 27.1 and form 4 26.3 -- those two hand their results from workgroup to workgroup
-// inside the launch (a coherent store, its completion, a device-scope count, coherent
-// reads), which costs as much as the launch boundary it removes -- so only form 2 is on.
-// SKYLA_HIP_MOEFUSE selects the forms as a bit mask (0 keeps the six launches).
-constexpr unsigned kMoeFormsDefault = 2;
+//   8: the same pair                              -> matvec_q4k_dcomb__8 (a workgroup owns
+//      8 rows of every slot, so it combines its own rows: no handoff; n_used <= 8 and
+//      n_in <= 1024; taken before form 4)
+// The expert forms keep the arithmetic of the launch shape the runtime's variant rule gives
+// expert matvecs (four waves, one row, 16 lanes per row), so each row sums exactly as it
+// would alone.  Config-4 decode, us per layer (graph replay, MI355X): six launches 25.9;
+// form 2 24.0; 2 + 8 21.8; 2 + 8 + 16 (three launches: logits, route + gate/up, down +
+// combine) 20.5-20.7.  Forms 1 and 4 hand results from workgroup to workgroup inside the
+// launch (a coherent store, its completion, a device-scope count, coherent reads), which
+// costs as much as the launch boundary it removes (27.1 and 26.3 against 26.3 for the six
+// launches), so they are off.  SKYLA_HIP_MOEFUSE selects the forms as a bit mask (0 keeps
+// the six launches).
+constexpr unsigned kMoeFormsDefault = 2 | 8 | 16;
+
+// The experts' gate dispatch at i, their up dispatch right after it and silu_mul after a
+// barrier (graph/moe.rs:63-72): the index of the silu_mul, or 0 when the pattern is not there.
+size_t glu_run(const std::vector<Command> &cmds, size_t i) {
+  const Command &a = cmds[i];
+  if (a.kind != Command::Dispatch || !a.moe_fn || a.name != "matvec_q4k" || a.push.size() != 9 ||
+      i + 1 >= cmds.size())
+    return 0;
+  const Command &b = cmds[i + 1];
+  const size_t j = next_dispatch(cmds, i + 1);
+  const bool ok = b.kind == Command::Dispatch && b.fn == a.fn && b.bufs == a.bufs && b.groups[1] == a.groups[1] &&
+                  b.groups[2] == 1 && a.groups[2] == 1 && b.push[2] == a.push[2] && b.push[4] == a.push[4] &&
+                  b.push[5] == a.push[5] && b.push[6] == a.push[6] && b.push[7] == a.push[7] &&
+                  b.push[8] == a.push[8] && j < cmds.size() && cmds[j].name == "silu_mul" &&
+                  cmds[j].groups[1] == 1 && cmds[j].push[0] == a.push[3] && cmds[j].push[1] == b.push[3] &&
+                  cmds[j].push[3] == 0 && cmds[j].push[2] == a.groups[1] * a.push[8] && a.push[8] >= a.push[5];
+  return ok ? j : 0;
+}
+
+// The gate/up pair launch of gate dispatch a and up dispatch b: the gate's words, then the
+// up matrix's regions.
+Command glu_command(const Command &a, const Command &b, hipFunction_t fn, const char *name) {
+  Command f = a;
+  f.fn = fn;
+  f.name = name;
+  f.threads = 256;
+  f.retile = nullptr;
+  f.groups[0] = (a.push[5] + 7) / 8;
+  f.push.push_back(b.push[0]);
+  f.push.push_back(b.push[1]);
+  return f;
+}
 std::vector<Command> fuse_moe(const std::vector<Command> &cmds) {
   const char *env = std::getenv("SKYLA_HIP_MOEFUSE");
   const unsigned forms = env ? (unsigned)std::strtoul(env, nullptr, 0) : kMoeFormsDefault;
@@ -441,35 +482,49 @@ std::vector<Command> fuse_moe(const std::vector<Command> &cmds) {
         continue;
       }
     }
+    // moe_route, then the experts' gate and up and silu_mul -> the pair that routes itself
+    if ((forms & 16) && a.kind == Command::Dispatch && a.name == "moe_route" && a.groups[0] == 1 &&
+        a.groups[1] == 1 && a.groups[2] == 1) {
+      const size_t jg = next_dispatch(cmds, i);
+      const size_t js = jg < cmds.size() ? glu_run(cmds, jg) : 0;
+      // the pair reads the logits and writes the weights through its y binding, the ids
+      // through its ids binding: the route's arena and ids buffers
+      if (js && cmds[jg].moe_fn4 && cmds[jg].push[6] == a.push[1] && a.bufs.size() == 2 &&
+          cmds[jg].bufs[2] == a.bufs[0] && cmds[jg].bufs[3] == a.bufs[1]) {
+        Command f = glu_command(cmds[jg], cmds[jg + 1], cmds[jg].moe_fn4, "matvec_q4k_glur");
+        f.push.insert(f.push.end(), a.push.begin(), a.push.end());
+        out.push_back(std::move(f));
+        i = js + 1;
+        continue;
+      }
+    }
     // expert matvec push: o0, o1, x_off, y_off, n_in, n_out, ids_off, x_stride, y_stride
     if (a.kind == Command::Dispatch && a.moe_fn && a.name == "matvec_q4k" && a.push.size() == 9) {
-      const size_t jb = i + 1 < cmds.size() ? i + 1 : cmds.size();
-      if ((forms & 2) && jb < cmds.size()) {
-        const Command &b = cmds[jb];
-        const size_t j = next_dispatch(cmds, jb);
-        if (b.kind == Command::Dispatch && b.fn == a.fn && b.bufs == a.bufs && b.groups[1] == a.groups[1] &&
-            b.groups[2] == 1 && a.groups[2] == 1 && b.push[2] == a.push[2] && b.push[4] == a.push[4] &&
-            b.push[5] == a.push[5] && b.push[6] == a.push[6] && b.push[7] == a.push[7] && b.push[8] == a.push[8] &&
-            j < cmds.size() && cmds[j].name == "silu_mul" && cmds[j].groups[1] == 1 && cmds[j].push[0] == a.push[3] &&
-            cmds[j].push[1] == b.push[3] && cmds[j].push[3] == 0 &&
-            cmds[j].push[2] == a.groups[1] * a.push[8] && a.push[8] >= a.push[5]) {
-          Command f = a;
-          f.fn = a.moe_fn;
-          f.name = "matvec_q4k_glu";
-          f.threads = 256;
-          f.retile = nullptr;
-          f.groups[0] = (a.push[5] + 7) / 8;
-          f.push.push_back(b.push[0]);
-          f.push.push_back(b.push[1]);
-          out.push_back(std::move(f));
-          i = j + 1;
-          continue;
-        }
+      if (const size_t js = (forms & 2) ? glu_run(cmds, i) : 0) {
+        out.push_back(glu_command(a, cmds[i + 1], a.moe_fn, "matvec_q4k_glu"));
+        i = js + 1;
+        continue;
       }
       const size_t j = next_dispatch(cmds, i);
-      if ((forms & 4) && a.moe_fn2 && j < cmds.size() && cmds[j].name == "moe_combine" && cmds[j].groups[1] == 1 &&
-          a.groups[2] == 1 && cmds[j].push[1] == a.push[3] && cmds[j].push[4] == a.push[8] &&
-          cmds[j].push[3] == a.push[5] && cmds[j].push[5] == a.groups[1]) {
+      const bool comb = j < cmds.size() && cmds[j].name == "moe_combine" && cmds[j].groups[1] == 1 &&
+                        a.groups[2] == 1 && cmds[j].push[1] == a.push[3] && cmds[j].push[4] == a.push[8] &&
+                        cmds[j].push[3] == a.push[5] && cmds[j].push[5] == a.groups[1];
+      if ((forms & 8) && comb && a.moe_fn3 && a.groups[1] <= 8 && a.push[4] <= 1024 && a.push[4] % 256 == 0) {
+        Command f = a;
+        f.fn = a.moe_fn3;
+        f.name = "matvec_q4k_dcomb";
+        f.threads = 256;
+        f.retile = nullptr;
+        f.groups[0] = (a.push[5] + 7) / 8;
+        f.groups[1] = 1;
+        f.push.push_back(cmds[j].push[0]);
+        f.push.push_back(cmds[j].push[2]);
+        f.push.push_back(cmds[j].push[5]);
+        out.push_back(std::move(f));
+        i = j + 1;
+        continue;
+      }
+      if ((forms & 4) && a.moe_fn2 && comb) {
         Command f = a;
         f.fn = a.moe_fn2;
         f.name = "matvec_q4k_ecomb";
@@ -1056,6 +1111,8 @@ int skyla_hip_pipeline_new(skyla_hip_context *ctx, const char *name, uint32_t n_
       p->retile->alts.size() == 1 && p->retile->alts[0].rwg == 16 && p->retile->alts[0].threads == 256) {
     p->moe_fn = find_function(ctx, "matvec_q4k_glu__4_0_1_1_16");
     p->moe_fn2 = find_function(ctx, "matvec_q4k_ecomb__4_1_16");
+    p->moe_fn3 = find_function(ctx, "matvec_q4k_dcomb__8");
+    p->moe_fn4 = find_function(ctx, "matvec_q4k_glur__4_0_1_1_16");
   }
   // dense decode matvecs matvec_chain can run (the shape is checked per launch)
   if (n_spec == 5 && spec[3] == 0 && ctx->chain_fn) {
@@ -1164,6 +1221,8 @@ int skyla_hip_record_dispatch(skyla_hip_recorder *r, const skyla_hip_pipeline *p
   c.name = p->name;
   c.moe_fn = p->moe_fn;
   c.moe_fn2 = p->moe_fn2;
+  c.moe_fn3 = p->moe_fn3;
+  c.moe_fn4 = p->moe_fn4;
   c.chain_kind = p->chain_kind;
   c.chain_accum = p->chain_accum;
   for (int i = 0; i < 3; i++) c.groups[i] = groups[i];

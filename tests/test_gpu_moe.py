@@ -304,11 +304,14 @@ def test_moe_decode_expert_variant_choice(ctx, moe):
     assert rel_l2(got["1"], out) <= F32
 
 
-@pytest.mark.parametrize("forms,n_launch", [("7", 3), ("2", 5), ("1", 5), ("4", 5)])
+@pytest.mark.parametrize("forms,n_launch", [("7", 3), ("2", 5), ("1", 5), ("4", 5), ("8", 5), ("10", 4), ("11", 3),
+                                            ("16", 4), ("18", 4), ("26", 3)])
 @pytest.mark.parametrize("seed", ["fuse-a", "fuse-b"])
 def test_moe_decode_fused_forms_equal_six_launches(ctx, moe, seed, forms, n_launch):
     """The runtime's MoE decode forms (bit 1: logits + route, 2: the experts' gate + up +
-    SiLU, 4: down + combine; 2 is the default) against the engine's six dispatches launched
+    SiLU, 16: route + gate + up + SiLU, 4 and 8: down + combine, with and without a handoff
+    between workgroups) against
+    the engine's six dispatches launched
     one by one (SKYLA_HIP_MOEFUSE=0): the same ids, routing weights, logits and residual,
     bit for bit."""
     n = synth.activations(CFG, f"{seed}-n", (1, N_EMBD))
