@@ -748,8 +748,10 @@ int chain_launches(skyla_hip_context *ctx, std::vector<Launch> &ls, void **owned
 // shapes, n_in 4096 and 12288): eight-wave workgroups (four for Q6_K launches of 12288 rows
 // or more); large launches gain from fewer lanes per row (more pipelined load steps per
 // lane, fewer workgroups staging the activations), small ones from more workgroups.
-// Q6_K 12288 -> 4096 (the down projection): 11.4 us on (8, 1, 32), 11.7 us on (4, 1, 32).  Expert rows (MOE = 1, grid.y = slots; config-4 gate/up
-// n_in 2048 and down n_in 768 over 8 slots): 16 lanes per row, one row each, four waves.
+// Q6_K 12288 -> 4096 (the down projection, f32 arithmetic), us per launch over 36 layers:
+// (8, 1, 64) 12.2, (8, 1, 32) 13.4-13.6, (4, 1, 32) 13.6, (4, 2, 64) 13.7, (4, 1, 16) 14.7.
+// Expert rows (MOE = 1, grid.y = slots; config-4 gate/up n_in 2048 and down n_in 768 over
+// 8 slots): 16 lanes per row, one row each, four waves.
 // Each entry is (min_rows, waves, rows, lanes per row); grid.x follows from n_out.
 struct VariantRule {
   const char *name;
@@ -760,7 +762,7 @@ struct VariantRule {
 };
 const VariantRule kVariantRules[] = {
     {"matvec_q4k", 0, 5, {{6144, 8, 1, 16}, {0, 8, 1, 64}}, 2},
-    {"matvec_q6k", 0, 7, {{12288, 4, 1, 16}, {0, 8, 1, 32}}, 2},
+    {"matvec_q6k", 0, 7, {{12288, 4, 1, 16}, {0, 8, 1, 64}}, 2},
     {"matvec_q4k", 1, 5, {{0, 4, 1, 16}}, 1},
     // the fused forms take the same variants (they are compiled for exactly these)
     {"matvec_q4k_norm", 0, 5, {{6144, 8, 1, 16}, {0, 8, 1, 64}}, 2},
@@ -829,8 +831,16 @@ std::shared_ptr<const Retile> make_retile(skyla_hip_context *ctx, const char *na
   auto t = std::make_shared<Retile>();
   t->n_out_word = 5;
   add_ks(ctx, name, spec, *t);
-  for (const VariantRule &r : kVariantRules) {
+  for (VariantRule r : kVariantRules) {
     if (std::strcmp(r.name, name) != 0 || r.moe != spec[3]) continue;
+    // SKYLA_HIP_VARIANT=W_R_L puts every dense launch of this kernel on one variant (sweeps)
+    if (const char *env = std::getenv("SKYLA_HIP_VARIANT"); env && !spec[3]) {
+      unsigned vw = 0, vr = 0, vl = 0;
+      if (std::sscanf(env, "%u_%u_%u", &vw, &vr, &vl) == 3) {
+        r.v[0] = {0, vw, vr, vl};
+        r.n = 1;
+      }
+    }
     t->n_out_word = r.n_out_word;
     std::vector<MatvecAlt> alts;
     for (int i = 0; i < r.n; i++) {
