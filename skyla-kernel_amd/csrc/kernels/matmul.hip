@@ -898,7 +898,10 @@ SK_DEV void matmul_tile128_w(const uint4 *__restrict__ w, const uint16_t *__rest
         const uint32_t tok = 32 * (tb + j) + 8 * (i >> 2) + 4 * hh + (i & 3);
         if (tok < n_tok) {
           float *o = y + p.y_off + (size_t)yrow[tok] * p.y_stride + my_row;
-          *o = ACCUM ? *o + acc[j][i] : acc[j][i];
+          float v = acc[j][i];
+          // XHALF = 2: the rows came from x_half_rows as x * 2^-e; scale back (exact)
+          if constexpr (XHALF == 2) v = __builtin_ldexpf(v, ((const int *)x)[yrow[tok]]);
+          *o = ACCUM ? *o + v : v;
         }
       }
     }
@@ -1105,6 +1108,76 @@ MMX(2, 0, 0, float)
 MMX(2, 1, 0, float)
 MMX(2, 0, 1, f16)
 MMX(2, 1, 1, f16)
+
+// Dense K-quant tiles on f16 rows that x_half_rows wrote (XHALF = 2): x is that buffer (the
+// per-row exponents first, then the rows), same arguments as matmul_w8.
+#define MMH(T, A)                                                                                 \
+  extern "C" __global__ __launch_bounds__(512) void matmul_x8__##T##_##A(                          \
+      const uint4 *w, const uint16_t *wd, const f16 *x, float *y, const uint32_t *ctl,            \
+      MatmulPush p, float *ws, uint32_t *cnt, uint32_t S) {                                       \
+    matmul_tile128_w<T, A, 2, 8>(w, wd, x, y, ctl, p, ws, cnt, S);                                \
+  }
+MMH(1, 0)
+MMH(1, 1)
+MMH(2, 0)
+MMH(2, 1)
+
+// f32 activation rows to f16 rows for the dense K-quant tiles, once per launch instead of
+// in every tile (the runtime inserts it before dense K-quant matmuls with f32 inputs; one
+// conversion serves every matmul that reads the same rows before the next barrier).  Row t
+// (t < ctl[2]) of x -- x_off + t * x_stride, n_in values -- becomes h[t * n_in ..] =
+// f16(x * 2^-e_t), with e_t = 0 unless the row's largest |x| reaches 2^15, then its
+// exponent - 14 (the tile's range guard, applied to the whole row): e[t] = e_t, and the tile
+// multiplies its sums back by 2^e_t.  With e_t = 0 the f16 values, and so the GEMM's bits,
+// are those of the tile's own conversion (round to nearest even).  Grid: one workgroup per
+// row of the launch's token tiles; out = [e: one int32 per row][rows: f16 from u32 h_off,
+// n_in per row, 16-byte aligned].
+struct XHalfPush {
+  uint32_t x_off, x_stride, n_in, h_off;
+};
+extern "C" __global__ __launch_bounds__(256) void x_half_rows(const float *x, uint32_t *out, const uint32_t *ctl,
+                                                              XHalfPush p) {
+  const uint32_t t = blockIdx.x, tid = threadIdx.x;
+  if (t >= ctl[2]) return;
+  const float *xr = x + p.x_off + (size_t)t * p.x_stride;
+  constexpr int MAXV = 48;  // values per thread: n_in <= 12288
+  float4 v[MAXV / 4];
+  float m = 0.0f;
+#pragma unroll
+  for (int i = 0; i < MAXV / 4; i++) {
+    const uint32_t k = 4 * (tid + 256 * i);
+    v[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (k < p.n_in) v[i] = *(const float4 *)(xr + k);
+    m = fmaxf(m, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
+  }
+  // the row's largest |x| (NaN counts as big, as in the tile's guard)
+  __shared__ uint32_t big[4];
+  __shared__ float wm[4];
+  const bool b = !(m < 32768.0f);
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) m = fmaxf(m, __shfl_xor(m, d, 64));
+  const uint64_t anyb = __ballot(b);
+  if ((tid & 63) == 0) {
+    wm[tid >> 6] = m;
+    big[tid >> 6] = anyb != 0;
+  }
+  __syncthreads();
+  const float tm = fmaxf(fmaxf(wm[0], wm[1]), fmaxf(wm[2], wm[3]));
+  const bool any = big[0] | big[1] | big[2] | big[3];
+  const int e = any && tm >= 32768.0f ? (int)((__builtin_bit_cast(uint32_t, tm) >> 23) & 255u) - 127 - 14 : 0;
+  const float sc = __builtin_ldexpf(1.0f, -e);
+  f16 *h = (f16 *)(out + p.h_off) + (size_t)t * p.n_in;
+#pragma unroll
+  for (int i = 0; i < MAXV / 4; i++) {
+    const uint32_t k = 4 * (tid + 256 * i);
+    if (k < p.n_in) {
+      float4 a = v[i];
+      if (e) a = make_float4(a.x * sc, a.y * sc, a.z * sc, a.w * sc);
+      *(uint2 *)(h + k) = make_uint2(as_u32(pack_f16x2(a.x, a.y)), as_u32(pack_f16x2(a.z, a.w)));
+    }
+  }
+  if (tid == 0) out[t] = (uint32_t)e;
+}
 
 // Workspace of skyla_hip_dispatch_noalloc, the entry point that allocates nothing: the K
 // split's f32 partial tiles (SCRATCH_TILES of 128 x 128), then its per-tile arrival

@@ -136,6 +136,7 @@ struct skyla_hip_context {
   // null when a workgroup cannot be resident on every CU at once
   hipFunction_t chain_fn = nullptr;
   uint32_t n_cu = 0;
+  hipFunction_t x_half_rows = nullptr;  // f16 row prepass of dense K-quant matmuls (matmul.hip)
 };
 
 struct HostFree {
@@ -185,6 +186,7 @@ struct skyla_hip_pipeline {
   bool segmented = false;
   std::shared_ptr<const Retile> retile;  // matvec pipelines with a variant rule
   hipFunction_t split_fn = nullptr;      // dense K-quant matmul: the K-split variant
+  hipFunction_t hx_fn = nullptr;         // and its variant on x_half_rows's f16 rows
   uint32_t split_threads = 0;
   hipFunction_t tok_fn = nullptr;        // batched form: a tok_per_wg x tok_per_wg block of
   uint32_t tok_per_wg = 0;               // grid.x and grid.y per workgroup
@@ -208,6 +210,7 @@ struct Command {
   std::shared_ptr<const Retile> retile;
   hipFunction_t split_fn = nullptr;
   uint32_t split_threads = 0;
+  hipFunction_t hx_fn = nullptr;
   hipFunction_t tok_fn = nullptr;
   uint32_t tok_per_wg = 0;
   std::string name;                 // the pipeline's shader name
@@ -242,6 +245,10 @@ struct Launch {
   // and for a chain launch its arguments (stage table, stage count, synchronisation words)
   bool stage_ok = false;
   ChainStage stage{};
+  // f16 row prepass: bufs[xh_buf] is replaced by the recording's f16-row buffer, which
+  // holds xh_bytes for this launch
+  int xh_buf = -1;
+  uint64_t xh_bytes = 0;
   bool chain = false;
   uint64_t chain_table = 0;
   uint32_t chain_n = 0;
@@ -546,24 +553,71 @@ std::vector<Command> fuse_moe(const std::vector<Command> &cmds) {
   return out;
 }
 
+// f16 rows for a dense K-quant matmul with f32 inputs (matmul.hip, x_half_rows), and the
+// matmul on them: the conversion the tile would do per stage, done once per launch with a
+// per-row scale, lets the tile read f16 (config-3 GEMMs 14-19% faster).  One prepass serves
+// every such matmul that reads the same rows before the next barrier (dispatches between
+// barriers are independent: none of them writes those rows).  Buffer pointers are filled
+// in by bind_workspace.  MatmulPush words: x_off 4, n_in 6, x_stride 8.
+Launch x_half_prepass(skyla_hip_context *ctx, const Command &a, uint64_t h_bytes_off) {
+  Launch l;
+  l.fn = ctx->x_half_rows;
+  l.threads = 256;
+  l.groups[0] = a.groups[2] * 128;  // every row of the launch's token tiles (rows >= ctl[2] skip)
+  l.groups[1] = l.groups[2] = 1;
+  l.bufs = {a.bufs[2], nullptr, a.bufs[4]};
+  l.args = {a.push[4], a.push[8], a.push[6], (uint32_t)(h_bytes_off / 4)};
+  l.xh_buf = 1;
+  l.xh_bytes = h_bytes_off + (uint64_t)l.groups[0] * a.push[6] * 2;
+  return l;
+}
+
 // The launch list of a recording.  Barriers need no command of their own: launches on one
 // stream (and the nodes of a graph captured from it) run in order.  SKYLA_HIP_FUSE=0 keeps
-// one launch per dispatch.
-std::vector<Launch> build_launches(const std::vector<Command> &recorded) {
+// one launch per dispatch; SKYLA_HIP_XHALF=0 keeps the matmuls' own f32 staging.
+std::vector<Launch> build_launches(skyla_hip_context *ctx, const std::vector<Command> &recorded) {
   const std::vector<Command> cmds = fuse_moe(recorded);
   const char *env = std::getenv("SKYLA_HIP_FUSE");
   const bool fuse = !(env && env[0] == '0');
+  const char *xenv = std::getenv("SKYLA_HIP_XHALF");
+  const bool xhalf = ctx && ctx->x_half_rows && !(xenv && xenv[0] == '0');
   std::vector<Launch> out;
+  std::vector<uint32_t> xkey;  // the rows the last prepass converted, until a barrier
   for (size_t i = 0; i < cmds.size();) {
     const Command &a = cmds[i];
     if (a.kind == Command::Mark) {
       Launch m;
       m.mark = true;
       out.push_back(std::move(m));
+      xkey.clear();
       i++;
       continue;
     }
     if (a.kind != Command::Dispatch) {
+      xkey.clear();
+      i++;
+      continue;
+    }
+    if (xhalf && a.hx_fn && !a.segmented && a.push.size() == 13 && a.bufs.size() == 5 && a.groups[1] == 1 &&
+        a.push[6] % 256 == 0 && a.push[6] <= 12288 && a.push[4] % 4 == 0 && a.push[8] % 4 == 0) {
+      const uint32_t rows = a.groups[2] * 128;
+      const uint64_t h_off = ((uint64_t)rows * 4 + 255) & ~(uint64_t)255;
+      const std::vector<uint32_t> key = {(uint32_t)((uintptr_t)a.bufs[2] >> 32), (uint32_t)(uintptr_t)a.bufs[2],
+                                         a.push[4], a.push[8], a.push[6], a.groups[2]};
+      if (key != xkey) {
+        out.push_back(x_half_prepass(ctx, a, h_off));
+        xkey = key;
+      }
+      const Command *one[1] = {&a};
+      Launch l = pack(one, 1);
+      l.fn = a.hx_fn;
+      l.threads = a.split_threads;
+      if (!l.split) l.split = 1;  // the K-split arguments, unsplit
+      l.args[4] = (uint32_t)(h_off / 2);  // f16 units
+      l.args[8] = a.push[6];
+      l.xh_buf = 2;
+      l.xh_bytes = out.back().xh_bytes;
+      out.push_back(std::move(l));
       i++;
       continue;
     }
@@ -606,33 +660,38 @@ int launch(hipStream_t stream, const Launch &l) {
 }
 
 // Gives the K-split launches of a list their workspace: one device allocation (partial
-// tiles, then per-tile counters) sized for the largest, shared by all of them since the
-// launches of a list run one after another on one stream.  The counters are zeroed here,
-// outside any graph capture, and every launch leaves them zero.  *owned receives the
-// allocation (nullptr when no launch splits).
+// tiles, then per-tile counters, then the f16 rows of the matmul prepass) sized for the
+// largest, shared by all of them since the launches of a list run one after another on one
+// stream.  The counters are zeroed here, outside any graph capture, and every launch leaves
+// them zero.  *owned receives the allocation (nullptr when no launch needs one).
 int bind_workspace(std::vector<Launch> &ls, void **owned) {
   *owned = nullptr;
-  uint64_t ws = 0, n_cnt = 0;
-  for (const Launch &l : ls)
+  uint64_t ws = 0, n_cnt = 0, xh = 0;
+  for (const Launch &l : ls) {
     if (l.split || l.cnt_arg) {
       ws = std::max(ws, l.ws_bytes);
       n_cnt = std::max<uint64_t>(n_cnt, l.n_cnt);
     }
-  if (!ws && !n_cnt) return SKYLA_HIP_OK;
+    if (l.xh_buf >= 0) xh = std::max(xh, l.xh_bytes);
+  }
+  if (!ws && !n_cnt && !xh) return SKYLA_HIP_OK;
   const uint64_t cnt_off = (ws + 255) & ~(uint64_t)255;
+  const uint64_t xh_off = (cnt_off + n_cnt * 4 + 255) & ~(uint64_t)255;
   void *mem = nullptr;
-  HIP_TRY(hipMalloc(&mem, cnt_off + n_cnt * 4));
+  HIP_TRY(hipMalloc(&mem, xh_off + xh));
   hipError_t e = hipMemset((char *)mem + cnt_off, 0, n_cnt * 4);
   if (e == hipSuccess) e = hipDeviceSynchronize();
   if (e != hipSuccess) {
     hipFree(mem);
     return fail(SKYLA_HIP_E_DEVICE, "K-split workspace: %s", hipGetErrorString(e));
   }
-  for (Launch &l : ls)
+  for (Launch &l : ls) {
     if (l.split || l.cnt_arg) {
       l.ws = mem;
       l.cnt = (char *)mem + cnt_off;
     }
+    if (l.xh_buf >= 0) l.bufs[l.xh_buf] = (char *)mem + xh_off;
+  }
   *owned = mem;
   return SKYLA_HIP_OK;
 }
@@ -927,6 +986,7 @@ int skyla_hip_context_new(int device, skyla_hip_context **out) {
       return fail(SKYLA_HIP_E_DEVICE, "hipModuleGetFunction(fill_u32): %s", hipGetErrorString(fe));
     }
   }
+  ctx->x_half_rows = find_function(ctx.get(), "x_half_rows");
   // matvec_chain waits at grid barriers, so it runs only if one workgroup fits on every CU
   // at once: the grid is one workgroup per CU and the kernel's occupancy must allow one
   {
@@ -1145,6 +1205,11 @@ int skyla_hip_pipeline_new(skyla_hip_context *ctx, const char *name, uint32_t n_
       p->split_fn = find_function(ctx, ssym);
       p->split_threads = 512;
     }
+    // f32 inputs: the tile on x_half_rows's f16 rows (build_launches inserts the prepass)
+    if (!(n_spec == 4 && spec[3])) {
+      p->hx_fn = find_function(ctx, "matmul_x8__" + std::to_string(spec[0]) + "_" + std::to_string(spec[1]));
+      p->split_threads = 512;
+    }
   }
   int max_threads = 0;
   if (hipFuncGetAttribute(&max_threads, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, p->fn) ==
@@ -1225,6 +1290,7 @@ int skyla_hip_record_dispatch(skyla_hip_recorder *r, const skyla_hip_pipeline *p
   c.segmented = p->segmented;
   c.retile = p->retile;
   c.split_fn = p->split_fn;
+  c.hx_fn = p->hx_fn;
   c.split_threads = p->split_threads;
   c.tok_fn = p->tok_fn;
   c.tok_per_wg = p->tok_per_wg;
@@ -1283,7 +1349,7 @@ int skyla_hip_record_end(skyla_hip_recorder *r, skyla_hip_recording **out) {
   rec->cmds = std::move(r->cmds);
   for (const Command &c : rec->cmds)
     if (c.kind == Command::Mark) rec->labels.push_back(c.label);
-  rec->launches = build_launches(rec->cmds);
+  rec->launches = build_launches(rec->ctx, rec->cmds);
   rec->mark_ns.assign(rec->labels.size(), 0.0);
   HIP_TRY(hipSetDevice(rec->ctx->device));
   if (int s = bind_workspace(rec->launches, &rec->workspace)) return s;
@@ -1465,6 +1531,7 @@ int skyla_hip_time_dispatch(skyla_hip_context *ctx, const skyla_hip_pipeline *p,
   c.segmented = p->segmented;
   c.retile = p->retile;
   c.split_fn = p->split_fn;
+  c.hx_fn = p->hx_fn;
   c.split_threads = p->split_threads;
   c.tok_fn = p->tok_fn;
   c.tok_per_wg = p->tok_per_wg;
@@ -1518,6 +1585,7 @@ int skyla_hip_dispatch_noalloc(skyla_hip_context *ctx, const skyla_hip_pipeline 
   c.segmented = p->segmented;
   c.retile = p->retile;
   c.split_fn = p->split_fn;
+  c.hx_fn = p->hx_fn;
   c.split_threads = p->split_threads;
   c.tok_fn = p->tok_fn;
   c.tok_per_wg = p->tok_per_wg;

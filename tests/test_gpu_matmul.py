@@ -8,7 +8,7 @@ the oracle as well.
 import numpy as np
 import pytest
 
-from helpers import Setup, rel_l2
+from helpers import Setup, env, rel_l2
 from oracle import skyla_oracle as so
 from skyla_hip import engine as E
 from skyla_hip import synth
@@ -86,3 +86,54 @@ def test_matmul_config3(ctx, name, dtype, n_in, n_out):
     got, want = _run(ctx, dtype, n_in, n_out, 512, tag="qwen3-8b-prefill")
     err = rel_l2(got, want)
     assert err <= TOL and err <= GUARD, err
+
+
+@pytest.mark.parametrize("name,dtype,n_in,n_out,n_tok,accum", [
+    ("q", E.DType.Q4K, 4096, 4096, 512, False), ("gate", E.DType.Q4K, 4096, 12288, 512, False),
+    ("down", E.DType.Q6K, 12288, 4096, 512, True), ("ragged", E.DType.Q4K, 1024, 200, 37, True),
+    ("ragged6", E.DType.Q6K, 768, 130, 100, False),
+])
+def test_matmul_f16_prepass_same_bits(ctx, name, dtype, n_in, n_out, n_tok, accum):
+    """The runtime's f16 row prepass (x_half_rows, then the tile on f16 rows) against the
+    tile's own f32 staging (SKYLA_HIP_XHALF=0): the same bits while no activation reaches
+    2^15, K split or not, ACCUM or not, ragged token counts."""
+    got1, want = _run(ctx, dtype, n_in, n_out, n_tok, accum=accum, tag="mm-xh")
+    with env(SKYLA_HIP_XHALF=0):
+        got0, _ = _run(ctx, dtype, n_in, n_out, n_tok, accum=accum, tag="mm-xh")
+    assert np.array_equal(got1.view(np.uint32), got0.view(np.uint32))
+    assert rel_l2(got1, want) <= GUARD
+
+
+def test_matmul_f16_prepass_shared(ctx):
+    """Two matmuls on the same rows with no barrier between them share one prepass (three
+    launches), and each gives the bits of its own f32-staged launch."""
+    n_in, n_tok = 1024, 70
+    mats = [(E.DType.Q4K, n_in, n, synth.matrix("mm-xh", f"shared-{n}", E.DType.Q4K, n_in, n)) for n in (256, 384)]
+    x = synth.activations("mm-xh", "shared-x", (n_tok, n_in))
+    got = {}
+    for xh in ("1", "0"):
+        with env(SKYLA_HIP_XHALF=xh):
+            s = Setup(ctx, mats, n_in, 384, rows=2 * n_tok)
+            try:
+                s.set_x(x)
+                z = -(-n_tok // E.MATMUL_TILE_COLS)
+
+                def body(r):
+                    g = E.Graph(r, s.k, None, None, True)
+                    for i, m in enumerate(s.q):
+                        g.matvec(m, (s.x_off, s.s_in), (s.y_off + i * n_tok * s.s_out, s.s_out), False, True,
+                                 groups_z=z)
+                rec = ctx.record(False, body)
+                try:
+                    launches = rec.launches()
+                    ctx.replay(rec)
+                finally:
+                    rec.free()
+                got[xh] = (launches, s.y(2 * n_tok, s.s_out))
+            finally:
+                s.free()
+    assert got["1"][0] == 3 and got["0"][0] == 2
+    assert np.array_equal(got["1"][1].view(np.uint32), got["0"][1].view(np.uint32))
+    for i, (dt, _, n, d) in enumerate(mats):
+        want = so.matmul(int(dt), d, n_in, n, x)
+        assert rel_l2(got["1"][1][i * n_tok:(i + 1) * n_tok, :n], want) <= GUARD
