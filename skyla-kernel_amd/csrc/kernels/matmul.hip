@@ -1122,6 +1122,19 @@ MMH(1, 1)
 MMH(2, 0)
 MMH(2, 1)
 
+// The four-wave tile on the same f16 rows (128 tokens per wave, 128-k chunks).
+#define MMH4(T, A)                                                                                \
+  extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void       \
+      matmul_x4__##T##_##A(                                                                       \
+      const uint4 *w, const uint16_t *wd, const f16 *x, float *y, const uint32_t *ctl,            \
+      MatmulPush p, float *ws, uint32_t *cnt, uint32_t S) {                                       \
+    matmul_tile128_w<T, A, 2, 4>(w, wd, x, y, ctl, p, ws, cnt, S);                                \
+  }
+MMH4(1, 0)
+MMH4(1, 1)
+MMH4(2, 0)
+MMH4(2, 1)
+
 // f32 activation rows to f16 rows for the dense K-quant tiles, once per launch instead of
 // in every tile (the runtime inserts it before dense K-quant matmuls with f32 inputs; one
 // conversion serves every matmul that reads the same rows before the next barrier).  Row t

@@ -187,6 +187,7 @@ struct skyla_hip_pipeline {
   std::shared_ptr<const Retile> retile;  // matvec pipelines with a variant rule
   hipFunction_t split_fn = nullptr;      // dense K-quant matmul: the K-split variant
   hipFunction_t hx_fn = nullptr;         // and its variant on x_half_rows's f16 rows
+  hipFunction_t hx4_fn = nullptr;        // the four-wave tile on those rows
   uint32_t split_threads = 0;
   hipFunction_t tok_fn = nullptr;        // batched form: a tok_per_wg x tok_per_wg block of
   uint32_t tok_per_wg = 0;               // grid.x and grid.y per workgroup
@@ -210,7 +211,7 @@ struct Command {
   std::shared_ptr<const Retile> retile;
   hipFunction_t split_fn = nullptr;
   uint32_t split_threads = 0;
-  hipFunction_t hx_fn = nullptr;
+  hipFunction_t hx_fn = nullptr, hx4_fn = nullptr;
   hipFunction_t tok_fn = nullptr;
   uint32_t tok_per_wg = 0;
   std::string name;                 // the pipeline's shader name
@@ -581,6 +582,7 @@ std::vector<Launch> build_launches(skyla_hip_context *ctx, const std::vector<Com
   const bool fuse = !(env && env[0] == '0');
   const char *xenv = std::getenv("SKYLA_HIP_XHALF");
   const bool xhalf = ctx && ctx->x_half_rows && !(xenv && xenv[0] == '0');
+  const bool x4 = !(xenv && xenv[0] == '8');  // SKYLA_HIP_XHALF=8: the eight-wave tile throughout
   std::vector<Launch> out;
   std::vector<uint32_t> xkey;  // the rows the last prepass converted, until a barrier
   for (size_t i = 0; i < cmds.size();) {
@@ -612,6 +614,14 @@ std::vector<Launch> build_launches(skyla_hip_context *ctx, const std::vector<Com
       Launch l = pack(one, 1);
       l.fn = a.hx_fn;
       l.threads = a.split_threads;
+      // Launches of more than 128 tiles (no K split) run the four-wave tile, two workgroups
+      // per CU: each dequantised fragment feeds four MFMAs (M = 512 gate: 124 -> 108 us).
+      // K-split launches keep the eight-wave tile (the four-wave one split four ways
+      // measured 1.2-1.7x slower).  Both give the same bits.
+      if (!l.split && x4 && a.hx4_fn) {
+        l.fn = a.hx4_fn;
+        l.threads = 256;
+      }
       if (!l.split) l.split = 1;  // the K-split arguments, unsplit
       l.args[4] = (uint32_t)(h_off / 2);  // f16 units
       l.args[8] = a.push[6];
@@ -1208,6 +1218,7 @@ int skyla_hip_pipeline_new(skyla_hip_context *ctx, const char *name, uint32_t n_
     // f32 inputs: the tile on x_half_rows's f16 rows (build_launches inserts the prepass)
     if (!(n_spec == 4 && spec[3])) {
       p->hx_fn = find_function(ctx, "matmul_x8__" + std::to_string(spec[0]) + "_" + std::to_string(spec[1]));
+      p->hx4_fn = find_function(ctx, "matmul_x4__" + std::to_string(spec[0]) + "_" + std::to_string(spec[1]));
       p->split_threads = 512;
     }
   }
@@ -1291,6 +1302,7 @@ int skyla_hip_record_dispatch(skyla_hip_recorder *r, const skyla_hip_pipeline *p
   c.retile = p->retile;
   c.split_fn = p->split_fn;
   c.hx_fn = p->hx_fn;
+  c.hx4_fn = p->hx4_fn;
   c.split_threads = p->split_threads;
   c.tok_fn = p->tok_fn;
   c.tok_per_wg = p->tok_per_wg;
@@ -1532,6 +1544,7 @@ int skyla_hip_time_dispatch(skyla_hip_context *ctx, const skyla_hip_pipeline *p,
   c.retile = p->retile;
   c.split_fn = p->split_fn;
   c.hx_fn = p->hx_fn;
+  c.hx4_fn = p->hx4_fn;
   c.split_threads = p->split_threads;
   c.tok_fn = p->tok_fn;
   c.tok_per_wg = p->tok_per_wg;
@@ -1586,6 +1599,7 @@ int skyla_hip_dispatch_noalloc(skyla_hip_context *ctx, const skyla_hip_pipeline 
   c.retile = p->retile;
   c.split_fn = p->split_fn;
   c.hx_fn = p->hx_fn;
+  c.hx4_fn = p->hx4_fn;
   c.split_threads = p->split_threads;
   c.tok_fn = p->tok_fn;
   c.tok_per_wg = p->tok_per_wg;

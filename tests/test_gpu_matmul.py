@@ -94,9 +94,10 @@ def test_matmul_config3(ctx, name, dtype, n_in, n_out):
     ("ragged6", E.DType.Q6K, 768, 130, 100, False),
 ])
 def test_matmul_f16_prepass_same_bits(ctx, name, dtype, n_in, n_out, n_tok, accum):
-    """The runtime's f16 row prepass (x_half_rows, then the tile on f16 rows) against the
-    tile's own f32 staging (SKYLA_HIP_XHALF=0): the same bits while no activation reaches
-    2^15, K split or not, ACCUM or not, ragged token counts."""
+    """The runtime's f16 row prepass (x_half_rows, then the tile on f16 rows: four waves
+    unless the launch is K-split) against the eight-wave tile's own f32 staging
+    (SKYLA_HIP_XHALF=0): the same bits while no activation reaches 2^15, K split or not,
+    ACCUM or not, ragged token counts."""
     got1, want = _run(ctx, dtype, n_in, n_out, n_tok, accum=accum, tag="mm-xh")
     with env(SKYLA_HIP_XHALF=0):
         got0, _ = _run(ctx, dtype, n_in, n_out, n_tok, accum=accum, tag="mm-xh")
