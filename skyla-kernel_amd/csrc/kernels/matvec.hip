@@ -1025,6 +1025,113 @@ SK_DEV void matvec_q6k_body(const uint4 *__restrict__ w, const uint16_t *__restr
 }
 
 // ---------------------------------------------------------------------------------------
+// Q6_K, K-split form for n_in = 12288 (the Qwen3-8B down projection).  Three waves split
+// every row the workgroup owns into its 192 units of 64 values: lane l of wave w takes unit
+// u = 64 w + l (super-block u/4, half hf = (u/2)%2, li = u%2, as in matvec_q6k_body) of
+// each row.  A lane's 64 activations and their four 16-value sums are the same for every
+// row it touches: they are loaded once, into registers, and no activation goes through
+// LDS.  Per row the lane loads its unit's 48 quant bytes (16 B of ql at l = 16 li, 16 B at
+// l + 32, 16 B of qh), the 8 scale bytes of its half and d, one row-group of RPL rows ahead
+// of the arithmetic.  Each group sum is matvec_q6k_body's (from -32 sum(x), four words of
+// rebuilt 6-bit quants); the four take d*sc (quant.rs:72-87) and are reduced over the wave
+// with DPP, and the three waves' row partials meet in LDS once, at the end, in wave order.
+// PD row-groups are loaded ahead of the arithmetic (at 4096 rows one row-group of one row
+// ahead measured fastest: issuing more of a lane's rows at once was slower).
+// ---------------------------------------------------------------------------------------
+template <int ACCUM, int RPL, int NG, int PD = 1>
+SK_DEV void matvec_q6k_ks_body(const uint4 *__restrict__ w, const uint16_t *__restrict__ wd, const float *x,
+                               float *y, const MatvecPush4 &p, uint32_t bx) {
+  constexpr int OUT = RPL * NG;     // rows per workgroup
+  constexpr uint32_t SUPERS = 48;   // super-blocks per row (n_in = 12288, checked by the host)
+  __shared__ float part[3][OUT];
+
+  const uint32_t tid = threadIdx.x, wv = tid >> 6, l = tid & 63;
+  const uint32_t u = wv * 64 + l;
+  const uint32_t sb = u >> 2, hf = (u >> 1) & 1, li = u & 1;
+  const uint32_t LO4 = opaque_mask(0x0f0f0f0fu), H2 = opaque_mask(0x30303030u);
+  const uint32_t out0 = bx * OUT;
+
+  struct RowQ {
+    uint4 a, b, h;
+    uint2 sc;
+    uint32_t d;
+  };
+  auto load_group = [&](uint32_t g, RowQ (&q)[RPL]) {
+#pragma unroll
+    for (int r = 0; r < RPL; r++) {
+      const uint32_t rs = min(out0 + g * RPL + r, p.n_out - 1) * SUPERS + sb;
+      q[r].a = w[p.o0 + rs * 8 + hf * 4 + li];
+      q[r].b = w[p.o0 + rs * 8 + hf * 4 + 2 + li];
+      q[r].h = w[p.o1 + rs * 4 + hf * 2 + li];
+      q[r].sc = ((const uint2 *)(w + p.o2 + rs))[hf];
+      q[r].d = wd[p.o3 + rs];
+    }
+  };
+
+  // activations first: group g = values 128 hf + 32 g + 16 li + [0, 16) of super-block sb
+  RowQ q[NG][RPL];  // row-group g's operands, loaded PD groups ahead of its arithmetic
+  const float *xv = x + p.x_off + sb * 256 + hf * 128 + li * 16;
+  float4 xg[4][4];
+#pragma unroll
+  for (int g = 0; g < 4; g++)
+#pragma unroll
+    for (int k = 0; k < 4; k++) xg[g][k] = *(const float4 *)(xv + 32 * g + 4 * k);
+#pragma unroll
+  for (int g = 0; g < PD && g < NG; g++) load_group(g, q[g]);
+  float ib[4];
+#pragma unroll
+  for (int g = 0; g < 4; g++)
+    ib[g] = -32.0f * ((sum4(xg[g][0]) + sum4(xg[g][1])) + (sum4(xg[g][2]) + sum4(xg[g][3])));
+
+#pragma unroll
+  for (int g = 0; g < NG; g++) {
+    if (g + PD < NG) load_group(g + PD, q[g + PD]);
+    const RowQ (&qc)[RPL] = q[g];
+#pragma unroll
+    for (int r = 0; r < RPL; r++) {
+      const uint32_t hv[4] = {qc[r].h.x, qc[r].h.y, qc[r].h.z, qc[r].h.w};
+      float t[4];
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const uint4 qv = (j & 1) ? qc[r].b : qc[r].a;
+        const uint32_t wv4[4] = {qv.x, qv.y, qv.z, qv.w};
+        float tg = ib[j];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+          const uint32_t lo = j < 2 ? wv4[k] : wv4[k] >> 4;
+          const uint32_t hb = j == 0 ? hv[k] << 4 : j == 1 ? hv[k] << 2 : j == 2 ? hv[k] : hv[k] >> 2;
+          tg = fma_bytes((lo & LO4) | (hb & H2), xg[j][k], tg);
+        }
+        t[j] = tg;
+      }
+      // d * sc[8 hf + li + 2 j]: bytes li + 2 j of the half's 8 scale bytes
+      const float d = f16_bits_to_f32(qc[r].d & 0xffffu);
+      float f[4];
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const uint32_t word = j < 2 ? qc[r].sc.x : qc[r].sc.y;
+        f[j] = d * (float)(int)(int8_t)((word >> (8 * (li + 2 * (j & 1)))) & 255u);
+      }
+      float v = f[0] * t[0];
+      v = __builtin_fmaf(f[1], t[1], v);
+      v = __builtin_fmaf(f[2], t[2], v);
+      v = __builtin_fmaf(f[3], t[3], v);
+      v = lane_sum<64>(v);
+      if (l == 0) part[wv][g * RPL + r] = v;
+    }
+  }
+  __syncthreads();
+  if (tid < (uint32_t)OUT && out0 + tid < p.n_out) {
+    const float t = (part[0][tid] + part[1][tid]) + part[2][tid];
+    const uint32_t yo = p.y_off + out0 + tid;
+    if (ACCUM)
+      y[yo] += t;
+    else
+      y[yo] = t;
+  }
+}
+
+// ---------------------------------------------------------------------------------------
 // Q8_0.  Lane step = 16 quants (half a block) of one row; the block scale d is staged per
 // (row, block) as f32.  q ^ 0x80 is q + 128 as a byte (0..255), converted exactly to f32;
 // the unit's sum starts at -128 * sum(x), then takes d.
@@ -1312,6 +1419,24 @@ MV_Q4K_KS_ALL(4, 3)
 MV_Q4K_KS_ALL(4, 6)
 MV_Q4K_KS_ALL(8, 1)
 MV_Q4K_KS_ALL(8, 3)
+
+// K-split Q6_K form for n_in = 12288 (matvec_q6k_ks_body): RPL rows per row-group, NG
+// row-groups per workgroup of three waves, loaded D row-groups ahead
+#define MV_Q6K_KS(A, R, G, D)                                                                \
+  extern "C" __global__ __launch_bounds__(192) void matvec_q6k_ks__##A##_##R##_##G##_##D(     \
+      const uint4 *w, const uint16_t *wd, const float *x, float *y, const uint32_t *ids,      \
+      Segments<MatvecPush4> m) {                                                              \
+    const uint32_t s = segment_of(m, blockIdx.x);                                             \
+    (void)ids;                                                                                \
+    matvec_q6k_ks_body<A, R, G, D>(w, wd, x, y, segment_push(m, s), blockIdx.x - m.start[s]); \
+  }
+#define MV_Q6K_KS_ALL(R, G, D) MV_Q6K_KS(0, R, G, D) MV_Q6K_KS(1, R, G, D)
+MV_Q6K_KS_ALL(1, 8, 1)
+MV_Q6K_KS_ALL(1, 8, 2)
+MV_Q6K_KS_ALL(1, 8, 7)
+MV_Q6K_KS_ALL(1, 16, 2)
+MV_Q6K_KS_ALL(2, 4, 2)
+MV_Q6K_KS_ALL(8, 1, 1)
 
 // Q4_K on the matrix cores for n_in = 4096 (matvec_q4k_mf_body): NG groups of 16 rows per
 // workgroup

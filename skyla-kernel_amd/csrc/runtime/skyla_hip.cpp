@@ -850,9 +850,16 @@ const VariantRule kVariantRules[] = {
 struct KsRule {
   uint64_t min_rows, max_rows;  // rows of the launch (outputs for the gate/up pair)
   uint32_t rpl, ng;
+  uint32_t pd = 1;              // Q6_K: row-groups loaded ahead
 };
 const KsRule kKsRules[] = {{0, 16383, 4, 1}};
 const KsRule kKsPairRules[] = {{0, 8191, 4, 1}};
+// K-split Q6_K form (n_in = 12288; rows per slot, row-groups, row-groups loaded ahead).
+// Config-2 down projection (4096 rows), us per launch over 36 layers on two boxes: (1, 8, 1)
+// 11.75 / 11.89 against 12.25 / 12.48 for the LDS-staged (8, 1, 64); (1, 8, 2) 12.40,
+// (1, 16, 2) 12.83, (2, 4, 2) 13.89, (8, 1, 1) 14.02, (1, 8, 7) 14.19.  SKYLA_HIP_KS6=R_G_D
+// forces one shape (sweeps); SKYLA_HIP_KS=0 turns it off with the Q4_K forms.
+const std::vector<KsRule> kKs6Rules = {{0, ~uint64_t{0}, 1, 8, 1}};
 
 void add_ks(skyla_hip_context *ctx, const char *name, const uint32_t *spec, Retile &t) {
   // SKYLA_HIP_MF=G: plain Q4_K launches with n_in = 4096 on the matrix-core form
@@ -870,6 +877,25 @@ void add_ks(skyla_hip_context *ctx, const char *name, const uint32_t *spec, Reti
   }
   const char *env = std::getenv("SKYLA_HIP_KS");
   if (env && env[0] == '0') return;
+  if (std::strcmp(name, "matvec_q6k") == 0 && spec[3] == 0) {
+    // K-split Q6_K form for launches whose rows all have n_in = 12288 (matvec_q6k_ks_body):
+    // three waves, RPL rows per row-group, NG row-groups per workgroup
+    std::vector<KsRule> rules(std::begin(kKs6Rules), std::end(kKs6Rules));
+    uint32_t fr = 0, fg = 0, fd = 0;
+    if (const char *e6 = std::getenv("SKYLA_HIP_KS6"); e6 && std::sscanf(e6, "%u_%u_%u", &fr, &fg, &fd) == 3)
+      rules = {{0, ~uint64_t{0}, fr, fg, fd}};
+    std::vector<MatvecAlt> alts;
+    for (const KsRule &r : rules) {
+      const std::string sym = "matvec_q6k_ks__" + std::to_string(spec[1]) + "_" + std::to_string(r.rpl) + "_" +
+                              std::to_string(r.ng) + "_" + std::to_string(r.pd);
+      hipFunction_t fn = find_function(ctx, sym);
+      if (!fn) return;  // all or nothing
+      alts.push_back({fn, r.rpl * r.ng, 192, r.min_rows, 12288, r.max_rows});
+    }
+    t.n_in_word = 6;  // MatvecPush4.n_in
+    t.alts.insert(t.alts.end(), alts.begin(), alts.end());
+    return;
+  }
   std::string ks;
   bool pair = false;
   if (std::strcmp(name, "matvec_q4k") == 0 && spec[3] == 0)
