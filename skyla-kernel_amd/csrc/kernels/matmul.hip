@@ -715,10 +715,14 @@ SK_DEV void lds_scales(const uint32_t *row, uint32_t hh, StageScales<TYPE> &o) {
 // coherent (sc1) stores, drains them, and counts itself in cnt[tile]; the last of the S
 // sums the partials in split order (deterministic) and writes y, then resets the count
 // for the next launch.  No workgroup ever waits for another.
-template <int TYPE, int ACCUM, int XHALF, int NW, int TN = TN2, int MOE = 0>
+// Balanced grid (HYB): grid.x = hf + 2 (tiles - hf) workgroups for a launch of more tiles
+// than one round of workgroup slots holds; workgroup b < hf runs tile b whole, the others
+// run tile hf + (b - hf) / 2 in two K halves (ws and cnt indexed from tile hf), so every CU
+// gets about the same work; hz token tiles per row tile.
+template <int TYPE, int ACCUM, int XHALF, int NW, int TN = TN2, int MOE = 0, int HYB = 0>
 SK_DEV void matmul_tile128_w(const uint4 *__restrict__ w, const uint16_t *__restrict__ wd, const void *x,
                              float *y, const uint32_t *ctl, const MatmulPush &p, float *ws = nullptr,
-                             uint32_t *cnt = nullptr, uint32_t S = 1) {
+                             uint32_t *cnt = nullptr, uint32_t S = 1, uint32_t hf = 0, uint32_t hz = 1) {
   static_assert(NW == 4 || TN == TN2, "eight waves split a 128-token tile");
   constexpr int NT = 64 * NW;
   constexpr int NB = NW == 8 ? 2 : TN / 32;  // 32-token blocks per wave
@@ -742,10 +746,24 @@ SK_DEV void matmul_tile128_w(const uint4 *__restrict__ w, const uint16_t *__rest
   // Expert groups (MOE): grid.y = expert e, whose group of (count, start) = table[e] tokens
   // is listed in list[]; tile z takes group tokens [z TN, z TN + TN), token i being slot
   // s = list[start + i] that reads x row s / x_div and writes y row s (matmul.comp:124-150).
-  const uint32_t gx = gridDim.x, gz = gridDim.z, Z = gz / S;
-  const uint32_t lin = blockIdx.x + gx * blockIdx.z;
-  const uint32_t rt = MOE ? blockIdx.x : lin / gz, rem = lin % gz;
-  const uint32_t tt = MOE ? blockIdx.z : rem % Z, sp = MOE ? 0 : rem / Z;
+  uint32_t rt, tt, sp, kt;  // row tile, token tile, split, the tile's slot in ws / cnt
+  if constexpr (HYB) {
+    const uint32_t b = blockIdx.x;
+    const uint32_t t = b < hf ? b : hf + ((b - hf) >> 1);
+    S = b < hf ? 1u : 2u;
+    sp = b < hf ? 0u : ((b - hf) & 1u);
+    rt = t / hz;
+    tt = t % hz;
+    kt = t - hf;
+  } else {
+    const uint32_t gx = gridDim.x, gz = gridDim.z, Z = gz / S;
+    const uint32_t lin = blockIdx.x + gx * blockIdx.z;
+    const uint32_t rem = lin % gz;
+    rt = MOE ? blockIdx.x : lin / gz;
+    tt = MOE ? blockIdx.z : rem % Z;
+    sp = MOE ? 0 : rem / Z;
+    kt = rt * Z + tt;
+  }
   const uint32_t e = MOE ? blockIdx.y : 0;
   const uint32_t base = MOE ? e * p.n_out : 0;
   const uint32_t row0 = rt * TM;
@@ -855,7 +873,7 @@ SK_DEV void matmul_tile128_w(const uint4 *__restrict__ w, const uint16_t *__rest
   }
 
   if (S > 1) {
-    const uint32_t tile = rt * Z + tt;
+    const uint32_t tile = kt;
     constexpr uint32_t PART = NW * NB * 16 * 64;  // floats of one partial tile
     float *mine = ws + (size_t)(tile * S + sp) * PART + wave * (NB * 16 * 64);
 #pragma unroll
@@ -1134,6 +1152,20 @@ MMH4(1, 0)
 MMH4(1, 1)
 MMH4(2, 0)
 MMH4(2, 1)
+
+// The four-wave tile on f16 rows over a balanced grid (HYB): hf whole tiles, the rest in
+// two K halves; hz token tiles per row tile.
+#define MMH4B(T, A)                                                                               \
+  extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void       \
+      matmul_x4b__##T##_##A(                                                                      \
+      const uint4 *w, const uint16_t *wd, const f16 *x, float *y, const uint32_t *ctl,            \
+      MatmulPush p, float *ws, uint32_t *cnt, uint32_t S, uint32_t hf, uint32_t hz) {             \
+    matmul_tile128_w<T, A, 2, 4, TN2, 0, 1>(w, wd, x, y, ctl, p, ws, cnt, S, hf, hz);             \
+  }
+MMH4B(1, 0)
+MMH4B(1, 1)
+MMH4B(2, 0)
+MMH4B(2, 1)
 
 // f32 activation rows to f16 rows for the dense K-quant tiles, once per launch instead of
 // in every tile (the runtime inserts it before dense K-quant matmuls with f32 inputs; one

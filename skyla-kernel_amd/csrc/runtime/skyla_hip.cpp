@@ -188,6 +188,7 @@ struct skyla_hip_pipeline {
   hipFunction_t split_fn = nullptr;      // dense K-quant matmul: the K-split variant
   hipFunction_t hx_fn = nullptr;         // and its variant on x_half_rows's f16 rows
   hipFunction_t hx4_fn = nullptr;        // the four-wave tile on those rows
+  hipFunction_t hx4b_fn = nullptr;       // and over a balanced grid (some tiles in K halves)
   uint32_t split_threads = 0;
   hipFunction_t tok_fn = nullptr;        // batched form: a tok_per_wg x tok_per_wg block of
   uint32_t tok_per_wg = 0;               // grid.x and grid.y per workgroup
@@ -211,7 +212,7 @@ struct Command {
   std::shared_ptr<const Retile> retile;
   hipFunction_t split_fn = nullptr;
   uint32_t split_threads = 0;
-  hipFunction_t hx_fn = nullptr, hx4_fn = nullptr;
+  hipFunction_t hx_fn = nullptr, hx4_fn = nullptr, hx4b_fn = nullptr;
   hipFunction_t tok_fn = nullptr;
   uint32_t tok_per_wg = 0;
   std::string name;                 // the pipeline's shader name
@@ -583,6 +584,7 @@ std::vector<Launch> build_launches(skyla_hip_context *ctx, const std::vector<Com
   const char *xenv = std::getenv("SKYLA_HIP_XHALF");
   const bool xhalf = ctx && ctx->x_half_rows && !(xenv && xenv[0] == '0');
   const bool x4 = !(xenv && xenv[0] == '8');  // SKYLA_HIP_XHALF=8: the eight-wave tile throughout
+  const bool balance = !(xenv && xenv[0] == '4');
   std::vector<Launch> out;
   std::vector<uint32_t> xkey;  // the rows the last prepass converted, until a barrier
   for (size_t i = 0; i < cmds.size();) {
@@ -621,6 +623,22 @@ std::vector<Launch> build_launches(skyla_hip_context *ctx, const std::vector<Com
       if (!l.split && x4 && a.hx4_fn) {
         l.fn = a.hx4_fn;
         l.threads = 256;
+        // More tiles than CUs but fewer than the two-per-CU slots: some CUs would run two
+        // tiles and the rest one.  Balanced grid instead: hf tiles whole and the rest in two
+        // K halves, hf + 2 (tiles - hf) = one workgroup per slot (M = 512 gate: 384 tiles,
+        // 256 whole + 128 halved).  SKYLA_HIP_XHALF=4 keeps the plain grid.
+        const uint64_t tiles = (uint64_t)a.groups[0] * a.groups[2];
+        const uint64_t slots = 2ull * (ctx->n_cu ? ctx->n_cu : 256);
+        if (balance && a.hx4b_fn && tiles > slots / 2 && tiles < slots && a.push[6] >= 2 * 256) {
+          const uint32_t hf = (uint32_t)(2 * tiles - slots);
+          l.fn = a.hx4b_fn;
+          l.groups[0] = (uint32_t)slots;
+          l.groups[1] = l.groups[2] = 1;
+          l.split = 2;
+          l.extra = {hf, a.groups[2]};
+          l.n_cnt = (uint32_t)(tiles - hf);
+          l.ws_bytes = (uint64_t)l.n_cnt * 2 * kSplitTileBytes;
+        }
       }
       if (!l.split) l.split = 1;  // the K-split arguments, unsplit
       l.args[4] = (uint32_t)(h_off / 2);  // f16 units
@@ -1245,6 +1263,7 @@ int skyla_hip_pipeline_new(skyla_hip_context *ctx, const char *name, uint32_t n_
     if (!(n_spec == 4 && spec[3])) {
       p->hx_fn = find_function(ctx, "matmul_x8__" + std::to_string(spec[0]) + "_" + std::to_string(spec[1]));
       p->hx4_fn = find_function(ctx, "matmul_x4__" + std::to_string(spec[0]) + "_" + std::to_string(spec[1]));
+      p->hx4b_fn = find_function(ctx, "matmul_x4b__" + std::to_string(spec[0]) + "_" + std::to_string(spec[1]));
       p->split_threads = 512;
     }
   }
@@ -1329,6 +1348,7 @@ int skyla_hip_record_dispatch(skyla_hip_recorder *r, const skyla_hip_pipeline *p
   c.split_fn = p->split_fn;
   c.hx_fn = p->hx_fn;
   c.hx4_fn = p->hx4_fn;
+  c.hx4b_fn = p->hx4b_fn;
   c.split_threads = p->split_threads;
   c.tok_fn = p->tok_fn;
   c.tok_per_wg = p->tok_per_wg;
@@ -1571,6 +1591,7 @@ int skyla_hip_time_dispatch(skyla_hip_context *ctx, const skyla_hip_pipeline *p,
   c.split_fn = p->split_fn;
   c.hx_fn = p->hx_fn;
   c.hx4_fn = p->hx4_fn;
+  c.hx4b_fn = p->hx4b_fn;
   c.split_threads = p->split_threads;
   c.tok_fn = p->tok_fn;
   c.tok_per_wg = p->tok_per_wg;
@@ -1626,6 +1647,7 @@ int skyla_hip_dispatch_noalloc(skyla_hip_context *ctx, const skyla_hip_pipeline 
   c.split_fn = p->split_fn;
   c.hx_fn = p->hx_fn;
   c.hx4_fn = p->hx4_fn;
+  c.hx4b_fn = p->hx4b_fn;
   c.split_threads = p->split_threads;
   c.tok_fn = p->tok_fn;
   c.tok_per_wg = p->tok_per_wg;

@@ -95,10 +95,11 @@ def test_matmul_config3(ctx, name, dtype, n_in, n_out):
 ])
 def test_matmul_f16_prepass_same_bits(ctx, name, dtype, n_in, n_out, n_tok, accum):
     """The runtime's f16 row prepass (x_half_rows, then the tile on f16 rows: four waves
-    unless the launch is K-split) against the eight-wave tile's own f32 staging
-    (SKYLA_HIP_XHALF=0): the same bits while no activation reaches 2^15, K split or not,
-    ACCUM or not, ragged token counts."""
-    got1, want = _run(ctx, dtype, n_in, n_out, n_tok, accum=accum, tag="mm-xh")
+    unless the launch is K-split; SKYLA_HIP_XHALF=4 keeps the four-wave tile's plain grid)
+    against the eight-wave tile's own f32 staging (SKYLA_HIP_XHALF=0): the same bits while
+    no activation reaches 2^15, K split or not, ACCUM or not, ragged token counts."""
+    with env(SKYLA_HIP_XHALF=4):
+        got1, want = _run(ctx, dtype, n_in, n_out, n_tok, accum=accum, tag="mm-xh")
     with env(SKYLA_HIP_XHALF=0):
         got0, _ = _run(ctx, dtype, n_in, n_out, n_tok, accum=accum, tag="mm-xh")
     assert np.array_equal(got1.view(np.uint32), got0.view(np.uint32))
@@ -138,3 +139,29 @@ def test_matmul_f16_prepass_shared(ctx):
     for i, (dt, _, n, d) in enumerate(mats):
         want = so.matmul(int(dt), d, n_in, n, x)
         assert rel_l2(got["1"][1][i * n_tok:(i + 1) * n_tok, :n], want) <= GUARD
+
+
+CUS = 256  # MI355X: two four-wave workgroups per CU, 512 slots
+
+
+@pytest.mark.parametrize("name,dtype,n_in,n_out,n_tok,accum", [
+    ("gate", E.DType.Q4K, 4096, 12288, 512, False), ("ragged6", E.DType.Q6K, 768, 9000, 500, True),
+])
+def test_matmul_balanced_grid(ctx, name, dtype, n_in, n_out, n_tok, accum):
+    """A launch of more tiles than CUs and fewer than the two-per-CU slots runs the four-wave
+    tile over a balanced grid: hf = 2 tiles - 512 tiles whole (the same bits as the plain
+    grid, SKYLA_HIP_XHALF=4) and the rest in two K halves added in order (within f32
+    reordering of the plain grid), against the oracle at the bar; ACCUM, ragged rows and
+    tokens."""
+    got, want = _run(ctx, dtype, n_in, n_out, n_tok, accum=accum, tag="mm-bal")
+    with env(SKYLA_HIP_XHALF=4):
+        plain, _ = _run(ctx, dtype, n_in, n_out, n_tok, accum=accum, tag="mm-bal")
+    hz = -(-n_tok // E.MATMUL_TILE_COLS)
+    tiles = -(-n_out // 128) * hz
+    assert CUS < tiles < 2 * CUS
+    hf = 2 * tiles - 2 * CUS
+    whole_rows = (hf // hz) * 128      # row tiles whose every token tile ran whole
+    assert 0 < whole_rows < n_out
+    assert np.array_equal(got[:, :whole_rows].view(np.uint32), plain[:, :whole_rows].view(np.uint32))
+    assert rel_l2(got[:, whole_rows:], plain[:, whole_rows:]) <= 1e-6
+    assert rel_l2(got, want) <= GUARD
