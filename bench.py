@@ -43,7 +43,7 @@ from skyla_hip.abi import Context  # noqa: E402
 # Recordings replay as one HIP graph; with --eager they replay as direct launches of the
 # same launch list (the runtime's profiled-recording path), for tools that trace launches.
 EAGER = False
-FUSE = "qkv"  # the decode graph's fusion level in the end-to-end runs (Engine fuse)
+FUSE = "auto"  # the decode graph's fusion level in the end-to-end runs (Engine fuse)
 
 HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, vendor peak
 MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense FP16 MFMA, vendor peak
@@ -356,7 +356,8 @@ def decode_config1(ctx: Context, steps: int = 64, warmup: int = 3) -> dict:
     c = synth.qwen3_config("qwen3-0.6b")
     t = synth.qwen3("qwen3-0.6b-q8_0", c, "q8_0", "ones", shared_layers=True)
     prompt = synth.prompt("qwen3-0.6b-q8_0", 16, c.n_vocab)
-    eng = E.Engine(ctx, t, c, len(prompt) + warmup + steps + 8, E.KvPrecision.F16_KEYS_Q8_VALUES, profile=EAGER)
+    eng = E.Engine(ctx, t, c, len(prompt) + warmup + steps + 8, E.KvPrecision.F16_KEYS_Q8_VALUES, profile=EAGER,
+                   fuse=FUSE)
     try:
         mats = [v for v in t.values() if isinstance(v, tuple)]
         weight_bytes = sum(m[2] * E.row_bytes(m[0], m[1]) for m in mats)  # the head is token_embd
@@ -440,7 +441,7 @@ def main() -> int:
                     help="only the config-3 prefill GEMMs (for hardware-counter runs)")
     ap.add_argument("--calibrate", action="store_true",
                     help="run only the two known-size kernels that scale rocprofv3 FETCH_SIZE/WRITE_SIZE")
-    ap.add_argument("--fuse", choices=["none", "qkv", "ffn", "all"], default="qkv",
+    ap.add_argument("--fuse", choices=["none", "qkv", "ffn", "all", "auto"], default="auto",
                     help="the decode graph's fusion level in the end-to-end runs")
     args = ap.parse_args()
     global EAGER, FUSE

@@ -30,7 +30,7 @@ EXPERT_LPR = (64, 32, 16)
 
 # arena.rs:6-7
 ATTENTION_CHUNK = 64
-FUSE_LEVELS = ("none", "qkv", "ffn", "all")  # the decode graph's fusion levels (Engine fuse)
+FUSE_LEVELS = ("none", "qkv", "ffn", "all", "auto")  # the decode graph's fusion levels (Engine fuse)
 MAX_SPLITS = 4096       # splits the attention merge weighs in LDS (kernels/attention.hip)
 BATCH = 128
 # What the MoE kernels hold (moe.hip): moe_route keeps 4 logits per lane of one wave and
@@ -519,12 +519,14 @@ class Graph:
         self.b = BATCH if batched else 1
         # decode with the fused matvecs (Kernels.fuse): "qkv" folds the attention norm into
         # q/k/v; "ffn" also the FFN norm into the Q4_K gate/up pair; "all" the FFN norm into
-        # gate/up, the SiLU into down and the output norm into the head
+        # gate/up, the SiLU into down and the output norm into the head; "auto" per layer:
+        # "ffn" where gate and up run as the Q4_K pair, the FFN forms of "all" elsewhere
         fuse = getattr(k, "fuse", "none")
         on = not batched and fuse != "none" and a is not None and a.norms is not None
         self.fused = on
-        self.fused_ffn = on and fuse == "ffn"
+        self.fused_ffn = on and fuse in ("ffn", "auto")
         self.fused_all = on and fuse == "all"
+        self.fused_auto = on and fuse == "auto"
 
     def stage(self, label: str) -> None:
         self.r.barrier()
@@ -615,6 +617,11 @@ class Graph:
         return (self.fused and not self.fused_all and self.k.glu is not None and gate.dtype == up.dtype == DType.Q4K
                 and gate.buf == up.buf and (gate.n_in, gate.n_out) == (up.n_in, up.n_out))
 
+    def ffn_all_forms(self, gate: QMatrix, up: QMatrix) -> bool:
+        """The FFN norm folded into gate and up, the SiLU into down (fuse "all"; "auto" where
+        gate and up are no Q4_K pair)."""
+        return self.fused_all or (self.fused_auto and not self.glu_pair(gate, up))
+
     def dense_ffn(self, gate: QMatrix, up: QMatrix, down: QMatrix, l: int = 0) -> None:
         """graph.rs:174-184 (after the ffn rmsnorm): gate, up -> silu -> down (+= x)."""
         a, c, b, bt = self.a, self.c, self.b, self.batched
@@ -633,7 +640,7 @@ class Graph:
             self.matvec(down, (a.gate, a.s_ff), (a.x, a.s_embd), True, False)
             self.stage("matvec down")
             return
-        if self.fused_all:  # the FFN norm folded into gate and up, the SiLU into down (decode)
+        if self.ffn_all_forms(gate, up):  # the FFN norm folded into gate and up, the SiLU into down
             f = dict(form="norm", aux=a.norm(l, True))
             self.matvec(gate, (a.x, a.s_embd), (a.gate, a.s_ff), False, False, **f)
             self.matvec(up, (a.x, a.s_embd), (a.up, a.s_ff), False, False, **f)
@@ -737,7 +744,7 @@ class Graph:
             self.stage("rmsnorm")
         self.attention(l, lw.attn, rope)
         moe = lw.router is not None
-        norm_folded = self.fused_all or (self.fused_ffn and self.glu_pair(lw.gate, lw.up))
+        norm_folded = self.ffn_all_forms(lw.gate, lw.up) or (self.fused_ffn and self.glu_pair(lw.gate, lw.up))
         if not norm_folded or moe:
             self.rmsnorm(a.x, lw.ffn_norm, a.n, b)
             self.stage("rmsnorm")
@@ -850,17 +857,15 @@ class Engine:
 
     def __init__(self, ctx: Context, model: dict, c: Config, max_ctx: int,
                  precision: KvPrecision = KvPrecision.F16_KEYS_Q8_VALUES, profile: bool = False,
-                 fuse: str = "qkv"):
+                 fuse: str = "auto"):
         """fuse (decode step only; prefill keeps the separate launches): "qkv" folds the
         attention RMSNorm into the q/k/v matvecs; "ffn" also the FFN norm into the Q4_K
         gate/up pair; "all" folds the FFN norm into gate/up, the SiLU gate into the down
-        projection and the output norm into the head; "none" keeps graph.rs's launches.
-        Measured on MI355X (config 5, 1k context) "qkv" saves a launch per layer for 1.3 us
-        more in the q/k/v launch; "ffn" saves one more launch per layer, but its pair launch
-        (94 VGPRs against 75: two workgroups per CU instead of three) is slower by as much
-        (477.8 against 477.6 tok/s); "all" is slower than "none": each of the down (+8 to
-        14 us) and head (+44 us) matvec workgroups repeats the elementwise work and its
-        loads, and the fused forms hold more registers."""
+        projection and the output norm into the head; "auto" (the default) is "ffn" for
+        layers whose gate and up run as the Q4_K pair and the FFN forms of "all" for the
+        others, the head unfused; "none" keeps graph.rs's launches.  Measured on MI355X
+        (tok/s, qkv / ffn / all): config 5 (Qwen3-8B Q4_K_M) at 1k context 495 / 513 / 474,
+        at 16k 382 / 394 / 371; config 1 (Qwen3-0.6B Q8_0, no pair form) 890 / 886 / 970."""
         self.ctx, self.c = ctx, c
         self.weights = load_weights(ctx, model, c)
         self.arena = Arena(ctx, c, max_ctx, precision)

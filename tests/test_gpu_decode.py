@@ -247,7 +247,7 @@ class Top1:
 
 
 
-@pytest.mark.parametrize("fuse", ["none", "qkv", "ffn", "all"])
+@pytest.mark.parametrize("fuse", ["none", "qkv", "ffn", "all", "auto"])
 @pytest.mark.parametrize("quant", ["q8_0", "q4_k_m", "q4_k_m_mixed"])
 @pytest.mark.parametrize("precision", [P.F16, P.F16_KEYS_Q8_VALUES])
 def test_decode_top1_against_oracle(ctx, quant, precision, fuse):
