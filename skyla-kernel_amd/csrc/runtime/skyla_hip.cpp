@@ -619,7 +619,9 @@ std::vector<Launch> build_launches(skyla_hip_context *ctx, const std::vector<Com
       // Launches of more than 128 tiles (no K split) run the four-wave tile, two workgroups
       // per CU: each dequantised fragment feeds four MFMAs (M = 512 gate: 124 -> 108 us).
       // K-split launches keep the eight-wave tile (the four-wave one split four ways
-      // measured 1.2-1.7x slower).  Both give the same bits.
+      // measured 1.2-1.7x slower, and in a later build made an illegal memory access at the
+      // config-3 shapes whose cause was not found: it is never launched split more than
+      // the balanced grid's two K halves).  Both give the same bits.
       if (!l.split && x4 && a.hx4_fn) {
         l.fn = a.hx4_fn;
         l.threads = 256;
