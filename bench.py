@@ -441,6 +441,8 @@ def main() -> int:
                     help="only the config-3 prefill GEMMs (for hardware-counter runs)")
     ap.add_argument("--calibrate", action="store_true",
                     help="run only the two known-size kernels that scale rocprofv3 FETCH_SIZE/WRITE_SIZE")
+    ap.add_argument("--no-config1", action="store_true",
+                    help="with --e2e-only: skip the config-1 decode (kernel traces of config 5 alone)")
     ap.add_argument("--fuse", choices=["none", "qkv", "ffn", "all", "auto"], default="auto",
                     help="the decode graph's fusion level in the end-to-end runs")
     args = ap.parse_args()
@@ -467,7 +469,8 @@ def main() -> int:
         return 0
     if args.e2e_only:
         e2e = decode_config5(ctx, tuple(int(v) for v in args.e2e_only.split(",")))
-        print(json.dumps({"decode_e2e_config5": e2e, "decode_e2e_config1": decode_config1(ctx)}))
+        print(json.dumps({"decode_e2e_config5": e2e,
+                          "decode_e2e_config1": None if args.no_config1 else decode_config1(ctx)}))
         ctx.free()
         return 0
     log(f"device {ctx.device_name()}; building {args.layers}-layer decode workload")
