@@ -32,6 +32,10 @@ EXPERT_LPR = (64, 32, 16)
 ATTENTION_CHUNK = 64
 FUSE_LEVELS = ("none", "qkv", "ffn", "all", "auto")  # the decode graph's fusion levels (Engine fuse)
 MAX_SPLITS = 4096       # splits the attention merge weighs in LDS (kernels/attention.hip)
+# Split counts the engine records its decode and prefill graphs for: a replay uses the
+# smallest that covers the positions in play (each recording's attention grid and merge
+# then span only those splits; the arena's own count is the last bucket).
+SPLIT_BUCKETS = (16, 64, 256)
 BATCH = 128
 # What the MoE kernels hold (moe.hip): moe_route keeps 4 logits per lane of one wave and
 # picks at most 16; moe_sort ranks at most 1024 slots (moe_sort.comp:15).
@@ -514,8 +518,11 @@ class Arena:
 class Graph:
     """The dispatches of graph.rs and graph/moe.rs that belong to the weight path."""
 
-    def __init__(self, r: Recorder, k: Kernels, a: Arena, c: Config, batched: bool):
+    def __init__(self, r: Recorder, k: Kernels, a: Arena, c: Config, batched: bool, n_split: int | None = None):
         self.r, self.k, self.a, self.c, self.batched = r, k, a, c, batched
+        # attention splits of this recording (the grids of attention / attention_prep and the
+        # merge's span): the arena's, or fewer for a recording that serves early positions
+        self.n_split = n_split if n_split is not None else getattr(a, "n_split", 0)
         self.b = BATCH if batched else 1
         # decode with the fused matvecs (Kernels.fuse): "qkv" folds the attention norm into
         # q/k/v; "ffn" also the FFN norm into the Q4_K gate/up pair; "all" the FFN norm into
@@ -716,11 +723,11 @@ class Graph:
         a, c, kv = self.a, self.c, self.a.kv_layout
         scale = np.float32(1.0) / np.sqrt(np.float32(c.head_dim))
         push = [a.q, a.k, a.v, q_norm, k_norm, kv.keys(l), kv.values(l), c.n_head_kv, f32_bits(c.eps), rope,
-                f32_bits(c.rope_mscale), kv.key_scales(l), kv.value_scales(l), a.part, a.n_split, f32_bits(scale),
+                f32_bits(c.rope_mscale), kv.key_scales(l), kv.value_scales(l), a.part, self.n_split, f32_bits(scale),
                 a.s_part]
-        self.r.dispatch(self.k.attn_prep, [c.n_head_kv, a.n_split, 1], push)
+        self.r.dispatch(self.k.attn_prep, [c.n_head_kv, self.n_split, 1], push)
         self.stage("attention (+ qk norm, rope, kv write)")
-        push = [a.part, a.attn, a.n_split, ATTENTION_CHUNK, a.s_part, a.s_attn]
+        push = [a.part, a.attn, self.n_split, ATTENTION_CHUNK, a.s_part, a.s_attn]
         self.r.dispatch(self.k.merge, [c.n_head, 1, 1], push)
         self.stage("attention merge")
 
@@ -728,11 +735,11 @@ class Graph:
         """graph.rs:89-109: split-K attention over layer l's cache, then the merge into attn."""
         a, c, kv = self.a, self.c, self.a.kv_layout
         scale = np.float32(1.0) / np.sqrt(np.float32(c.head_dim))
-        push = [a.q, a.part, kv.keys(l), kv.values(l), c.n_head_kv, a.n_split, f32_bits(scale), a.s_q,
+        push = [a.q, a.part, kv.keys(l), kv.values(l), c.n_head_kv, self.n_split, f32_bits(scale), a.s_q,
                 a.s_part, kv.key_scales(l), kv.value_scales(l)]
-        self.r.dispatch(self.k.attention, [c.n_head_kv, a.n_split, self.b], push)
+        self.r.dispatch(self.k.attention, [c.n_head_kv, self.n_split, self.b], push)
         self.stage("attention")
-        push = [a.part, a.attn, a.n_split, ATTENTION_CHUNK, a.s_part, a.s_attn]
+        push = [a.part, a.attn, self.n_split, ATTENTION_CHUNK, a.s_part, a.s_attn]
         self.r.dispatch(self.k.merge, [c.n_head, self.b, 1], push)
         self.stage("attention merge")
 
@@ -825,11 +832,13 @@ def load_weights(ctx: Context, model: dict, c: Config) -> Weights:
 
 
 # ---- graph.rs::record, engine.rs ---------------------------------------------------------
-def record(ctx: Context, k: Kernels, w: Weights, a: Arena, c: Config, batched: bool, profile: bool = False):
+def record(ctx: Context, k: Kernels, w: Weights, a: Arena, c: Config, batched: bool, profile: bool = False,
+           n_split: int | None = None):
     """graph.rs:199-233: the decode step (one token) or a prefill chunk (BATCH rows, ctl[2]
-    of them live), ending in the output head over the last row."""
+    of them live), ending in the output head over the last row; `n_split` attention splits
+    (default: the arena's), enough for positions below n_split * ATTENTION_CHUNK."""
     def body(r: Recorder) -> None:
-        g = Graph(r, k, a, c, batched)
+        g = Graph(r, k, a, c, batched, n_split)
         g.embed(w.embd)
         for l, lw in enumerate(w.layers):
             g.layer(l, lw, w.rope)
@@ -880,9 +889,37 @@ class Engine:
             a.buffer.upload(a.norms * 4, a.s_norm * (2 * c.n_layer + 1) * 4)
         self.kernels = Kernels(ctx, self.weights.buffers, self.arena.buffer, kv=self.arena.kv, c=c,
                                precision=precision, embd_dtype=self.weights.embd.dtype, fuse=fuse)
-        self.decode = record(ctx, self.kernels, self.weights, self.arena, c, False, profile)
-        self.prefill_rec = record(ctx, self.kernels, self.weights, self.arena, c, True, profile)
+        self.profile = profile
+        self.recordings = {}  # (batched, attention splits) -> recording, made on first use
         self.pos = 0
+        self.recording(False, 1)
+        self.recording(True, BATCH)
+
+    def recording(self, batched: bool, n_pos: int):
+        """The decode (batched False) or prefill recording for a replay whose positions stay
+        below n_pos: the smallest split bucket that covers them.  graph.rs records one graph
+        over the arena's splits; the splits past a token's position do no work there, but
+        their workgroups still launch (an arena sized for 16k positions launches 2056 decode
+        attention workgroups per layer, 136 of them with work at 1k), so the engine keeps a
+        recording per bucket.  The merge adds the same splits in the same order either way,
+        so the logits are the same bits."""
+        need = -(-n_pos // ATTENTION_CHUNK)
+        n_split = next((b for b in SPLIT_BUCKETS if need <= b < self.arena.n_split), self.arena.n_split)
+        key = (batched, n_split)
+        if key not in self.recordings:
+            self.recordings[key] = record(self.ctx, self.kernels, self.weights, self.arena, self.c, batched,
+                                          self.profile, n_split)
+        return self.recordings[key]
+
+    @property
+    def decode(self):
+        """The decode step's recording for the current position."""
+        return self.recording(False, self.pos + 1)
+
+    @property
+    def prefill_rec(self):
+        """The prefill chunk's recording for the current position."""
+        return self.recording(True, self.pos + BATCH)
 
     def reset(self) -> None:
         self.pos = 0
@@ -926,8 +963,9 @@ class Engine:
         return self.logits()
 
     def free(self) -> None:
-        for rec in (self.decode, self.prefill_rec):
+        for rec in self.recordings.values():
             rec.free()
+        self.recordings = {}
         for b in self.weights.buffers:
             b.free()
         if self.arena.kv is not None:

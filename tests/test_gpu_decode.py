@@ -500,3 +500,45 @@ def test_moe_model_from_gguf_against_oracle(ctx, tmp_path, precision):
         assert err < 2e-2, err
     finally:
         eng.free()
+
+
+def test_split_buckets_same_logits(ctx):
+    """Recordings over fewer attention splits (Engine.recording picks the smallest bucket
+    that covers the positions in play) give the logits of the arena-wide recording bit for
+    bit, prefill and decode: the splits past a token's position do no work in either."""
+    c = synth.qwen3_config("tiny")
+    tensors = synth.qwen3(f"{CFG}-q4_k_m", c, "q4_k_m", "random")
+    eng = E.Engine(ctx, tensors, c, 40 * E.ATTENTION_CHUNK, P.F16_KEYS_Q8_VALUES)
+    full_p = full_d = None
+    try:
+        a = eng.arena
+        assert a.n_split == 40 and E.SPLIT_BUCKETS[0] < a.n_split
+        full_p = E.record(ctx, eng.kernels, eng.weights, a, c, True, False, a.n_split)
+        full_d = E.record(ctx, eng.kernels, eng.weights, a, c, False, False, a.n_split)
+        prompt = synth.prompt(f"{CFG}-buckets", 150, c.n_vocab)
+        got = eng.prefill(prompt)                      # chunks at positions 0 and 128: 16 splits
+        assert eng.recording(True, 128 + E.BATCH) is not full_p
+        eng.reset()
+        for i in range(0, len(prompt), E.BATCH):
+            chunk = prompt[i: i + E.BATCH]
+            eng.load(chunk)
+            ctx.replay(full_p)
+            eng.pos += len(chunk)
+        want = eng.logits()
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+        tok = int(np.argmax(want))
+        for _ in range(3):                             # decode from position 150
+            pos = eng.pos
+            got = eng.step(tok)
+            eng.pos = pos
+            eng.load([tok], batched=False)
+            ctx.replay(full_d)
+            eng.pos += 1
+            want = eng.logits()
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+            tok = int(np.argmax(want))
+    finally:
+        for rec in (full_p, full_d):
+            if rec is not None:
+                rec.free()
+        eng.free()
