@@ -1,4 +1,4 @@
-// moe_route's selection (moe_route.comp:55-106), shared by moe.hip (moe_route, the fused
+// moe_route's selection (moe_route.comp:23-75), shared by moe.hip (moe_route, the fused
 // logits + route form) and matvec.hip (the experts' gate/up form that routes for itself).
 #pragma once
 
@@ -7,7 +7,7 @@
 struct RoutePush { uint32_t logits_off, ids_off, weights_off, n_expert, n_used; };
 
 // Monotone u32 key of a float with -0 folded onto +0 (so equal values tie exactly as the
-// float comparisons of moe_route.comp:66-81 do).
+// float comparisons of moe_route.comp:36-52 do).
 SK_DEV uint32_t order_key(float v) {
   const uint32_t b = __builtin_bit_cast(uint32_t, v + 0.0f);
   return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
@@ -23,7 +23,7 @@ SK_DEV uint32_t dpp_u(uint32_t v) {
   return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xf, 0xf, false);
 }
 
-// moe_route (moe_route.comp:55-106): per token, n_used rounds of "largest logit, lowest
+// moe_route (moe_route.comp:23-75): per token, n_used rounds of "largest logit, lowest
 // index on ties", then weights exp(v_k - v_0) / sum.  One wave per token: expert
 // e = lane + 64 j is held in key[j] (n_expert <= 256), a round is a lane maximum, a wave
 // maximum (DPP within rows of 16, then two shuffles) and a ballot for the lowest expert

@@ -166,7 +166,7 @@ class Pipeline:
 
 
 class Recorder:
-    """skyla-vk Recorder (record.rs:293-331)."""
+    """skyla-vk Recorder (record.rs:17-58)."""
 
     def __init__(self, handle: int):
         self._h = handle
@@ -205,7 +205,7 @@ class Recording:
 
 
 class Context:
-    """skyla-vk Context (context.rs:85, buffer.rs:59-73, pipeline.rs:138-220, record.rs:351-148)."""
+    """skyla-vk Context (context.rs:85, buffer.rs:59-73, pipeline.rs:6-135, record.rs:82-149)."""
 
     def __init__(self, device: int = -1):
         load_library()
