@@ -719,10 +719,17 @@ SK_DEV void lds_scales(const uint32_t *row, uint32_t hh, StageScales<TYPE> &o) {
 // than one round of workgroup slots holds; workgroup b < hf runs tile b whole, the others
 // run tile hf + (b - hf) / 2 in two K halves (ws and cnt indexed from tile hf), so every CU
 // gets about the same work; hz token tiles per row tile.
-template <int TYPE, int ACCUM, int XHALF, int NW, int TN = TN2, int MOE = 0, int HYB = 0>
+// Segments (SEG): up to four matrices on the same rows in one launch (the runtime fuses
+// matmuls with no barrier between them that read the same activations); the row tiles of
+// segment s follow those of segment s - 1, and each takes its own push words (regions,
+// y_off, n_out, y_stride); x_off, n_in and x_stride are the same for all.
+struct NoSegments {};
+template <int TYPE, int ACCUM, int XHALF, int NW, int TN = TN2, int MOE = 0, int HYB = 0, int SEG = 0,
+          typename SG = NoSegments>
 SK_DEV void matmul_tile128_w(const uint4 *__restrict__ w, const uint16_t *__restrict__ wd, const void *x,
-                             float *y, const uint32_t *ctl, const MatmulPush &p, float *ws = nullptr,
-                             uint32_t *cnt = nullptr, uint32_t S = 1, uint32_t hf = 0, uint32_t hz = 1) {
+                             float *y, const uint32_t *ctl, const MatmulPush &p0, float *ws = nullptr,
+                             uint32_t *cnt = nullptr, uint32_t S = 1, uint32_t hf = 0, uint32_t hz = 1,
+                             const SG &segs = SG{}) {
   static_assert(NW == 4 || TN == TN2, "eight waves split a 128-token tile");
   constexpr int NT = 64 * NW;
   constexpr int NB = NW == 8 ? 2 : TN / 32;  // 32-token blocks per wave
@@ -763,6 +770,24 @@ SK_DEV void matmul_tile128_w(const uint4 *__restrict__ w, const uint16_t *__rest
     tt = MOE ? blockIdx.z : rem % Z;
     sp = MOE ? 0 : rem / Z;
     kt = rt * Z + tt;
+  }
+  MatmulPush p = p0;
+  if constexpr (SEG) {  // kt stays the launch-wide tile index (ws and cnt span every segment)
+    // field by field, with the (wave-uniform) segment in an SGPR: selecting whole push
+    // structs made the compiler copy the table to scratch and index it
+    const uint32_t sg = __builtin_amdgcn_readfirstlane(segment_of(segs, rt));
+    auto pick = [&](uint32_t MatmulPush::*f) -> uint32_t {
+      const uint32_t a = segs.p[0].*f, b = segs.p[1].*f, c = segs.p[2].*f, d = segs.p[3].*f;
+      return sg == 0 ? a : sg == 1 ? b : sg == 2 ? c : d;
+    };
+    p.o0 = pick(&MatmulPush::o0);
+    p.o1 = pick(&MatmulPush::o1);
+    p.o2 = pick(&MatmulPush::o2);
+    p.o3 = pick(&MatmulPush::o3);
+    p.y_off = pick(&MatmulPush::y_off);
+    p.n_out = pick(&MatmulPush::n_out);
+    p.y_stride = pick(&MatmulPush::y_stride);
+    rt -= sg == 0 ? 0u : sg == 1 ? segs.start[1] : sg == 2 ? segs.start[2] : segs.start[3];
   }
   const uint32_t e = MOE ? blockIdx.y : 0;
   const uint32_t base = MOE ? e * p.n_out : 0;
@@ -1181,6 +1206,19 @@ MMH4B(1, 0)
 MMH4B(1, 1)
 MMH4B(2, 0)
 MMH4B(2, 1)
+
+// The eight-wave tile on f16 rows over up to four matrices that read the same rows
+// (segment table as the matvecs take it; start[] counts row tiles).
+#define MMHS(T, A)                                                                                \
+  extern "C" __global__ __launch_bounds__(512) void matmul_x8s__##T##_##A(                         \
+      const uint4 *w, const uint16_t *wd, const f16 *x, float *y, const uint32_t *ctl,            \
+      Segments<MatmulPush> m, float *ws, uint32_t *cnt, uint32_t S) {                              \
+    matmul_tile128_w<T, A, 2, 8, TN2, 0, 0, 1>(w, wd, x, y, ctl, m.p[0], ws, cnt, S, 0, 1, m);     \
+  }
+MMHS(1, 0)
+MMHS(1, 1)
+MMHS(2, 0)
+MMHS(2, 1)
 
 // f32 activation rows to f16 rows for the dense K-quant tiles, once per launch instead of
 // in every tile (the runtime inserts it before dense K-quant matmuls with f32 inputs; one

@@ -189,6 +189,7 @@ struct skyla_hip_pipeline {
   hipFunction_t hx_fn = nullptr;         // and its variant on x_half_rows's f16 rows
   hipFunction_t hx4_fn = nullptr;        // the four-wave tile on those rows
   hipFunction_t hx4b_fn = nullptr;       // and over a balanced grid (some tiles in K halves)
+  hipFunction_t hxs_fn = nullptr;        // the eight-wave tile over several matrices (segments)
   uint32_t split_threads = 0;
   hipFunction_t tok_fn = nullptr;        // batched form: a tok_per_wg x tok_per_wg block of
   uint32_t tok_per_wg = 0;               // grid.x and grid.y per workgroup
@@ -212,7 +213,7 @@ struct Command {
   std::shared_ptr<const Retile> retile;
   hipFunction_t split_fn = nullptr;
   uint32_t split_threads = 0;
-  hipFunction_t hx_fn = nullptr, hx4_fn = nullptr, hx4b_fn = nullptr;
+  hipFunction_t hx_fn = nullptr, hx4_fn = nullptr, hx4b_fn = nullptr, hxs_fn = nullptr;
   hipFunction_t tok_fn = nullptr;
   uint32_t tok_per_wg = 0;
   std::string name;                 // the pipeline's shader name
@@ -574,6 +575,15 @@ Launch x_half_prepass(skyla_hip_context *ctx, const Command &a, uint64_t h_bytes
   return l;
 }
 
+// Can matmul c run as a further segment of a fused launch of matmul a on f16 rows?  The
+// same kernel, bindings and token grid, and the same activation rows (x_off, n_in,
+// x_stride); dispatches with no barrier between them are independent.
+bool fusable_matmul(const Command &a, const Command &c) {
+  return c.kind == Command::Dispatch && c.hx_fn == a.hx_fn && c.hxs_fn == a.hxs_fn && !c.segmented &&
+         c.push.size() == 13 && c.bufs == a.bufs && c.groups[1] == 1 && c.groups[2] == a.groups[2] &&
+         c.push[4] == a.push[4] && c.push[6] == a.push[6] && c.push[8] == a.push[8];
+}
+
 // The launch list of a recording.  Barriers need no command of their own: launches on one
 // stream (and the nodes of a graph captured from it) run in order.  SKYLA_HIP_FUSE=0 keeps
 // one launch per dispatch; SKYLA_HIP_XHALF=0 keeps the matmuls' own f32 staging.
@@ -611,6 +621,54 @@ std::vector<Launch> build_launches(skyla_hip_context *ctx, const std::vector<Com
       if (key != xkey) {
         out.push_back(x_half_prepass(ctx, a, h_off));
         xkey = key;
+      }
+      // Matmuls on the same rows with no barrier between them (q, k, v of a prefill chunk)
+      // run as one launch of segments while the run stays a K-split launch (at most 128
+      // tiles: the split spreads the few tiles of each small matrix over more CUs).
+      uint32_t n_run = 1;
+      uint64_t row_tiles = a.groups[0];
+      if (fuse && a.hxs_fn && a.split_fn) {
+        while (n_run < kMaxSeg && i + n_run < cmds.size() && fusable_matmul(a, cmds[i + n_run]) &&
+               (row_tiles + cmds[i + n_run].groups[0]) * a.groups[2] <= 128) {
+          row_tiles += cmds[i + n_run].groups[0];
+          n_run++;
+        }
+      }
+      if (n_run > 1) {
+        const uint64_t tiles = row_tiles * a.groups[2];
+        uint32_t S = (uint32_t)(256 / tiles);  // split_of's rule on the fused tile count
+        S = std::min(std::min(S, a.push[6] / 256 / 4), 8u);
+        if (S < 2) S = 1;
+        Launch l;
+        l.fn = a.hxs_fn;
+        l.threads = 512;
+        l.bufs = a.bufs;
+        const size_t w = 13;
+        l.args.assign(1 + kMaxSeg + kMaxSeg * w, 0u);
+        l.args[0] = n_run;
+        uint32_t start = 0;
+        for (uint32_t sgi = 0; sgi < kMaxSeg; sgi++) {
+          l.args[1 + sgi] = sgi < n_run ? start : 0xffffffffu;
+          if (sgi < n_run) {
+            const Command &c = cmds[i + sgi];
+            uint32_t *dst = l.args.data() + 1 + kMaxSeg + sgi * w;
+            std::copy(c.push.begin(), c.push.end(), dst);
+            dst[4] = (uint32_t)(h_off / 2);  // f16 units
+            dst[8] = a.push[6];
+            start += c.groups[0];
+          }
+        }
+        l.groups[0] = (uint32_t)row_tiles;
+        l.groups[1] = 1;
+        l.groups[2] = a.groups[2] * S;
+        l.split = S;
+        l.n_cnt = S > 1 ? (uint32_t)tiles : 0;
+        l.ws_bytes = S > 1 ? tiles * S * kSplitTileBytes : 0;
+        l.xh_buf = 2;
+        l.xh_bytes = out.back().xh_bytes;
+        out.push_back(std::move(l));
+        i += n_run;
+        continue;
       }
       const Command *one[1] = {&a};
       Launch l = pack(one, 1);
@@ -1266,6 +1324,7 @@ int skyla_hip_pipeline_new(skyla_hip_context *ctx, const char *name, uint32_t n_
       p->hx_fn = find_function(ctx, "matmul_x8__" + std::to_string(spec[0]) + "_" + std::to_string(spec[1]));
       p->hx4_fn = find_function(ctx, "matmul_x4__" + std::to_string(spec[0]) + "_" + std::to_string(spec[1]));
       p->hx4b_fn = find_function(ctx, "matmul_x4b__" + std::to_string(spec[0]) + "_" + std::to_string(spec[1]));
+      p->hxs_fn = find_function(ctx, "matmul_x8s__" + std::to_string(spec[0]) + "_" + std::to_string(spec[1]));
       p->split_threads = 512;
     }
   }
@@ -1351,6 +1410,7 @@ int skyla_hip_record_dispatch(skyla_hip_recorder *r, const skyla_hip_pipeline *p
   c.hx_fn = p->hx_fn;
   c.hx4_fn = p->hx4_fn;
   c.hx4b_fn = p->hx4b_fn;
+  c.hxs_fn = p->hxs_fn;
   c.split_threads = p->split_threads;
   c.tok_fn = p->tok_fn;
   c.tok_per_wg = p->tok_per_wg;
@@ -1594,6 +1654,7 @@ int skyla_hip_time_dispatch(skyla_hip_context *ctx, const skyla_hip_pipeline *p,
   c.hx_fn = p->hx_fn;
   c.hx4_fn = p->hx4_fn;
   c.hx4b_fn = p->hx4b_fn;
+  c.hxs_fn = p->hxs_fn;
   c.split_threads = p->split_threads;
   c.tok_fn = p->tok_fn;
   c.tok_per_wg = p->tok_per_wg;
@@ -1650,6 +1711,7 @@ int skyla_hip_dispatch_noalloc(skyla_hip_context *ctx, const skyla_hip_pipeline 
   c.hx_fn = p->hx_fn;
   c.hx4_fn = p->hx4_fn;
   c.hx4b_fn = p->hx4b_fn;
+  c.hxs_fn = p->hxs_fn;
   c.split_threads = p->split_threads;
   c.tok_fn = p->tok_fn;
   c.tok_per_wg = p->tok_per_wg;

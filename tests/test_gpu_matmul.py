@@ -107,8 +107,9 @@ def test_matmul_f16_prepass_same_bits(ctx, name, dtype, n_in, n_out, n_tok, accu
 
 
 def test_matmul_f16_prepass_shared(ctx):
-    """Two matmuls on the same rows with no barrier between them share one prepass (three
-    launches), and each gives the bits of its own f32-staged launch."""
+    """Two matmuls on the same rows with no barrier between them share one prepass and run as
+    one launch of two segments (two launches in all, three without the f16 rows), and each
+    gives the bits of its own f32-staged launch."""
     n_in, n_tok = 1024, 70
     mats = [(E.DType.Q4K, n_in, n, synth.matrix("mm-xh", f"shared-{n}", E.DType.Q4K, n_in, n)) for n in (256, 384)]
     x = synth.activations("mm-xh", "shared-x", (n_tok, n_in))
@@ -134,7 +135,7 @@ def test_matmul_f16_prepass_shared(ctx):
                 got[xh] = (launches, s.y(2 * n_tok, s.s_out))
             finally:
                 s.free()
-    assert got["1"][0] == 3 and got["0"][0] == 2
+    assert got["1"][0] == 2 and got["0"][0] == 2
     assert np.array_equal(got["1"][1].view(np.uint32), got["0"][1].view(np.uint32))
     for i, (dt, _, n, d) in enumerate(mats):
         want = so.matmul(int(dt), d, n_in, n, x)
@@ -165,3 +166,43 @@ def test_matmul_balanced_grid(ctx, name, dtype, n_in, n_out, n_tok, accum):
     assert np.array_equal(got[:, :whole_rows].view(np.uint32), plain[:, :whole_rows].view(np.uint32))
     assert rel_l2(got[:, whole_rows:], plain[:, whole_rows:]) <= 1e-6
     assert rel_l2(got, want) <= GUARD
+
+
+@pytest.mark.parametrize("n_tok", [128, 100])
+def test_matmul_segments_qkv(ctx, n_tok):
+    """q, k and v of a prefill chunk (Q4_K 4096 -> 4096, 1024, 1024 in one buffer, no barrier
+    between them) run as one launch of three segments after the shared f16 row prepass: the
+    bits of the three separate launches (SKYLA_HIP_FUSE=0; the same K split here), and each
+    within the bar of the oracle."""
+    n_in = 4096
+    outs = [4096, 1024, 1024]
+    mats = [(E.DType.Q4K, n_in, n, synth.matrix("mm-seg", f"qkv-{i}-{n}", E.DType.Q4K, n_in, n))
+            for i, n in enumerate(outs)]
+    x = synth.activations("mm-seg", f"x-{n_tok}", (n_tok, n_in))
+    got = {}
+    for fuse in ("1", "0"):
+        with env(SKYLA_HIP_FUSE=fuse):
+            s = Setup(ctx, mats, n_in, max(outs), rows=len(outs) * n_tok)
+            try:
+                s.set_x(x)
+                z = -(-n_tok // E.MATMUL_TILE_COLS)
+
+                def body(r):
+                    g = E.Graph(r, s.k, None, None, True)
+                    for i, m in enumerate(s.q):
+                        g.matvec(m, (s.x_off, s.s_in), (s.y_off + i * n_tok * s.s_out, s.s_out), False, True,
+                                 groups_z=z)
+                rec = ctx.record(False, body)
+                try:
+                    launches = rec.launches()
+                    ctx.replay(rec)
+                finally:
+                    rec.free()
+                got[fuse] = (launches, s.y(len(outs) * n_tok, s.s_out))
+            finally:
+                s.free()
+    assert got["1"][0] == 2 and got["0"][0] == 4   # prepass + one fused launch / + three launches
+    assert np.array_equal(got["1"][1].view(np.uint32), got["0"][1].view(np.uint32))
+    for i, (dt, _, n, d) in enumerate(mats):
+        want = so.matmul(int(dt), d, n_in, n, x)
+        assert rel_l2(got["1"][1][i * n_tok:(i + 1) * n_tok, :n], want) <= GUARD
