@@ -553,6 +553,42 @@ extern "C" __global__ __launch_bounds__(1024) void attention_merge__128_0(float 
   }
 }
 
+// attention_merge for batched steps (prefill chunks, grid [ceil(n_head / 4), tokens] by the
+// runtime): one wave per (head, token), lane l the head's dims 2l and 2l + 1.  The split
+// weights exp(m_s - M) are formed 64 at a time, one per lane, and broadcast by readlane (the
+// split index is wave-uniform).  The same quantity as attention_merge__128_0 in another
+// summation order; a prefill token has few splits, which the 1024-thread form leaves idle.
+extern "C" __global__ __launch_bounds__(256) void attention_merge_t__128_0(float *a, const uint32_t *ctl,
+                                                                             MergePush p, uint32_t n_head,
+                                                                             uint32_t n_tok) {
+  const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const uint32_t h = blockIdx.x * 4 + wave, tok = blockIdx.y;
+  (void)n_tok;
+  if (tok >= ctl[2] || h >= n_head) return;
+  const uint32_t used = min(min((ctl[1] + tok + p.chunk) / p.chunk, p.n_split), MAX_SPLITS);
+  const uint32_t first = p.part_off + tok * p.part_stride + h * p.n_split * PART;
+  float big = -INFINITY;
+  for (uint32_t s = lane; s < used; s += 64) big = fmaxf(big, a[first + s * PART]);
+  big = wave_max(big);
+  float total = 0.0f, ox = 0.0f, oy = 0.0f;
+  for (uint32_t s0 = 0; s0 < used; s0 += 64) {
+    const uint32_t s = s0 + lane;
+    const float wl = s < used ? expf(a[first + s * PART] - big) : 0.0f;
+    if (s < used) total = __builtin_fmaf(wl, a[first + s * PART + 1], total);
+    const uint32_t n = min(used - s0, 64u);
+    for (uint32_t j = 0; j < n; j++) {
+      const float wj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wl), (int)j));
+      const float *v = a + first + (s0 + j) * PART + 2 + 2 * lane;
+      ox = __builtin_fmaf(wj, v[0], ox);
+      oy = __builtin_fmaf(wj, v[1], oy);
+    }
+  }
+  total = wave_sum(total);
+  float *o = a + p.o_off + tok * p.o_stride + h * HD + 2 * lane;
+  o[0] = ox / total;
+  o[1] = oy / total;
+}
+
 // take_last (take_last.comp): the last token row of a chunk, for the output head.
 extern "C" __global__ __launch_bounds__(256) void take_last(float *a, const uint32_t *ctl, LastPush p) {
   const uint32_t i = blockIdx.x * 256 + threadIdx.x;

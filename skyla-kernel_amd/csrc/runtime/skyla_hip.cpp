@@ -191,8 +191,10 @@ struct skyla_hip_pipeline {
   hipFunction_t hx4b_fn = nullptr;       // and over a balanced grid (some tiles in K halves)
   hipFunction_t hxs_fn = nullptr;        // the eight-wave tile over several matrices (segments)
   uint32_t split_threads = 0;
-  hipFunction_t tok_fn = nullptr;        // batched form: a tok_per_wg x tok_per_wg block of
+  hipFunction_t tok_fn = nullptr;        // batched form: a tok_per_wg x tok_per_wg_y block of
   uint32_t tok_per_wg = 0;               // grid.x and grid.y per workgroup
+  uint32_t tok_per_wg_y = 0;
+  uint32_t tok_threads = 0;              // its workgroup size (0: the pipeline's)
   std::string name;                      // shader name
   hipFunction_t moe_fn = nullptr;        // MoE decode forms (fuse_moe): moe_logits -> moe_logits_route,
   hipFunction_t moe_fn2 = nullptr;       // Q4_K experts -> the gate/up pair, and the down + combine forms
@@ -215,7 +217,7 @@ struct Command {
   uint32_t split_threads = 0;
   hipFunction_t hx_fn = nullptr, hx4_fn = nullptr, hx4b_fn = nullptr, hxs_fn = nullptr;
   hipFunction_t tok_fn = nullptr;
-  uint32_t tok_per_wg = 0;
+  uint32_t tok_per_wg = 0, tok_per_wg_y = 0, tok_threads = 0;
   std::string name;                 // the pipeline's shader name
   hipFunction_t moe_fn = nullptr, moe_fn2 = nullptr, moe_fn3 = nullptr, moe_fn4 = nullptr;
   uint32_t chain_kind = 0, chain_accum = 0;
@@ -340,7 +342,8 @@ Launch pack(const Command *const *run, uint32_t n) {
     if (a.tok_fn && a.groups[1] > 1) {  // grid (x, y) = (experts, tokens): blocks of both
       l.fn = a.tok_fn;
       l.groups[0] = (a.groups[0] + a.tok_per_wg - 1) / a.tok_per_wg;
-      l.groups[1] = (a.groups[1] + a.tok_per_wg - 1) / a.tok_per_wg;
+      l.groups[1] = (a.groups[1] + a.tok_per_wg_y - 1) / a.tok_per_wg_y;
+      if (a.tok_threads) l.threads = a.tok_threads;
       l.extra = {a.groups[0], a.groups[1]};
     }
     const uint32_t S = split_of(a);
@@ -1307,7 +1310,19 @@ int skyla_hip_pipeline_new(skyla_hip_context *ctx, const char *name, uint32_t n_
   // router logits of a batch: 8 x 8 (expert, token) blocks per workgroup (moe.hip, moe_logits_t)
   if (std::strcmp(name, "moe_logits") == 0) {
     p->tok_fn = find_function(ctx, "moe_logits_t");
-    p->tok_per_wg = 8;
+    p->tok_per_wg = p->tok_per_wg_y = 8;
+  }
+  // the attention merge of a batched step (grid (heads, tokens)): one wave per (head, token),
+  // four heads per workgroup (attention.hip, attention_merge_t); SKYLA_HIP_MERGE_T=0 keeps
+  // the 1024-thread form
+  if (std::strcmp(name, "attention_merge") == 0 && n_spec == 2 && spec[0] == 128 && spec[1] == 0) {
+    const char *env = std::getenv("SKYLA_HIP_MERGE_T");
+    if (!(env && env[0] == '0')) {
+      p->tok_fn = find_function(ctx, "attention_merge_t__128_0");
+      p->tok_per_wg = 4;
+      p->tok_per_wg_y = 1;
+      p->tok_threads = 256;
+    }
   }
   // dense K-quant matmul (TYPE 1/2, MOE 0): its K-split variant, used for launches with few
   // tiles (split_of); SKYLA_HIP_SPLITK=0 keeps every launch on the engine's kernel
@@ -1327,6 +1342,13 @@ int skyla_hip_pipeline_new(skyla_hip_context *ctx, const char *name, uint32_t n_
       p->hxs_fn = find_function(ctx, "matmul_x8s__" + std::to_string(spec[0]) + "_" + std::to_string(spec[1]));
       p->split_threads = 512;
     }
+  }
+  if (p->tok_fn) {  // the batched form must take the workgroup it is launched with
+    int tok_max = 0;
+    const uint32_t want = p->tok_threads ? p->tok_threads : threads;
+    if (hipFuncGetAttribute(&tok_max, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, p->tok_fn) != hipSuccess ||
+        tok_max <= 0 || want > (uint32_t)tok_max)
+      p->tok_fn = nullptr;
   }
   int max_threads = 0;
   if (hipFuncGetAttribute(&max_threads, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, p->fn) ==
@@ -1414,6 +1436,8 @@ int skyla_hip_record_dispatch(skyla_hip_recorder *r, const skyla_hip_pipeline *p
   c.split_threads = p->split_threads;
   c.tok_fn = p->tok_fn;
   c.tok_per_wg = p->tok_per_wg;
+  c.tok_per_wg_y = p->tok_per_wg_y;
+  c.tok_threads = p->tok_threads;
   c.name = p->name;
   c.moe_fn = p->moe_fn;
   c.moe_fn2 = p->moe_fn2;
@@ -1658,6 +1682,8 @@ int skyla_hip_time_dispatch(skyla_hip_context *ctx, const skyla_hip_pipeline *p,
   c.split_threads = p->split_threads;
   c.tok_fn = p->tok_fn;
   c.tok_per_wg = p->tok_per_wg;
+  c.tok_per_wg_y = p->tok_per_wg_y;
+  c.tok_threads = p->tok_threads;
   for (int i = 0; i < 3; i++) c.groups[i] = groups[i];
   c.bufs = p->sets[0];
   c.push.assign(push, push + n_push);
@@ -1715,6 +1741,8 @@ int skyla_hip_dispatch_noalloc(skyla_hip_context *ctx, const skyla_hip_pipeline 
   c.split_threads = p->split_threads;
   c.tok_fn = p->tok_fn;
   c.tok_per_wg = p->tok_per_wg;
+  c.tok_per_wg_y = p->tok_per_wg_y;
+  c.tok_threads = p->tok_threads;
   for (int i = 0; i < 3; i++) c.groups[i] = groups[i];
   c.bufs = p->sets[0];
   c.push.assign(push, push + n_push);
