@@ -909,13 +909,17 @@ SK_DEV void matmul_tile128_w(const uint4 *__restrict__ w, const uint16_t *__rest
     __builtin_amdgcn_s_waitcnt(0);  // each wave's partial stores complete before the barrier
     __syncthreads();
     // Release at agent scope: the count is made after this workgroup's partial stores are
-    // visible device-wide (buffer_wbl2 sc1 and a wait, by one thread).  The last workgroup
-    // reads the partials with agent-scope atomic loads, which go to the coherence point past
-    // the XCD's L2, so it needs no acquire-side L2 invalidate (that was the 2x cost of a
-    // full __threadfence here).
+    // visible device-wide (buffer_wbl2 sc1 and a wait, by one thread).  Only the last
+    // workgroup of a tile reads the partials, with agent-scope loads; a full __threadfence in
+    // every workgroup (release and acquire) made the split 2x slower.
     if (tid == 0) last = __hip_atomic_fetch_add(&cnt[tile], 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT) == S - 1;
     __syncthreads();
     if (!last) return;
+    // No acquire fence here: the partials are read with agent-scope loads (sc1, served past
+    // the XCD's non-coherent L2 state) that issue only after the count's result is back and
+    // the workgroup has met at the barrier.  An agent-scope acquire (buffer_inv sc1 in the
+    // last workgroup of each tile) invalidates the L2 the other workgroups stream through:
+    // M = 512 q 51 -> 59 us, config-5 prefill 13.7k -> 12.4k tok/s.
     // The partials added in split order.  Split by split, all of a lane's values are loaded
     // before any is added (a wave-uniform branch per split), so a partial costs one round
     // trip past the L2; a branch per value made the compiler wait for every load in turn

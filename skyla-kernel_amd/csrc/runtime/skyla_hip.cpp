@@ -1498,7 +1498,10 @@ int skyla_hip_record_end(skyla_hip_recorder *r, skyla_hip_recording **out) {
   HIP_TRY(hipSetDevice(rec->ctx->device));
   if (int s = bind_workspace(rec->launches, &rec->workspace)) return s;
   if (int s = chain_launches(rec->ctx, rec->launches, &rec->chain_mem)) return s;
-  if (!rec->profile && skyla_hip_recording_len(rec.get()) > 0) {
+  // SKYLA_HIP_NOGRAPH=1: replay the launch list as direct launches (kernel traces of the
+  // exact launches a graph would hold, fused forms included)
+  const char *nograph = std::getenv("SKYLA_HIP_NOGRAPH");
+  if (!rec->profile && skyla_hip_recording_len(rec.get()) > 0 && !(nograph && nograph[0] == '1')) {
     // One graph for the whole recording, captured from the launch list on the stream.
     skyla_hip_context *ctx = rec->ctx;
     HIP_TRY(hipSetDevice(ctx->device));
