@@ -925,15 +925,17 @@ const VariantRule kVariantRules[] = {
 // matvec_q4k_ks_body): (rows per slot, row-groups per workgroup) by launch size, from sweeps
 // on MI355X.  A workgroup of 512 threads covers 4 * rpl * ng rows (half as many outputs for
 // the gate/up pair).  Config-2 launches (us, K-split 4 x 1 against the LDS-staged forms):
-// q+k+v 6.50 / 6.71, o 5.28 / 6.13, gate+up 13.33 / 13.04 -- so launches of 16384 rows or
-// more (gate+up; 8192 outputs of the pair) stay on the LDS-staged forms.  SKYLA_HIP_KS=0
-// keeps the LDS-staged forms everywhere; SKYLA_HIP_KS=R_G forces one shape (for sweeps).
+// q+k+v 6.50 / 6.71, o 5.28 / 6.13; gate+up was 13.33 / 13.04 in an earlier build, and the
+// whole config-2 step now measures 3385 against 3322 GB/s with gate+up on 4 x 1 too, so
+// every plain launch takes it.  The gate/up pair (8192 outputs or more) stays on the
+// LDS-staged pair form.  SKYLA_HIP_KS=0 keeps the LDS-staged forms everywhere;
+// SKYLA_HIP_KS=R_G forces one shape (for sweeps).
 struct KsRule {
   uint64_t min_rows, max_rows;  // rows of the launch (outputs for the gate/up pair)
   uint32_t rpl, ng;
   uint32_t pd = 1;              // Q6_K: row-groups loaded ahead
 };
-const KsRule kKsRules[] = {{0, 16383, 4, 1}};
+const KsRule kKsRules[] = {{0, ~uint64_t{0}, 4, 1}};
 const KsRule kKsPairRules[] = {{0, 8191, 4, 1}};
 // K-split Q6_K form (n_in = 12288; rows per slot, row-groups, row-groups loaded ahead).
 // Config-2 down projection (4096 rows), us per launch over 36 layers on two boxes: (1, 8, 1)

@@ -282,9 +282,11 @@ def test_glu_pair_equals_gate_up_then_silu(ctx, n_in, n_out):
     finally:
         s.free()
     assert np.isfinite(got).all()
-    if 2 * n_out >= 6144:  # the plain gate+up launch runs the same variant (K-split, or 8, 1, 16)
+    # plain Q4_K launches with n_in 4096 run the K-split form; the pair takes it below 8192
+    # outputs (the runtime's K-split rules) and the LDS-staged pair form above
+    if n_in == 4096 and n_out < 8192:  # the same K-split sums on both sides
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
-    else:                  # another lane split of the same sums
+    else:                              # another lane split of the same sums
         assert rel_l2(got, want) <= 1e-5
 
 
