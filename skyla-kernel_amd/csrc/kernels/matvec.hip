@@ -411,7 +411,7 @@ SK_DEV void matvec_q4k_body(const uint4 *__restrict__ w, const float *x, float *
 template <int ACCUM, int RPL, int NG, int MODE = 0, typename P = MatvecPush2>
 SK_DEV void matvec_q4k_ks_body(const uint4 *__restrict__ w, const float *x, float *y, const P &p,
                                uint32_t bx) {
-  constexpr bool PAIR = MODE == 3;
+  constexpr bool PAIR = MODE == 3 || MODE == 4, NORM = MODE == 2 || MODE == 4;
   constexpr int RG = 4 * RPL;             // rows per row-group
   constexpr int OG = PAIR ? RG / 2 : RG;  // outputs per row-group
   constexpr int OUT = OG * NG;            // outputs per workgroup
@@ -419,7 +419,7 @@ SK_DEV void matvec_q4k_ks_body(const uint4 *__restrict__ w, const float *x, floa
   static_assert(RG % 8 == 0 && CPL >= 1 && CPL <= 4, "two headers per row, 64 lanes");
   __shared__ float4 hp[8][RG][2][4];      // per wave: row, super-block, chunk
   __shared__ float part[8][RG * NG];
-  __shared__ float wss[MODE == 2 ? 8 : 1];
+  __shared__ float wss[NORM ? 8 : 1];
 
   const uint32_t tid = threadIdx.x, wv = tid >> 6, l = tid & 63;
   const uint32_t ul = l & 15, slot = l >> 4;
@@ -470,7 +470,7 @@ SK_DEV void matvec_q4k_ks_body(const uint4 *__restrict__ w, const float *x, floa
   }
   uint4 qc[RPL], hc;
   load_group(0, qc, hc);
-  if constexpr (MODE == 2) {  // x * w (the norm weights sit at aux_off), and sum(x^2)
+  if constexpr (NORM) {  // x * w (the norm weights sit at aux_off), and sum(x^2)
     const float *wn = x + p.aux_off;
     float sq = 0.0f;
 #pragma unroll
@@ -531,11 +531,13 @@ SK_DEV void matvec_q4k_ks_body(const uint4 *__restrict__ w, const float *x, floa
       t += part[i][g * RG + o];
       if constexpr (PAIR) u += part[i][g * RG + 2 * RPL + o];
     }
-    if constexpr (MODE == 2) {
+    if constexpr (NORM) {  // the pair scales its gate and up sums alike, before the SiLU
       float s2 = 0.0f;
 #pragma unroll
       for (int i = 0; i < 8; i++) s2 += wss[i];
-      t *= 1.0f / sqrtf(s2 / (float)p.n_in + p.eps);
+      const float r = 1.0f / sqrtf(s2 / (float)p.n_in + p.eps);
+      t *= r;
+      if constexpr (PAIR) u *= r;
     }
     const uint32_t yo = p.y_off + out0 + tid;
     if constexpr (PAIR) {
@@ -1410,7 +1412,15 @@ MV_Q6K(4, 1, 1, 0, 16)
     (void)ids;                                                                               \
     matvec_q4k_ks_body<0, R, G, 3>(w, x, y, segment_push(m, s), blockIdx.x - m.start[s]);    \
   }
-#define MV_Q4K_KS_ALL(R, G) MV_Q4K_KS(0, R, G) MV_Q4K_KS(1, R, G) MV_Q4K_KS_NORM(R, G) MV_Q4K_KS_GLU(R, G)
+#define MV_Q4K_KS_GLUN(R, G)                                                                 \
+  extern "C" __global__ __launch_bounds__(512) void matvec_q4k_ks_glun__0_##R##_##G(          \
+      const uint4 *w, const float *x, float *y, const uint32_t *ids, Segments<MatvecPushGluN> m) { \
+    const uint32_t s = segment_of(m, blockIdx.x);                                            \
+    (void)ids;                                                                               \
+    matvec_q4k_ks_body<0, R, G, 4>(w, x, y, segment_push(m, s), blockIdx.x - m.start[s]);    \
+  }
+#define MV_Q4K_KS_ALL(R, G) MV_Q4K_KS(0, R, G) MV_Q4K_KS(1, R, G) MV_Q4K_KS_NORM(R, G) MV_Q4K_KS_GLU(R, G) \
+  MV_Q4K_KS_GLUN(R, G)
 MV_Q4K_KS_ALL(2, 1)
 MV_Q4K_KS_ALL(2, 2)
 MV_Q4K_KS_ALL(4, 1)

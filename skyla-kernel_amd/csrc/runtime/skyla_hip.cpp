@@ -937,6 +937,10 @@ struct KsRule {
 };
 const KsRule kKsRules[] = {{0, ~uint64_t{0}, 4, 1}};
 const KsRule kKsPairRules[] = {{0, 8191, 4, 1}};
+// the gate/up pair with the FFN norm folded in (MODE 4 of the K-split body), opt-in with
+// SKYLA_HIP_KSGLUN=1: config 5 measured 466 against 505 tok/s at 1k context for the
+// LDS-staged pair form (102 VGPRs with the norm weights held beside x, against 94)
+const KsRule kKsGlunRules[] = {{0, ~uint64_t{0}, 4, 1}};
 // K-split Q6_K form (n_in = 12288; rows per slot, row-groups, row-groups loaded ahead).
 // Config-2 down projection (4096 rows), us per launch over 36 layers on two boxes: (1, 8, 1)
 // 11.75 / 11.89 against 12.25 / 12.48 for the LDS-staged (8, 1, 64); (1, 8, 2) 12.40,
@@ -980,17 +984,20 @@ void add_ks(skyla_hip_context *ctx, const char *name, const uint32_t *spec, Reti
     return;
   }
   std::string ks;
-  bool pair = false;
+  bool pair = false, glun = false;
   if (std::strcmp(name, "matvec_q4k") == 0 && spec[3] == 0)
     ks = "matvec_q4k_ks__" + std::to_string(spec[1]);
   else if (std::strcmp(name, "matvec_q4k_norm") == 0 && spec[1] == 0)
     ks = "matvec_q4k_ks_norm__0";
   else if (std::strcmp(name, "matvec_q4k_glu") == 0)
     ks = "matvec_q4k_ks_glu__0", pair = true;
+  else if (std::strcmp(name, "matvec_q4k_glun") == 0 && std::getenv("SKYLA_HIP_KSGLUN") &&
+           std::getenv("SKYLA_HIP_KSGLUN")[0] == '1')
+    ks = "matvec_q4k_ks_glun__0", pair = true, glun = true;
   else
     return;
-  std::vector<KsRule> rules(pair ? std::begin(kKsPairRules) : std::begin(kKsRules),
-                            pair ? std::end(kKsPairRules) : std::end(kKsRules));
+  std::vector<KsRule> rules(glun ? std::begin(kKsGlunRules) : pair ? std::begin(kKsPairRules) : std::begin(kKsRules),
+                            glun ? std::end(kKsGlunRules) : pair ? std::end(kKsPairRules) : std::end(kKsRules));
   uint32_t fr = 0, fg = 0;
   if (env && std::sscanf(env, "%u_%u", &fr, &fg) == 2) rules = {{0, ~uint64_t{0}, fr, fg}};
   std::vector<MatvecAlt> alts;

@@ -214,12 +214,14 @@ def test_fused_matvec_forms(ctx, dtype, n_in, n_out, form, retile):
     assert err <= F32, err
 
 
+@pytest.mark.parametrize("ks", ["1", "0"])
 @pytest.mark.parametrize("big", [False, True])
 @pytest.mark.parametrize("n_in,n_out", [(4096, 12288), (1024, 1536), (2048, 100)])
-def test_glu_norm_pair_against_oracle(ctx, n_in, n_out, big):
+def test_glu_norm_pair_against_oracle(ctx, n_in, n_out, big, ks):
     """matvec_q4k_glun (the gate/up pair with the FFN RMSNorm folded in, from the raw
     residual) against the oracle's rmsnorm, the two Matrix::matvec and silu * up; `big`
-    puts an eighth of the residual past the f16 range (3e4 to 1e5)."""
+    puts an eighth of the residual past the f16 range (3e4 to 1e5).  With n_in 4096 and
+    SKYLA_HIP_KSGLUN=1 the runtime runs the K-split pair form, else the LDS-staged one."""
     g = synth.matrix("test-glu", f"gate-{n_in}-{n_out}", E.DType.Q4K, n_in, n_out)
     u = synth.matrix("test-glu", f"up-{n_in}-{n_out}", E.DType.Q4K, n_in, n_out)
     rg = synth.rng("test-glu", f"norm-{n_in}-{big}")
@@ -229,7 +231,8 @@ def test_glu_norm_pair_against_oracle(ctx, n_in, n_out, big):
     w = rg.uniform(0.5, 1.5, n_in).astype(np.float32)
     eps = 1e-6
     s = Setup(ctx, [(E.DType.Q4K, n_in, n_out, g), (E.DType.Q4K, n_in, n_out, u)], n_in, n_out, extra_f32=n_in)
-    k = E.Kernels(ctx, s.weights, s.arena, fuse="ffn")
+    with env(SKYLA_HIP_KSGLUN=ks):
+        k = E.Kernels(ctx, s.weights, s.arena, fuse="ffn")
     try:
         s.arena.as_f32()[s.extra_off: s.extra_off + n_in] = w
         s.set_x(x)
