@@ -432,6 +432,18 @@ constexpr int TN2 = 128;            // tokens per tile
 constexpr int NT2 = 512;            // threads per dense workgroup (8 waves, 2 per SIMD)
 constexpr int KX_W = 256;           // k per activation chunk: K-quant tiles (one super-block)
 constexpr int KX_Q8 = 128;          // k per activation chunk: Q8_0 tile (register weights)
+constexpr int DL_KX = 64;           // k per activation chunk: direct-to-LDS tile
+constexpr uint32_t DL_WBYTES = 128 * 128 + 128 * 16;  // one Q4_K weight stage: qs rows, headers
+
+// 16 B unit slot swizzle of a direct-to-LDS row (128 B rows, 8 units): distinct banks for 16
+// consecutive rows in a 256 B bank line and for 8 in a 128 B one
+SK_DEV uint32_t dl_swz(uint32_t r) { return (r & 7u) ^ ((r >> 3) & 1u); }
+typedef __attribute__((address_space(3))) void dl_lds;
+// vmcnt(N), the other counters unconstrained (gfx9 s_waitcnt encoding)
+template <int N>
+SK_DEV void dl_wait_vm() {
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0f70);
+}
 template <int KX>
 constexpr int pitch2() { return KX + 8; }  // f16 per staged token row (16 B pad)
 
@@ -538,7 +550,10 @@ SK_DEV bool store_chunk(f16 *lds, XChunk<KX, XHALF, NT, TN> &c, int *exps, uint3
   for (int i = 0; i < IPT; i++) {
     const uint32_t J = threadIdx.x + NT * i;
     const uint32_t n = J / IPR, kq = J % IPR;
-    if constexpr (XHALF) {
+    if constexpr (XHALF == 2) {  // x_half_rows wrote the rows pair-permuted already
+      *(uint4 *)(lds + n * PITCH2 + 8 * kq) = c.h[i];
+      if (kq == 0) exps[n] = 0;
+    } else if constexpr (XHALF) {
       const uint4 v = c.h[i];
       uint4 o;
       o.x = __builtin_amdgcn_perm(v.y, v.x, 0x05040100u);
@@ -654,22 +669,28 @@ struct WLds<2, NT> {  // Q6_K row: ql 128 | qh 64 | scales 16 | d 2
   }
 };
 
+// Q4_K fragment of lane half hh from the 8 qs bytes of its step (same arithmetic as
+// weight_frag): low nibbles for hh = 0, high nibbles (16q, the 1/16 is in the scale) for 1.
+SK_DEV f16x8 q4k_frag(uint2 v, uint32_t hh, f16x2 scale, f16x2 negmin) {
+  const uint32_t M = 0x64006400u;
+  const uint32_t mask = hh ? 0x00f000f0u : 0x000f000fu;
+  const f16x2 off = splat((f16)-1024.0f);
+  const uint32_t a = (v.x & mask) | M, b = ((v.x >> 8) & mask) | M;
+  const uint32_t e = (v.y & mask) | M, f = ((v.y >> 8) & mask) | M;
+  f16x2 w0 = __builtin_elementwise_fma(as_f16x2(a) + off, scale, negmin);
+  f16x2 w1 = __builtin_elementwise_fma(as_f16x2(b) + off, scale, negmin);
+  f16x2 w2 = __builtin_elementwise_fma(as_f16x2(e) + off, scale, negmin);
+  f16x2 w3 = __builtin_elementwise_fma(as_f16x2(f) + off, scale, negmin);
+  f16x8 r = {w0.x, w0.y, w1.x, w1.y, w2.x, w2.y, w3.x, w3.y};
+  return r;
+}
+
 // Fragment of step t for lane half hh from the LDS row (same arithmetic as weight_frag).
 template <int TYPE>
 SK_DEV f16x8 lds_frag(const uint32_t *row, int t, uint32_t hh, f16x2 scale, f16x2 negmin) {
   const uint32_t M = 0x64006400u;
   if constexpr (TYPE == 1) {
-    const uint2 v = *(const uint2 *)(row + 2 * t);  // qs bytes [8t, 8t + 8)
-    const uint32_t mask = hh ? 0x00f000f0u : 0x000f000fu;
-    const f16x2 off = splat((f16)-1024.0f);
-    const uint32_t a = (v.x & mask) | M, b = ((v.x >> 8) & mask) | M;
-    const uint32_t e = (v.y & mask) | M, f = ((v.y >> 8) & mask) | M;
-    f16x2 w0 = __builtin_elementwise_fma(as_f16x2(a) + off, scale, negmin);
-    f16x2 w1 = __builtin_elementwise_fma(as_f16x2(b) + off, scale, negmin);
-    f16x2 w2 = __builtin_elementwise_fma(as_f16x2(e) + off, scale, negmin);
-    f16x2 w3 = __builtin_elementwise_fma(as_f16x2(f) + off, scale, negmin);
-    f16x8 r = {w0.x, w0.y, w1.x, w1.y, w2.x, w2.y, w3.x, w3.y};
-    return r;
+    return q4k_frag(*(const uint2 *)(row + 2 * t), hh, scale, negmin);  // qs bytes [8t, 8t + 8)
   } else {
     const int hf = t >> 3, g = (t >> 1) & 3;
     const uint32_t l0 = 16 * (t & 1) + 8 * hh;
@@ -723,6 +744,115 @@ SK_DEV void lds_scales(const uint32_t *row, uint32_t hh, StageScales<TYPE> &o) {
 // matmuls with no barrier between them that read the same activations); the row tiles of
 // segment s follow those of segment s - 1, and each takes its own push words (regions,
 // y_off, n_out, y_stride); x_off, n_in and x_stride are the same for all.
+// Per-lane state of the direct-to-LDS tile: buffer resources, this lane's load offsets
+// (activation pieces, weight pieces) and its read swizzles.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+struct DLLanes {
+  u32x4 xres, wres;
+  uint32_t xo[4], wo[5];
+  uint32_t wv, lane, lrow, hh, wsw, xsw;
+};
+
+// Buffer resource words over [base, base + bytes) (as buf_res builds them: stride 0, raw
+// 32-bit data), for the loads below, which take it as an SGPR quad.
+SK_DEV u32x4 dl_res(const void *base, uint64_t bytes) {
+  const uint64_t a = (uint64_t)base;
+  u32x4 r = {(uint32_t)a, (uint32_t)(a >> 32) & 0xffffu, (uint32_t)(bytes < 0xffffffffull ? bytes : 0xffffffffull),
+             0x00020000u};
+  return r;
+}
+// One 16 B-per-lane buffer load into LDS: lane l's 16 B land at byte lds + 16 l (wave-
+// uniform lds, in M0); a load past the resource's end writes zeros.  Written as assembly on
+// purpose: with the compiler's own form of this load, every later LDS read waits until all
+// such loads in flight are done (the compiler cannot tell which LDS bytes they write),
+// which serialises the double buffering; here the explicit waits of dl_stage order each
+// buffer's loads before its reads, and the compiler's own waits (it does not count these
+// loads) can only wait longer than needed, never less.
+// (m0 is declared clobbered; the compiler warns that it reserves m0, which these kernels
+// use for nothing else)
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+SK_DEV void dl_load16(const u32x4 &res, uint32_t lds, uint32_t voff, uint32_t soff) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :
+               : "s"(lds), "v"(voff), "s"(res), "s"(soff)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+SK_DEV uint32_t lds_addr(const void *p) { return (uint32_t)(uintptr_t)(dl_lds *)p; }
+
+// A 64-k activation chunk (at k) into buffer dst: blocks 4 i + wave, 1 KiB each.
+SK_DEV void dl_issue_x(const DLLanes &L, f16 *__restrict__ dst, uint32_t k) {
+#pragma unroll
+  for (int i = 0; i < 4; i++) dl_load16(L.xres, lds_addr(dst + (4 * i + L.wv) * 512), L.xo[i], 2u * k);
+}
+// The Q4_K weights of super-block sb into buffer dst: qs blocks 4 i + wave, header blocks
+// 16 + wave (waves 0 and 1).
+SK_DEV void dl_issue_w(const DLLanes &L, uint32_t *__restrict__ dst, uint32_t sb) {
+#pragma unroll
+  for (int i = 0; i < 4; i++) dl_load16(L.wres, lds_addr(dst + (4 * i + L.wv) * 256), L.wo[i], 128u * sb);
+  if (L.wv < 2) dl_load16(L.wres, lds_addr(dst + (16 + L.wv) * 256), L.wo[4], 16u * sb);
+}
+
+// One 256-k stage of the direct-to-LDS tile: four 64-k chunks alternating between the
+// activation buffers x0 (chunks 0, 2) and x1 (1, 3), weights in wc; the loads of the next
+// chunk go to the other activation buffer, and at chunk 0 (when `more`) the next stage's
+// weights (super-block nsb) go to wn.  Every buffer is its own restrict pointer, so the
+// compiler sees that reading one buffer need not wait for the loads into another; the
+// waits that order the loads before the reads are the explicit ones here.
+template <int NB>
+SK_DEV void dl_stage(const DLLanes &L, f32x16 (&acc)[NB], f16 *__restrict__ x0, f16 *__restrict__ x1,
+                     const uint32_t *__restrict__ wc, uint32_t *__restrict__ wn, bool more, uint32_t k0,
+                     uint32_t nsb) {
+  StageScales<1> ss;
+#pragma unroll
+  for (int c4 = 0; c4 < KC / DL_KX; c4++) {
+    // this wave's loads of chunk c4 (and, at c4 = 0, of the stage's weights) are in LDS; at
+    // c4 = 1 the next stage's weight loads, issued after the chunk's, may stay in flight
+    if (c4 == 1 && more)
+      dl_wait_vm<4>();
+    else
+      dl_wait_vm<0>();
+    __syncthreads();
+    if (c4 + 1 < KC / DL_KX)
+      dl_issue_x(L, (c4 & 1) ? x0 : x1, k0 + DL_KX * (c4 + 1));
+    else if (more)
+      dl_issue_x(L, x0, k0 + KC);
+    if (c4 == 0) {
+      __builtin_amdgcn_sched_barrier(0);  // the weight loads stay behind the chunk's
+      if (more) dl_issue_w(L, wn, nsb);
+      WStage<1> hs;
+      hs.hd = *(const uint4 *)(wc + 4096 + 4 * L.lrow);
+      stage_scales<1>(hs, L.hh, ss);
+    }
+    const f16 *xb = (c4 & 1) ? x1 : x0;
+    f16x8 xf0[NB], xf1[NB], wf0, wf1;
+    auto frags = [&](int ts, f16x8(&xf)[NB], f16x8 &wf) {
+      const int t = 4 * c4 + ts;  // chunk c4 holds steps 4 c4 .. 4 c4 + 3 (koff: 32 hh + 8 ts)
+      f16x2 sc, nm;
+      ss.get(t, sc, nm);
+      wf = q4k_frag(*(const uint2 *)(wc + L.lrow * 32 + 4 * ((t >> 1) ^ L.wsw) + 2 * (t & 1)), L.hh, sc, nm);
+      const uint32_t xu = (4 * L.hh + ts) ^ L.xsw;
+#pragma unroll
+      for (int j = 0; j < NB; j++) xf[j] = *(const f16x8 *)(xb + (32 * j + (L.lane & 31)) * DL_KX + 8 * xu);
+    };
+    frags(0, xf0, wf0);
+#pragma unroll
+    for (int ts = 0; ts < 4; ts++) {
+      if (ts + 1 < 4) {
+        if (ts & 1)
+          frags(ts + 1, xf0, wf0);
+        else
+          frags(ts + 1, xf1, wf1);
+      }
+#pragma unroll
+      for (int j = 0; j < NB; j++)
+        acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16((ts & 1) ? xf1[j] : xf0[j], (ts & 1) ? wf1 : wf0, acc[j],
+                                                        0, 0, 0);
+    }
+  }
+}
+
 struct NoSegments {};
 template <int TYPE, int ACCUM, int XHALF, int NW, int TN = TN2, int MOE = 0, int HYB = 0, int SEG = 0,
           typename SG = NoSegments>
@@ -731,12 +861,15 @@ SK_DEV void matmul_tile128_w(const uint4 *__restrict__ w, const uint16_t *__rest
                              uint32_t *cnt = nullptr, uint32_t S = 1, uint32_t hf = 0, uint32_t hz = 1,
                              const SG &segs = SG{}) {
   static_assert(NW == 4 || TN == TN2, "eight waves split a 128-token tile");
+  // XHALF = 3: the f16 rows of x_half_rows and the Q4_K weights loaded straight into LDS
+  constexpr bool DL = XHALF == 3;
+  static_assert(!DL || (TYPE == 1 && NW == 4 && TN == TN2 && !MOE && !SEG), "direct-to-LDS form");
   constexpr int NT = 64 * NW;
   constexpr int NB = NW == 8 ? 2 : TN / 32;  // 32-token blocks per wave
-  constexpr int KX = (NW == 8 || TN < TN2) ? KX_W : 128, PITCH2 = pitch2<KX>();
+  constexpr int KX = DL ? DL_KX : (NW == 8 || TN < TN2) ? KX_W : 128, PITCH2 = pitch2<KX>();
   constexpr uint32_t PW = WLds<TYPE, NT>::PW;
-  __shared__ __attribute__((aligned(16))) f16 xs[TN * PITCH2];
-  __shared__ __attribute__((aligned(16))) uint32_t wl[TM * PW / 4];
+  __shared__ __attribute__((aligned(16))) f16 xs[DL ? 2 * TN * DL_KX : TN * PITCH2];
+  __shared__ __attribute__((aligned(16))) uint32_t wl[DL ? 2 * DL_WBYTES / 4 : TM * PW / 4];
   __shared__ uint32_t xrow[TN];
   __shared__ uint32_t yrow[TN];
   __shared__ int xexp[TN];
@@ -817,6 +950,42 @@ SK_DEV void matmul_tile128_w(const uint4 *__restrict__ w, const uint16_t *__rest
   const uint32_t n_stage = st1 - st0;
   const uint32_t n_chunk = n_stage * (KC / KX);
   const uint32_t kbase = st0 * KC;
+  if constexpr (DL) {
+    // Every operand byte goes from global memory straight into LDS (buffer loads with the
+    // LDS bit), double buffered: 64-k activation chunks (128 tokens x 128 B) and 256-k
+    // weight stages (128 rows x 128 B of qs, then the rows' 16 B headers).  One
+    // wave-instruction fills 1 KiB, lane l the 16 B at 16 l, so rows are unpadded and their
+    // 16 B units are stored XOR-swizzled by dl_swz(row).  One barrier per chunk: after it,
+    // chunk c + 1 loads into the other activation buffer (last read in chunk c - 1) and, at a
+    // stage's first chunk, the next stage's weights into the other weight buffer (last read
+    // in the stage before).  vmcnt counts a wave's loads in issue order, so before each
+    // barrier a wave waits for its loads of the chunk to come, letting only the weight loads
+    // issued after them stay in flight.
+    constexpr uint32_t XB = TN * DL_KX, WB = DL_WBYTES / 4;
+    const uint32_t wv = __builtin_amdgcn_readfirstlane(wave);
+    const uint32_t units = p.n_in >> 5, supers = p.n_in >> 8;
+    __syncthreads();  // xrow
+    const u32x4 xres = dl_res(x, 2ull * ((uint64_t)p.x_off + (uint64_t)n_all * p.x_stride));
+    const u32x4 wres = dl_res(w, 0xffffffffull);
+    uint32_t xo[4], wo[5];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const uint32_t r = 8 * (4 * i + wv) + (lane >> 3), slot = lane & 7;  // token / local row
+      xo[i] = 2u * (p.x_off + xrow[r] * p.x_stride + 8u * (slot ^ dl_swz(r)));
+      wo[i] = 16u * (p.o0 + min(row0 + r, p.n_out - 1) * units + (slot ^ dl_swz(r)));
+    }
+    wo[4] = 16u * (p.o1 + min(row0 + 64 * (wv & 1) + lane, p.n_out - 1) * supers);
+    const uint32_t wsw = dl_swz(lrow), xsw = dl_swz(lane & 31);
+    DLLanes L{xres, wres, {xo[0], xo[1], xo[2], xo[3]}, {wo[0], wo[1], wo[2], wo[3], wo[4]}, wv, lane, lrow, hh, wsw,
+              xsw};
+    dl_issue_x(L, xs, kbase);
+    dl_issue_w(L, wl, st0);
+    for (uint32_t st = 0; st < n_stage; st++) {
+      const uint32_t b = st & 1;
+      dl_stage<NB>(L, acc, xs, xs + XB, wl + b * WB, wl + (b ^ 1) * WB, st + 1 < n_stage, kbase + KC * st,
+                   st0 + st + 1);
+    }
+  } else {
   WLds<TYPE, NT> wr;
   if constexpr (TYPE == 1) wr.load(wr, w, p, row0, st0, tid, base);
   else wr.load(wr, w, wd, p, row0, st0, tid, base);
@@ -896,6 +1065,7 @@ SK_DEV void matmul_tile128_w(const uint4 *__restrict__ w, const uint16_t *__rest
       chunk++;
     }
   }
+  }
 
   if (S > 1) {
     const uint32_t tile = kt;
@@ -961,8 +1131,8 @@ SK_DEV void matmul_tile128_w(const uint4 *__restrict__ w, const uint16_t *__rest
         if (tok < n_tok) {
           float *o = y + p.y_off + (size_t)yrow[tok] * p.y_stride + my_row;
           float v = acc[j][i];
-          // XHALF = 2: the rows came from x_half_rows as x * 2^-e; scale back (exact)
-          if constexpr (XHALF == 2) v = __builtin_ldexpf(v, ((const int *)x)[yrow[tok]]);
+          // XHALF = 2, 3: the rows came from x_half_rows as x * 2^-e; scale back (exact)
+          if constexpr (XHALF >= 2) v = __builtin_ldexpf(v, ((const int *)x)[yrow[tok]]);
           *o = ACCUM ? *o + v : v;
         }
       }
@@ -1211,6 +1381,24 @@ MMH4B(1, 1)
 MMH4B(2, 0)
 MMH4B(2, 1)
 
+// The four-wave Q4_K tile with activations and weights loaded straight into LDS (XHALF 3),
+// on a plain grid (x4d) and on the balanced grid (x4db).
+#define MMH4D(A)                                                                                  \
+  extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void       \
+      matmul_x4d__1_##A(                                                                          \
+      const uint4 *w, const uint16_t *wd, const f16 *x, float *y, const uint32_t *ctl,            \
+      MatmulPush p, float *ws, uint32_t *cnt, uint32_t S) {                                       \
+    matmul_tile128_w<1, A, 3, 4>(w, wd, x, y, ctl, p, ws, cnt, S);                                \
+  }                                                                                               \
+  extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void       \
+      matmul_x4db__1_##A(                                                                         \
+      const uint4 *w, const uint16_t *wd, const f16 *x, float *y, const uint32_t *ctl,            \
+      MatmulPush p, float *ws, uint32_t *cnt, uint32_t S, uint32_t hf, uint32_t hz) {             \
+    matmul_tile128_w<1, A, 3, 4, TN2, 0, 1>(w, wd, x, y, ctl, p, ws, cnt, S, hf, hz);             \
+  }
+MMH4D(0)
+MMH4D(1)
+
 // The eight-wave tile on f16 rows over up to four matrices that read the same rows
 // (segment table as the matvecs take it; start[] counts row tiles).
 #define MMHS(T, A)                                                                                \
@@ -1228,7 +1416,8 @@ MMHS(2, 1)
 // in every tile (the runtime inserts it before dense K-quant matmuls with f32 inputs; one
 // conversion serves every matmul that reads the same rows before the next barrier).  Row t
 // (t < ctl[2]) of x -- x_off + t * x_stride, n_in values -- becomes h[t * n_in ..] =
-// f16(x * 2^-e_t), with e_t = 0 unless the row's largest |x| reaches 2^15, then its
+// f16(x * 2^-e_t), each four values k..k+3 stored in the order k, k+2, k+1, k+3 (the
+// order of the packed-quant extraction, so the tiles copy the rows as they are), with e_t = 0 unless the row's largest |x| reaches 2^15, then its
 // exponent - 14 (the tile's range guard, applied to the whole row): e[t] = e_t, and the tile
 // multiplies its sums back by 2^e_t.  With e_t = 0 the f16 values, and so the GEMM's bits,
 // are those of the tile's own conversion (round to nearest even).  Grid: one workgroup per
@@ -1275,7 +1464,8 @@ extern "C" __global__ __launch_bounds__(256) void x_half_rows(const float *x, ui
     if (k < p.n_in) {
       float4 a = v[i];
       if (e) a = make_float4(a.x * sc, a.y * sc, a.z * sc, a.w * sc);
-      *(uint2 *)(h + k) = make_uint2(as_u32(pack_f16x2(a.x, a.y)), as_u32(pack_f16x2(a.z, a.w)));
+      // pairs (0,2),(1,3) of every four values: the order the tiles' LDS rows hold
+      *(uint2 *)(h + k) = make_uint2(as_u32(pack_f16x2(a.x, a.z)), as_u32(pack_f16x2(a.y, a.w)));
     }
   }
   if (tid == 0) out[t] = (uint32_t)e;

@@ -88,17 +88,20 @@ def test_matmul_config3(ctx, name, dtype, n_in, n_out):
     assert err <= TOL and err <= GUARD, err
 
 
+@pytest.mark.parametrize("x4d", ["1", "0"])
 @pytest.mark.parametrize("name,dtype,n_in,n_out,n_tok,accum", [
     ("q", E.DType.Q4K, 4096, 4096, 512, False), ("gate", E.DType.Q4K, 4096, 12288, 512, False),
     ("down", E.DType.Q6K, 12288, 4096, 512, True), ("ragged", E.DType.Q4K, 1024, 200, 37, True),
-    ("ragged6", E.DType.Q6K, 768, 130, 100, False),
+    ("ragged6", E.DType.Q6K, 768, 130, 100, False), ("ragged4", E.DType.Q4K, 1024, 20000, 37, True),
 ])
-def test_matmul_f16_prepass_same_bits(ctx, name, dtype, n_in, n_out, n_tok, accum):
+def test_matmul_f16_prepass_same_bits(ctx, name, dtype, n_in, n_out, n_tok, accum, x4d):
     """The runtime's f16 row prepass (x_half_rows, then the tile on f16 rows: four waves
     unless the launch is K-split; SKYLA_HIP_XHALF=4 keeps the four-wave tile's plain grid)
     against the eight-wave tile's own f32 staging (SKYLA_HIP_XHALF=0): the same bits while
-    no activation reaches 2^15, K split or not, ACCUM or not, ragged token counts."""
-    with env(SKYLA_HIP_XHALF=4):
+    no activation reaches 2^15, K split or not, ACCUM or not, ragged rows and token counts.
+    Q4_K launches of more than 128 tiles (gate, ragged4) run the four-wave tile with its
+    operands loaded straight into LDS, or with SKYLA_HIP_X4D=0 the register-staged one."""
+    with env(SKYLA_HIP_XHALF=4, SKYLA_HIP_X4D=x4d):
         got1, want = _run(ctx, dtype, n_in, n_out, n_tok, accum=accum, tag="mm-xh")
     with env(SKYLA_HIP_XHALF=0):
         got0, _ = _run(ctx, dtype, n_in, n_out, n_tok, accum=accum, tag="mm-xh")
@@ -145,17 +148,19 @@ def test_matmul_f16_prepass_shared(ctx):
 CUS = 256  # MI355X: two four-wave workgroups per CU, 512 slots
 
 
-@pytest.mark.parametrize("name,dtype,n_in,n_out,n_tok,accum", [
-    ("gate", E.DType.Q4K, 4096, 12288, 512, False), ("ragged6", E.DType.Q6K, 768, 9000, 500, True),
+@pytest.mark.parametrize("name,dtype,n_in,n_out,n_tok,accum,x4d", [
+    ("gate", E.DType.Q4K, 4096, 12288, 512, False, "1"), ("gate", E.DType.Q4K, 4096, 12288, 512, False, "0"),
+    ("ragged4", E.DType.Q4K, 768, 20000, 200, True, "1"), ("ragged6", E.DType.Q6K, 768, 9000, 500, True, "1"),
 ])
-def test_matmul_balanced_grid(ctx, name, dtype, n_in, n_out, n_tok, accum):
+def test_matmul_balanced_grid(ctx, name, dtype, n_in, n_out, n_tok, accum, x4d):
     """A launch of more tiles than CUs and fewer than the two-per-CU slots runs the four-wave
     tile over a balanced grid: hf = 2 tiles - 512 tiles whole (the same bits as the plain
     grid, SKYLA_HIP_XHALF=4) and the rest in two K halves added in order (within f32
     reordering of the plain grid), against the oracle at the bar; ACCUM, ragged rows and
     tokens."""
-    got, want = _run(ctx, dtype, n_in, n_out, n_tok, accum=accum, tag="mm-bal")
-    with env(SKYLA_HIP_XHALF=4):
+    with env(SKYLA_HIP_X4D=x4d):
+        got, want = _run(ctx, dtype, n_in, n_out, n_tok, accum=accum, tag="mm-bal")
+    with env(SKYLA_HIP_XHALF=4, SKYLA_HIP_X4D=x4d):
         plain, _ = _run(ctx, dtype, n_in, n_out, n_tok, accum=accum, tag="mm-bal")
     hz = -(-n_tok // E.MATMUL_TILE_COLS)
     tiles = -(-n_out // 128) * hz
