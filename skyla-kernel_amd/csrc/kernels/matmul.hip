@@ -433,7 +433,6 @@ constexpr int NT2 = 512;            // threads per dense workgroup (8 waves, 2 p
 constexpr int KX_W = 256;           // k per activation chunk: K-quant tiles (one super-block)
 constexpr int KX_Q8 = 128;          // k per activation chunk: Q8_0 tile (register weights)
 constexpr int DL_KX = 64;           // k per activation chunk: direct-to-LDS tile
-constexpr uint32_t DL_WBYTES = 128 * 128 + 128 * 16;  // one Q4_K weight stage: qs rows, headers
 
 // 16 B unit slot swizzle of a direct-to-LDS row (128 B rows, 8 units): distinct banks for 16
 // consecutive rows in a 256 B bank line and for 8 in a 128 B one
@@ -685,10 +684,27 @@ SK_DEV f16x8 q4k_frag(uint2 v, uint32_t hh, f16x2 scale, f16x2 negmin) {
   return r;
 }
 
+// Q6_K fragment of step t from its 8 ql bytes l and 8 qh bytes h (same arithmetic as
+// weight_frag): quant groups g >= 2 take the high nibbles (16q, the 1/16 is in the scale).
+SK_DEV f16x8 q6k_frag(uint2 l, uint2 h, int t, f16x2 scale) {
+  const uint32_t M = 0x64006400u;
+  const int g = (t >> 1) & 3;
+  const uint32_t lmask = (g >= 2) ? 0x00f000f0u : 0x000f000fu;
+  const uint32_t hmask = (g >= 2) ? 0x03000300u : 0x00300030u;
+  const int hs = 4 - 2 * (g & 1);
+  auto q6 = [&](uint32_t lv, uint32_t hv) -> uint32_t { return (lv & lmask) | M | ((hv << hs) & hmask); };
+  const f16x2 off = splat((g >= 2) ? (f16)-1536.0f : (f16)-1056.0f);
+  f16x2 w0 = (as_f16x2(q6(l.x, h.x)) + off) * scale;
+  f16x2 w1 = (as_f16x2(q6(l.x >> 8, h.x >> 8)) + off) * scale;
+  f16x2 w2 = (as_f16x2(q6(l.y, h.y)) + off) * scale;
+  f16x2 w3 = (as_f16x2(q6(l.y >> 8, h.y >> 8)) + off) * scale;
+  f16x8 r = {w0.x, w0.y, w1.x, w1.y, w2.x, w2.y, w3.x, w3.y};
+  return r;
+}
+
 // Fragment of step t for lane half hh from the LDS row (same arithmetic as weight_frag).
 template <int TYPE>
 SK_DEV f16x8 lds_frag(const uint32_t *row, int t, uint32_t hh, f16x2 scale, f16x2 negmin) {
-  const uint32_t M = 0x64006400u;
   if constexpr (TYPE == 1) {
     return q4k_frag(*(const uint2 *)(row + 2 * t), hh, scale, negmin);  // qs bytes [8t, 8t + 8)
   } else {
@@ -696,18 +712,8 @@ SK_DEV f16x8 lds_frag(const uint32_t *row, int t, uint32_t hh, f16x2 scale, f16x
     const uint32_t l0 = 16 * (t & 1) + 8 * hh;
     const uint2 l = *(const uint2 *)(row + (hf * 64 + ((g & 1) ? 32 : 0) + l0) / 4);
     const uint2 h = *(const uint2 *)(row + (128 + hf * 32 + l0) / 4);
-    const uint32_t lmask = (g >= 2) ? 0x00f000f0u : 0x000f000fu;
-    const uint32_t hmask = (g >= 2) ? 0x03000300u : 0x00300030u;
-    const int hs = 4 - 2 * (g & 1);
-    auto q6 = [&](uint32_t lv, uint32_t hv) -> uint32_t { return (lv & lmask) | M | ((hv << hs) & hmask); };
-    const f16x2 off = splat((g >= 2) ? (f16)-1536.0f : (f16)-1056.0f);
-    f16x2 w0 = (as_f16x2(q6(l.x, h.x)) + off) * scale;
-    f16x2 w1 = (as_f16x2(q6(l.x >> 8, h.x >> 8)) + off) * scale;
-    f16x2 w2 = (as_f16x2(q6(l.y, h.y)) + off) * scale;
-    f16x2 w3 = (as_f16x2(q6(l.y >> 8, h.y >> 8)) + off) * scale;
     (void)negmin;
-    f16x8 r = {w0.x, w0.y, w1.x, w1.y, w2.x, w2.y, w3.x, w3.y};
-    return r;
+    return q6k_frag(l, h, t, scale);
   }
 }
 
@@ -747,10 +753,33 @@ SK_DEV void lds_scales(const uint32_t *row, uint32_t hh, StageScales<TYPE> &o) {
 // Per-lane state of the direct-to-LDS tile: buffer resources, this lane's load offsets
 // (activation pieces, weight pieces) and its read swizzles.
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Weight stage layout of the direct-to-LDS tile (byte offsets in one stage buffer; each
+// region is whole 1 KiB blocks, loaded block by block, one 16 B piece per lane):
+//   Q4_K, 18 blocks: qs rows (128 B) at 128 r, headers (16 B) at 16384 + 16 r
+//   Q6_K, 28 blocks: ql rows (128 B) at 128 r, qh rows (64 B) at 16384 + 64 r, scales (16 B)
+//                    at 24576 + 16 r, and at 26624 + 16 r the 16 B-aligned 16 B that hold the
+//                    row's d (at byte dpos: regions and buffers are 16 B-aligned, so those
+//                    16 B lie inside the buffer)
+template <int TYPE>
+constexpr uint32_t dl_wblocks() {
+  return TYPE == 1 ? 18 : 28;
+}
+// 16 B unit slot swizzle of a 64 B qh row (4 units): distinct banks for 8 consecutive rows
+SK_DEV uint32_t dl_swz4(uint32_t r) { return (r >> 1) & 3u; }
+
+// Per-lane state of the direct-to-LDS tile: buffer resources, this lane's load offsets for
+// its activation blocks (wave + NW i) and weight blocks (the same), the bytes a weight
+// block's source moves per super-block, and the read swizzles.
+template <int NW, int TYPE>
 struct DLLanes {
-  u32x4 xres, wres;
-  uint32_t xo[4], wo[5];
-  uint32_t wv, lane, lrow, hh, wsw, xsw;
+  static constexpr int XS = 16 / NW;                                    // activation blocks per wave
+  static constexpr int WS = (dl_wblocks<TYPE>() + NW - 1) / NW;          // weight block slots per wave
+  static constexpr int WMIN = dl_wblocks<TYPE>() / NW;                   // weight loads of every wave
+  u32x4 xres, wres, dres;
+  uint32_t xo[XS], wo[WS], wm[WS];
+  uint32_t wv, lane, lrow, hh, tb, wsw, wsw4, xsw;
+  uint32_t dpos0;  // Q6_K: byte offset of this lane's row's d at super-block 0
 };
 
 // Buffer resource words over [base, base + bytes) (as buf_res builds them: stride 0, raw
@@ -781,36 +810,70 @@ SK_DEV void dl_load16(const u32x4 &res, uint32_t lds, uint32_t voff, uint32_t so
 #pragma clang diagnostic pop
 SK_DEV uint32_t lds_addr(const void *p) { return (uint32_t)(uintptr_t)(dl_lds *)p; }
 
-// A 64-k activation chunk (at k) into buffer dst: blocks 4 i + wave, 1 KiB each.
-SK_DEV void dl_issue_x(const DLLanes &L, f16 *__restrict__ dst, uint32_t k) {
-#pragma unroll
-  for (int i = 0; i < 4; i++) dl_load16(L.xres, lds_addr(dst + (4 * i + L.wv) * 512), L.xo[i], 2u * k);
+// Source of weight block b for this lane: byte offset (super-block 0) and bytes per
+// super-block, with rows past n_out clamped to the last row.
+template <int TYPE>
+SK_DEV void dl_wpiece(uint32_t b, uint32_t lane, const MatmulPush &p, uint32_t row0, uint32_t &off, uint32_t &per) {
+  const uint32_t supers = p.n_in >> 8, last = p.n_out - 1;
+  auto R = [&](uint32_t r) { return min(row0 + r, last); };
+  if (b < 16) {  // qs / ql: 8 rows, lane = 8 r + unit slot
+    const uint32_t r = 8 * b + (lane >> 3);
+    off = 16u * (p.o0 + R(r) * supers * 8 + ((lane & 7) ^ dl_swz(r)));
+    per = 128;
+  } else if (TYPE == 1) {  // headers: 64 rows
+    off = 16u * (p.o1 + R(64 * (b - 16) + lane) * supers);
+    per = 16;
+  } else if (b < 24) {  // qh: 16 rows, lane = 4 r + unit slot
+    const uint32_t r = 16 * (b - 16) + (lane >> 2);
+    off = 16u * (p.o1 + R(r) * supers * 4 + ((lane & 3) ^ dl_swz4(r)));
+    per = 64;
+  } else if (b < 26) {  // scales: 64 rows
+    off = 16u * (p.o2 + R(64 * (b - 24) + lane) * supers);
+    per = 16;
+  } else {  // d: 64 rows (the 16 B-aligned piece that holds d: see dl_issue_w)
+    off = 2u * (p.o3 + R(64 * (b - 26) + lane) * supers);
+    per = 2;
+  }
 }
-// The Q4_K weights of super-block sb into buffer dst: qs blocks 4 i + wave, header blocks
-// 16 + wave (waves 0 and 1).
-SK_DEV void dl_issue_w(const DLLanes &L, uint32_t *__restrict__ dst, uint32_t sb) {
+
+// A 64-k activation chunk (at k) into buffer dst.
+template <int NW, int TYPE>
+SK_DEV void dl_issue_x(const DLLanes<NW, TYPE> &L, f16 *__restrict__ dst, uint32_t k) {
 #pragma unroll
-  for (int i = 0; i < 4; i++) dl_load16(L.wres, lds_addr(dst + (4 * i + L.wv) * 256), L.wo[i], 128u * sb);
-  if (L.wv < 2) dl_load16(L.wres, lds_addr(dst + (16 + L.wv) * 256), L.wo[4], 16u * sb);
+  for (int i = 0; i < L.XS; i++) dl_load16(L.xres, lds_addr(dst + (NW * i + L.wv) * 512), L.xo[i], 2u * k);
+}
+// The weights of super-block sb into buffer dst.
+template <int NW, int TYPE>
+SK_DEV void dl_issue_w(const DLLanes<NW, TYPE> &L, uint32_t *__restrict__ dst, uint32_t sb) {
+#pragma unroll
+  for (int i = 0; i < L.WS; i++) {
+    const uint32_t b = NW * i + L.wv;
+    if (i < L.WMIN || b < dl_wblocks<TYPE>()) {
+      if (TYPE == 2 && b >= 26)  // d: 2 B-aligned, so the piece is the aligned 16 B around it
+        dl_load16(L.dres, lds_addr(dst + b * 256), (L.wo[i] + 2u * sb) & ~15u, 0);
+      else
+        dl_load16(L.wres, lds_addr(dst + b * 256), L.wo[i], L.wm[i] * sb);
+    }
+  }
 }
 
 // One 256-k stage of the direct-to-LDS tile: four 64-k chunks alternating between the
 // activation buffers x0 (chunks 0, 2) and x1 (1, 3), weights in wc; the loads of the next
 // chunk go to the other activation buffer, and at chunk 0 (when `more`) the next stage's
-// weights (super-block nsb) go to wn.  Every buffer is its own restrict pointer, so the
-// compiler sees that reading one buffer need not wait for the loads into another; the
-// waits that order the loads before the reads are the explicit ones here.
-template <int NB>
-SK_DEV void dl_stage(const DLLanes &L, f32x16 (&acc)[NB], f16 *__restrict__ x0, f16 *__restrict__ x1,
+// weights (super-block nsb) go to wn.  The waits that order a buffer's loads before its
+// reads are the explicit ones here (the loads are assembly the compiler does not count).
+template <int NW, int TYPE, int NB>
+SK_DEV void dl_stage(const DLLanes<NW, TYPE> &L, f32x16 (&acc)[NB], f16 *__restrict__ x0, f16 *__restrict__ x1,
                      const uint32_t *__restrict__ wc, uint32_t *__restrict__ wn, bool more, uint32_t k0,
                      uint32_t nsb) {
-  StageScales<1> ss;
+  // (wc holds super-block nsb - 1)
+  StageScales<TYPE> ss;
 #pragma unroll
   for (int c4 = 0; c4 < KC / DL_KX; c4++) {
     // this wave's loads of chunk c4 (and, at c4 = 0, of the stage's weights) are in LDS; at
     // c4 = 1 the next stage's weight loads, issued after the chunk's, may stay in flight
     if (c4 == 1 && more)
-      dl_wait_vm<4>();
+      dl_wait_vm<DLLanes<NW, TYPE>::WMIN>();
     else
       dl_wait_vm<0>();
     __syncthreads();
@@ -821,20 +884,36 @@ SK_DEV void dl_stage(const DLLanes &L, f32x16 (&acc)[NB], f16 *__restrict__ x0, 
     if (c4 == 0) {
       __builtin_amdgcn_sched_barrier(0);  // the weight loads stay behind the chunk's
       if (more) dl_issue_w(L, wn, nsb);
-      WStage<1> hs;
-      hs.hd = *(const uint4 *)(wc + 4096 + 4 * L.lrow);
-      stage_scales<1>(hs, L.hh, ss);
+      WStage<TYPE> hs;
+      if constexpr (TYPE == 1) {
+        hs.hd = *(const uint4 *)(wc + 4096 + 4 * L.lrow);
+      } else {
+        hs.sc = *(const uint4 *)(wc + 6144 + 4 * L.lrow);
+        const uint32_t pos = (L.dpos0 + 2u * (nsb - 1)) & 15u;  // d's byte in its 16 B
+        const uint4 dq = *(const uint4 *)(wc + 6656 + 4 * L.lrow);
+        const uint32_t dw = pos < 8 ? (pos < 4 ? dq.x : dq.y) : (pos < 12 ? dq.z : dq.w);
+        hs.d = (dw >> (8 * (pos & 2))) & 0xffffu;
+      }
+      stage_scales<TYPE>(hs, L.hh, ss);
     }
     const f16 *xb = (c4 & 1) ? x1 : x0;
     f16x8 xf0[NB], xf1[NB], wf0, wf1;
     auto frags = [&](int ts, f16x8(&xf)[NB], f16x8 &wf) {
-      const int t = 4 * c4 + ts;  // chunk c4 holds steps 4 c4 .. 4 c4 + 3 (koff: 32 hh + 8 ts)
+      const int t = 4 * c4 + ts;  // chunk c4 holds steps 4 c4 .. 4 c4 + 3 (their koff lie in it)
       f16x2 sc, nm;
       ss.get(t, sc, nm);
-      wf = q4k_frag(*(const uint2 *)(wc + L.lrow * 32 + 4 * ((t >> 1) ^ L.wsw) + 2 * (t & 1)), L.hh, sc, nm);
-      const uint32_t xu = (4 * L.hh + ts) ^ L.xsw;
+      if constexpr (TYPE == 1) {
+        wf = q4k_frag(*(const uint2 *)(wc + L.lrow * 32 + 4 * ((t >> 1) ^ L.wsw) + 2 * (t & 1)), L.hh, sc, nm);
+      } else {  // ql unit 4 hf + 2 (g & 1) + (t & 1), qh unit 2 hf + (t & 1); lane half hh: bytes 8 hh..
+        const int hf = t >> 3, g = (t >> 1) & 3;
+        const uint2 l = *(const uint2 *)(wc + L.lrow * 32 + 4 * ((4 * hf + 2 * (g & 1) + (t & 1)) ^ L.wsw) + 2 * L.hh);
+        const uint2 h = *(const uint2 *)(wc + 4096 + L.lrow * 16 + 4 * ((2 * hf + (t & 1)) ^ L.wsw4) + 2 * L.hh);
+        wf = q6k_frag(l, h, t, sc);
+      }
+      const uint32_t xu = ((koff<TYPE>(t, L.hh) - DL_KX * c4) >> 3) ^ L.xsw;
 #pragma unroll
-      for (int j = 0; j < NB; j++) xf[j] = *(const f16x8 *)(xb + (32 * j + (L.lane & 31)) * DL_KX + 8 * xu);
+      for (int j = 0; j < NB; j++)
+        xf[j] = *(const f16x8 *)(xb + (32 * (L.tb + j) + (L.lane & 31)) * DL_KX + 8 * xu);
     };
     frags(0, xf0, wf0);
 #pragma unroll
@@ -861,15 +940,15 @@ SK_DEV void matmul_tile128_w(const uint4 *__restrict__ w, const uint16_t *__rest
                              uint32_t *cnt = nullptr, uint32_t S = 1, uint32_t hf = 0, uint32_t hz = 1,
                              const SG &segs = SG{}) {
   static_assert(NW == 4 || TN == TN2, "eight waves split a 128-token tile");
-  // XHALF = 3: the f16 rows of x_half_rows and the Q4_K weights loaded straight into LDS
+  // XHALF = 3: the f16 rows of x_half_rows and the K-quant weights loaded straight into LDS
   constexpr bool DL = XHALF == 3;
-  static_assert(!DL || (TYPE == 1 && NW == 4 && TN == TN2 && !MOE && !SEG), "direct-to-LDS form");
+  static_assert(!DL || (TYPE != 0 && TN == TN2 && !MOE), "direct-to-LDS form");
   constexpr int NT = 64 * NW;
   constexpr int NB = NW == 8 ? 2 : TN / 32;  // 32-token blocks per wave
   constexpr int KX = DL ? DL_KX : (NW == 8 || TN < TN2) ? KX_W : 128, PITCH2 = pitch2<KX>();
   constexpr uint32_t PW = WLds<TYPE, NT>::PW;
   __shared__ __attribute__((aligned(16))) f16 xs[DL ? 2 * TN * DL_KX : TN * PITCH2];
-  __shared__ __attribute__((aligned(16))) uint32_t wl[DL ? 2 * DL_WBYTES / 4 : TM * PW / 4];
+  __shared__ __attribute__((aligned(16))) uint32_t wl[DL ? 2 * 256 * dl_wblocks<TYPE>() : TM * PW / 4];
   __shared__ uint32_t xrow[TN];
   __shared__ uint32_t yrow[TN];
   __shared__ int xexp[TN];
@@ -953,37 +1032,43 @@ SK_DEV void matmul_tile128_w(const uint4 *__restrict__ w, const uint16_t *__rest
   if constexpr (DL) {
     // Every operand byte goes from global memory straight into LDS (buffer loads with the
     // LDS bit), double buffered: 64-k activation chunks (128 tokens x 128 B) and 256-k
-    // weight stages (128 rows x 128 B of qs, then the rows' 16 B headers).  One
-    // wave-instruction fills 1 KiB, lane l the 16 B at 16 l, so rows are unpadded and their
-    // 16 B units are stored XOR-swizzled by dl_swz(row).  One barrier per chunk: after it,
-    // chunk c + 1 loads into the other activation buffer (last read in chunk c - 1) and, at a
-    // stage's first chunk, the next stage's weights into the other weight buffer (last read
-    // in the stage before).  vmcnt counts a wave's loads in issue order, so before each
-    // barrier a wave waits for its loads of the chunk to come, letting only the weight loads
-    // issued after them stay in flight.
-    constexpr uint32_t XB = TN * DL_KX, WB = DL_WBYTES / 4;
-    const uint32_t wv = __builtin_amdgcn_readfirstlane(wave);
-    const uint32_t units = p.n_in >> 5, supers = p.n_in >> 8;
+    // weight stages (the layout at dl_wblocks).  One wave-instruction fills 1 KiB, lane l the
+    // 16 B at 16 l, so rows are unpadded and their 16 B units are stored XOR-swizzled.  One
+    // barrier per chunk: after it, chunk c + 1 loads into the other activation buffer (last
+    // read in chunk c - 1) and, at a stage's first chunk, the next stage's weights into the
+    // other weight buffer (last read in the stage before).  vmcnt counts a wave's loads in
+    // issue order, so before each barrier a wave waits for its loads of the chunk, letting
+    // only the weight loads issued after them stay in flight.
+    constexpr uint32_t XB = TN * DL_KX, WB = 256 * dl_wblocks<TYPE>();
+    using DL_L = DLLanes<NW, TYPE>;
+    DL_L L;
+    L.wv = __builtin_amdgcn_readfirstlane(wave);
+    L.lane = lane;
+    L.lrow = lrow;
+    L.hh = hh;
+    L.tb = tb;
+    L.wsw = dl_swz(lrow);
+    L.wsw4 = dl_swz4(lrow);
+    L.xsw = dl_swz(lane & 31);
     __syncthreads();  // xrow
-    const u32x4 xres = dl_res(x, 2ull * ((uint64_t)p.x_off + (uint64_t)n_all * p.x_stride));
-    const u32x4 wres = dl_res(w, 0xffffffffull);
-    uint32_t xo[4], wo[5];
+    L.xres = dl_res(x, 2ull * ((uint64_t)p.x_off + (uint64_t)n_all * p.x_stride));
+    L.wres = dl_res(w, 0xffffffffull);
+    // d pieces: the 16 B-aligned 16 B around each d, to the end of the d region's last 16 B
+    L.dres = dl_res(wd, (2ull * ((uint64_t)p.o3 + (uint64_t)p.n_out * (p.n_in >> 8)) + 15) & ~15ull);
+    L.dpos0 = 2u * (p.o3 + min(row0 + lrow, p.n_out - 1) * (p.n_in >> 8));
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const uint32_t r = 8 * (4 * i + wv) + (lane >> 3), slot = lane & 7;  // token / local row
-      xo[i] = 2u * (p.x_off + xrow[r] * p.x_stride + 8u * (slot ^ dl_swz(r)));
-      wo[i] = 16u * (p.o0 + min(row0 + r, p.n_out - 1) * units + (slot ^ dl_swz(r)));
+    for (int i = 0; i < DL_L::XS; i++) {
+      const uint32_t r = 8 * (NW * i + L.wv) + (lane >> 3);  // token
+      L.xo[i] = 2u * (p.x_off + xrow[r] * p.x_stride + 8u * ((lane & 7) ^ dl_swz(r)));
     }
-    wo[4] = 16u * (p.o1 + min(row0 + 64 * (wv & 1) + lane, p.n_out - 1) * supers);
-    const uint32_t wsw = dl_swz(lrow), xsw = dl_swz(lane & 31);
-    DLLanes L{xres, wres, {xo[0], xo[1], xo[2], xo[3]}, {wo[0], wo[1], wo[2], wo[3], wo[4]}, wv, lane, lrow, hh, wsw,
-              xsw};
+#pragma unroll
+    for (int i = 0; i < DL_L::WS; i++) dl_wpiece<TYPE>(NW * i + L.wv, lane, p, row0, L.wo[i], L.wm[i]);
     dl_issue_x(L, xs, kbase);
     dl_issue_w(L, wl, st0);
     for (uint32_t st = 0; st < n_stage; st++) {
       const uint32_t b = st & 1;
-      dl_stage<NB>(L, acc, xs, xs + XB, wl + b * WB, wl + (b ^ 1) * WB, st + 1 < n_stage, kbase + KC * st,
-                   st0 + st + 1);
+      dl_stage<NW, TYPE, NB>(L, acc, xs, xs + XB, wl + b * WB, wl + (b ^ 1) * WB, st + 1 < n_stage,
+                             kbase + KC * st, st0 + st + 1);
     }
   } else {
   WLds<TYPE, NT> wr;
@@ -1382,7 +1467,8 @@ MMH4B(2, 0)
 MMH4B(2, 1)
 
 // The four-wave Q4_K tile with activations and weights loaded straight into LDS (XHALF 3),
-// on a plain grid (x4d) and on the balanced grid (x4db).
+// on a plain grid (x4d) and on the balanced grid (x4db).  (Q6_K's 28 KiB weight stages,
+// double buffered, would leave one four-wave workgroup per CU: it keeps the x4 tiles.)
 #define MMH4D(A)                                                                                  \
   extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void       \
       matmul_x4d__1_##A(                                                                          \
@@ -1398,6 +1484,24 @@ MMH4B(2, 1)
   }
 MMH4D(0)
 MMH4D(1)
+
+// The eight-wave tile with operands loaded straight into LDS: K-split launches (x8d) and
+// segments (x8ds), Q4_K and Q6_K.
+#define MMH8D(T, A)                                                                               \
+  extern "C" __global__ __launch_bounds__(512) void matmul_x8d__##T##_##A(                         \
+      const uint4 *w, const uint16_t *wd, const f16 *x, float *y, const uint32_t *ctl,            \
+      MatmulPush p, float *ws, uint32_t *cnt, uint32_t S) {                                       \
+    matmul_tile128_w<T, A, 3, 8>(w, wd, x, y, ctl, p, ws, cnt, S);                                \
+  }                                                                                               \
+  extern "C" __global__ __launch_bounds__(512) void matmul_x8ds__##T##_##A(                        \
+      const uint4 *w, const uint16_t *wd, const f16 *x, float *y, const uint32_t *ctl,            \
+      Segments<MatmulPush> m, float *ws, uint32_t *cnt, uint32_t S) {                              \
+    matmul_tile128_w<T, A, 3, 8, TN2, 0, 0, 1>(w, wd, x, y, ctl, m.p[0], ws, cnt, S, 0, 1, m);     \
+  }
+MMH8D(1, 0)
+MMH8D(1, 1)
+MMH8D(2, 0)
+MMH8D(2, 1)
 
 // The eight-wave tile on f16 rows over up to four matrices that read the same rows
 // (segment table as the matvecs take it; start[] counts row tiles).

@@ -1343,17 +1343,18 @@ int skyla_hip_pipeline_new(skyla_hip_context *ctx, const char *name, uint32_t n_
       p->split_fn = find_function(ctx, ssym);
       p->split_threads = 512;
     }
-    // f32 inputs: the tile on x_half_rows's f16 rows (build_launches inserts the prepass).
-    // Q4_K takes the four-wave tile whose operands go straight into LDS (x4d / x4db);
-    // SKYLA_HIP_X4D=0 keeps the register-staged one.
+    // f32 inputs: the tile on x_half_rows's f16 rows (build_launches inserts the prepass),
+    // by default the forms whose operands go straight into LDS (eight waves: x8d, x8ds; four
+    // waves, Q4_K only: x4d, x4db); SKYLA_HIP_DL=0 keeps the register-staged tiles.
     if (!(n_spec == 4 && spec[3])) {
-      const char *denv = std::getenv("SKYLA_HIP_X4D");
-      const bool dl = spec[0] == 1 && !(denv && denv[0] == '0');
+      const char *denv = std::getenv("SKYLA_HIP_DL");
+      const bool dl = !(denv && denv[0] == '0');
+      const bool dl4 = dl && spec[0] == 1;
       const std::string ts = std::to_string(spec[0]) + "_" + std::to_string(spec[1]);
-      p->hx_fn = find_function(ctx, "matmul_x8__" + ts);
-      p->hx4_fn = find_function(ctx, (dl ? "matmul_x4d__" : "matmul_x4__") + ts);
-      p->hx4b_fn = find_function(ctx, (dl ? "matmul_x4db__" : "matmul_x4b__") + ts);
-      p->hxs_fn = find_function(ctx, "matmul_x8s__" + std::to_string(spec[0]) + "_" + std::to_string(spec[1]));
+      p->hx_fn = find_function(ctx, (dl ? "matmul_x8d__" : "matmul_x8__") + ts);
+      p->hx4_fn = find_function(ctx, (dl4 ? "matmul_x4d__" : "matmul_x4__") + ts);
+      p->hx4b_fn = find_function(ctx, (dl4 ? "matmul_x4db__" : "matmul_x4b__") + ts);
+      p->hxs_fn = find_function(ctx, (dl ? "matmul_x8ds__" : "matmul_x8s__") + ts);
       p->split_threads = 512;
     }
   }

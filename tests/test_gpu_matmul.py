@@ -100,8 +100,8 @@ def test_matmul_f16_prepass_same_bits(ctx, name, dtype, n_in, n_out, n_tok, accu
     against the eight-wave tile's own f32 staging (SKYLA_HIP_XHALF=0): the same bits while
     no activation reaches 2^15, K split or not, ACCUM or not, ragged rows and token counts.
     Q4_K launches of more than 128 tiles (gate, ragged4) run the four-wave tile with its
-    operands loaded straight into LDS, or with SKYLA_HIP_X4D=0 the register-staged one."""
-    with env(SKYLA_HIP_XHALF=4, SKYLA_HIP_X4D=x4d):
+    operands loaded straight into LDS, or with SKYLA_HIP_DL=0 the register-staged one."""
+    with env(SKYLA_HIP_XHALF=4, SKYLA_HIP_DL=x4d):
         got1, want = _run(ctx, dtype, n_in, n_out, n_tok, accum=accum, tag="mm-xh")
     with env(SKYLA_HIP_XHALF=0):
         got0, _ = _run(ctx, dtype, n_in, n_out, n_tok, accum=accum, tag="mm-xh")
@@ -158,9 +158,9 @@ def test_matmul_balanced_grid(ctx, name, dtype, n_in, n_out, n_tok, accum, x4d):
     grid, SKYLA_HIP_XHALF=4) and the rest in two K halves added in order (within f32
     reordering of the plain grid), against the oracle at the bar; ACCUM, ragged rows and
     tokens."""
-    with env(SKYLA_HIP_X4D=x4d):
+    with env(SKYLA_HIP_DL=x4d):
         got, want = _run(ctx, dtype, n_in, n_out, n_tok, accum=accum, tag="mm-bal")
-    with env(SKYLA_HIP_XHALF=4, SKYLA_HIP_X4D=x4d):
+    with env(SKYLA_HIP_XHALF=4, SKYLA_HIP_DL=x4d):
         plain, _ = _run(ctx, dtype, n_in, n_out, n_tok, accum=accum, tag="mm-bal")
     hz = -(-n_tok // E.MATMUL_TILE_COLS)
     tiles = -(-n_out // 128) * hz
