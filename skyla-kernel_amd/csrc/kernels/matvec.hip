@@ -65,16 +65,29 @@ struct MatvecPush4F {
   float eps;
 };
 
+// The old outputs of an accumulating launch (lane 0 of each row group, the lane that stores
+// them), read at entry next to the first loads: the store at the end then adds without
+// waiting for a load (the same y + total).
+template <int ACCUM, int ROWS>
+SK_DEV void load_old(const float *y, uint32_t y_off, uint32_t first, uint32_t n_out, uint32_t lane,
+                     float (&old)[ROWS]) {
+#pragma unroll
+  for (int r = 0; r < ROWS; r++) {
+    old[r] = 0.0f;
+    if (ACCUM && lane == 0 && first + r < n_out) old[r] = y[y_off + first + r];
+  }
+}
+
 template <int ACCUM, int ROWS, int LPR>
 SK_DEV void store_rows(float *y, uint32_t y_off, uint32_t first, uint32_t n_out, uint32_t lane,
-                       const float (&acc)[ROWS]) {
+                       const float (&acc)[ROWS], const float (&old)[ROWS]) {
 #pragma unroll
   for (int r = 0; r < ROWS; r++) {
     const float total = lane_sum<LPR>(acc[r]);
     const uint32_t row = first + r;
     if (lane == 0 && row < n_out) {
       if (ACCUM)
-        y[y_off + row] += total;
+        y[y_off + row] = old[r] + total;
       else
         y[y_off + row] = total;
     }
@@ -218,6 +231,8 @@ SK_DEV void matvec_q4k_body(const uint4 *__restrict__ w, const float *x, float *
   float acc[ROWS];
 #pragma unroll
   for (int r = 0; r < ROWS; r++) acc[r] = 0.0f;
+  float yold[ROWS];
+  load_old<ACCUM, ROWS>(y, y_off, first, p.n_out, lane, yold);
 
   for (uint32_t k0 = 0; k0 < p.n_in; k0 += CHU * 32) {
     const uint32_t nk = min(p.n_in - k0, (uint32_t)CHU * 32);
@@ -387,7 +402,7 @@ SK_DEV void matvec_q4k_body(const uint4 *__restrict__ w, const float *x, float *
     }
     if (tid == 0) __hip_atomic_store(&cnt[bx], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   } else {
-    store_rows<ACCUM, ROWS, LPR>(y, y_off, first, p.n_out, lane, acc);
+    store_rows<ACCUM, ROWS, LPR>(y, y_off, first, p.n_out, lane, acc, yold);
   }
 }
 
@@ -470,6 +485,10 @@ SK_DEV void matvec_q4k_ks_body(const uint4 *__restrict__ w, const float *x, floa
   }
   uint4 qc[RPL], hc;
   load_group(0, qc, hc);
+  // an accumulating launch reads its old outputs now, so the store at the end waits for none
+  float yold = 0.0f;
+  if constexpr (ACCUM && !PAIR)
+    if (tid < (uint32_t)OUT && out0 + tid < p.n_out) yold = y[p.y_off + out0 + tid];
   if constexpr (NORM) {  // x * w (the norm weights sit at aux_off), and sum(x^2)
     const float *wn = x + p.aux_off;
     float sq = 0.0f;
@@ -544,7 +563,7 @@ SK_DEV void matvec_q4k_ks_body(const uint4 *__restrict__ w, const float *x, floa
 #pragma clang fp contract(off)
       y[yo] = t / (1.0f + expf(-t)) * u;  // silu_mul.comp:15-23
     } else if (ACCUM) {
-      y[yo] += t;
+      y[yo] = yold + t;
     } else {
       y[yo] = t;
     }
@@ -894,6 +913,8 @@ SK_DEV void matvec_q6k_body(const uint4 *__restrict__ w, const uint16_t *__restr
   float acc[ROWS];
 #pragma unroll
   for (int r = 0; r < ROWS; r++) acc[r] = 0.0f;
+  float yold[ROWS];
+  load_old<ACCUM, ROWS>(y, y_off, first, p.n_out, lane, yold);
 
   for (uint32_t k0 = 0; k0 < p.n_in; k0 += G::CH) {
     const uint32_t nk = min(p.n_in - k0, (uint32_t)G::CH);
@@ -1023,7 +1044,7 @@ SK_DEV void matvec_q6k_body(const uint4 *__restrict__ w, const uint16_t *__restr
     }
   }
   norm_apply<MODE>(acc, ss, p);
-  store_rows<ACCUM, ROWS, LPR>(y, y_off, first, p.n_out, lane, acc);
+  store_rows<ACCUM, ROWS, LPR>(y, y_off, first, p.n_out, lane, acc, yold);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -1080,6 +1101,10 @@ SK_DEV void matvec_q6k_ks_body(const uint4 *__restrict__ w, const uint16_t *__re
     for (int k = 0; k < 4; k++) xg[g][k] = *(const float4 *)(xv + 32 * g + 4 * k);
 #pragma unroll
   for (int g = 0; g < PD && g < NG; g++) load_group(g, q[g]);
+  // an accumulating launch reads its old outputs now, so the store at the end waits for none
+  float yold = 0.0f;
+  if constexpr (ACCUM)
+    if (tid < (uint32_t)OUT && out0 + tid < p.n_out) yold = y[p.y_off + out0 + tid];
   float ib[4];
 #pragma unroll
   for (int g = 0; g < 4; g++)
@@ -1127,7 +1152,7 @@ SK_DEV void matvec_q6k_ks_body(const uint4 *__restrict__ w, const uint16_t *__re
     const float t = (part[0][tid] + part[1][tid]) + part[2][tid];
     const uint32_t yo = p.y_off + out0 + tid;
     if (ACCUM)
-      y[yo] += t;
+      y[yo] = yold + t;
     else
       y[yo] = t;
   }
@@ -1182,6 +1207,8 @@ SK_DEV void matvec_q8_0_body(const uint4 *__restrict__ w, const uint16_t *__rest
   float acc[ROWS];
 #pragma unroll
   for (int r = 0; r < ROWS; r++) acc[r] = 0.0f;
+  float yold[ROWS];
+  load_old<ACCUM, ROWS>(y, y_off, first, p.n_out, lane, yold);
 
   for (uint32_t k0 = 0; k0 < p.n_in; k0 += G::CH) {
     const uint32_t nk = min(p.n_in - k0, (uint32_t)G::CH);
@@ -1260,7 +1287,7 @@ SK_DEV void matvec_q8_0_body(const uint4 *__restrict__ w, const uint16_t *__rest
     }
   }
   norm_apply<MODE>(acc, ss, p);
-  store_rows<ACCUM, ROWS, LPR>(y, y_off, first, p.n_out, lane, acc);
+  store_rows<ACCUM, ROWS, LPR>(y, y_off, first, p.n_out, lane, acc, yold);
 }
 
 }  // namespace

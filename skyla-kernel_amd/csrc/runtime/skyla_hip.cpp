@@ -267,12 +267,20 @@ constexpr uint64_t kSplitTileBytes = 128 * 128 * 4;  // one f32 partial tile (ke
 // most 128 tiles of 128 x 128 leave CUs idle (the tile keeps one workgroup per CU), so
 // their super-blocks are split over up to 256 workgroups, keeping at least 4 per split.
 // Measured on MI355X at M = 512: 4096 x 4096 68.6 -> 53.0 us, 4096 x 12288 191.6 -> 119.3 us.
+// Workgroup slots a K split fills (SKYLA_HIP_SPLIT_SLOTS, default 256: one eight-wave
+// workgroup per CU).
+uint64_t split_slots() {
+  const char *e = std::getenv("SKYLA_HIP_SPLIT_SLOTS");
+  const long v = e ? std::atol(e) : 0;
+  return v >= 64 && v <= 2048 ? (uint64_t)v : 256;
+}
+
 uint32_t split_of(const Command &a) {
   if (!a.split_fn || a.push.size() < 7) return 1;
   const uint64_t tiles = (uint64_t)a.groups[0] * a.groups[1] * a.groups[2];
   const uint32_t n_stage = a.push[6] / 256;  // MatmulPush.n_in
   if (tiles == 0 || tiles > 128) return 1;
-  uint32_t S = (uint32_t)(256 / tiles);
+  uint32_t S = (uint32_t)(split_slots() / tiles);
   S = std::min(S, n_stage / 4);
   S = std::min(S, 8u);
   return S < 2 ? 1 : S;
@@ -639,7 +647,7 @@ std::vector<Launch> build_launches(skyla_hip_context *ctx, const std::vector<Com
       }
       if (n_run > 1) {
         const uint64_t tiles = row_tiles * a.groups[2];
-        uint32_t S = (uint32_t)(256 / tiles);  // split_of's rule on the fused tile count
+        uint32_t S = (uint32_t)(split_slots() / tiles);  // split_of's rule on the fused tile count
         S = std::min(std::min(S, a.push[6] / 256 / 4), 8u);
         if (S < 2) S = 1;
         Launch l;
