@@ -765,8 +765,9 @@ template <int TYPE>
 constexpr uint32_t dl_wblocks() {
   return TYPE == 1 ? 18 : 28;
 }
-// 16 B unit slot swizzle of a 64 B qh row (4 units): distinct banks for 8 consecutive rows
-SK_DEV uint32_t dl_swz4(uint32_t r) { return (r >> 1) & 3u; }
+// 16 B unit slot swizzle of a 64 B qh row (4 units): the 8 B reads of 32 rows at one
+// position meet at most twice on a bank (64 or 32 banks)
+SK_DEV uint32_t dl_swz4(uint32_t r) { return ((r >> 1) ^ (r >> 3)) & 3u; }
 
 // Per-lane state of the direct-to-LDS tile: buffer resources, this lane's load offsets for
 // its activation blocks (wave + NW i) and weight blocks (the same), the bytes a weight
