@@ -945,10 +945,13 @@ struct KsRule {
 };
 const KsRule kKsRules[] = {{0, ~uint64_t{0}, 4, 1}};
 const KsRule kKsPairRules[] = {{0, 8191, 4, 1}};
-// the gate/up pair with the FFN norm folded in (MODE 4 of the K-split body), opt-in with
-// SKYLA_HIP_KSGLUN=1: config 5 measured 466 against 505 tok/s at 1k context for the
-// LDS-staged pair form (102 VGPRs with the norm weights held beside x, against 94)
-const KsRule kKsGlunRules[] = {{0, ~uint64_t{0}, 4, 1}};
+// the gate/up pair with the FFN norm folded in (MODE 4 of the K-split body).  Its 102 VGPRs
+// (the norm weights held beside x) leave two 8-wave workgroups per CU, so the shape is the
+// one whose workgroups all fit at once: config 5 at 1k context, device ms per token on one
+// box, (4, 3) 1.854 and (4, 6) 1.855 against 1.877-1.882 for the LDS-staged pair form;
+// (4, 2) 1.883, (8, 1) 1.894, (8, 3) 1.917, and (4, 1) 2.049 and (2, 2) 2.046 (three rounds
+// of workgroups).  SKYLA_HIP_KSGLUN=0 keeps the LDS-staged pair, =R_G forces a shape.
+const KsRule kKsGlunRules[] = {{0, ~uint64_t{0}, 4, 3}};
 // K-split Q6_K form (n_in = 12288; rows per slot, row-groups, row-groups loaded ahead).
 // Config-2 down projection (4096 rows), us per launch over 36 layers on two boxes: (1, 8, 1)
 // 11.75 / 11.89 against 12.25 / 12.48 for the LDS-staged (8, 1, 64); (1, 8, 2) 12.40,
@@ -999,8 +1002,8 @@ void add_ks(skyla_hip_context *ctx, const char *name, const uint32_t *spec, Reti
     ks = "matvec_q4k_ks_norm__0";
   else if (std::strcmp(name, "matvec_q4k_glu") == 0)
     ks = "matvec_q4k_ks_glu__0", pair = true;
-  else if (std::strcmp(name, "matvec_q4k_glun") == 0 && std::getenv("SKYLA_HIP_KSGLUN") &&
-           std::getenv("SKYLA_HIP_KSGLUN")[0] == '1')
+  else if (std::strcmp(name, "matvec_q4k_glun") == 0 &&
+           !(std::getenv("SKYLA_HIP_KSGLUN") && std::getenv("SKYLA_HIP_KSGLUN")[0] == '0'))
     ks = "matvec_q4k_ks_glun__0", pair = true, glun = true;
   else
     return;
@@ -1008,6 +1011,9 @@ void add_ks(skyla_hip_context *ctx, const char *name, const uint32_t *spec, Reti
                             glun ? std::end(kKsGlunRules) : pair ? std::end(kKsPairRules) : std::end(kKsRules));
   uint32_t fr = 0, fg = 0;
   if (env && std::sscanf(env, "%u_%u", &fr, &fg) == 2) rules = {{0, ~uint64_t{0}, fr, fg}};
+  // SKYLA_HIP_KSGLUN=R_G: the norm-folded pair on that shape (sweeps)
+  if (const char *eg = std::getenv("SKYLA_HIP_KSGLUN"); glun && eg && std::sscanf(eg, "%u_%u", &fr, &fg) == 2)
+    rules = {{0, ~uint64_t{0}, fr, fg}};
   std::vector<MatvecAlt> alts;
   for (const KsRule &r : rules) {
     hipFunction_t fn = find_function(ctx, ks + "_" + std::to_string(r.rpl) + "_" + std::to_string(r.ng));

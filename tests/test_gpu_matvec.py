@@ -214,14 +214,16 @@ def test_fused_matvec_forms(ctx, dtype, n_in, n_out, form, retile):
     assert err <= F32, err
 
 
-@pytest.mark.parametrize("ks", ["1", "0"])
+@pytest.mark.parametrize("ks", ["1", "4_1", "0"])
 @pytest.mark.parametrize("big", [False, True])
-@pytest.mark.parametrize("n_in,n_out", [(4096, 12288), (1024, 1536), (2048, 100)])
+@pytest.mark.parametrize("n_in,n_out", [(4096, 12288), (4096, 1000), (1024, 1536), (2048, 100)])
 def test_glu_norm_pair_against_oracle(ctx, n_in, n_out, big, ks):
     """matvec_q4k_glun (the gate/up pair with the FFN RMSNorm folded in, from the raw
     residual) against the oracle's rmsnorm, the two Matrix::matvec and silu * up; `big`
-    puts an eighth of the residual past the f16 range (3e4 to 1e5).  With n_in 4096 and
-    SKYLA_HIP_KSGLUN=1 the runtime runs the K-split pair form, else the LDS-staged one."""
+    puts an eighth of the residual past the f16 range (3e4 to 1e5).  With n_in 4096 the
+    runtime runs the K-split pair form (its default shape, or SKYLA_HIP_KSGLUN=4_1), with
+    SKYLA_HIP_KSGLUN=0 and for other widths the LDS-staged one; n_out 1000 leaves a ragged
+    last workgroup."""
     g = synth.matrix("test-glu", f"gate-{n_in}-{n_out}", E.DType.Q4K, n_in, n_out)
     u = synth.matrix("test-glu", f"up-{n_in}-{n_out}", E.DType.Q4K, n_in, n_out)
     rg = synth.rng("test-glu", f"norm-{n_in}-{big}")
