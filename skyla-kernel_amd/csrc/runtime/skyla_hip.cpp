@@ -952,6 +952,10 @@ const KsRule kKsPairRules[] = {{0, 8191, 4, 1}};
 // (4, 2) 1.883, (8, 1) 1.894, (8, 3) 1.917, and (4, 1) 2.049 and (2, 2) 2.046 (three rounds
 // of workgroups).  SKYLA_HIP_KSGLUN=0 keeps the LDS-staged pair, =R_G forces a shape.
 const KsRule kKsGlunRules[] = {{0, ~uint64_t{0}, 4, 3}};
+// q/k/v with the attention norm folded in (MODE 2, the same 102 VGPRs): config 5 at 1k
+// context, device ms per token on one box, (4, 2) 1.809 against 1.833-1.838 for (4, 1);
+// (8, 1) 1.826, (2, 2) 1.850, (4, 3) 1.849, (2, 1) 1.900.  SKYLA_HIP_KSNORM=R_G forces a shape.
+const KsRule kKsNormRules[] = {{0, ~uint64_t{0}, 4, 2}};
 // K-split Q6_K form (n_in = 12288; rows per slot, row-groups, row-groups loaded ahead).
 // Config-2 down projection (4096 rows), us per launch over 36 layers on two boxes: (1, 8, 1)
 // 11.75 / 11.89 against 12.25 / 12.48 for the LDS-staged (8, 1, 64); (1, 8, 2) 12.40,
@@ -995,11 +999,11 @@ void add_ks(skyla_hip_context *ctx, const char *name, const uint32_t *spec, Reti
     return;
   }
   std::string ks;
-  bool pair = false, glun = false;
+  bool pair = false, glun = false, norm = false;
   if (std::strcmp(name, "matvec_q4k") == 0 && spec[3] == 0)
     ks = "matvec_q4k_ks__" + std::to_string(spec[1]);
   else if (std::strcmp(name, "matvec_q4k_norm") == 0 && spec[1] == 0)
-    ks = "matvec_q4k_ks_norm__0";
+    ks = "matvec_q4k_ks_norm__0", norm = true;
   else if (std::strcmp(name, "matvec_q4k_glu") == 0)
     ks = "matvec_q4k_ks_glu__0", pair = true;
   else if (std::strcmp(name, "matvec_q4k_glun") == 0 &&
@@ -1007,12 +1011,17 @@ void add_ks(skyla_hip_context *ctx, const char *name, const uint32_t *spec, Reti
     ks = "matvec_q4k_ks_glun__0", pair = true, glun = true;
   else
     return;
-  std::vector<KsRule> rules(glun ? std::begin(kKsGlunRules) : pair ? std::begin(kKsPairRules) : std::begin(kKsRules),
-                            glun ? std::end(kKsGlunRules) : pair ? std::end(kKsPairRules) : std::end(kKsRules));
+  std::vector<KsRule> rules(glun ? std::begin(kKsGlunRules) : pair ? std::begin(kKsPairRules)
+                            : norm ? std::begin(kKsNormRules) : std::begin(kKsRules),
+                            glun ? std::end(kKsGlunRules) : pair ? std::end(kKsPairRules)
+                            : norm ? std::end(kKsNormRules) : std::end(kKsRules));
   uint32_t fr = 0, fg = 0;
   if (env && std::sscanf(env, "%u_%u", &fr, &fg) == 2) rules = {{0, ~uint64_t{0}, fr, fg}};
   // SKYLA_HIP_KSGLUN=R_G: the norm-folded pair on that shape (sweeps)
   if (const char *eg = std::getenv("SKYLA_HIP_KSGLUN"); glun && eg && std::sscanf(eg, "%u_%u", &fr, &fg) == 2)
+    rules = {{0, ~uint64_t{0}, fr, fg}};
+  // SKYLA_HIP_KSNORM=R_G: the norm-folded form on that shape (sweeps)
+  if (const char *en = std::getenv("SKYLA_HIP_KSNORM"); norm && en && std::sscanf(en, "%u_%u", &fr, &fg) == 2)
     rules = {{0, ~uint64_t{0}, fr, fg}};
   std::vector<MatvecAlt> alts;
   for (const KsRule &r : rules) {
