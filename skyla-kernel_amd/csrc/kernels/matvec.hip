@@ -1047,6 +1047,96 @@ SK_DEV void matvec_q6k_body(const uint4 *__restrict__ w, const uint16_t *__restr
   store_rows<ACCUM, ROWS, LPR>(y, y_off, first, p.n_out, lane, acc, yold);
 }
 
+// matvec_q4k_ks12_body -- K-split Q4_K rows of n_in = 12288 (matrix.rs matvec over
+// quant.rs:51-70 blocks): lane u = 64 wave + l of the three waves owns chunk c = u % 4 of
+// super-block u / 4 of every row, i.e. values 64 c .. 64 c + 63, the 32 qs bytes 32 c ..
+// 32 c + 31 (low nibbles for the first 32 values, high nibbles for the rest: sub-blocks 2 c
+// and 2 c + 1).  Its 64 activations and their two sums are loaded once, into registers; per
+// row it loads the chunk's qs and its super-block's header (four lanes share one), decodes
+// its two (scale, min) pairs as q4k_scale_min does, and the row's sum meets over the wave
+// with DPP and over the three waves in LDS, in wave order.  RPL rows per row-group, NG
+// row-groups per workgroup, operands loaded PD row-groups ahead.
+template <int ACCUM, int RPL, int NG, int PD>
+SK_DEV void matvec_q4k_ks12_body(const uint4 *__restrict__ w, const float *x, float *y, const MatvecPush2 &p,
+                                 uint32_t bx) {
+  constexpr int OUT = RPL * NG;                     // rows per workgroup
+  constexpr uint32_t SUPERS = 48, UNITS = 384;      // per row (n_in = 12288, checked by the host)
+  __shared__ float part[3][OUT];
+
+  const uint32_t tid = threadIdx.x, wv = tid >> 6, l = tid & 63;
+  const uint32_t u = wv * 64 + l;
+  const uint32_t sb = u >> 2, c = u & 3;
+  const uint32_t LO4 = opaque_mask(0x0f0f0f0fu), HI4 = opaque_mask(0xf0f0f0f0u);
+  const uint32_t out0 = bx * OUT;
+
+  struct RowQ {
+    uint4 a, b, h;
+  };
+  auto load_group = [&](uint32_t g, RowQ (&q)[RPL]) {
+#pragma unroll
+    for (int r = 0; r < RPL; r++) {
+      const uint32_t row = min(out0 + g * RPL + r, p.n_out - 1);
+      q[r].a = w[p.o0 + row * UNITS + sb * 8 + 2 * c];
+      q[r].b = w[p.o0 + row * UNITS + sb * 8 + 2 * c + 1];
+      q[r].h = w[p.o1 + row * SUPERS + sb];
+    }
+  };
+
+  // activations first: values 64 c + [0, 32) (low nibbles) and + [32, 64) (high)
+  const float *xv = x + p.x_off + sb * 256 + 64 * c;
+  float4 xl[2][4], xh[2][4];
+#pragma unroll
+  for (int h = 0; h < 2; h++)
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      xl[h][k] = *(const float4 *)(xv + 16 * h + 4 * k);
+      xh[h][k] = *(const float4 *)(xv + 32 + 16 * h + 4 * k);
+    }
+  RowQ q[NG][RPL];  // row-group g's operands, loaded PD groups ahead of its arithmetic
+#pragma unroll
+  for (int g = 0; g < PD && g < NG; g++) load_group(g, q[g]);
+  // an accumulating launch reads its old outputs now, so the store at the end waits for none
+  float yold = 0.0f;
+  if constexpr (ACCUM)
+    if (tid < (uint32_t)OUT && out0 + tid < p.n_out) yold = y[p.y_off + out0 + tid];
+  const float sl = (sum4(xl[0][0]) + sum4(xl[0][1])) + (sum4(xl[0][2]) + sum4(xl[0][3])) +
+                   ((sum4(xl[1][0]) + sum4(xl[1][1])) + (sum4(xl[1][2]) + sum4(xl[1][3])));
+  const float sh = (sum4(xh[0][0]) + sum4(xh[0][1])) + (sum4(xh[0][2]) + sum4(xh[0][3])) +
+                   ((sum4(xh[1][0]) + sum4(xh[1][1])) + (sum4(xh[1][2]) + sum4(xh[1][3])));
+
+#pragma unroll
+  for (int g = 0; g < NG; g++) {
+    if (g + PD < NG) load_group(g + PD, q[g + PD]);
+    const RowQ (&qc)[RPL] = q[g];
+#pragma unroll
+    for (int r = 0; r < RPL; r++) {
+      float sa = fma_bytes16(qc[r].a, LO4, xl[0], 0.0f);
+      sa = fma_bytes16(qc[r].b, LO4, xl[1], sa);
+      float sb16 = fma_bytes16(qc[r].a, HI4, xh[0], 0.0f);  // 16 q: the 1/16 is in the scale
+      sb16 = fma_bytes16(qc[r].b, HI4, xh[1], sb16);
+      uint32_t sc0, m0, sc1, m1;
+      q4k_scale_min(2 * c, qc[r].h.y, qc[r].h.z, qc[r].h.w, sc0, m0);
+      q4k_scale_min(2 * c + 1, qc[r].h.y, qc[r].h.z, qc[r].h.w, sc1, m1);
+      const float d = f16_bits_to_f32(qc[r].h.x & 0xffffu), dmin = f16_bits_to_f32(qc[r].h.x >> 16);
+      float v = (d * (float)sc0) * sa;
+      v = __builtin_fmaf(d * 0.0625f * (float)sc1, sb16, v);
+      v = __builtin_fmaf(-(dmin * (float)m0), sl, v);
+      v = __builtin_fmaf(-(dmin * (float)m1), sh, v);
+      v = lane_sum<64>(v);
+      if (l == 0) part[wv][g * RPL + r] = v;
+    }
+  }
+  __syncthreads();
+  if (tid < (uint32_t)OUT && out0 + tid < p.n_out) {
+    const float t = (part[0][tid] + part[1][tid]) + part[2][tid];
+    const uint32_t yo = p.y_off + out0 + tid;
+    if (ACCUM)
+      y[yo] = yold + t;
+    else
+      y[yo] = t;
+  }
+}
+
 // ---------------------------------------------------------------------------------------
 // Q6_K, K-split form for n_in = 12288 (the Qwen3-8B down projection).  Three waves split
 // every row the workgroup owns into its 192 units of 64 values: lane l of wave w takes unit
@@ -1456,6 +1546,22 @@ MV_Q4K_KS_ALL(4, 3)
 MV_Q4K_KS_ALL(4, 6)
 MV_Q4K_KS_ALL(8, 1)
 MV_Q4K_KS_ALL(8, 3)
+
+// K-split Q4_K form for n_in = 12288 (matvec_q4k_ks12_body): RPL rows per row-group, NG
+// row-groups per workgroup of three waves, loaded D row-groups ahead
+#define MV_Q4K_KS12(A, R, G, D)                                                              \
+  extern "C" __global__ __launch_bounds__(192) void matvec_q4k_ks12__##A##_##R##_##G##_##D(   \
+      const uint4 *w, const float *x, float *y, const uint32_t *ids, Segments<MatvecPush2> m) { \
+    const uint32_t s = segment_of(m, blockIdx.x);                                             \
+    (void)ids;                                                                                \
+    matvec_q4k_ks12_body<A, R, G, D>(w, x, y, segment_push(m, s), blockIdx.x - m.start[s]);   \
+  }
+#define MV_Q4K_KS12_ALL(R, G, D) MV_Q4K_KS12(0, R, G, D) MV_Q4K_KS12(1, R, G, D)
+MV_Q4K_KS12_ALL(1, 8, 1)
+MV_Q4K_KS12_ALL(1, 8, 2)
+MV_Q4K_KS12_ALL(2, 4, 1)
+MV_Q4K_KS12_ALL(1, 16, 1)
+MV_Q4K_KS12_ALL(2, 8, 1)
 
 // K-split Q6_K form for n_in = 12288 (matvec_q6k_ks_body): RPL rows per row-group, NG
 // row-groups per workgroup of three waves, loaded D row-groups ahead

@@ -962,6 +962,11 @@ const KsRule kKsNormRules[] = {{0, ~uint64_t{0}, 4, 2}};
 // (1, 16, 2) 12.83, (2, 4, 2) 13.89, (8, 1, 1) 14.02, (1, 8, 7) 14.19.  SKYLA_HIP_KS6=R_G_D
 // forces one shape (sweeps); SKYLA_HIP_KS=0 turns it off with the Q4_K forms.
 const std::vector<KsRule> kKs6Rules = {{0, ~uint64_t{0}, 1, 8, 1}};
+// K-split Q4_K form for n_in = 12288 (matvec_q4k_ks12_body: three waves, each lane one
+// 64-value chunk of every row), opt-in with SKYLA_HIP_KS12=R_G_D: config 5 (its odd
+// layers' down projections) measured slower than the LDS-staged form, device ms per token
+// at 1k context 1.839 (1, 8, 1), 1.842 (1, 8, 2), 1.852 (2, 4, 1), 1.866-1.870 (1, 16, 1),
+// (2, 8, 1) against 1.811.
 
 void add_ks(skyla_hip_context *ctx, const char *name, const uint32_t *spec, Retile &t) {
   // SKYLA_HIP_MF=G: plain Q4_K launches with n_in = 4096 on the matrix-core form
@@ -1028,6 +1033,19 @@ void add_ks(skyla_hip_context *ctx, const char *name, const uint32_t *spec, Reti
     hipFunction_t fn = find_function(ctx, ks + "_" + std::to_string(r.rpl) + "_" + std::to_string(r.ng));
     if (!fn) return;  // all or nothing
     alts.push_back({fn, (pair ? 2u : 4u) * r.rpl * r.ng, 512, r.min_rows, 4096, r.max_rows});
+  }
+  uint32_t fd = 0;
+  if (const char *e12 = std::getenv("SKYLA_HIP_KS12");
+      !pair && !norm && e12 && std::sscanf(e12, "%u_%u_%u", &fr, &fg, &fd) == 3) {
+    // plain Q4_K: the n_in = 12288 form beside the 4096 one
+    const KsRule r12[] = {{0, ~uint64_t{0}, fr, fg, fd}};
+    for (const KsRule &r : r12) {
+      const std::string sym = "matvec_q4k_ks12__" + std::to_string(spec[1]) + "_" + std::to_string(r.rpl) + "_" +
+                              std::to_string(r.ng) + "_" + std::to_string(r.pd);
+      hipFunction_t fn = find_function(ctx, sym);
+      if (!fn) return;  // all or nothing
+      alts.push_back({fn, r.rpl * r.ng, 192, r.min_rows, 12288, r.max_rows});
+    }
   }
   t.alts.insert(t.alts.end(), alts.begin(), alts.end());
 }

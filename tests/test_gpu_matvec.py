@@ -396,6 +396,47 @@ def test_ks6_other_widths_keep_their_variant(ctx):
     assert rel_l2(got, want) <= f32_reorder_bar(E.DType.Q6K, data, n_in, n_out, x, want)
 
 
+KS12_SHAPES = ["1_8_1", "1_8_2", "2_4_1", "1_16_1", "2_8_1"]
+
+
+@pytest.mark.parametrize("shape", KS12_SHAPES)
+@pytest.mark.parametrize("accum", [False, True])
+def test_ks12_shapes_against_oracle(ctx, shape, accum):
+    """Every compiled shape of the K-split Q4_K form for n_in = 12288 (SKYLA_HIP_KS12 forces
+    one) over three fused segments whose row counts are not multiples of its workgroup
+    (4096 + 333 + 1), ACCUM on and off, against the oracle at the f32 bar; rows past n_out
+    stay untouched."""
+    n_in, outs = 12288, [4096, 333, 1]
+    datas = [synth.matrix("test-ks12", f"{i}-{n}", E.DType.Q4K, n_in, n) for i, n in enumerate(outs)]
+    x = synth.activations("test-ks12", "x", n_in)
+    with env(SKYLA_HIP_KS12=shape):
+        s = Setup(ctx, [(E.DType.Q4K, n_in, n, d) for n, d in zip(outs, datas)], n_in, max(outs), rows=len(outs))
+    try:
+        y0 = synth.activations("test-ks12", "y0", (len(outs), s.s_out))
+        s.set_x(x)
+        s.set_y(y0)
+
+        def body(r):
+            g = E.Graph(r, s.k, None, None, False)
+            for i, m in enumerate(s.q):
+                g.matvec(m, (s.x_off, 0), (s.y_off + i * s.s_out, 0), accum, False)
+        rec = ctx.record(False, body)
+        try:
+            assert rec.launches() == 1           # the three dispatches run as one launch
+            ctx.replay(rec)
+        finally:
+            rec.free()
+        got = s.y(len(outs), s.s_out)
+    finally:
+        s.free()
+    for i, (n, d) in enumerate(zip(outs, datas)):
+        want = so.matvec(int(E.DType.Q4K), d, n_in, n, x)
+        part = got[i, :n].astype(np.float64) - (y0[i, :n] if accum else 0.0)
+        bar = f32_reorder_bar(E.DType.Q4K, d, n_in, n, x, want) + (4e-7 if accum else 0.0)
+        assert rel_l2(part, want) <= bar, (shape, i, rel_l2(part, want), bar)
+        assert np.array_equal(got[i, n:].view(np.uint32), y0[i, n:].view(np.uint32))
+
+
 @pytest.mark.parametrize("groups", ["1", "2", "4"])
 @pytest.mark.parametrize("accum", [False, True])
 def test_mf_shapes_against_oracle(ctx, groups, accum):
