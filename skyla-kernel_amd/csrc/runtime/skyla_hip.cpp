@@ -943,6 +943,8 @@ struct KsRule {
   uint32_t rpl, ng;
   uint32_t pd = 1;              // Q6_K: row-groups loaded ahead
 };
+// (the launches of at most 8191 rows, q+k+v and o, on their own shape: config-2 step
+// (4, 1) 3387-3397 GB/s, (2, 2) 3336, (2, 1) 3331-3340, (8, 1) 3247 on one box)
 const KsRule kKsRules[] = {{0, ~uint64_t{0}, 4, 1}};
 const KsRule kKsPairRules[] = {{0, 8191, 4, 1}};
 // the gate/up pair with the FFN norm folded in (MODE 4 of the K-split body).  Its 102 VGPRs
