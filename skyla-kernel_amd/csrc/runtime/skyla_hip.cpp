@@ -189,6 +189,8 @@ struct skyla_hip_pipeline {
   hipFunction_t hx_fn = nullptr;         // and its variant on x_half_rows's f16 rows
   hipFunction_t hx4_fn = nullptr;        // the four-wave tile on those rows
   hipFunction_t hx4b_fn = nullptr;       // and over a balanced grid (some tiles in K halves)
+  hipFunction_t hxw_fn = nullptr;        // the 256-row x 64-token tile for K-split launches
+  hipFunction_t hxws_fn = nullptr;       // and for segments
   hipFunction_t hxs_fn = nullptr;        // the eight-wave tile over several matrices (segments)
   uint32_t split_threads = 0;
   hipFunction_t tok_fn = nullptr;        // batched form: a tok_per_wg x tok_per_wg_y block of
@@ -216,6 +218,7 @@ struct Command {
   hipFunction_t split_fn = nullptr;
   uint32_t split_threads = 0;
   hipFunction_t hx_fn = nullptr, hx4_fn = nullptr, hx4b_fn = nullptr, hxs_fn = nullptr;
+  hipFunction_t hxw_fn = nullptr, hxws_fn = nullptr;
   hipFunction_t tok_fn = nullptr;
   uint32_t tok_per_wg = 0, tok_per_wg_y = 0, tok_threads = 0;
   std::string name;                 // the pipeline's shader name
@@ -284,6 +287,16 @@ uint32_t split_of(const Command &a) {
   S = std::min(S, n_stage / 4);
   S = std::min(S, 8u);
   return S < 2 ? 1 : S;
+}
+
+// split_of's rule for the 256-row x 64-token tile: tiles (of that tile) at most 128, S
+// workgroups per tile filling the K-split slots, at least four super-blocks per split, at
+// most eight; 0 when the rule gives no split.
+uint32_t wide_split(uint64_t tiles, uint32_t n_in) {
+  if (tiles == 0 || tiles > 128) return 0;
+  uint32_t S = (uint32_t)(split_slots() / tiles);
+  S = std::min(std::min(S, n_in / 256 / 4), 8u);
+  return S >= 2 ? S : 0;
 }
 
 // The matvec_chain stage (chain_table.h) of a launch of n dispatches of one dense matvec
@@ -646,12 +659,24 @@ std::vector<Launch> build_launches(skyla_hip_context *ctx, const std::vector<Com
         }
       }
       if (n_run > 1) {
-        const uint64_t tiles = row_tiles * a.groups[2];
+        uint64_t tiles = row_tiles * a.groups[2];
         uint32_t S = (uint32_t)(split_slots() / tiles);  // split_of's rule on the fused tile count
         S = std::min(std::min(S, a.push[6] / 256 / 4), 8u);
         if (S < 2) S = 1;
+        // the 256-row x 64-token tile when its split rule splits the run (row tiles of 256)
+        bool wide = false;
+        uint64_t rt256 = 0;
+        for (uint32_t sgi = 0; sgi < n_run; sgi++) rt256 += (cmds[i + sgi].push[7] + 255) / 256;
+        if (a.hxws_fn) {
+          const uint32_t Sw = wide_split(rt256 * a.groups[2] * 2, a.push[6]);
+          if (Sw >= 2) {
+            wide = true;
+            S = Sw;
+            tiles = rt256 * a.groups[2] * 2;
+          }
+        }
         Launch l;
-        l.fn = a.hxs_fn;
+        l.fn = wide ? a.hxws_fn : a.hxs_fn;
         l.threads = 512;
         l.bufs = a.bufs;
         const size_t w = 13;
@@ -666,12 +691,12 @@ std::vector<Launch> build_launches(skyla_hip_context *ctx, const std::vector<Com
             std::copy(c.push.begin(), c.push.end(), dst);
             dst[4] = (uint32_t)(h_off / 2);  // f16 units
             dst[8] = a.push[6];
-            start += c.groups[0];
+            start += wide ? (c.push[7] + 255) / 256 : c.groups[0];
           }
         }
-        l.groups[0] = (uint32_t)row_tiles;
+        l.groups[0] = (uint32_t)(wide ? rt256 : row_tiles);
         l.groups[1] = 1;
-        l.groups[2] = a.groups[2] * S;
+        l.groups[2] = a.groups[2] * (wide ? 2 : 1) * S;
         l.split = S;
         l.n_cnt = S > 1 ? (uint32_t)tiles : 0;
         l.ws_bytes = S > 1 ? tiles * S * kSplitTileBytes : 0;
@@ -709,6 +734,23 @@ std::vector<Launch> build_launches(skyla_hip_context *ctx, const std::vector<Com
           l.extra = {hf, a.groups[2]};
           l.n_cnt = (uint32_t)(tiles - hf);
           l.ws_bytes = (uint64_t)l.n_cnt * 2 * kSplitTileBytes;
+        }
+      }
+      // K-split launches on the 256-row x 64-token tile (when built in: SKYLA_HIP_DL=2) if
+      // its own split rule splits it (M = 512 at the Qwen3-8B shapes: 128 tiles, two K
+      // halves, as the 128 x 128 tile)
+      if (l.split > 1 && a.hxw_fn) {
+        const uint64_t rt = (a.push[7] + 255) / 256, zt = (uint64_t)a.groups[2] * 2;
+        const uint32_t S = wide_split(rt * zt, a.push[6]);
+        if (S >= 2) {
+          l.fn = a.hxw_fn;
+          l.threads = 512;
+          l.groups[0] = (uint32_t)rt;
+          l.groups[1] = 1;
+          l.groups[2] = (uint32_t)(zt * S);
+          l.split = S;
+          l.n_cnt = (uint32_t)(rt * zt);
+          l.ws_bytes = rt * zt * S * kSplitTileBytes;
         }
       }
       if (!l.split) l.split = 1;  // the K-split arguments, unsplit
@@ -1397,6 +1439,15 @@ int skyla_hip_pipeline_new(skyla_hip_context *ctx, const char *name, uint32_t n_
       p->hx_fn = find_function(ctx, (dl ? "matmul_x8d__" : "matmul_x8__") + ts);
       p->hx4_fn = find_function(ctx, (dl4 ? "matmul_x4d__" : "matmul_x4__") + ts);
       p->hx4b_fn = find_function(ctx, (dl4 ? "matmul_x4db__" : "matmul_x4b__") + ts);
+      // the 256-row x 64-token tile for K-split launches, opt-in with SKYLA_HIP_DL=2: each
+      // wave dequantises its own rows, but M = 512 measured q 42.2-42.5 us against
+      // 42.3-42.5 and down (Q6_K) 124.6-124.9 against 113.7-113.8 for the 128 x 128 tile,
+      // and the config-5 512-token prefill 14.7k against 15.0k tok/s
+      const bool dlw = dl && denv && denv[0] == '2';
+      if (dlw) {
+        p->hxw_fn = find_function(ctx, "matmul_x8w__" + ts);
+        p->hxws_fn = find_function(ctx, "matmul_x8ws__" + ts);
+      }
       p->hxs_fn = find_function(ctx, (dl ? "matmul_x8ds__" : "matmul_x8s__") + ts);
       p->split_threads = 512;
     }
@@ -1490,6 +1541,8 @@ int skyla_hip_record_dispatch(skyla_hip_recorder *r, const skyla_hip_pipeline *p
   c.hx_fn = p->hx_fn;
   c.hx4_fn = p->hx4_fn;
   c.hx4b_fn = p->hx4b_fn;
+  c.hxw_fn = p->hxw_fn;
+  c.hxws_fn = p->hxws_fn;
   c.hxs_fn = p->hxs_fn;
   c.split_threads = p->split_threads;
   c.tok_fn = p->tok_fn;
@@ -1739,6 +1792,8 @@ int skyla_hip_time_dispatch(skyla_hip_context *ctx, const skyla_hip_pipeline *p,
   c.hx_fn = p->hx_fn;
   c.hx4_fn = p->hx4_fn;
   c.hx4b_fn = p->hx4b_fn;
+  c.hxw_fn = p->hxw_fn;
+  c.hxws_fn = p->hxws_fn;
   c.hxs_fn = p->hxs_fn;
   c.split_threads = p->split_threads;
   c.tok_fn = p->tok_fn;
@@ -1798,6 +1853,8 @@ int skyla_hip_dispatch_noalloc(skyla_hip_context *ctx, const skyla_hip_pipeline 
   c.hx_fn = p->hx_fn;
   c.hx4_fn = p->hx4_fn;
   c.hx4b_fn = p->hx4b_fn;
+  c.hxw_fn = p->hxw_fn;
+  c.hxws_fn = p->hxws_fn;
   c.hxs_fn = p->hxs_fn;
   c.split_threads = p->split_threads;
   c.tok_fn = p->tok_fn;

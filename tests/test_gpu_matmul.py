@@ -88,7 +88,7 @@ def test_matmul_config3(ctx, name, dtype, n_in, n_out):
     assert err <= TOL and err <= GUARD, err
 
 
-@pytest.mark.parametrize("x4d", ["1", "0"])
+@pytest.mark.parametrize("x4d", ["2", "1", "0"])
 @pytest.mark.parametrize("name,dtype,n_in,n_out,n_tok,accum", [
     ("q", E.DType.Q4K, 4096, 4096, 512, False), ("gate", E.DType.Q4K, 4096, 12288, 512, False),
     ("down", E.DType.Q6K, 12288, 4096, 512, True), ("ragged", E.DType.Q4K, 1024, 200, 37, True),
@@ -100,7 +100,9 @@ def test_matmul_f16_prepass_same_bits(ctx, name, dtype, n_in, n_out, n_tok, accu
     against the eight-wave tile's own f32 staging (SKYLA_HIP_XHALF=0): the same bits while
     no activation reaches 2^15, K split or not, ACCUM or not, ragged rows and token counts.
     Q4_K launches of more than 128 tiles (gate, ragged4) run the four-wave tile with its
-    operands loaded straight into LDS, or with SKYLA_HIP_DL=0 the register-staged one."""
+    operands loaded straight into LDS, or with SKYLA_HIP_DL=0 the register-staged one; the
+    K-split launches (q, down) run the 128 x 128 direct-to-LDS tile (SKYLA_HIP_DL unset or
+    1), the 256-row x 64-token one (=2) or the register-staged one (=0)."""
     with env(SKYLA_HIP_XHALF=4, SKYLA_HIP_DL=x4d):
         got1, want = _run(ctx, dtype, n_in, n_out, n_tok, accum=accum, tag="mm-xh")
     with env(SKYLA_HIP_XHALF=0):
@@ -173,12 +175,13 @@ def test_matmul_balanced_grid(ctx, name, dtype, n_in, n_out, n_tok, accum, x4d):
     assert rel_l2(got, want) <= GUARD
 
 
+@pytest.mark.parametrize("dl", ["1", "2"])
 @pytest.mark.parametrize("n_tok", [128, 100])
-def test_matmul_segments_qkv(ctx, n_tok):
+def test_matmul_segments_qkv(ctx, n_tok, dl):
     """q, k and v of a prefill chunk (Q4_K 4096 -> 4096, 1024, 1024 in one buffer, no barrier
     between them) run as one launch of three segments after the shared f16 row prepass: the
     bits of the three separate launches (SKYLA_HIP_FUSE=0; the same K split here), and each
-    within the bar of the oracle."""
+    within the bar of the oracle; on the 128 x 128 tile and (SKYLA_HIP_DL=2) the 256 x 64 one."""
     n_in = 4096
     outs = [4096, 1024, 1024]
     mats = [(E.DType.Q4K, n_in, n, synth.matrix("mm-seg", f"qkv-{i}-{n}", E.DType.Q4K, n_in, n))
@@ -186,7 +189,7 @@ def test_matmul_segments_qkv(ctx, n_tok):
     x = synth.activations("mm-seg", f"x-{n_tok}", (n_tok, n_in))
     got = {}
     for fuse in ("1", "0"):
-        with env(SKYLA_HIP_FUSE=fuse):
+        with env(SKYLA_HIP_FUSE=fuse, SKYLA_HIP_DL=dl):
             s = Setup(ctx, mats, n_in, max(outs), rows=len(outs) * n_tok)
             try:
                 s.set_x(x)
