@@ -779,7 +779,7 @@ struct DLLanes {
   static constexpr int WS = (dl_wblocks<TYPE, WR>() + NW - 1) / NW;      // weight block slots per wave
   static constexpr int WMIN = dl_wblocks<TYPE, WR>() / NW;               // weight loads of every wave
   static_assert(XS >= 1 && XS * NW * 8 == TN, "whole 1 KiB activation blocks per wave");
-  u32x4 xres, wres, dres;
+  u32x4 xres, wres, dres, nres;  // nres: no bytes (every load past its end reads zeros)
   uint32_t xo[XS], wo[WS], wm[WS];
   uint32_t wv, lane, lrow, hh, tb, wsw, wsw4, xsw;
   uint32_t dpos0;  // Q6_K: byte offset of this lane's row's d at super-block 0
@@ -935,9 +935,120 @@ SK_DEV void dl_stage(const DLLanes<NW, TYPE, TN, WR> &L, f32x16 (&acc)[NB], f16 
   }
 }
 
+// The eight-wave 128 x 128 direct-to-LDS tile with a deeper ring (one workgroup per CU, so
+// the LDS allows it): four activation buffers, chunk c in buffer c % 4, loaded three chunks
+// ahead; three weight buffers, stage s in buffer s % 3, loaded two stages ahead.  Every
+// chunk issues the same loads (past the last chunk or stage they read from nres and write
+// zeros into the buffer they would fill, which nothing reads again; a wave with one weight
+// block fewer than another loads zeros into the spare block `dummy`), so the loads a wave
+// has issued after those of chunk c are the same count at every chunk and each wait is a
+// constant: before the barrier of chunk c (c4 = c % 4) the wave lets the next two chunks'
+// loads stay in flight, and for c4 != 0 also the weight loads issued at the stage's first
+// chunk.  Buffer reuse: chunk c + 3's loads go to the buffer chunk c - 1 used and stage
+// s + 2's to the one stage s - 1 used, both issued after the barrier that every wave
+// reaches only when done with them.
+template <int NW, int TYPE, int NB>
+SK_DEV void dl_run_deep(const DLLanes<NW, TYPE> &L, f32x16 (&acc)[NB], f16 *xs, uint32_t *wl, uint32_t *dummy,
+                        uint32_t n_stage, uint32_t kbase, uint32_t st0) {
+  using DL_L = DLLanes<NW, TYPE>;
+  constexpr uint32_t XB = TN2 * DL_KX, WB = 256 * dl_wblocks<TYPE>(), NA = 4, NWB = 3;
+  const uint32_t n_chunk = (KC / DL_KX) * n_stage;
+  auto issue_x = [&](uint32_t c) {
+    f16 *dst = xs + (c % NA) * XB;
+    const bool live = c < n_chunk;
+#pragma unroll
+    for (int i = 0; i < DL_L::XS; i++)
+      dl_load16(live ? L.xres : L.nres, lds_addr(dst + (NW * i + L.wv) * 512), L.xo[i], 2u * (kbase + DL_KX * c));
+  };
+  auto issue_w = [&](uint32_t s) {
+    uint32_t *dst = wl + (s % NWB) * WB;
+    const bool live = s < n_stage;
+    const uint32_t sb = st0 + s;
+#pragma unroll
+    for (int i = 0; i < DL_L::WS; i++) {
+      const uint32_t b = NW * i + L.wv;
+      if (i < DL_L::WMIN || b < dl_wblocks<TYPE>()) {
+        if (TYPE == 2 && b >= 26)  // d: the aligned 16 B around it (as dl_issue_w)
+          dl_load16(live ? L.dres : L.nres, lds_addr(dst + b * 256), (L.wo[i] + 2u * sb) & ~15u, 0);
+        else
+          dl_load16(live ? L.wres : L.nres, lds_addr(dst + b * 256), L.wo[i], L.wm[i] * sb);
+      } else {
+        dl_load16(L.nres, lds_addr(dummy), 0, 0);
+      }
+    }
+  };
+  issue_w(0);
+  issue_w(1);
+  issue_x(0);
+  issue_x(1);
+  issue_x(2);
+  for (uint32_t st = 0; st < n_stage; st++) {
+    const uint32_t *wc = wl + (st % NWB) * WB;
+    StageScales<TYPE> ss;
+#pragma unroll
+    for (int c4 = 0; c4 < KC / DL_KX; c4++) {
+      const uint32_t c = (KC / DL_KX) * st + c4;
+      if (c4 == 0)
+        dl_wait_vm<2 * DL_L::XS>();
+      else
+        dl_wait_vm<2 * DL_L::XS + DL_L::WS>();
+      __syncthreads();
+      issue_x(c + 3);
+      if (c4 == 0) {
+        __builtin_amdgcn_sched_barrier(0);  // the weight loads stay behind the chunk's
+        issue_w(st + 2);
+        WStage<TYPE> hs;
+        if constexpr (TYPE == 1) {
+          hs.hd = *(const uint4 *)(wc + 4096 + 4 * L.lrow);
+        } else {
+          hs.sc = *(const uint4 *)(wc + 6144 + 4 * L.lrow);
+          const uint32_t pos = (L.dpos0 + 2u * (st0 + st)) & 15u;  // d's byte in its 16 B
+          const uint4 dq = *(const uint4 *)(wc + 6656 + 4 * L.lrow);
+          const uint32_t dw = pos < 8 ? (pos < 4 ? dq.x : dq.y) : (pos < 12 ? dq.z : dq.w);
+          hs.d = (dw >> (8 * (pos & 2))) & 0xffffu;
+        }
+        stage_scales<TYPE>(hs, L.hh, ss);
+      }
+      const f16 *xb = xs + c4 * XB;  // c % 4 == c4
+      f16x8 xf0[NB], xf1[NB], wf0, wf1;
+      auto frags = [&](int ts, f16x8(&xf)[NB], f16x8 &wf) {
+        const int t = 4 * c4 + ts;
+        f16x2 sc, nm;
+        ss.get(t, sc, nm);
+        if constexpr (TYPE == 1) {
+          wf = q4k_frag(*(const uint2 *)(wc + L.lrow * 32 + 4 * ((t >> 1) ^ L.wsw) + 2 * (t & 1)), L.hh, sc, nm);
+        } else {
+          const int hf = t >> 3, g = (t >> 1) & 3;
+          const uint2 l = *(const uint2 *)(wc + L.lrow * 32 + 4 * ((4 * hf + 2 * (g & 1) + (t & 1)) ^ L.wsw) + 2 * L.hh);
+          const uint2 h = *(const uint2 *)(wc + 4096 + L.lrow * 16 + 4 * ((2 * hf + (t & 1)) ^ L.wsw4) + 2 * L.hh);
+          wf = q6k_frag(l, h, t, sc);
+        }
+        const uint32_t xu = ((koff<TYPE>(t, L.hh) - DL_KX * c4) >> 3) ^ L.xsw;
+#pragma unroll
+        for (int j = 0; j < NB; j++)
+          xf[j] = *(const f16x8 *)(xb + (32 * (L.tb + j) + (L.lane & 31)) * DL_KX + 8 * xu);
+      };
+      frags(0, xf0, wf0);
+#pragma unroll
+      for (int ts = 0; ts < 4; ts++) {
+        if (ts + 1 < 4) {
+          if (ts & 1)
+            frags(ts + 1, xf0, wf0);
+          else
+            frags(ts + 1, xf1, wf1);
+        }
+#pragma unroll
+        for (int j = 0; j < NB; j++)
+          acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16((ts & 1) ? xf1[j] : xf0[j], (ts & 1) ? wf1 : wf0, acc[j],
+                                                          0, 0, 0);
+      }
+    }
+  }
+}
+
 struct NoSegments {};
 template <int TYPE, int ACCUM, int XHALF, int NW, int TN = TN2, int MOE = 0, int HYB = 0, int SEG = 0,
-          typename SG = NoSegments, int WR = 1>
+          typename SG = NoSegments, int WR = 1, int DEEP = 0>
 SK_DEV void matmul_tile128_w(const uint4 *__restrict__ w, const uint16_t *__restrict__ wd, const void *x,
                              float *y, const uint32_t *ctl, const MatmulPush &p0, float *ws = nullptr,
                              uint32_t *cnt = nullptr, uint32_t S = 1, uint32_t hf = 0, uint32_t hz = 1,
@@ -948,6 +1059,7 @@ SK_DEV void matmul_tile128_w(const uint4 *__restrict__ w, const uint16_t *__rest
   static_assert(!DL || (TYPE != 0 && TN == TN2 && !MOE) || (WR == 2 && NW == 8 && TN == 64 && !MOE && !HYB),
                 "direct-to-LDS form");
   static_assert(WR == 1 || DL, "the 256-row tile is a direct-to-LDS form");
+  static_assert(!DEEP || (DL && NW == 8 && WR == 1 && TN == TN2), "the deep ring: eight-wave 128 x 128 tile");
   // WR = 2: eight waves of 32 rows x 64 tokens over a 256-row x 64-token tile, so each
   // wave dequantises its own rows (the 128-row eight-wave tile has two waves per row block)
   constexpr bool W2 = NW == 8 && WR == 1;  // two waves per row block
@@ -955,8 +1067,9 @@ SK_DEV void matmul_tile128_w(const uint4 *__restrict__ w, const uint16_t *__rest
   constexpr int NB = W2 ? 2 : TN / 32;  // 32-token blocks per wave
   constexpr int KX = DL ? DL_KX : (NW == 8 || TN < TN2) ? KX_W : 128, PITCH2 = pitch2<KX>();
   constexpr uint32_t PW = WLds<TYPE, NT>::PW;
-  __shared__ __attribute__((aligned(16))) f16 xs[DL ? 2 * TN * DL_KX : TN * PITCH2];
-  __shared__ __attribute__((aligned(16))) uint32_t wl[DL ? 2 * 256 * dl_wblocks<TYPE, WR>() : TM * PW / 4];
+  __shared__ __attribute__((aligned(16))) f16 xs[DL ? (DEEP ? 4 : 2) * TN * DL_KX : TN * PITCH2];
+  __shared__ __attribute__((aligned(16))) uint32_t wl[DL ? (DEEP ? 3 : 2) * 256 * dl_wblocks<TYPE, WR>() + (DEEP ? 256 : 0)
+                                                        : TM * PW / 4];
   __shared__ uint32_t xrow[TN];
   __shared__ uint32_t yrow[TN];
   __shared__ int xexp[TN];
@@ -1063,6 +1176,7 @@ SK_DEV void matmul_tile128_w(const uint4 *__restrict__ w, const uint16_t *__rest
     L.wres = dl_res(w, 0xffffffffull);
     // d pieces: the 16 B-aligned 16 B around each d, to the end of the d region's last 16 B
     L.dres = dl_res(wd, (2ull * ((uint64_t)p.o3 + (uint64_t)p.n_out * (p.n_in >> 8)) + 15) & ~15ull);
+    L.nres = dl_res(nullptr, 0);
     L.dpos0 = 2u * (p.o3 + min(row0 + lrow, p.n_out - 1) * (p.n_in >> 8));
 #pragma unroll
     for (int i = 0; i < DL_L::XS; i++) {
@@ -1071,12 +1185,16 @@ SK_DEV void matmul_tile128_w(const uint4 *__restrict__ w, const uint16_t *__rest
     }
 #pragma unroll
     for (int i = 0; i < DL_L::WS; i++) dl_wpiece<TYPE, WR>(NW * i + L.wv, lane, p, row0, L.wo[i], L.wm[i]);
-    dl_issue_x(L, xs, kbase);
-    dl_issue_w(L, wl, st0);
-    for (uint32_t st = 0; st < n_stage; st++) {
-      const uint32_t b = st & 1;
-      dl_stage<NW, TYPE, NB, TN, WR>(L, acc, xs, xs + XB, wl + b * WB, wl + (b ^ 1) * WB, st + 1 < n_stage,
-                             kbase + KC * st, st0 + st + 1);
+    if constexpr (DEEP) {
+      dl_run_deep<NW, TYPE, NB>(L, acc, xs, wl, wl + 3 * WB, n_stage, kbase, st0);
+    } else {
+      dl_issue_x(L, xs, kbase);
+      dl_issue_w(L, wl, st0);
+      for (uint32_t st = 0; st < n_stage; st++) {
+        const uint32_t b = st & 1;
+        dl_stage<NW, TYPE, NB, TN, WR>(L, acc, xs, xs + XB, wl + b * WB, wl + (b ^ 1) * WB, st + 1 < n_stage,
+                                       kbase + KC * st, st0 + st + 1);
+      }
     }
   } else {
   WLds<TYPE, NT> wr;
@@ -1529,6 +1647,25 @@ MMH8W(1, 0)
 MMH8W(1, 1)
 MMH8W(2, 0)
 MMH8W(2, 1)
+
+// The eight-wave 128 x 128 direct-to-LDS tile on the deeper ring (dl_run_deep): K-split
+// launches (x8e) and segments (x8es).
+#define MMH8E(T, A)                                                                               \
+  extern "C" __global__ __launch_bounds__(512) void matmul_x8e__##T##_##A(                         \
+      const uint4 *w, const uint16_t *wd, const f16 *x, float *y, const uint32_t *ctl,            \
+      MatmulPush p, float *ws, uint32_t *cnt, uint32_t S) {                                       \
+    matmul_tile128_w<T, A, 3, 8, TN2, 0, 0, 0, NoSegments, 1, 1>(w, wd, x, y, ctl, p, ws, cnt, S); \
+  }                                                                                               \
+  extern "C" __global__ __launch_bounds__(512) void matmul_x8es__##T##_##A(                        \
+      const uint4 *w, const uint16_t *wd, const f16 *x, float *y, const uint32_t *ctl,            \
+      Segments<MatmulPush> m, float *ws, uint32_t *cnt, uint32_t S) {                              \
+    matmul_tile128_w<T, A, 3, 8, TN2, 0, 0, 1, Segments<MatmulPush>, 1, 1>(w, wd, x, y, ctl, m.p[0], ws, cnt, S, \
+                                                                           0, 1, m);             \
+  }
+MMH8E(1, 0)
+MMH8E(1, 1)
+MMH8E(2, 0)
+MMH8E(2, 1)
 
 // The eight-wave tile on f16 rows over up to four matrices that read the same rows
 // (segment table as the matvecs take it; start[] counts row tiles).

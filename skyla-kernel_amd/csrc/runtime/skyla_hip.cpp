@@ -1435,8 +1435,12 @@ int skyla_hip_pipeline_new(skyla_hip_context *ctx, const char *name, uint32_t n_
       const char *denv = std::getenv("SKYLA_HIP_DL");
       const bool dl = !(denv && denv[0] == '0');
       const bool dl4 = dl && spec[0] == 1;
+      // the eight-wave tiles on the deeper ring (x8e, x8es), opt-in with SKYLA_HIP_DL=3: M = 512
+      // measured q 42.5-44.2 against 41.6-42.2 us, down 114.5-119.4 against 115.8-116.0, the
+      // config-5 512-token prefill 14.67k against 14.82k tok/s (one box)
+      const bool deep = dl && denv && denv[0] == '3';
       const std::string ts = std::to_string(spec[0]) + "_" + std::to_string(spec[1]);
-      p->hx_fn = find_function(ctx, (dl ? "matmul_x8d__" : "matmul_x8__") + ts);
+      p->hx_fn = find_function(ctx, (deep ? "matmul_x8e__" : dl ? "matmul_x8d__" : "matmul_x8__") + ts);
       p->hx4_fn = find_function(ctx, (dl4 ? "matmul_x4d__" : "matmul_x4__") + ts);
       p->hx4b_fn = find_function(ctx, (dl4 ? "matmul_x4db__" : "matmul_x4b__") + ts);
       // the 256-row x 64-token tile for K-split launches, opt-in with SKYLA_HIP_DL=2: each
@@ -1448,7 +1452,7 @@ int skyla_hip_pipeline_new(skyla_hip_context *ctx, const char *name, uint32_t n_
         p->hxw_fn = find_function(ctx, "matmul_x8w__" + ts);
         p->hxws_fn = find_function(ctx, "matmul_x8ws__" + ts);
       }
-      p->hxs_fn = find_function(ctx, (dl ? "matmul_x8ds__" : "matmul_x8s__") + ts);
+      p->hxs_fn = find_function(ctx, (deep ? "matmul_x8es__" : dl ? "matmul_x8ds__" : "matmul_x8s__") + ts);
       p->split_threads = 512;
     }
   }

@@ -88,7 +88,7 @@ def test_matmul_config3(ctx, name, dtype, n_in, n_out):
     assert err <= TOL and err <= GUARD, err
 
 
-@pytest.mark.parametrize("x4d", ["2", "1", "0"])
+@pytest.mark.parametrize("x4d", ["3", "2", "1", "0"])
 @pytest.mark.parametrize("name,dtype,n_in,n_out,n_tok,accum", [
     ("q", E.DType.Q4K, 4096, 4096, 512, False), ("gate", E.DType.Q4K, 4096, 12288, 512, False),
     ("down", E.DType.Q6K, 12288, 4096, 512, True), ("ragged", E.DType.Q4K, 1024, 200, 37, True),
@@ -102,7 +102,8 @@ def test_matmul_f16_prepass_same_bits(ctx, name, dtype, n_in, n_out, n_tok, accu
     Q4_K launches of more than 128 tiles (gate, ragged4) run the four-wave tile with its
     operands loaded straight into LDS, or with SKYLA_HIP_DL=0 the register-staged one; the
     K-split launches (q, down) run the 128 x 128 direct-to-LDS tile (SKYLA_HIP_DL unset or
-    1), the 256-row x 64-token one (=2) or the register-staged one (=0)."""
+    1), the same on its deeper ring (=3), the 256-row x 64-token one (=2) or the
+    register-staged one (=0)."""
     with env(SKYLA_HIP_XHALF=4, SKYLA_HIP_DL=x4d):
         got1, want = _run(ctx, dtype, n_in, n_out, n_tok, accum=accum, tag="mm-xh")
     with env(SKYLA_HIP_XHALF=0):
@@ -175,7 +176,7 @@ def test_matmul_balanced_grid(ctx, name, dtype, n_in, n_out, n_tok, accum, x4d):
     assert rel_l2(got, want) <= GUARD
 
 
-@pytest.mark.parametrize("dl", ["1", "2"])
+@pytest.mark.parametrize("dl", ["3", "1", "2"])
 @pytest.mark.parametrize("n_tok", [128, 100])
 def test_matmul_segments_qkv(ctx, n_tok, dl):
     """q, k and v of a prefill chunk (Q4_K 4096 -> 4096, 1024, 1024 in one buffer, no barrier
