@@ -52,6 +52,11 @@ struct PrepPush {
   float scale;
   uint32_t part_stride;
 };
+// attention_prep1: attention_prep's words, then attention_merge's output offset and stride
+struct PrepPush1 {
+  PrepPush pp;
+  uint32_t o_off, o_stride;
+};
 struct LastPush { uint32_t src_off, dst_off, n, stride; };
 
 SK_DEV float wave_sum(float v) { return group_sum<64>(v); }
@@ -176,9 +181,14 @@ SK_DEV float load_kv(const f16 *kv, const int8_t *kv8, uint32_t cache, uint32_t 
 // position's key and value rows to the cache as qkv_prep would, keeping the stored bytes
 // in LDS: its threads take them from there in place of the rows they loaded from the cache
 // before the write (the new row and the masked slots clamped to it).
-template <int N_REP, int K8, int V8, bool PREP = false>
+//
+// DIRECT (attention_prep1, a grid of one split: every position of the step in the first 64):
+// the workgroup writes the merged output itself, o = (acc + 0) / l per dim -- what
+// attention_merge computes over one split (its weight is exp(0) = 1 and every other term
+// adds zero), so the same bits -- and no partial; o_off / o_stride are the merge's.
+template <int N_REP, int K8, int V8, bool PREP = false, bool DIRECT = false>
 SK_DEV void attention_body(const float *w, float *a, const uint32_t *ctl, f16 *kv, int8_t *kv8, const AttnPush &p,
-                           const PrepPush *pp) {
+                           const PrepPush *pp, uint32_t o_off = 0, uint32_t o_stride = 0) {
   constexpr int HG = N_REP < 4 ? N_REP : 4;  // heads per value reduction round
   __shared__ float qs[N_REP][HD];
   __shared__ __attribute__((aligned(16))) uint32_t nk[PREP ? 64 : 1], nv[PREP ? 64 : 1];
@@ -186,6 +196,7 @@ SK_DEV void attention_body(const float *w, float *a, const uint32_t *ctl, f16 *k
   __shared__ float es[N_REP][CHUNK];
   __shared__ float wm[4][N_REP];
   __shared__ float4 vp[16][HG * HD / 4];
+  __shared__ float lsh[DIRECT ? N_REP : 1];
   const uint32_t kvh = blockIdx.x, split = blockIdx.y, tok = blockIdx.z;
   const uint32_t n_pos = ctl[1] + tok + 1;
   if (tok >= ctl[2] || split * CHUNK >= n_pos) return;
@@ -352,6 +363,11 @@ SK_DEV void attention_body(const float *w, float *a, const uint32_t *ctl, f16 *k
   if (wave == 0) {
 #pragma unroll
     for (int j = 0; j < N_REP; j++) lrow[j] = wave_sum(es[j][t]);
+    if constexpr (DIRECT) {  // every thread divides by l (read after the value round's barrier)
+#pragma unroll
+      for (int j = 0; j < N_REP; j++)
+        if (t == 0) lsh[j] = lrow[j];
+    }
   }
 
   float v[4][8];
@@ -395,9 +411,13 @@ SK_DEV void attention_body(const float *w, float *a, const uint32_t *ctl, f16 *k
 #pragma unroll
       for (int g = 0; g < 16; g++) sum += ((const float *)vp[g])[o];
       const uint32_t j = h0 + o / HD;
-      a[part_base + ((kvh * N_REP + j) * p.n_split + split) * PART + 2 + o % HD] = sum;
+      if constexpr (DIRECT)
+        a[o_off + tok * o_stride + (kvh * N_REP + j) * HD + o % HD] = (sum + 0.0f) / lsh[j];
+      else
+        a[part_base + ((kvh * N_REP + j) * p.n_split + split) * PART + 2 + o % HD] = sum;
     }
   }
+  if constexpr (DIRECT) return;
   if (t < N_REP) {
     const uint32_t base = part_base + ((kvh * N_REP + t) * p.n_split + split) * PART;
     float l = 0.0f, m = 0.0f;
@@ -492,6 +512,13 @@ QKV(1, 1)
     const AttnPush p = {pp.q_off, pp.part_off, pp.kc_off, pp.vc_off, pp.n_kv, pp.n_split,         \
                         pp.scale, 0u, pp.part_stride, pp.ks_off, pp.vs_off};                     \
     attention_body<R, K8, V8, true>(w, a, ctl, kv, kv8, p, &pp);                                 \
+  }                                                                                              \
+  extern "C" __global__ __launch_bounds__(256) void attention_prep1__##R##_64_##K8##_##V8##_128_128( \
+      const float *w, float *a, const uint32_t *ctl, f16 *kv, int8_t *kv8, PrepPush1 q) {        \
+    const PrepPush &pp = q.pp;                                                                   \
+    const AttnPush p = {pp.q_off, pp.part_off, pp.kc_off, pp.vc_off, pp.n_kv, pp.n_split,         \
+                        pp.scale, 0u, pp.part_stride, pp.ks_off, pp.vs_off};                     \
+    attention_body<R, K8, V8, true, true>(w, a, ctl, kv, kv8, p, &pp, q.o_off, q.o_stride);      \
   }
 #define ATTN_REP(K8, V8) ATTN(1, K8, V8) ATTN(2, K8, V8) ATTN(4, K8, V8) ATTN(8, K8, V8)
 ATTN_REP(0, 0)

@@ -104,6 +104,7 @@ const KernelInfo kKernels[] = {
     {"attention", 5, 11, 6, 6, -1, false, false, 256},     // four waves per (kv head, split, token)
     {"attention_merge", 2, 6, 2, 2, -1, false, false, 1024},
     {"attention_prep", 5, 17, 6, 6, -1, false, false, 256},  // qkv_prep + attention, one token
+    {"attention_prep1", 5, 19, 6, 6, -1, false, false, 256},  // the same over one split, merged
     {"take_last", 2, 4, 0, 0, -1, false, false},
     {"embed", 4, 8, 1, 1, -1, false, false},  // token rows from the HBM token_embd (util.hip)
 };

@@ -12,6 +12,8 @@ import dataclasses
 from enum import IntEnum
 from typing import Sequence
 
+import os
+
 import numpy as np
 
 from .abi import Buffer, Context, Pipeline, Recorder
@@ -35,7 +37,7 @@ MAX_SPLITS = 4096       # splits the attention merge weighs in LDS (kernels/atte
 # Split counts the engine records its decode and prefill graphs for: a replay uses the
 # smallest that covers the positions in play (each recording's attention grid and merge
 # then span only those splits; the arena's own count is the last bucket).
-SPLIT_BUCKETS = (16, 64, 256)
+SPLIT_BUCKETS = (1, 16, 64, 256)
 BATCH = 128
 # What the MoE kernels hold (moe.hip): moe_route keeps 4 logits per lane of one wave and
 # picks at most 16; moe_sort ranks at most 1024 slots (moe_sort.comp:15).
@@ -289,10 +291,14 @@ class Kernels:
                                     [c.n_head // c.n_head_kv, ATTENTION_CHUNK, k8, v8, c.head_dim, c.head_dim])
         self.merge = build_spec("attention_merge", [a, a], 24, [c.head_dim, 0])
         # single-token steps: qkv_prep folded into the attention (kernels/attention.hip)
-        self.attn_prep = None
+        self.attn_prep = self.attn_prep1 = None
         if self.fuse != "none":
-            self.attn_prep = build_spec("attention_prep", [w0, a, a, kv, kv], 68,
-                                        [c.n_head // c.n_head_kv, ATTENTION_CHUNK, k8, v8, c.head_dim, c.head_dim])
+            spec = [c.n_head // c.n_head_kv, ATTENTION_CHUNK, k8, v8, c.head_dim, c.head_dim]
+            self.attn_prep = build_spec("attention_prep", [w0, a, a, kv, kv], 68, spec)
+            # recordings of one split: the attention writes the merged rows itself
+            # (SKYLA_HIP_PREP1=0 keeps attention_prep and the merge there)
+            if os.environ.get("SKYLA_HIP_PREP1", "1") != "0":
+                self.attn_prep1 = build_spec("attention_prep1", [w0, a, a, kv, kv], 76, spec)
         self.take_last = build("take_last", [a, a], 16)
         # token rows gathered from the HBM token_embd, one binding set per weight buffer
         ty = {DType.Q8_0: 0, DType.Q4K: 1, DType.Q6K: 2}[DType(embd_dtype)]
@@ -725,6 +731,12 @@ class Graph:
         push = [a.q, a.k, a.v, q_norm, k_norm, kv.keys(l), kv.values(l), c.n_head_kv, f32_bits(c.eps), rope,
                 f32_bits(c.rope_mscale), kv.key_scales(l), kv.value_scales(l), a.part, self.n_split, f32_bits(scale),
                 a.s_part]
+        if self.n_split == 1 and self.k.attn_prep1 is not None:
+            # one split (every position in the first 64): the merged rows straight from the
+            # attention (attention_prep1: the merge over one split is acc / l, same bits)
+            self.r.dispatch(self.k.attn_prep1, [c.n_head_kv, 1, 1], push + [a.attn, a.s_attn])
+            self.stage("attention (+ qk norm, rope, kv write, merge of one split)")
+            return
         self.r.dispatch(self.k.attn_prep, [c.n_head_kv, self.n_split, 1], push)
         self.stage("attention (+ qk norm, rope, kv write)")
         push = [a.part, a.attn, self.n_split, ATTENTION_CHUNK, a.s_part, a.s_attn]

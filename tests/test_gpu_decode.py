@@ -542,3 +542,37 @@ def test_split_buckets_same_logits(ctx):
             if rec is not None:
                 rec.free()
         eng.free()
+
+
+def test_single_split_direct_same_logits(ctx):
+    """Single-token steps whose positions all lie in the first 64 replay the one-split
+    recording, where attention_prep1 writes the merged rows itself (no merge launch): the
+    logits of the arena-wide recording (attention_prep over 40 splits, then the merge) bit
+    for bit, on both sides of the one-split bound (positions 60..67)."""
+    c = synth.qwen3_config("tiny")
+    tensors = synth.qwen3(f"{CFG}-q4_k_m", c, "q4_k_m", "random")
+    eng = E.Engine(ctx, tensors, c, 40 * E.ATTENTION_CHUNK, P.F16_KEYS_Q8_VALUES)
+    full_d = None
+    try:
+        a = eng.arena
+        assert E.SPLIT_BUCKETS[0] == 1 and eng.kernels.attn_prep1 is not None
+        full_d = E.record(ctx, eng.kernels, eng.weights, a, c, False, False, a.n_split)
+        one = eng.recording(False, 1)
+        assert one.launches() < full_d.launches()      # one merge launch fewer per layer
+        prompt = synth.prompt(f"{CFG}-direct", 60, c.n_vocab)
+        eng.prefill(prompt)
+        tok = int(np.argmax(eng.logits()))
+        for _ in range(8):                             # positions 60..67
+            pos = eng.pos
+            got = eng.step(tok)
+            eng.pos = pos
+            eng.load([tok], batched=False)
+            ctx.replay(full_d)
+            eng.pos += 1
+            want = eng.logits()
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), pos
+            tok = int(np.argmax(want))
+    finally:
+        if full_d is not None:
+            full_d.free()
+        eng.free()
