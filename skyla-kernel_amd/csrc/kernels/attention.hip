@@ -51,7 +51,9 @@ struct PrepPush {
   uint32_t ks_off, vs_off, part_off, n_split;
   float scale;
   uint32_t part_stride;
+  uint32_t cs_off;  // the step's rope pairs (rope_table) in the arena, or NO_TABLE: computed here
 };
+constexpr uint32_t NO_TABLE = 0xffffffffu;
 // attention_prep1: attention_prep's words, then attention_merge's output offset and stride
 struct PrepPush1 {
   PrepPush pp;
@@ -116,14 +118,34 @@ SK_DEV void store_kv(f16 *kv, int8_t *kv8, uint32_t cache, uint32_t scales, uint
 // QK-norm (rmsnorm.comp over one 128-wide head, weights at nw) and NeoX RoPE (rope.rs:60-68)
 // of the pair (element t, element t + 64), one wave per head.
 SK_DEV void norm_rope(const float *w, uint32_t nw, uint32_t rope_off, float eps, float mscale, uint32_t pos,
-                      uint32_t t, float x0, float x1, float &y0, float &y1) {
+                      uint32_t t, float x0, float x1, float &y0, float &y1, const float *cs = nullptr) {
 #pragma clang fp contract(off)
   const float r = 1.0f / sqrtf(wave_sum(x0 * x0 + x1 * x1) / (float)HD + eps);
   const float n0 = x0 * r * w[nw + t], n1 = x1 * r * w[nw + t + 64];
-  const float angle = (float)pos * w[rope_off + t];
-  const float c = cosf(angle) * mscale, s = sinf(angle) * mscale;
+  float c, s;
+  if (cs) {  // rope_table's pairs for this position: the same two products
+    c = cs[2 * t];
+    s = cs[2 * t + 1];
+  } else {
+    const float angle = (float)pos * w[rope_off + t];
+    c = cosf(angle) * mscale;
+    s = sinf(angle) * mscale;
+  }
   y0 = n0 * c - n1 * s;
   y1 = n0 * s + n1 * c;
+}
+
+// rope_table: the (cos, sin) x mscale pairs of the step's position (ctl[1]) for the 64
+// rotation frequencies, computed once per decode step into the arena for every layer's
+// attention_prep -- its workgroups (one per kv head and split) would each reduce the same
+// large angles otherwise.  norm_rope's expressions, so the same values.
+struct RopePush { uint32_t rope_off, o_off; float mscale; };
+extern "C" __global__ __launch_bounds__(64) void rope_table(const float *w, float *a, const uint32_t *ctl, RopePush p) {
+#pragma clang fp contract(off)
+  const uint32_t t = threadIdx.x;
+  const float angle = (float)ctl[1] * w[p.rope_off + t];
+  a[p.o_off + 2 * t] = cosf(angle) * p.mscale;
+  a[p.o_off + 2 * t + 1] = sinf(angle) * p.mscale;
 }
 
 template <int K8, int V8>
@@ -240,10 +262,11 @@ SK_DEV void attention_body(const float *w, float *a, const uint32_t *ctl, f16 *k
   const uint32_t q_base = p.q_off + tok * p.q_stride + kvh * N_REP * HD;
   if constexpr (PREP) {
     const uint32_t pos = ctl[1], lane = t & 63;
+    const float *cs = pp->cs_off != NO_TABLE ? a + pp->cs_off : nullptr;
     for (uint32_t j = wave; j < (uint32_t)N_REP; j += 4) {
       float y0, y1;
       norm_rope(w, pp->qn_off, pp->rope_off, pp->eps, pp->mscale, pos, lane, a[q_base + j * HD + lane],
-                a[q_base + j * HD + lane + 64], y0, y1);
+                a[q_base + j * HD + lane + 64], y0, y1, cs);
       qs[j][lane] = y0 * p.scale;
       qs[j][lane + 64] = y1 * p.scale;
     }
@@ -252,7 +275,7 @@ SK_DEV void attention_body(const float *w, float *a, const uint32_t *ctl, f16 *k
         float y0, y1;
         const uint32_t src = pp->k_off + kvh * HD;
         norm_rope(w, pp->kn_off, pp->rope_off, pp->eps, pp->mscale, pos, lane, a[src + lane], a[src + lane + 64], y0,
-                  y1);
+                  y1, cs);
         store_kv<K8>(kv, kv8, p.kc_off, p.ks_off, kv_dim, pos, kvh, lane, y0, y1, nk, nks);
       } else if (wave == 1) {
         const uint32_t src = pp->v_off + kvh * HD;

@@ -103,8 +103,9 @@ const KernelInfo kKernels[] = {
     {"qkv_prep", 5, 16, 5, 5, -1, false, false, 64},       // one wave per (head, token)
     {"attention", 5, 11, 6, 6, -1, false, false, 256},     // four waves per (kv head, split, token)
     {"attention_merge", 2, 6, 2, 2, -1, false, false, 1024},
-    {"attention_prep", 5, 17, 6, 6, -1, false, false, 256},  // qkv_prep + attention, one token
-    {"attention_prep1", 5, 19, 6, 6, -1, false, false, 256},  // the same over one split, merged
+    {"attention_prep", 5, 18, 6, 6, -1, false, false, 256},  // qkv_prep + attention, one token
+    {"attention_prep1", 5, 20, 6, 6, -1, false, false, 256},  // the same over one split, merged
+    {"rope_table", 3, 3, 0, 0, -1, false, false, 64},         // a decode step's rope pairs
     {"take_last", 2, 4, 0, 0, -1, false, false},
     {"embed", 4, 8, 1, 1, -1, false, false},  // token rows from the HBM token_embd (util.hip)
 };

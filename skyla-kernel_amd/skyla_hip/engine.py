@@ -291,14 +291,18 @@ class Kernels:
                                     [c.n_head // c.n_head_kv, ATTENTION_CHUNK, k8, v8, c.head_dim, c.head_dim])
         self.merge = build_spec("attention_merge", [a, a], 24, [c.head_dim, 0])
         # single-token steps: qkv_prep folded into the attention (kernels/attention.hip)
-        self.attn_prep = self.attn_prep1 = None
+        self.attn_prep = self.attn_prep1 = self.rope_table = None
         if self.fuse != "none":
             spec = [c.n_head // c.n_head_kv, ATTENTION_CHUNK, k8, v8, c.head_dim, c.head_dim]
-            self.attn_prep = build_spec("attention_prep", [w0, a, a, kv, kv], 68, spec)
+            self.attn_prep = build_spec("attention_prep", [w0, a, a, kv, kv], 72, spec)
+            # a decode step's rope pairs, once for every layer's attention_prep
+            # (SKYLA_HIP_ROPE_TABLE=0: each workgroup computes them)
+            if os.environ.get("SKYLA_HIP_ROPE_TABLE", "1") != "0":
+                self.rope_table = build("rope_table", [w0, a, a], 12)
             # recordings of one split: the attention writes the merged rows itself
             # (SKYLA_HIP_PREP1=0 keeps attention_prep and the merge there)
             if os.environ.get("SKYLA_HIP_PREP1", "1") != "0":
-                self.attn_prep1 = build_spec("attention_prep1", [w0, a, a, kv, kv], 76, spec)
+                self.attn_prep1 = build_spec("attention_prep1", [w0, a, a, kv, kv], 80, spec)
         self.take_last = build("take_last", [a, a], 16)
         # token rows gathered from the HBM token_embd, one binding set per weight buffer
         ty = {DType.Q8_0: 0, DType.Q4K: 1, DType.Q6K: 2}[DType(embd_dtype)]
@@ -468,6 +472,7 @@ class Arena:
         self.part, self.s_part = batched(c.n_head * n_split * (c.head_dim + 2))
         self.last = single(c.n_embd)
         self.logits = single(c.n_vocab)
+        self.rope_cs = single(c.head_dim)  # a decode step's (cos, sin) pairs (rope_table)
         stride = _next64(c.n_ff_expert)
         slots = c.n_expert_used * BATCH
         if c.n_expert:  # the limits of the MoE kernels (moe.hip), checked before any launch
@@ -530,6 +535,7 @@ class Graph:
         # merge's span): the arena's, or fewer for a recording that serves early positions
         self.n_split = n_split if n_split is not None else getattr(a, "n_split", 0)
         self.b = BATCH if batched else 1
+        self.rope_done = False  # rope_table has written the step's pairs (decode_rope)
         # decode with the fused matvecs (Kernels.fuse): "qkv" folds the attention norm into
         # q/k/v; "ffn" also the FFN norm into the Q4_K gate/up pair; "all" the FFN norm into
         # gate/up, the SiLU into down and the output norm into the head; "auto" per layer:
@@ -678,6 +684,17 @@ class Graph:
         push = [x, w, y, c.n_embd, f32_bits(c.eps), self.a.s_embd]
         self.r.dispatch(self.k.rmsnorm, [1, tokens, 1], push)
 
+    def decode_rope(self, rope: int) -> None:
+        """A single-token step's rope pairs for its position, once for every layer's
+        attention_prep (rope_table; the values norm_rope would compute in each of its
+        workgroups)."""
+        if not (self.fused and self.k.attn_prep is not None and getattr(self.k, "rope_table", None) is not None):
+            return
+        a, c = self.a, self.c
+        self.r.dispatch(self.k.rope_table, [1, 1, 1], [rope, a.rope_cs, f32_bits(c.rope_mscale)])
+        self.stage("rope table")
+        self.rope_done = True
+
     def embed(self, m: QMatrix) -> None:
         """The chunk's token rows into x (the reference's host-side Engine::load,
         engine.rs:100-117, as a gather from the HBM token_embd)."""
@@ -730,7 +747,7 @@ class Graph:
         scale = np.float32(1.0) / np.sqrt(np.float32(c.head_dim))
         push = [a.q, a.k, a.v, q_norm, k_norm, kv.keys(l), kv.values(l), c.n_head_kv, f32_bits(c.eps), rope,
                 f32_bits(c.rope_mscale), kv.key_scales(l), kv.value_scales(l), a.part, self.n_split, f32_bits(scale),
-                a.s_part]
+                a.s_part, a.rope_cs if self.rope_done else 0xFFFFFFFF]
         if self.n_split == 1 and self.k.attn_prep1 is not None:
             # one split (every position in the first 64): the merged rows straight from the
             # attention (attention_prep1: the merge over one split is acc / l, same bits)
@@ -852,6 +869,7 @@ def record(ctx: Context, k: Kernels, w: Weights, a: Arena, c: Config, batched: b
     def body(r: Recorder) -> None:
         g = Graph(r, k, a, c, batched, n_split)
         g.embed(w.embd)
+        g.decode_rope(w.rope)
         for l, lw in enumerate(w.layers):
             g.layer(l, lw, w.rope)
         src = a.x

@@ -9,6 +9,9 @@ f16 rows or q8 blocks).  Every step's top-1 is compared: the tests print the num
 disagreements, the smallest oracle top-2 margin met and the worst logits distance, and
 assert that no step disagrees.
 """
+import contextlib
+import os
+
 import numpy as np
 import pytest
 
@@ -22,6 +25,20 @@ pytestmark = pytest.mark.gpu
 
 P = E.KvPrecision
 CFG = "test-decode"
+
+
+@contextlib.contextmanager
+def env_var(name, value):
+    """A runtime switch read when the engine builds its kernels."""
+    old = os.environ.get(name)
+    os.environ[name] = value
+    try:
+        yield
+    finally:
+        if old is None:
+            del os.environ[name]
+        else:
+            os.environ[name] = old
 
 
 class Bench:
@@ -576,3 +593,28 @@ def test_single_split_direct_same_logits(ctx):
         if full_d is not None:
             full_d.free()
         eng.free()
+
+
+@pytest.mark.parametrize("ctx_len", [60, 1500])
+def test_rope_table_same_logits(ctx, ctx_len):
+    """Decode steps whose attention_prep reads the step's rope pairs from rope_table (one
+    launch per step) against the same steps with every workgroup computing them: the same
+    logits bit for bit, at one split and past the one-split bucket."""
+    c = synth.qwen3_config("tiny")
+    tensors = synth.qwen3(f"{CFG}-q4_k_m", c, "q4_k_m", "random")
+    got = {}
+    for table in ("1", "0"):
+        with env_var("SKYLA_HIP_ROPE_TABLE", table):
+            eng = E.Engine(ctx, tensors, c, 32 * E.ATTENTION_CHUNK, P.F16_KEYS_Q8_VALUES)
+        try:
+            assert (eng.kernels.rope_table is not None) == (table == "1")
+            eng.prefill(synth.prompt(f"{CFG}-rope", ctx_len, c.n_vocab))
+            tok = int(np.argmax(eng.logits()))
+            rows = []
+            for _ in range(3):
+                rows.append(eng.step(tok).copy())
+                tok = int(np.argmax(rows[-1]))
+            got[table] = np.stack(rows)
+        finally:
+            eng.free()
+    assert np.array_equal(got["1"].view(np.uint32), got["0"].view(np.uint32))
