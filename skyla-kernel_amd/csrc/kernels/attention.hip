@@ -211,7 +211,10 @@ SK_DEV float load_kv(const f16 *kv, const int8_t *kv8, uint32_t cache, uint32_t 
 template <int N_REP, int K8, int V8, bool PREP = false, bool DIRECT = false>
 SK_DEV void attention_body(const float *w, float *a, const uint32_t *ctl, f16 *kv, int8_t *kv8, const AttnPush &p,
                            const PrepPush *pp, uint32_t o_off = 0, uint32_t o_stride = 0) {
-  constexpr int HG = N_REP < 4 ? N_REP : 4;  // heads per value reduction round
+  // heads per value reduction round: two keep vp at 16 KB, so five workgroups share a CU
+  // (83 VGPRs allow five; with four heads, 32 KB, LDS allowed four, and a 16k-position
+  // step's 2056 workgroups took a third round of eight)
+  constexpr int HG = N_REP < 2 ? N_REP : 2;
   __shared__ float qs[N_REP][HD];
   __shared__ __attribute__((aligned(16))) uint32_t nk[PREP ? 64 : 1], nv[PREP ? 64 : 1];
   __shared__ float nks[PREP ? 4 : 1], nvs[PREP ? 4 : 1];
