@@ -527,13 +527,15 @@ QKV(0, 1)
 QKV(1, 1)
 
 // attention (attention.comp): spec [N_REP, CHUNK, K_Q8, V_Q8, head_dim, q_head].
+// Six waves per SIMD for the forms of at most four query heads per kv head (80 VGPRs, no
+// spill; with 16 KB of LDS, six workgroups per CU); eight heads keep their registers.
 #define ATTN(R, K8, V8)                                                                          \
-  extern "C" __global__ __launch_bounds__(256) void attention__##R##_64_##K8##_##V8##_128_128(   \
+  extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(R == 8 ? 1 : 6))) void attention__##R##_64_##K8##_##V8##_128_128(   \
       float *a, const uint32_t *ctl, const f16 *kv, const int8_t *kv8, const f16 *kvs, AttnPush p) { \
     (void)kvs;                                                                                   \
     attention_body<R, K8, V8>(nullptr, a, ctl, const_cast<f16 *>(kv), const_cast<int8_t *>(kv8), p, nullptr); \
   }                                                                                              \
-  extern "C" __global__ __launch_bounds__(256) void attention_prep__##R##_64_##K8##_##V8##_128_128( \
+  extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(R == 8 ? 1 : 6))) void attention_prep__##R##_64_##K8##_##V8##_128_128( \
       const float *w, float *a, const uint32_t *ctl, f16 *kv, int8_t *kv8, PrepPush pp) {        \
     const AttnPush p = {pp.q_off, pp.part_off, pp.kc_off, pp.vc_off, pp.n_kv, pp.n_split,         \
                         pp.scale, 0u, pp.part_stride, pp.ks_off, pp.vs_off};                     \
