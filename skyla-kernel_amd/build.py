@@ -21,7 +21,7 @@ BUILD = os.path.join(PKG, "build")
 LIB_DIR = os.path.join(PKG, "lib")
 LIB = os.path.join(LIB_DIR, "libskyla_hip.so")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
-KERNELS = ("matvec", "matmul", "moe", "util", "attention", "chain")
+KERNELS = ("matvec", "matmul", "moe", "util", "attention")
 
 # Packed FP32 instructions are disabled for all device code; f16 packed math is kept.
 HIP_FLAGS = [

@@ -69,7 +69,7 @@ SK_DEV float lane_sum(float v) {
 SK_DEV uint32_t ctl_word(const uint32_t *ctl, uint32_t i) { return ctl[i]; }
 
 // ---------------------------------------------------------------------------------------
-// f32 products of exact integer quants (the decode matvecs, matvec.hip and chain.hip).
+// f32 products of exact integer quants (the decode matvecs, matvec.hip).
 // ---------------------------------------------------------------------------------------
 // s + sum over the four bytes b of word v of f32(b) * x[b], in byte order: four
 // v_cvt_f32_ubyte0..3 (exact for 0..255) and four FMAs.

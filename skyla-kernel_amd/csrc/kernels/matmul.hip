@@ -761,10 +761,9 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 //                    at 24576 + 16 r, and at 26624 + 16 r the 16 B-aligned 16 B that hold the
 //                    row's d (at byte dpos: regions and buffers are 16 B-aligned, so those
 //                    16 B lie inside the buffer)
-// (WR = 2: a 256-row tile, every region twice as long, at offsets twice as far)
-template <int TYPE, int WR = 1>
+template <int TYPE>
 constexpr uint32_t dl_wblocks() {
-  return (TYPE == 1 ? 18 : 28) * WR;
+  return TYPE == 1 ? 18 : 28;
 }
 // 16 B unit slot swizzle of a 64 B qh row (4 units): the 8 B reads of 32 rows at one
 // position meet at most twice on a bank (64 or 32 banks)
@@ -773,11 +772,11 @@ SK_DEV uint32_t dl_swz4(uint32_t r) { return ((r >> 1) ^ (r >> 3)) & 3u; }
 // Per-lane state of the direct-to-LDS tile: buffer resources, this lane's load offsets for
 // its activation blocks (wave + NW i) and weight blocks (the same), the bytes a weight
 // block's source moves per super-block, and the read swizzles.
-template <int NW, int TYPE, int TN = TN2, int WR = 1>
+template <int NW, int TYPE, int TN = TN2>
 struct DLLanes {
   static constexpr int XS = TN / 8 / NW;                                 // activation blocks per wave
-  static constexpr int WS = (dl_wblocks<TYPE, WR>() + NW - 1) / NW;      // weight block slots per wave
-  static constexpr int WMIN = dl_wblocks<TYPE, WR>() / NW;               // weight loads of every wave
+  static constexpr int WS = (dl_wblocks<TYPE>() + NW - 1) / NW;      // weight block slots per wave
+  static constexpr int WMIN = dl_wblocks<TYPE>() / NW;               // weight loads of every wave
   static_assert(XS >= 1 && XS * NW * 8 == TN, "whole 1 KiB activation blocks per wave");
   u32x4 xres, wres, dres, nres;  // nres: no bytes (every load past its end reads zeros)
   uint32_t xo[XS], wo[WS], wm[WS];
@@ -815,44 +814,44 @@ SK_DEV uint32_t lds_addr(const void *p) { return (uint32_t)(uintptr_t)(dl_lds *)
 
 // Source of weight block b for this lane: byte offset (super-block 0) and bytes per
 // super-block, with rows past n_out clamped to the last row.
-template <int TYPE, int WR = 1>
+template <int TYPE>
 SK_DEV void dl_wpiece(uint32_t b, uint32_t lane, const MatmulPush &p, uint32_t row0, uint32_t &off, uint32_t &per) {
   const uint32_t supers = p.n_in >> 8, last = p.n_out - 1;
   auto R = [&](uint32_t r) { return min(row0 + r, last); };
-  if (b < 16 * WR) {  // qs / ql: 8 rows, lane = 8 r + unit slot
+  if (b < 16) {  // qs / ql: 8 rows, lane = 8 r + unit slot
     const uint32_t r = 8 * b + (lane >> 3);
     off = 16u * (p.o0 + R(r) * supers * 8 + ((lane & 7) ^ dl_swz(r)));
     per = 128;
   } else if (TYPE == 1) {  // headers: 64 rows
-    off = 16u * (p.o1 + R(64 * (b - 16 * WR) + lane) * supers);
+    off = 16u * (p.o1 + R(64 * (b - 16) + lane) * supers);
     per = 16;
-  } else if (b < 24 * WR) {  // qh: 16 rows, lane = 4 r + unit slot
-    const uint32_t r = 16 * (b - 16 * WR) + (lane >> 2);
+  } else if (b < 24) {  // qh: 16 rows, lane = 4 r + unit slot
+    const uint32_t r = 16 * (b - 16) + (lane >> 2);
     off = 16u * (p.o1 + R(r) * supers * 4 + ((lane & 3) ^ dl_swz4(r)));
     per = 64;
-  } else if (b < 26 * WR) {  // scales: 64 rows
-    off = 16u * (p.o2 + R(64 * (b - 24 * WR) + lane) * supers);
+  } else if (b < 26) {  // scales: 64 rows
+    off = 16u * (p.o2 + R(64 * (b - 24) + lane) * supers);
     per = 16;
   } else {  // d: 64 rows (the 16 B-aligned piece that holds d: see dl_issue_w)
-    off = 2u * (p.o3 + R(64 * (b - 26 * WR) + lane) * supers);
+    off = 2u * (p.o3 + R(64 * (b - 26) + lane) * supers);
     per = 2;
   }
 }
 
 // A 64-k activation chunk (at k) into buffer dst.
-template <int NW, int TYPE, int TN, int WR>
-SK_DEV void dl_issue_x(const DLLanes<NW, TYPE, TN, WR> &L, f16 *__restrict__ dst, uint32_t k) {
+template <int NW, int TYPE, int TN>
+SK_DEV void dl_issue_x(const DLLanes<NW, TYPE, TN> &L, f16 *__restrict__ dst, uint32_t k) {
 #pragma unroll
   for (int i = 0; i < L.XS; i++) dl_load16(L.xres, lds_addr(dst + (NW * i + L.wv) * 512), L.xo[i], 2u * k);
 }
 // The weights of super-block sb into buffer dst.
-template <int NW, int TYPE, int TN, int WR>
-SK_DEV void dl_issue_w(const DLLanes<NW, TYPE, TN, WR> &L, uint32_t *__restrict__ dst, uint32_t sb) {
+template <int NW, int TYPE, int TN>
+SK_DEV void dl_issue_w(const DLLanes<NW, TYPE, TN> &L, uint32_t *__restrict__ dst, uint32_t sb) {
 #pragma unroll
   for (int i = 0; i < L.WS; i++) {
     const uint32_t b = NW * i + L.wv;
-    if (i < L.WMIN || b < dl_wblocks<TYPE, WR>()) {
-      if (TYPE == 2 && b >= 26 * WR)  // d: 2 B-aligned, so the piece is the aligned 16 B around it
+    if (i < L.WMIN || b < dl_wblocks<TYPE>()) {
+      if (TYPE == 2 && b >= 26)  // d: 2 B-aligned, so the piece is the aligned 16 B around it
         dl_load16(L.dres, lds_addr(dst + b * 256), (L.wo[i] + 2u * sb) & ~15u, 0);
       else
         dl_load16(L.wres, lds_addr(dst + b * 256), L.wo[i], L.wm[i] * sb);
@@ -865,8 +864,8 @@ SK_DEV void dl_issue_w(const DLLanes<NW, TYPE, TN, WR> &L, uint32_t *__restrict_
 // chunk go to the other activation buffer, and at chunk 0 (when `more`) the next stage's
 // weights (super-block nsb) go to wn.  The waits that order a buffer's loads before its
 // reads are the explicit ones here (the loads are assembly the compiler does not count).
-template <int NW, int TYPE, int NB, int TN, int WR>
-SK_DEV void dl_stage(const DLLanes<NW, TYPE, TN, WR> &L, f32x16 (&acc)[NB], f16 *__restrict__ x0, f16 *__restrict__ x1,
+template <int NW, int TYPE, int NB, int TN>
+SK_DEV void dl_stage(const DLLanes<NW, TYPE, TN> &L, f32x16 (&acc)[NB], f16 *__restrict__ x0, f16 *__restrict__ x1,
                      const uint32_t *__restrict__ wc, uint32_t *__restrict__ wn, bool more, uint32_t k0,
                      uint32_t nsb) {
   // (wc holds super-block nsb - 1)
@@ -876,7 +875,7 @@ SK_DEV void dl_stage(const DLLanes<NW, TYPE, TN, WR> &L, f32x16 (&acc)[NB], f16 
     // this wave's loads of chunk c4 (and, at c4 = 0, of the stage's weights) are in LDS; at
     // c4 = 1 the next stage's weight loads, issued after the chunk's, may stay in flight
     if (c4 == 1 && more)
-      dl_wait_vm<DLLanes<NW, TYPE, TN, WR>::WMIN>();
+      dl_wait_vm<DLLanes<NW, TYPE, TN>::WMIN>();
     else
       dl_wait_vm<0>();
     __syncthreads();
@@ -889,11 +888,11 @@ SK_DEV void dl_stage(const DLLanes<NW, TYPE, TN, WR> &L, f32x16 (&acc)[NB], f16 
       if (more) dl_issue_w(L, wn, nsb);
       WStage<TYPE> hs;
       if constexpr (TYPE == 1) {
-        hs.hd = *(const uint4 *)(wc + 4096 * WR + 4 * L.lrow);
+        hs.hd = *(const uint4 *)(wc + 4096 + 4 * L.lrow);
       } else {
-        hs.sc = *(const uint4 *)(wc + 6144 * WR + 4 * L.lrow);
+        hs.sc = *(const uint4 *)(wc + 6144 + 4 * L.lrow);
         const uint32_t pos = (L.dpos0 + 2u * (nsb - 1)) & 15u;  // d's byte in its 16 B
-        const uint4 dq = *(const uint4 *)(wc + 6656 * WR + 4 * L.lrow);
+        const uint4 dq = *(const uint4 *)(wc + 6656 + 4 * L.lrow);
         const uint32_t dw = pos < 8 ? (pos < 4 ? dq.x : dq.y) : (pos < 12 ? dq.z : dq.w);
         hs.d = (dw >> (8 * (pos & 2))) & 0xffffu;
       }
@@ -910,7 +909,7 @@ SK_DEV void dl_stage(const DLLanes<NW, TYPE, TN, WR> &L, f32x16 (&acc)[NB], f16 
       } else {  // ql unit 4 hf + 2 (g & 1) + (t & 1), qh unit 2 hf + (t & 1); lane half hh: bytes 8 hh..
         const int hf = t >> 3, g = (t >> 1) & 3;
         const uint2 l = *(const uint2 *)(wc + L.lrow * 32 + 4 * ((4 * hf + 2 * (g & 1) + (t & 1)) ^ L.wsw) + 2 * L.hh);
-        const uint2 h = *(const uint2 *)(wc + 4096 * WR + L.lrow * 16 + 4 * ((2 * hf + (t & 1)) ^ L.wsw4) + 2 * L.hh);
+        const uint2 h = *(const uint2 *)(wc + 4096 + L.lrow * 16 + 4 * ((2 * hf + (t & 1)) ^ L.wsw4) + 2 * L.hh);
         wf = q6k_frag(l, h, t, sc);
       }
       const uint32_t xu = ((koff<TYPE>(t, L.hh) - DL_KX * c4) >> 3) ^ L.xsw;
@@ -935,141 +934,24 @@ SK_DEV void dl_stage(const DLLanes<NW, TYPE, TN, WR> &L, f32x16 (&acc)[NB], f16 
   }
 }
 
-// The eight-wave 128 x 128 direct-to-LDS tile with a deeper ring (one workgroup per CU, so
-// the LDS allows it): four activation buffers, chunk c in buffer c % 4, loaded three chunks
-// ahead; three weight buffers, stage s in buffer s % 3, loaded two stages ahead.  Every
-// chunk issues the same loads (past the last chunk or stage they read from nres and write
-// zeros into the buffer they would fill, which nothing reads again; a wave with one weight
-// block fewer than another loads zeros into the spare block `dummy`), so the loads a wave
-// has issued after those of chunk c are the same count at every chunk and each wait is a
-// constant: before the barrier of chunk c (c4 = c % 4) the wave lets the next two chunks'
-// loads stay in flight, and for c4 != 0 also the weight loads issued at the stage's first
-// chunk.  Buffer reuse: chunk c + 3's loads go to the buffer chunk c - 1 used and stage
-// s + 2's to the one stage s - 1 used, both issued after the barrier that every wave
-// reaches only when done with them.
-template <int NW, int TYPE, int NB>
-SK_DEV void dl_run_deep(const DLLanes<NW, TYPE> &L, f32x16 (&acc)[NB], f16 *xs, uint32_t *wl, uint32_t *dummy,
-                        uint32_t n_stage, uint32_t kbase, uint32_t st0) {
-  using DL_L = DLLanes<NW, TYPE>;
-  constexpr uint32_t XB = TN2 * DL_KX, WB = 256 * dl_wblocks<TYPE>(), NA = 4, NWB = 3;
-  const uint32_t n_chunk = (KC / DL_KX) * n_stage;
-  auto issue_x = [&](uint32_t c) {
-    f16 *dst = xs + (c % NA) * XB;
-    const bool live = c < n_chunk;
-#pragma unroll
-    for (int i = 0; i < DL_L::XS; i++)
-      dl_load16(live ? L.xres : L.nres, lds_addr(dst + (NW * i + L.wv) * 512), L.xo[i], 2u * (kbase + DL_KX * c));
-  };
-  auto issue_w = [&](uint32_t s) {
-    uint32_t *dst = wl + (s % NWB) * WB;
-    const bool live = s < n_stage;
-    const uint32_t sb = st0 + s;
-#pragma unroll
-    for (int i = 0; i < DL_L::WS; i++) {
-      const uint32_t b = NW * i + L.wv;
-      if (i < DL_L::WMIN || b < dl_wblocks<TYPE>()) {
-        if (TYPE == 2 && b >= 26)  // d: the aligned 16 B around it (as dl_issue_w)
-          dl_load16(live ? L.dres : L.nres, lds_addr(dst + b * 256), (L.wo[i] + 2u * sb) & ~15u, 0);
-        else
-          dl_load16(live ? L.wres : L.nres, lds_addr(dst + b * 256), L.wo[i], L.wm[i] * sb);
-      } else {
-        dl_load16(L.nres, lds_addr(dummy), 0, 0);
-      }
-    }
-  };
-  issue_w(0);
-  issue_w(1);
-  issue_x(0);
-  issue_x(1);
-  issue_x(2);
-  for (uint32_t st = 0; st < n_stage; st++) {
-    const uint32_t *wc = wl + (st % NWB) * WB;
-    StageScales<TYPE> ss;
-#pragma unroll
-    for (int c4 = 0; c4 < KC / DL_KX; c4++) {
-      const uint32_t c = (KC / DL_KX) * st + c4;
-      if (c4 == 0)
-        dl_wait_vm<2 * DL_L::XS>();
-      else
-        dl_wait_vm<2 * DL_L::XS + DL_L::WS>();
-      __syncthreads();
-      issue_x(c + 3);
-      if (c4 == 0) {
-        __builtin_amdgcn_sched_barrier(0);  // the weight loads stay behind the chunk's
-        issue_w(st + 2);
-        WStage<TYPE> hs;
-        if constexpr (TYPE == 1) {
-          hs.hd = *(const uint4 *)(wc + 4096 + 4 * L.lrow);
-        } else {
-          hs.sc = *(const uint4 *)(wc + 6144 + 4 * L.lrow);
-          const uint32_t pos = (L.dpos0 + 2u * (st0 + st)) & 15u;  // d's byte in its 16 B
-          const uint4 dq = *(const uint4 *)(wc + 6656 + 4 * L.lrow);
-          const uint32_t dw = pos < 8 ? (pos < 4 ? dq.x : dq.y) : (pos < 12 ? dq.z : dq.w);
-          hs.d = (dw >> (8 * (pos & 2))) & 0xffffu;
-        }
-        stage_scales<TYPE>(hs, L.hh, ss);
-      }
-      const f16 *xb = xs + c4 * XB;  // c % 4 == c4
-      f16x8 xf0[NB], xf1[NB], wf0, wf1;
-      auto frags = [&](int ts, f16x8(&xf)[NB], f16x8 &wf) {
-        const int t = 4 * c4 + ts;
-        f16x2 sc, nm;
-        ss.get(t, sc, nm);
-        if constexpr (TYPE == 1) {
-          wf = q4k_frag(*(const uint2 *)(wc + L.lrow * 32 + 4 * ((t >> 1) ^ L.wsw) + 2 * (t & 1)), L.hh, sc, nm);
-        } else {
-          const int hf = t >> 3, g = (t >> 1) & 3;
-          const uint2 l = *(const uint2 *)(wc + L.lrow * 32 + 4 * ((4 * hf + 2 * (g & 1) + (t & 1)) ^ L.wsw) + 2 * L.hh);
-          const uint2 h = *(const uint2 *)(wc + 4096 + L.lrow * 16 + 4 * ((2 * hf + (t & 1)) ^ L.wsw4) + 2 * L.hh);
-          wf = q6k_frag(l, h, t, sc);
-        }
-        const uint32_t xu = ((koff<TYPE>(t, L.hh) - DL_KX * c4) >> 3) ^ L.xsw;
-#pragma unroll
-        for (int j = 0; j < NB; j++)
-          xf[j] = *(const f16x8 *)(xb + (32 * (L.tb + j) + (L.lane & 31)) * DL_KX + 8 * xu);
-      };
-      frags(0, xf0, wf0);
-#pragma unroll
-      for (int ts = 0; ts < 4; ts++) {
-        if (ts + 1 < 4) {
-          if (ts & 1)
-            frags(ts + 1, xf0, wf0);
-          else
-            frags(ts + 1, xf1, wf1);
-        }
-#pragma unroll
-        for (int j = 0; j < NB; j++)
-          acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16((ts & 1) ? xf1[j] : xf0[j], (ts & 1) ? wf1 : wf0, acc[j],
-                                                          0, 0, 0);
-      }
-    }
-  }
-}
-
 struct NoSegments {};
 template <int TYPE, int ACCUM, int XHALF, int NW, int TN = TN2, int MOE = 0, int HYB = 0, int SEG = 0,
-          typename SG = NoSegments, int WR = 1, int DEEP = 0>
+          typename SG = NoSegments>
 SK_DEV void matmul_tile128_w(const uint4 *__restrict__ w, const uint16_t *__restrict__ wd, const void *x,
                              float *y, const uint32_t *ctl, const MatmulPush &p0, float *ws = nullptr,
                              uint32_t *cnt = nullptr, uint32_t S = 1, uint32_t hf = 0, uint32_t hz = 1,
                              const SG &segs = SG{}) {
-  static_assert(NW == 4 || TN == TN2 || WR == 2, "eight waves split a 128-token tile");
+  static_assert(NW == 4 || TN == TN2, "eight waves split a 128-token tile");
   // XHALF = 3: the f16 rows of x_half_rows and the K-quant weights loaded straight into LDS
   constexpr bool DL = XHALF == 3;
-  static_assert(!DL || (TYPE != 0 && TN == TN2 && !MOE) || (WR == 2 && NW == 8 && TN == 64 && !MOE && !HYB),
-                "direct-to-LDS form");
-  static_assert(WR == 1 || DL, "the 256-row tile is a direct-to-LDS form");
-  static_assert(!DEEP || (DL && NW == 8 && WR == 1 && TN == TN2), "the deep ring: eight-wave 128 x 128 tile");
-  // WR = 2: eight waves of 32 rows x 64 tokens over a 256-row x 64-token tile, so each
-  // wave dequantises its own rows (the 128-row eight-wave tile has two waves per row block)
-  constexpr bool W2 = NW == 8 && WR == 1;  // two waves per row block
+  static_assert(!DL || (TYPE != 0 && TN == TN2 && !MOE), "direct-to-LDS form");
+  constexpr bool W2 = NW == 8;  // two waves per row block
   constexpr int NT = 64 * NW;
   constexpr int NB = W2 ? 2 : TN / 32;  // 32-token blocks per wave
   constexpr int KX = DL ? DL_KX : (NW == 8 || TN < TN2) ? KX_W : 128, PITCH2 = pitch2<KX>();
   constexpr uint32_t PW = WLds<TYPE, NT>::PW;
-  __shared__ __attribute__((aligned(16))) f16 xs[DL ? (DEEP ? 4 : 2) * TN * DL_KX : TN * PITCH2];
-  __shared__ __attribute__((aligned(16))) uint32_t wl[DL ? (DEEP ? 3 : 2) * 256 * dl_wblocks<TYPE, WR>() + (DEEP ? 256 : 0)
-                                                        : TM * PW / 4];
+  __shared__ __attribute__((aligned(16))) f16 xs[DL ? 2 * TN * DL_KX : TN * PITCH2];
+  __shared__ __attribute__((aligned(16))) uint32_t wl[DL ? 2 * 256 * dl_wblocks<TYPE>() : TM * PW / 4];
   __shared__ uint32_t xrow[TN];
   __shared__ uint32_t yrow[TN];
   __shared__ int xexp[TN];
@@ -1124,7 +1006,7 @@ SK_DEV void matmul_tile128_w(const uint4 *__restrict__ w, const uint16_t *__rest
   }
   const uint32_t e = MOE ? blockIdx.y : 0;
   const uint32_t base = MOE ? e * p.n_out : 0;
-  const uint32_t row0 = rt * TM * WR;
+  const uint32_t row0 = rt * TM;
   const uint32_t n_all = MOE ? ctl[p.table_off + 2 * e] : ctl[2];
   const uint32_t col0 = tt * TN;
   if (col0 >= n_all) return;
@@ -1160,8 +1042,8 @@ SK_DEV void matmul_tile128_w(const uint4 *__restrict__ w, const uint16_t *__rest
     // other weight buffer (last read in the stage before).  vmcnt counts a wave's loads in
     // issue order, so before each barrier a wave waits for its loads of the chunk, letting
     // only the weight loads issued after them stay in flight.
-    constexpr uint32_t XB = TN * DL_KX, WB = 256 * dl_wblocks<TYPE, WR>();
-    using DL_L = DLLanes<NW, TYPE, TN, WR>;
+    constexpr uint32_t XB = TN * DL_KX, WB = 256 * dl_wblocks<TYPE>();
+    using DL_L = DLLanes<NW, TYPE, TN>;
     DL_L L;
     L.wv = __builtin_amdgcn_readfirstlane(wave);
     L.lane = lane;
@@ -1184,17 +1066,13 @@ SK_DEV void matmul_tile128_w(const uint4 *__restrict__ w, const uint16_t *__rest
       L.xo[i] = 2u * (p.x_off + xrow[r] * p.x_stride + 8u * ((lane & 7) ^ dl_swz(r)));
     }
 #pragma unroll
-    for (int i = 0; i < DL_L::WS; i++) dl_wpiece<TYPE, WR>(NW * i + L.wv, lane, p, row0, L.wo[i], L.wm[i]);
-    if constexpr (DEEP) {
-      dl_run_deep<NW, TYPE, NB>(L, acc, xs, wl, wl + 3 * WB, n_stage, kbase, st0);
-    } else {
-      dl_issue_x(L, xs, kbase);
-      dl_issue_w(L, wl, st0);
-      for (uint32_t st = 0; st < n_stage; st++) {
-        const uint32_t b = st & 1;
-        dl_stage<NW, TYPE, NB, TN, WR>(L, acc, xs, xs + XB, wl + b * WB, wl + (b ^ 1) * WB, st + 1 < n_stage,
-                                       kbase + KC * st, st0 + st + 1);
-      }
+    for (int i = 0; i < DL_L::WS; i++) dl_wpiece<TYPE>(NW * i + L.wv, lane, p, row0, L.wo[i], L.wm[i]);
+    dl_issue_x(L, xs, kbase);
+    dl_issue_w(L, wl, st0);
+    for (uint32_t st = 0; st < n_stage; st++) {
+      const uint32_t b = st & 1;
+      dl_stage<NW, TYPE, NB, TN>(L, acc, xs, xs + XB, wl + b * WB, wl + (b ^ 1) * WB, st + 1 < n_stage,
+                                 kbase + KC * st, st0 + st + 1);
     }
   } else {
   WLds<TYPE, NT> wr;
@@ -1628,44 +1506,6 @@ MMH8D(1, 0)
 MMH8D(1, 1)
 MMH8D(2, 0)
 MMH8D(2, 1)
-
-// The 256-row x 64-token eight-wave tile (WR = 2; operands straight into LDS), for K-split
-// launches (x8w) and segments (x8ws): each wave dequantises its own 32 rows.
-#define MMH8W(T, A)                                                                               \
-  extern "C" __global__ __launch_bounds__(512) void matmul_x8w__##T##_##A(                         \
-      const uint4 *w, const uint16_t *wd, const f16 *x, float *y, const uint32_t *ctl,            \
-      MatmulPush p, float *ws, uint32_t *cnt, uint32_t S) {                                       \
-    matmul_tile128_w<T, A, 3, 8, 64, 0, 0, 0, NoSegments, 2>(w, wd, x, y, ctl, p, ws, cnt, S);    \
-  }                                                                                               \
-  extern "C" __global__ __launch_bounds__(512) void matmul_x8ws__##T##_##A(                        \
-      const uint4 *w, const uint16_t *wd, const f16 *x, float *y, const uint32_t *ctl,            \
-      Segments<MatmulPush> m, float *ws, uint32_t *cnt, uint32_t S) {                              \
-    matmul_tile128_w<T, A, 3, 8, 64, 0, 0, 1, Segments<MatmulPush>, 2>(w, wd, x, y, ctl, m.p[0], ws, cnt, S, 0, \
-                                                                       1, m);                    \
-  }
-MMH8W(1, 0)
-MMH8W(1, 1)
-MMH8W(2, 0)
-MMH8W(2, 1)
-
-// The eight-wave 128 x 128 direct-to-LDS tile on the deeper ring (dl_run_deep): K-split
-// launches (x8e) and segments (x8es).
-#define MMH8E(T, A)                                                                               \
-  extern "C" __global__ __launch_bounds__(512) void matmul_x8e__##T##_##A(                         \
-      const uint4 *w, const uint16_t *wd, const f16 *x, float *y, const uint32_t *ctl,            \
-      MatmulPush p, float *ws, uint32_t *cnt, uint32_t S) {                                       \
-    matmul_tile128_w<T, A, 3, 8, TN2, 0, 0, 0, NoSegments, 1, 1>(w, wd, x, y, ctl, p, ws, cnt, S); \
-  }                                                                                               \
-  extern "C" __global__ __launch_bounds__(512) void matmul_x8es__##T##_##A(                        \
-      const uint4 *w, const uint16_t *wd, const f16 *x, float *y, const uint32_t *ctl,            \
-      Segments<MatmulPush> m, float *ws, uint32_t *cnt, uint32_t S) {                              \
-    matmul_tile128_w<T, A, 3, 8, TN2, 0, 0, 1, Segments<MatmulPush>, 1, 1>(w, wd, x, y, ctl, m.p[0], ws, cnt, S, \
-                                                                           0, 1, m);             \
-  }
-MMH8E(1, 0)
-MMH8E(1, 1)
-MMH8E(2, 0)
-MMH8E(2, 1)
 
 // The eight-wave tile on f16 rows over up to four matrices that read the same rows
 // (segment table as the matvecs take it; start[] counts row tiles).

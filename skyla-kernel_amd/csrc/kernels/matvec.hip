@@ -176,7 +176,7 @@ struct GeoQ4 {
 
 template <int WAVES, int ACCUM, int ROWS, int MOE, int LPR, int MODE = 0, typename P = MatvecPush2>
 SK_DEV void matvec_q4k_body(const uint4 *__restrict__ w, const float *x, float *y,
-                            const uint32_t *ids, const P &p, uint32_t bx, uint32_t *cnt = nullptr) {
+                            const uint32_t *ids, const P &p, uint32_t bx) {
   using G = GeoQ4<WAVES, ROWS, LPR>;
   constexpr int CHU = G::CHU, PF = G::PF;
   __shared__ float4 xf[8][CHU];  // component-major: lanes read consecutive 16 B
@@ -187,11 +187,6 @@ SK_DEV void matvec_q4k_body(const uint4 *__restrict__ w, const float *x, float *
   // the second half the up rows of the same outputs, and the store writes silu(g) * u.
   // MODE 4: MODE 3 with the FFN RMSNorm folded in as MODE 2 folds it (x * w staged, r
   // applied to the gate and up sums before the SiLU).
-  // MODE 5 (an expert down projection with moe_combine after it, MOE = 1): each slot's rows
-  // are stored with agent-scope (coherent) stores, which complete before the workgroup
-  // counts itself in cnt[bx]; the last of the grid.y slots to arrive reads the other slots'
-  // rows with agent-scope loads, adds sum_s w_s * y_s to the residual for those rows in
-  // moe_combine's order (moe_combine.comp:16-27), and resets the count.
   constexpr bool PAIR = MODE == 3 || MODE == 4, AUX = MODE == 1 || MODE == 2 || MODE == 4;
   constexpr int OUT = PAIR ? G::RWG / 2 : G::RWG;  // outputs per workgroup
   __shared__ float ush[PAIR ? OUT : 1];
@@ -375,32 +370,6 @@ SK_DEV void matvec_q4k_body(const uint4 *__restrict__ w, const float *x, float *
         const float g = tot[r];
         y[y_off + first + r] = g / (1.0f + expf(-g)) * ush[lrow0 + r];  // silu_mul.comp:15-23
       }
-  } else if constexpr (MODE == 5) {
-    __shared__ bool last;
-#pragma unroll
-    for (int r = 0; r < ROWS; r++) {
-      const float total = lane_sum<LPR>(acc[r]);
-      if (lane == 0 && first + r < p.n_out)
-        __hip_atomic_store(y + y_off + first + r, total, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    __builtin_amdgcn_s_waitcnt(0);  // each wave's coherent stores complete before the barrier
-    __syncthreads();
-    if (tid == 0) last = __hip_atomic_fetch_add(&cnt[bx], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.y - 1;
-    __syncthreads();
-    if (!last) return;
-    for (uint32_t t = tid; t < (uint32_t)G::RWG; t += G::NT) {
-#pragma clang fp contract(off)
-      const uint32_t row = row0 + t;
-      if (row >= p.n_out) continue;
-      float sum = 0.0f;
-      for (uint32_t s = 0; s < p.n_used; s++) {
-        const float ys = __hip_atomic_load(y + p.y_off + s * p.y_stride + row, __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT);
-        sum += y[p.w_off + s] * ys;
-      }
-      y[p.res_off + row] += sum;
-    }
-    if (tid == 0) __hip_atomic_store(&cnt[bx], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   } else {
     store_rows<ACCUM, ROWS, LPR>(y, y_off, first, p.n_out, lane, acc, yold);
   }
@@ -688,179 +657,6 @@ SK_DEV void matvec_q4k_dcomb_body(const uint4 *__restrict__ w, float *a, const u
 }
 
 // ---------------------------------------------------------------------------------------
-// Q4_K on the matrix cores, n_in = 4096 (matvec_q4k_mf__A_G): the K-split geometry of
-// matvec_q4k_ks_body -- wave w takes super-blocks 2w and 2w + 1 of 16 rows at a time, the
-// eight wave partials meet in LDS and are added in wave order -- with the products on
-// v_mfma_f32_16x16x32_f16, D[m][n] = sum over 32 values k of A[m][k] B[k][n]:
-//   A = the exact integer q * sc (4-bit quant times its 6-bit sub-block scale: at most 945,
-//       an exact f16), made from the packed nibbles with one and-or per pair (0x6400 | q is
-//       the f16 1024 + q; 0x6400 | 16 q is 1024 + 16 q) and one packed f16 FMA,
-//       (1024 + q) sc - 1024 sc or (1024 + 16 q) sc / 16 - 64 sc, rounded once from q sc;
-//   B column 0 = x_hi = f16(x 2^e), column 1 = x_lo = f16(x 2^e - x_hi) (the other columns
-//       are not read back); 2^e puts the wave's largest |x| in [2^13, 2^14), so x_hi + x_lo
-//       holds x to 2^-22 of itself (or 2^-38 of the wave's largest) and nothing overflows.
-// A super-block's row sum is then d (D[m][0] + D[m][1]) 2^-e, less the minimum terms
-// dmin * sum_j m_j * (sum of x over sub-block j) in f32 (quant.rs:56-66, regrouped as the
-// f32 forms do).  9 VALU instructions per 8 values instead of ~20.
-//
-// Lane (m = l % 16, kg = l / 16) loads bytes [16 kg, +16) and [64 + 16 kg, +16) of row m's
-// 128 qs bytes of each super-block: its words 0..3 lie in chunk kg / 2, words 4..7 in chunk
-// 2 + kg / 2 (chunk c: 32 bytes holding the low nibbles of sub-block 2c and the high
-// nibbles of sub-block 2c + 1).  Word j is the lane's A for step j of the super-block, its
-// eight values in A's element order: the low nibbles of bytes 0 and 2, their high nibbles,
-// then the same of bytes 1 and 3.  Lane (n, kg) of B holds the activations of the same
-// positions, staged once per workgroup through LDS (bq) in that order.
-// ---------------------------------------------------------------------------------------
-typedef _Float16 h2v __attribute__((ext_vector_type(2)));
-typedef _Float16 h8v __attribute__((ext_vector_type(8)));
-typedef float f4v __attribute__((ext_vector_type(4)));
-
-// the two f16 constants that turn a nibble pair into q * sc: low nibbles (1024 + q) and
-// high nibbles (1024 + 16 q)
-struct NibScale {
-  h2v lo_mul, lo_add, hi_mul, hi_add;
-};
-SK_DEV NibScale nib_scale(uint32_t sc_lo, uint32_t sc_hi) {
-  const _Float16 a = (_Float16)(float)sc_lo, b = (_Float16)((float)sc_hi * 0.0625f);
-  const _Float16 c = (_Float16)(-1024.0f * (float)sc_lo), d = (_Float16)(-64.0f * (float)sc_hi);
-  return {h2v{a, a}, h2v{c, c}, h2v{b, b}, h2v{d, d}};
-}
-// A of one word: its eight values times their sub-block scales, exact
-SK_DEV h8v nib_a(uint32_t w, const NibScale &k, uint32_t M1, uint32_t M2, uint32_t F) {
-  const uint32_t t = w >> 8;
-  const h2v p0 = __builtin_elementwise_fma(__builtin_bit_cast(h2v, (w & M1) | F), k.lo_mul, k.lo_add);
-  const h2v p1 = __builtin_elementwise_fma(__builtin_bit_cast(h2v, (w & M2) | F), k.hi_mul, k.hi_add);
-  const h2v p2 = __builtin_elementwise_fma(__builtin_bit_cast(h2v, (t & M1) | F), k.lo_mul, k.lo_add);
-  const h2v p3 = __builtin_elementwise_fma(__builtin_bit_cast(h2v, (t & M2) | F), k.hi_mul, k.hi_add);
-  return h8v{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
-}
-
-template <int ACCUM, int NG, typename P = MatvecPush2>
-SK_DEV void matvec_q4k_mf_body(const uint4 *__restrict__ w, const float *x, float *y, const P &p, uint32_t bx) {
-  constexpr int OUT = 16 * NG;
-  __shared__ uint4 bq[8][2][2][8][4];  // per wave: [column][super-block][step][kg], 8 f16 each
-  __shared__ float xsum[8][16];        // per wave: its 16 sub-block sums of x
-  __shared__ float cs[8][2][16];       // per wave: D[m][0] + D[m][1] per (super-block, row)
-  __shared__ float part[8][OUT];
-
-  const uint32_t tid = threadIdx.x, wv = tid >> 6, l = tid & 63;
-  const uint32_t m = l & 15, kg = l >> 4, h = kg >> 1;
-  const uint32_t out0 = bx * OUT;
-  // masks in SGPRs, the exponent bits in a VGPR: v_and_or_b32 reads one scalar operand
-  const uint32_t M1 = opaque_mask(0x000f000fu), M2 = opaque_mask(0x00f000f0u);
-  uint32_t F;
-  asm volatile("v_mov_b32 %0, %1" : "=v"(F) : "i"(0x64006400));
-
-  uint4 q[2][2][2], hd[2][2];  // [buffer][super-block][half] qs, [buffer][super-block] header
-  auto load_group = [&](uint32_t g, uint32_t b) {
-    const uint32_t r = min(out0 + g * 16 + m, p.n_out - 1);
-#pragma unroll
-    for (int s = 0; s < 2; s++) {
-      const uint32_t sb = 2 * wv + s;
-      q[b][s][0] = w[p.o0 + (size_t)r * 128 + sb * 8 + kg];
-      q[b][s][1] = w[p.o0 + (size_t)r * 128 + sb * 8 + 4 + kg];
-      hd[b][s] = w[p.o1 + (size_t)r * 16 + sb];
-    }
-  };
-
-  // the wave's 512 activations: lane l holds values 8 l .. 8 l + 7 (super-block l / 32)
-  const float *xv = x + p.x_off + 512 * wv;
-  const float4 a0 = *(const float4 *)(xv + 8 * l), a1 = *(const float4 *)(xv + 8 * l + 4);
-  load_group(0, 0);
-  {
-    const float va[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-    float mx = 0.0f, sm = 0.0f;
-#pragma unroll
-    for (int t = 0; t < 8; t++) {
-      mx = fmaxf(mx, fabsf(va[t]));
-      sm += va[t];
-    }
-    // sub-block sums (32 values = 4 lanes) and the wave's largest |x|
-    sm += __shfl_xor(sm, 1, 64);
-    sm += __shfl_xor(sm, 2, 64);
-    if ((l & 3) == 0) xsum[wv][l >> 2] = sm;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) mx = fmaxf(mx, __shfl_xor(mx, d, 64));
-    const int e = 14 - __builtin_amdgcn_frexp_expf(mx);
-    // hi / lo halves into B order: value v of a super-block -> chunk c = v / 64, high half
-    // hf, position p = v % 32 rounded down to 4, byte r = v % 4 -> (kg, step, element)
-    const uint32_t s = l >> 5, v0 = 8 * (l & 31);
-    const uint32_t c = v0 >> 6, hf = (v0 >> 5) & 1;
-    _Float16 *bh = (_Float16 *)&bq[wv][0][s][0][0], *bl = (_Float16 *)&bq[wv][1][s][0][0];
-#pragma unroll
-    for (int t = 0; t < 8; t++) {
-      const uint32_t pp = (v0 & 24) + (t & 4), r = t & 3;
-      const uint32_t kgv = 2 * (c & 1) + (pp >> 4), j = 4 * (c >> 1) + ((pp >> 2) & 3);
-      const uint32_t el = (r & 1) * 4 + hf * 2 + (r >> 1);
-      const float xs = __builtin_ldexpf(va[t], e);
-      const _Float16 hi = (_Float16)xs;
-      const _Float16 lo = (_Float16)(xs - (float)hi);
-      bh[(j * 4 + kgv) * 8 + el] = hi;
-      bl[(j * 4 + kgv) * 8 + el] = lo;
-    }
-    cs[wv][0][0] = __builtin_bit_cast(float, e);  // the wave's scale exponent, read back below
-  }
-  const int e = __builtin_bit_cast(int, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, cs[wv][0][0])));
-  // this lane's minimum sums: chunk kg of each super-block (sub-blocks 2 kg, 2 kg + 1)
-  const float xa0 = xsum[wv][2 * kg], xb0 = xsum[wv][2 * kg + 1];
-  const float xa1 = xsum[wv][8 + 2 * kg], xb1 = xsum[wv][8 + 2 * kg + 1];
-  const uint32_t bcol = m == 1 ? 1u : 0u;  // B lanes of column 0 and 1 (others: any values)
-
-#pragma unroll
-  for (int g = 0; g < NG; g++) {
-    const int b = g & 1;
-    if (g + 1 < NG) load_group(g + 1, b ^ 1);
-    float dsb[2], bias = 0.0f;
-#pragma unroll
-    for (int s = 0; s < 2; s++) {
-      const uint4 hc = hd[b][s];
-      const float d = f16_bits_to_f32(hc.x & 0xffffu), dmin = f16_bits_to_f32(hc.x >> 16);
-      const uint32_t sw0 = hc.y & 0x3f3f3f3fu, sw1 = (hc.w & 0x0f0f0f0fu) | ((hc.y >> 2) & 0x30303030u);
-      const uint32_t mw0 = hc.z & 0x3f3f3f3fu, mw1 = ((hc.w >> 4) & 0x0f0f0f0fu) | ((hc.z >> 2) & 0x30303030u);
-      // scales of chunks kg / 2 (words 0..3) and 2 + kg / 2 (words 4..7)
-      const NibScale k0 = nib_scale((sw0 >> (16 * h)) & 255u, (sw0 >> (16 * h + 8)) & 255u);
-      const NibScale k1 = nib_scale((sw1 >> (16 * h)) & 255u, (sw1 >> (16 * h + 8)) & 255u);
-      // minimum terms of chunk kg
-      const uint32_t mv = (kg < 2 ? mw0 : mw1) >> (16 * (kg & 1));
-      const float xa = s ? xa1 : xa0, xb = s ? xb1 : xb0;
-      bias = __builtin_fmaf(dmin, __builtin_fmaf((float)(mv & 255u), xa, (float)((mv >> 8) & 255u) * xb), bias);
-      dsb[s] = d;
-      const uint32_t wd[8] = {q[b][s][0].x, q[b][s][0].y, q[b][s][0].z, q[b][s][0].w,
-                              q[b][s][1].x, q[b][s][1].y, q[b][s][1].z, q[b][s][1].w};
-      f4v acc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-      for (int j = 0; j < 8; j++) {
-        const h8v bv = __builtin_bit_cast(h8v, bq[wv][bcol][s][j][kg]);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(nib_a(wd[j], j < 4 ? k0 : k1, M1, M2, F), bv, acc, 0, 0, 0);
-      }
-      // D[4 kg + i][m] in lane (m, kg): columns 0 and 1 are lanes 16 kg and 16 kg + 1
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const float v = acc[i] + dpp_f<0xb1>(acc[i]);  // + the neighbouring column
-        if (m == 0) cs[wv][s][4 * kg + i] = v;
-      }
-    }
-    bias += __shfl_xor(bias, 16, 64);
-    bias += __shfl_xor(bias, 32, 64);
-    if (kg == 0) {
-      const float t = __builtin_fmaf(dsb[1], cs[wv][1][m], dsb[0] * cs[wv][0][m]);
-      part[wv][g * 16 + m] = __builtin_ldexpf(t, -e) - bias;
-    }
-  }
-  __syncthreads();
-  if (tid < (uint32_t)OUT && out0 + tid < p.n_out) {
-    float t = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 8; i++) t += part[i][tid];
-    const uint32_t yo = p.y_off + out0 + tid;
-    if (ACCUM)
-      y[yo] += t;
-    else
-      y[yo] = t;
-  }
-}
-
-// ---------------------------------------------------------------------------------------
 // Q6_K.  Lane step = 64 values of one super-block: u -> super-block u/4, half hf = (u%4)/2,
 // li = u%2.  It reads 16 B of ql at l = 16 li (a), 16 B at l + 32 (b) and 16 B of qh.
 // Group g = 0..3 is values 128 hf + 32 g + 16 li + [0,16) with scale sc[8 hf + li + 2g]
@@ -1045,96 +841,6 @@ SK_DEV void matvec_q6k_body(const uint4 *__restrict__ w, const uint16_t *__restr
   }
   norm_apply<MODE>(acc, ss, p);
   store_rows<ACCUM, ROWS, LPR>(y, y_off, first, p.n_out, lane, acc, yold);
-}
-
-// matvec_q4k_ks12_body -- K-split Q4_K rows of n_in = 12288 (matrix.rs matvec over
-// quant.rs:51-70 blocks): lane u = 64 wave + l of the three waves owns chunk c = u % 4 of
-// super-block u / 4 of every row, i.e. values 64 c .. 64 c + 63, the 32 qs bytes 32 c ..
-// 32 c + 31 (low nibbles for the first 32 values, high nibbles for the rest: sub-blocks 2 c
-// and 2 c + 1).  Its 64 activations and their two sums are loaded once, into registers; per
-// row it loads the chunk's qs and its super-block's header (four lanes share one), decodes
-// its two (scale, min) pairs as q4k_scale_min does, and the row's sum meets over the wave
-// with DPP and over the three waves in LDS, in wave order.  RPL rows per row-group, NG
-// row-groups per workgroup, operands loaded PD row-groups ahead.
-template <int ACCUM, int RPL, int NG, int PD>
-SK_DEV void matvec_q4k_ks12_body(const uint4 *__restrict__ w, const float *x, float *y, const MatvecPush2 &p,
-                                 uint32_t bx) {
-  constexpr int OUT = RPL * NG;                     // rows per workgroup
-  constexpr uint32_t SUPERS = 48, UNITS = 384;      // per row (n_in = 12288, checked by the host)
-  __shared__ float part[3][OUT];
-
-  const uint32_t tid = threadIdx.x, wv = tid >> 6, l = tid & 63;
-  const uint32_t u = wv * 64 + l;
-  const uint32_t sb = u >> 2, c = u & 3;
-  const uint32_t LO4 = opaque_mask(0x0f0f0f0fu), HI4 = opaque_mask(0xf0f0f0f0u);
-  const uint32_t out0 = bx * OUT;
-
-  struct RowQ {
-    uint4 a, b, h;
-  };
-  auto load_group = [&](uint32_t g, RowQ (&q)[RPL]) {
-#pragma unroll
-    for (int r = 0; r < RPL; r++) {
-      const uint32_t row = min(out0 + g * RPL + r, p.n_out - 1);
-      q[r].a = w[p.o0 + row * UNITS + sb * 8 + 2 * c];
-      q[r].b = w[p.o0 + row * UNITS + sb * 8 + 2 * c + 1];
-      q[r].h = w[p.o1 + row * SUPERS + sb];
-    }
-  };
-
-  // activations first: values 64 c + [0, 32) (low nibbles) and + [32, 64) (high)
-  const float *xv = x + p.x_off + sb * 256 + 64 * c;
-  float4 xl[2][4], xh[2][4];
-#pragma unroll
-  for (int h = 0; h < 2; h++)
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-      xl[h][k] = *(const float4 *)(xv + 16 * h + 4 * k);
-      xh[h][k] = *(const float4 *)(xv + 32 + 16 * h + 4 * k);
-    }
-  RowQ q[NG][RPL];  // row-group g's operands, loaded PD groups ahead of its arithmetic
-#pragma unroll
-  for (int g = 0; g < PD && g < NG; g++) load_group(g, q[g]);
-  // an accumulating launch reads its old outputs now, so the store at the end waits for none
-  float yold = 0.0f;
-  if constexpr (ACCUM)
-    if (tid < (uint32_t)OUT && out0 + tid < p.n_out) yold = y[p.y_off + out0 + tid];
-  const float sl = (sum4(xl[0][0]) + sum4(xl[0][1])) + (sum4(xl[0][2]) + sum4(xl[0][3])) +
-                   ((sum4(xl[1][0]) + sum4(xl[1][1])) + (sum4(xl[1][2]) + sum4(xl[1][3])));
-  const float sh = (sum4(xh[0][0]) + sum4(xh[0][1])) + (sum4(xh[0][2]) + sum4(xh[0][3])) +
-                   ((sum4(xh[1][0]) + sum4(xh[1][1])) + (sum4(xh[1][2]) + sum4(xh[1][3])));
-
-#pragma unroll
-  for (int g = 0; g < NG; g++) {
-    if (g + PD < NG) load_group(g + PD, q[g + PD]);
-    const RowQ (&qc)[RPL] = q[g];
-#pragma unroll
-    for (int r = 0; r < RPL; r++) {
-      float sa = fma_bytes16(qc[r].a, LO4, xl[0], 0.0f);
-      sa = fma_bytes16(qc[r].b, LO4, xl[1], sa);
-      float sb16 = fma_bytes16(qc[r].a, HI4, xh[0], 0.0f);  // 16 q: the 1/16 is in the scale
-      sb16 = fma_bytes16(qc[r].b, HI4, xh[1], sb16);
-      uint32_t sc0, m0, sc1, m1;
-      q4k_scale_min(2 * c, qc[r].h.y, qc[r].h.z, qc[r].h.w, sc0, m0);
-      q4k_scale_min(2 * c + 1, qc[r].h.y, qc[r].h.z, qc[r].h.w, sc1, m1);
-      const float d = f16_bits_to_f32(qc[r].h.x & 0xffffu), dmin = f16_bits_to_f32(qc[r].h.x >> 16);
-      float v = (d * (float)sc0) * sa;
-      v = __builtin_fmaf(d * 0.0625f * (float)sc1, sb16, v);
-      v = __builtin_fmaf(-(dmin * (float)m0), sl, v);
-      v = __builtin_fmaf(-(dmin * (float)m1), sh, v);
-      v = lane_sum<64>(v);
-      if (l == 0) part[wv][g * RPL + r] = v;
-    }
-  }
-  __syncthreads();
-  if (tid < (uint32_t)OUT && out0 + tid < p.n_out) {
-    const float t = (part[0][tid] + part[1][tid]) + part[2][tid];
-    const uint32_t yo = p.y_off + out0 + tid;
-    if (ACCUM)
-      y[yo] = yold + t;
-    else
-      y[yo] = t;
-  }
 }
 
 // ---------------------------------------------------------------------------------------
@@ -1547,22 +1253,6 @@ MV_Q4K_KS_ALL(4, 6)
 MV_Q4K_KS_ALL(8, 1)
 MV_Q4K_KS_ALL(8, 3)
 
-// K-split Q4_K form for n_in = 12288 (matvec_q4k_ks12_body): RPL rows per row-group, NG
-// row-groups per workgroup of three waves, loaded D row-groups ahead
-#define MV_Q4K_KS12(A, R, G, D)                                                              \
-  extern "C" __global__ __launch_bounds__(192) void matvec_q4k_ks12__##A##_##R##_##G##_##D(   \
-      const uint4 *w, const float *x, float *y, const uint32_t *ids, Segments<MatvecPush2> m) { \
-    const uint32_t s = segment_of(m, blockIdx.x);                                             \
-    (void)ids;                                                                                \
-    matvec_q4k_ks12_body<A, R, G, D>(w, x, y, segment_push(m, s), blockIdx.x - m.start[s]);   \
-  }
-#define MV_Q4K_KS12_ALL(R, G, D) MV_Q4K_KS12(0, R, G, D) MV_Q4K_KS12(1, R, G, D)
-MV_Q4K_KS12_ALL(1, 8, 1)
-MV_Q4K_KS12_ALL(1, 8, 2)
-MV_Q4K_KS12_ALL(2, 4, 1)
-MV_Q4K_KS12_ALL(1, 16, 1)
-MV_Q4K_KS12_ALL(2, 8, 1)
-
 // K-split Q6_K form for n_in = 12288 (matvec_q6k_ks_body): RPL rows per row-group, NG
 // row-groups per workgroup of three waves, loaded D row-groups ahead
 #define MV_Q6K_KS(A, R, G, D)                                                                \
@@ -1581,25 +1271,10 @@ MV_Q6K_KS_ALL(1, 16, 2)
 MV_Q6K_KS_ALL(2, 4, 2)
 MV_Q6K_KS_ALL(8, 1, 1)
 
-// Q4_K on the matrix cores for n_in = 4096 (matvec_q4k_mf_body): NG groups of 16 rows per
-// workgroup
-#define MV_Q4K_MF(A, G)                                                                      \
-  extern "C" __global__ __launch_bounds__(512) void matvec_q4k_mf__##A##_##G(                  \
-      const uint4 *w, const float *x, float *y, const uint32_t *ids, Segments<MatvecPush2> m) { \
-    const uint32_t s = segment_of(m, blockIdx.x);                                            \
-    (void)ids;                                                                               \
-    matvec_q4k_mf_body<A, G>(w, x, y, segment_push(m, s), blockIdx.x - m.start[s]);          \
-  }
-MV_Q4K_MF(0, 1)
-MV_Q4K_MF(1, 1)
-MV_Q4K_MF(0, 2)
-MV_Q4K_MF(1, 2)
-MV_Q4K_MF(0, 4)
-MV_Q4K_MF(1, 4)
-
-// MoE decode forms the runtime substitutes for engine dispatch pairs (skyla_hip.cpp,
+// MoE decode forms the runtime substitutes for engine dispatch runs (skyla_hip.cpp,
 // fuse_moe): an expert's gate and up with silu_mul after them (MODE 3 over the slot grid),
-// and an expert down projection with moe_combine after it (MODE 5, counters in `cnt`).
+// the same with moe_route's selection in front, and an expert down projection with
+// moe_combine after it.
 extern "C" __global__ __launch_bounds__(256) void matvec_q4k_glu__4_0_1_1_16(
     const uint4 *w, const float *x, float *y, const uint32_t *ids, Segments<MatvecPushGlu> m) {
   const uint32_t s = segment_of(m, blockIdx.x);
@@ -1619,7 +1294,7 @@ extern "C" __global__ __launch_bounds__(256) void matvec_q4k_glur__4_0_1_1_16(
     RoutePush rp = pp.r;
     rp.ids_off = 0;
     rp.weights_off = 0;
-    route_token<false>(y, swt, sid, rp, 0, threadIdx.x);
+    route_token(y, swt, sid, rp, 0, threadIdx.x);
     if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x < min(pp.r.n_used, 16u)) {
       ids[pp.r.ids_off + threadIdx.x] = sid[threadIdx.x];
       y[pp.r.weights_off + threadIdx.x] = swt[threadIdx.x];
@@ -1635,9 +1310,4 @@ extern "C" __global__ __launch_bounds__(256) void matvec_q4k_dcomb__8(
     const uint4 *w, const float *x, float *y, const uint32_t *ids, Segments<MatvecPushComb> m) {
   (void)x;  // the arena is bound as x, y and ids; y is its writable view
   matvec_q4k_dcomb_body<8>(w, y, ids, m.p[0], blockIdx.x);
-}
-extern "C" __global__ __launch_bounds__(256) void matvec_q4k_ecomb__4_1_16(
-    const uint4 *w, const float *x, float *y, const uint32_t *ids, Segments<MatvecPushComb> m, uint32_t *cnt) {
-  const uint32_t s = segment_of(m, blockIdx.x);
-  matvec_q4k_body<4, 0, 1, 1, 16, 5>(w, x, y, ids, segment_push(m, s), blockIdx.x - m.start[s], cnt);
 }

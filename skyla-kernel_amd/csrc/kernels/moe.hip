@@ -15,12 +15,6 @@ struct SortPush { uint32_t ids_off, table_off, list_off, n_expert, n_used; };
 struct CombinePush { uint32_t x_off, y_off, weights_off, n, stride, n_used; };
 struct SiluPush { uint32_t g_off, u_off, n, stride; };
 struct HalfPush { uint32_t src_off, dst_off, n, src_stride, dst_stride, per_token; };
-// moe_logits_route: moe_logits's words, then moe_route's (one by-value argument)
-struct LogitsRoutePush {
-  LogitsPush lp;
-  RoutePush rp;
-};
-
 }  // namespace
 
 // moe_logits (moe_logits.comp:18-31): logits[tok * n_expert + e] = router_e . x_tok, one
@@ -105,47 +99,7 @@ extern "C" __global__ __launch_bounds__(64) void moe_route(float *a, uint32_t *i
   const uint32_t tok = blockIdx.y;
   const uint32_t n_tok = __builtin_bit_cast(uint32_t, a[2]);
   if (tok >= n_tok) return;
-  route_token<false>(a, a, ids, p, tok, threadIdx.x);
-}
-
-// moe_logits then moe_route of one decode token in one launch (the runtime fuses the pair
-// when the engine records them back to back; no counterpart kernel in the reference).
-// Grid [n_expert, 1, 1]: each workgroup computes its logit exactly as moe_logits does and
-// stores it with an agent-scope (coherent, sc1) store, waits for it to complete and counts
-// the workgroup in cnt[0]; the last of the n_expert workgroups reads every logit back with
-// agent-scope loads (served past the XCD's L2, so no invalidate is needed), runs
-// moe_route's selection on its first wave and resets the counter.  Same logits, ids and
-// weights, bit for bit, as the two launches.  (An agent-scope release on the count writes
-// back the XCD's L2 from every workgroup: 33.5 against 26.5 us per config-4 layer.)
-extern "C" __global__ __launch_bounds__(256) void moe_logits_route(const float *w, float *a, uint32_t *ids,
-                                                                    LogitsRoutePush p, uint32_t *cnt) {
-  const LogitsPush &lp = p.lp;
-  const RoutePush &rp = p.rp;
-  __shared__ float part[4];
-  __shared__ bool last;
-  const uint32_t e = blockIdx.x, tid = threadIdx.x;
-  const float4 *row = (const float4 *)(w + lp.router_off + e * lp.n_embd);
-  const float4 *x = (const float4 *)(a + lp.x_off);
-  float s = 0.0f;
-  for (uint32_t i = tid; i < lp.n_embd / 4; i += 256) {
-    const float4 r = row[i], v = x[i];
-    s += r.x * v.x + r.y * v.y + r.z * v.z + r.w * v.w;
-  }
-  s = group_sum<64>(s);
-  if ((tid & 63) == 0) part[tid >> 6] = s;
-  __syncthreads();
-  if (tid == 0) {
-    __hip_atomic_store(a + lp.logits_off + e, part[0] + part[1] + part[2] + part[3], __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
-    __builtin_amdgcn_s_waitcnt(0);  // the coherent store is done before the count
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    last = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
-  }
-  __syncthreads();
-  if (!last || tid >= 64) return;
-  const uint32_t n_tok = __builtin_bit_cast(uint32_t, a[2]);
-  if (n_tok > 0) route_token<true>(a, a, ids, rp, 0, tid);
-  if (tid == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  route_token(a, a, ids, p, tok, threadIdx.x);
 }
 
 // moe_sort (moe_sort.comp:21-55): slot s = tok * n_used + k is routed to ids[s].  Writes

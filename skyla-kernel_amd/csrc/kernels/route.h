@@ -1,5 +1,5 @@
-// moe_route's selection (moe_route.comp:23-75), shared by moe.hip (moe_route, the fused
-// logits + route form) and matvec.hip (the experts' gate/up form that routes for itself).
+// moe_route's selection (moe_route.comp:23-75), shared by moe.hip (moe_route) and
+// matvec.hip (the experts' gate/up form that routes for itself).
 #pragma once
 
 #include "common.h"
@@ -30,9 +30,7 @@ SK_DEV uint32_t dpp_u(uint32_t v) {
 // holding it.  Lane k keeps round k's choice; the exponentials are computed in parallel
 // and summed in round order, as the reference does.
 // This is the selection for token `tok` on one wave (lane t), writing ids[ids_off + ..] and
-// aw[weights_off + ..].  COHERENT reads the logits with agent-scope loads (written by other
-// workgroups of the same launch).
-template <bool COHERENT>
+// aw[weights_off + ..].
 SK_DEV void route_token(const float *a, float *aw, uint32_t *ids, const RoutePush &p, uint32_t tok,
                         uint32_t t) {
   const uint32_t n_used = min(p.n_used, 16u);
@@ -45,8 +43,7 @@ SK_DEV void route_token(const float *a, float *aw, uint32_t *ids, const RoutePus
     const uint32_t e = t + 64 * j;
     float v = 0.0f;
     if (e < n_expert)
-      v = COHERENT ? __hip_atomic_load(a + logits_off + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                   : a[logits_off + e];
+      v = a[logits_off + e];
     key[j] = e < n_expert ? max(order_key(v), 1u) : 0u;
   }
   float chosen = 0.0f;

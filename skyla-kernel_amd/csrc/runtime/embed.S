@@ -15,5 +15,4 @@ EMBED(skyla_co_matmul, "matmul.hsaco")
 EMBED(skyla_co_moe, "moe.hsaco")
 EMBED(skyla_co_util, "util.hsaco")
 EMBED(skyla_co_attention, "attention.hsaco")
-EMBED(skyla_co_chain, "chain.hsaco")
     .section .note.GNU-stack,"",@progbits

@@ -17,7 +17,6 @@
 //   * Buffers are HBM allocations with a host mirror that the caller synchronises
 //     explicitly (the reference's buffers are host-coherent; a discrete GPU's are not).
 #include "../../../include/skyla_hip.h"
-#include "../kernels/chain_table.h"
 
 #include <hip/hip_runtime.h>
 
@@ -36,7 +35,6 @@ extern "C" const unsigned char skyla_co_matmul[], skyla_co_matmul_end[];
 extern "C" const unsigned char skyla_co_moe[], skyla_co_moe_end[];
 extern "C" const unsigned char skyla_co_util[], skyla_co_util_end[];
 extern "C" const unsigned char skyla_co_attention[], skyla_co_attention_end[];
-extern "C" const unsigned char skyla_co_chain[], skyla_co_chain_end[];
 
 namespace {
 
@@ -62,6 +60,61 @@ int fail(int code, const char *fmt, ...) {
 constexpr uint64_t kMaxBuffer = 4ull << 30;  // keeps u32 element offsets valid
 constexpr uint32_t kMaxMarks = 2048;          // skyla-vk/src/record.rs:6
 constexpr uint64_t kMaxPinned = 1ull << 30;   // host mirrors pinned up to this size
+
+// Tactics: every choice the runtime makes between kernel forms that compute the same
+// values, in one table.  The defaults are the forms measured fastest on MI355X; the
+// environment variable SKYLA_HIP_TACTIC="key=value,key=value" overrides entries (for
+// sweeps, and for the parity tests that run every compiled form).  Read when a pipeline is
+// created or a recording ends.
+struct Tactic {
+  const char *key, *def, *what;
+};
+const Tactic kTactics[] = {
+    {"fuse", "1", "independent dispatches of one kernel run as one segmented launch (0: one launch each)"},
+    {"retile", "1", "dense matvec launches take the variant the size rule gives them (0: the engine's)"},
+    {"variant", "", "W_R_L: every dense launch of a matvec kernel on that (waves, rows, lanes) variant"},
+    {"ks", "1", "K-split matvec forms for n_in 4096 (Q4_K) and 12288 (Q6_K); 0: none; R_G: Q4_K shape"},
+    {"ks6", "", "R_G_D: the Q6_K K-split form on that (rows, groups, groups ahead) shape"},
+    {"ksnorm", "", "R_G: the Q4_K K-split form with the RMSNorm folded in on that shape"},
+    {"ksglun", "1", "the norm-folded gate/up pair on its K-split form (0: LDS-staged form; R_G: shape)"},
+    {"moe_fuse", "26", "bit mask of the MoE decode forms (2 gate/up pair, 8 down + combine, 16 route + pair)"},
+    {"splitk", "1", "dense K-quant matmuls of at most 128 tiles split their super-blocks (0: never)"},
+    {"split_slots", "256", "workgroup slots a matmul K split fills (64..2048)"},
+    {"xhalf", "1", "f16 row prepass for matmuls on f32 rows: 1 four-wave tile where it fits, 4 without "
+                   "the balanced K halves, 8 eight-wave tile throughout, 0 the tile's own f32 staging"},
+    {"dl", "1", "matmul tiles with their operands loaded straight into LDS (0: register-staged)"},
+    {"merge_t", "1", "batched attention merge as one wave per (head, token) (0: 1024-thread form)"},
+    {"nograph", "0", "1: recordings replay as direct launches instead of one HIP graph (kernel traces)"},
+};
+
+// The value of tactic `key`: the last `key=value` entry of SKYLA_HIP_TACTIC, else the
+// table's default.  An unknown key is a programming error and reads as "".
+std::string tactic(const char *key) {
+  std::string v;
+  bool known = false;
+  for (const Tactic &t : kTactics)
+    if (std::strcmp(t.key, key) == 0) {
+      v = t.def;
+      known = true;
+    }
+  if (!known) return "";
+  const char *env = std::getenv("SKYLA_HIP_TACTIC");
+  if (!env) return v;
+  const std::string all(env), k = std::string(key) + "=";
+  size_t pos = 0;
+  while (pos <= all.size()) {
+    size_t end = all.find(',', pos);
+    if (end == std::string::npos) end = all.size();
+    const std::string item = all.substr(pos, end - pos);
+    if (item.compare(0, k.size(), k) == 0) v = item.substr(k.size());
+    pos = end + 1;
+  }
+  return v;
+}
+bool tactic_on(const char *key) {
+  const std::string v = tactic(key);
+  return !v.empty() && v != "0";
+}
 
 // Bindings, push words and workgroup shape of every kernel the engine creates
 // (kernels.rs:170-205; workgroup shapes as skyla-metal/src/pipeline.rs:14-24).
@@ -134,10 +187,7 @@ struct skyla_hip_context {
   char *scratch = nullptr;
   size_t scratch_bytes = 0;
   hipFunction_t fill_u32 = nullptr;
-  // chained decode matvecs (chain.hip): the kernel, and its grid (one workgroup per CU);
-  // null when a workgroup cannot be resident on every CU at once
-  hipFunction_t chain_fn = nullptr;
-  uint32_t n_cu = 0;
+  uint32_t n_cu = 256;  // compute units of the device (hipDeviceProp_t.multiProcessorCount)
   hipFunction_t x_half_rows = nullptr;  // f16 row prepass of dense K-quant matmuls (matmul.hip)
 };
 
@@ -191,8 +241,6 @@ struct skyla_hip_pipeline {
   hipFunction_t hx_fn = nullptr;         // and its variant on x_half_rows's f16 rows
   hipFunction_t hx4_fn = nullptr;        // the four-wave tile on those rows
   hipFunction_t hx4b_fn = nullptr;       // and over a balanced grid (some tiles in K halves)
-  hipFunction_t hxw_fn = nullptr;        // the 256-row x 64-token tile for K-split launches
-  hipFunction_t hxws_fn = nullptr;       // and for segments
   hipFunction_t hxs_fn = nullptr;        // the eight-wave tile over several matrices (segments)
   uint32_t split_threads = 0;
   hipFunction_t tok_fn = nullptr;        // batched form: a tok_per_wg x tok_per_wg_y block of
@@ -200,12 +248,9 @@ struct skyla_hip_pipeline {
   uint32_t tok_per_wg_y = 0;
   uint32_t tok_threads = 0;              // its workgroup size (0: the pipeline's)
   std::string name;                      // shader name
-  hipFunction_t moe_fn = nullptr;        // MoE decode forms (fuse_moe): moe_logits -> moe_logits_route,
-  hipFunction_t moe_fn2 = nullptr;       // Q4_K experts -> the gate/up pair, and the down + combine forms
-  hipFunction_t moe_fn3 = nullptr;
-  hipFunction_t moe_fn4 = nullptr;       // the gate/up pair that routes for itself
-  uint32_t chain_kind = 0;               // dense matvecs matvec_chain can run (CHAIN_*), and
-  uint32_t chain_accum = 0;              // whether they accumulate
+  hipFunction_t moe_fn = nullptr;        // MoE decode forms (fuse_moe), Q4_K experts: the gate/up pair,
+  hipFunction_t moe_fn3 = nullptr;       // the down projection with moe_combine,
+  hipFunction_t moe_fn4 = nullptr;       // and the gate/up pair that routes for itself
   std::vector<std::vector<void *>> sets;
 };
 
@@ -220,13 +265,10 @@ struct Command {
   hipFunction_t split_fn = nullptr;
   uint32_t split_threads = 0;
   hipFunction_t hx_fn = nullptr, hx4_fn = nullptr, hx4b_fn = nullptr, hxs_fn = nullptr;
-  hipFunction_t hxw_fn = nullptr, hxws_fn = nullptr;
   hipFunction_t tok_fn = nullptr;
   uint32_t tok_per_wg = 0, tok_per_wg_y = 0, tok_threads = 0;
   std::string name;                 // the pipeline's shader name
-  hipFunction_t moe_fn = nullptr, moe_fn2 = nullptr, moe_fn3 = nullptr, moe_fn4 = nullptr;
-  uint32_t chain_kind = 0, chain_accum = 0;
-  uint32_t n_cnt = 0;               // fused MoE forms: self-resetting counters the kernel takes
+  hipFunction_t moe_fn = nullptr, moe_fn3 = nullptr, moe_fn4 = nullptr;
   uint32_t groups[3] = {0, 0, 0};
   std::vector<void *> bufs;
   std::vector<uint32_t> push;
@@ -250,19 +292,10 @@ struct Launch {
   void *ws = nullptr;
   void *cnt = nullptr;
   std::vector<uint32_t> extra;  // trailing by-value u32 arguments (batched forms: the token count)
-  bool cnt_arg = false;         // fused MoE forms: a trailing counter pointer (n_cnt counters)
-  // a dense matvec launch matvec_chain can run as one of its stages (stage_ok), that stage;
-  // and for a chain launch its arguments (stage table, stage count, synchronisation words)
-  bool stage_ok = false;
-  ChainStage stage{};
   // f16 row prepass: bufs[xh_buf] is replaced by the recording's f16-row buffer, which
   // holds xh_bytes for this launch
   int xh_buf = -1;
   uint64_t xh_bytes = 0;
-  bool chain = false;
-  uint64_t chain_table = 0;
-  uint32_t chain_n = 0;
-  void *chain_sync = nullptr;
 };
 
 constexpr uint32_t kMaxSeg = 4;  // MAXSEG in kernels/common.h
@@ -272,11 +305,10 @@ constexpr uint64_t kSplitTileBytes = 128 * 128 * 4;  // one f32 partial tile (ke
 // most 128 tiles of 128 x 128 leave CUs idle (the tile keeps one workgroup per CU), so
 // their super-blocks are split over up to 256 workgroups, keeping at least 4 per split.
 // Measured on MI355X at M = 512: 4096 x 4096 68.6 -> 53.0 us, 4096 x 12288 191.6 -> 119.3 us.
-// Workgroup slots a K split fills (SKYLA_HIP_SPLIT_SLOTS, default 256: one eight-wave
+// Workgroup slots a K split fills (the split_slots tactic, default 256: one eight-wave
 // workgroup per CU).
 uint64_t split_slots() {
-  const char *e = std::getenv("SKYLA_HIP_SPLIT_SLOTS");
-  const long v = e ? std::atol(e) : 0;
+  const long v = std::atol(tactic("split_slots").c_str());
   return v >= 64 && v <= 2048 ? (uint64_t)v : 256;
 }
 
@@ -291,63 +323,6 @@ uint32_t split_of(const Command &a) {
   return S < 2 ? 1 : S;
 }
 
-// split_of's rule for the 256-row x 64-token tile: tiles (of that tile) at most 128, S
-// workgroups per tile filling the K-split slots, at least four super-blocks per split, at
-// most eight; 0 when the rule gives no split.
-uint32_t wide_split(uint64_t tiles, uint32_t n_in) {
-  if (tiles == 0 || tiles > 128) return 0;
-  uint32_t S = (uint32_t)(split_slots() / tiles);
-  S = std::min(std::min(S, n_in / 256 / 4), 8u);
-  return S >= 2 ? S : 0;
-}
-
-// The matvec_chain stage (chain_table.h) of a launch of n dispatches of one dense matvec
-// pipeline, if the chain computes that shape: Q4_K with n_in 4096 or Q6_K with n_in 12288,
-// one token (grid y = z = 1), every segment reading the same activations at a 16-byte
-// aligned offset, and every region inside the first 4 GiB - 256 B of the weights buffer.
-bool chain_stage(const Command *const *run, uint32_t n, ChainStage &st) {
-  const Command &a = *run[0];
-  if (!a.chain_kind || a.groups[1] != 1 || a.groups[2] != 1 || n == 0 || n > 4) return false;
-  const bool q4 = a.chain_kind == CHAIN_Q4K_4096;
-  const size_t words = q4 ? 9 : 11;
-  if (a.push.size() != words || a.bufs.size() != (q4 ? 4u : 5u)) return false;
-  if (!q4 && a.bufs[0] != a.bufs[1]) return false;  // ql/qh/scales and d read one buffer
-  st = ChainStage{};
-  st.kind = a.chain_kind;
-  st.accum = a.chain_accum;
-  st.n_seg = n;
-  st.w = (uint64_t)(uintptr_t)a.bufs[0];
-  st.x = (uint64_t)(uintptr_t)a.bufs[q4 ? 1 : 2];
-  st.y = (uint64_t)(uintptr_t)a.bufs[q4 ? 2 : 3];
-  const uint32_t rows = q4 ? 8 : 2, n_in = q4 ? 4096 : 12288;
-  uint64_t records = 0, chunks = 0;
-  for (uint32_t i = 0; i < n; i++) {
-    const std::vector<uint32_t> &p = run[i]->push;
-    const uint32_t x_off = p[q4 ? 2 : 4], y_off = p[q4 ? 3 : 5], in = p[q4 ? 4 : 6], out = p[q4 ? 5 : 7];
-    if (in != n_in || out == 0 || x_off % 4 != 0 || (i && x_off != st.x_off)) return false;
-    st.x_off = x_off;
-    ChainSeg &sg = st.seg[i];
-    for (int k = 0; k < 4; k++) sg.o[k] = (q4 && k >= 2) ? 0 : p[k];
-    if (!q4 && sg.o[3] % 8 != 0) return false;  // d rows start 16-byte aligned
-    sg.n_out = out;
-    sg.y_off = y_off;
-    chunks += (out + rows - 1) / rows;
-    sg.g_end = (uint32_t)chunks;
-    const uint64_t nb = out;
-    if (q4) {
-      records = std::max({records, 16 * ((uint64_t)sg.o[0] + nb * 128), 16 * ((uint64_t)sg.o[1] + nb * 16)});
-    } else {
-      records = std::max({records, 16 * ((uint64_t)sg.o[0] + nb * 384), 16 * ((uint64_t)sg.o[1] + nb * 192),
-                          16 * ((uint64_t)sg.o[2] + nb * 48), 2 * ((uint64_t)sg.o[3] + nb * 48)});
-    }
-  }
-  if (records > 0xffffff00ull || chunks > 0x7fffffffull) return false;
-  for (uint32_t i = n; i < 4; i++) st.seg[i].g_end = 0xffffffffu;  // no chunk is past them
-  st.n_chunks = (uint32_t)chunks;
-  st.w_records = (uint32_t)records;
-  return true;
-}
-
 // Packs consecutive dispatches of one segmented kernel into one launch.
 Launch pack(const Command *const *run, uint32_t n) {
   Launch l;
@@ -355,10 +330,6 @@ Launch pack(const Command *const *run, uint32_t n) {
   l.fn = a.fn;
   l.threads = a.threads;
   l.bufs = a.bufs;
-  if (a.n_cnt) {  // the kernel takes a trailing counter pointer (fused MoE forms)
-    l.cnt_arg = true;
-    l.n_cnt = a.n_cnt;
-  }
   if (!a.segmented) {
     for (int i = 0; i < 3; i++) l.groups[i] = a.groups[i];
     l.args = a.push;
@@ -414,14 +385,13 @@ Launch pack(const Command *const *run, uint32_t n) {
   l.groups[0] = x;
   l.groups[1] = a.groups[1];
   l.groups[2] = a.groups[2];
-  l.stage_ok = chain_stage(run, n, l.stage);
   return l;
 }
 
 // Can dispatch c join a fused launch that starts with dispatch a and holds `x` blocks?
 // (Dispatches between two barriers are independent; same kernel, bindings and grid y/z.)
 bool fusable(const Command &a, const Command &c, uint64_t x) {
-  return a.segmented && !a.n_cnt && c.kind == Command::Dispatch && c.fn == a.fn && c.bufs == a.bufs &&
+  return a.segmented && c.kind == Command::Dispatch && c.fn == a.fn && c.bufs == a.bufs &&
          c.retile == a.retile &&
          c.threads == a.threads && c.groups[1] == a.groups[1] && c.groups[2] == a.groups[2] &&
          x + c.groups[0] <= 0x7fffffffu;
@@ -442,25 +412,22 @@ size_t next_dispatch(const std::vector<Command> &cmds, size_t i) {
 // MI355X costs ~2.3 us before any work.  The runtime can replace runs of them with one
 // launch each, computing the same values bit for bit (tests/test_gpu_moe.py compares every
 // form with the six launches):
-//   1: moe_logits then moe_route (one token)      -> moe_logits_route
 //   2: a Q4_K expert gate and up then silu_mul    -> matvec_q4k_glu__4_0_1_1_16 (writes
 //      silu(gate) * up where silu_mul leaves it; the up rows are not stored)
 //  16: moe_route, then form 2's three dispatches   -> matvec_q4k_glur__4_0_1_1_16 (every
 //      workgroup runs the route selection itself, so it needs no other's result)
-//   4: a Q4_K expert down then moe_combine        -> matvec_q4k_ecomb__4_1_16
-//   8: the same pair                              -> matvec_q4k_dcomb__8 (a workgroup owns
+//   8: a Q4_K expert down then moe_combine        -> matvec_q4k_dcomb__8 (a workgroup owns
 //      8 rows of every slot, so it combines its own rows: no handoff; n_used <= 8 and
-//      n_in <= 1024; taken before form 4)
+//      n_in <= 1024)
 // The expert forms keep the arithmetic of the launch shape the runtime's variant rule gives
 // expert matvecs (four waves, one row, 16 lanes per row), so each row sums exactly as it
 // would alone.  Config-4 decode, us per layer (graph replay, MI355X): six launches 25.9;
 // form 2 24.0; 2 + 8 21.8; 2 + 8 + 16 (three launches: logits, route + gate/up, down +
-// combine) 20.5-20.7.  Forms 1 and 4 hand results from workgroup to workgroup inside the
-// launch (a coherent store, its completion, a device-scope count, coherent reads), which
-// costs as much as the launch boundary it removes (27.1 and 26.3 against 26.3 for the six
-// launches), so they are off.  SKYLA_HIP_MOEFUSE selects the forms as a bit mask (0 keeps
-// the six launches).
-constexpr unsigned kMoeFormsDefault = 2 | 8 | 16;
+// combine) 20.5-20.7.  Two forms that handed results from workgroup to workgroup inside
+// the launch (a coherent store, its completion, a device-scope count, coherent reads) cost
+// as much as the launch boundary they removed and were taken out.  The moe_fuse tactic
+// selects the forms as a bit mask (0 keeps the six launches).
+constexpr unsigned kMoeForms = 2 | 8 | 16;  // all built forms, and the default
 
 // The experts' gate dispatch at i, their up dispatch right after it and silu_mul after a
 // barrier (graph/moe.rs:63-72): the index of the silu_mul, or 0 when the pattern is not there.
@@ -494,30 +461,12 @@ Command glu_command(const Command &a, const Command &b, hipFunction_t fn, const 
   return f;
 }
 std::vector<Command> fuse_moe(const std::vector<Command> &cmds) {
-  const char *env = std::getenv("SKYLA_HIP_MOEFUSE");
-  const unsigned forms = env ? (unsigned)std::strtoul(env, nullptr, 0) : kMoeFormsDefault;
+  const unsigned forms = (unsigned)std::strtoul(tactic("moe_fuse").c_str(), nullptr, 0) & kMoeForms;
   if (!forms) return cmds;
   std::vector<Command> out;
   out.reserve(cmds.size());
   for (size_t i = 0; i < cmds.size();) {
     const Command &a = cmds[i];
-    if ((forms & 1) && a.kind == Command::Dispatch && a.moe_fn && a.name == "moe_logits" && a.groups[1] == 1 &&
-        a.groups[2] == 1) {
-      const size_t j = next_dispatch(cmds, i);
-      if (j < cmds.size() && cmds[j].name == "moe_route" && cmds[j].groups[0] == 1 && cmds[j].groups[1] == 1 &&
-          cmds[j].groups[2] == 1 && cmds[j].push[0] == a.push[2]) {
-        Command f = a;
-        f.fn = a.moe_fn;
-        f.name = "moe_logits_route";
-        f.tok_fn = nullptr;
-        f.bufs = {a.bufs[0], a.bufs[1], cmds[j].bufs[1]};
-        f.push.insert(f.push.end(), cmds[j].push.begin(), cmds[j].push.end());
-        f.n_cnt = 1;
-        out.push_back(std::move(f));
-        i = j + 1;
-        continue;
-      }
-    }
     // moe_route, then the experts' gate and up and silu_mul -> the pair that routes itself
     if ((forms & 16) && a.kind == Command::Dispatch && a.name == "moe_route" && a.groups[0] == 1 &&
         a.groups[1] == 1 && a.groups[2] == 1) {
@@ -560,21 +509,6 @@ std::vector<Command> fuse_moe(const std::vector<Command> &cmds) {
         i = j + 1;
         continue;
       }
-      if ((forms & 4) && a.moe_fn2 && comb) {
-        Command f = a;
-        f.fn = a.moe_fn2;
-        f.name = "matvec_q4k_ecomb";
-        f.threads = 256;
-        f.retile = nullptr;
-        f.groups[0] = (a.push[5] + 15) / 16;
-        f.push.push_back(cmds[j].push[0]);
-        f.push.push_back(cmds[j].push[2]);
-        f.push.push_back(cmds[j].push[5]);
-        f.n_cnt = f.groups[0];
-        out.push_back(std::move(f));
-        i = j + 1;
-        continue;
-      }
     }
     out.push_back(a);
     i++;
@@ -611,16 +545,15 @@ bool fusable_matmul(const Command &a, const Command &c) {
 }
 
 // The launch list of a recording.  Barriers need no command of their own: launches on one
-// stream (and the nodes of a graph captured from it) run in order.  SKYLA_HIP_FUSE=0 keeps
-// one launch per dispatch; SKYLA_HIP_XHALF=0 keeps the matmuls' own f32 staging.
+// stream (and the nodes of a graph captured from it) run in order.  The fuse tactic 0 keeps
+// one launch per dispatch; the xhalf tactic 0 keeps the matmuls' own f32 staging.
 std::vector<Launch> build_launches(skyla_hip_context *ctx, const std::vector<Command> &recorded) {
   const std::vector<Command> cmds = fuse_moe(recorded);
-  const char *env = std::getenv("SKYLA_HIP_FUSE");
-  const bool fuse = !(env && env[0] == '0');
-  const char *xenv = std::getenv("SKYLA_HIP_XHALF");
-  const bool xhalf = ctx && ctx->x_half_rows && !(xenv && xenv[0] == '0');
-  const bool x4 = !(xenv && xenv[0] == '8');  // SKYLA_HIP_XHALF=8: the eight-wave tile throughout
-  const bool balance = !(xenv && xenv[0] == '4');
+  const bool fuse = tactic_on("fuse");
+  const std::string xh = tactic("xhalf");
+  const bool xhalf = ctx && ctx->x_half_rows && xh != "0";
+  const bool x4 = xh != "8";       // 8: the eight-wave tile throughout
+  const bool balance = xh != "4";  // 4: the plain grid
   std::vector<Launch> out;
   std::vector<uint32_t> xkey;  // the rows the last prepass converted, until a barrier
   for (size_t i = 0; i < cmds.size();) {
@@ -661,24 +594,12 @@ std::vector<Launch> build_launches(skyla_hip_context *ctx, const std::vector<Com
         }
       }
       if (n_run > 1) {
-        uint64_t tiles = row_tiles * a.groups[2];
+        const uint64_t tiles = row_tiles * a.groups[2];
         uint32_t S = (uint32_t)(split_slots() / tiles);  // split_of's rule on the fused tile count
         S = std::min(std::min(S, a.push[6] / 256 / 4), 8u);
         if (S < 2) S = 1;
-        // the 256-row x 64-token tile when its split rule splits the run (row tiles of 256)
-        bool wide = false;
-        uint64_t rt256 = 0;
-        for (uint32_t sgi = 0; sgi < n_run; sgi++) rt256 += (cmds[i + sgi].push[7] + 255) / 256;
-        if (a.hxws_fn) {
-          const uint32_t Sw = wide_split(rt256 * a.groups[2] * 2, a.push[6]);
-          if (Sw >= 2) {
-            wide = true;
-            S = Sw;
-            tiles = rt256 * a.groups[2] * 2;
-          }
-        }
         Launch l;
-        l.fn = wide ? a.hxws_fn : a.hxs_fn;
+        l.fn = a.hxs_fn;
         l.threads = 512;
         l.bufs = a.bufs;
         const size_t w = 13;
@@ -693,12 +614,12 @@ std::vector<Launch> build_launches(skyla_hip_context *ctx, const std::vector<Com
             std::copy(c.push.begin(), c.push.end(), dst);
             dst[4] = (uint32_t)(h_off / 2);  // f16 units
             dst[8] = a.push[6];
-            start += wide ? (c.push[7] + 255) / 256 : c.groups[0];
+            start += c.groups[0];
           }
         }
-        l.groups[0] = (uint32_t)(wide ? rt256 : row_tiles);
+        l.groups[0] = (uint32_t)row_tiles;
         l.groups[1] = 1;
-        l.groups[2] = a.groups[2] * (wide ? 2 : 1) * S;
+        l.groups[2] = a.groups[2] * S;
         l.split = S;
         l.n_cnt = S > 1 ? (uint32_t)tiles : 0;
         l.ws_bytes = S > 1 ? tiles * S * kSplitTileBytes : 0;
@@ -724,9 +645,9 @@ std::vector<Launch> build_launches(skyla_hip_context *ctx, const std::vector<Com
         // More tiles than CUs but fewer than the two-per-CU slots: some CUs would run two
         // tiles and the rest one.  Balanced grid instead: hf tiles whole and the rest in two
         // K halves, hf + 2 (tiles - hf) = one workgroup per slot (M = 512 gate: 384 tiles,
-        // 256 whole + 128 halved).  SKYLA_HIP_XHALF=4 keeps the plain grid.
+        // 256 whole + 128 halved).  The xhalf tactic 4 keeps the plain grid.
         const uint64_t tiles = (uint64_t)a.groups[0] * a.groups[2];
-        const uint64_t slots = 2ull * (ctx->n_cu ? ctx->n_cu : 256);
+        const uint64_t slots = 2ull * ctx->n_cu;
         if (balance && a.hx4b_fn && tiles > slots / 2 && tiles < slots && a.push[6] >= 2 * 256) {
           const uint32_t hf = (uint32_t)(2 * tiles - slots);
           l.fn = a.hx4b_fn;
@@ -736,23 +657,6 @@ std::vector<Launch> build_launches(skyla_hip_context *ctx, const std::vector<Com
           l.extra = {hf, a.groups[2]};
           l.n_cnt = (uint32_t)(tiles - hf);
           l.ws_bytes = (uint64_t)l.n_cnt * 2 * kSplitTileBytes;
-        }
-      }
-      // K-split launches on the 256-row x 64-token tile (when built in: SKYLA_HIP_DL=2) if
-      // its own split rule splits it (M = 512 at the Qwen3-8B shapes: 128 tiles, two K
-      // halves, as the 128 x 128 tile)
-      if (l.split > 1 && a.hxw_fn) {
-        const uint64_t rt = (a.push[7] + 255) / 256, zt = (uint64_t)a.groups[2] * 2;
-        const uint32_t S = wide_split(rt * zt, a.push[6]);
-        if (S >= 2) {
-          l.fn = a.hxw_fn;
-          l.threads = 512;
-          l.groups[0] = (uint32_t)rt;
-          l.groups[1] = 1;
-          l.groups[2] = (uint32_t)(zt * S);
-          l.split = S;
-          l.n_cnt = (uint32_t)(rt * zt);
-          l.ws_bytes = rt * zt * S * kSplitTileBytes;
         }
       }
       if (!l.split) l.split = 1;  // the K-split arguments, unsplit
@@ -779,12 +683,6 @@ std::vector<Launch> build_launches(skyla_hip_context *ctx, const std::vector<Com
 }
 
 int launch(hipStream_t stream, const Launch &l) {
-  if (l.chain) {  // matvec_chain(table, n_stages, sync)
-    void *cp[] = {const_cast<uint64_t *>(&l.chain_table), const_cast<uint32_t *>(&l.chain_n),
-                  const_cast<void **>(&l.chain_sync)};
-    HIP_TRY(hipModuleLaunchKernel(l.fn, l.groups[0], 1, 1, l.threads, 1, 1, 0, stream, cp, nullptr));
-    return SKYLA_HIP_OK;
-  }
   // kernel parameters: binding pointers in order, then the push struct by value
   std::vector<void *> params;
   params.reserve(l.bufs.size() + 1);
@@ -796,7 +694,6 @@ int launch(hipStream_t stream, const Launch &l) {
     params.push_back(const_cast<uint32_t *>(&l.split));
   }
   for (const uint32_t &v : l.extra) params.push_back(const_cast<uint32_t *>(&v));
-  if (l.cnt_arg) params.push_back(const_cast<void **>(&l.cnt));
   HIP_TRY(hipModuleLaunchKernel(l.fn, l.groups[0], l.groups[1], l.groups[2], l.threads, 1, 1, 0,
                                 stream, params.data(), nullptr));
   return SKYLA_HIP_OK;
@@ -811,7 +708,7 @@ int bind_workspace(std::vector<Launch> &ls, void **owned) {
   *owned = nullptr;
   uint64_t ws = 0, n_cnt = 0, xh = 0;
   for (const Launch &l : ls) {
-    if (l.split || l.cnt_arg) {
+    if (l.split) {
       ws = std::max(ws, l.ws_bytes);
       n_cnt = std::max<uint64_t>(n_cnt, l.n_cnt);
     }
@@ -829,7 +726,7 @@ int bind_workspace(std::vector<Launch> &ls, void **owned) {
     return fail(SKYLA_HIP_E_DEVICE, "K-split workspace: %s", hipGetErrorString(e));
   }
   for (Launch &l : ls) {
-    if (l.split || l.cnt_arg) {
+    if (l.split) {
       l.ws = mem;
       l.cnt = (char *)mem + cnt_off;
     }
@@ -856,7 +753,6 @@ struct skyla_hip_recording {
   std::vector<Command> cmds;
   std::vector<Launch> launches;
   void *workspace = nullptr;  // K-split partials and counters of the launches
-  void *chain_mem = nullptr;  // matvec_chain stage tables and synchronisation words
   hipGraphExec_t exec = nullptr;
   hipGraph_t graph = nullptr;
   std::vector<std::string> labels;
@@ -871,11 +767,40 @@ struct skyla_hip_recording {
     if (exec) hipGraphExecDestroy(exec);
     if (graph) hipGraphDestroy(graph);
     if (workspace) hipFree(workspace);
-    if (chain_mem) hipFree(chain_mem);
   }
 };
 
 namespace {
+
+// The command a dispatch of pipeline p records: its kernel and every form the runtime
+// may substitute for it (binding set `bufs`, grid `groups`, the push words).
+Command dispatch_command(const skyla_hip_pipeline *p, const std::vector<void *> &bufs, const uint32_t *groups,
+                         const uint32_t *push, uint32_t n_push) {
+  Command c;
+  c.kind = Command::Dispatch;
+  c.fn = p->fn;
+  c.threads = p->threads;
+  c.segmented = p->segmented;
+  c.retile = p->retile;
+  c.split_fn = p->split_fn;
+  c.hx_fn = p->hx_fn;
+  c.hx4_fn = p->hx4_fn;
+  c.hx4b_fn = p->hx4b_fn;
+  c.hxs_fn = p->hxs_fn;
+  c.split_threads = p->split_threads;
+  c.tok_fn = p->tok_fn;
+  c.tok_per_wg = p->tok_per_wg;
+  c.tok_per_wg_y = p->tok_per_wg_y;
+  c.tok_threads = p->tok_threads;
+  c.name = p->name;
+  c.moe_fn = p->moe_fn;
+  c.moe_fn3 = p->moe_fn3;
+  c.moe_fn4 = p->moe_fn4;
+  for (int i = 0; i < 3; i++) c.groups[i] = groups[i];
+  c.bufs = bufs;
+  c.push.assign(push, push + n_push);
+  return c;
+}
 
 hipFunction_t find_function(skyla_hip_context *ctx, const std::string &sym) {
   for (hipModule_t m : ctx->modules) {
@@ -884,66 +809,6 @@ hipFunction_t find_function(skyla_hip_context *ctx, const std::string &sym) {
   }
   (void)hipGetLastError();  // lookups that missed leave a sticky error behind
   return nullptr;
-}
-
-// Chained decode matvecs (chain.hip).  A run of two or more consecutive launches that
-// matvec_chain can run as stages (chain_stage) becomes one launch of one workgroup per CU,
-// which streams the weights of all of them through LDS and meets at a grid barrier between
-// stages, instead of paying a launch and a ramp per stage.  The stage tables of a recording
-// and the chain's synchronisation words share one device allocation (*owned), cleared here,
-// outside any graph capture; every chain launch leaves the words as it found them.
-// Measured on MI355X it is slower than the launches it replaces (config-2 step 1.78 ms
-// against 1.33 ms): a grid barrier between dependent stages costs 4-6 us (the last
-// workgroup's stores, its count, the others' polls, all past the XCDs' L2s), more than a
-// launch boundary, and the per-chunk workgroup barrier keeps the waves in lockstep.  So it
-// is off unless SKYLA_HIP_CHAIN=1.
-int chain_launches(skyla_hip_context *ctx, std::vector<Launch> &ls, void **owned) {
-  *owned = nullptr;
-  const char *env = std::getenv("SKYLA_HIP_CHAIN");
-  if (!ctx->chain_fn || !(env && env[0] == '1')) return SKYLA_HIP_OK;
-  std::vector<std::pair<size_t, size_t>> runs;  // [begin, end) of each run
-  for (size_t i = 0; i < ls.size();) {
-    size_t j = i;
-    while (j < ls.size() && !ls[j].mark && ls[j].stage_ok) j++;
-    if (j - i >= 2) runs.push_back({i, j});
-    i = j > i ? j : i + 1;
-  }
-  if (runs.empty()) return SKYLA_HIP_OK;
-  std::vector<ChainStage> table;
-  for (const auto &r : runs)
-    for (size_t i = r.first; i < r.second; i++) table.push_back(ls[i].stage);
-  const size_t sync_bytes = 256, bytes = sync_bytes + table.size() * sizeof(ChainStage);
-  void *mem = nullptr;
-  HIP_TRY(hipMalloc(&mem, bytes));
-  hipError_t e = hipMemset(mem, 0, sync_bytes);
-  if (e == hipSuccess) e = hipMemcpy((char *)mem + sync_bytes, table.data(), table.size() * sizeof(ChainStage),
-                                     hipMemcpyHostToDevice);
-  if (e == hipSuccess) e = hipDeviceSynchronize();
-  if (e != hipSuccess) {
-    hipFree(mem);
-    return fail(SKYLA_HIP_E_DEVICE, "chain tables: %s", hipGetErrorString(e));
-  }
-  std::vector<Launch> out;
-  size_t next = 0, t = 0;
-  for (const auto &r : runs) {
-    for (; next < r.first; next++) out.push_back(std::move(ls[next]));
-    Launch c;
-    c.fn = ctx->chain_fn;
-    c.threads = CHAIN_THREADS;
-    c.groups[0] = ctx->n_cu;
-    c.groups[1] = c.groups[2] = 1;
-    c.chain = true;
-    c.chain_table = (uint64_t)(uintptr_t)((char *)mem + sync_bytes + t * sizeof(ChainStage));
-    c.chain_n = (uint32_t)(r.second - r.first);
-    c.chain_sync = mem;
-    t += c.chain_n;
-    out.push_back(std::move(c));
-    next = r.second;
-  }
-  for (; next < ls.size(); next++) out.push_back(std::move(ls[next]));
-  ls = std::move(out);
-  *owned = mem;
-  return SKYLA_HIP_OK;
 }
 
 // Variant choice for matvec launches, from sweeps on MI355X.  Dense rows (Qwen3-8B decode
@@ -980,8 +845,8 @@ const VariantRule kVariantRules[] = {
 // q+k+v 6.50 / 6.71, o 5.28 / 6.13; gate+up was 13.33 / 13.04 in an earlier build, and the
 // whole config-2 step now measures 3385 against 3322 GB/s with gate+up on 4 x 1 too, so
 // every plain launch takes it.  The gate/up pair (8192 outputs or more) stays on the
-// LDS-staged pair form.  SKYLA_HIP_KS=0 keeps the LDS-staged forms everywhere;
-// SKYLA_HIP_KS=R_G forces one shape (for sweeps).
+// LDS-staged pair form.  The ks tactic 0 keeps the LDS-staged forms everywhere; ks=R_G
+// forces one shape (for sweeps).
 struct KsRule {
   uint64_t min_rows, max_rows;  // rows of the launch (outputs for the gate/up pair)
   uint32_t rpl, ng;
@@ -996,47 +861,28 @@ const KsRule kKsPairRules[] = {{0, 8191, 4, 1}};
 // one whose workgroups all fit at once: config 5 at 1k context, device ms per token on one
 // box, (4, 3) 1.854 and (4, 6) 1.855 against 1.877-1.882 for the LDS-staged pair form;
 // (4, 2) 1.883, (8, 1) 1.894, (8, 3) 1.917, and (4, 1) 2.049 and (2, 2) 2.046 (three rounds
-// of workgroups).  SKYLA_HIP_KSGLUN=0 keeps the LDS-staged pair, =R_G forces a shape.
+// of workgroups).  The ksglun tactic 0 keeps the LDS-staged pair, R_G forces a shape.
 const KsRule kKsGlunRules[] = {{0, ~uint64_t{0}, 4, 3}};
 // q/k/v with the attention norm folded in (MODE 2, the same 102 VGPRs): config 5 at 1k
 // context, device ms per token on one box, (4, 2) 1.809 against 1.833-1.838 for (4, 1);
-// (8, 1) 1.826, (2, 2) 1.850, (4, 3) 1.849, (2, 1) 1.900.  SKYLA_HIP_KSNORM=R_G forces a shape.
+// (8, 1) 1.826, (2, 2) 1.850, (4, 3) 1.849, (2, 1) 1.900.  The ksnorm tactic R_G forces a shape.
 const KsRule kKsNormRules[] = {{0, ~uint64_t{0}, 4, 2}};
 // K-split Q6_K form (n_in = 12288; rows per slot, row-groups, row-groups loaded ahead).
 // Config-2 down projection (4096 rows), us per launch over 36 layers on two boxes: (1, 8, 1)
 // 11.75 / 11.89 against 12.25 / 12.48 for the LDS-staged (8, 1, 64); (1, 8, 2) 12.40,
-// (1, 16, 2) 12.83, (2, 4, 2) 13.89, (8, 1, 1) 14.02, (1, 8, 7) 14.19.  SKYLA_HIP_KS6=R_G_D
-// forces one shape (sweeps); SKYLA_HIP_KS=0 turns it off with the Q4_K forms.
+// (1, 16, 2) 12.83, (2, 4, 2) 13.89, (8, 1, 1) 14.02, (1, 8, 7) 14.19.  The ks6 tactic R_G_D
+// forces one shape (sweeps); ks=0 turns it off with the Q4_K forms.
 const std::vector<KsRule> kKs6Rules = {{0, ~uint64_t{0}, 1, 8, 1}};
-// K-split Q4_K form for n_in = 12288 (matvec_q4k_ks12_body: three waves, each lane one
-// 64-value chunk of every row), opt-in with SKYLA_HIP_KS12=R_G_D: config 5 (its odd
-// layers' down projections) measured slower than the LDS-staged form, device ms per token
-// at 1k context 1.839 (1, 8, 1), 1.842 (1, 8, 2), 1.852 (2, 4, 1), 1.866-1.870 (1, 16, 1),
-// (2, 8, 1) against 1.811.
 
 void add_ks(skyla_hip_context *ctx, const char *name, const uint32_t *spec, Retile &t) {
-  // SKYLA_HIP_MF=G: plain Q4_K launches with n_in = 4096 on the matrix-core form
-  // (matvec_q4k_mf_body), G groups of 16 rows per workgroup.  Off by default: on MI355X it
-  // measured no faster than the f32 forms (config-2 kernel trace: q+k+v 6.27 against 6.45
-  // us, o 6.41 against 5.25, gate+up 14.00 against 13.41) -- these launches are bound by
-  // their loads' latency, not by the VALU the matrix cores take over.
-  if (const char *mf = std::getenv("SKYLA_HIP_MF");
-      mf && mf[0] != '0' && std::strcmp(name, "matvec_q4k") == 0 && spec[3] == 0) {
-    const unsigned g = (unsigned)std::strtoul(mf, nullptr, 10);
-    if (hipFunction_t fn = find_function(ctx, "matvec_q4k_mf__" + std::to_string(spec[1]) + "_" + std::to_string(g))) {
-      t.alts.push_back({fn, 16 * g, 512, 0, 4096});
-      return;
-    }
-  }
-  const char *env = std::getenv("SKYLA_HIP_KS");
-  if (env && env[0] == '0') return;
+  const std::string ksv = tactic("ks");
+  if (ksv == "0") return;
+  uint32_t fr = 0, fg = 0, fd = 0;
   if (std::strcmp(name, "matvec_q6k") == 0 && spec[3] == 0) {
     // K-split Q6_K form for launches whose rows all have n_in = 12288 (matvec_q6k_ks_body):
     // three waves, RPL rows per row-group, NG row-groups per workgroup
     std::vector<KsRule> rules(std::begin(kKs6Rules), std::end(kKs6Rules));
-    uint32_t fr = 0, fg = 0, fd = 0;
-    if (const char *e6 = std::getenv("SKYLA_HIP_KS6"); e6 && std::sscanf(e6, "%u_%u_%u", &fr, &fg, &fd) == 3)
-      rules = {{0, ~uint64_t{0}, fr, fg, fd}};
+    if (std::sscanf(tactic("ks6").c_str(), "%u_%u_%u", &fr, &fg, &fd) == 3) rules = {{0, ~uint64_t{0}, fr, fg, fd}};
     std::vector<MatvecAlt> alts;
     for (const KsRule &r : rules) {
       const std::string sym = "matvec_q6k_ks__" + std::to_string(spec[1]) + "_" + std::to_string(r.rpl) + "_" +
@@ -1057,8 +903,7 @@ void add_ks(skyla_hip_context *ctx, const char *name, const uint32_t *spec, Reti
     ks = "matvec_q4k_ks_norm__0", norm = true;
   else if (std::strcmp(name, "matvec_q4k_glu") == 0)
     ks = "matvec_q4k_ks_glu__0", pair = true;
-  else if (std::strcmp(name, "matvec_q4k_glun") == 0 &&
-           !(std::getenv("SKYLA_HIP_KSGLUN") && std::getenv("SKYLA_HIP_KSGLUN")[0] == '0'))
+  else if (std::strcmp(name, "matvec_q4k_glun") == 0 && tactic("ksglun") != "0")
     ks = "matvec_q4k_ks_glun__0", pair = true, glun = true;
   else
     return;
@@ -1066,32 +911,15 @@ void add_ks(skyla_hip_context *ctx, const char *name, const uint32_t *spec, Reti
                             : norm ? std::begin(kKsNormRules) : std::begin(kKsRules),
                             glun ? std::end(kKsGlunRules) : pair ? std::end(kKsPairRules)
                             : norm ? std::end(kKsNormRules) : std::end(kKsRules));
-  uint32_t fr = 0, fg = 0;
-  if (env && std::sscanf(env, "%u_%u", &fr, &fg) == 2) rules = {{0, ~uint64_t{0}, fr, fg}};
-  // SKYLA_HIP_KSGLUN=R_G: the norm-folded pair on that shape (sweeps)
-  if (const char *eg = std::getenv("SKYLA_HIP_KSGLUN"); glun && eg && std::sscanf(eg, "%u_%u", &fr, &fg) == 2)
-    rules = {{0, ~uint64_t{0}, fr, fg}};
-  // SKYLA_HIP_KSNORM=R_G: the norm-folded form on that shape (sweeps)
-  if (const char *en = std::getenv("SKYLA_HIP_KSNORM"); norm && en && std::sscanf(en, "%u_%u", &fr, &fg) == 2)
-    rules = {{0, ~uint64_t{0}, fr, fg}};
+  // forced shapes (sweeps and the parity tests of every compiled shape): ks=R_G for the plain
+  // and pair forms, ksglun=R_G for the norm-folded pair, ksnorm=R_G for the norm-folded form
+  const std::string forced = glun ? tactic("ksglun") : norm ? tactic("ksnorm") : ksv;
+  if (std::sscanf(forced.c_str(), "%u_%u", &fr, &fg) == 2) rules = {{0, ~uint64_t{0}, fr, fg}};
   std::vector<MatvecAlt> alts;
   for (const KsRule &r : rules) {
     hipFunction_t fn = find_function(ctx, ks + "_" + std::to_string(r.rpl) + "_" + std::to_string(r.ng));
     if (!fn) return;  // all or nothing
     alts.push_back({fn, (pair ? 2u : 4u) * r.rpl * r.ng, 512, r.min_rows, 4096, r.max_rows});
-  }
-  uint32_t fd = 0;
-  if (const char *e12 = std::getenv("SKYLA_HIP_KS12");
-      !pair && !norm && e12 && std::sscanf(e12, "%u_%u_%u", &fr, &fg, &fd) == 3) {
-    // plain Q4_K: the n_in = 12288 form beside the 4096 one
-    const KsRule r12[] = {{0, ~uint64_t{0}, fr, fg, fd}};
-    for (const KsRule &r : r12) {
-      const std::string sym = "matvec_q4k_ks12__" + std::to_string(spec[1]) + "_" + std::to_string(r.rpl) + "_" +
-                              std::to_string(r.ng) + "_" + std::to_string(r.pd);
-      hipFunction_t fn = find_function(ctx, sym);
-      if (!fn) return;  // all or nothing
-      alts.push_back({fn, r.rpl * r.ng, 192, r.min_rows, 12288, r.max_rows});
-    }
   }
   t.alts.insert(t.alts.end(), alts.begin(), alts.end());
 }
@@ -1099,16 +927,16 @@ void add_ks(skyla_hip_context *ctx, const char *name, const uint32_t *spec, Reti
 std::shared_ptr<const Retile> make_retile(skyla_hip_context *ctx, const char *name, const uint32_t *spec,
                                           uint32_t n_spec) {
   if (n_spec != 5) return nullptr;
-  if (const char *env = std::getenv("SKYLA_HIP_RETILE"); env && env[0] == '0') return nullptr;
+  if (!tactic_on("retile")) return nullptr;
   auto t = std::make_shared<Retile>();
   t->n_out_word = 5;
   add_ks(ctx, name, spec, *t);
   for (VariantRule r : kVariantRules) {
     if (std::strcmp(r.name, name) != 0 || r.moe != spec[3]) continue;
-    // SKYLA_HIP_VARIANT=W_R_L puts every dense launch of this kernel on one variant (sweeps)
-    if (const char *env = std::getenv("SKYLA_HIP_VARIANT"); env && !spec[3]) {
+    // the variant tactic W_R_L puts every dense launch of this kernel on one variant (sweeps)
+    if (!spec[3]) {
       unsigned vw = 0, vr = 0, vl = 0;
-      if (std::sscanf(env, "%u_%u_%u", &vw, &vr, &vl) == 3) {
+      if (std::sscanf(tactic("variant").c_str(), "%u_%u_%u", &vw, &vr, &vl) == 3) {
         r.v[0] = {0, vw, vr, vl};
         r.n = 1;
       }
@@ -1167,7 +995,7 @@ int skyla_hip_context_new(int device, skyla_hip_context **out) {
   ctx->warp = (uint32_t)prop.warpSize;
   HIP_TRY(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking));
   const unsigned char *images[] = {skyla_co_matvec, skyla_co_matmul, skyla_co_moe, skyla_co_util,
-                                   skyla_co_attention, skyla_co_chain};
+                                   skyla_co_attention};
   for (const unsigned char *img : images) {
     hipModule_t m = nullptr;
     hipError_t le = hipModuleLoadData(&m, img);
@@ -1200,18 +1028,7 @@ int skyla_hip_context_new(int device, skyla_hip_context **out) {
     }
   }
   ctx->x_half_rows = find_function(ctx.get(), "x_half_rows");
-  // matvec_chain waits at grid barriers, so it runs only if one workgroup fits on every CU
-  // at once: the grid is one workgroup per CU and the kernel's occupancy must allow one
-  {
-    hipFunction_t fn = find_function(ctx.get(), "matvec_chain");
-    int per_cu = 0;
-    if (fn && hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, CHAIN_THREADS, 0) == hipSuccess &&
-        per_cu >= 1 && prop.multiProcessorCount > 0) {
-      ctx->chain_fn = fn;
-      ctx->n_cu = (uint32_t)prop.multiProcessorCount;
-    }
-    (void)hipGetLastError();
-  }
+  if (prop.multiProcessorCount > 0) ctx->n_cu = (uint32_t)prop.multiProcessorCount;
   *out = ctx.release();
   return SKYLA_HIP_OK;
 }
@@ -1387,21 +1204,13 @@ int skyla_hip_pipeline_new(skyla_hip_context *ctx, const char *name, uint32_t n_
     return fail(SKYLA_HIP_E_NO_KERNEL, "no gfx950 kernel %s for this spec", sym.c_str());
   p->retile = make_retile(ctx, name, spec, n_spec);
   p->name = name;
-  // MoE decode forms (fuse_moe): the router pair, and Q4_K expert matvecs whose launches the
-  // variant rule puts on (4, 1, 16)
-  if (std::strcmp(name, "moe_logits") == 0) p->moe_fn = find_function(ctx, "moe_logits_route");
+  // MoE decode forms (fuse_moe): Q4_K expert matvecs whose launches the variant rule puts
+  // on (4, 1, 16)
   if (std::strcmp(name, "matvec_q4k") == 0 && n_spec == 5 && spec[1] == 0 && spec[3] == 1 && p->retile &&
       p->retile->alts.size() == 1 && p->retile->alts[0].rwg == 16 && p->retile->alts[0].threads == 256) {
     p->moe_fn = find_function(ctx, "matvec_q4k_glu__4_0_1_1_16");
-    p->moe_fn2 = find_function(ctx, "matvec_q4k_ecomb__4_1_16");
     p->moe_fn3 = find_function(ctx, "matvec_q4k_dcomb__8");
     p->moe_fn4 = find_function(ctx, "matvec_q4k_glur__4_0_1_1_16");
-  }
-  // dense decode matvecs matvec_chain can run (the shape is checked per launch)
-  if (n_spec == 5 && spec[3] == 0 && ctx->chain_fn) {
-    if (std::strcmp(name, "matvec_q4k") == 0) p->chain_kind = CHAIN_Q4K_4096;
-    if (std::strcmp(name, "matvec_q6k") == 0) p->chain_kind = CHAIN_Q6K_12288;
-    p->chain_accum = spec[1] != 0;
   }
   // router logits of a batch: 8 x 8 (expert, token) blocks per workgroup (moe.hip, moe_logits_t)
   if (std::strcmp(name, "moe_logits") == 0) {
@@ -1409,11 +1218,10 @@ int skyla_hip_pipeline_new(skyla_hip_context *ctx, const char *name, uint32_t n_
     p->tok_per_wg = p->tok_per_wg_y = 8;
   }
   // the attention merge of a batched step (grid (heads, tokens)): one wave per (head, token),
-  // four heads per workgroup (attention.hip, attention_merge_t); SKYLA_HIP_MERGE_T=0 keeps
+  // four heads per workgroup (attention.hip, attention_merge_t); the merge_t tactic 0 keeps
   // the 1024-thread form
   if (std::strcmp(name, "attention_merge") == 0 && n_spec == 2 && spec[0] == 128 && spec[1] == 0) {
-    const char *env = std::getenv("SKYLA_HIP_MERGE_T");
-    if (!(env && env[0] == '0')) {
+    if (tactic_on("merge_t")) {
       p->tok_fn = find_function(ctx, "attention_merge_t__128_0");
       p->tok_per_wg = 4;
       p->tok_per_wg_y = 1;
@@ -1421,10 +1229,9 @@ int skyla_hip_pipeline_new(skyla_hip_context *ctx, const char *name, uint32_t n_
     }
   }
   // dense K-quant matmul (TYPE 1/2, MOE 0): its K-split variant, used for launches with few
-  // tiles (split_of); SKYLA_HIP_SPLITK=0 keeps every launch on the engine's kernel
+  // tiles (split_of); the splitk tactic 0 keeps every launch on the engine's kernel
   if (std::strcmp(name, "matmul") == 0 && n_spec >= 3 && (spec[0] == 1 || spec[0] == 2) && spec[2] == 0) {
-    const char *env = std::getenv("SKYLA_HIP_SPLITK");
-    if (!(env && env[0] == '0')) {
+    if (tactic_on("splitk")) {
       const std::string ssym = "matmul_w8__" + std::to_string(spec[0]) + "_" + std::to_string(spec[1]) + "_" +
                                std::to_string(n_spec == 4 ? spec[3] : 0);
       p->split_fn = find_function(ctx, ssym);
@@ -1432,29 +1239,15 @@ int skyla_hip_pipeline_new(skyla_hip_context *ctx, const char *name, uint32_t n_
     }
     // f32 inputs: the tile on x_half_rows's f16 rows (build_launches inserts the prepass),
     // by default the forms whose operands go straight into LDS (eight waves: x8d, x8ds; four
-    // waves, Q4_K only: x4d, x4db); SKYLA_HIP_DL=0 keeps the register-staged tiles.
+    // waves, Q4_K only: x4d, x4db); the dl tactic 0 keeps the register-staged tiles.
     if (!(n_spec == 4 && spec[3])) {
-      const char *denv = std::getenv("SKYLA_HIP_DL");
-      const bool dl = !(denv && denv[0] == '0');
+      const bool dl = tactic_on("dl");
       const bool dl4 = dl && spec[0] == 1;
-      // the eight-wave tiles on the deeper ring (x8e, x8es), opt-in with SKYLA_HIP_DL=3: M = 512
-      // measured q 42.5-44.2 against 41.6-42.2 us, down 114.5-119.4 against 115.8-116.0, the
-      // config-5 512-token prefill 14.67k against 14.82k tok/s (one box)
-      const bool deep = dl && denv && denv[0] == '3';
       const std::string ts = std::to_string(spec[0]) + "_" + std::to_string(spec[1]);
-      p->hx_fn = find_function(ctx, (deep ? "matmul_x8e__" : dl ? "matmul_x8d__" : "matmul_x8__") + ts);
+      p->hx_fn = find_function(ctx, (dl ? "matmul_x8d__" : "matmul_x8__") + ts);
       p->hx4_fn = find_function(ctx, (dl4 ? "matmul_x4d__" : "matmul_x4__") + ts);
       p->hx4b_fn = find_function(ctx, (dl4 ? "matmul_x4db__" : "matmul_x4b__") + ts);
-      // the 256-row x 64-token tile for K-split launches, opt-in with SKYLA_HIP_DL=2: each
-      // wave dequantises its own rows, but M = 512 measured q 42.2-42.5 us against
-      // 42.3-42.5 and down (Q6_K) 124.6-124.9 against 113.7-113.8 for the 128 x 128 tile,
-      // and the config-5 512-token prefill 14.7k against 15.0k tok/s
-      const bool dlw = dl && denv && denv[0] == '2';
-      if (dlw) {
-        p->hxw_fn = find_function(ctx, "matmul_x8w__" + ts);
-        p->hxws_fn = find_function(ctx, "matmul_x8ws__" + ts);
-      }
-      p->hxs_fn = find_function(ctx, (deep ? "matmul_x8es__" : dl ? "matmul_x8ds__" : "matmul_x8s__") + ts);
+      p->hxs_fn = find_function(ctx, (dl ? "matmul_x8ds__" : "matmul_x8s__") + ts);
       p->split_threads = 512;
     }
   }
@@ -1537,34 +1330,7 @@ int skyla_hip_record_dispatch(skyla_hip_recorder *r, const skyla_hip_pipeline *p
     if (!b)
       return record_fail(r, fail(SKYLA_HIP_E_STATE, "record_dispatch: %s set %u is not bound",
                                  p->symbol.c_str(), set));
-  Command c;
-  c.kind = Command::Dispatch;
-  c.fn = p->fn;
-  c.threads = p->threads;
-  c.segmented = p->segmented;
-  c.retile = p->retile;
-  c.split_fn = p->split_fn;
-  c.hx_fn = p->hx_fn;
-  c.hx4_fn = p->hx4_fn;
-  c.hx4b_fn = p->hx4b_fn;
-  c.hxw_fn = p->hxw_fn;
-  c.hxws_fn = p->hxws_fn;
-  c.hxs_fn = p->hxs_fn;
-  c.split_threads = p->split_threads;
-  c.tok_fn = p->tok_fn;
-  c.tok_per_wg = p->tok_per_wg;
-  c.tok_per_wg_y = p->tok_per_wg_y;
-  c.tok_threads = p->tok_threads;
-  c.name = p->name;
-  c.moe_fn = p->moe_fn;
-  c.moe_fn2 = p->moe_fn2;
-  c.moe_fn3 = p->moe_fn3;
-  c.moe_fn4 = p->moe_fn4;
-  c.chain_kind = p->chain_kind;
-  c.chain_accum = p->chain_accum;
-  for (int i = 0; i < 3; i++) c.groups[i] = groups[i];
-  c.bufs = p->sets[set];
-  c.push.assign(push, push + n_push);
+  Command c = dispatch_command(p, p->sets[set], groups, push, n_push);
   if (groups[0] && groups[1] && groups[2]) r->cmds.push_back(std::move(c));
   return SKYLA_HIP_OK;
 }
@@ -1614,11 +1380,9 @@ int skyla_hip_record_end(skyla_hip_recorder *r, skyla_hip_recording **out) {
   rec->mark_ns.assign(rec->labels.size(), 0.0);
   HIP_TRY(hipSetDevice(rec->ctx->device));
   if (int s = bind_workspace(rec->launches, &rec->workspace)) return s;
-  if (int s = chain_launches(rec->ctx, rec->launches, &rec->chain_mem)) return s;
-  // SKYLA_HIP_NOGRAPH=1: replay the launch list as direct launches (kernel traces of the
+  // the nograph tactic 1: replay the launch list as direct launches (kernel traces of the
   // exact launches a graph would hold, fused forms included)
-  const char *nograph = std::getenv("SKYLA_HIP_NOGRAPH");
-  if (!rec->profile && skyla_hip_recording_len(rec.get()) > 0 && !(nograph && nograph[0] == '1')) {
+  if (!rec->profile && skyla_hip_recording_len(rec.get()) > 0 && tactic("nograph") != "1") {
     // One graph for the whole recording, captured from the launch list on the stream.
     skyla_hip_context *ctx = rec->ctx;
     HIP_TRY(hipSetDevice(ctx->device));
@@ -1700,26 +1464,6 @@ struct Events {
 
 }  // namespace
 
-}  // extern "C"
-
-namespace {
-// SKYLA_HIP_CHAIN_CHECK=1: after each replay, fail if a chain launch of the recording timed
-// out at its grid barrier (its workgroups were not all resident; the outputs are wrong) or
-// left its arrival count set.
-int chain_check(const skyla_hip_recording *rec) {
-  const char *env = std::getenv("SKYLA_HIP_CHAIN_CHECK");
-  if (!rec->chain_mem || !(env && env[0] == '1')) return SKYLA_HIP_OK;
-  uint32_t words[CHAIN_SYNC_WORDS] = {0, 0};
-  HIP_TRY(hipMemcpy(words, rec->chain_mem, sizeof words, hipMemcpyDeviceToHost));
-  if (words[0] != 0 || words[1] != 0)
-    return fail(SKYLA_HIP_E_DEVICE, "matvec_chain: grid barrier state %u / time-out %u after a replay", words[0],
-                words[1]);
-  return SKYLA_HIP_OK;
-}
-}  // namespace
-
-extern "C" {
-
 int skyla_hip_replay(skyla_hip_context *ctx, const skyla_hip_recording *rec) {
   if (!ctx || !rec) return fail(SKYLA_HIP_E_ARG, "replay: bad argument");
   if (rec->ctx != ctx) return fail(SKYLA_HIP_E_ARG, "replay: recording of another context");
@@ -1728,7 +1472,7 @@ int skyla_hip_replay(skyla_hip_context *ctx, const skyla_hip_recording *rec) {
     int s = submit(ctx, rec, nullptr);
     if (s) return s;
     HIP_TRY(hipStreamSynchronize(ctx->stream));
-    return chain_check(rec);
+    return SKYLA_HIP_OK;
   }
   Events e;
   int s = e.make(rec->labels.size() + 1);
@@ -1743,7 +1487,7 @@ int skyla_hip_replay(skyla_hip_context *ctx, const skyla_hip_recording *rec) {
     mut->mark_ns[i] = (double)ms * 1e6;
   }
   mut->replayed = true;
-  return chain_check(rec);
+  return SKYLA_HIP_OK;
 }
 
 int skyla_hip_replay_timed(skyla_hip_context *ctx, const skyla_hip_recording *rec, double *ns) {
@@ -1788,27 +1532,7 @@ int skyla_hip_time_dispatch(skyla_hip_context *ctx, const skyla_hip_pipeline *p,
   for (void *b : p->sets[0])
     if (!b) return fail(SKYLA_HIP_E_STATE, "time_dispatch: %s is not bound", p->symbol.c_str());
   HIP_TRY(hipSetDevice(ctx->device));
-  Command c;
-  c.kind = Command::Dispatch;
-  c.fn = p->fn;
-  c.threads = p->threads;
-  c.segmented = p->segmented;
-  c.retile = p->retile;
-  c.split_fn = p->split_fn;
-  c.hx_fn = p->hx_fn;
-  c.hx4_fn = p->hx4_fn;
-  c.hx4b_fn = p->hx4b_fn;
-  c.hxw_fn = p->hxw_fn;
-  c.hxws_fn = p->hxws_fn;
-  c.hxs_fn = p->hxs_fn;
-  c.split_threads = p->split_threads;
-  c.tok_fn = p->tok_fn;
-  c.tok_per_wg = p->tok_per_wg;
-  c.tok_per_wg_y = p->tok_per_wg_y;
-  c.tok_threads = p->tok_threads;
-  for (int i = 0; i < 3; i++) c.groups[i] = groups[i];
-  c.bufs = p->sets[0];
-  c.push.assign(push, push + n_push);
+  const Command c = dispatch_command(p, p->sets[0], groups, push, n_push);
   const Command *one[1] = {&c};
   std::vector<Launch> ls{pack(one, 1)};
   void *workspace = nullptr;
@@ -1849,27 +1573,7 @@ int skyla_hip_dispatch_noalloc(skyla_hip_context *ctx, const skyla_hip_pipeline 
     if (!b) return fail(SKYLA_HIP_E_STATE, "dispatch_noalloc: %s is not bound", p->symbol.c_str());
   if (!ctx->scratch || !ctx->fill_u32) return fail(SKYLA_HIP_E_STATE, "dispatch_noalloc: no scratch on this context");
   HIP_TRY(hipSetDevice(ctx->device));
-  Command c;
-  c.kind = Command::Dispatch;
-  c.fn = p->fn;
-  c.threads = p->threads;
-  c.segmented = p->segmented;
-  c.retile = p->retile;
-  c.split_fn = p->split_fn;
-  c.hx_fn = p->hx_fn;
-  c.hx4_fn = p->hx4_fn;
-  c.hx4b_fn = p->hx4b_fn;
-  c.hxw_fn = p->hxw_fn;
-  c.hxws_fn = p->hxws_fn;
-  c.hxs_fn = p->hxs_fn;
-  c.split_threads = p->split_threads;
-  c.tok_fn = p->tok_fn;
-  c.tok_per_wg = p->tok_per_wg;
-  c.tok_per_wg_y = p->tok_per_wg_y;
-  c.tok_threads = p->tok_threads;
-  for (int i = 0; i < 3; i++) c.groups[i] = groups[i];
-  c.bufs = p->sets[0];
-  c.push.assign(push, push + n_push);
+  const Command c = dispatch_command(p, p->sets[0], groups, push, n_push);
   const Command *one[1] = {&c};
   Launch l = pack(one, 1);
   if (l.split) {  // the K split's partials and counters live in the static scratch array

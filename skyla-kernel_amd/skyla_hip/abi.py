@@ -64,6 +64,18 @@ SIGNATURES = [
 _lib = None
 
 
+def tactic(key: str, default: str) -> str:
+    """The value of tactic `key` from SKYLA_HIP_TACTIC ("key=value,key=value"; the last entry
+    for a key wins), else `default`.  The runtime reads its own kernel-selection keys from the
+    same variable; the engine reads its recording choices here."""
+    value = default
+    for item in os.environ.get("SKYLA_HIP_TACTIC", "").split(","):
+        k, sep, v = item.partition("=")
+        if sep and k.strip() == key:
+            value = v.strip()
+    return value
+
+
 def load_library(path: str = LIB_PATH) -> C.CDLL:
     """Loads the C-ABI library and declares every signature (raises if any is missing)."""
     global _lib

@@ -12,11 +12,11 @@ import dataclasses
 from enum import IntEnum
 from typing import Sequence
 
-import os
 
 import numpy as np
 
 from .abi import Buffer, Context, Pipeline, Recorder
+from .abi import tactic as switch
 
 # ---- backend.rs: the skyla-hip arm of `mod selected` ----------------------------------
 MATMUL_TILE_COLS = 128   # tokens per matmul workgroup (matmul.hip TN, dense)
@@ -296,12 +296,12 @@ class Kernels:
             spec = [c.n_head // c.n_head_kv, ATTENTION_CHUNK, k8, v8, c.head_dim, c.head_dim]
             self.attn_prep = build_spec("attention_prep", [w0, a, a, kv, kv], 72, spec)
             # a decode step's rope pairs, once for every layer's attention_prep
-            # (SKYLA_HIP_ROPE_TABLE=0: each workgroup computes them)
-            if os.environ.get("SKYLA_HIP_ROPE_TABLE", "1") != "0":
+            # (tactic rope_table=0: each workgroup computes them)
+            if switch("rope_table", "1") != "0":
                 self.rope_table = build("rope_table", [w0, a, a], 12)
             # recordings of one split: the attention writes the merged rows itself
-            # (SKYLA_HIP_PREP1=0 keeps attention_prep and the merge there)
-            if os.environ.get("SKYLA_HIP_PREP1", "1") != "0":
+            # (tactic prep1=0 keeps attention_prep and the merge there)
+            if switch("prep1", "1") != "0":
                 self.attn_prep1 = build_spec("attention_prep1", [w0, a, a, kv, kv], 80, spec)
         self.take_last = build("take_last", [a, a], 16)
         # token rows gathered from the HBM token_embd, one binding set per weight buffer

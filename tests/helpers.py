@@ -38,18 +38,19 @@ def pad64(n: int) -> int:
 
 
 @contextlib.contextmanager
-def env(**kw):
-    """Runtime switches (SKYLA_HIP_*) read when a pipeline is created or a recording ends."""
-    old = {k: os.environ.get(k) for k in kw}
-    os.environ.update({k: str(v) for k, v in kw.items()})
+def tactics(**kw):
+    """Tactic overrides (SKYLA_HIP_TACTIC's key=value entries, added after any already set),
+    read when a pipeline is created or a recording ends.  A value of None adds nothing."""
+    old = os.environ.get("SKYLA_HIP_TACTIC")
+    items = [f"{k}={v}" for k, v in kw.items() if v is not None]
+    os.environ["SKYLA_HIP_TACTIC"] = ",".join(([old] if old else []) + items)
     try:
         yield
     finally:
-        for k, v in old.items():
-            if v is None:
-                del os.environ[k]
-            else:
-                os.environ[k] = v
+        if old is None:
+            del os.environ["SKYLA_HIP_TACTIC"]
+        else:
+            os.environ["SKYLA_HIP_TACTIC"] = old
 
 
 class Setup:

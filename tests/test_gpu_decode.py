@@ -9,13 +9,11 @@ f16 rows or q8 blocks).  Every step's top-1 is compared: the tests print the num
 disagreements, the smallest oracle top-2 margin met and the worst logits distance, and
 assert that no step disagrees.
 """
-import contextlib
-import os
 
 import numpy as np
 import pytest
 
-from helpers import rel_l2
+from helpers import rel_l2, tactics
 from oracle import skyla_oracle as so
 from oracle.model import Model
 from skyla_hip import engine as E
@@ -25,20 +23,6 @@ pytestmark = pytest.mark.gpu
 
 P = E.KvPrecision
 CFG = "test-decode"
-
-
-@contextlib.contextmanager
-def env_var(name, value):
-    """A runtime switch read when the engine builds its kernels."""
-    old = os.environ.get(name)
-    os.environ[name] = value
-    try:
-        yield
-    finally:
-        if old is None:
-            del os.environ[name]
-        else:
-            os.environ[name] = old
 
 
 class Bench:
@@ -604,7 +588,7 @@ def test_rope_table_same_logits(ctx, ctx_len):
     tensors = synth.qwen3(f"{CFG}-q4_k_m", c, "q4_k_m", "random")
     got = {}
     for table in ("1", "0"):
-        with env_var("SKYLA_HIP_ROPE_TABLE", table):
+        with tactics(rope_table=table):
             eng = E.Engine(ctx, tensors, c, 32 * E.ATTENTION_CHUNK, P.F16_KEYS_Q8_VALUES)
         try:
             assert (eng.kernels.rope_table is not None) == (table == "1")

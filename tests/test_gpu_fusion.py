@@ -1,13 +1,11 @@
 """GPU check of launch fusion: consecutive dispatches of one matvec pipeline with no barrier
 between them (independent by the engine's contract, graph.rs:23-34) replay as one launch
 over their combined rows.  The fused replay must give the same bits as one launch per
-dispatch (SKYLA_HIP_FUSE=0) and stay within the oracle bar."""
-import os
-
+dispatch (tactic fuse=0) and stay within the oracle bar."""
 import numpy as np
 import pytest
 
-from helpers import Setup, rel_l2
+from helpers import Setup, rel_l2, tactics
 from oracle import skyla_oracle as so
 from skyla_hip import engine as E
 from skyla_hip import synth
@@ -22,20 +20,13 @@ CASES = [
 
 
 def _record(s, ms, accum, fuse):
-    old = os.environ.get("SKYLA_HIP_FUSE")
-    os.environ["SKYLA_HIP_FUSE"] = "1" if fuse else "0"
-    try:
+    with tactics(fuse=1 if fuse else 0):
         def body(r):
             g = E.Graph(r, s.k, None, None, False)
             for i, m in enumerate(ms):
                 g.matvec(m, (s.x_off, 0), (s.y_off + i * s.s_out, 0), accum, False)
             r.barrier()
         return s.ctx.record(False, body)
-    finally:
-        if old is None:
-            del os.environ["SKYLA_HIP_FUSE"]
-        else:
-            os.environ["SKYLA_HIP_FUSE"] = old
 
 
 @pytest.mark.parametrize("dtype,n_in,outs", CASES)
@@ -105,15 +96,8 @@ def test_variant_choice_matches_requested_variant(ctx, dtype, n_in, n_out, accum
     y0 = synth.activations("test-fusion", f"ry-{n_out}", n_out)
     got = {}
     for retile in ("0", "1"):
-        old = os.environ.get("SKYLA_HIP_RETILE")
-        os.environ["SKYLA_HIP_RETILE"] = retile
-        try:
+        with tactics(retile=retile):
             s = Setup(ctx, [(dtype, n_in, n_out, data)], n_in, n_out)
-        finally:
-            if old is None:
-                del os.environ["SKYLA_HIP_RETILE"]
-            else:
-                os.environ["SKYLA_HIP_RETILE"] = old
         try:
             s.set_x(x)
             s.set_y(y0)

@@ -8,7 +8,7 @@ the oracle as well.
 import numpy as np
 import pytest
 
-from helpers import Setup, env, rel_l2
+from helpers import Setup, rel_l2, tactics
 from oracle import skyla_oracle as so
 from skyla_hip import engine as E
 from skyla_hip import synth
@@ -88,7 +88,7 @@ def test_matmul_config3(ctx, name, dtype, n_in, n_out):
     assert err <= TOL and err <= GUARD, err
 
 
-@pytest.mark.parametrize("x4d", ["3", "2", "1", "0"])
+@pytest.mark.parametrize("x4d", ["1", "0"])
 @pytest.mark.parametrize("name,dtype,n_in,n_out,n_tok,accum", [
     ("q", E.DType.Q4K, 4096, 4096, 512, False), ("gate", E.DType.Q4K, 4096, 12288, 512, False),
     ("down", E.DType.Q6K, 12288, 4096, 512, True), ("ragged", E.DType.Q4K, 1024, 200, 37, True),
@@ -96,17 +96,16 @@ def test_matmul_config3(ctx, name, dtype, n_in, n_out):
 ])
 def test_matmul_f16_prepass_same_bits(ctx, name, dtype, n_in, n_out, n_tok, accum, x4d):
     """The runtime's f16 row prepass (x_half_rows, then the tile on f16 rows: four waves
-    unless the launch is K-split; SKYLA_HIP_XHALF=4 keeps the four-wave tile's plain grid)
-    against the eight-wave tile's own f32 staging (SKYLA_HIP_XHALF=0): the same bits while
-    no activation reaches 2^15, K split or not, ACCUM or not, ragged rows and token counts.
+    unless the launch is K-split; tactic xhalf=4 keeps the four-wave tile's plain grid)
+    against the eight-wave tile's own f32 staging (xhalf=0): the same bits while no
+    activation reaches 2^15, K split or not, ACCUM or not, ragged rows and token counts.
     Q4_K launches of more than 128 tiles (gate, ragged4) run the four-wave tile with its
-    operands loaded straight into LDS, or with SKYLA_HIP_DL=0 the register-staged one; the
-    K-split launches (q, down) run the 128 x 128 direct-to-LDS tile (SKYLA_HIP_DL unset or
-    1), the same on its deeper ring (=3), the 256-row x 64-token one (=2) or the
-    register-staged one (=0)."""
-    with env(SKYLA_HIP_XHALF=4, SKYLA_HIP_DL=x4d):
+    operands loaded straight into LDS, or with tactic dl=0 the register-staged one; the
+    K-split launches (q, down) run the 128 x 128 direct-to-LDS tile (dl=1) or the
+    register-staged one (dl=0)."""
+    with tactics(xhalf=4, dl=x4d):
         got1, want = _run(ctx, dtype, n_in, n_out, n_tok, accum=accum, tag="mm-xh")
-    with env(SKYLA_HIP_XHALF=0):
+    with tactics(xhalf=0):
         got0, _ = _run(ctx, dtype, n_in, n_out, n_tok, accum=accum, tag="mm-xh")
     assert np.array_equal(got1.view(np.uint32), got0.view(np.uint32))
     assert rel_l2(got1, want) <= GUARD
@@ -121,7 +120,7 @@ def test_matmul_f16_prepass_shared(ctx):
     x = synth.activations("mm-xh", "shared-x", (n_tok, n_in))
     got = {}
     for xh in ("1", "0"):
-        with env(SKYLA_HIP_XHALF=xh):
+        with tactics(xhalf=xh):
             s = Setup(ctx, mats, n_in, 384, rows=2 * n_tok)
             try:
                 s.set_x(x)
@@ -158,12 +157,12 @@ CUS = 256  # MI355X: two four-wave workgroups per CU, 512 slots
 def test_matmul_balanced_grid(ctx, name, dtype, n_in, n_out, n_tok, accum, x4d):
     """A launch of more tiles than CUs and fewer than the two-per-CU slots runs the four-wave
     tile over a balanced grid: hf = 2 tiles - 512 tiles whole (the same bits as the plain
-    grid, SKYLA_HIP_XHALF=4) and the rest in two K halves added in order (within f32
+    grid, tactic xhalf=4) and the rest in two K halves added in order (within f32
     reordering of the plain grid), against the oracle at the bar; ACCUM, ragged rows and
     tokens."""
-    with env(SKYLA_HIP_DL=x4d):
+    with tactics(dl=x4d):
         got, want = _run(ctx, dtype, n_in, n_out, n_tok, accum=accum, tag="mm-bal")
-    with env(SKYLA_HIP_XHALF=4, SKYLA_HIP_DL=x4d):
+    with tactics(xhalf=4, dl=x4d):
         plain, _ = _run(ctx, dtype, n_in, n_out, n_tok, accum=accum, tag="mm-bal")
     hz = -(-n_tok // E.MATMUL_TILE_COLS)
     tiles = -(-n_out // 128) * hz
@@ -176,13 +175,14 @@ def test_matmul_balanced_grid(ctx, name, dtype, n_in, n_out, n_tok, accum, x4d):
     assert rel_l2(got, want) <= GUARD
 
 
-@pytest.mark.parametrize("dl", ["3", "1", "2"])
+@pytest.mark.parametrize("dl", ["1", "0"])
 @pytest.mark.parametrize("n_tok", [128, 100])
 def test_matmul_segments_qkv(ctx, n_tok, dl):
     """q, k and v of a prefill chunk (Q4_K 4096 -> 4096, 1024, 1024 in one buffer, no barrier
     between them) run as one launch of three segments after the shared f16 row prepass: the
-    bits of the three separate launches (SKYLA_HIP_FUSE=0; the same K split here), and each
-    within the bar of the oracle; on the 128 x 128 tile and (SKYLA_HIP_DL=2) the 256 x 64 one."""
+    bits of the three separate launches (tactic fuse=0; the same K split here), and each
+    within the bar of the oracle; on the direct-to-LDS 128 x 128 tile (dl=1) and the
+    register-staged one (dl=0)."""
     n_in = 4096
     outs = [4096, 1024, 1024]
     mats = [(E.DType.Q4K, n_in, n, synth.matrix("mm-seg", f"qkv-{i}-{n}", E.DType.Q4K, n_in, n))
@@ -190,7 +190,7 @@ def test_matmul_segments_qkv(ctx, n_tok, dl):
     x = synth.activations("mm-seg", f"x-{n_tok}", (n_tok, n_in))
     got = {}
     for fuse in ("1", "0"):
-        with env(SKYLA_HIP_FUSE=fuse, SKYLA_HIP_DL=dl):
+        with tactics(fuse=fuse, dl=dl):
             s = Setup(ctx, mats, n_in, max(outs), rows=len(outs) * n_tok)
             try:
                 s.set_x(x)

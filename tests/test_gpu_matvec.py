@@ -9,7 +9,7 @@ about 1.5e-6 to 2.5e-6 at the Qwen3-8B shapes).
 import numpy as np
 import pytest
 
-from helpers import F32_FLOOR, Setup, env, f32_reorder_bar, pad64, rel_l2
+from helpers import F32_FLOOR, Setup, f32_reorder_bar, pad64, rel_l2, tactics
 from oracle import skyla_oracle as so
 from skyla_hip import engine as E
 from skyla_hip import synth
@@ -192,7 +192,7 @@ def test_fused_matvec_forms(ctx, dtype, n_in, n_out, form, retile):
         aux[: n_in // 8] *= np.float32(2e4)   # silu(g) * u past the f16 range, as in real checkpoints
         y0 = g.standard_normal(n_out).astype(np.float32)
     c = E.Config(n_embd=n_in, eps=1e-6)
-    with env(SKYLA_HIP_RETILE=retile):
+    with tactics(retile=retile):
         s = Setup(ctx, [(dtype, n_in, n_out, data)], n_in, n_out, extra_f32=n_in)
         k = E.Kernels(ctx, s.weights, s.arena, fuse="all")
     try:
@@ -221,8 +221,8 @@ def test_glu_norm_pair_against_oracle(ctx, n_in, n_out, big, ks):
     """matvec_q4k_glun (the gate/up pair with the FFN RMSNorm folded in, from the raw
     residual) against the oracle's rmsnorm, the two Matrix::matvec and silu * up; `big`
     puts an eighth of the residual past the f16 range (3e4 to 1e5).  With n_in 4096 the
-    runtime runs the K-split pair form (its default shape, or SKYLA_HIP_KSGLUN=4_1), with
-    SKYLA_HIP_KSGLUN=0 and for other widths the LDS-staged one; n_out 1000 leaves a ragged
+    runtime runs the K-split pair form (its default shape, or tactic ksglun=4_1), with
+    ksglun=0 and for other widths the LDS-staged one; n_out 1000 leaves a ragged
     last workgroup."""
     g = synth.matrix("test-glu", f"gate-{n_in}-{n_out}", E.DType.Q4K, n_in, n_out)
     u = synth.matrix("test-glu", f"up-{n_in}-{n_out}", E.DType.Q4K, n_in, n_out)
@@ -233,7 +233,7 @@ def test_glu_norm_pair_against_oracle(ctx, n_in, n_out, big, ks):
     w = rg.uniform(0.5, 1.5, n_in).astype(np.float32)
     eps = 1e-6
     s = Setup(ctx, [(E.DType.Q4K, n_in, n_out, g), (E.DType.Q4K, n_in, n_out, u)], n_in, n_out, extra_f32=n_in)
-    with env(SKYLA_HIP_KSGLUN=ks):
+    with tactics(ksglun=ks):
         k = E.Kernels(ctx, s.weights, s.arena, fuse="ffn")
     try:
         s.arena.as_f32()[s.extra_off: s.extra_off + n_in] = w
@@ -301,14 +301,14 @@ KS_SHAPES = ["2_1", "2_2", "4_1", "4_2", "4_3", "4_6", "8_1", "8_3"]
 @pytest.mark.parametrize("shape", KS_SHAPES)
 @pytest.mark.parametrize("accum", [False, True])
 def test_ks_shapes_against_oracle(ctx, shape, accum):
-    """Every compiled shape of the K-split Q4_K form (n_in = 4096; SKYLA_HIP_KS forces one)
+    """Every compiled shape of the K-split Q4_K form (n_in = 4096; tactic ks=R_G forces one)
     over three fused segments whose row counts are not multiples of its workgroup (q, k, v
     of 4096 + 333 + 1), ACCUM on and off, against the oracle at the f32 bar; rows past
     n_out stay untouched."""
     n_in, outs = 4096, [4096, 333, 1]
     datas = [synth.matrix("test-ks", f"{i}-{n}", E.DType.Q4K, n_in, n) for i, n in enumerate(outs)]
     x = synth.activations("test-ks", "x", n_in)
-    with env(SKYLA_HIP_KS=shape):
+    with tactics(ks=shape):
         s = Setup(ctx, [(E.DType.Q4K, n_in, n, d) for n, d in zip(outs, datas)], n_in, max(outs), rows=len(outs))
     try:
         y0 = synth.activations("test-ks", "y0", (len(outs), s.s_out))
@@ -342,14 +342,14 @@ KS6_SHAPES = ["1_8_1", "1_8_2", "1_8_7", "1_16_2", "2_4_2", "8_1_1"]
 @pytest.mark.parametrize("shape", KS6_SHAPES)
 @pytest.mark.parametrize("accum", [False, True])
 def test_ks6_shapes_against_oracle(ctx, shape, accum):
-    """Every compiled shape of the K-split Q6_K form (n_in = 12288; SKYLA_HIP_KS6 forces one)
+    """Every compiled shape of the K-split Q6_K form (n_in = 12288; tactic ks6=R_G_D forces one)
     over three fused segments whose row counts are not multiples of its workgroup (4096 +
     333 + 1), ACCUM on and off, against the oracle at the f32 bar; rows past n_out stay
     untouched."""
     n_in, outs = 12288, [4096, 333, 1]
     datas = [synth.matrix("test-ks6", f"{i}-{n}", E.DType.Q6K, n_in, n) for i, n in enumerate(outs)]
     x = synth.activations("test-ks6", "x", n_in)
-    with env(SKYLA_HIP_KS6=shape):
+    with tactics(ks6=shape):
         s = Setup(ctx, [(E.DType.Q6K, n_in, n, d) for n, d in zip(outs, datas)], n_in, max(outs), rows=len(outs))
     try:
         y0 = synth.activations("test-ks6", "y0", (len(outs), s.s_out))
@@ -383,7 +383,7 @@ def test_ks6_other_widths_keep_their_variant(ctx):
     n_in, n_out = 1024, 301
     data = synth.matrix("test-ks6", "narrow", E.DType.Q6K, n_in, n_out)
     x = synth.activations("test-ks6", "x-narrow", n_in)
-    with env(SKYLA_HIP_KS6="1_8_2"):
+    with tactics(ks6="1_8_2"):
         s = Setup(ctx, [(E.DType.Q6K, n_in, n_out, data)], n_in, n_out)
     try:
         s.set_x(x)
@@ -394,104 +394,3 @@ def test_ks6_other_widths_keep_their_variant(ctx):
         s.free()
     want = so.matvec(int(E.DType.Q6K), data, n_in, n_out, x)
     assert rel_l2(got, want) <= f32_reorder_bar(E.DType.Q6K, data, n_in, n_out, x, want)
-
-
-KS12_SHAPES = ["1_8_1", "1_8_2", "2_4_1", "1_16_1", "2_8_1"]
-
-
-@pytest.mark.parametrize("shape", KS12_SHAPES)
-@pytest.mark.parametrize("accum", [False, True])
-def test_ks12_shapes_against_oracle(ctx, shape, accum):
-    """Every compiled shape of the K-split Q4_K form for n_in = 12288 (SKYLA_HIP_KS12 forces
-    one) over three fused segments whose row counts are not multiples of its workgroup
-    (4096 + 333 + 1), ACCUM on and off, against the oracle at the f32 bar; rows past n_out
-    stay untouched."""
-    n_in, outs = 12288, [4096, 333, 1]
-    datas = [synth.matrix("test-ks12", f"{i}-{n}", E.DType.Q4K, n_in, n) for i, n in enumerate(outs)]
-    x = synth.activations("test-ks12", "x", n_in)
-    with env(SKYLA_HIP_KS12=shape):
-        s = Setup(ctx, [(E.DType.Q4K, n_in, n, d) for n, d in zip(outs, datas)], n_in, max(outs), rows=len(outs))
-    try:
-        y0 = synth.activations("test-ks12", "y0", (len(outs), s.s_out))
-        s.set_x(x)
-        s.set_y(y0)
-
-        def body(r):
-            g = E.Graph(r, s.k, None, None, False)
-            for i, m in enumerate(s.q):
-                g.matvec(m, (s.x_off, 0), (s.y_off + i * s.s_out, 0), accum, False)
-        rec = ctx.record(False, body)
-        try:
-            assert rec.launches() == 1           # the three dispatches run as one launch
-            ctx.replay(rec)
-        finally:
-            rec.free()
-        got = s.y(len(outs), s.s_out)
-    finally:
-        s.free()
-    for i, (n, d) in enumerate(zip(outs, datas)):
-        want = so.matvec(int(E.DType.Q4K), d, n_in, n, x)
-        part = got[i, :n].astype(np.float64) - (y0[i, :n] if accum else 0.0)
-        bar = f32_reorder_bar(E.DType.Q4K, d, n_in, n, x, want) + (4e-7 if accum else 0.0)
-        assert rel_l2(part, want) <= bar, (shape, i, rel_l2(part, want), bar)
-        assert np.array_equal(got[i, n:].view(np.uint32), y0[i, n:].view(np.uint32))
-
-
-@pytest.mark.parametrize("groups", ["1", "2", "4"])
-@pytest.mark.parametrize("accum", [False, True])
-def test_mf_shapes_against_oracle(ctx, groups, accum):
-    """The matrix-core Q4_K form (n_in = 4096; SKYLA_HIP_MF=G puts every plain Q4_K launch on
-    it with G groups of 16 rows per workgroup): three fused segments whose row counts are not
-    multiples of its workgroup, ACCUM on and off, against the oracle at the f32 bar; rows past
-    n_out stay untouched."""
-    n_in, outs = 4096, [4096, 333, 1]
-    datas = [synth.matrix("test-mf", f"{i}-{n}", E.DType.Q4K, n_in, n) for i, n in enumerate(outs)]
-    x = synth.activations("test-mf", "x", n_in)
-    with env(SKYLA_HIP_MF=groups):
-        s = Setup(ctx, [(E.DType.Q4K, n_in, n, d) for n, d in zip(outs, datas)], n_in, max(outs), rows=len(outs))
-    try:
-        y0 = synth.activations("test-mf", "y0", (len(outs), s.s_out))
-        s.set_x(x)
-        s.set_y(y0)
-
-        def body(r):
-            g = E.Graph(r, s.k, None, None, False)
-            for i, m in enumerate(s.q):
-                g.matvec(m, (s.x_off, 0), (s.y_off + i * s.s_out, 0), accum, False)
-        rec = ctx.record(False, body)
-        try:
-            assert rec.launches() == 1
-            ctx.replay(rec)
-        finally:
-            rec.free()
-        got = s.y(len(outs), s.s_out)
-    finally:
-        s.free()
-    for i, (n, d) in enumerate(zip(outs, datas)):
-        want = so.matvec(int(E.DType.Q4K), d, n_in, n, x)
-        part = got[i, :n].astype(np.float64) - (y0[i, :n] if accum else 0.0)
-        bar = f32_reorder_bar(E.DType.Q4K, d, n_in, n, x, want) + (4e-7 if accum else 0.0)
-        assert rel_l2(part, want) <= bar, (groups, i, rel_l2(part, want), bar)
-        assert np.array_equal(got[i, n:], y0[i, n:])
-
-
-@pytest.mark.parametrize("scale", [1e-30, 1e-4, 1.0, 3e4, 1e30])
-def test_mf_activation_range(ctx, scale):
-    """The matrix-core form splits x into f16 halves after a power-of-two scale per wave:
-    activations far outside the f16 range, and a vector mixing magnitudes 2^-20 .. 1 (each
-    wave's largest sets its scale), stay within the f32 bar."""
-    n_in, n_out = 4096, 512
-    d = synth.matrix("test-mf", "range", E.DType.Q4K, n_in, n_out)
-    g = synth.rng("test-mf", "range-x")
-    x = (g.standard_normal(n_in) * np.exp2(-20.0 * g.random(n_in)) * scale).astype(np.float32)
-    with env(SKYLA_HIP_MF="1"):
-        s = Setup(ctx, [(E.DType.Q4K, n_in, n_out, d)], n_in, n_out)
-    try:
-        s.set_x(x)
-        s.matvec(0)
-        got = s.y(1, n_out)[0]
-    finally:
-        s.free()
-    want = so.matvec(int(E.DType.Q4K), d, n_in, n_out, x)
-    assert np.all(np.isfinite(got))
-    assert rel_l2(got, want) <= f32_reorder_bar(E.DType.Q4K, d, n_in, n_out, x, want), rel_l2(got, want)

@@ -3,12 +3,11 @@ tiles: the launch runs the split kernel (partials in a recording-owned workspace
 split order by the last workgroup of each tile), and must agree with the single-pass kernel
 up to f32 summation order and with the oracle to the matmul bar.  Replaying the recording
 again must give the same bits (the per-tile counters are left at zero by every launch)."""
-import os
 
 import numpy as np
 import pytest
 
-from helpers import Setup, rel_l2
+from helpers import Setup, rel_l2, tactics
 from oracle import skyla_oracle as so
 from skyla_hip import engine as E
 from skyla_hip import synth
@@ -25,17 +24,10 @@ def _run(ctx, dtype, n_in, n_out, n_tok, accum, x_half, split, replays):
         x = x.astype(np.float16).astype(np.float32)
     y0 = synth.activations("mm-split", f"y0-{n_tok}-{n_out}", (n_tok, n_out))
     s = Setup(ctx, [(dtype, n_in, n_out, data)], n_in, n_out, rows=n_tok)
-    old = os.environ.get("SKYLA_HIP_SPLITK")
-    os.environ["SKYLA_HIP_SPLITK"] = split
-    try:
+    with tactics(splitk=split):
         m = s.q[0]
         ty = {E.DType.Q4K: 1, E.DType.Q6K: 2}[dtype]
         p = ctx.create_pipeline("matmul", 5, 52, [ty, int(accum), 0] + ([1] if x_half else []))
-    finally:
-        if old is None:
-            del os.environ["SKYLA_HIP_SPLITK"]
-        else:
-            os.environ["SKYLA_HIP_SPLITK"] = old
     outs = []
     try:
         w = s.weights[m.buf]
