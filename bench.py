@@ -304,7 +304,7 @@ def decode_config5(ctx: Context, contexts=(1024, 16384), steps: int = 20, warmup
     try:
         a, kvl = eng.arena, eng.arena.kv_layout
         kv_dim = c.n_head_kv * c.head_dim
-        synth.fill_kv(kvl, a.kv.host(), max(contexts), kv_dim, "qwen3-8b-q4_k_m")
+        synth.fill_kv(kvl, a.kv.host(), max(contexts), kv_dim, "qwen3-8b-q4_k_m", shared=True)
         a.kv.upload()
         mats = [v for k, v in t.items() if isinstance(v, tuple) and k != "token_embd.weight"]
         weight_bytes = sum(m[2] * E.row_bytes(m[0], m[1]) for m in mats) + E.row_bytes(E.DType.Q4K, c.n_embd)
@@ -406,6 +406,108 @@ def cpu_baseline(w: DecodeWorkload, budget_s: float = 15.0) -> dict:
                       f"sk_matvec = skyla-ref Matrix::matvec (one thread per core, row dequant + "
                       f"sequential f32 dot), -O2",
             "tok_s_equiv": round(gbs * 1e9 / w.step_bytes, 3)}
+
+
+def host_cpu() -> dict:
+    """The host the CPU baselines ran on: model name (/proc/cpuinfo), logical CPUs, and the
+    threads the oracle uses (available_parallelism, as skyla-ref's Matrix::matvec)."""
+    from oracle import skyla_oracle as so
+
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"model": model, "logical_cpus": os.cpu_count(), "threads_used": so.available_parallelism()}
+
+
+def cpu_config1(budget_s: float = 20.0) -> dict:
+    """Config 1 on the CPU: skyla-ref's Model::forward (oracle/model.py: Matrix::matvec per
+    weight, f32 KV cache) over the Qwen3-0.6B Q8_0 model with 28 distinct seeded layers
+    (633 MB of weights streamed per token), the 16-token prompt, then greedy decode steps
+    until 64 or about budget_s seconds; tok/s over the decode steps."""
+    from oracle import skyla_oracle as so
+    from oracle.model import Model
+
+    c = synth.qwen3_config("qwen3-0.6b")
+    t = synth.qwen3("qwen3-0.6b-q8_0", c, "q8_0", "ones", shared_layers=False)
+    prompt = synth.prompt("qwen3-0.6b-q8_0", 16, c.n_vocab)
+    m = Model(c, t)
+    t0 = time.perf_counter()
+    for tok in prompt:
+        logits = m.forward(tok)
+    t_prompt = time.perf_counter() - t0
+    tok, steps, t1 = so.argmax(logits), 0, time.perf_counter()
+    while steps < 64 and time.perf_counter() - t1 < budget_s:
+        tok = so.argmax(m.forward(tok))
+        steps += 1
+    el = time.perf_counter() - t1
+    return {"value": round(steps / el, 2), "unit": "tok/s", "cores": so.available_parallelism(), "kind": "port",
+            "sample": f"Qwen3-0.6B Q8_0 (28 distinct layers): 16-token prompt ({t_prompt:.1f} s, "
+                      f"{16 / t_prompt:.2f} tok/s) then {steps} greedy decode steps ({el:.1f} s); oracle/model.py "
+                      f"= skyla-ref Model::forward with Matrix::matvec (one thread per core), f32 KV",
+            "prompt_tok_s": round(16 / t_prompt, 2)}
+
+
+def cpu_config3(budget_s: float = 10.0, n_tok: int = 16) -> dict:
+    """Config 3 on the CPU: skyla-ref's f32 GEMM (one Matrix::matvec per token row, the
+    oracle's sk_matmul) over the q, gate and down matrices of config 3 on the first n_tok of
+    the 512 f16-valued N(0,1) rows, repeated for about budget_s seconds; GFLOP/s, and the
+    time M = 512 would take at that rate."""
+    from oracle import skyla_oracle as so
+
+    mats = [(name, dt, n_in, n_out, synth.matrix(CONFIG, name, dt, n_in, n_out))
+            for name, dt, n_in, n_out in [("q", E.DType.Q4K, N_EMBD, N_EMBD), ("gate", E.DType.Q4K, N_EMBD, N_FF),
+                                          ("down", E.DType.Q6K, N_FF, N_EMBD)]]
+    xs = {n_in: synth.activations("qwen3-8b-prefill", f"x-512-{n_in}", (512, n_in))[:n_tok]
+          .astype(np.float16).astype(np.float32) for n_in in (N_EMBD, N_FF)}
+    flops_pass = sum(2.0 * n_tok * n_in * n_out for _, _, n_in, n_out, _ in mats)
+    passes, t0 = 0, time.perf_counter()
+    while True:
+        for _, dt, n_in, n_out, d in mats:
+            so.matmul(int(dt), d, n_in, n_out, xs[n_in])
+        passes += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s:
+            break
+    gflops = passes * flops_pass / el / 1e9
+    m512 = sum(2.0 * 512 * n_in * n_out for _, _, n_in, n_out, _ in mats) / (gflops * 1e9)
+    return {"value": round(gflops, 2), "unit": "GFLOP/s", "cores": so.available_parallelism(), "kind": "port",
+            "sample": f"{passes} passes of q, gate, down (Q4_K, Q4_K, Q6_K) over {n_tok} of the 512 token rows, "
+                      f"{el:.1f} s; oracle sk_matmul = skyla-ref's M x Matrix::matvec",
+            "m512_q_gate_down_s": round(m512, 2)}
+
+
+def cpu_config4(budget_s: float = 10.0) -> dict:
+    """Config 4 on the CPU: skyla-ref's Ffn::forward Moe arm (route, then the selected
+    experts' swiglu, the oracle's sk_moe_forward) over the config-4 layer, one token at a
+    time, for about budget_s seconds; us per token per layer and the GB/s of the experts
+    and router it reads."""
+    from oracle import skyla_oracle as so
+
+    router = synth.router(MOE_CFG, "router", MOE_EXPERT, MOE_EMBD)
+    d = {name: synth.matrix(MOE_CFG, f"{name}_exps", E.DType.Q4K, n_in, n_out, MOE_EXPERT)
+         for name, n_in, n_out in [("gate", MOE_EMBD, MOE_FF), ("up", MOE_EMBD, MOE_FF), ("down", MOE_FF, MOE_EMBD)]}
+    g = synth.rng(MOE_CFG, "cpu-tokens")
+    q = int(E.DType.Q4K)
+    tokens, t0 = 0, time.perf_counter()
+    while True:
+        n = g.standard_normal(MOE_EMBD, dtype=np.float32)
+        so.moe_forward(router, q, d["gate"], q, d["up"], q, d["down"], MOE_EMBD, MOE_FF, MOE_EXPERT, MOE_USED, n)
+        tokens += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s:
+            break
+    us = el / tokens * 1e6
+    moved = MOE_USED * 3 * MOE_FF * E.row_bytes(E.DType.Q4K, MOE_EMBD) + MOE_EXPERT * MOE_EMBD * 4
+    return {"value": round(us, 1), "unit": "us per token per layer", "cores": so.available_parallelism(),
+            "kind": "port", "gbs": round(moved / us / 1e3, 2),
+            "sample": f"{tokens} single-token MoE layer forwards (route + 8 experts' swiglu), {el:.1f} s; "
+                      f"oracle sk_moe_forward = skyla-ref Ffn::forward Moe arm"}
 
 
 def parity_check(w: DecodeWorkload) -> float:
@@ -521,8 +623,12 @@ def main() -> int:
         log(f"end-to-end decode (config 5): {e2e}")
         log(f"end-to-end decode (config 1): {e2e1}")
     cpu = None if args.no_cpu else cpu_baseline(w, args.cpu_seconds)
+    cpus = None
     if cpu:
         log(f"cpu baseline {cpu['value']} GB/s on {cpu['cores']} threads")
+        cpus = {"host": host_cpu(), "config1_decode": cpu_config1(), "config3_gemm": cpu_config3(),
+                "config4_moe": cpu_config4()}
+        log(f"cpu baselines: {cpus}")
 
     # HBM bytes of the matvec_q4k launches of one layer, measured with rocprofv3 PMC
     # (FETCH_SIZE / WRITE_SIZE scaled by known-size kernels), spread over this run's launches
@@ -568,6 +674,7 @@ def main() -> int:
         "decode_e2e_config5": e2e,
         "decode_e2e_config1": e2e1,
         "cpu_baseline": cpu,
+        "cpu_baselines": cpus,
     }
     step.free()
     w.free()

@@ -33,14 +33,18 @@ class Model:
         self.v_cache = [[] for _ in range(self.c.n_layer)]
         self.pos = 0
 
-    def load_cache(self, keys: np.ndarray, values: np.ndarray) -> None:
-        """A pre-filled context: positions [0, n) of every layer's cache hold the rows
-        keys / values [n, kv_dim] (as the attention reads them back), and the next forward
-        runs at position n."""
-        n = keys.shape[0]
+    def load_cache(self, keys, values) -> None:
+        """A pre-filled context: positions [0, n) of each layer's cache hold the rows
+        keys / values (as the attention reads them back), and the next forward runs at
+        position n.  keys / values are [n, kv_dim] arrays for every layer, or one such
+        array per layer."""
+        per_layer = not isinstance(keys, np.ndarray)
+        n = (keys[0] if per_layer else keys).shape[0]
         for l in range(self.c.n_layer):
-            self.k_cache[l] = [np.ascontiguousarray(keys, np.float32).reshape(-1)]
-            self.v_cache[l] = [np.ascontiguousarray(values, np.float32).reshape(-1)]
+            kl, vl = (keys[l], values[l]) if per_layer else (keys, values)
+            assert kl.shape[0] == n and vl.shape[0] == n
+            self.k_cache[l] = [np.ascontiguousarray(kl, np.float32).reshape(-1)]
+            self.v_cache[l] = [np.ascontiguousarray(vl, np.float32).reshape(-1)]
         self.pos = n
 
     def _mv(self, name: str, x: np.ndarray) -> np.ndarray:

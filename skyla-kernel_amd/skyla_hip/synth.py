@@ -182,29 +182,34 @@ def qwen3moe(config: str, c, norms: str = "random") -> dict:
     return t
 
 
-def fill_kv(layout, kv_host: np.ndarray, n_pos: int, kv_dim: int, config: str) -> None:
+def fill_kv(layout, kv_host: np.ndarray, n_pos: int, kv_dim: int, config: str, shared: bool = False) -> None:
     """Positions [0, n_pos) of every layer's cache, in the host mirror of the KV buffer,
     with seeded N(0,1) keys and values stored at the layout's precision (f16 rows, or 8-bit
     rows with one f16 scale max|y| / 127 per 32 values, as the KV write kernel stores them).
-    One layer's rows are drawn and copied into every layer."""
-    g = rng(config, "kv")
+    Layer l's rows come from their own seed, so a layer that read another layer's slot
+    would see other values; with `shared` one layer's rows are drawn and copied into every
+    layer (cheaper, for timing runs)."""
     pr = layout.precision
-    for keys, q8 in ((True, pr.keys_q8), (False, pr.values_q8)):
-        y = g.standard_normal(size=(n_pos * kv_dim // 32, 32), dtype=np.float32)
-        if q8:
-            s = (np.abs(y).max(1) / np.float32(127.0)).astype(np.float32)
-            q = np.rint(y / s[:, None]).astype(np.int8).reshape(-1)
-            sh = s.astype(np.float16)
-        else:
-            h = y.reshape(-1).astype(np.float16)
-        for l in range(len(layout.slots)):
+    drawn = None
+    for l in range(len(layout.slots)):
+        if drawn is None or not shared:
+            g = rng(config, "kv" if shared else f"kv-{l}")
+            drawn = []
+            for q8 in (pr.keys_q8, pr.values_q8):
+                y = g.standard_normal(size=(n_pos * kv_dim // 32, 32), dtype=np.float32)
+                if q8:
+                    sc = (np.abs(y).max(1) / np.float32(127.0)).astype(np.float32)
+                    drawn.append((np.rint(y / sc[:, None]).astype(np.int8).reshape(-1), sc.astype(np.float16)))
+                else:
+                    drawn.append((y.reshape(-1).astype(np.float16), None))
+        for keys, (rows, scales) in zip((True, False), drawn):
             off = layout.keys(l) if keys else layout.values(l)
-            if q8:
-                kv_host.view(np.int8)[off: off + q.size] = q
+            if scales is not None:
+                kv_host.view(np.int8)[off: off + rows.size] = rows
                 so = layout.key_scales(l) if keys else layout.value_scales(l)
-                kv_host.view("<f2")[so: so + sh.size] = sh
+                kv_host.view("<f2")[so: so + scales.size] = scales
             else:
-                kv_host.view("<f2")[off: off + h.size] = h
+                kv_host.view("<f2")[off: off + rows.size] = rows
 
 
 def prompt(config: str, n: int, n_vocab: int) -> list[int]:

@@ -416,15 +416,15 @@ def test_attention_prep_equals_qkv_prep_then_attention(ctx, precision, pos0, hea
         b.free()
 
 
-def _stored_rows(kvl, kv_host, n_pos, kv_dim):
-    """Layer 0's first n_pos cache rows as the attention reads them back (f16 keys; 8-bit
+def _stored_rows(kvl, kv_host, n_pos, kv_dim, layer=0):
+    """A layer's first n_pos cache rows as the attention reads them back (f16 keys; 8-bit
     values times their f16 scale), from the host mirror synth.fill_kv wrote."""
     pr = kvl.precision
     assert not pr.keys_q8 and pr.values_q8
-    k = kv_host.view("<f2")[kvl.keys(0): kvl.keys(0) + n_pos * kv_dim].astype(np.float32)
-    q = kv_host.view(np.int8)[kvl.values(0): kvl.values(0) + n_pos * kv_dim].astype(np.float32)
-    sc = kv_host.view("<f2")[kvl.value_scales(0): kvl.value_scales(0) + n_pos * kv_dim // 32].astype(np.float32)
-    v = (q.reshape(-1, 32) * sc[:, None]).reshape(n_pos, kv_dim)
+    k = kv_host.view("<f2")[kvl.keys(layer): kvl.keys(layer) + n_pos * kv_dim].astype(np.float32)
+    q = kv_host.view(np.int8)[kvl.values(layer): kvl.values(layer) + n_pos * kv_dim].astype(np.float32)
+    sc = kv_host.view("<f2")[kvl.value_scales(layer): kvl.value_scales(layer) + n_pos * kv_dim // 32]
+    v = (q.reshape(-1, 32) * sc.astype(np.float32)[:, None]).reshape(n_pos, kv_dim)
     return k.reshape(n_pos, kv_dim), v
 
 
@@ -434,7 +434,9 @@ def test_config5_qwen3_8b_prefilled_contexts(ctx):
     the f16-key / 8-bit-value cache pre-filled with N(0,1) rows to 16384 positions (256
     splits of 64 merged) and then to 1024, three teacher-forced steps at each, against the
     oracle Model holding the same stored rows: top-1 equal at every step, logits within
-    2e-2 relative L2 (engine.rs:137-152, arena.rs:83-181, kv.rs:33-88)."""
+    2e-2 relative L2 (engine.rs:137-152, arena.rs:83-181, kv.rs:33-88).  Every layer's
+    cache rows are drawn from their own seed and the oracle holds each layer's own rows, so
+    a layer reading another layer's cache slot would not match."""
     c = synth.qwen3_config("qwen3-8b")
     t = synth.qwen3("qwen3-8b-q4_k_m", c, "q4_k_m", "ones", shared_layers=True)
     kv_dim = c.n_head_kv * c.head_dim
@@ -443,11 +445,12 @@ def test_config5_qwen3_8b_prefilled_contexts(ctx):
         kvl, kv_host = eng.arena.kv_layout, eng.arena.kv.host()
         synth.fill_kv(kvl, kv_host, 16384, kv_dim, "qwen3-8b-q4_k_m")
         eng.arena.kv.upload()
-        keys, values = _stored_rows(kvl, kv_host, 16384, kv_dim)
+        rows = [_stored_rows(kvl, kv_host, 16384, kv_dim, l) for l in range(c.n_layer)]
+        assert not np.array_equal(rows[0][0][:4], rows[1][0][:4])  # distinct rows per layer
         # 16384 first: the 1024 case's steps overwrite positions 1024..1026 of the fill
         for n_ctx in (16384, 1024):
             oracle = Model(c, t, (False, True))
-            oracle.load_cache(keys[:n_ctx], values[:n_ctx])
+            oracle.load_cache([k[:n_ctx] for k, _ in rows], [v[:n_ctx] for _, v in rows])
             eng.pos = n_ctx
             top = Top1()
             tok = synth.prompt("qwen3-8b-q4_k_m", 1, c.n_vocab)[0]

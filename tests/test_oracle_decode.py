@@ -141,20 +141,45 @@ def test_kv_quantize_q8_closed_forms():
     assert np.array_equal(so.kv_stored(y, False), y.astype(np.float16).astype(np.float32))
 
 
-def test_fill_kv_rows_per_layer():
-    """synth.fill_kv (the bench's N(0,1) pre-fill): every layer's first n_pos rows hold the same
-    f16 keys and 8-bit values; each 32-value block's largest quant is +-127; about N(0,1)."""
+@pytest.mark.parametrize("shared", [False, True])
+def test_fill_kv_rows_per_layer(shared):
+    """synth.fill_kv (the N(0,1) pre-fill): each layer's first n_pos rows hold f16 keys and
+    8-bit values whose 32-value blocks reach +-127, about N(0,1); the layers' rows differ
+    (each its own seed), or with `shared` every layer holds the same rows."""
     layout = E.KvLayout(E.KvPrecision.F16_KEYS_Q8_VALUES, [True] * 3, 96, 256)
     host = np.zeros(layout.bytes(), np.uint8)
-    synth.fill_kv(layout, host, 64, 256, "test-fill")
+    synth.fill_kv(layout, host, 64, 256, "test-fill", shared=shared)
     n = 64 * 256
     keys = [host.view("<f2")[layout.keys(l): layout.keys(l) + n].astype(np.float32) for l in range(3)]
     vals = [host.view(np.int8)[layout.values(l): layout.values(l) + n] for l in range(3)]
     scl = [host.view("<f2")[layout.value_scales(l): layout.value_scales(l) + n // 32] for l in range(3)]
-    assert all(np.array_equal(keys[0], k) for k in keys) and all(np.array_equal(vals[0], v) for v in vals)
-    assert np.array_equal(np.abs(vals[0].reshape(-1, 32).astype(np.int32)).max(1), np.full(n // 32, 127))
-    v = vals[0].reshape(-1, 32).astype(np.float32) * scl[0].astype(np.float32)[:, None]
-    for x in (keys[0], v.reshape(-1)):
-        assert abs(float(x.mean())) < 0.05 and abs(float(x.std()) - 1.0) < 0.05
-    # rows past n_pos stay untouched
-    assert not host.view("<f2")[layout.keys(0) + n: layout.keys(0) + 96 * 256].any()
+    for l in (1, 2):
+        same = np.array_equal(keys[0], keys[l]) and np.array_equal(vals[0], vals[l])
+        assert same == shared, l
+    for l in range(3):
+        assert np.array_equal(np.abs(vals[l].reshape(-1, 32).astype(np.int32)).max(1), np.full(n // 32, 127))
+        v = vals[l].reshape(-1, 32).astype(np.float32) * scl[l].astype(np.float32)[:, None]
+        for x in (keys[l], v.reshape(-1)):
+            assert abs(float(x.mean())) < 0.05 and abs(float(x.std()) - 1.0) < 0.05
+        # rows past n_pos stay untouched
+        assert not host.view("<f2")[layout.keys(l) + n: layout.keys(l) + 96 * 256].any()
+
+
+def test_model_load_cache_per_layer():
+    """Model.load_cache with one row set per layer: each layer's attention reads its own
+    rows (a forward differs from the one with layer 0's rows in every layer)."""
+    from oracle.model import Model
+    c = synth.qwen3_config("tiny")
+    t = synth.qwen3("test-load-cache", c, "q4_k_m", "random")
+    kv_dim = c.n_head_kv * c.head_dim
+    g = synth.rng("test-load-cache", "rows")
+    rows = [(g.standard_normal((5, kv_dim)).astype(np.float32), g.standard_normal((5, kv_dim)).astype(np.float32))
+            for _ in range(c.n_layer)]
+    per, same = Model(c, t, (False, False)), Model(c, t, (False, False))
+    per.load_cache([k for k, _ in rows], [v for _, v in rows])
+    same.load_cache(rows[0][0], rows[0][1])
+    assert per.pos == same.pos == 5
+    for l in range(c.n_layer):
+        assert np.array_equal(per.k_cache[l][0], rows[l][0].reshape(-1))
+        assert np.array_equal(same.k_cache[l][0], rows[0][0].reshape(-1))
+    assert not np.array_equal(per.forward(1), same.forward(1))
