@@ -6,8 +6,8 @@ skyla_oracle.c: Matrix::row / matvec, rmsnorm, rmsnorm_inplace, rope_neox, the a
 model.rs:150-169 and the two arms of Ffn::forward (ffn.rs:58-76: swiglu, or route then the
 weighted sum of the selected experts' swiglu for a qwen3moe layer), with the f32 KV cache
 the reference keeps.  Element-wise additions are numpy float32 (one IEEE rounding each, as
-Rust's).  No RoPE scaling, no output gate, no recurrent layers: the attention layouts of
-the Qwen3 decode configurations.
+Rust's).  RoPE with or without YaRN scaling; no output gate, no recurrent layers: the
+attention layouts of the Qwen3 decode configurations.
 
 `kv_store` selects the cache the attention reads: None keeps the reference CPU model's f32
 rows (model.rs:140-148); a pair (keys_q8, values_q8) stores every key and value row as the
@@ -24,7 +24,12 @@ from . import skyla_oracle as so
 class Model:
     def __init__(self, c, tensors: dict, kv_store: tuple[bool, bool] | None = None):
         self.c, self.t, self.kv_store = c, tensors, kv_store
-        self.freqs = so.rope_freqs(c.head_dim, c.rope_theta)
+        # Config::from_gguf's (rope_freqs, rope_mscale) (lib.rs:96-97, rope.rs:36-58)
+        scaling = getattr(c, "rope_scaling", None)
+        if scaling is None:
+            self.freqs, self.mscale = so.rope_freqs(c.head_dim, c.rope_theta), 1.0
+        else:
+            self.freqs, self.mscale = so.rope_freqs_yarn(c.head_dim, c.rope_theta, *scaling)
         self.reset()
 
     def reset(self) -> None:
@@ -60,7 +65,7 @@ class Model:
             for h in range(heads):
                 part = x[h * hd:(h + 1) * hd]
                 so.rmsnorm_inplace(part, self.t[w], c.eps)
-                so.rope_neox(part, self.pos, self.freqs, c.rope_mscale)
+                so.rope_neox(part, self.pos, self.freqs, self.mscale)
         if self.kv_store is not None:
             k, v = so.kv_stored(k, self.kv_store[0]), so.kv_stored(v, self.kv_store[1])
         self.k_cache[l].append(k)

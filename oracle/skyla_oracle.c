@@ -252,6 +252,31 @@ void sk_rope_freqs(uint64_t head_dim, float theta, float *out) {
     for (uint64_t i = 0; i < head_dim / 2; i++) out[i] = powf(theta, -2.0f * (float)i / d);
 }
 
+/* rope.rs:32-34 corr_dim: the dimension whose wavelength makes n_rot turns over
+ * original_ctx positions, n_dims * ln(original_ctx / (n_rot * 2 pi)) / (2 ln base) */
+static float corr_dim(float n_dims, float original_ctx, float n_rot, float base) {
+    return n_dims * logf(original_ctx / (n_rot * 2.0f * (float)M_PI)) / (2.0f * logf(base));
+}
+
+/* rope.rs:36-58 frequencies with YaRN scaling (factor, original_ctx, attn_factor): each
+ * base frequency f_i times freq_scale (1 - mix) + mix, where mix ramps from 1 below the
+ * dimension of beta_fast = 32 turns to 0 above that of beta_slow = 1 turn and freq_scale =
+ * 1 / factor; returns the magnitude scale attn_factor * (1 + 0.1 ln(1 / freq_scale)). */
+float sk_rope_freqs_yarn(uint64_t head_dim, float theta, float factor, float original_ctx, float attn_factor,
+                         float *out) {
+    const float d = (float)head_dim;
+    const float freq_scale = 1.0f / factor;
+    const float low = fmaxf(floorf(corr_dim(d, original_ctx, 32.0f, theta)), 0.0f);
+    const float high = fminf(ceilf(corr_dim(d, original_ctx, 1.0f, theta)), d - 1.0f);
+    for (uint64_t i = 0; i < head_dim / 2; i++) {
+        const float f = powf(theta, -2.0f * (float)i / d);
+        const float y = ((float)i - low) / fmaxf(high - low, 0.001f);
+        const float mix = 1.0f - fminf(fmaxf(y, 0.0f), 1.0f);
+        out[i] = f * (freq_scale * (1.0f - mix) + mix);
+    }
+    return attn_factor * (1.0f + 0.1f * logf(1.0f / freq_scale));
+}
+
 /* rope.rs:60-68 rope_neox over x[0..n): pairs (i, i + n/2) rotated by pos * freqs[i] */
 void sk_rope_neox(float *x, uint64_t n, uint64_t pos, const float *freqs, float mscale) {
     uint64_t half = n / 2;

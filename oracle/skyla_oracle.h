@@ -90,6 +90,8 @@ uint32_t sk_available_parallelism(void);
 /* The rest of the dense decode step (skyla-ref/src/ops.rs, rope.rs, model.rs:131-170). */
 void sk_rmsnorm_inplace(float *x, const float *w, uint64_t n, float eps);
 void sk_rope_freqs(uint64_t head_dim, float theta, float *out);
+float sk_rope_freqs_yarn(uint64_t head_dim, float theta, float factor, float original_ctx, float attn_factor,
+                         float *out);
 void sk_rope_neox(float *x, uint64_t n, uint64_t pos, const float *freqs, float mscale);
 void sk_attention(const float *q, const float *k_cache, const float *v_cache, uint64_t n_pos,
                   uint64_t n_head, uint64_t n_head_kv, uint64_t hd, float *scores, float *out);

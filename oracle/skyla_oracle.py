@@ -76,6 +76,8 @@ def lib() -> C.CDLL:
         l.sk_rmsnorm_inplace.argtypes = [_f, _f, C.c_uint64, C.c_float]
         l.sk_rope_freqs.restype = None
         l.sk_rope_freqs.argtypes = [C.c_uint64, C.c_float, _f]
+        l.sk_rope_freqs_yarn.restype = C.c_float
+        l.sk_rope_freqs_yarn.argtypes = [C.c_uint64, C.c_float, C.c_float, C.c_float, C.c_float, _f]
         l.sk_rope_neox.restype = None
         l.sk_rope_neox.argtypes = [_f, C.c_uint64, C.c_uint64, _f, C.c_float]
         l.sk_attention.restype = None
@@ -239,6 +241,14 @@ def rope_freqs(head_dim: int, theta: float) -> np.ndarray:
     out = np.zeros(head_dim // 2, np.float32)
     lib().sk_rope_freqs(head_dim, theta, _p(out, _f))
     return out
+
+
+def rope_freqs_yarn(head_dim: int, theta: float, factor: float, original_ctx: float,
+                    attn_factor: float) -> tuple[np.ndarray, float]:
+    """rope.rs:36-58 frequencies with YaRN scaling, and the magnitude scale mscale."""
+    out = np.zeros(head_dim // 2, np.float32)
+    m = lib().sk_rope_freqs_yarn(head_dim, theta, factor, original_ctx, attn_factor, _p(out, _f))
+    return out, float(m)
 
 
 def rope_neox(x: np.ndarray, pos: int, freqs: np.ndarray, mscale: float = 1.0) -> None:

@@ -322,7 +322,8 @@ class Kernels:
 @dataclasses.dataclass
 class Config:
     """The fields of skyla_ref::Config (skyla-ref/src/lib.rs:17-37) the path reads (the
-    plain attention layout: no RoPE scaling, n_rot = head_dim, no output gate)."""
+    attention layouts of qwen3, qwen3moe and qwen3vl text: n_rot = head_dim, no output gate,
+    no recurrent layers; RoPE with or without YaRN scaling)."""
     n_embd: int
     n_ff: int = 0
     n_head: int = 1
@@ -335,25 +336,70 @@ class Config:
     eps: float = 1e-6
     n_layer: int = 0
     rope_theta: float = 1e6
-    rope_mscale: float = 1.0
+    # YaRN (rope.rs:7-31): (factor, original context length, attn_factor), or None
+    rope_scaling: tuple | None = None
+
+    @property
+    def rope_mscale(self) -> float:
+        """rope.rs:56: the magnitude YaRN puts on every rotated pair (1 without scaling)."""
+        return rope_table(self)[1]
 
 
 _libm = None
 
 
-def rope_frequencies(c: Config) -> np.ndarray:
-    """rope.rs:36-40 without scaling: theta^(-2i / head_dim), with the f32 exponent and the
-    C library's powf that Rust's f32::powf calls."""
+def _libm_f32(name: str):
+    """The C library's f32 function `name` (powf, logf): the ones Rust's f32::powf and
+    f32::ln call on this platform."""
     global _libm
     if _libm is None:
         import ctypes
         import ctypes.util
         _libm = ctypes.CDLL(ctypes.util.find_library("m"))
-        _libm.powf.restype = ctypes.c_float
-        _libm.powf.argtypes = [ctypes.c_float, ctypes.c_float]
-    d = np.float32(c.head_dim)
-    out = [_libm.powf(np.float32(c.rope_theta), np.float32(-2.0) * np.float32(i) / d) for i in range(c.head_dim // 2)]
-    return np.asarray(out, np.float32)
+        for fn, n_args in (("powf", 2), ("logf", 1)):
+            f = getattr(_libm, fn)
+            f.restype = ctypes.c_float
+            f.argtypes = [ctypes.c_float] * n_args
+    return getattr(_libm, name)
+
+
+def _corr_dim(n_dims: np.float32, original_ctx: np.float32, n_rot: float, base: np.float32) -> np.float32:
+    """rope.rs:32-34, in f32."""
+    f32, logf = np.float32, _libm_f32("logf")
+    turns = f32(f32(f32(n_rot) * f32(2.0)) * f32(np.pi))  # n_rot * 2 * pi, left to right
+    return f32(n_dims * f32(logf(f32(original_ctx / turns)))) / f32(f32(2.0) * f32(logf(base)))
+
+
+def rope_table(c: Config) -> tuple[np.ndarray, float]:
+    """rope.rs:36-58: the RoPE frequency of every pair, theta^(-2i / head_dim) with the f32
+    exponent and the C library's powf, and under YaRN scaling each times
+    freq_scale (1 - mix) + mix, mix ramping from 1 below the dimension of 32 turns over the
+    original context to 0 above that of 1 turn; and the magnitude scale
+    attn_factor (1 + 0.1 ln(1 / freq_scale)) (1 without scaling).  f32 arithmetic throughout,
+    one rounding per operation as in Rust."""
+    f32 = np.float32
+    powf = _libm_f32("powf")
+    d = f32(c.head_dim)
+    base = [f32(powf(f32(c.rope_theta), f32(-2.0) * f32(i) / d)) for i in range(c.head_dim // 2)]
+    if c.rope_scaling is None:
+        return np.asarray(base, np.float32), 1.0
+    factor, original_ctx, attn_factor = (f32(v) for v in c.rope_scaling)
+    theta = f32(c.rope_theta)
+    freq_scale = f32(1.0) / factor
+    low = max(f32(np.floor(_corr_dim(d, original_ctx, 32.0, theta))), f32(0.0))
+    high = min(f32(np.ceil(_corr_dim(d, original_ctx, 1.0, theta))), f32(d - f32(1.0)))
+    out = []
+    for i, f in enumerate(base):
+        y = f32(f32(i) - low) / max(f32(high - low), f32(0.001))
+        mix = f32(1.0) - min(max(y, f32(0.0)), f32(1.0))
+        out.append(f32(f * f32(f32(freq_scale * f32(f32(1.0) - mix)) + mix)))
+    mscale = f32(attn_factor * f32(f32(1.0) + f32(f32(0.1) * f32(_libm_f32("logf")(f32(f32(1.0) / freq_scale))))))
+    return np.asarray(out, np.float32), float(mscale)
+
+
+def rope_frequencies(c: Config) -> np.ndarray:
+    """The frequency table the attention kernels read (rope_table's first half)."""
+    return rope_table(c)[0]
 
 
 # ---- kv.rs -------------------------------------------------------------------------------

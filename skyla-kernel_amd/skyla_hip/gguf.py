@@ -175,19 +175,36 @@ def write(path: str, metadata: dict, tensors: list, alignment: int = 32) -> None
 
 
 # ---- skyla-ref Config::from_gguf and the tensor map ------------------------------------
-ARCHS = ("qwen3", "qwen3moe")
+# Config::from_gguf also accepts qwen35 (skyla-ref/src/lib.rs:80-83), whose recurrent
+# layers and gated attention output are not on this path.
+ARCHS = ("qwen3", "qwen3moe", "qwen3vl")
+
+
+def rope_scaling_from_gguf(g: Gguf, arch: str):
+    """RopeScaling::from_gguf (skyla-ref/src/rope.rs:14-30): (factor, original context
+    length, attn_factor) for "yarn", None when the type is absent or "none"."""
+    k = lambda s: f"{arch}.rope.scaling.{s}"  # noqa: E731
+    kind = g.metadata.get(k("type"))
+    if kind is None or kind == "none":
+        return None
+    if kind != "yarn":
+        raise ValueError(f"unsupported rope scaling {kind}")
+    f32 = lambda v: float(np.float32(v))  # noqa: E731  (meta_f64 as f32)
+    return (f32(g.meta(k("factor"))), f32(g.meta(k("original_context_length"))),
+            f32(g.metadata.get(k("attn_factor"), 1.0)))
 
 
 def config_from_gguf(g: Gguf) -> Config:
-    """skyla-ref/src/lib.rs:77-121 for the plain attention layouts (no RoPE scaling, no
-    recurrent layers, n_rot = head_dim)."""
+    """skyla-ref/src/lib.rs:77-121 for the attention layouts of qwen3, qwen3moe and the
+    qwen3vl text model (n_rot = head_dim, no recurrent layers); layers past block_count -
+    nextn_predict_layers (the multi-token prediction heads) are not part of the model."""
     arch = g.meta("general.architecture")
     if arch not in ARCHS:
         raise ValueError(f"unsupported architecture {arch} (the GPU path serves {', '.join(ARCHS)})")
     k = lambda s: f"{arch}.{s}"  # noqa: E731
     opt = lambda s: int(g.metadata.get(k(s), 0))  # noqa: E731
-    if k("rope.scaling.type") in g.metadata and g.metadata[k("rope.scaling.type")] not in ("none", ""):
-        raise ValueError("RoPE scaling is outside the GPU path")
+    if g.metadata.get(k("ssm.state_size")) is not None:
+        raise ValueError("recurrent (ssm) layers are outside the GPU path")
     n_embd, n_head = int(g.meta(k("embedding_length"))), int(g.meta(k("attention.head_count")))
     head_dim = int(g.metadata.get(k("attention.key_length"), n_embd // n_head))
     n_rot = opt("rope.dimension_count") or head_dim
@@ -200,7 +217,8 @@ def config_from_gguf(g: Gguf) -> Config:
         n_expert_used=opt("expert_used_count"), n_ff_expert=opt("expert_feed_forward_length"),
         eps=float(np.float32(g.meta(k("attention.layer_norm_rms_epsilon")))),
         n_layer=int(g.meta(k("block_count"))) - opt("nextn_predict_layers"),
-        rope_theta=float(np.float32(g.meta(k("rope.freq_base")))))
+        rope_theta=float(np.float32(g.meta(k("rope.freq_base")))),
+        rope_scaling=rope_scaling_from_gguf(g, arch))
 
 
 def tensors_from_gguf(g: Gguf) -> dict:
@@ -230,6 +248,11 @@ def write_model(path: str, arch: str, c: Config, tensors: dict) -> None:
             f"{arch}.feed_forward_length": (U32, c.n_ff),
             f"{arch}.rope.freq_base": (F32, c.rope_theta),
             f"{arch}.attention.layer_norm_rms_epsilon": (F32, c.eps)}
+    if c.rope_scaling is not None:
+        factor, original_ctx, attn_factor = c.rope_scaling
+        meta.update({f"{arch}.rope.scaling.type": (STR, "yarn"), f"{arch}.rope.scaling.factor": (F32, factor),
+                     f"{arch}.rope.scaling.original_context_length": (U32, int(original_ctx)),
+                     f"{arch}.rope.scaling.attn_factor": (F32, attn_factor)})
     if c.n_expert:
         meta.update({f"{arch}.expert_count": (U32, c.n_expert), f"{arch}.expert_used_count": (U32, c.n_expert_used),
                      f"{arch}.expert_feed_forward_length": (U32, c.n_ff_expert)})

@@ -8,7 +8,8 @@ every step is float64 numpy:
   per layer: n = rmsnorm(x) * attn_norm; x += attention(n)     (model.rs:104-112, ops.rs:1-16)
              n = rmsnorm(x) * ffn_norm;  x += ffn(n)           (model.rs:113-114)
   attention: q, k, v = Wq n, Wk n, Wv n; per head rmsnorm * q_norm / k_norm, then NeoX
-             RoPE of the (i, i + head_dim/2) pairs by pos * theta^(-2i/head_dim); the KV
+             RoPE of the (i, i + head_dim/2) pairs by pos * theta^(-2i/head_dim) (under
+             YaRN the frequencies of yarn64, every pair scaled by its magnitude); the KV
              cache keeps k, v; head h reads kv head h / (n_head / n_head_kv); softmax of
              q.k / sqrt(head_dim) over the positions so far; Wo of the heads' sums
                                                                (model.rs:131-170, rope.rs:36-67)
@@ -40,6 +41,24 @@ def _silu(x: np.ndarray) -> np.ndarray:
     return x * 0.5 * (1.0 + np.tanh(0.5 * x))   # x / (1 + e^-x), without overflow
 
 
+def yarn64(head_dim: int, theta: float, factor: float, original_ctx: float, attn_factor: float):
+    """YaRN's RoPE frequencies and magnitude in float64, from the method (Peng et al., "YaRN:
+    Efficient Context Window Extension of Large Language Models", 2023): pair i keeps its
+    frequency theta^(-2i/d) where it turns more than beta_fast = 32 times over the original
+    context, is interpolated by 1/factor where it turns less than beta_slow = 1 time, and
+    ramps linearly between the two (whole) dimensions; every rotated pair is scaled by
+    attn_factor (1 + 0.1 ln factor)  (rope.rs:4-58)."""
+    d = float(head_dim)
+    base = theta ** (-2.0 * np.arange(head_dim // 2) / d)
+
+    def dim_of(turns):  # the i at which the wavelength 2 pi / base_i spans original_ctx / turns
+        return d * np.log(original_ctx / (turns * 2.0 * np.pi)) / (2.0 * np.log(theta))
+
+    low, high = max(np.floor(dim_of(32.0)), 0.0), min(np.ceil(dim_of(1.0)), d - 1.0)
+    keep = 1.0 - np.clip((np.arange(head_dim // 2) - low) / max(high - low, 0.001), 0.0, 1.0)
+    return base * (keep + (1.0 - keep) / factor), attn_factor * (1.0 + 0.1 * np.log(factor))
+
+
 class Model64:
     def __init__(self, c, tensors: dict):
         self.c = c
@@ -47,6 +66,9 @@ class Model64:
         self.head = self.w.get("output.weight", self.w["token_embd.weight"])
         hd = c.head_dim
         self.freqs = c.rope_theta ** (-2.0 * np.arange(hd // 2) / hd)
+        self.mscale = 1.0
+        if getattr(c, "rope_scaling", None) is not None:
+            self.freqs, self.mscale = yarn64(hd, c.rope_theta, *c.rope_scaling)
         self.k_cache = [[] for _ in range(c.n_layer)]
         self.v_cache = [[] for _ in range(c.n_layer)]
         self.pos = 0
@@ -56,7 +78,8 @@ class Model64:
         half = h.size // 2
         ang = self.pos * self.freqs[:half]
         a, b = h[:half], h[half:]
-        return np.concatenate([a * np.cos(ang) - b * np.sin(ang), a * np.sin(ang) + b * np.cos(ang)])
+        cs, sn = self.mscale * np.cos(ang), self.mscale * np.sin(ang)
+        return np.concatenate([a * cs - b * sn, a * sn + b * cs])
 
     def _attention(self, l: int, n: np.ndarray) -> np.ndarray:
         c, hd, w = self.c, self.c.head_dim, self.w

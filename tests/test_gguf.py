@@ -105,3 +105,63 @@ def test_config_rejects_other_layouts(tmp_path):
     G.write_model(path, "llama", c, t)
     with pytest.raises(ValueError, match="unsupported architecture llama"):
         G.config_from_gguf(G.Gguf(path))
+
+
+def _with_meta(tmp_path, name, arch, c, t, extra):
+    """A model file whose metadata adds `extra` (key -> (type, value)) to write_model's."""
+    base = str(tmp_path / ("base-" + name))
+    G.write_model(base, arch, c, t)
+    g = G.Gguf(base)
+    meta = {k: (G.STR if isinstance(v, str) else G.F32 if isinstance(v, float) else G.U32, v)
+            for k, v in g.metadata.items() if k != "general.alignment"}
+    meta.update(extra)
+    ts = [(n, tuple(ti.dims), int(ti.dtype), np.array(g.data(n))) for n, ti in g.tensors.items()]
+    path = str(tmp_path / name)  # a new file: the first stays mapped by its reader
+    G.write(path, meta, ts)
+    return G.Gguf(path)
+
+
+def test_config_reads_yarn_scaling(tmp_path):
+    """RopeScaling::from_gguf (rope.rs:14-30): type yarn with factor, original context and
+    attn_factor (default 1.0), the frequencies and magnitude of rope.rs:36-58; "none" and an
+    absent type give no scaling; any other type is an error."""
+    from oracle import skyla_oracle as so
+    c = synth.qwen3_config("tiny")
+    t = synth.qwen3("test-gguf-yarn", c, "q8_0", "ones")
+    key = "qwen3.rope.scaling."
+    g = _with_meta(tmp_path, "y.gguf", "qwen3", c, t, {key + "type": (G.STR, "yarn"), key + "factor": (G.F32, 4.0),
+                                                        key + "original_context_length": (G.U32, 32768)})
+    c2 = G.config_from_gguf(g)
+    assert c2.rope_scaling == (4.0, 32768.0, 1.0)
+    f, m = E.rope_table(c2)
+    of, om = so.rope_freqs_yarn(c2.head_dim, c2.rope_theta, 4.0, 32768.0, 1.0)
+    assert np.array_equal(f, of) and np.float32(m) == np.float32(om) and abs(m - (1 + 0.1 * np.log(4.0))) < 1e-6
+    g = _with_meta(tmp_path, "n.gguf", "qwen3", c, t, {key + "type": (G.STR, "none")})
+    assert G.config_from_gguf(g).rope_scaling is None and G.config_from_gguf(g).rope_mscale == 1.0
+    g = _with_meta(tmp_path, "l.gguf", "qwen3", c, t, {key + "type": (G.STR, "linear"), key + "factor": (G.F32, 2.0)})
+    with pytest.raises(ValueError, match="unsupported rope scaling linear"):
+        G.config_from_gguf(g)
+
+
+def test_config_round_trips_yarn(tmp_path):
+    """write_model stores a Config's YaRN scaling under the keys config_from_gguf reads."""
+    import dataclasses
+    c = dataclasses.replace(synth.qwen3_config("tiny"), rope_scaling=(8.0, 4096.0, 0.75))
+    t = synth.qwen3("test-gguf-yarn2", c, "q8_0", "ones")
+    path = str(tmp_path / "r.gguf")
+    G.write_model(path, "qwen3", c, t)
+    assert G.config_from_gguf(G.Gguf(path)).rope_scaling == (8.0, 4096.0, 0.75)
+
+
+def test_config_qwen3vl_text_and_nextn(tmp_path):
+    """Config::from_gguf (lib.rs:78-101) accepts the qwen3vl text model with the qwen3
+    layout, and drops the nextn_predict_layers multi-token-prediction blocks from n_layer;
+    recurrent (ssm) layouts are refused."""
+    c = synth.qwen3_config("tiny")
+    t = synth.qwen3("test-gguf-vl", c, "q4_k_m", "ones")
+    g = _with_meta(tmp_path, "vl.gguf", "qwen3vl", c, t, {"qwen3vl.nextn_predict_layers": (G.U32, 1)})
+    c2 = G.config_from_gguf(g)
+    assert (c2.n_layer, c2.n_embd, c2.n_head, c2.head_dim) == (c.n_layer - 1, c.n_embd, c.n_head, c.head_dim)
+    g = _with_meta(tmp_path, "ssm.gguf", "qwen3", c, t, {"qwen3.ssm.state_size": (G.U32, 128)})
+    with pytest.raises(ValueError, match="recurrent"):
+        G.config_from_gguf(g)

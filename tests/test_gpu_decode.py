@@ -370,6 +370,49 @@ def test_engine_from_gguf_file(ctx, tmp_path):
         e2.free()
 
 
+@pytest.mark.parametrize("fuse", ["none", "auto"])
+@pytest.mark.parametrize("arch,original_ctx", [("qwen3", 64.0), ("qwen3vl", 32768.0)])
+def test_yarn_model_from_gguf_against_oracle(ctx, tmp_path, arch, original_ctx, fuse):
+    """A qwen3 model with YaRN RoPE scaling (factor 4; over an original context of 64, so the
+    interpolated pairs turn visibly within the test, and 32768 as the R1-0528 Qwen3-8B
+    distill declares) written to a GGUF file (and as qwen3vl text), read back
+    (RopeScaling::from_gguf, rope.rs:14-58) and decoded through the engine: the host's
+    frequency table and magnitude go to the attention kernels.  24 greedy steps
+    teacher-forced against the oracle Model (its own C restatement of the table), then a
+    40-token prompt through Engine::prefill: no top-1 disagreement."""
+    import dataclasses
+    from skyla_hip import gguf as G
+    c = dataclasses.replace(synth.qwen3_config("tiny"), rope_scaling=(4.0, original_ctx, 1.0))
+    tensors = synth.qwen3(f"{CFG}-yarn", c, "q4_k_m", "random")
+    path = str(tmp_path / "yarn.gguf")
+    G.write_model(path, arch, c, tensors)
+    g = G.Gguf(path)
+    c2, t2 = G.config_from_gguf(g), G.tensors_from_gguf(g)
+    assert c2.rope_scaling == (4.0, original_ctx, 1.0) and abs(c2.rope_mscale - 1.1386294) < 1e-6
+    precision = P.F16_KEYS_Q8_VALUES
+    oracle = Model(c2, t2, (precision.keys_q8, precision.values_q8))
+    eng = E.Engine(ctx, t2, c2, 96, precision, fuse=fuse)
+    try:
+        top = Top1()
+        tok = synth.prompt(f"{CFG}-yarn", 1, c.n_vocab)[0]
+        for _ in range(24):
+            top.judge(eng.step(tok), oracle.forward(tok))
+            tok = top.last
+        top.report(f"yarn {arch} {original_ctx:g} {fuse}")
+        assert top.flips == 0, (top.flips, top.margin)
+        assert top.worst < 5e-3, top.worst
+        eng.reset()
+        oracle.reset()
+        prompt = synth.prompt(f"{CFG}-yarn-prefill", 40, c.n_vocab)
+        gl = eng.prefill(prompt)
+        for t_ in prompt:
+            ol = oracle.forward(t_)
+        assert int(np.argmax(gl)) == so.argmax(ol)
+        assert rel_l2(gl, ol) < 2e-2, rel_l2(gl, ol)
+    finally:
+        eng.free()
+
+
 @pytest.mark.parametrize("precision", list(P))
 @pytest.mark.parametrize("pos0", [0, 37, 64, 130])
 @pytest.mark.parametrize("heads", [(4, 2), (8, 1), (4, 4)])

@@ -183,3 +183,42 @@ def test_model_load_cache_per_layer():
         assert np.array_equal(per.k_cache[l][0], rows[l][0].reshape(-1))
         assert np.array_equal(same.k_cache[l][0], rows[0][0].reshape(-1))
     assert not np.array_equal(per.forward(1), same.forward(1))
+
+
+YARN = [(128, 1e6, 4.0, 32768.0, 1.0), (128, 1e6, 8.0, 4096.0, 0.7), (64, 1e4, 2.0, 2048.0, 1.0),
+        (128, 5e5, 16.0, 8192.0, 1.2)]
+
+
+@pytest.mark.parametrize("hd,theta,factor,ctx,attn", YARN)
+def test_rope_yarn_closed_form(hd, theta, factor, ctx, attn):
+    """The oracle's YaRN table (rope.rs:36-58 in f32) against the method in float64
+    (tests/model64.yarn64): pairs below the beta_fast dimension keep theta^(-2i/d), pairs
+    above the beta_slow one take 1/factor of it, the ramp between is linear, and the
+    magnitude is attn_factor (1 + 0.1 ln factor); within f32 rounding of each."""
+    from model64 import yarn64
+    f, m = so.rope_freqs_yarn(hd, theta, factor, ctx, attn)
+    f64, m64 = yarn64(hd, theta, factor, ctx, attn)
+    assert np.allclose(f, f64, rtol=2e-6, atol=0) and abs(m - m64) <= 2e-6 * m64
+    base = so.rope_freqs(hd, theta)
+    kept = np.isclose(f64, theta ** (-2.0 * np.arange(hd // 2) / hd), rtol=1e-12)
+    scaled = np.isclose(f64, theta ** (-2.0 * np.arange(hd // 2) / hd) / factor, rtol=1e-12)
+    assert kept.any() and scaled.any() and not (kept & scaled).any()
+    assert np.allclose(f[kept], base[kept], rtol=1e-7) and np.allclose(f[scaled], base[scaled] / factor, rtol=2e-7)
+
+
+def test_rope_yarn_factor_one_is_plain():
+    """YaRN with factor 1 leaves every frequency as theta^(-2i/d) and the magnitude at
+    attn_factor."""
+    f, m = so.rope_freqs_yarn(128, 1e6, 1.0, 32768.0, 1.0)
+    assert np.array_equal(f, so.rope_freqs(128, 1e6)) and m == 1.0
+
+
+@pytest.mark.parametrize("hd,theta,factor,ctx,attn", YARN)
+def test_rope_yarn_host_table_equals_oracle(hd, theta, factor, ctx, attn):
+    """The engine's host table (engine.rope_table, what the attention kernels read) and its
+    magnitude: the oracle's bits."""
+    c = E.Config(n_embd=hd, head_dim=hd, rope_theta=theta, rope_scaling=(factor, ctx, attn))
+    f, m = E.rope_table(c)
+    of, om = so.rope_freqs_yarn(hd, theta, factor, ctx, attn)
+    assert np.array_equal(f.view(np.uint32), of.view(np.uint32))
+    assert np.float32(m) == np.float32(om) and c.rope_mscale == m

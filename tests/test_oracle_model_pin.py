@@ -97,3 +97,44 @@ def test_pin_catches_wrong_expert_weights(monkeypatch):
     monkeypatch.setattr(oracle_model.so, "moe_forward", bad)
     errs, _ = _run(c, t, t, 3)
     assert min(errs) > 1e-3, errs
+
+
+def _yarn_setup(original_ctx=64.0):
+    """YaRN factor 4; an original context of 64 puts the ramp at pairs 0..11, so the
+    interpolated pairs turn visibly within the pin's few positions."""
+    c = dataclasses.replace(synth.qwen3_config("tiny"), n_layer=2, rope_scaling=(4.0, original_ctx, 1.0))
+    return c, synth.qwen3("pin-yarn", c, "q4_k_m", "random")
+
+
+@pytest.mark.parametrize("original_ctx", [64.0, 32768.0])
+def test_model_yarn_matches_float64_forward(original_ctx):
+    """Under YaRN scaling (factor 4; over an original context of 64, and of 32768 as the
+    reference's R1-0528 Qwen3-8B distill declares) the oracle Model's RoPE (the C
+    restatement of rope.rs:36-58) against the float64 forward built from the method."""
+    c, t = _yarn_setup(original_ctx)
+    errs, _ = _run(c, t, t)
+    assert max(errs) <= TOL, errs
+
+
+def test_pin_catches_yarn_scale_inverted(monkeypatch):
+    """The interpolated pairs' frequencies multiplied by the factor instead of divided by it
+    (freq_scale inverted) move the logits past three times the pin's tolerance."""
+    c, t = _yarn_setup()
+    real = oracle_model.so.rope_freqs_yarn
+
+    def inverted(head_dim, theta, factor, original_ctx, attn_factor):
+        f, m = real(head_dim, theta, factor, original_ctx, attn_factor)
+        base = oracle_model.so.rope_freqs(head_dim, theta)
+        return (base * base / f).astype(np.float32), m   # base * (1 / scale) for base * scale
+    monkeypatch.setattr(oracle_model.so, "rope_freqs_yarn", inverted)
+    errs, _ = _run(c, t, t)
+    assert max(errs) > 3 * TOL, errs
+
+
+def test_pin_catches_yarn_magnitude_dropped(monkeypatch):
+    """Dropping YaRN's magnitude (mscale = 1) moves the logits past three times the tolerance."""
+    c, t = _yarn_setup()
+    real = oracle_model.so.rope_freqs_yarn
+    monkeypatch.setattr(oracle_model.so, "rope_freqs_yarn", lambda *a: (real(*a)[0], 1.0))
+    errs, _ = _run(c, t, t)
+    assert max(errs) > 3 * TOL, errs
