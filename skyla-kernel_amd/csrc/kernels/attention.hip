@@ -555,55 +555,76 @@ ATTN_REP(1, 1)
 
 // attention_merge (attention_merge.comp): o = sum_s w_s acc_s / sum_s w_s l_s with
 // w_s = exp(m_s - max m) over the splits that hold positions.  Spec [head_dim, gated] =
-// [128, 0].  One workgroup of 1024 threads per (head, token): the weights go to LDS, then
-// thread t sums dims 2 (t % 64) + {0, 1} over the splits s = t / 64 (mod 16), every split's
-// load in flight at once, and the 16 groups are added in LDS.
+// [128, 0].  One workgroup of 1024 threads per (head, token).  Wave w takes the splits
+// s = w + 16 i; lane l holds dims 2 l and 2 l + 1.  Every load of a round of 1024 splits is
+// issued before any arithmetic: lane j loads (m, l) of the wave's split i = j, and each lane
+// its two dims of the wave's splits, MG at a time.  A wave keeps its own running maximum
+// M_w, and its sums over its splits weighted by exp(m_s - M_w); the waves then meet in LDS:
+// M = max M_w, and each wave's sums are scaled by exp(M_w - M) before they are added in
+// wave order.  That is the same quantity as the reference's single pass with M from the
+// start, in another rounding: exp(m_s - M_w) exp(M_w - M) for exp(m_s - M).  Over a single
+// split every factor is exp(0) = 1, so o = (acc + 0) / l, the bits attention_prep1 writes.
 constexpr uint32_t MAX_SPLITS = 4096;  // 262144 positions; the engine's arena stays below
+constexpr uint32_t MG = 24;            // a wave's splits whose loads are in flight together
 
 extern "C" __global__ __launch_bounds__(1024) void attention_merge__128_0(float *a, const uint32_t *ctl,
                                                                            MergePush p) {
-  __shared__ float wts[MAX_SPLITS];
-  __shared__ float red[16];
+  __shared__ float wmax[16], wl[16];
   __shared__ float2 sums[16][HD / 2];
-  const uint32_t h = blockIdx.x, tok = blockIdx.y, t = threadIdx.x, wave = t >> 6;
+  const uint32_t h = blockIdx.x, tok = blockIdx.y, t = threadIdx.x, wave = t >> 6, lane = t & 63;
   if (tok >= ctl[2]) return;
   const uint32_t used = min(min((ctl[1] + tok + p.chunk) / p.chunk, p.n_split), MAX_SPLITS);
   const uint32_t first = p.part_off + tok * p.part_stride + h * p.n_split * PART;
-  float big = -INFINITY;
-  for (uint32_t s = t; s < used; s += 1024) big = fmaxf(big, a[first + s * PART]);
-  big = wave_max(big);
-  if ((t & 63) == 0) red[wave] = big;
-  __syncthreads();
-  big = red[0];
+  float mw = -INFINITY, lw = 0.0f, ax = 0.0f, ay = 0.0f;
+  for (uint32_t base = 0; base < used; base += 1024) {
+    // this round's splits of the wave: s_i = base + wave + 16 i, i < n_i
+    const uint32_t s0 = base + wave;
+    const uint32_t n_i = s0 < used ? min(64u, (used - s0 + 15) / 16) : 0u;
+    if (n_i == 0) break;  // wave-uniform; no later round holds a split of this wave either
+    const uint32_t sj = s0 + 16 * lane;
+    const bool live = lane < n_i;
+    const float mj = live ? a[first + sj * PART] : -INFINITY;
+    const float lj = live ? a[first + sj * PART + 1] : 0.0f;
+    float2 v[MG];
 #pragma unroll
-  for (int w = 1; w < 16; w++) big = fmaxf(big, red[w]);
-  __syncthreads();  // red is reused
-  float total = 0.0f;
-  for (uint32_t s = t; s < used; s += 1024) {
-    const float wgt = expf(a[first + s * PART] - big);
-    wts[s] = wgt;
-    total = __builtin_fmaf(wgt, a[first + s * PART + 1], total);
-  }
-  total = wave_sum(total);
-  if ((t & 63) == 0) red[wave] = total;
-  __syncthreads();
-  total = 0.0f;
+    for (uint32_t i = 0; i < MG; i++)
+      v[i] = i < n_i ? *(const float2 *)(a + first + (s0 + 16 * i) * PART + 2 + 2 * lane) : make_float2(0.f, 0.f);
+    const float mn = fmaxf(mw, wave_max(mj));
+    const float r = expf(mw - mn);  // 0 in the first round (mw = -inf)
+    const float wj = expf(mj - mn);  // 0 for lanes past n_i
+    lw = __builtin_fmaf(lw, r, wave_sum(wj * lj));
+    ax *= r;
+    ay *= r;
 #pragma unroll
-  for (int w = 0; w < 16; w++) total += red[w];
-  const uint32_t dp = t & 63;
-  float2 acc = make_float2(0.0f, 0.0f);
-#pragma unroll 8
-  for (uint32_t s = wave; s < used; s += 16) {
-    const float2 v = *(const float2 *)(a + first + s * PART + 2 + 2 * dp);
-    acc.x = __builtin_fmaf(wts[s], v.x, acc.x);
-    acc.y = __builtin_fmaf(wts[s], v.y, acc.y);
+    for (uint32_t i = 0; i < MG; i++) {
+      const float wi = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wj), (int)i));
+      ax = __builtin_fmaf(wi, v[i].x, ax);
+      ay = __builtin_fmaf(wi, v[i].y, ay);
+    }
+    for (uint32_t i = MG; i < n_i; i++) {  // past MG splits of the wave in one round (long contexts)
+      const float wi = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wj), (int)i));
+      const float2 u = *(const float2 *)(a + first + (s0 + 16 * i) * PART + 2 + 2 * lane);
+      ax = __builtin_fmaf(wi, u.x, ax);
+      ay = __builtin_fmaf(wi, u.y, ay);
+    }
+    mw = mn;
   }
-  sums[wave][dp] = acc;
+  if (lane == 0) wmax[wave] = mw;
+  __syncthreads();
+  float big = wmax[0];
+#pragma unroll
+  for (int w = 1; w < 16; w++) big = fmaxf(big, wmax[w]);
+  const float f = expf(mw - big);  // 0 for a wave without splits (mw = -inf)
+  sums[wave][lane] = make_float2(ax * f, ay * f);
+  if (lane == 0) wl[wave] = lw * f;
   __syncthreads();
   if (t < HD) {
-    float o = 0.0f;
+    float o = 0.0f, total = 0.0f;
 #pragma unroll
-    for (int g = 0; g < 16; g++) o += ((const float *)sums[g])[t];
+    for (int g = 0; g < 16; g++) {
+      o += ((const float *)sums[g])[t];
+      total += wl[g];
+    }
     a[p.o_off + tok * p.o_stride + h * HD + t] = o / total;
   }
 }
