@@ -141,21 +141,42 @@ def time_replays(ctx: Context, rec, warmup: int, steps: int) -> tuple[float, lis
     return wall, dev
 
 
-def hbm_probe(ctx: Context, gib: float = 2.0) -> float:
-    """Stream-read bandwidth of the bandwidth kernel (bandwidth.comp) over `gib` GiB."""
+# (threads, loads in flight per lane, non-temporal) of the probe sweep; (256, 4, 0) is the
+# reference's bandwidth.comp form
+PROBE_FORMS = [(256, 4, 0), (512, 4, 0), (1024, 4, 0), (256, 8, 0), (256, 16, 0), (512, 8, 0),
+               (1024, 8, 0), (256, 4, 1), (256, 8, 1), (256, 16, 1), (512, 8, 1), (1024, 8, 1)]
+
+
+def hbm_probe(ctx: Context, gib: float = 2.0) -> tuple[float, dict]:
+    """Stream-read bandwidth of the bandwidth kernel (bandwidth.comp) over `gib` GiB: the
+    best over a sweep of workgroup sizes, loads in flight per lane, non-temporal loads and
+    grid sizes (workgroups per CU), with the form that reached it."""
     n_bytes = int(gib * (1 << 30)) // 16 * 16
     src = ctx.alloc_host(n_bytes)
-    dst = ctx.alloc_host(1 << 20)
-    p = ctx.create_pipeline("bandwidth", 2, 4, [256])
-    p.bind_buffers([src, dst])
+    dst = ctx.alloc_host(1 << 25)
     n_vec4 = n_bytes // 16
-    groups = 256 * 8 * 4
-    ns = ctx.time_dispatch(p, [groups, 1, 1], [n_vec4], 12)
-    p.free()
-    src.free()
-    dst.free()
-    best = min(ns[2:])
-    return n_bytes / best  # bytes per ns == GB/s
+    best, form = 0.0, {}
+    try:
+        for t, depth, nt in PROBE_FORMS:
+            spec = [t] if (depth, nt) == (4, 0) else [t, depth] + ([1] if nt else [])
+            p = ctx.create_pipeline("bandwidth", 2, 4, spec)
+            try:
+                p.bind_buffers([src, dst])
+                for per_cu in (1, 2, 4, 8, 16, 32):
+                    groups = 256 * per_cu
+                    if groups * t * 4 > dst.size:   # dst holds one word per thread
+                        continue
+                    ns = ctx.time_dispatch(p, [groups, 1, 1], [n_vec4], 8)
+                    gbs = n_bytes / min(ns[2:])  # bytes per ns == GB/s
+                    if gbs > best:
+                        best, form = gbs, {"threads": t, "depth": depth, "nontemporal": bool(nt),
+                                           "workgroups": groups}
+            finally:
+                p.free()
+    finally:
+        src.free()
+        dst.free()
+    return best, form
 
 
 def calibrate(ctx: Context, mib: int = 1024) -> dict:
@@ -609,8 +630,8 @@ def main() -> int:
 
     parity = parity_check(w)
     log(f"parity (q, layer 0) rel-L2 {parity:.2e}")
-    probe = hbm_probe(ctx)
-    log(f"HBM stream-read probe {probe:.0f} GB/s")
+    probe, probe_form = hbm_probe(ctx)
+    log(f"HBM stream-read probe {probe:.0f} GB/s ({probe_form})")
     prefill = None if args.no_prefill else prefill_gemm(ctx)
     if prefill:
         log(f"prefill GEMM M=512: {prefill}")
@@ -668,6 +689,7 @@ def main() -> int:
                      "avg_launch_us": round(q4k_ns / 1e3, 3), "launches_per_layer": n_launch / args.layers},
         "matvec_q6k": {"avg_launch_us": round(q6k_ns / 1e3, 3), "gbs": round(q6k_bytes / q6k_ns, 1)},
         "hbm_probe_gbs": round(probe, 1),
+        "hbm_probe_form": probe_form,
         "parity_rel_l2": parity,
         "prefill_gemm_m512": prefill,
         "moe_layer_config4": moe,

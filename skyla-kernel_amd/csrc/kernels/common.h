@@ -25,6 +25,20 @@ SK_DEV float f16_bits_to_f32(uint32_t bits16) {
   return (float)__builtin_bit_cast(f16, (uint16_t)bits16);
 }
 
+// Loads of weights that a step reads once: non-temporal, so the lines are not kept in the
+// caches at the expense of what is re-read (activations, headers shared by a workgroup).
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+SK_DEV uint4 load_nt(const uint4 *p) {
+  const u32x4_t t = __builtin_nontemporal_load((const u32x4_t *)p);
+  return make_uint4(t.x, t.y, t.z, t.w);
+}
+SK_DEV uint2 load_nt(const uint2 *p) {
+  const u32x2_t t = __builtin_nontemporal_load((const u32x2_t *)p);
+  return make_uint2(t.x, t.y);
+}
+SK_DEV uint16_t load_nt(const uint16_t *p) { return __builtin_nontemporal_load(p); }
+
 SK_DEV f16x2 as_f16x2(uint32_t u) { return __builtin_bit_cast(f16x2, u); }
 SK_DEV uint32_t as_u32(f16x2 h) { return __builtin_bit_cast(uint32_t, h); }
 
@@ -116,6 +130,10 @@ SK_DEV BufRes buf_res(const void *base, uint64_t bytes) {
 }
 SK_DEV uint4 buf_load(BufRes r, uint32_t voffset, uint32_t soffset) {
   return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voffset, soffset, 0));
+}
+// the same, non-temporal (cache policy bit 1, nt)
+SK_DEV uint4 buf_load_nt(BufRes r, uint32_t voffset, uint32_t soffset) {
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voffset, soffset, 2));
 }
 
 // ---------------------------------------------------------------------------------------

@@ -259,16 +259,16 @@ SK_DEV void matvec_q4k_body(const uint4 *__restrict__ w, const float *x, float *
       const uint32_t i = tid + j * G::NT, lr = i / G::CH_SUP, s = i % G::CH_SUP;
       if constexpr (PAIR) {  // rows [0, OUT) of the gate, then the same rows of up
         if (i < NH && s < ns)
-          hd[j] = w[(lr >= (uint32_t)OUT ? p.u1 : p.o1) + (base + min(row0 + lr % OUT, p.n_out - 1)) * supers + s0 + s];
+          hd[j] = load_nt(w + (lr >= (uint32_t)OUT ? p.u1 : p.o1) + (base + min(row0 + lr % OUT, p.n_out - 1)) * supers + s0 + s);
       } else {
-        if (i < NH && s < ns) hd[j] = buf_load(wh, ((base + min(row0 + lr, p.n_out - 1)) * supers + s) * 16, s0 * 16);
+        if (i < NH && s < ns) hd[j] = buf_load_nt(wh, ((base + min(row0 + lr, p.n_out - 1)) * supers + s) * 16, s0 * 16);
       }
     }
     uint4 q[PF][ROWS];
 #pragma unroll
     for (int j = 0; j < PF; j++)
 #pragma unroll
-      for (int r = 0; r < ROWS; r++) q[j][r] = buf_load(wq, voff[r], (u0 + j * LPR) * 16);
+      for (int r = 0; r < ROWS; r++) q[j][r] = buf_load_nt(wq, voff[r], (u0 + j * LPR) * 16);
 
     // stage: item t = quarter t%4 of unit t/4 (values 0-7, 8-15 of the low-nibble half,
     // then of the high half); the pair sums of quarters make the unit's two 16-value sums
@@ -346,7 +346,7 @@ SK_DEV void matvec_q4k_body(const uint4 *__restrict__ w, const float *x, float *
       for (int j = 0; j < PF; j++) {
         step(j0 + j, q[j]);
 #pragma unroll
-        for (int r = 0; r < ROWS; r++) q[j][r] = buf_load(wq, voff[r], (u0 + (j0 + j + PF) * LPR) * 16);
+        for (int r = 0; r < ROWS; r++) q[j][r] = buf_load_nt(wq, voff[r], (u0 + (j0 + j + PF) * LPR) * 16);
         __builtin_amdgcn_sched_barrier(0);  // each refill right behind the step it replaces
       }
     }
@@ -376,39 +376,42 @@ SK_DEV void matvec_q4k_body(const uint4 *__restrict__ w, const float *x, float *
 }
 
 // ---------------------------------------------------------------------------------------
-// Q4_K, K-split form for n_in = 4096 (the Qwen3-8B q, k, v, o, gate and up rows).  The
-// workgroup's eight waves split every row it owns by super-blocks: wave w takes units
-// 16w .. 16w+15 (super-blocks 2w, 2w+1), lane l the unit 16w + l%16 of the rows of its slot
-// l/16.  A lane's 32 activations are therefore the same for every row it touches: they are
-// loaded once, into registers, with their two 16-value sums, and no activation goes
-// through LDS.  A row-group is 4 slots x RPL rows; its weights (one 16 B unit per lane and
-// row) and headers (16 B per row and super-block) are loaded one group ahead of the
-// arithmetic.  Each wave decodes its own headers into the products d*sc_lo, d*sc_hi/16,
-// dmin*m_lo and dmin*m_hi (quant.rs:40-49, 60-61) in a region of LDS that only it touches,
-// so no workgroup barrier is needed there; a lane's unit sum is reduced over its 16 lanes
-// with DPP, and the eight waves' partial rows meet in LDS once, at the end, added in wave
-// order.
+// Q4_K, K-split form for n_in = 4096 KU (KU = 1: the Qwen3-8B q, k, v, o, gate and up rows;
+// KU = 3: the 12288-wide down rows).  The workgroup's eight waves split every row it owns
+// by super-blocks: wave w takes units 16w .. 16w+15 (super-blocks 2w, 2w+1) of each
+// 4096-value part k < KU of the row, lane l the unit 16w + l%16 of the rows of its slot
+// l/16.  A lane's 32 KU activations are therefore the same for every row it touches: they
+// are loaded once, into registers, with their two 16-value sums per part, and no
+// activation goes through LDS.  A row-group is 4 slots x RPL rows; its weights (KU 16 B
+// units per lane and row) and headers (16 B per row and super-block) are loaded one group
+// ahead of the arithmetic.  Each wave decodes its own headers into the products d*sc_lo,
+// d*sc_hi/16, dmin*m_lo and dmin*m_hi (quant.rs:40-49, 60-61) in a region of LDS that only
+// it touches, so no workgroup barrier is needed there; a lane's sum over its KU units is
+// reduced over its 16 lanes with DPP, and the eight waves' partial rows meet in LDS once,
+// at the end, added in wave order.
 // MODE 2 (RMSNorm folded in: x * w in the registers, the totals scaled by r) and MODE 3
 // (gate and up of the same outputs in one launch: slots 0, 1 take gate rows, 2, 3 the same
-// rows of up, and the store writes silu(gate) * up) as in the forms above.
+// rows of up, and the store writes silu(gate) * up) as in the forms above (KU = 1).
 // ---------------------------------------------------------------------------------------
-template <int ACCUM, int RPL, int NG, int MODE = 0, typename P = MatvecPush2>
+template <int ACCUM, int RPL, int NG, int MODE = 0, typename P = MatvecPush2, int KU = 1>
 SK_DEV void matvec_q4k_ks_body(const uint4 *__restrict__ w, const float *x, float *y, const P &p,
                                uint32_t bx) {
   constexpr bool PAIR = MODE == 3 || MODE == 4, NORM = MODE == 2 || MODE == 4;
   constexpr int RG = 4 * RPL;             // rows per row-group
   constexpr int OG = PAIR ? RG / 2 : RG;  // outputs per row-group
   constexpr int OUT = OG * NG;            // outputs per workgroup
-  constexpr int CPL = RG / 8;             // header chunks each lane decodes per row-group
+  constexpr int CPL = RG / 8;             // header chunks each lane decodes per row-group and part
+  constexpr uint32_t SUP = 16 * KU, UNITS = 128 * KU;  // super-blocks and 16 B units per row
   static_assert(RG % 8 == 0 && CPL >= 1 && CPL <= 4, "two headers per row, 64 lanes");
-  __shared__ float4 hp[8][RG][2][4];      // per wave: row, super-block, chunk
+  static_assert(KU == 1 || MODE == 0, "the fused forms are compiled for n_in 4096");
+  __shared__ float4 hp[8][RG][2 * KU][4];  // per wave: row, (part, super-block), chunk
   __shared__ float part[8][RG * NG];
   __shared__ float wss[NORM ? 8 : 1];
 
   const uint32_t tid = threadIdx.x, wv = tid >> 6, l = tid & 63;
   const uint32_t ul = l & 15, slot = l >> 4;
-  const uint32_t unit = wv * 16 + ul;  // of the row's 128
-  const uint32_t sbl = ul >> 3;        // the unit's super-block is 2 wv + sbl
+  const uint32_t unit = wv * 16 + ul;  // of each part's 128
+  const uint32_t sbl = ul >> 3;        // the unit's super-block is 2 wv + sbl (of its part)
   const uint32_t c = (unit >> 1) & 3;  // its chunk
   const uint32_t LO4 = opaque_mask(0x0f0f0f0fu), HI4 = opaque_mask(0xf0f0f0f0u);
   const uint32_t out0 = bx * OUT;
@@ -437,22 +440,30 @@ SK_DEV void matvec_q4k_ks_body(const uint4 *__restrict__ w, const float *x, floa
   regions(h_rl / RPL, hqo, hho);
   (void)hqo;
 
-  auto load_group = [&](uint32_t g, uint4 (&q)[RPL], uint4 &h) {
-    h = w[hho + (size_t)row_of(g, h_rl / RPL, h_rl % RPL) * 16 + 2 * wv + h_sb];
+  auto load_group = [&](uint32_t g, uint4 (&q)[RPL][KU], uint4 (&h)[KU]) {
+    const size_t hrow = (size_t)row_of(g, h_rl / RPL, h_rl % RPL) * SUP + 2 * wv + h_sb;
 #pragma unroll
-    for (int r = 0; r < RPL; r++) q[r] = w[qo + (size_t)row_of(g, slot, r) * 128 + unit];
+    for (int k = 0; k < KU; k++) h[k] = load_nt(w + hho + hrow + 16 * k);
+#pragma unroll
+    for (int r = 0; r < RPL; r++) {
+      const size_t qrow = (size_t)row_of(g, slot, r) * UNITS + unit;
+#pragma unroll
+      for (int k = 0; k < KU; k++) q[r][k] = load_nt(w + qo + qrow + 128 * k);
+    }
   };
 
   // activations first: they are what every row waits on
   const uint32_t at = (unit >> 3) * 256 + c * 64 + (unit & 1) * 16;
   const float *xv = x + p.x_off;
-  float4 xl[4], xh[4];
+  float4 xl[KU][4], xh[KU][4];
 #pragma unroll
-  for (int k = 0; k < 4; k++) {
-    xl[k] = *(const float4 *)(xv + at + 4 * k);
-    xh[k] = *(const float4 *)(xv + at + 32 + 4 * k);
-  }
-  uint4 qc[RPL], hc;
+  for (int k = 0; k < KU; k++)
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      xl[k][j] = *(const float4 *)(xv + at + 4096 * k + 4 * j);
+      xh[k][j] = *(const float4 *)(xv + at + 4096 * k + 32 + 4 * j);
+    }
+  uint4 qc[RPL][KU], hc[KU];
   load_group(0, qc, hc);
   // an accumulating launch reads its old outputs now, so the store at the end waits for none
   float yold = 0.0f;
@@ -462,52 +473,65 @@ SK_DEV void matvec_q4k_ks_body(const uint4 *__restrict__ w, const float *x, floa
     const float *wn = x + p.aux_off;
     float sq = 0.0f;
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
-      const float4 a = *(const float4 *)(wn + at + 4 * k), b = *(const float4 *)(wn + at + 32 + 4 * k);
-      xl[k] = fuse4<2>(xl[k], a, sq);
-      xh[k] = fuse4<2>(xh[k], b, sq);
+    for (int j = 0; j < 4; j++) {
+      const float4 a = *(const float4 *)(wn + at + 4 * j), b = *(const float4 *)(wn + at + 32 + 4 * j);
+      xl[0][j] = fuse4<2>(xl[0][j], a, sq);
+      xh[0][j] = fuse4<2>(xh[0][j], b, sq);
     }
     sq = lane_sum<16>(slot == 0 ? sq : 0.0f);  // each value once: slot 0's lanes
     if (l == 0) wss[wv] = sq;
   }
-  const float sl = (sum4(xl[0]) + sum4(xl[1])) + (sum4(xl[2]) + sum4(xl[3]));
-  const float sh = (sum4(xh[0]) + sum4(xh[1])) + (sum4(xh[2]) + sum4(xh[3]));
+  float sl[KU], sh[KU];
+#pragma unroll
+  for (int k = 0; k < KU; k++) {
+    sl[k] = (sum4(xl[k][0]) + sum4(xl[k][1])) + (sum4(xl[k][2]) + sum4(xl[k][3]));
+    sh[k] = (sum4(xh[k][0]) + sum4(xh[k][1])) + (sum4(xh[k][2]) + sum4(xh[k][3]));
+  }
 
 #pragma unroll
   for (int g = 0; g < NG; g++) {
-    uint4 qn[RPL], hn;
+    uint4 qn[RPL][KU], hn[KU];
     if (g + 1 < NG) load_group(g + 1, qn, hn);
     // decode this group's headers into the wave's products
-    {
-      const float d = f16_bits_to_f32(hc.x & 0xffffu), dmin = f16_bits_to_f32(hc.x >> 16);
+#pragma unroll
+    for (int k = 0; k < KU; k++) {
+      const uint4 hk = hc[k];
+      const float d = f16_bits_to_f32(hk.x & 0xffffu), dmin = f16_bits_to_f32(hk.x >> 16);
       const float d16 = d * 0.0625f;
-      const uint32_t sw[2] = {hc.y & 0x3f3f3f3fu, (hc.w & 0x0f0f0f0fu) | ((hc.y >> 2) & 0x30303030u)};
-      const uint32_t mw[2] = {hc.z & 0x3f3f3f3fu, ((hc.w >> 4) & 0x0f0f0f0fu) | ((hc.z >> 2) & 0x30303030u)};
+      const uint32_t sw[2] = {hk.y & 0x3f3f3f3fu, (hk.w & 0x0f0f0f0fu) | ((hk.y >> 2) & 0x30303030u)};
+      const uint32_t mw[2] = {hk.z & 0x3f3f3f3fu, ((hk.w >> 4) & 0x0f0f0f0fu) | ((hk.z >> 2) & 0x30303030u)};
 #pragma unroll
       for (int i = 0; i < CPL; i++) {
         const uint32_t cc = hc0 + i;
         const uint32_t sv = (cc < 2 ? sw[0] : sw[1]) >> (16 * (cc & 1));
         const uint32_t mv = (cc < 2 ? mw[0] : mw[1]) >> (16 * (cc & 1));
-        hp[wv][h_rl][h_sb][cc] = make_float4(d * (float)(sv & 255u), d16 * (float)((sv >> 8) & 255u),
-                                             dmin * (float)(mv & 255u), dmin * (float)((mv >> 8) & 255u));
+        hp[wv][h_rl][2 * k + h_sb][cc] = make_float4(d * (float)(sv & 255u), d16 * (float)((sv >> 8) & 255u),
+                                                     dmin * (float)(mv & 255u), dmin * (float)((mv >> 8) & 255u));
       }
     }
 #pragma unroll
     for (int r = 0; r < RPL; r++) {
-      const float sa = fma_bytes16(qc[r], LO4, xl, 0.0f);
-      const float sb = fma_bytes16(qc[r], HI4, xh, 0.0f);
-      const float4 f = hp[wv][slot * RPL + r][sbl][c];
-      float v = f.x * sa;
-      v = __builtin_fmaf(f.y, sb, v);
-      v = __builtin_fmaf(-f.z, sl, v);
-      v = __builtin_fmaf(-f.w, sh, v);
+      float v = 0.0f;
+#pragma unroll
+      for (int k = 0; k < KU; k++) {
+        const float sa = fma_bytes16(qc[r][k], LO4, xl[k], 0.0f);
+        const float sb = fma_bytes16(qc[r][k], HI4, xh[k], 0.0f);
+        const float4 f = hp[wv][slot * RPL + r][2 * k + sbl][c];
+        v = k == 0 ? f.x * sa : __builtin_fmaf(f.x, sa, v);
+        v = __builtin_fmaf(f.y, sb, v);
+        v = __builtin_fmaf(-f.z, sl[k], v);
+        v = __builtin_fmaf(-f.w, sh[k], v);
+      }
       v = lane_sum<16>(v);
       if (ul == 0) part[wv][g * RG + slot * RPL + r] = v;
     }
     if (g + 1 < NG) {
 #pragma unroll
-      for (int r = 0; r < RPL; r++) qc[r] = qn[r];
-      hc = hn;
+      for (int r = 0; r < RPL; r++)
+#pragma unroll
+        for (int k = 0; k < KU; k++) qc[r][k] = qn[r][k];
+#pragma unroll
+      for (int k = 0; k < KU; k++) hc[k] = hn[k];
     }
   }
   __syncthreads();
@@ -582,7 +606,7 @@ SK_DEV void matvec_q4k_dcomb_body(const uint4 *__restrict__ w, float *a, const u
     for (int st = 0; st < S; st++) {
       const uint32_t i = L + st * LPR;
       q[k][st] = make_uint4(0, 0, 0, 0);  // past n_in: multiplied by zero activations
-      if (live && i < units) q[k][st] = w[p.o0 + (size_t)(gbase + row) * units + i];
+      if (live && i < units) q[k][st] = load_nt(w + p.o0 + (size_t)(gbase + row) * units + i);
     }
   }
   // stage every slot's activations (items: slot, unit, quarter) and decode the headers
@@ -610,7 +634,7 @@ SK_DEV void matvec_q4k_dcomb_body(const uint4 *__restrict__ w, float *a, const u
       continue;
     }
     const uint32_t base = ids[p.ids_off + sl] * p.n_out;
-    const uint4 h = w[p.o1 + (size_t)(base + min(row0 + lr, p.n_out - 1)) * supers + sb];
+    const uint4 h = load_nt(w + p.o1 + (size_t)(base + min(row0 + lr, p.n_out - 1)) * supers + sb);
     const float d = f16_bits_to_f32(h.x & 0xffffu), dmin = f16_bits_to_f32(h.x >> 16);
     const float d16 = d * 0.0625f;
     const uint32_t sw[2] = {h.y & 0x3f3f3f3fu, (h.w & 0x0f0f0f0fu) | ((h.y >> 2) & 0x30303030u)};
@@ -723,9 +747,9 @@ SK_DEV void matvec_q6k_body(const uint4 *__restrict__ w, const uint16_t *__restr
 #pragma unroll
       for (int r = 0; r < ROWS; r++) {
         const uint32_t rs = rb[r] + s;
-        a[r] = w[p.o0 + rs * 8 + hf * 4 + li];
-        b[r] = w[p.o0 + rs * 8 + hf * 4 + 2 + li];
-        h[r] = w[p.o1 + rs * 4 + hf * 2 + li];
+        a[r] = load_nt(w + p.o0 + rs * 8 + hf * 4 + li);
+        b[r] = load_nt(w + p.o0 + rs * 8 + hf * 4 + 2 + li);
+        h[r] = load_nt(w + p.o1 + rs * 4 + hf * 2 + li);
       }
     };
     // activation item t = group t%4 of unit t/4: 16 values (4 x 16 B) and their sum
@@ -756,8 +780,8 @@ SK_DEV void matvec_q6k_body(const uint4 *__restrict__ w, const uint16_t *__restr
     auto h_load = [&](uint32_t i, uint4 &sv, uint32_t &dv) {
       const uint32_t lr = i / ns, s = i % ns;
       const uint32_t rs = (base + min(row0 + lr, p.n_out - 1)) * supers + s0 + s;
-      sv = w[p.o2 + rs];
-      dv = wd[p.o3 + rs];
+      sv = load_nt(w + p.o2 + rs);
+      dv = load_nt(wd + p.o3 + rs);
     };
     auto h_store = [&](uint32_t i, const uint4 sv, uint32_t dv) {
       const uint32_t lr = i / ns, s = i % ns;
@@ -879,11 +903,11 @@ SK_DEV void matvec_q6k_ks_body(const uint4 *__restrict__ w, const uint16_t *__re
 #pragma unroll
     for (int r = 0; r < RPL; r++) {
       const uint32_t rs = min(out0 + g * RPL + r, p.n_out - 1) * SUPERS + sb;
-      q[r].a = w[p.o0 + rs * 8 + hf * 4 + li];
-      q[r].b = w[p.o0 + rs * 8 + hf * 4 + 2 + li];
-      q[r].h = w[p.o1 + rs * 4 + hf * 2 + li];
-      q[r].sc = ((const uint2 *)(w + p.o2 + rs))[hf];
-      q[r].d = wd[p.o3 + rs];
+      q[r].a = load_nt(w + p.o0 + rs * 8 + hf * 4 + li);
+      q[r].b = load_nt(w + p.o0 + rs * 8 + hf * 4 + 2 + li);
+      q[r].h = load_nt(w + p.o1 + rs * 4 + hf * 2 + li);
+      q[r].sc = load_nt((const uint2 *)(w + p.o2 + rs) + hf);
+      q[r].d = load_nt(wd + p.o3 + rs);
     }
   };
 
@@ -1033,7 +1057,7 @@ SK_DEV void matvec_q8_0_body(const uint4 *__restrict__ w, const uint16_t *__rest
     auto d_load = [&](uint32_t i) -> uint32_t {
       const uint32_t lr = i / nb, bl = i % nb;
       const uint32_t row = base + min(row0 + lr, p.n_out - 1);
-      return wd[p.o1 + row * blocks + b0 + bl];
+      return load_nt(wd + p.o1 + row * blocks + b0 + bl);
     };
     if (k0 != 0) __syncthreads();
     float4 xv4[4];
@@ -1046,7 +1070,7 @@ SK_DEV void matvec_q8_0_body(const uint4 *__restrict__ w, const uint16_t *__rest
     for (int j = 0; j < PF; j++) {
       const uint32_t i = min(lane + j * LPR, nu - 1);
 #pragma unroll
-      for (int r = 0; r < ROWS; r++) q[j][r] = qr[r][u0 + i];
+      for (int r = 0; r < ROWS; r++) q[j][r] = load_nt(qr[r] + u0 + i);
     }
     if (tid < nu) x_store(tid, xv4);
     if (tid < n_items) dd[tid / nb][tid % nb] = f16_bits_to_f32(dv0);
@@ -1078,7 +1102,7 @@ SK_DEV void matvec_q8_0_body(const uint4 *__restrict__ w, const uint16_t *__rest
         }
         const uint32_t inext = min(i + PF * LPR, nu - 1);
 #pragma unroll
-        for (int r = 0; r < ROWS; r++) q[j][r] = qr[r][u0 + inext];
+        for (int r = 0; r < ROWS; r++) q[j][r] = load_nt(qr[r] + u0 + inext);
       }
     }
   }
@@ -1252,6 +1276,20 @@ MV_Q4K_KS_ALL(4, 3)
 MV_Q4K_KS_ALL(4, 6)
 MV_Q4K_KS_ALL(8, 1)
 MV_Q4K_KS_ALL(8, 3)
+// K-split Q4_K form for n_in = 12288 (KU = 3): the Qwen3-8B Q4_K down projection
+#define MV_Q4K_KS3(A, R, G)                                                                  \
+  extern "C" __global__ __launch_bounds__(512) void matvec_q4k_ks3__##A##_##R##_##G(          \
+      const uint4 *w, const float *x, float *y, const uint32_t *ids, Segments<MatvecPush2> m) { \
+    const uint32_t s = segment_of(m, blockIdx.x);                                            \
+    (void)ids;                                                                               \
+    matvec_q4k_ks_body<A, R, G, 0, MatvecPush2, 3>(w, x, y, segment_push(m, s), blockIdx.x - m.start[s]); \
+  }
+MV_Q4K_KS3(0, 2, 1)
+MV_Q4K_KS3(1, 2, 1)
+MV_Q4K_KS3(0, 2, 2)
+MV_Q4K_KS3(1, 2, 2)
+MV_Q4K_KS3(0, 4, 1)
+MV_Q4K_KS3(1, 4, 1)
 
 // K-split Q6_K form for n_in = 12288 (matvec_q6k_ks_body): RPL rows per row-group, NG
 // row-groups per workgroup of three waves, loaded D row-groups ahead

@@ -5,19 +5,34 @@ struct BandwidthPush { uint32_t n_vec4; };
 
 // bandwidth (bandwidth.comp:1-23): grid-stride XOR stream over n_vec4 uint4; writes only
 // if the fold hits a fixed constant, which keeps the loads live.  Roofline probe for the
-// HBM-bound kernels.  spec [threads per workgroup].
-template <int THREADS>
+// HBM-bound kernels.  spec [threads per workgroup] is the reference's form (four loads in
+// flight per lane); spec [threads, depth] keeps `depth` loads in flight, and a third word 1
+// issues them non-temporal, so the probe can sweep for the device's stream-read ceiling.
+// Each uint4 is folded by thread (index mod grid threads) whatever the depth.
+template <int THREADS, int DEPTH, bool NT>
 SK_DEV void bandwidth_body(const uint4 *src, uint32_t *dst, BandwidthPush p) {
   const uint32_t gid = blockIdx.x * THREADS + threadIdx.x;
   const uint32_t stride = gridDim.x * THREADS;
   uint4 acc = make_uint4(0, 0, 0, 0);
   uint32_t i = gid;
-  for (; i + 3 * stride < p.n_vec4; i += 4 * stride) {
-    const uint4 a = src[i], b = src[i + stride], c = src[i + 2 * stride], d = src[i + 3 * stride];
-    acc.x ^= a.x ^ b.x ^ c.x ^ d.x;
-    acc.y ^= a.y ^ b.y ^ c.y ^ d.y;
-    acc.z ^= a.z ^ b.z ^ c.z ^ d.z;
-    acc.w ^= a.w ^ b.w ^ c.w ^ d.w;
+  for (; i + (DEPTH - 1) * stride < p.n_vec4; i += DEPTH * stride) {
+    uint4 v[DEPTH];
+#pragma unroll
+    for (int d = 0; d < DEPTH; d++)
+      if constexpr (NT) {
+        typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+        const u32x4 t = __builtin_nontemporal_load((const u32x4 *)(src + i + d * stride));
+        v[d] = make_uint4(t.x, t.y, t.z, t.w);
+      } else {
+        v[d] = src[i + d * stride];
+      }
+#pragma unroll
+    for (int d = 0; d < DEPTH; d++) {
+      acc.x ^= v[d].x;
+      acc.y ^= v[d].y;
+      acc.z ^= v[d].z;
+      acc.w ^= v[d].w;
+    }
   }
   for (; i < p.n_vec4; i += stride) {
     const uint4 a = src[i];
@@ -30,17 +45,25 @@ SK_DEV void bandwidth_body(const uint4 *src, uint32_t *dst, BandwidthPush p) {
   if (r == 0x9e3779b9u) dst[gid] = r;
 }
 
-#define BW(T)                                                                               \
-  extern "C" __global__ __launch_bounds__(T) void bandwidth__##T(const uint4 *src,          \
-                                                                 uint32_t *dst,             \
-                                                                 BandwidthPush p) {         \
-    bandwidth_body<T>(src, dst, p);                                                         \
+#define BW(NAME, T, D, NT)                                                                  \
+  extern "C" __global__ __launch_bounds__(T) void NAME(const uint4 *src, uint32_t *dst,      \
+                                                       BandwidthPush p) {                   \
+    bandwidth_body<T, D, NT>(src, dst, p);                                                  \
   }
-BW(64)
-BW(128)
-BW(256)
-BW(512)
-BW(1024)
+BW(bandwidth__64, 64, 4, false)
+BW(bandwidth__128, 128, 4, false)
+BW(bandwidth__256, 256, 4, false)
+BW(bandwidth__512, 512, 4, false)
+BW(bandwidth__1024, 1024, 4, false)
+BW(bandwidth__256_8, 256, 8, false)
+BW(bandwidth__256_16, 256, 16, false)
+BW(bandwidth__512_8, 512, 8, false)
+BW(bandwidth__1024_8, 1024, 8, false)
+BW(bandwidth__256_4_1, 256, 4, true)
+BW(bandwidth__256_8_1, 256, 8, true)
+BW(bandwidth__256_16_1, 256, 16, true)
+BW(bandwidth__512_8_1, 512, 8, true)
+BW(bandwidth__1024_8_1, 1024, 8, true)
 
 // dequant: the bit-exact dequantisation the path's arithmetic is judged against
 // (quant.rs:5-89), run on the GPU over planner regions.  One thread per 32-value group,

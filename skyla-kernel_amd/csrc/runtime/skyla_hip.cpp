@@ -75,6 +75,7 @@ const Tactic kTactics[] = {
     {"variant", "", "W_R_L: every dense launch of a matvec kernel on that (waves, rows, lanes) variant"},
     {"ks", "1", "K-split matvec forms for n_in 4096 (Q4_K) and 12288 (Q6_K); 0: none; R_G: Q4_K shape"},
     {"ks6", "", "R_G_D: the Q6_K K-split form on that (rows, groups, groups ahead) shape"},
+    {"ks3", "1", "the Q4_K K-split form for n_in 12288 (0: LDS-staged form; R_G: that shape)"},
     {"ksnorm", "", "R_G: the Q4_K K-split form with the RMSNorm folded in on that shape"},
     {"ksglun", "1", "the norm-folded gate/up pair on its K-split form (0: LDS-staged form; R_G: shape)"},
     {"moe_fuse", "26", "bit mask of the MoE decode forms (2 gate/up pair, 8 down + combine, 16 route + pair)"},
@@ -149,7 +150,7 @@ const KernelInfo kKernels[] = {
     {"moe_combine", 1, 6, 0, 0, -1, false, false},
     {"silu_mul", 2, 4, 0, 0, -1, false, false},
     {"to_half", 3, 6, 0, 0, -1, false, false},
-    {"bandwidth", 2, 1, 1, 1, 0, false, false},
+    {"bandwidth", 2, 1, 1, 3, 0, false, false},  // [threads] or [threads, depth, nt]
     {"dequant", 3, 7, 1, 1, -1, false, false},
     // the decode step around the matvecs (kernels/attention.hip; kernels.rs:186-193)
     {"rmsnorm", 3, 6, 0, 0, -1, false, false},
@@ -873,6 +874,9 @@ const KsRule kKsNormRules[] = {{0, ~uint64_t{0}, 4, 2}};
 // (1, 16, 2) 12.83, (2, 4, 2) 13.89, (8, 1, 1) 14.02, (1, 8, 7) 14.19.  The ks6 tactic R_G_D
 // forces one shape (sweeps); ks=0 turns it off with the Q4_K forms.
 const std::vector<KsRule> kKs6Rules = {{0, ~uint64_t{0}, 1, 8, 1}};
+// K-split Q4_K form for n_in = 12288 (rows per slot, row-groups; matvec_q4k_ks3).  The ks3
+// tactic R_G forces one shape, 0 keeps the LDS-staged form.
+const KsRule kKs3Rules[] = {{0, ~uint64_t{0}, 2, 2}};
 
 void add_ks(skyla_hip_context *ctx, const char *name, const uint32_t *spec, Retile &t) {
   const std::string ksv = tactic("ks");
@@ -920,6 +924,19 @@ void add_ks(skyla_hip_context *ctx, const char *name, const uint32_t *spec, Reti
     hipFunction_t fn = find_function(ctx, ks + "_" + std::to_string(r.rpl) + "_" + std::to_string(r.ng));
     if (!fn) return;  // all or nothing
     alts.push_back({fn, (pair ? 2u : 4u) * r.rpl * r.ng, 512, r.min_rows, 4096, r.max_rows});
+  }
+  // plain Q4_K launches whose rows all have n_in = 12288 (the down projection): the same
+  // body with three 4096-value parts per row (matvec_q4k_ks3)
+  if (!pair && !norm) {
+    std::vector<KsRule> rules3(std::begin(kKs3Rules), std::end(kKs3Rules));
+    if (std::sscanf(tactic("ks3").c_str(), "%u_%u", &fr, &fg) == 2) rules3 = {{0, ~uint64_t{0}, fr, fg}};
+    for (const KsRule &r : rules3) {
+      if (tactic("ks3") == "0") break;
+      hipFunction_t fn = find_function(ctx, "matvec_q4k_ks3__" + std::to_string(spec[1]) + "_" +
+                                                std::to_string(r.rpl) + "_" + std::to_string(r.ng));
+      if (!fn) return;  // all or nothing
+      alts.push_back({fn, 4u * r.rpl * r.ng, 512, r.min_rows, 12288, r.max_rows});
+    }
   }
   t.alts.insert(t.alts.end(), alts.begin(), alts.end());
 }

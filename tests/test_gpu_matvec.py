@@ -377,6 +377,81 @@ def test_ks6_shapes_against_oracle(ctx, shape, accum):
         assert np.array_equal(got[i, n:], y0[i, n:])        # rows past n_out untouched
 
 
+KS3_SHAPES = ["2_1", "2_2", "4_1"]
+
+
+@pytest.mark.parametrize("shape", KS3_SHAPES)
+@pytest.mark.parametrize("accum", [False, True])
+def test_ks3_shapes_against_oracle(ctx, shape, accum):
+    """Every compiled shape of the K-split Q4_K form for n_in = 12288 (three 4096-value parts
+    per row; tactic ks3=R_G forces one) over three fused segments whose row counts are not
+    multiples of its workgroup (4096 + 333 + 1), ACCUM on and off, against the oracle at the
+    f32 bar; rows past n_out stay untouched."""
+    n_in, outs = 12288, [4096, 333, 1]
+    datas = [synth.matrix("test-ks3", f"{i}-{n}", E.DType.Q4K, n_in, n) for i, n in enumerate(outs)]
+    x = synth.activations("test-ks3", "x", n_in)
+    with tactics(ks3=shape):
+        s = Setup(ctx, [(E.DType.Q4K, n_in, n, d) for n, d in zip(outs, datas)], n_in, max(outs), rows=len(outs))
+    try:
+        y0 = synth.activations("test-ks3", "y0", (len(outs), s.s_out))
+        s.set_x(x)
+        s.set_y(y0)
+
+        def body(r):
+            g = E.Graph(r, s.k, None, None, False)
+            for i, m in enumerate(s.q):
+                g.matvec(m, (s.x_off, 0), (s.y_off + i * s.s_out, 0), accum, False)
+        rec = ctx.record(False, body)
+        try:
+            assert rec.launches() == 1           # the three dispatches run as one launch
+            ctx.replay(rec)
+        finally:
+            rec.free()
+        got = s.y(len(outs), s.s_out)
+    finally:
+        s.free()
+    for i, (n, d) in enumerate(zip(outs, datas)):
+        want = so.matvec(int(E.DType.Q4K), d, n_in, n, x)
+        part = got[i, :n].astype(np.float64) - (y0[i, :n] if accum else 0.0)
+        bar = f32_reorder_bar(E.DType.Q4K, d, n_in, n, x, want) + (4e-7 if accum else 0.0)
+        assert rel_l2(part, want) <= bar, (shape, i, rel_l2(part, want), bar)
+        assert np.array_equal(got[i, n:], y0[i, n:])        # rows past n_out untouched
+
+
+@pytest.mark.parametrize("ks3", ["2_2", "0"])
+def test_q4k_mixed_widths_in_one_launch(ctx, ks3):
+    """A fused launch whose segments have n_in 12288 and 4096 fits neither K-split form (each
+    needs every segment at its width): it runs the LDS-staged variant, within the bar; with
+    the ks3 tactic off, a 12288-wide launch alone does too."""
+    shapes = [(12288, 300), (4096, 77)]
+    datas = [synth.matrix("test-ks3", f"mixed-{n_in}", E.DType.Q4K, n_in, n) for n_in, n in shapes]
+    x = synth.activations("test-ks3", "x-mixed", 12288)
+    with tactics(ks3=ks3):
+        s = Setup(ctx, [(E.DType.Q4K, n_in, n, d) for (n_in, n), d in zip(shapes, datas)], 12288, 300,
+                  rows=len(shapes))
+    try:
+        s.set_x(x)
+        s.set_y(np.zeros((len(shapes), s.s_out), np.float32))
+
+        def body(r):
+            g = E.Graph(r, s.k, None, None, False)
+            for i, m in enumerate(s.q):
+                g.matvec(m, (s.x_off, 0), (s.y_off + i * s.s_out, 0), False, False)
+        rec = ctx.record(False, body)
+        try:
+            assert rec.launches() == 1
+            ctx.replay(rec)
+        finally:
+            rec.free()
+        got = s.y(len(shapes), s.s_out)
+    finally:
+        s.free()
+    for i, ((n_in, n), d) in enumerate(zip(shapes, datas)):
+        xi = x[:n_in]
+        want = so.matvec(int(E.DType.Q4K), d, n_in, n, xi)
+        assert rel_l2(got[i, :n], want) <= f32_reorder_bar(E.DType.Q4K, d, n_in, n, xi, want), (i, ks3)
+
+
 def test_ks6_other_widths_keep_their_variant(ctx):
     """The K-split Q6_K form serves n_in = 12288 only: a forced shape leaves a launch of
     another width (n_in 1024) on the LDS-staged variant, and the result stays in the bar."""

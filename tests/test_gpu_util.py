@@ -19,11 +19,13 @@ def _folds(src: np.ndarray, threads: int) -> np.ndarray:
     return acc[:, 0] ^ acc[:, 1] ^ acc[:, 2] ^ acc[:, 3]
 
 
-@pytest.mark.parametrize("n_vec4", [4096, 4096 + 1000, 37])
-def test_bandwidth_fold_against_numpy(ctx, n_vec4):
-    """Every uint4 is folded exactly once, by thread i % (grid x threads): the kernel writes
-    dst[g] only for the threads whose fold is 0x9e3779b9, and two threads are made so."""
-    wg, groups = 256, 4
+@pytest.mark.parametrize("spec", [[256], [256, 8], [256, 16, 1], [512, 8], [1024, 8, 1]])
+@pytest.mark.parametrize("n_vec4", [4096, 4096 + 1000, 37, 3 * 4096 + 4095])
+def test_bandwidth_fold_against_numpy(ctx, n_vec4, spec):
+    """Every uint4 is folded exactly once, by thread i % (grid x threads), whatever the loads
+    in flight per lane: the kernel writes dst[g] only for the threads whose fold is
+    0x9e3779b9, and two threads are made so."""
+    wg, groups = spec[0], 4
     threads = wg * groups
     g = np.random.default_rng(n_vec4)
     src = g.integers(0, 2**32, size=(n_vec4, 4), dtype=np.uint64).astype(np.uint32)
@@ -34,7 +36,7 @@ def test_bandwidth_fold_against_numpy(ctx, n_vec4):
     assert want.sum() >= 2
     a = ctx.alloc_host(src.nbytes)
     d = ctx.alloc_host(threads * 4)
-    p = ctx.create_pipeline("bandwidth", 2, 4, [wg])
+    p = ctx.create_pipeline("bandwidth", 2, 4, spec)
     try:
         a.host()[:] = src.reshape(-1).view(np.uint8)
         a.upload()
