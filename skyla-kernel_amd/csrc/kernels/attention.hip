@@ -186,10 +186,14 @@ SK_DEV float load_kv(const f16 *kv, const int8_t *kv8, uint32_t cache, uint32_t 
 }
 
 // One workgroup of four waves per (kv head, split of CHUNK positions, token); every load of
-// the split is issued up front.  Scores: thread t takes dims 8 (t % 16) ... of the key rows
-// of positions t / 16 + 16 k (k < 4), so 16 lanes read one row's whole cache lines, and
-// dots them with the N_REP query heads that share the kv head (held in LDS, scaled); the
-// 16 partial dots of a row meet in a DPP sum.  The chunk's softmax numerators
+// the split is issued up front.  Scores with f16 keys run on the matrix cores: wave w
+// computes the N_REP query heads (A, from LDS) against its 16 positions (B, one key row's
+// 32 dims per lane group and k-step) in four v_mfma_f32_16x16x32_f16 k-steps, once with
+// the heads' f16 high parts and once with their low parts (the heads scaled by a power of
+// two first, so hi + lo carries each value to 2^-22 of the head's largest and the products
+// with the f16 keys are exact in the f32 sums).  With 8-bit keys, thread t takes dims
+// 8 (t % 16) ... of the key rows of positions t / 16 + 16 k (k < 4) and dots them with the
+// heads in f32; the 16 partial dots of a row meet in a DPP sum.  The chunk's softmax numerators
 // e_p = exp(s_p - m) go through LDS to the value phase, where thread t weights 8 dims
 // (8 (t % 16) ...) of the value rows of positions 4 (t / 16) ... 4 (t / 16) + 3; the 16
 // position groups are then summed in LDS.  The partial (m, l = sum e_p, acc = sum e_p v_p)
@@ -215,7 +219,15 @@ SK_DEV void attention_body(const float *w, float *a, const uint32_t *ctl, f16 *k
   // (83 VGPRs allow five; with four heads, 32 KB, LDS allowed four, and a 16k-position
   // step's 2056 workgroups took a third round of eight)
   constexpr int HG = N_REP < 2 ? N_REP : 2;
-  __shared__ float qs[N_REP][HD];
+  // f16 keys: the scores on the matrix cores (MQ); 8-bit keys keep the VALU dots
+  constexpr bool MQ = !K8;
+  // the A operand's rows: head m % N_REP in row m (rows past the heads repeat them, and
+  // their products are not used); a row pitch of 320 B (80 banks) puts the 16 distinct
+  // 16 B pieces that a k-step's lanes read (four heads x four dim groups) on distinct banks
+  constexpr int QP = HD + 32;
+  __shared__ float qs[MQ ? 1 : N_REP][HD];
+  __shared__ __attribute__((aligned(16))) f16 qh[2][MQ ? N_REP : 1][MQ ? QP : 8];
+  __shared__ int qsh[MQ ? N_REP : 1];
   __shared__ __attribute__((aligned(16))) uint32_t nk[PREP ? 64 : 1], nv[PREP ? 64 : 1];
   __shared__ float nks[PREP ? 4 : 1], nvs[PREP ? 4 : 1];
   __shared__ float es[N_REP][CHUNK];
@@ -230,16 +242,20 @@ SK_DEV void attention_body(const float *w, float *a, const uint32_t *ctl, f16 *k
 
   // keys: dims [8 kd, 8 kd + 8) of positions kg + 16 k, k < 4 (16 lanes cover a row: every
   // load instruction reads whole cache lines)
+  // MQ: lane i of wave w takes position mp = 16 w + i % 16 and dims 8 (mg + 4 k), mg = i / 16:
+  // its B operand of k-step k (32 dims) of v_mfma_f32_16x16x32_f16
   const uint32_t kd = t & 15, kg = t >> 4;
+  const uint32_t lane = t & 63, mp = 16 * wave + (lane & 15), mg = lane >> 4;
   uint4 kr[4];
   float ksc[4];
 #pragma unroll
   for (int k = 0; k < 4; k++) {
-    const uint32_t kpos = begin + min(kg + 16 * k, cnt - 1);
-    if constexpr (!K8) {
-      kr[k] = *(const uint4 *)(kv + p.kc_off + kpos * kv_dim + kvh * HD + 8 * kd);
+    if constexpr (MQ) {
+      const uint32_t kpos = begin + min(mp, cnt - 1);
+      kr[k] = *(const uint4 *)(kv + p.kc_off + kpos * kv_dim + kvh * HD + 8 * (mg + 4 * k));
       ksc[k] = 1.0f;
     } else {
+      const uint32_t kpos = begin + min(kg + 16 * k, cnt - 1);
       const uint2 r = *(const uint2 *)(kv8 + p.kc_off + kpos * kv_dim + kvh * HD + 8 * kd);
       kr[k] = make_uint4(r.x, r.y, 0u, 0u);
       ksc[k] = (float)kv[p.ks_off + kpos * (kv_dim / 32) + kvh * 4 + (kd >> 2)];
@@ -261,17 +277,36 @@ SK_DEV void attention_body(const float *w, float *a, const uint32_t *ctl, f16 *k
       vsc[q] = (float)kv[p.vs_off + vpos * (kv_dim / 32) + kvh * 4 + (vg >> 2)];
     }
   }
+  // the scaled query head j (this lane's dims lane and lane + 64; the caller's wave holds
+  // the whole head).  MQ: as f16 hi + lo parts of v 2^sh, sh putting the head's largest
+  // |v| in [2^10, 2^11): hi + lo is v 2^sh to 2^-22 of that largest value, nothing
+  // overflows, and each product with an f16 key is exact in the f32 accumulation
+  auto put_q = [&](uint32_t j, float v0, float v1) {
+    if constexpr (MQ) {
+      const float big = wave_max(fmaxf(fabsf(v0), fabsf(v1)));
+      const int sh = big > 0.0f ? 11 - __builtin_amdgcn_frexp_expf(big) : 0;
+      const float s0 = ldexpf(v0, sh), s1 = ldexpf(v1, sh);
+      const f16 h0 = (f16)s0, h1 = (f16)s1;
+      qh[0][j][lane] = h0;
+      qh[0][j][lane + 64] = h1;
+      qh[1][j][lane] = (f16)(s0 - (float)h0);
+      qh[1][j][lane + 64] = (f16)(s1 - (float)h1);
+      if (lane == 0) qsh[j] = sh;
+    } else {
+      qs[j][lane] = v0;
+      qs[j][lane + 64] = v1;
+    }
+  };
   // the query heads of this kv head, scaled
   const uint32_t q_base = p.q_off + tok * p.q_stride + kvh * N_REP * HD;
   if constexpr (PREP) {
-    const uint32_t pos = ctl[1], lane = t & 63;
+    const uint32_t pos = ctl[1];
     const float *cs = pp->cs_off != NO_TABLE ? a + pp->cs_off : nullptr;
     for (uint32_t j = wave; j < (uint32_t)N_REP; j += 4) {
       float y0, y1;
       norm_rope(w, pp->qn_off, pp->rope_off, pp->eps, pp->mscale, pos, lane, a[q_base + j * HD + lane],
                 a[q_base + j * HD + lane + 64], y0, y1, cs);
-      qs[j][lane] = y0 * p.scale;
-      qs[j][lane + 64] = y1 * p.scale;
+      put_q(j, y0 * p.scale, y1 * p.scale);
     }
     if (pos / CHUNK == split) {
       if (wave == 0) {
@@ -285,6 +320,9 @@ SK_DEV void attention_body(const float *w, float *a, const uint32_t *ctl, f16 *k
         store_kv<V8>(kv, kv8, p.vc_off, p.vs_off, kv_dim, pos, kvh, lane, a[src + lane], a[src + lane + 64], nv, nvs);
       }
     }
+  } else if constexpr (MQ) {
+    for (uint32_t j = wave; j < (uint32_t)N_REP; j += 4)
+      put_q(j, a[q_base + j * HD + lane] * p.scale, a[q_base + j * HD + lane + 64] * p.scale);
   } else {
     for (uint32_t i = t; i < N_REP * HD; i += 256) qs[i / HD][i % HD] = a[q_base + i] * p.scale;
   }
@@ -292,17 +330,19 @@ SK_DEV void attention_body(const float *w, float *a, const uint32_t *ctl, f16 *k
   if constexpr (PREP) {
     if (ctl[1] / CHUNK == split) {  // the new row (pl = cnt - 1) and the masked slots clamped to it
       const uint32_t pl = cnt - 1;
+      if constexpr (MQ) {
+        if (mp >= pl)
 #pragma unroll
-      for (int k = 0; k < 4; k++)
-        if (kg + 16 * k >= pl) {
-          if constexpr (!K8) {
-            kr[k] = ((const uint4 *)nk)[kd];
-          } else {
+          for (int k = 0; k < 4; k++) kr[k] = ((const uint4 *)nk)[mg + 4 * k];
+      } else {
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+          if (kg + 16 * k >= pl) {
             const uint2 u = ((const uint2 *)nk)[kd];
             kr[k] = make_uint4(u.x, u.y, 0u, 0u);
             ksc[k] = nks[kd >> 2];
           }
-        }
+      }
 #pragma unroll
       for (int q = 0; q < 4; q++)
         if (4 * vq + q >= pl) {
@@ -317,73 +357,108 @@ SK_DEV void attention_body(const float *w, float *a, const uint32_t *ctl, f16 *k
     }
   }
 
-  float sc[4][N_REP];
-#pragma unroll
-  for (int k = 0; k < 4; k++) {
-    float key[8];
-    if constexpr (!K8) {
-      const uint32_t wd[4] = {kr[k].x, kr[k].y, kr[k].z, kr[k].w};
-#pragma unroll
-      for (int h = 0; h < 4; h++) {
-        const f16x2 v = as_f16x2(wd[h]);
-        key[2 * h] = (float)v.x;
-        key[2 * h + 1] = (float)v.y;
-      }
-    } else {
-      const uint32_t wd[2] = {kr[k].x, kr[k].y};
-#pragma unroll
-      for (int b = 0; b < 8; b++) key[b] = (float)(int8_t)((wd[b >> 2] >> (8 * (b & 3))) & 255u) * ksc[k];
-    }
-#pragma unroll
-    for (int j = 0; j < N_REP; j++) {
-      const float4 q0 = *(const float4 *)&qs[j][8 * kd], q1 = *(const float4 *)&qs[j][8 * kd + 4];
-      float s = 0.0f;
-      s = __builtin_fmaf(q0.x, key[0], s);
-      s = __builtin_fmaf(q0.y, key[1], s);
-      s = __builtin_fmaf(q0.z, key[2], s);
-      s = __builtin_fmaf(q0.w, key[3], s);
-      s = __builtin_fmaf(q1.x, key[4], s);
-      s = __builtin_fmaf(q1.y, key[5], s);
-      s = __builtin_fmaf(q1.z, key[6], s);
-      s = __builtin_fmaf(q1.w, key[7], s);
-      sc[k][j] = lane_sum<16>(s);  // the row's dot, in all 16 lanes
-    }
-  }
-  // The 16 lanes of a group hold the same 4 x N_REP scores, so the wave maximum needs only
-  // the two cross-group steps, and each lane then exponentiates its own share of them.
-#pragma unroll
-  for (int j = 0; j < N_REP; j++) {
-    float m = -INFINITY;
+  float mx[N_REP];
+  if constexpr (MQ) {
+    // scores on the matrix cores: A rows are the query heads (hi, then lo parts, each k-step
+    // 32 dims), B columns the wave's 16 positions; lane i then holds the scores of heads
+    // 4 (i / 16) + r (r < 4, those below N_REP) at position mp
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    const uint32_t m = lane & (N_REP - 1);  // A row lane % 16 holds head (lane % 16) % N_REP
 #pragma unroll
     for (int k = 0; k < 4; k++) {
-      if (kg + 16 * k >= cnt) sc[k][j] = -INFINITY;
-      m = fmaxf(m, sc[k][j]);
+      const f16x8 bk = __builtin_bit_cast(f16x8, kr[k]);
+#pragma unroll
+      for (int part = 0; part < 2; part++)
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(*(const f16x8 *)&qh[part][m][8 * (mg + 4 * k)], bk, acc, 0, 0, 0);
     }
-    m = fmaxf(m, __shfl_xor(m, 16, 64));
-    m = fmaxf(m, __shfl_xor(m, 32, 64));
-    if ((t & 63) == 0) wm[wave][j] = m;
-  }
-  __syncthreads();
-  float mx[N_REP];
+    // heads of this lane: 4 mg + r; with at most four heads, only mg = 0 holds any
+    constexpr int MGS = N_REP > 4 ? 2 : 1;
+    float sr[4];
 #pragma unroll
-  for (int j = 0; j < N_REP; j++) mx[j] = fmaxf(fmaxf(wm[0][j], wm[1][j]), fmaxf(wm[2][j], wm[3][j]));
-  constexpr int NS = 4 * N_REP;  // scores of a lane group: (position k, head j) = (i / N_REP, i % N_REP)
+    for (int r = 0; r < 4; r++) {
+      const uint32_t h = 4 * mg + r;
+      sr[r] = -INFINITY;
+      if (h < (uint32_t)N_REP && mp < cnt) sr[r] = ldexpf(acc[r], -qsh[h < (uint32_t)N_REP ? h : 0]);
+      // the head's maximum over the wave's 16 positions (one DPP row)
+      float v = sr[r];
+      v = fmaxf(v, dpp_f<0xb1>(v));
+      v = fmaxf(v, dpp_f<0x4e>(v));
+      v = fmaxf(v, dpp_f<0x141>(v));
+      v = fmaxf(v, dpp_f<0x140>(v));
+      if ((lane & 15) == 0 && h < (uint32_t)N_REP) wm[wave][h] = v;
+    }
+    __syncthreads();
 #pragma unroll
-  for (int i0 = 0; i0 < NS; i0 += 16) {
-    const int i = i0 + (int)kd;
-    if (i < NS) {
-      float s = -INFINITY, m = 0.0f;
+    for (int j = 0; j < N_REP; j++) mx[j] = fmaxf(fmaxf(wm[0][j], wm[1][j]), fmaxf(wm[2][j], wm[3][j]));
+    if (mg < (uint32_t)MGS) {
 #pragma unroll
-      for (int u = i0; u < (i0 + 16 < NS ? i0 + 16 : NS); u++)
-        if (u == i) {
-          s = sc[u / N_REP][u % N_REP];
-          m = mx[u % N_REP];
+      for (int r = 0; r < 4; r++) {
+        const int h = MGS == 1 ? r : (mg ? 4 + r : r);
+        if (h < N_REP) {
+          const float mh = MGS == 1 ? mx[r < N_REP ? r : 0] : (mg ? mx[(4 + r) % N_REP] : mx[r % N_REP]);
+          es[h][mp] = mp < cnt ? expf(sr[r] - mh) : 0.0f;
         }
-      const uint32_t pk = kg + 16 * (uint32_t)(i / N_REP);
-      es[i % N_REP][pk] = pk < cnt ? expf(s - m) : 0.0f;
+      }
     }
+    __syncthreads();
+  } else {
+    float sc[4][N_REP];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      float key[8];
+      const uint32_t wd[2] = {kr[k].x, kr[k].y};
+#pragma unroll
+      for (int bb = 0; bb < 8; bb++) key[bb] = (float)(int8_t)((wd[bb >> 2] >> (8 * (bb & 3))) & 255u) * ksc[k];
+#pragma unroll
+      for (int j = 0; j < N_REP; j++) {
+        const float4 q0 = *(const float4 *)&qs[j][8 * kd], q1 = *(const float4 *)&qs[j][8 * kd + 4];
+        float s = 0.0f;
+        s = __builtin_fmaf(q0.x, key[0], s);
+        s = __builtin_fmaf(q0.y, key[1], s);
+        s = __builtin_fmaf(q0.z, key[2], s);
+        s = __builtin_fmaf(q0.w, key[3], s);
+        s = __builtin_fmaf(q1.x, key[4], s);
+        s = __builtin_fmaf(q1.y, key[5], s);
+        s = __builtin_fmaf(q1.z, key[6], s);
+        s = __builtin_fmaf(q1.w, key[7], s);
+        sc[k][j] = lane_sum<16>(s);  // the row's dot, in all 16 lanes
+      }
+    }
+    // The 16 lanes of a group hold the same 4 x N_REP scores, so the wave maximum needs only
+    // the two cross-group steps, and each lane then exponentiates its own share of them.
+#pragma unroll
+    for (int j = 0; j < N_REP; j++) {
+      float m = -INFINITY;
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        if (kg + 16 * k >= cnt) sc[k][j] = -INFINITY;
+        m = fmaxf(m, sc[k][j]);
+      }
+      m = fmaxf(m, __shfl_xor(m, 16, 64));
+      m = fmaxf(m, __shfl_xor(m, 32, 64));
+      if ((t & 63) == 0) wm[wave][j] = m;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < N_REP; j++) mx[j] = fmaxf(fmaxf(wm[0][j], wm[1][j]), fmaxf(wm[2][j], wm[3][j]));
+    constexpr int NS = 4 * N_REP;  // scores of a lane group: (position k, head j) = (i / N_REP, i % N_REP)
+#pragma unroll
+    for (int i0 = 0; i0 < NS; i0 += 16) {
+      const int i = i0 + (int)kd;
+      if (i < NS) {
+        float s = -INFINITY, m = 0.0f;
+#pragma unroll
+        for (int u = i0; u < (i0 + 16 < NS ? i0 + 16 : NS); u++)
+          if (u == i) {
+            s = sc[u / N_REP][u % N_REP];
+            m = mx[u % N_REP];
+          }
+        const uint32_t pk = kg + 16 * (uint32_t)(i / N_REP);
+        es[i % N_REP][pk] = pk < cnt ? expf(s - m) : 0.0f;
+      }
+    }
+    __syncthreads();
   }
-  __syncthreads();
   // l = sum of the split's e per head: wave 0 adds the LDS rows while the others go on
   float lrow[N_REP];
   if (wave == 0) {
@@ -410,7 +485,7 @@ SK_DEV void attention_body(const float *w, float *a, const uint32_t *ctl, f16 *k
     } else {
       const uint32_t wd[2] = {vr[q].x, vr[q].y};
 #pragma unroll
-      for (int b = 0; b < 8; b++) v[q][b] = (float)(int8_t)((wd[b >> 2] >> (8 * (b & 3))) & 255u) * vsc[q];
+      for (int bb = 0; bb < 8; bb++) v[q][bb] = (float)(int8_t)((wd[bb >> 2] >> (8 * (bb & 3))) & 255u) * vsc[q];
     }
   }
   const uint32_t part_base = p.part_off + tok * p.part_stride;
