@@ -854,8 +854,13 @@ struct KsRule {
   uint32_t pd = 1;              // Q6_K: row-groups loaded ahead
 };
 // (the launches of at most 8191 rows, q+k+v and o, on their own shape: config-2 step
-// (4, 1) 3387-3397 GB/s, (2, 2) 3336, (2, 1) 3331-3340, (8, 1) 3247 on one box)
-const KsRule kKsRules[] = {{0, ~uint64_t{0}, 4, 1}};
+// (4, 1) 3387-3397 GB/s, (2, 2) 3336, (2, 1) 3331-3340, (8, 1) 3247 on one box.)  Launches
+// of 16384 rows or more (the fused gate+up, 24576 rows) take (4, 6), 1024 workgroups
+// instead of 1536: config-2 step 3540-3547 against 3503-3510 GB/s, matvec_q4k 7.58-7.65
+// against 7.71-7.77 us per launch (four runs each, one box); (8, 1) 3518-3538, (4, 3)
+// 3469-3482, (4, 2), (8, 3), (2, 2), (2, 1) slower.  A row's sum does not depend on the
+// shape, so every shape gives the same bits.
+const KsRule kKsRules[] = {{0, 16383, 4, 1}, {16384, ~uint64_t{0}, 4, 6}};
 const KsRule kKsPairRules[] = {{0, 8191, 4, 1}};
 // the gate/up pair with the FFN norm folded in (MODE 4 of the K-split body).  Its 102 VGPRs
 // (the norm weights held beside x) leave two 8-wave workgroups per CU, so the shape is the

@@ -336,6 +336,37 @@ def test_ks_shapes_against_oracle(ctx, shape, accum):
         assert np.array_equal(got[i, n:], y0[i, n:])        # rows past n_out untouched
 
 
+def test_ks_shapes_same_bits(ctx):
+    """A row's K-split sum does not depend on the shape that computes it: every compiled
+    (rows per slot, row-groups) shape, and the default size rule (a fused gate+up launch of
+    2 x 12288 rows on its own shape), give the same bits."""
+    n_in, outs = 4096, [12288, 12288]
+    datas = [synth.matrix("test-ks-bits", f"{i}", E.DType.Q4K, n_in, n) for i, n in enumerate(outs)]
+    x = synth.activations("test-ks-bits", "x", n_in)
+    got = {}
+    for shape in [None] + KS_SHAPES:
+        with tactics(ks=shape):
+            s = Setup(ctx, [(E.DType.Q4K, n_in, n, d) for n, d in zip(outs, datas)], n_in, max(outs), rows=2)
+        try:
+            s.set_x(x)
+
+            def body(r):
+                g = E.Graph(r, s.k, None, None, False)
+                for i, m in enumerate(s.q):
+                    g.matvec(m, (s.x_off, 0), (s.y_off + i * s.s_out, 0), False, False)
+            rec = ctx.record(False, body)
+            try:
+                assert rec.launches() == 1
+                ctx.replay(rec)
+            finally:
+                rec.free()
+            got[shape] = s.y(2, s.s_out)[:, :12288].copy()
+        finally:
+            s.free()
+    for shape, y in got.items():
+        assert np.array_equal(y.view(np.uint32), got[None].view(np.uint32)), shape
+
+
 KS6_SHAPES = ["1_8_1", "1_8_2", "1_8_7", "1_16_2", "2_4_2", "8_1_1"]
 
 
