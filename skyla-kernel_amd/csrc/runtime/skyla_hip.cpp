@@ -867,8 +867,11 @@ const KsRule kKsPairRules[] = {{0, 8191, 4, 1}};
 // one whose workgroups all fit at once: config 5 at 1k context, device ms per token on one
 // box, (4, 3) 1.854 and (4, 6) 1.855 against 1.877-1.882 for the LDS-staged pair form;
 // (4, 2) 1.883, (8, 1) 1.894, (8, 3) 1.917, and (4, 1) 2.049 and (2, 2) 2.046 (three rounds
-// of workgroups).  The ksglun tactic 0 keeps the LDS-staged pair, R_G forces a shape.
-const KsRule kKsGlunRules[] = {{0, ~uint64_t{0}, 4, 3}};
+// of workgroups).  With the weights loaded non-temporal, (4, 6) 1.781-1.783 against (4, 3)
+// 1.792-1.793 at 1k and 2.266-2.267 against 2.274-2.279 at 16k (two runs each, one box;
+// (4, 2) 1.836, (8, 1) 1.855).  The ksglun tactic 0 keeps the LDS-staged pair, R_G forces a
+// shape.
+const KsRule kKsGlunRules[] = {{0, ~uint64_t{0}, 4, 6}};
 // q/k/v with the attention norm folded in (MODE 2, the same 102 VGPRs): config 5 at 1k
 // context, device ms per token on one box, (4, 2) 1.809 against 1.833-1.838 for (4, 1);
 // (8, 1) 1.826, (2, 2) 1.850, (4, 3) 1.849, (2, 1) 1.900.  The ksnorm tactic R_G forces a shape.

@@ -214,7 +214,7 @@ def test_fused_matvec_forms(ctx, dtype, n_in, n_out, form, retile):
     assert err <= F32, err
 
 
-@pytest.mark.parametrize("ks", ["1", "4_1", "0"])
+@pytest.mark.parametrize("ks", ["1", "4_1", "4_3", "0"])
 @pytest.mark.parametrize("big", [False, True])
 @pytest.mark.parametrize("n_in,n_out", [(4096, 12288), (4096, 1000), (1024, 1536), (2048, 100)])
 def test_glu_norm_pair_against_oracle(ctx, n_in, n_out, big, ks):
