@@ -215,8 +215,8 @@ SK_DEV float load_kv(const f16 *kv, const int8_t *kv8, uint32_t cache, uint32_t 
 template <int N_REP, int K8, int V8, bool PREP = false, bool DIRECT = false>
 SK_DEV void attention_body(const float *w, float *a, const uint32_t *ctl, f16 *kv, int8_t *kv8, const AttnPush &p,
                            const PrepPush *pp, uint32_t o_off = 0, uint32_t o_stride = 0) {
-  // heads per value reduction round: two keep vp at 16 KB, so five workgroups share a CU
-  // (83 VGPRs allow five; with four heads, 32 KB, LDS allowed four, and a 16k-position
+  // heads per value reduction round: two keep vp at 16 KB and the workgroup near 20 KB of
+  // LDS, so six share a CU (with four heads, 32 KB, LDS allowed four, and a 16k-position
   // step's 2056 workgroups took a third round of eight)
   constexpr int HG = N_REP < 2 ? N_REP : 2;
   // f16 keys: the scores on the matrix cores (MQ); 8-bit keys keep the VALU dots
@@ -602,8 +602,9 @@ QKV(0, 1)
 QKV(1, 1)
 
 // attention (attention.comp): spec [N_REP, CHUNK, K_Q8, V_Q8, head_dim, q_head].
-// Six waves per SIMD for the forms of at most four query heads per kv head (80 VGPRs, no
-// spill; with 16 KB of LDS, six workgroups per CU); eight heads keep their registers.
+// Six waves per SIMD for the forms of at most four query heads per kv head (at most 80
+// VGPRs, no spill; about 20 KB of LDS, six workgroups per CU); eight heads keep their
+// registers.
 #define ATTN(R, K8, V8)                                                                          \
   extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(R == 8 ? 1 : 6))) void attention__##R##_64_##K8##_##V8##_128_128(   \
       float *a, const uint32_t *ctl, const f16 *kv, const int8_t *kv8, const f16 *kvs, AttnPush p) { \
