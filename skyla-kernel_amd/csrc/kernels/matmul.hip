@@ -499,9 +499,11 @@ struct XChunk {
   uint4 h[XHALF ? IPT : 1];
 };
 
-template <int KX, int XHALF, int NT, int TN>
+// LIVE (expert groups): token rows past `live` (the group's last tile pads its 32 columns
+// with copies of its last row) are zeroed instead of loaded; their columns are not stored.
+template <int KX, int XHALF, int NT, int TN, bool LIVE = false>
 SK_DEV void load_chunk(XChunk<KX, XHALF, NT, TN> &c, const void *xv, const uint32_t *xrow, uint32_t x_off,
-                       uint32_t x_stride, uint32_t k0, uint32_t n_in) {
+                       uint32_t x_stride, uint32_t k0, uint32_t n_in, uint32_t live = 0) {
   using C = XChunk<KX, XHALF, NT, TN>;
   constexpr int IPT = C::IPT, IPR = C::IPR, PER = C::PER;
 #pragma unroll
@@ -514,8 +516,10 @@ SK_DEV void load_chunk(XChunk<KX, XHALF, NT, TN> &c, const void *xv, const uint3
     const size_t base = (size_t)x_off + (size_t)xrow[J / IPR] * x_stride + (kb < n_in ? kb : n_in - PER);
     if constexpr (XHALF)
       c.h[i] = *(const uint4 *)((const f16 *)xv + base);
-    else
+    else if (!LIVE || J / IPR < live)
       c.v[i] = *(const float4 *)((const float *)xv + base);
+    else
+      c.v[i] = make_float4(0.f, 0.f, 0.f, 0.f);
   }
 }
 
@@ -1081,7 +1085,7 @@ SK_DEV void matmul_tile128_w(const uint4 *__restrict__ w, const uint16_t *__rest
   __syncthreads();  // xrow
   {
     XChunk<KX, XHALF, NT, TN> c0;
-    load_chunk<KX, XHALF, NT, TN>(c0, x, xrow, p.x_off, p.x_stride, kbase, p.n_in);
+    load_chunk<KX, XHALF, NT, TN, MOE != 0>(c0, x, xrow, p.x_off, p.x_stride, kbase, p.n_in, n_tok);
     wr.store(wr, wl, tid);
     const bool r = store_chunk<KX, XHALF, NT, TN>(xs, c0, xexp, kbase, p.n_in);
     if (lane == 0) xflag[wave] = r;
@@ -1101,7 +1105,9 @@ SK_DEV void matmul_tile128_w(const uint4 *__restrict__ w, const uint16_t *__rest
     for (int c4 = 0; c4 < KC / KX; c4++) {
       XChunk<KX, XHALF, NT, TN> xn;
       const bool next = chunk + 1 < n_chunk;
-      if (next) load_chunk<KX, XHALF, NT, TN>(xn, x, xrow, p.x_off, p.x_stride, kbase + (chunk + 1) * KX, p.n_in);
+      if (next)
+        load_chunk<KX, XHALF, NT, TN, MOE != 0>(xn, x, xrow, p.x_off, p.x_stride, kbase + (chunk + 1) * KX, p.n_in,
+                                                n_tok);
       bool rescaled = false;
 #pragma unroll
       for (int q = 0; q < NW; q++) rescaled |= xflag[q] != 0;
