@@ -514,9 +514,12 @@ SK_DEV void load_chunk(XChunk<KX, XHALF, NT, TN> &c, const void *xv, const uint3
     // when the chunk is stored (a select here would make the loads wait at once, and a
     // predicated load is split into per-dword branches)
     const size_t base = (size_t)x_off + (size_t)xrow[J / IPR] * x_stride + (kb < n_in ? kb : n_in - PER);
-    if constexpr (XHALF)
-      c.h[i] = *(const uint4 *)((const f16 *)xv + base);
-    else if (!LIVE || J / IPR < live)
+    if constexpr (XHALF) {
+      if (!LIVE || J / IPR < live)
+        c.h[i] = *(const uint4 *)((const f16 *)xv + base);
+      else
+        c.h[i] = make_uint4(0u, 0u, 0u, 0u);
+    } else if (!LIVE || J / IPR < live)
       c.v[i] = *(const float4 *)((const float *)xv + base);
     else
       c.v[i] = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -1226,8 +1229,9 @@ SK_DEV void matmul_tile128_w(const uint4 *__restrict__ w, const uint16_t *__rest
         if (tok < n_tok) {
           float *o = y + p.y_off + (size_t)yrow[tok] * p.y_stride + my_row;
           float v = acc[j][i];
-          // XHALF = 2, 3: the rows came from x_half_rows as x * 2^-e; scale back (exact)
-          if constexpr (XHALF >= 2) v = __builtin_ldexpf(v, ((const int *)x)[yrow[tok]]);
+          // XHALF = 2, 3: the rows came from x_half_rows as x * 2^-e; scale back (exact) by
+          // the exponent of the token's input row (its output row for dense launches)
+          if constexpr (XHALF >= 2) v = __builtin_ldexpf(v, ((const int *)x)[xrow[tok]]);
           *o = ACCUM ? *o + v : v;
         }
       }
@@ -1449,6 +1453,18 @@ MMH(1, 1)
 MMH(2, 0)
 MMH(2, 1)
 
+// Expert groups (MOE = 1, 128 x 32 tiles, four waves) on the f16 rows x_half_rows wrote:
+// the rows of the launch's inputs (tokens for gate and up, slots for down), no K split.
+#define MMXM(T, A)                                                                                \
+  extern "C" __global__ __launch_bounds__(256) void matmul_xm__##T##_##A(                          \
+      const uint4 *w, const uint16_t *wd, const f16 *x, float *y, const uint32_t *ctl, MatmulPush p) { \
+    matmul_tile128_w<T, A, 2, 4, 32, 1>(w, wd, x, y, ctl, p);                                     \
+  }
+MMXM(1, 0)
+MMXM(1, 1)
+MMXM(2, 0)
+MMXM(2, 1)
+
 // The four-wave tile on the same f16 rows (128 tokens per wave, 128-k chunks).
 #define MMH4(T, A)                                                                                \
   extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void       \
@@ -1539,11 +1555,12 @@ MMHS(2, 1)
 // n_in per row, 16-byte aligned].
 struct XHalfPush {
   uint32_t x_off, x_stride, n_in, h_off;
+  uint32_t rows_per_token;  // input rows per token of ctl[2]: 1, or the slots of an expert down
 };
 extern "C" __global__ __launch_bounds__(256) void x_half_rows(const float *x, uint32_t *out, const uint32_t *ctl,
                                                               XHalfPush p) {
   const uint32_t t = blockIdx.x, tid = threadIdx.x;
-  if (t >= ctl[2]) return;
+  if (t >= ctl[2] * p.rows_per_token) return;
   const float *xr = x + p.x_off + (size_t)t * p.x_stride;
   constexpr int MAXV = 48;  // values per thread: n_in <= 12288
   float4 v[MAXV / 4];

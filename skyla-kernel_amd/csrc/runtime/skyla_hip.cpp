@@ -83,6 +83,7 @@ const Tactic kTactics[] = {
     {"split_slots", "256", "workgroup slots a matmul K split fills (64..2048)"},
     {"xhalf", "1", "f16 row prepass for matmuls on f32 rows: 1 four-wave tile where it fits, 4 without "
                    "the balanced K halves, 8 eight-wave tile throughout, 0 the tile's own f32 staging"},
+    {"xhalf_moe", "1", "expert-group matmuls on f32 rows take the f16 row prepass (0: the tile's own f32 staging)"},
     {"dl", "1", "matmul tiles with their operands loaded straight into LDS (0: register-staged)"},
     {"merge_t", "1", "batched attention merge as one wave per (head, token) (0: 1024-thread form)"},
     {"nograph", "0", "1: recordings replay as direct launches instead of one HIP graph (kernel traces)"},
@@ -243,6 +244,7 @@ struct skyla_hip_pipeline {
   hipFunction_t hx4_fn = nullptr;        // the four-wave tile on those rows
   hipFunction_t hx4b_fn = nullptr;       // and over a balanced grid (some tiles in K halves)
   hipFunction_t hxs_fn = nullptr;        // the eight-wave tile over several matrices (segments)
+  hipFunction_t hxm_fn = nullptr;        // expert groups (MOE = 1) on x_half_rows's f16 rows
   uint32_t split_threads = 0;
   hipFunction_t tok_fn = nullptr;        // batched form: a tok_per_wg x tok_per_wg_y block of
   uint32_t tok_per_wg = 0;               // grid.x and grid.y per workgroup
@@ -265,7 +267,7 @@ struct Command {
   std::shared_ptr<const Retile> retile;
   hipFunction_t split_fn = nullptr;
   uint32_t split_threads = 0;
-  hipFunction_t hx_fn = nullptr, hx4_fn = nullptr, hx4b_fn = nullptr, hxs_fn = nullptr;
+  hipFunction_t hx_fn = nullptr, hx4_fn = nullptr, hx4b_fn = nullptr, hxs_fn = nullptr, hxm_fn = nullptr;
   hipFunction_t tok_fn = nullptr;
   uint32_t tok_per_wg = 0, tok_per_wg_y = 0, tok_threads = 0;
   std::string name;                 // the pipeline's shader name
@@ -523,14 +525,17 @@ std::vector<Command> fuse_moe(const std::vector<Command> &cmds) {
 // every such matmul that reads the same rows before the next barrier (dispatches between
 // barriers are independent: none of them writes those rows).  Buffer pointers are filled
 // in by bind_workspace.  MatmulPush words: x_off 4, n_in 6, x_stride 8.
-Launch x_half_prepass(skyla_hip_context *ctx, const Command &a, uint64_t h_bytes_off) {
+// rows: the most input rows the launch can read (groups[0] of the prepass, rows past
+// ctl[2] x rows_per_token skip); the exponents come first, h_bytes_off bytes, then the rows.
+Launch x_half_prepass(skyla_hip_context *ctx, const Command &a, uint64_t h_bytes_off, uint32_t rows,
+                      uint32_t rows_per_token = 1) {
   Launch l;
   l.fn = ctx->x_half_rows;
   l.threads = 256;
-  l.groups[0] = a.groups[2] * 128;  // every row of the launch's token tiles (rows >= ctl[2] skip)
+  l.groups[0] = rows;
   l.groups[1] = l.groups[2] = 1;
   l.bufs = {a.bufs[2], nullptr, a.bufs[4]};
-  l.args = {a.push[4], a.push[8], a.push[6], (uint32_t)(h_bytes_off / 4)};
+  l.args = {a.push[4], a.push[8], a.push[6], (uint32_t)(h_bytes_off / 4), rows_per_token};
   l.xh_buf = 1;
   l.xh_bytes = h_bytes_off + (uint64_t)l.groups[0] * a.push[6] * 2;
   return l;
@@ -555,6 +560,8 @@ std::vector<Launch> build_launches(skyla_hip_context *ctx, const std::vector<Com
   const bool xhalf = ctx && ctx->x_half_rows && xh != "0";
   const bool x4 = xh != "8";       // 8: the eight-wave tile throughout
   const bool balance = xh != "4";  // 4: the plain grid
+  const bool moe_xh = tactic_on("xhalf_moe");
+  uint32_t moe_used = 0;  // experts used per token: the x_div of the last expert gate/up matmul
   std::vector<Launch> out;
   std::vector<uint32_t> xkey;  // the rows the last prepass converted, until a barrier
   for (size_t i = 0; i < cmds.size();) {
@@ -572,6 +579,36 @@ std::vector<Launch> build_launches(skyla_hip_context *ctx, const std::vector<Com
       i++;
       continue;
     }
+    // expert groups (graph/moe.rs:26-40: grid (row tiles, experts, token tiles of 32)) on
+    // f16 rows: gate and up read the token rows (x_div = experts used per token), down the
+    // slot rows (x_div = 1), as many as the tokens times the experts used, which the last
+    // gate/up launch's x_div gives
+    if (a.kind == Command::Dispatch && a.name == "matmul" && a.push.size() == 13 && a.groups[1] > 1 && a.push[12] > 1)
+      moe_used = a.push[12];
+    if (xhalf && moe_xh && a.hxm_fn && !a.segmented && a.push.size() == 13 && a.bufs.size() == 5 && a.groups[1] > 1 &&
+        a.push[6] % 256 == 0 && a.push[6] <= 12288 && a.push[4] % 4 == 0 && a.push[8] % 4 == 0 &&
+        (a.push[12] > 1 || moe_used > 1)) {
+      const uint32_t per_token = a.push[12] > 1 ? 1u : moe_used;
+      const uint32_t rows = a.groups[2] * 32 * per_token;  // token tiles of 32: the chunk's tokens
+      const uint64_t h_off = ((uint64_t)rows * 4 + 255) & ~(uint64_t)255;
+      const std::vector<uint32_t> key = {(uint32_t)((uintptr_t)a.bufs[2] >> 32), (uint32_t)(uintptr_t)a.bufs[2],
+                                         a.push[4], a.push[8], a.push[6], rows, 1u};
+      if (key != xkey) {
+        out.push_back(x_half_prepass(ctx, a, h_off, rows, per_token));
+        xkey = key;
+      }
+      const Command *one[1] = {&a};
+      Launch l = pack(one, 1);
+      l.fn = a.hxm_fn;
+      l.split = 0;
+      l.args[4] = (uint32_t)(h_off / 2);  // f16 units
+      l.args[8] = a.push[6];
+      l.xh_buf = 2;
+      l.xh_bytes = out.back().xh_bytes;
+      out.push_back(std::move(l));
+      i++;
+      continue;
+    }
     if (xhalf && a.hx_fn && !a.segmented && a.push.size() == 13 && a.bufs.size() == 5 && a.groups[1] == 1 &&
         a.push[6] % 256 == 0 && a.push[6] <= 12288 && a.push[4] % 4 == 0 && a.push[8] % 4 == 0) {
       const uint32_t rows = a.groups[2] * 128;
@@ -579,7 +616,7 @@ std::vector<Launch> build_launches(skyla_hip_context *ctx, const std::vector<Com
       const std::vector<uint32_t> key = {(uint32_t)((uintptr_t)a.bufs[2] >> 32), (uint32_t)(uintptr_t)a.bufs[2],
                                          a.push[4], a.push[8], a.push[6], a.groups[2]};
       if (key != xkey) {
-        out.push_back(x_half_prepass(ctx, a, h_off));
+        out.push_back(x_half_prepass(ctx, a, h_off, rows));
         xkey = key;
       }
       // Matmuls on the same rows with no barrier between them (q, k, v of a prefill chunk)
@@ -785,6 +822,7 @@ Command dispatch_command(const skyla_hip_pipeline *p, const std::vector<void *> 
   c.retile = p->retile;
   c.split_fn = p->split_fn;
   c.hx_fn = p->hx_fn;
+  c.hxm_fn = p->hxm_fn;
   c.hx4_fn = p->hx4_fn;
   c.hx4b_fn = p->hx4b_fn;
   c.hxs_fn = p->hxs_fn;
@@ -1276,6 +1314,11 @@ int skyla_hip_pipeline_new(skyla_hip_context *ctx, const char *name, uint32_t n_
       p->split_threads = 512;
     }
   }
+  // expert-group K-quant matmul (MOE = 1) on f32 inputs: the same tile on x_half_rows's f16
+  // rows (build_launches inserts the prepass of the launch's input rows)
+  if (std::strcmp(name, "matmul") == 0 && n_spec >= 3 && (spec[0] == 1 || spec[0] == 2) && spec[2] == 1 &&
+      !(n_spec == 4 && spec[3]))
+    p->hxm_fn = find_function(ctx, "matmul_xm__" + std::to_string(spec[0]) + "_" + std::to_string(spec[1]));
   if (p->tok_fn) {  // the batched form must take the workgroup it is launched with
     int tok_max = 0;
     const uint32_t want = p->tok_threads ? p->tok_threads : threads;

@@ -274,6 +274,34 @@ def test_moe_prefill_chunk(ctx, moe):
     assert rel_l2(np.concatenate(gots), np.concatenate(outs)) <= 2e-3
 
 
+@pytest.mark.parametrize("n_tok", [128, 37, 1])
+def test_moe_prefill_f16_rows_same_bits(ctx, moe, n_tok):
+    """The expert-group matmuls of a prefill chunk on the f16 row prepass (the tokens' rows
+    for gate and up, the slot rows for down; tactic xhalf_moe=1) against the tile's own f32
+    staging (xhalf_moe=0): the same bits for every row whose input stays below 2^15 (the
+    gate/up outputs; the down rows of slots whose SiLU row does), and for rows past it
+    (the prepass scales the whole row by a power of two, the f32 tile each 256-column chunk
+    that holds such a value) within the f16 rounding of their inputs; 128, 37, 1 tokens."""
+    n = synth.activations(CFG, f"xh-n-{n_tok}", (n_tok, N_EMBD))
+    x0 = synth.activations(CFG, f"xh-x-{n_tok}", (n_tok, N_EMBD))
+    got = {}
+    slots = n_tok * N_USED
+    for xh in ("1", "0"):
+        with tactics(xhalf_moe=xh):
+            moe.load(n, x0)
+            moe.run_moe(batched=True)
+        a, m = moe.a, moe.a.moe
+        gate = a.f32()[m.gate: m.gate + slots * m.stride].reshape(slots, m.stride)[:, :N_FF_EXP].copy()
+        down = a.f32()[m.down: m.down + slots * a.s_embd].reshape(slots, a.s_embd)[:, :N_EMBD].copy()
+        got[xh] = (gate, down)
+    (g1, d1), (g0, d0) = got["1"], got["0"]
+    assert np.array_equal(g1.view(np.uint32), g0.view(np.uint32))
+    small = np.abs(g0).max(axis=1) < 32768.0           # slot rows with no value at 2^15 or above
+    assert np.array_equal(d1[small].view(np.uint32), d0[small].view(np.uint32))
+    if (~small).any():
+        assert rel_l2(d1[~small], d0[~small]) <= 2e-3
+
+
 def test_moe_decode_expert_variant_choice(ctx, moe):
     """Expert launches run on the variant the runtime picks for them (four waves, 16 lanes
     per row); the layer output equals the engine-requested variants' up to f32 summation

@@ -218,3 +218,26 @@ def test_check_catches_undersized_workspace():
     rt, tt, sp, kt = tile_map(gx, z * s + 1, s)     # one stray z row of workgroups
     with pytest.raises(AssertionError):
         assert np.array_equal(np.sort((rt * z + tt) * s + sp), np.arange(gx * z * s))
+
+
+@pytest.mark.parametrize("n_tok,used,n_expert", [(128, 8, 128), (1, 8, 128), (37, 2, 16), (128, 4, 64), (100, 8, 8)])
+def test_expert_prepass_rows(n_tok, used, n_expert):
+    """The f16 row prepass of an expert-group matmul (build_launches: rows = token tiles of
+    32 x rows per token, exponents then rows in the workspace) covers every input row the
+    expert tiles read: gate and up read token rows slot / used, down the slot rows; the
+    engine's grid has BATCH / 32 token tiles and a chunk holds at most BATCH tokens."""
+    from skyla_hip import engine as E
+    z = E.BATCH // E.MOE_TILE_COLS
+    assert n_tok <= z * 32
+    rng = np.random.default_rng(n_tok * 1000 + used)
+    ids = np.stack([rng.choice(n_expert, used, replace=False) for _ in range(n_tok)]).reshape(-1)
+    slots = np.argsort(ids, kind="stable")            # moe_sort's list: slots grouped by expert
+    for x_div, per_token in ((used, 1), (1, used)):   # gate / up, then down
+        rows = z * 32 * per_token
+        h_off = (rows * 4 + 255) // 256 * 256           # bytes of exponents before the rows
+        xrow = slots // x_div                             # the tile's input rows
+        assert xrow.max() < n_tok * per_token <= rows     # converted (t < ctl[2] x per_token)
+        assert xrow.max() * 4 < h_off                      # exponent words
+        n_in = 2048
+        last = h_off // 2 + int(xrow.max()) * n_in + n_in  # f16 units, end of the last row read
+        assert last <= (h_off + rows * n_in * 2) // 2      # inside the workspace region
