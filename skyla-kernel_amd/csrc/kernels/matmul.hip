@@ -1464,6 +1464,18 @@ MMXM(1, 0)
 MMXM(1, 1)
 MMXM(2, 0)
 MMXM(2, 1)
+// the same over up to four matrices on the same rows (gate and up): row tiles of segment s
+// after those of s - 1, each with its own regions, y_off, n_out and y_stride
+#define MMXMS(T, A)                                                                               \
+  extern "C" __global__ __launch_bounds__(256) void matmul_xms__##T##_##A(                         \
+      const uint4 *w, const uint16_t *wd, const f16 *x, float *y, const uint32_t *ctl,            \
+      Segments<MatmulPush> m) {                                                                   \
+    matmul_tile128_w<T, A, 2, 4, 32, 1, 0, 1>(w, wd, x, y, ctl, m.p[0], nullptr, nullptr, 1, 0, 1, m); \
+  }
+MMXMS(1, 0)
+MMXMS(1, 1)
+MMXMS(2, 0)
+MMXMS(2, 1)
 
 // The four-wave tile on the same f16 rows (128 tokens per wave, 128-k chunks).
 #define MMH4(T, A)                                                                                \

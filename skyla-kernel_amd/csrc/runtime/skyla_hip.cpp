@@ -245,6 +245,7 @@ struct skyla_hip_pipeline {
   hipFunction_t hx4b_fn = nullptr;       // and over a balanced grid (some tiles in K halves)
   hipFunction_t hxs_fn = nullptr;        // the eight-wave tile over several matrices (segments)
   hipFunction_t hxm_fn = nullptr;        // expert groups (MOE = 1) on x_half_rows's f16 rows
+  hipFunction_t hxms_fn = nullptr;       // and over several matrices on the same rows (segments)
   uint32_t split_threads = 0;
   hipFunction_t tok_fn = nullptr;        // batched form: a tok_per_wg x tok_per_wg_y block of
   uint32_t tok_per_wg = 0;               // grid.x and grid.y per workgroup
@@ -267,7 +268,8 @@ struct Command {
   std::shared_ptr<const Retile> retile;
   hipFunction_t split_fn = nullptr;
   uint32_t split_threads = 0;
-  hipFunction_t hx_fn = nullptr, hx4_fn = nullptr, hx4b_fn = nullptr, hxs_fn = nullptr, hxm_fn = nullptr;
+  hipFunction_t hx_fn = nullptr, hx4_fn = nullptr, hx4b_fn = nullptr, hxs_fn = nullptr, hxm_fn = nullptr,
+                hxms_fn = nullptr;
   hipFunction_t tok_fn = nullptr;
   uint32_t tok_per_wg = 0, tok_per_wg_y = 0, tok_threads = 0;
   std::string name;                 // the pipeline's shader name
@@ -597,16 +599,57 @@ std::vector<Launch> build_launches(skyla_hip_context *ctx, const std::vector<Com
         out.push_back(x_half_prepass(ctx, a, h_off, rows, per_token));
         xkey = key;
       }
-      const Command *one[1] = {&a};
-      Launch l = pack(one, 1);
-      l.fn = a.hxm_fn;
+      // expert matmuls on the same rows with no barrier between them (gate and up) run as
+      // one launch of segments: row tiles of segment s after those of s - 1
+      uint32_t n_run = 1;
+      uint64_t row_tiles = a.groups[0];
+      while (fuse && a.hxms_fn && n_run < kMaxSeg && i + n_run < cmds.size()) {
+        const Command &c = cmds[i + n_run];
+        if (!(c.kind == Command::Dispatch && c.hxm_fn == a.hxm_fn && c.hxms_fn == a.hxms_fn && !c.segmented &&
+              c.bufs == a.bufs && c.push.size() == 13 && c.groups[1] == a.groups[1] && c.groups[2] == a.groups[2] &&
+              c.push[4] == a.push[4] && c.push[6] == a.push[6] && c.push[8] == a.push[8] &&
+              c.push[10] == a.push[10] && c.push[11] == a.push[11] && c.push[12] == a.push[12]))
+          break;
+        row_tiles += c.groups[0];
+        n_run++;
+      }
+      Launch l;
+      l.bufs = a.bufs;
+      l.threads = 256;
       l.split = 0;
-      l.args[4] = (uint32_t)(h_off / 2);  // f16 units
-      l.args[8] = a.push[6];
+      if (n_run > 1) {
+        l.fn = a.hxms_fn;
+        const size_t w = 13;
+        l.args.assign(1 + kMaxSeg + kMaxSeg * w, 0u);
+        l.args[0] = n_run;
+        uint32_t start = 0;
+        for (uint32_t sgi = 0; sgi < kMaxSeg; sgi++) {
+          l.args[1 + sgi] = sgi < n_run ? start : 0xffffffffu;
+          if (sgi < n_run) {
+            const Command &c = cmds[i + sgi];
+            uint32_t *dst = l.args.data() + 1 + kMaxSeg + sgi * w;
+            std::copy(c.push.begin(), c.push.end(), dst);
+            dst[4] = (uint32_t)(h_off / 2);  // f16 units
+            dst[8] = a.push[6];
+            start += c.groups[0];
+          }
+        }
+        l.groups[0] = (uint32_t)row_tiles;
+      } else {
+        const Command *one[1] = {&a};
+        l = pack(one, 1);
+        l.fn = a.hxm_fn;
+        l.threads = 256;
+        l.split = 0;
+        l.args[4] = (uint32_t)(h_off / 2);  // f16 units
+        l.args[8] = a.push[6];
+      }
+      l.groups[1] = a.groups[1];
+      l.groups[2] = a.groups[2];
       l.xh_buf = 2;
       l.xh_bytes = out.back().xh_bytes;
       out.push_back(std::move(l));
-      i++;
+      i += n_run;
       continue;
     }
     if (xhalf && a.hx_fn && !a.segmented && a.push.size() == 13 && a.bufs.size() == 5 && a.groups[1] == 1 &&
@@ -823,6 +866,7 @@ Command dispatch_command(const skyla_hip_pipeline *p, const std::vector<void *> 
   c.split_fn = p->split_fn;
   c.hx_fn = p->hx_fn;
   c.hxm_fn = p->hxm_fn;
+  c.hxms_fn = p->hxms_fn;
   c.hx4_fn = p->hx4_fn;
   c.hx4b_fn = p->hx4b_fn;
   c.hxs_fn = p->hxs_fn;
@@ -1318,7 +1362,10 @@ int skyla_hip_pipeline_new(skyla_hip_context *ctx, const char *name, uint32_t n_
   // rows (build_launches inserts the prepass of the launch's input rows)
   if (std::strcmp(name, "matmul") == 0 && n_spec >= 3 && (spec[0] == 1 || spec[0] == 2) && spec[2] == 1 &&
       !(n_spec == 4 && spec[3]))
+  {
     p->hxm_fn = find_function(ctx, "matmul_xm__" + std::to_string(spec[0]) + "_" + std::to_string(spec[1]));
+    p->hxms_fn = find_function(ctx, "matmul_xms__" + std::to_string(spec[0]) + "_" + std::to_string(spec[1]));
+  }
   if (p->tok_fn) {  // the batched form must take the workgroup it is launched with
     int tok_max = 0;
     const uint32_t want = p->tok_threads ? p->tok_threads : threads;

@@ -274,20 +274,22 @@ def test_moe_prefill_chunk(ctx, moe):
     assert rel_l2(np.concatenate(gots), np.concatenate(outs)) <= 2e-3
 
 
+@pytest.mark.parametrize("fuse", ["1", "0"])
 @pytest.mark.parametrize("n_tok", [128, 37, 1])
-def test_moe_prefill_f16_rows_same_bits(ctx, moe, n_tok):
+def test_moe_prefill_f16_rows_same_bits(ctx, moe, n_tok, fuse):
     """The expert-group matmuls of a prefill chunk on the f16 row prepass (the tokens' rows
     for gate and up, the slot rows for down; tactic xhalf_moe=1) against the tile's own f32
     staging (xhalf_moe=0): the same bits for every row whose input stays below 2^15 (the
     gate/up outputs; the down rows of slots whose SiLU row does), and for rows past it
     (the prepass scales the whole row by a power of two, the f32 tile each 256-column chunk
-    that holds such a value) within the f16 rounding of their inputs; 128, 37, 1 tokens."""
+    that holds such a value) within the f16 rounding of their inputs; 128, 37, 1 tokens;
+    gate and up as one launch of two segments (fuse=1) or two launches (fuse=0)."""
     n = synth.activations(CFG, f"xh-n-{n_tok}", (n_tok, N_EMBD))
     x0 = synth.activations(CFG, f"xh-x-{n_tok}", (n_tok, N_EMBD))
     got = {}
     slots = n_tok * N_USED
     for xh in ("1", "0"):
-        with tactics(xhalf_moe=xh):
+        with tactics(xhalf_moe=xh, fuse=fuse if xh == "1" else None):
             moe.load(n, x0)
             moe.run_moe(batched=True)
         a, m = moe.a, moe.a.moe
