@@ -1569,21 +1569,18 @@ struct XHalfPush {
   uint32_t x_off, x_stride, n_in, h_off;
   uint32_t rows_per_token;  // input rows per token of ctl[2]: 1, or the slots of an expert down
 };
-extern "C" __global__ __launch_bounds__(256) void x_half_rows(const float *x, uint32_t *out, const uint32_t *ctl,
-                                                              XHalfPush p) {
-  const uint32_t t = blockIdx.x, tid = threadIdx.x;
-  if (t >= ctl[2] * p.rows_per_token) return;
-  const float *xr = x + p.x_off + (size_t)t * p.x_stride;
-  constexpr int MAXV = 48;  // values per thread: n_in <= 12288
-  float4 v[MAXV / 4];
+// One row of f16 for the tiles from its values v (n_in <= 12288 at 4 per thread and 256
+// threads), with e = 0 unless the row's largest |x| reaches 2^15 (then the row is x * 2^-e,
+// e putting it below 2^15): the rows at out + h_off (f16 row t at t * n_in), pairs (0,2),
+// (1,3) of every four values as the tiles' LDS rows hold them; the exponent at out[t].
+constexpr int HALF_ROW_V = 48;  // values per thread: n_in <= 12288
+SK_DEV void store_half_row(const float4 (&v)[HALF_ROW_V / 4], uint32_t *out, uint32_t h_off, uint32_t n_in,
+                           uint32_t t) {
+  const uint32_t tid = threadIdx.x;
   float m = 0.0f;
 #pragma unroll
-  for (int i = 0; i < MAXV / 4; i++) {
-    const uint32_t k = 4 * (tid + 256 * i);
-    v[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (k < p.n_in) v[i] = *(const float4 *)(xr + k);
+  for (int i = 0; i < HALF_ROW_V / 4; i++)
     m = fmaxf(m, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
-  }
   // the row's largest |x| (NaN counts as big, as in the tile's guard)
   __shared__ uint32_t big[4];
   __shared__ float wm[4];
@@ -1600,18 +1597,64 @@ extern "C" __global__ __launch_bounds__(256) void x_half_rows(const float *x, ui
   const bool any = big[0] | big[1] | big[2] | big[3];
   const int e = any && tm >= 32768.0f ? (int)((__builtin_bit_cast(uint32_t, tm) >> 23) & 255u) - 127 - 14 : 0;
   const float sc = __builtin_ldexpf(1.0f, -e);
-  f16 *h = (f16 *)(out + p.h_off) + (size_t)t * p.n_in;
+  f16 *h = (f16 *)(out + h_off) + (size_t)t * n_in;
 #pragma unroll
-  for (int i = 0; i < MAXV / 4; i++) {
+  for (int i = 0; i < HALF_ROW_V / 4; i++) {
     const uint32_t k = 4 * (tid + 256 * i);
-    if (k < p.n_in) {
+    if (k < n_in) {
       float4 a = v[i];
       if (e) a = make_float4(a.x * sc, a.y * sc, a.z * sc, a.w * sc);
-      // pairs (0,2),(1,3) of every four values: the order the tiles' LDS rows hold
       *(uint2 *)(h + k) = make_uint2(as_u32(pack_f16x2(a.x, a.z)), as_u32(pack_f16x2(a.y, a.w)));
     }
   }
   if (tid == 0) out[t] = (uint32_t)e;
+}
+
+extern "C" __global__ __launch_bounds__(256) void x_half_rows(const float *x, uint32_t *out, const uint32_t *ctl,
+                                                              XHalfPush p) {
+  const uint32_t t = blockIdx.x, tid = threadIdx.x;
+  if (t >= ctl[2] * p.rows_per_token) return;
+  const float *xr = x + p.x_off + (size_t)t * p.x_stride;
+  float4 v[HALF_ROW_V / 4];
+#pragma unroll
+  for (int i = 0; i < HALF_ROW_V / 4; i++) {
+    const uint32_t k = 4 * (tid + 256 * i);
+    v[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (k < p.n_in) v[i] = *(const float4 *)(xr + k);
+  }
+  store_half_row(v, out, p.h_off, p.n_in, t);
+}
+
+// silu_mul (silu_mul.comp:15-23) on the rows an expert down projection reads, with that
+// matmul's f16 row prepass in the same launch: slot row t (t < ctl[2] x rows_per_token)
+// becomes g / (1 + e^-g) * u in place, in silu_mul's expression (the same f32 values), and
+// its f16 row and exponent go to the workspace as x_half_rows writes them.  The columns
+// past n_in of a row and the rows past the slots are not computed: no later launch reads
+// them.
+struct SiluHalfPush {
+  uint32_t g_off, u_off, x_stride, n_in, h_off, rows_per_token;
+};
+extern "C" __global__ __launch_bounds__(256) void silu_half_rows(float *a, uint32_t *out, const uint32_t *ctl,
+                                                                 SiluHalfPush p) {
+  const uint32_t t = blockIdx.x, tid = threadIdx.x;
+  if (t >= ctl[2] * p.rows_per_token) return;
+  float4 v[HALF_ROW_V / 4];
+#pragma unroll
+  for (int i = 0; i < HALF_ROW_V / 4; i++) {
+    const uint32_t k = 4 * (tid + 256 * i);
+    v[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (k < p.n_in) {
+      float *gr = a + p.g_off + (size_t)t * p.x_stride + k;
+      const float4 g = *(const float4 *)gr, u = *(const float4 *)(a + p.u_off + (size_t)t * p.x_stride + k);
+      {
+#pragma clang fp contract(off)
+        v[i] = make_float4(g.x / (1.0f + expf(-g.x)) * u.x, g.y / (1.0f + expf(-g.y)) * u.y,
+                           g.z / (1.0f + expf(-g.z)) * u.z, g.w / (1.0f + expf(-g.w)) * u.w);
+      }
+      *(float4 *)gr = v[i];
+    }
+  }
+  store_half_row(v, out, p.h_off, p.n_in, t);
 }
 
 // Workspace of skyla_hip_dispatch_noalloc, the entry point that allocates nothing: the K

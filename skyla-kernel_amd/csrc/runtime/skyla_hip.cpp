@@ -191,6 +191,8 @@ struct skyla_hip_context {
   hipFunction_t fill_u32 = nullptr;
   uint32_t n_cu = 256;  // compute units of the device (hipDeviceProp_t.multiProcessorCount)
   hipFunction_t x_half_rows = nullptr;  // f16 row prepass of dense K-quant matmuls (matmul.hip)
+  hipFunction_t silu_half_rows = nullptr;  // silu_mul with the expert down projection's prepass
+  hipFunction_t silu_mul = nullptr;        // (moe.hip): the launch it replaces
 };
 
 struct HostFree {
@@ -595,6 +597,20 @@ std::vector<Launch> build_launches(skyla_hip_context *ctx, const std::vector<Com
       const uint64_t h_off = ((uint64_t)rows * 4 + 255) & ~(uint64_t)255;
       const std::vector<uint32_t> key = {(uint32_t)((uintptr_t)a.bufs[2] >> 32), (uint32_t)(uintptr_t)a.bufs[2],
                                          a.push[4], a.push[8], a.push[6], rows, 1u};
+      // the down projection's rows come from silu_mul, the launch before it: one launch of
+      // both (silu_half_rows: the same f32 rows and the same f16 rows) when it covers them
+      // (g_off = the rows read, one flat region of at least rows x x_stride values)
+      Launch *prev = out.empty() ? nullptr : &out.back();
+      if (key != xkey && per_token > 1 && ctx->silu_half_rows && prev && !prev->mark && prev->fn == ctx->silu_mul &&
+          prev->args.size() == 4 && prev->args[0] == a.push[4] && prev->args[3] == 0 &&
+          (uint64_t)prev->args[2] >= (uint64_t)rows * a.push[8] && prev->groups[1] == 1 && prev->groups[2] == 1) {
+        Launch f = x_half_prepass(ctx, a, h_off, rows, per_token);
+        f.fn = ctx->silu_half_rows;
+        f.bufs = {prev->bufs[0], nullptr, a.bufs[4]};
+        f.args = {prev->args[0], prev->args[1], a.push[8], a.push[6], (uint32_t)(h_off / 4), per_token};
+        *prev = std::move(f);
+        xkey = key;
+      }
       if (key != xkey) {
         out.push_back(x_half_prepass(ctx, a, h_off, rows, per_token));
         xkey = key;
@@ -1135,6 +1151,8 @@ int skyla_hip_context_new(int device, skyla_hip_context **out) {
     }
   }
   ctx->x_half_rows = find_function(ctx.get(), "x_half_rows");
+  ctx->silu_half_rows = find_function(ctx.get(), "silu_half_rows");
+  ctx->silu_mul = find_function(ctx.get(), "silu_mul");
   if (prop.multiProcessorCount > 0) ctx->n_cu = (uint32_t)prop.multiProcessorCount;
   *out = ctx.release();
   return SKYLA_HIP_OK;
