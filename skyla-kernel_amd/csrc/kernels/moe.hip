@@ -105,79 +105,77 @@ extern "C" __global__ __launch_bounds__(64) void moe_route(float *a, uint32_t *i
 // moe_sort (moe_sort.comp:21-55): slot s = tok * n_used + k is routed to ids[s].  Writes
 // table[2e] = count, table[2e+1] = start (exclusive scan in expert order) and list[start +
 // rank] = s with rank = number of earlier slots of the same expert (stable).  One
-// workgroup; the ids are read once into LDS (the list writes go to the same arena, so
-// reads from it could not be hoisted past them), and the ranking runs on wave 0, 64 slots
-// at a time, using ballots to find the lanes that share an expert.
+// workgroup of four waves; wave w owns the slots [256 w, 256 w + 256) and counts them per
+// expert in its own LDS row, so its first slot of expert e goes after the table's start of
+// e plus the earlier waves' counts of e.  Each wave then ranks its slots 64 at a time in
+// slot order, using ballots to find the lanes that share an expert.  The ids are read once
+// (the list writes go to the same arena, so reads from it could not be hoisted past them).
 extern "C" __global__ __launch_bounds__(256) void moe_sort(uint32_t *a, SortPush p) {
-  __shared__ uint32_t count[256];
-  __shared__ uint32_t next[256];
-  __shared__ uint32_t sid[MAX_SLOTS];
-  const uint32_t t = threadIdx.x;
+  __shared__ uint32_t count[4][256];  // per wave and expert; then that wave's cursor
+  __shared__ uint32_t wsum[4];
+  const uint32_t t = threadIdx.x, wave = t >> 6, lane = t & 63;
   const uint32_t n = min(a[2] * p.n_used, MAX_SLOTS);
   const uint32_t n_expert = min(p.n_expert, 256u);
-  count[t] = 0;
-  uint32_t mine[MAX_SLOTS / 256];
+  constexpr uint32_t PER_WAVE = MAX_SLOTS / 4, CHUNKS = PER_WAVE / 64;
 #pragma unroll
-  for (uint32_t j = 0; j < MAX_SLOTS / 256; j++) {
-    const uint32_t i = t + 256 * j;
+  for (uint32_t w = 0; w < 4; w++) count[w][t] = 0;
+  uint32_t mine[CHUNKS];
+#pragma unroll
+  for (uint32_t j = 0; j < CHUNKS; j++) {
+    const uint32_t i = PER_WAVE * wave + 64 * j + lane;
     mine[j] = i < n ? a[p.ids_off + i] : 0xffffffffu;
   }
   __syncthreads();
 #pragma unroll
-  for (uint32_t j = 0; j < MAX_SLOTS / 256; j++) {
-    sid[t + 256 * j] = mine[j];
-    if (mine[j] < n_expert) atomicAdd(&count[mine[j]], 1u);
-  }
+  for (uint32_t j = 0; j < CHUNKS; j++)
+    if (mine[j] < n_expert) atomicAdd(&count[wave][mine[j]], 1u);
   __syncthreads();
-  if (t < 64) {
-    // exclusive scan of count over 256 experts: 4 per lane, then a wave scan
-    uint32_t c[4], s = 0;
+  // thread t: expert e = t.  Its total over the waves, the exclusive scan of the totals in
+  // expert order (a wave scan, then the waves' sums), and each wave's cursor.
+  const uint32_t c0 = count[0][t], c1 = count[1][t], c2 = count[2][t], c3 = count[3][t];
+  const uint32_t tot = c0 + c1 + c2 + c3;
+  uint32_t incl = tot;
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-      c[j] = count[4 * t + j];
-      s += c[j];
-    }
-    uint32_t incl = s;
+  for (int d = 1; d < 64; d <<= 1) {
+    const uint32_t o = __shfl_up(incl, d, 64);
+    if (lane >= (uint32_t)d) incl += o;
+  }
+  if (lane == 63) wsum[wave] = incl;
+  __syncthreads();
+  uint32_t start = incl - tot;
+  for (uint32_t w = 0; w < wave; w++) start += wsum[w];
+  if (t < n_expert) {
+    a[p.table_off + 2 * t] = tot;
+    a[p.table_off + 2 * t + 1] = start;
+  }
+  count[0][t] = start;
+  count[1][t] = start + c0;
+  count[2][t] = start + c0 + c1;
+  count[3][t] = start + c0 + c1 + c2;
+  __syncthreads();
+  const uint64_t below = (1ull << lane) - 1;
 #pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-      const uint32_t o = __shfl_up(incl, d, 64);
-      if (t >= (uint32_t)d) incl += o;
-    }
-    uint32_t run = incl - s;
+  for (uint32_t j = 0; j < CHUNKS; j++) {
+    const uint32_t i = PER_WAVE * wave + 64 * j + lane;
+    const uint32_t e = mine[j];
+    const bool ok = e < n_expert;  // slots past n hold 0xffffffff
+    // lanes with the same expert: intersect the ballots of all 8 expert bits
+    uint64_t same = __ballot(ok);
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const uint32_t e = 4 * t + j;
-      next[e] = run;
-      if (e < n_expert) {
-        a[p.table_off + 2 * e] = c[j];
-        a[p.table_off + 2 * e + 1] = run;
-      }
-      run += c[j];
+    for (int bit = 0; bit < 8; bit++) {
+      const uint64_t ones = __ballot(ok && ((e >> bit) & 1u));
+      same &= ((e >> bit) & 1u) ? ones : ~ones;
     }
-    const uint64_t below = (1ull << t) - 1;
-    for (uint32_t base = 0; base < n; base += 64) {
-      const uint32_t i = base + t;
-      const bool live = i < n;
-      const uint32_t e = live ? sid[i] : 0xffffffffu;
-      const bool ok = live && e < n_expert;
-      // lanes with the same expert: intersect the ballots of all 8 expert bits
-      uint64_t same = __ballot(ok);
-#pragma unroll
-      for (int b = 0; b < 8; b++) {
-        const uint64_t ones = __ballot(ok && ((e >> b) & 1u));
-        same &= ((e >> b) & 1u) ? ones : ~ones;
-      }
-      if (ok) {
-        const uint32_t rank = __popcll(same & below);
-        const uint32_t at = next[e] + rank;
-        a[p.list_off + at] = i;
-        // the highest lane of the group advances the expert's cursor
-        if ((same >> t) == 1ull) next[e] = at + 1;
-      }
-      // a single wave's LDS accesses complete in program order; the fence only keeps the
-      // compiler from moving the next step's cursor reads above these writes
-      __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    if (ok) {
+      const uint32_t rank = __popcll(same & below);
+      const uint32_t at = count[wave][e] + rank;
+      a[p.list_off + at] = i;
+      // the highest lane of the group advances the wave's cursor
+      if ((same >> lane) == 1ull) count[wave][e] = at + 1;
     }
+    // a single wave's LDS accesses complete in program order; the fence only keeps the
+    // compiler from moving the next step's cursor reads above these writes
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
   }
 }
 
