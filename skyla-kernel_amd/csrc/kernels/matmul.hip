@@ -29,6 +29,7 @@
 namespace {
 
 constexpr int TM = 128;        // rows per workgroup
+constexpr uint32_t TILE_MAP = 320;  // words of moe_sort's tile map before its table (moe.hip)
 constexpr int KC = 256;        // k per LDS stage (one K-quant super-block)
 constexpr int PITCH = KC + 8;  // f16 per staged token row (16 B pad: conflict-free b128)
 
@@ -358,7 +359,8 @@ SK_DEV void matmul_body(const uint4 *__restrict__ w, const uint16_t *__restrict_
       load_x<TN, XHALF>(xn, x, xrow, p.x_off, p.x_stride, kn, min(p.n_in - kn, (uint32_t)KC));
     }
     const int steps = (int)(nk >> 4);
-    const bool rescaled = (xflag[buf][0] | xflag[buf][1] | xflag[buf][2] | xflag[buf][3]) != 0;
+    // f16 rows never rescale (store_x leaves the flags 0): the check compiles away
+    const bool rescaled = !XHALF && (xflag[buf][0] | xflag[buf][1] | xflag[buf][2] | xflag[buf][3]) != 0;
     auto run = [&](f32x16 *dst) {
 #pragma unroll
       for (int t = 0; t < 16; t++) {
@@ -500,7 +502,12 @@ struct XChunk {
 };
 
 // LIVE (expert groups): token rows past `live` (the group's last tile pads its 32 columns
-// with copies of its last row) are zeroed instead of loaded; their columns are not stored.
+// with copies of its last row) read zeros without touching memory; their columns are not
+// stored.  f16 rows: a raw buffer load over the rows from x_off, whose offset for a padding
+// row lies past the resource's end.  f32 rows: the padding rows are not loaded and keep the
+// chunk's contents, which the caller zeroes once before its first load.  A branch around
+// the load or zeros written here, in the loop, made every chunk wait for all loads in
+// flight, the next stage's weights included, before issuing its own.
 template <int KX, int XHALF, int NT, int TN, bool LIVE = false>
 SK_DEV void load_chunk(XChunk<KX, XHALF, NT, TN> &c, const void *xv, const uint32_t *xrow, uint32_t x_off,
                        uint32_t x_stride, uint32_t k0, uint32_t n_in, uint32_t live = 0) {
@@ -514,16 +521,25 @@ SK_DEV void load_chunk(XChunk<KX, XHALF, NT, TN> &c, const void *xv, const uint3
     // when the chunk is stored (a select here would make the loads wait at once, and a
     // predicated load is split into per-dword branches)
     const size_t base = (size_t)x_off + (size_t)xrow[J / IPR] * x_stride + (kb < n_in ? kb : n_in - PER);
-    if constexpr (XHALF) {
-      if (!LIVE || J / IPR < live)
-        c.h[i] = *(const uint4 *)((const f16 *)xv + base);
-      else
-        c.h[i] = make_uint4(0u, 0u, 0u, 0u);
-    } else if (!LIVE || J / IPR < live)
+    if constexpr (LIVE && XHALF) {
+      const BufRes xr = buf_res((const f16 *)xv + x_off, 0x7fffffffull);
+      const uint32_t off = J / IPR < live && kb < n_in ? 2u * (uint32_t)(base - x_off) : 0x80000000u;
+      c.h[i] = buf_load(xr, off, 0);
+    } else if constexpr (XHALF) {
+      c.h[i] = *(const uint4 *)((const f16 *)xv + base);
+    } else if (!LIVE || J / IPR < live) {
       c.v[i] = *(const float4 *)((const float *)xv + base);
-    else
-      c.v[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
   }
+}
+
+template <int KX, int XHALF, int NT, int TN>
+SK_DEV void zero_chunk(XChunk<KX, XHALF, NT, TN> &c) {
+  using C = XChunk<KX, XHALF, NT, TN>;
+#pragma unroll
+  for (int i = 0; i < (XHALF ? C::IPT : 1); i++) c.h[i] = make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+  for (int i = 0; i < (XHALF ? 1 : C::IPT); i++) c.v[i] = make_float4(0.f, 0.f, 0.f, 0.f);
 }
 
 // Stores a chunk to LDS, pair-permuted as the weight fragments; returns whether this
@@ -674,6 +690,96 @@ struct WLds<2, NT> {  // Q6_K row: ql 128 | qh 64 | scales 16 | d 2
     }
   }
 };
+
+// Expert groups: the same stage loads (WLds layout), read through buffer resources over
+// this expert's slice of each tensor.  A thread's offsets are fixed and a stage adds a
+// scalar offset; a stage past the last, and a wave that owns none of a load's rows, read
+// through a resource of no bytes, which returns zeros without touching memory.  Every load
+// is thus one unconditional instruction: with the loads inside branches, the compiler's
+// in-order load counting merged the paths and waited for every load in flight (the next
+// stage's included) at each use.
+template <int TYPE, int NT>
+struct WBuf;
+template <int NT>
+struct WBuf<1, NT> {
+  using R = WLds<1, NT>;
+  BufRes rq, rh, none;
+  uint32_t vq[R::QI], vh;
+  bool hwave;  // waves 0, 1: the header loads (rows tid < TM)
+  __device__ __forceinline__ WBuf(const uint4 *w, const MatmulPush &p, uint32_t base, uint32_t row0, uint32_t tid) {
+    const uint32_t units = p.n_in >> 5, supers = p.n_in >> 8;
+    rq = buf_res(w + p.o0 + (size_t)base * units, (uint64_t)p.n_out * units * 16);
+    rh = buf_res(w + p.o1 + (size_t)base * supers, (uint64_t)p.n_out * supers * 16);
+    none = buf_res(nullptr, 0);
+#pragma unroll
+    for (int i = 0; i < R::QI; i++) {
+      const uint32_t u = tid + NT * i;
+      vq[i] = (min(row0 + (u >> 3), p.n_out - 1) * units + (u & 7)) * 16;
+    }
+    vh = min(row0 + (tid & (TM - 1)), p.n_out - 1) * supers * 16;
+    hwave = __builtin_amdgcn_readfirstlane(tid >> 6) < (uint32_t)(TM / 64);
+  }
+  __device__ __forceinline__ void load(R &r, uint32_t sb, bool live) const {
+    const BufRes q = live ? rq : none, h = live && hwave ? rh : none;
+#pragma unroll
+    for (int i = 0; i < R::QI; i++) r.q[i] = buf_load(q, vq[i], sb * 128);
+    r.hd = buf_load(h, vh, sb * 16);
+  }
+};
+template <int NT>
+struct WBuf<2, NT> {
+  using R = WLds<2, NT>;
+  BufRes rl, rq, rs, rd, none;
+  uint32_t vl[R::LI], vq[R::HI], vs, vd;
+  bool swave, dwave;  // waves 0, 1: the scales (rows tid < TM); waves 2, 3: the d (tid - TM)
+  __device__ __forceinline__ WBuf(const uint4 *w, const uint16_t *wd, const MatmulPush &p, uint32_t base, uint32_t row0,
+              uint32_t tid) {
+    const uint32_t supers = p.n_in >> 8;
+    const uint64_t rows = (uint64_t)p.n_out * supers;  // (row, super-block) pairs of the expert
+    rl = buf_res(w + p.o0 + (size_t)base * supers * 8, rows * 128);
+    rq = buf_res(w + p.o1 + (size_t)base * supers * 4, rows * 64);
+    rs = buf_res(w + p.o2 + (size_t)base * supers, rows * 16);
+    rd = buf_res(wd + p.o3 + (size_t)base * supers, rows * 2);
+    none = buf_res(nullptr, 0);
+#pragma unroll
+    for (int i = 0; i < R::LI; i++) {
+      const uint32_t u = tid + NT * i;
+      vl[i] = (min(row0 + (u >> 3), p.n_out - 1) * supers * 8 + (u & 7)) * 16;
+    }
+#pragma unroll
+    for (int i = 0; i < R::HI; i++) {
+      const uint32_t u = tid + NT * i;
+      vq[i] = (min(row0 + (u >> 2), p.n_out - 1) * supers * 4 + (u & 3)) * 16;
+    }
+    const uint32_t rr = min(row0 + (tid & (TM - 1)), p.n_out - 1) * supers;
+    vs = rr * 16;
+    vd = rr * 2;
+    const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    swave = wv < (uint32_t)(TM / 64);
+    dwave = !swave && wv < (uint32_t)(2 * TM / 64);
+  }
+  __device__ __forceinline__ void load(R &r, uint32_t sb, bool live) const {
+    const BufRes l = live ? rl : none, q = live ? rq : none;
+    const BufRes sc = live && swave ? rs : none, d = live && dwave ? rd : none;
+#pragma unroll
+    for (int i = 0; i < R::LI; i++) r.ql[i] = buf_load(l, vl[i], sb * 128);
+#pragma unroll
+    for (int i = 0; i < R::HI; i++) r.qh[i] = buf_load(q, vq[i], sb * 64);
+    r.sc = buf_load(sc, vs, sb * 16);
+    r.d = __builtin_amdgcn_raw_buffer_load_b16(d, vd, sb * 2, 0);
+  }
+};
+
+template <int TYPE, int NT>
+SK_DEV WBuf<TYPE, NT> make_wbuf(const uint4 *w, const uint16_t *wd, const MatmulPush &p, uint32_t base,
+                                uint32_t row0, uint32_t tid) {
+  if constexpr (TYPE == 1) {
+    (void)wd;
+    return WBuf<1, NT>(w, p, base, row0, tid);
+  } else {
+    return WBuf<2, NT>(w, wd, p, base, row0, tid);
+  }
+}
 
 // Q4_K fragment of lane half hh from the 8 qs bytes of its step (same arithmetic as
 // weight_frag): low nibbles for hh = 0, high nibbles (16q, the 1/16 is in the scale) for 1.
@@ -1011,7 +1117,16 @@ SK_DEV void matmul_tile128_w(const uint4 *__restrict__ w, const uint16_t *__rest
     p.y_stride = pick(&MatmulPush::y_stride);
     rt -= sg == 0 ? 0u : sg == 1 ? segs.start[1] : sg == 2 ? segs.start[2] : segs.start[3];
   }
-  const uint32_t e = MOE ? blockIdx.y : 0;
+  uint32_t e = MOE ? blockIdx.y : 0;
+  if constexpr (MOE == 2) {
+    // grid.y walks moe_sort's tile map (the (expert, 32-slot tile) pairs the chunk has,
+    // TILE_MAP words before the table) instead of every expert times every token tile
+    const uint32_t *map = ctl + p.table_off - TILE_MAP;
+    if (blockIdx.y >= map[0]) return;
+    const uint32_t v = map[1 + blockIdx.y];
+    e = v & 0xffffu;
+    tt = v >> 16;
+  }
   const uint32_t base = MOE ? e * p.n_out : 0;
   const uint32_t row0 = rt * TM;
   const uint32_t n_all = MOE ? ctl[p.table_off + 2 * e] : ctl[2];
@@ -1081,16 +1196,75 @@ SK_DEV void matmul_tile128_w(const uint4 *__restrict__ w, const uint16_t *__rest
       dl_stage<NW, TYPE, NB, TN>(L, acc, xs, xs + XB, wl + b * WB, wl + (b ^ 1) * WB, st + 1 < n_stage,
                                  kbase + KC * st, st0 + st + 1);
     }
+  } else if constexpr (MOE != 0 && XHALF == 2) {
+    // Expert groups on f16 rows: the stage weights are loaded two stages ahead, alternating
+    // between two register sets (WBuf: unconditional buffer loads), and each stage issues
+    // the next chunk's activations before the weights of the stage after next, so the waits
+    // for the data of stage st + 1 (at the end of stage st) leave those in flight.
+    static_assert(KX == KC, "one activation chunk per stage");
+    const WBuf<TYPE, NT> wb = make_wbuf<TYPE, NT>(w, wd, p, base, row0, tid);
+    WLds<TYPE, NT> wa, wc;
+    wb.load(wa, st0, true);
+    __syncthreads();  // xrow
+    XChunk<KX, XHALF, NT, TN> xn;
+    load_chunk<KX, XHALF, NT, TN, true>(xn, x, xrow, p.x_off, p.x_stride, kbase, p.n_in, n_tok);
+    wa.store(wa, wl, tid);
+    store_chunk<KX, XHALF, NT, TN>(xs, xn, xexp, kbase, p.n_in);
+    wb.load(wa, st0 + 1, 1 < n_stage);
+    __syncthreads();
+    // stage st: `held` holds the weights of stage st + 1, `fill` receives those of st + 2
+    auto stage = [&](uint32_t st, WLds<TYPE, NT> &held, WLds<TYPE, NT> &fill) {
+      StageScales<TYPE> ss;
+      lds_scales<TYPE>(wrow, hh, ss);
+      const bool next = st + 1 < n_stage;
+      load_chunk<KX, XHALF, NT, TN, true>(xn, x, xrow, p.x_off, p.x_stride, kbase + (st + 1) * KC, p.n_in, n_tok);
+      wb.load(fill, st0 + st + 2, st + 2 < n_stage);
+      constexpr int SPC = KX / 16;
+      f16x8 xf0[NB], xf1[NB], wf0, wf1;
+      auto frags = [&](int t, f16x8(&xf)[NB], f16x8 &wf) {
+        f16x2 sc, nm;
+        ss.get(t, sc, nm);
+        wf = lds_frag<TYPE>(wrow, t, hh, sc, nm);
+        const uint32_t ko = koff<TYPE>(t, hh);
+#pragma unroll
+        for (int j = 0; j < NB; j++) xf[j] = *(const f16x8 *)(xs + (32 * (tb + j) + (lane & 31)) * PITCH2 + ko);
+      };
+      frags(0, xf0, wf0);
+#pragma unroll
+      for (int ts = 0; ts < SPC; ts++) {
+        if (ts + 1 < SPC) {
+          if (ts & 1)
+            frags(ts + 1, xf0, wf0);
+          else
+            frags(ts + 1, xf1, wf1);
+        }
+#pragma unroll
+        for (int j = 0; j < NB; j++)
+          acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16((ts & 1) ? xf1[j] : xf0[j], (ts & 1) ? wf1 : wf0,
+                                                          acc[j], 0, 0, 0);
+      }
+      __syncthreads();  // every wave is done with this stage's weights and activations
+      if (next) {
+        held.store(held, wl, tid);
+        store_chunk<KX, XHALF, NT, TN>(xs, xn, xexp, kbase + (st + 1) * KC, p.n_in);
+        __syncthreads();
+      }
+    };
+    for (uint32_t st = 0; st < n_stage; st += 2) {
+      stage(st, wa, wc);
+      if (st + 1 < n_stage) stage(st + 1, wc, wa);
+    }
   } else {
   WLds<TYPE, NT> wr;
   if constexpr (TYPE == 1) wr.load(wr, w, p, row0, st0, tid, base);
   else wr.load(wr, w, wd, p, row0, st0, tid, base);
   __syncthreads();  // xrow
+  XChunk<KX, XHALF, NT, TN> xn;  // the chunk in flight; expert groups: padding rows stay zero
+  if constexpr (MOE != 0 && !XHALF) zero_chunk(xn);
+  load_chunk<KX, XHALF, NT, TN, MOE != 0>(xn, x, xrow, p.x_off, p.x_stride, kbase, p.n_in, n_tok);
+  wr.store(wr, wl, tid);
   {
-    XChunk<KX, XHALF, NT, TN> c0;
-    load_chunk<KX, XHALF, NT, TN, MOE != 0>(c0, x, xrow, p.x_off, p.x_stride, kbase, p.n_in, n_tok);
-    wr.store(wr, wl, tid);
-    const bool r = store_chunk<KX, XHALF, NT, TN>(xs, c0, xexp, kbase, p.n_in);
+    const bool r = store_chunk<KX, XHALF, NT, TN>(xs, xn, xexp, kbase, p.n_in);
     if (lane == 0) xflag[wave] = r;
   }
   __syncthreads();
@@ -1106,14 +1280,14 @@ SK_DEV void matmul_tile128_w(const uint4 *__restrict__ w, const uint16_t *__rest
     }
 #pragma unroll
     for (int c4 = 0; c4 < KC / KX; c4++) {
-      XChunk<KX, XHALF, NT, TN> xn;
       const bool next = chunk + 1 < n_chunk;
       if (next)
         load_chunk<KX, XHALF, NT, TN, MOE != 0>(xn, x, xrow, p.x_off, p.x_stride, kbase + (chunk + 1) * KX, p.n_in,
                                                 n_tok);
-      bool rescaled = false;
+      bool rescaled = false;  // f16 rows never rescale (store_chunk returns false)
+      if constexpr (!XHALF)
 #pragma unroll
-      for (int q = 0; q < NW; q++) rescaled |= xflag[q] != 0;
+        for (int q = 0; q < NW; q++) rescaled |= xflag[q] != 0;
       if (rescaled) {
 #pragma unroll
         for (int j = 0; j < NB; j++)
@@ -1306,9 +1480,10 @@ SK_DEV void matmul_tile128(const uint4 *__restrict__ w, const uint16_t *__restri
         const bool next = chunk + 1 < n_chunk;
         if (next) load_chunk<KX, XHALF, NT2>(xn, x, xrow, p.x_off, p.x_stride, (chunk + 1) * KX, p.n_in);
         if (c4 == KC / KX - 1 && more) load_stage<TYPE>(wn, w, wd, p, wrow, kc + KC, min(p.n_in - kc - KC, (uint32_t)KC));
-        bool rescaled = false;
+        bool rescaled = false;  // f16 rows never rescale (store_chunk returns false)
+        if constexpr (!XHALF)
 #pragma unroll
-        for (int q = 0; q < NT2 / 64; q++) rescaled |= xflag[q] != 0;
+          for (int q = 0; q < NT2 / 64; q++) rescaled |= xflag[q] != 0;
         const f16 *cur = xs;
         if (rescaled) {  // acc *= 2^-e(token) before this chunk (exact)
 #pragma unroll
@@ -1453,12 +1628,13 @@ MMH(1, 1)
 MMH(2, 0)
 MMH(2, 1)
 
-// Expert groups (MOE = 1, 128 x 32 tiles, four waves) on the f16 rows x_half_rows wrote:
-// the rows of the launch's inputs (tokens for gate and up, slots for down), no K split.
+// Expert groups (128 x 32 tiles, four waves) on the f16 rows x_half_rows wrote: the rows of
+// the launch's inputs (tokens for gate and up, slots for down), no K split.  MOE = 2: grid
+// (row tiles, at least the tile map's pairs, 1), grid.y indexing moe_sort's tile map.
 #define MMXM(T, A)                                                                                \
   extern "C" __global__ __launch_bounds__(256) void matmul_xm__##T##_##A(                          \
       const uint4 *w, const uint16_t *wd, const f16 *x, float *y, const uint32_t *ctl, MatmulPush p) { \
-    matmul_tile128_w<T, A, 2, 4, 32, 1>(w, wd, x, y, ctl, p);                                     \
+    matmul_tile128_w<T, A, 2, 4, 32, 2>(w, wd, x, y, ctl, p);                                     \
   }
 MMXM(1, 0)
 MMXM(1, 1)
@@ -1470,7 +1646,7 @@ MMXM(2, 1)
   extern "C" __global__ __launch_bounds__(256) void matmul_xms__##T##_##A(                         \
       const uint4 *w, const uint16_t *wd, const f16 *x, float *y, const uint32_t *ctl,            \
       Segments<MatmulPush> m) {                                                                   \
-    matmul_tile128_w<T, A, 2, 4, 32, 1, 0, 1>(w, wd, x, y, ctl, m.p[0], nullptr, nullptr, 1, 0, 1, m); \
+    matmul_tile128_w<T, A, 2, 4, 32, 2, 0, 1>(w, wd, x, y, ctl, m.p[0], nullptr, nullptr, 1, 0, 1, m); \
   }
 MMXMS(1, 0)
 MMXMS(1, 1)

@@ -577,7 +577,9 @@ SK_DEV void matvec_q4k_ks_body(const uint4 *__restrict__ w, const float *x, floa
 //   * the rows' weighted sum is added to the residual in moe_combine's order
 //     (moe_combine.comp:16-27), so the residual is bit-identical to the two launches;
 //   * all the workgroup's weights are in flight at once: 16 groups of 16 lanes, group g
-//     taking slot g % 8 and rows g / 8, g / 8 + 2, ...  (n_used <= 8, n_in <= 1024).
+//     taking slot g % 8 and rows g / 8, g / 8 + 2, ...  (n_used <= 8, n_in <= 1024), and
+//     with them every header (one per thread), the routing weights and the residual rows:
+//     one dependent round trip after the ids.
 // The per-slot down rows are not written (nothing after moe_combine reads them).
 // ---------------------------------------------------------------------------------------
 template <int DR>
@@ -585,15 +587,33 @@ SK_DEV void matvec_q4k_dcomb_body(const uint4 *__restrict__ w, float *a, const u
                                   const MatvecPushComb &p, uint32_t bx) {
   constexpr int SLOTS = 8, CHU = 32, CH_SUP = CHU / 8, LPR = 16, S = CHU / LPR;
   static_assert(DR % 2 == 0, "two row sets per slot");
+  static_assert(SLOTS * DR * CH_SUP == 256, "one (slot, row, super-block) header per thread");
   __shared__ float4 xf[SLOTS][8][CHU];
   __shared__ float2 xs[SLOTS][CHU];
   __shared__ float4 sc[SLOTS][DR][CH_SUP][4];
   __shared__ float tot[SLOTS][DR];
+  __shared__ float rw[SLOTS];
   const uint32_t tid = threadIdx.x;
   const uint32_t units = p.n_in >> 5, supers = p.n_in >> 8;
   const uint32_t row0 = bx * DR;
   const uint32_t LO4 = opaque_mask(0x0f0f0f0fu), HI4 = opaque_mask(0xf0f0f0f0u);
 
+  // Everything is loaded before anything is used, so the launch waits for one round trip
+  // after the ids: the slots' activations (which need no ids), then this lane's weights, its
+  // header and the combine's routing weights and residual row.
+  constexpr int XJ = SLOTS * 4 * CHU / 256;  // activation items per thread: slot, unit, quarter
+  float4 va[XJ], vb[XJ];
+#pragma unroll
+  for (int j = 0; j < XJ; j++) {
+    const uint32_t t = tid + 256 * j, sl = t / (4 * CHU), tt = t % (4 * CHU), u = tt >> 2, qq = tt & 3;
+    va[j] = vb[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (sl < p.n_used && u < units) {
+      const float *xv = a + p.x_off + sl * p.x_stride;
+      const uint32_t at = (u >> 3) * 256 + ((u >> 1) & 3) * 64 + (u & 1) * 16 + (qq >> 1) * 32 + (qq & 1) * 8;
+      va[j] = *(const float4 *)(xv + at);
+      vb[j] = *(const float4 *)(xv + at + 4);
+    }
+  }
   // this lane's weights: group gi (slot gs, rows gr, gr + 2, ..), lane L of its 16
   const uint32_t gi = tid >> 4, L = tid & 15, gs = gi % SLOTS, gr = gi / SLOTS;
   const bool live = gs < p.n_used;
@@ -609,32 +629,31 @@ SK_DEV void matvec_q4k_dcomb_body(const uint4 *__restrict__ w, float *a, const u
       if (live && i < units) q[k][st] = load_nt(w + p.o0 + (size_t)(gbase + row) * units + i);
     }
   }
-  // stage every slot's activations (items: slot, unit, quarter) and decode the headers
+  // this thread's header: slot hs, row hr, super-block hb
+  const uint32_t hs = tid / (DR * CH_SUP), hr = (tid / CH_SUP) % DR, hb = tid % CH_SUP;
+  const bool hlive = hs < p.n_used && hb < supers;
+  uint4 h = make_uint4(0, 0, 0, 0);
+  if (hlive)
+    h = load_nt(w + p.o1 + (size_t)(ids[p.ids_off + hs] * p.n_out + min(row0 + hr, p.n_out - 1)) * supers + hb);
+  const bool owner = tid < (uint32_t)DR && row0 + tid < p.n_out;  // combines row row0 + tid
+  const float res = owner ? a[p.res_off + row0 + tid] : 0.0f;
+  if (tid < SLOTS) rw[tid] = tid < p.n_used ? a[p.w_off + tid] : 0.0f;
+
+  // stage every slot's activations and decode the headers (zero products past the last
+  // super-block and for absent slots)
 #pragma unroll
-  for (int j = 0; j < SLOTS * 4 * CHU / 256; j++) {
+  for (int j = 0; j < XJ; j++) {
     const uint32_t t = tid + 256 * j, sl = t / (4 * CHU), tt = t % (4 * CHU), u = tt >> 2, qq = tt & 3;
-    float4 va = make_float4(0.f, 0.f, 0.f, 0.f), vb = va;
-    if (sl < p.n_used && u < units) {
-      const float *xv = a + p.x_off + sl * p.x_stride;
-      const uint32_t at = (u >> 3) * 256 + ((u >> 1) & 3) * 64 + (u & 1) * 16 + (qq >> 1) * 32 + (qq & 1) * 8;
-      va = *(const float4 *)(xv + at);
-      vb = *(const float4 *)(xv + at + 4);
-    }
-    float sum = sum4(va) + sum4(vb);
+    float sum = sum4(va[j]) + sum4(vb[j]);
     sum += dpp_f<0xb1>(sum);  // + the other quarter of the same half
-    xf[sl][(qq >> 1) * 4 + (qq & 1) * 2][u] = va;
-    xf[sl][(qq >> 1) * 4 + (qq & 1) * 2 + 1][u] = vb;
+    xf[sl][(qq >> 1) * 4 + (qq & 1) * 2][u] = va[j];
+    xf[sl][(qq >> 1) * 4 + (qq & 1) * 2 + 1][u] = vb[j];
     if ((qq & 1) == 0) ((float *)&xs[sl][u])[qq >> 1] = sum;
   }
-  for (uint32_t i = tid; i < (uint32_t)(SLOTS * DR * CH_SUP); i += 256) {
-    const uint32_t sl = i / (DR * CH_SUP), lr = (i / CH_SUP) % DR, sb = i % CH_SUP;
-    if (sl >= p.n_used || sb >= supers) {
+  if (!hlive) {
 #pragma unroll
-      for (int cc = 0; cc < 4; cc++) sc[sl][lr][sb][cc] = make_float4(0.f, 0.f, 0.f, 0.f);
-      continue;
-    }
-    const uint32_t base = ids[p.ids_off + sl] * p.n_out;
-    const uint4 h = load_nt(w + p.o1 + (size_t)(base + min(row0 + lr, p.n_out - 1)) * supers + sb);
+    for (int cc = 0; cc < 4; cc++) sc[hs][hr][hb][cc] = make_float4(0.f, 0.f, 0.f, 0.f);
+  } else {
     const float d = f16_bits_to_f32(h.x & 0xffffu), dmin = f16_bits_to_f32(h.x >> 16);
     const float d16 = d * 0.0625f;
     const uint32_t sw[2] = {h.y & 0x3f3f3f3fu, (h.w & 0x0f0f0f0fu) | ((h.y >> 2) & 0x30303030u)};
@@ -644,7 +663,7 @@ SK_DEV void matvec_q4k_dcomb_body(const uint4 *__restrict__ w, float *a, const u
       const uint32_t sv = sw[cc >> 1] >> (16 * (cc & 1)), mv = mw[cc >> 1] >> (16 * (cc & 1));
       const float s_lo = (float)(sv & 255u), s_hi = (float)((sv >> 8) & 255u);
       const float m_lo = (float)(mv & 255u), m_hi = (float)((mv >> 8) & 255u);
-      sc[sl][lr][sb][cc] = make_float4(d * s_lo, d16 * s_hi, dmin * m_lo, dmin * m_hi);
+      sc[hs][hr][hb][cc] = make_float4(d * s_lo, d16 * s_hi, dmin * m_lo, dmin * m_hi);
     }
   }
   __syncthreads();
@@ -672,11 +691,11 @@ SK_DEV void matvec_q4k_dcomb_body(const uint4 *__restrict__ w, float *a, const u
     if (L == 0) tot[gs][lr] = total;
   }
   __syncthreads();
-  if (tid < (uint32_t)DR && row0 + tid < p.n_out) {
+  if (owner) {
 #pragma clang fp contract(off)
     float sum = 0.0f;
-    for (uint32_t s = 0; s < p.n_used; s++) sum += a[p.w_off + s] * tot[s][tid];
-    a[p.res_off + row0 + tid] += sum;
+    for (uint32_t s = 0; s < p.n_used; s++) sum += rw[s] * tot[s][tid];
+    a[p.res_off + row0 + tid] = res + sum;
   }
 }
 
@@ -1318,27 +1337,25 @@ extern "C" __global__ __launch_bounds__(256) void matvec_q4k_glu__4_0_1_1_16(
   const uint32_t s = segment_of(m, blockIdx.x);
   matvec_q4k_body<4, 0, 1, 1, 16, 3>(w, x, y, ids, segment_push(m, s), blockIdx.x - m.start[s]);
 }
-// moe_route then the experts' gate + up + silu of one decode token in one launch: wave 0 of
-// every workgroup runs moe_route's selection (route.h) on the logits, so each workgroup
-// knows its slot's expert without waiting for another; workgroup (0, 0) also stores the
-// ids and routing weights for the launches after it.  Same ids, weights and outputs, bit
-// for bit, as moe_route then matvec_q4k_glu__4_0_1_1_16.
+// moe_route then the experts' gate + up + silu of one decode token in one launch: every
+// workgroup ranks the logits itself (route_ranked, all four waves), so each knows its slot's
+// expert without waiting for another; workgroup (0, 0) also stores the ids and routing
+// weights for the launches after it.  Same ids, weights and outputs, bit for bit, as
+// moe_route then matvec_q4k_glu__4_0_1_1_16.
 extern "C" __global__ __launch_bounds__(256) void matvec_q4k_glur__4_0_1_1_16(
     const uint4 *w, const float *x, float *y, uint32_t *ids, Segments<MatvecPushGluR> m) {
   __shared__ uint32_t sid[16];
-  __shared__ float swt[16];
+  __shared__ float sval[16];
   const MatvecPushGluR pp = m.p[0];
-  if (threadIdx.x < 64) {
-    RoutePush rp = pp.r;
-    rp.ids_off = 0;
-    rp.weights_off = 0;
-    route_token(y, swt, sid, rp, 0, threadIdx.x);
-    if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x < min(pp.r.n_used, 16u)) {
-      ids[pp.r.ids_off + threadIdx.x] = sid[threadIdx.x];
-      y[pp.r.weights_off + threadIdx.x] = swt[threadIdx.x];
+  route_ranked(y, pp.r, 0, threadIdx.x, sid, sval);
+  if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x < 64) {
+    const uint32_t n_used = min(pp.r.n_used, 16u), t = threadIdx.x;
+    const float wt = route_weight(t < n_used ? sval[t] : 0.0f, n_used);
+    if (t < n_used) {
+      ids[pp.r.ids_off + t] = sid[t];
+      y[pp.r.weights_off + t] = wt;
     }
   }
-  __syncthreads();
   MatvecPushGlu g = pp.g;
   g.ids_off = 0;
   matvec_q4k_body<4, 0, 1, 1, 16, 3>(w, x, y, sid, g, blockIdx.x);

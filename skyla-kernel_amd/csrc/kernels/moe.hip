@@ -9,6 +9,8 @@
 namespace {
 
 constexpr uint32_t MAX_SLOTS = 1024;  // moe_sort.comp:15 (BATCH * n_used <= 1024)
+constexpr uint32_t TILE_MAP = 320;    // words of the tile map before the table (matmul.hip)
+constexpr uint32_t TILE_SLOTS = 32;   // slots per expert tile of the grouped matmuls
 
 struct LogitsPush { uint32_t x_off, router_off, logits_off, n_embd, x_stride; };
 struct SortPush { uint32_t ids_off, table_off, list_off, n_expert, n_used; };
@@ -110,6 +112,9 @@ extern "C" __global__ __launch_bounds__(64) void moe_route(float *a, uint32_t *i
 // e plus the earlier waves' counts of e.  Each wave then ranks its slots 64 at a time in
 // slot order, using ballots to find the lanes that share an expert.  The ids are read once
 // (the list writes go to the same arena, so reads from it could not be hoisted past them).
+// Beside the table it writes the tile map the grouped matmuls launch over, TILE_MAP words
+// before the table: map[0] = the number of (expert, 32-slot tile) pairs, map[1 + i] = pair i
+// as e | z << 16, in expert order (at most n_expert + MAX_SLOTS / 32 pairs, 289 words).
 extern "C" __global__ __launch_bounds__(256) void moe_sort(uint32_t *a, SortPush p) {
   __shared__ uint32_t count[4][256];  // per wave and expert; then that wave's cursor
   __shared__ uint32_t wsum[4];
@@ -130,11 +135,14 @@ extern "C" __global__ __launch_bounds__(256) void moe_sort(uint32_t *a, SortPush
   for (uint32_t j = 0; j < CHUNKS; j++)
     if (mine[j] < n_expert) atomicAdd(&count[wave][mine[j]], 1u);
   __syncthreads();
-  // thread t: expert e = t.  Its total over the waves, the exclusive scan of the totals in
-  // expert order (a wave scan, then the waves' sums), and each wave's cursor.
+  // thread t: expert e = t.  Its total over the waves and its tiles, the exclusive scans of
+  // both in expert order (one scan of tot | tiles << 16: the totals sum to at most 1024 and
+  // the tiles to at most 289, so neither half carries), and each wave's cursor.
   const uint32_t c0 = count[0][t], c1 = count[1][t], c2 = count[2][t], c3 = count[3][t];
   const uint32_t tot = c0 + c1 + c2 + c3;
-  uint32_t incl = tot;
+  const uint32_t tiles = (tot + TILE_SLOTS - 1) / TILE_SLOTS;
+  const uint32_t pk = tot | (tiles << 16);
+  uint32_t incl = pk;
 #pragma unroll
   for (int d = 1; d < 64; d <<= 1) {
     const uint32_t o = __shfl_up(incl, d, 64);
@@ -142,12 +150,16 @@ extern "C" __global__ __launch_bounds__(256) void moe_sort(uint32_t *a, SortPush
   }
   if (lane == 63) wsum[wave] = incl;
   __syncthreads();
-  uint32_t start = incl - tot;
-  for (uint32_t w = 0; w < wave; w++) start += wsum[w];
+  uint32_t first = incl - pk;
+  for (uint32_t w = 0; w < wave; w++) first += wsum[w];
+  const uint32_t start = first & 0xffffu, tile0 = first >> 16;
+  uint32_t *map = a + p.table_off - TILE_MAP;
   if (t < n_expert) {
     a[p.table_off + 2 * t] = tot;
     a[p.table_off + 2 * t + 1] = start;
+    for (uint32_t z = 0; z < tiles; z++) map[1 + tile0 + z] = t | (z << 16);
   }
+  if (t == 0) map[0] = (wsum[0] + wsum[1] + wsum[2] + wsum[3]) >> 16;
   count[0][t] = start;
   count[1][t] = start + c0;
   count[2][t] = start + c0 + c1;

@@ -29,6 +29,16 @@ SK_DEV uint32_t dpp_u(uint32_t v) {
 // maximum (DPP within rows of 16, then two shuffles) and a ballot for the lowest expert
 // holding it.  Lane k keeps round k's choice; the exponentials are computed in parallel
 // and summed in round order, as the reference does.
+// The routing weight of lane t's choice `chosen` (lane k holds round k's logit): exp(v_k - v_0)
+// over the sum of the n_used exponentials, added in round order (moe_route.comp:66-73).
+SK_DEV float route_weight(float chosen, uint32_t n_used) {
+  const float largest = __shfl(chosen, 0, 64);
+  const float e = expf(chosen - largest);
+  float total = 0.0f;
+  for (uint32_t k = 0; k < n_used; k++) total += __shfl(e, (int)k, 64);
+  return e / total;
+}
+
 // This is the selection for token `tok` on one wave (lane t), writing ids[ids_off + ..] and
 // aw[weights_off + ..].
 SK_DEV void route_token(const float *a, float *aw, uint32_t *ids, const RoutePush &p, uint32_t tok,
@@ -75,12 +85,48 @@ SK_DEV void route_token(const float *a, float *aw, uint32_t *ids, const RoutePus
       chosen_idx = idx;
     }
   }
-  const float largest = __shfl(chosen, 0, 64);
-  const float e = expf(chosen - largest);
-  float total = 0.0f;
-  for (uint32_t k = 0; k < n_used; k++) total += __shfl(e, (int)k, 64);
+  const float wt = route_weight(chosen, n_used);
   if (t < n_used) {
     ids[p.ids_off + tok * p.n_used + t] = chosen_idx;
-    aw[p.weights_off + tok * p.n_used + t] = e / total;
+    aw[p.weights_off + tok * p.n_used + t] = wt;
   }
+}
+
+// The same selection by a workgroup of 256 threads, for a kernel whose every workgroup
+// routes for itself before it can load anything.  Expert e's place is the number of experts
+// before it in the order "larger key first, lower index on ties" (all (key, index) pairs are
+// distinct, so the places are 0, 1, ..), and the expert in place k is round k's choice in
+// route_token.  Each (key, ~index) pair is one 64-bit word in LDS; thread t counts the words
+// above expert t % 128's over half of the experts (n_expert <= 128) or expert t's over all of
+// them, with no serial rounds.  Leaves sid[k] = the expert in place k and sval[k] = its logit
+// (as route_token's rounds read it back from the key) for k < n_used, behind a barrier.
+// Needs n_used <= n_expert (the runtime's configuration check).
+SK_DEV void route_ranked(const float *a, const RoutePush &p, uint32_t tok, uint32_t t, uint32_t *sid,
+                         float *sval) {
+  __shared__ uint64_t kk[256];
+  __shared__ uint32_t half[256];
+  const uint32_t n_used = min(p.n_used, 16u);
+  const uint32_t n_expert = min(p.n_expert, 256u);
+  uint32_t key = 0;
+  if (t < n_expert) key = max(order_key(a[p.logits_off + tok * p.n_expert + t]), 1u);
+  kk[t] = ((uint64_t)key << 32) | (uint32_t)~t;
+  __syncthreads();
+  const bool halves = n_expert <= 128;  // wave-uniform: waves 0, 1 take the first half
+  const uint32_t e = halves ? (t & 127) : t;
+  const uint32_t len = halves ? (n_expert + 1) / 2 : n_expert;
+  const uint32_t f0 = halves ? (t >> 7) * len : 0, f1 = min(f0 + len, n_expert);
+  const uint64_t mine = kk[e];
+  uint32_t before = 0;
+#pragma unroll 8
+  for (uint32_t f = f0; f < f1; f++) before += kk[f] > mine ? 1u : 0u;
+  half[t] = before;
+  __syncthreads();
+  if (t < n_expert) {  // with halves, t < 128: thread t + 128 counted the second half
+    const uint32_t place = before + (halves ? half[t + 128] : 0u);
+    if (place < n_used) {
+      sid[place] = t;
+      sval[place] = key_value(key);
+    }
+  }
+  __syncthreads();
 }

@@ -660,8 +660,14 @@ std::vector<Launch> build_launches(skyla_hip_context *ctx, const std::vector<Com
         l.args[4] = (uint32_t)(h_off / 2);  // f16 units
         l.args[8] = a.push[6];
       }
-      l.groups[1] = a.groups[1];
-      l.groups[2] = a.groups[2];
+      // grid.y over moe_sort's tile map: at most sum_e ceil(c_e / 32) <= (S + 31 k) / 32
+      // pairs, S = the slots (the token tiles' 32 columns times the experts used per token)
+      // and k <= min(experts, S) the experts with slots, and at most every expert's every
+      // token tile (an expert takes a token at most once)
+      const uint64_t used = a.push[12] > 1 ? a.push[12] : moe_used;
+      const uint64_t slots = (uint64_t)a.groups[2] * 32 * used, experts = a.groups[1];
+      l.groups[1] = (uint32_t)std::min(experts * a.groups[2], (slots + 31 * std::min(experts, slots)) / 32);
+      l.groups[2] = 1;
       l.xh_buf = 2;
       l.xh_bytes = out.back().xh_bytes;
       out.push_back(std::move(l));

@@ -42,6 +42,9 @@ BATCH = 128
 # What the MoE kernels hold (moe.hip): moe_route keeps 4 logits per lane of one wave and
 # picks at most 16; moe_sort ranks at most 1024 slots (moe_sort.comp:15).
 MOE_MAX_EXPERTS, MOE_MAX_USED, MOE_MAX_SLOTS = 256, 16, 1024
+# moe_sort's tile map of the grouped matmuls, directly before its table: a count and up to
+# MOE_MAX_EXPERTS + MOE_MAX_SLOTS / 32 (expert, 32-slot tile) pairs (moe.hip, matmul.hip)
+MOE_TILE_MAP = 320
 
 
 class DType(IntEnum):
@@ -481,14 +484,15 @@ class MoeRegions:
     table: int
     list: int
     stride: int
+    tiles: int = 0  # the tile map, MOE_TILE_MAP words ending where the table starts
 
 
 class Arena:
     """arena.rs:82-181 without the recurrent-state regions: fixed f32 offsets after 64
     control words, BATCH rows per batched region, and (with a precision) the KV cache
-    buffer of kv.rs.  One region more than the reference: `tokens`, the u32 ids of the
+    buffer of kv.rs.  Two regions more than the reference: `tokens`, the u32 ids of the
     chunk, which the embed kernel gathers rows for (the reference dequantises them on the
-    host into x, engine.rs:100-117)."""
+    host into x, engine.rs:100-117), and the MoE tile map moe_sort writes before its table."""
 
     def __init__(self, ctx: Context, c: Config, max_ctx: int = 64, precision: KvPrecision | None = None):
         self.size = 64
@@ -530,10 +534,12 @@ class Arena:
             if slots > MOE_MAX_SLOTS:
                 raise ValueError(f"{c.n_expert_used} experts x {BATCH} tokens = {slots} slots: moe_sort sorts at "
                                  f"most {MOE_MAX_SLOTS} (moe_sort.comp:15)")
-        self.moe = MoeRegions(
-            logits=single(c.n_expert * BATCH), ids=single(slots), weights=single(slots),
-            gate=single(stride * slots), up=single(stride * slots), down=single(self.s_embd * slots),
-            table=single(2 * c.n_expert), list=single(slots), stride=stride)
+        logits, ids, weights = single(c.n_expert * BATCH), single(slots), single(slots)
+        gate, up, down = single(stride * slots), single(stride * slots), single(self.s_embd * slots)
+        tiles = single(MOE_TILE_MAP)
+        self.moe = MoeRegions(logits=logits, ids=ids, weights=weights, gate=gate, up=up, down=down,
+                              table=single(2 * c.n_expert), list=single(slots), stride=stride, tiles=tiles)
+        assert self.moe.table == tiles + MOE_TILE_MAP
         widest = max([_next64(w) * BATCH for w in (c.n_embd, c.n_head * c.head_dim, c.n_ff)]
                      + [stride * slots])
         self.half = single(widest // 2 + 64)

@@ -29,13 +29,17 @@ def _cfg():
 
 
 class MoeSetup:
-    def __init__(self, ctx):
+    def __init__(self, ctx, router=None, base=None):
+        """Config 4's MoE layer; `router` replaces the seeded router, `base` lends its experts."""
         self.ctx = ctx
         self.c = _cfg()
-        self.router = synth.router(CFG, "router", N_EXPERT, N_EMBD)
-        self.gate = synth.matrix(CFG, "gate_exps", E.DType.Q4K, N_EMBD, N_FF_EXP, N_EXPERT)
-        self.up = synth.matrix(CFG, "up_exps", E.DType.Q4K, N_EMBD, N_FF_EXP, N_EXPERT)
-        self.down = synth.matrix(CFG, "down_exps", E.DType.Q4K, N_FF_EXP, N_EMBD, N_EXPERT)
+        self.router = synth.router(CFG, "router", N_EXPERT, N_EMBD) if router is None else router
+        if base is None:
+            self.gate = synth.matrix(CFG, "gate_exps", E.DType.Q4K, N_EMBD, N_FF_EXP, N_EXPERT)
+            self.up = synth.matrix(CFG, "up_exps", E.DType.Q4K, N_EMBD, N_FF_EXP, N_EXPERT)
+            self.down = synth.matrix(CFG, "down_exps", E.DType.Q4K, N_FF_EXP, N_EMBD, N_EXPERT)
+        else:
+            self.gate, self.up, self.down = base.gate, base.up, base.down
         p = E.Planner(ctx.max_buffer())
         self.router_off = p.table(self.router.reshape(-1))
         self.qg = p.matrix(E.DType.Q4K, N_EMBD, N_FF_EXP, self.gate)
@@ -171,6 +175,12 @@ def test_sort_kernel_matches_stable_counting_sort(ctx, moe):
     assert np.array_equal(lst, want_list)
     # brute force: stable argsort by expert
     assert np.array_equal(lst, np.argsort(ids.reshape(-1), kind="stable"))
+    # the tile map before the table: every (expert, 32-slot tile) pair in expert order
+    counts = np.bincount(ids.reshape(-1), minlength=N_EXPERT)
+    pairs = [e | (z << 16) for e in range(N_EXPERT) for z in range(-(-int(counts[e]) // 32))]
+    tiles = a.u32()[m.tiles: m.tiles + E.MOE_TILE_MAP]
+    assert counts[17] > 32 and tiles[0] == len(pairs)
+    assert list(tiles[1: 1 + len(pairs)]) == pairs
 
 
 def test_combine_kernel_bit_exact(ctx, moe):
@@ -304,6 +314,46 @@ def test_moe_prefill_f16_rows_same_bits(ctx, moe, n_tok, fuse):
         assert rel_l2(d1[~small], d0[~small]) <= 2e-3
 
 
+@pytest.mark.parametrize("n_tok", [128, 45])
+def test_moe_prefill_crowded_experts_same_bits(ctx, moe, n_tok):
+    """Every token routed to the same 8 experts (router rows aligned with a component all
+    the tokens share), so each expert holds every token and the grouped matmuls walk several
+    32-slot tiles of one expert through the tile map (xhalf_moe=1) against the f32-staged
+    tile over every expert times every token tile (xhalf_moe=0): the same bits for gate and
+    up, and for the down rows whose inputs stay below 2^15."""
+    rng = np.random.default_rng(5)
+    common = rng.standard_normal(N_EMBD).astype(np.float32)
+    n = (common + np.float32(0.3) * rng.standard_normal((n_tok, N_EMBD))).astype(np.float32)
+    x0 = synth.activations(CFG, f"crowd-x-{n_tok}", (n_tok, N_EMBD))
+    router = moe.router.copy()
+    chosen = [3, 9, 20, 33, 64, 90, 111, 127]
+    router[chosen] = common / np.float32(np.linalg.norm(common)) * np.float32(0.5)
+    s = MoeSetup(ctx, router=router, base=moe)
+    slots = n_tok * N_USED
+    got = {}
+    try:
+        for xh in ("1", "0"):
+            with tactics(xhalf_moe=xh):
+                s.load(n, x0)
+                s.run_moe(batched=True)
+            a, m = s.a, s.a.moe
+            ids = a.u32()[m.ids: m.ids + slots].reshape(n_tok, N_USED)
+            assert np.all(np.sort(ids, axis=1) == chosen)
+            gate = a.f32()[m.gate: m.gate + slots * m.stride].reshape(slots, m.stride)[:, :N_FF_EXP].copy()
+            down = a.f32()[m.down: m.down + slots * a.s_embd].reshape(slots, a.s_embd)[:, :N_EMBD].copy()
+            got[xh] = (gate, down, a.u32()[m.tiles])
+    finally:
+        s.free()
+    (g1, d1, t1), (g0, d0, _) = got["1"], got["0"]
+    assert t1 == N_USED * -(-n_tok // 32)
+    assert np.array_equal(g1.view(np.uint32), g0.view(np.uint32))
+    small = np.abs(g0).max(axis=1) < 32768.0
+    assert small.any()
+    assert np.array_equal(d1[small].view(np.uint32), d0[small].view(np.uint32))
+    if (~small).any():
+        assert rel_l2(d1[~small], d0[~small]) <= 2e-3
+
+
 def test_moe_decode_expert_variant_choice(ctx, moe):
     """Expert launches run on the variant the runtime picks for them (four waves, 16 lanes
     per row); the layer output equals the engine-requested variants' up to f32 summation
@@ -358,3 +408,54 @@ def test_moe_decode_fused_forms_equal_six_launches(ctx, moe, seed, forms, n_laun
     if not _near_tie(moe.router, n[0]):
         assert list(got[forms][0]) == list(ids)
         assert rel_l2(got[forms][3] - x0[0], out) <= F32
+
+
+def _decode_forms(s, n, x0, forms):
+    """One decode token through the MoE layer on the launch forms `forms` (tactic moe_fuse):
+    launches, ids, routing weights, logits and residual."""
+    with tactics(moe_fuse=forms):
+        s.load(n, x0)
+
+        def body(r):
+            E.Graph(r, s.k, s.a, s.c, False).moe(s.qg, s.qu, s.qd, s.router_off)
+        rec = s.ctx.record(False, body)
+        launches = rec.launches()
+        s.ctx.replay(rec)
+        rec.free()
+    s.a.buffer.download()
+    a, m = s.a, s.a.moe
+    return (launches, a.u32()[m.ids: m.ids + N_USED].copy(), a.f32()[m.weights: m.weights + N_USED].copy(),
+            a.f32()[m.logits: m.logits + N_EXPERT].copy(), s.rows(a.x, a.s_embd, 1, N_EMBD)[0].copy())
+
+
+@pytest.mark.parametrize("case", ["top5-and-across-8th", "all-tied"])
+def test_moe_decode_fused_route_ties(ctx, moe, case):
+    """Exact logit ties through the fused route (form 16: every workgroup of the gate/up
+    launch ranks the logits itself) against moe_route's rounds (the six launches): router rows
+    copied so that five experts tie at the top and four more tie across the 8th place, or all
+    128 tie.  The same ids, routing weights, logits and residual, bit for bit, and the ids are
+    the logits' descending order with ties to the lower index."""
+    n = synth.activations(CFG, "tie-n", (1, N_EMBD))
+    x0 = synth.activations(CFG, "tie-x", (1, N_EMBD))
+    router = moe.router.copy()
+    unit = n[0] / np.float32(np.linalg.norm(n[0]))
+    if case == "all-tied":
+        router[:] = router[17]
+        want = list(range(N_USED))
+    else:  # the other logits are below 2.7
+        router[[40, 3, 77, 9, 5]] = unit * np.float32(0.1)     # logit ~4.6
+        router[[101, 60, 20, 100]] = unit * np.float32(0.08)   # logit ~3.6
+        want = [3, 5, 9, 40, 77, 20, 60, 100]
+    s = MoeSetup(ctx, router=router, base=moe)
+    try:
+        fused = _decode_forms(s, n, x0, "26")
+        six = _decode_forms(s, n, x0, "0")
+    finally:
+        s.free()
+    assert (fused[0], six[0]) == (3, 6)
+    for g1, g0 in zip(fused[1:], six[1:]):
+        assert np.array_equal(g1.view(np.uint32), g0.view(np.uint32))
+    logits = fused[3]
+    assert list(fused[1]) == sorted(range(N_EXPERT), key=lambda e: (-float(logits[e]), e))[:N_USED] == want
+    if case == "all-tied":
+        assert np.all(fused[2] == np.float32(1.0 / N_USED))
