@@ -1216,7 +1216,6 @@ SK_DEV void matmul_tile128_w(const uint4 *__restrict__ w, const uint16_t *__rest
     auto stage = [&](uint32_t st, WLds<TYPE, NT> &held, WLds<TYPE, NT> &fill) {
       StageScales<TYPE> ss;
       lds_scales<TYPE>(wrow, hh, ss);
-      const bool next = st + 1 < n_stage;
       load_chunk<KX, XHALF, NT, TN, true>(xn, x, xrow, p.x_off, p.x_stride, kbase + (st + 1) * KC, p.n_in, n_tok);
       wb.load(fill, st0 + st + 2, st + 2 < n_stage);
       constexpr int SPC = KX / 16;
@@ -1244,16 +1243,20 @@ SK_DEV void matmul_tile128_w(const uint4 *__restrict__ w, const uint16_t *__rest
                                                           acc[j], 0, 0, 0);
       }
       __syncthreads();  // every wave is done with this stage's weights and activations
-      if (next) {
-        held.store(held, wl, tid);
-        store_chunk<KX, XHALF, NT, TN>(xs, xn, xexp, kbase + (st + 1) * KC, p.n_in);
-        __syncthreads();
-      }
+      // stored unconditionally (past the last stage: zeros no one reads), and the stage pairs
+      // below run unconditionally, so that on every path the loads a stage waits for are
+      // complete at the loop's back edge; with a branch around either, the compiler waited
+      // at the top of each pair for the weights issued two stages ahead
+      held.store(held, wl, tid);
+      store_chunk<KX, XHALF, NT, TN>(xs, xn, xexp, kbase + (st + 1) * KC, p.n_in);
+      __syncthreads();
     };
-    for (uint32_t st = 0; st < n_stage; st += 2) {
+    uint32_t st = 0;
+    for (; st + 1 < n_stage; st += 2) {
       stage(st, wa, wc);
-      if (st + 1 < n_stage) stage(st + 1, wc, wa);
+      stage(st + 1, wc, wa);
     }
+    if (st < n_stage) stage(st, wa, wc);
   } else {
   WLds<TYPE, NT> wr;
   if constexpr (TYPE == 1) wr.load(wr, w, p, row0, st0, tid, base);
