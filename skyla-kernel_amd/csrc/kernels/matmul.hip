@@ -29,7 +29,7 @@
 namespace {
 
 constexpr int TM = 128;        // rows per workgroup
-constexpr uint32_t TILE_MAP = 320;  // words of moe_sort's tile map before its table (moe.hip)
+constexpr uint32_t TILE_MAP = 640;  // words of moe_sort's tile map before its table (moe.hip)
 constexpr int KC = 256;        // k per LDS stage (one K-quant super-block)
 constexpr int PITCH = KC + 8;  // f16 per staged token row (16 B pad: conflict-free b128)
 
@@ -1117,25 +1117,32 @@ SK_DEV void matmul_tile128_w(const uint4 *__restrict__ w, const uint16_t *__rest
     p.y_stride = pick(&MatmulPush::y_stride);
     rt -= sg == 0 ? 0u : sg == 1 ? segs.start[1] : sg == 2 ? segs.start[2] : segs.start[3];
   }
-  uint32_t e = MOE ? blockIdx.y : 0;
+  uint32_t e = MOE ? blockIdx.y : 0, n_all, lstart;
   if constexpr (MOE == 2) {
-    // grid.y walks moe_sort's tile map (the (expert, 32-slot tile) pairs the chunk has,
-    // TILE_MAP words before the table) instead of every expert times every token tile
+    // grid.y walks moe_sort's tile map (TILE_MAP words before the table) instead of every
+    // expert times every token tile: the count and this workgroup's entry (e | z << 16,
+    // then the expert's list start | its slot count << 16) are read together, so the slots
+    // are one dependent load away (an entry past the count is never used; the grid stays
+    // within the map: at most 280 entries)
     const uint32_t *map = ctl + p.table_off - TILE_MAP;
-    if (blockIdx.y >= map[0]) return;
-    const uint32_t v = map[1 + blockIdx.y];
-    e = v & 0xffffu;
-    tt = v >> 16;
+    const uint32_t cnt = map[0], va = map[1 + 2 * blockIdx.y], vb = map[2 + 2 * blockIdx.y];
+    if (blockIdx.y >= cnt) return;
+    e = va & 0xffffu;
+    tt = va >> 16;
+    lstart = vb & 0xffffu;
+    n_all = vb >> 16;
+  } else {
+    n_all = MOE ? ctl[p.table_off + 2 * e] : ctl[2];
+    lstart = MOE ? ctl[p.table_off + 2 * e + 1] : 0;
   }
   const uint32_t base = MOE ? e * p.n_out : 0;
   const uint32_t row0 = rt * TM;
-  const uint32_t n_all = MOE ? ctl[p.table_off + 2 * e] : ctl[2];
   const uint32_t col0 = tt * TN;
   if (col0 >= n_all) return;
   const uint32_t n_tok = min(n_all - col0, (uint32_t)TN);
   if (tid < TN) {
     const uint32_t i = min(tid, n_tok - 1);
-    const uint32_t slot = MOE ? ctl[p.list_off + ctl[p.table_off + 2 * e + 1] + col0 + i] : col0 + i;
+    const uint32_t slot = MOE ? ctl[p.list_off + lstart + col0 + i] : col0 + i;
     xrow[tid] = MOE ? slot / p.x_div : slot;
     yrow[tid] = slot;
   }
@@ -1633,7 +1640,7 @@ MMH(2, 1)
 
 // Expert groups (128 x 32 tiles, four waves) on the f16 rows x_half_rows wrote: the rows of
 // the launch's inputs (tokens for gate and up, slots for down), no K split.  MOE = 2: grid
-// (row tiles, at least the tile map's pairs, 1), grid.y indexing moe_sort's tile map.
+// (row tiles, at least the tile map's entries, 1), grid.y indexing moe_sort's tile map.
 #define MMXM(T, A)                                                                                \
   extern "C" __global__ __launch_bounds__(256) void matmul_xm__##T##_##A(                          \
       const uint4 *w, const uint16_t *wd, const f16 *x, float *y, const uint32_t *ctl, MatmulPush p) { \

@@ -9,7 +9,7 @@
 namespace {
 
 constexpr uint32_t MAX_SLOTS = 1024;  // moe_sort.comp:15 (BATCH * n_used <= 1024)
-constexpr uint32_t TILE_MAP = 320;    // words of the tile map before the table (matmul.hip)
+constexpr uint32_t TILE_MAP = 640;    // words of the tile map before the table (matmul.hip)
 constexpr uint32_t TILE_SLOTS = 32;   // slots per expert tile of the grouped matmuls
 
 struct LogitsPush { uint32_t x_off, router_off, logits_off, n_embd, x_stride; };
@@ -113,8 +113,10 @@ extern "C" __global__ __launch_bounds__(64) void moe_route(float *a, uint32_t *i
 // slot order, using ballots to find the lanes that share an expert.  The ids are read once
 // (the list writes go to the same arena, so reads from it could not be hoisted past them).
 // Beside the table it writes the tile map the grouped matmuls launch over, TILE_MAP words
-// before the table: map[0] = the number of (expert, 32-slot tile) pairs, map[1 + i] = pair i
-// as e | z << 16, in expert order (at most n_expert + MAX_SLOTS / 32 pairs, 289 words).
+// before the table: map[0] = the number of (expert, 32-slot tile) entries, and entry i, in
+// expert order, as map[1 + 2i] = e | z << 16 and map[2 + 2i] = the expert's list start |
+// its slot count << 16 (at most 280 entries: the sum of ceil(c_e / 32) over the experts
+// with slots is at most (MAX_SLOTS + 31 * 256) / 32).
 extern "C" __global__ __launch_bounds__(256) void moe_sort(uint32_t *a, SortPush p) {
   __shared__ uint32_t count[4][256];  // per wave and expert; then that wave's cursor
   __shared__ uint32_t wsum[4];
@@ -157,7 +159,10 @@ extern "C" __global__ __launch_bounds__(256) void moe_sort(uint32_t *a, SortPush
   if (t < n_expert) {
     a[p.table_off + 2 * t] = tot;
     a[p.table_off + 2 * t + 1] = start;
-    for (uint32_t z = 0; z < tiles; z++) map[1 + tile0 + z] = t | (z << 16);
+    for (uint32_t z = 0; z < tiles; z++) {
+      map[1 + 2 * (tile0 + z)] = t | (z << 16);
+      map[2 + 2 * (tile0 + z)] = start | (tot << 16);
+    }
   }
   if (t == 0) map[0] = (wsum[0] + wsum[1] + wsum[2] + wsum[3]) >> 16;
   count[0][t] = start;

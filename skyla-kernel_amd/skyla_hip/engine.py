@@ -43,8 +43,8 @@ BATCH = 128
 # picks at most 16; moe_sort ranks at most 1024 slots (moe_sort.comp:15).
 MOE_MAX_EXPERTS, MOE_MAX_USED, MOE_MAX_SLOTS = 256, 16, 1024
 # moe_sort's tile map of the grouped matmuls, directly before its table: a count and up to
-# MOE_MAX_EXPERTS + MOE_MAX_SLOTS / 32 (expert, 32-slot tile) pairs (moe.hip, matmul.hip)
-MOE_TILE_MAP = 320
+# 280 two-word (expert, 32-slot tile) entries (moe.hip, matmul.hip)
+MOE_TILE_MAP = 640
 
 
 class DType(IntEnum):

@@ -177,10 +177,12 @@ def test_sort_kernel_matches_stable_counting_sort(ctx, moe):
     assert np.array_equal(lst, np.argsort(ids.reshape(-1), kind="stable"))
     # the tile map before the table: every (expert, 32-slot tile) pair in expert order
     counts = np.bincount(ids.reshape(-1), minlength=N_EXPERT)
-    pairs = [e | (z << 16) for e in range(N_EXPERT) for z in range(-(-int(counts[e]) // 32))]
+    starts = np.concatenate([[0], np.cumsum(counts)[:-1]])
+    entries = [(e | (z << 16), int(starts[e]) | (int(counts[e]) << 16))
+               for e in range(N_EXPERT) for z in range(-(-int(counts[e]) // 32))]
     tiles = a.u32()[m.tiles: m.tiles + E.MOE_TILE_MAP]
-    assert counts[17] > 32 and tiles[0] == len(pairs)
-    assert list(tiles[1: 1 + len(pairs)]) == pairs
+    assert counts[17] > 32 and tiles[0] == len(entries)
+    assert list(tiles[1: 1 + 2 * len(entries)]) == [w for en in entries for w in en]
 
 
 def test_combine_kernel_bit_exact(ctx, moe):
