@@ -96,12 +96,24 @@ extern "C" __global__ __launch_bounds__(256) void moe_logits_t(const float *w, c
   }
 }
 
-// moe_route: one wave per token; tokens at or beyond ctl[2] do nothing.
-extern "C" __global__ __launch_bounds__(64) void moe_route(float *a, uint32_t *ids, RoutePush p) {
+// moe_route (moe_route.comp:23-74): one workgroup of four waves per token ranks its logits
+// (route_ranked), then wave 0 computes the routing weights; tokens at or beyond ctl[2] do
+// nothing.
+extern "C" __global__ __launch_bounds__(256) void moe_route(float *a, uint32_t *ids, RoutePush p) {
+  __shared__ uint32_t sid[16];
+  __shared__ float sval[16];
   const uint32_t tok = blockIdx.y;
   const uint32_t n_tok = __builtin_bit_cast(uint32_t, a[2]);
   if (tok >= n_tok) return;
-  route_token(a, a, ids, p, tok, threadIdx.x);
+  route_ranked(a, p, tok, threadIdx.x, sid, sval);
+  if (threadIdx.x < 64) {
+    const uint32_t n_used = min(p.n_used, 16u), t = threadIdx.x;
+    const float wt = route_weight(t < n_used ? sval[t] : 0.0f, n_used);
+    if (t < n_used) {
+      ids[p.ids_off + tok * p.n_used + t] = sid[t];
+      a[p.weights_off + tok * p.n_used + t] = wt;
+    }
+  }
 }
 
 // moe_sort (moe_sort.comp:21-55): slot s = tok * n_used + k is routed to ids[s].  Writes

@@ -146,7 +146,7 @@ const KernelInfo kKernels[] = {
     {"matvec_q4k_glun", 4, 13, 5, 5, 0, true, true},  // the same after the FFN RMSNorm
     {"matmul", 5, 13, 3, 4, -1, false, false},
     {"moe_logits", 3, 5, 0, 0, -1, false, false},
-    {"moe_route", 2, 5, 0, 0, -1, false, false, 64},  // one wave per token
+    {"moe_route", 2, 5, 0, 0, -1, false, false, 256},  // one workgroup per token
     {"moe_sort", 1, 5, 0, 0, -1, false, false},
     {"moe_combine", 1, 6, 0, 0, -1, false, false},
     {"silu_mul", 2, 4, 0, 0, -1, false, false},

@@ -39,8 +39,8 @@ MAX_SPLITS = 4096       # splits the attention merge weighs in LDS (kernels/atte
 # then span only those splits; the arena's own count is the last bucket).
 SPLIT_BUCKETS = (1, 16, 64, 256)
 BATCH = 128
-# What the MoE kernels hold (moe.hip): moe_route keeps 4 logits per lane of one wave and
-# picks at most 16; moe_sort ranks at most 1024 slots (moe_sort.comp:15).
+# What the MoE kernels hold (moe.hip): moe_route ranks at most 256 logits, one per thread of
+# its workgroup, and picks at most 16; moe_sort ranks at most 1024 slots (moe_sort.comp:15).
 MOE_MAX_EXPERTS, MOE_MAX_USED, MOE_MAX_SLOTS = 256, 16, 1024
 # moe_sort's tile map of the grouped matmuls, directly before its table: a count and up to
 # 280 two-word (expert, 32-slot tile) entries (moe.hip, matmul.hip)
