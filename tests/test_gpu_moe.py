@@ -461,3 +461,53 @@ def test_moe_decode_fused_route_ties(ctx, moe, case):
     assert list(fused[1]) == sorted(range(N_EXPERT), key=lambda e: (-float(logits[e]), e))[:N_USED] == want
     if case == "all-tied":
         assert np.all(fused[2] == np.float32(1.0 / N_USED))
+
+
+@pytest.mark.parametrize("n_expert", [256, 160])
+def test_route_and_sort_past_128_experts(ctx, moe, n_expert):
+    """moe_route and moe_sort with more experts than the 128 of config 4 (the engine takes up to
+    256): the route's ranking then counts every expert per thread instead of two halves, and
+    the sort's counts span more than half of its LDS rows.  Ids in the logits' descending order
+    with ties to the lower index (brute force), weights as the softmax over the chosen,
+    the sort's table and list against the oracle, and its tile map against the counts."""
+    c = E.Config(n_embd=N_EMBD, n_ff=64, n_expert=n_expert, n_expert_used=N_USED, n_ff_expert=N_FF_EXP)
+    arena = E.Arena(ctx, c)
+    try:
+        k = E.Kernels(ctx, moe.weights, arena.buffer)
+        m = arena.moe
+        n_tok = 128
+        g = np.random.default_rng(n_expert)
+        logits = g.standard_normal((n_tok, n_expert)).astype(np.float32)
+        logits[0, :] = 1.0                                   # all tied: experts 0..7
+        logits[1, [n_expert - 1, 130, 7, 200 % n_expert]] = 9.0  # a tie at the top past expert 128
+        logits[2, :] = -1.0
+        logits[2, n_expert - 3:] = 2.0                        # the top three are the last experts
+        f = arena.f32()
+        f[m.logits: m.logits + logits.size] = logits.reshape(-1)
+        arena.set_ctl(0, 0, n_tok)
+        arena.buffer.upload()
+        _dispatch(ctx, k.route, [1, n_tok, 1], [m.logits, m.ids, m.weights, n_expert, N_USED])
+        _dispatch(ctx, k.sort, [1, 1, 1], [m.ids, m.table, m.list, n_expert, N_USED])
+        arena.buffer.download()
+        ids = arena.u32()[m.ids: m.ids + n_tok * N_USED].reshape(n_tok, N_USED).copy()
+        w = arena.f32()[m.weights: m.weights + n_tok * N_USED].reshape(n_tok, N_USED)
+        for t in range(n_tok):
+            order = sorted(range(n_expert), key=lambda e: (-float(logits[t, e]), e))[:N_USED]
+            assert list(ids[t]) == order, t
+            v = logits[t, order].astype(np.float64)
+            want = np.exp(v - v[0]) / np.exp(v - v[0]).sum()
+            assert np.allclose(w[t], want, rtol=2e-6, atol=1e-7), t
+        table = arena.u32()[m.table: m.table + 2 * n_expert].reshape(n_expert, 2)
+        lst = arena.u32()[m.list: m.list + ids.size]
+        want_table, want_list = so.moe_sort(ids.reshape(-1), n_expert)
+        assert np.array_equal(table, want_table)
+        assert np.array_equal(lst, want_list)
+        counts = np.bincount(ids.reshape(-1), minlength=n_expert)
+        starts = np.concatenate([[0], np.cumsum(counts)[:-1]])
+        entries = [(e | (z << 16), int(starts[e]) | (int(counts[e]) << 16))
+                   for e in range(n_expert) for z in range(-(-int(counts[e]) // 32))]
+        tiles = arena.u32()[m.tiles: m.tiles + E.MOE_TILE_MAP]
+        assert tiles[0] == len(entries)
+        assert list(tiles[1: 1 + 2 * len(entries)]) == [wd for en in entries for wd in en]
+    finally:
+        arena.buffer.free()
