@@ -1099,6 +1099,16 @@ SK_DEV void matmul_tile128_w(const uint4 *__restrict__ w, const uint16_t *__rest
     sp = MOE ? 0 : rem / Z;
     kt = rt * Z + tt;
   }
+  // MOE = 2: the tile map entry (grid.y, a multiple of 8).  The XCDs take workgroups
+  // round-robin by linear id, so ids of one residue mod 8 walk all the row tiles of one entry
+  // before the next: every row tile of an entry (the same slots' activation rows, in every
+  // segment) runs on one XCD and reads the rows through its L2 once
+  uint32_t ent = blockIdx.y;
+  if constexpr (MOE == 2) {
+    const uint32_t lin = blockIdx.x + gridDim.x * blockIdx.y, k8 = lin / 8;
+    rt = k8 % gridDim.x;
+    ent = (k8 / gridDim.x) * 8 + lin % 8;
+  }
   MatmulPush p = p0;
   if constexpr (SEG) {  // kt stays the launch-wide tile index (ws and cnt span every segment)
     // field by field, with the (wave-uniform) segment in an SGPR: selecting whole push
@@ -1125,8 +1135,8 @@ SK_DEV void matmul_tile128_w(const uint4 *__restrict__ w, const uint16_t *__rest
     // are one dependent load away (an entry past the count is never used; the grid stays
     // within the map: at most 280 entries)
     const uint32_t *map = ctl + p.table_off - TILE_MAP;
-    const uint32_t cnt = map[0], va = map[1 + 2 * blockIdx.y], vb = map[2 + 2 * blockIdx.y];
-    if (blockIdx.y >= cnt) return;
+    const uint32_t cnt = map[0], va = map[1 + 2 * ent], vb = map[2 + 2 * ent];
+    if (ent >= cnt) return;
     e = va & 0xffffu;
     tt = va >> 16;
     lstart = vb & 0xffffu;

@@ -667,9 +667,10 @@ std::vector<Launch> build_launches(skyla_hip_context *ctx, const std::vector<Com
       const uint64_t used = a.push[12] > 1 ? a.push[12] : moe_used;
       const uint64_t slots = (uint64_t)a.groups[2] * 32 * used, experts = a.groups[1];
       // (at most 280 with 256 experts and 1024 slots, the engine's limits; the map's 640 words
-      // hold 319 entries, which bounds what a workgroup reads in any case)
-      l.groups[1] = (uint32_t)std::min({experts * a.groups[2], (slots + 31 * std::min(experts, slots)) / 32,
-                                        (uint64_t)319});
+      // hold 319 entries, which bounds what a workgroup reads in any case), rounded up to a
+      // multiple of 8 for the tiles' XCD-aware order (the entries past the count return)
+      const uint64_t bound = std::min(experts * a.groups[2], (slots + 31 * std::min(experts, slots)) / 32);
+      l.groups[1] = (uint32_t)std::min<uint64_t>((bound + 7) & ~7ull, 312);
       l.groups[2] = 1;
       l.xh_buf = 2;
       l.xh_bytes = out.back().xh_bytes;

@@ -241,3 +241,26 @@ def test_expert_prepass_rows(n_tok, used, n_expert):
         n_in = 2048
         last = h_off // 2 + int(xrow.max()) * n_in + n_in  # f16 units, end of the last row read
         assert last <= (h_off + rows * n_in * 2) // 2      # inside the workspace region
+
+
+def expert_grid(rt_n: int, y: int):
+    """matmul_tile128_w, MOE = 2 (expert tiles over moe_sort's tile map): (row tile, map entry,
+    XCD = linear id mod 8) of every workgroup of grid (rt_n, y, 1)."""
+    lin = np.arange(rt_n * y, dtype=np.int64)
+    k8 = lin // 8
+    return k8 % rt_n, (k8 // rt_n) * 8 + lin % 8, lin % 8
+
+
+@pytest.mark.parametrize("rt_n", [6, 12, 16, 5])
+@pytest.mark.parametrize("bound", [1, 8, 150, 156, 280])
+def test_expert_grid_order(rt_n, bound):
+    """The runtime's grid.y for expert tiles (the map bound rounded up to a multiple of 8, at
+    most 312 entries of the map's 319) and the tile's XCD-aware order: every (row tile,
+    entry) exactly once, and all the row tiles of an entry on one XCD (one residue mod 8)."""
+    y = min((bound + 7) // 8 * 8, 312)
+    assert y % 8 == 0 and y >= min(bound, 312)
+    rt, ent, xcd = expert_grid(rt_n, y)
+    assert rt.max() < rt_n and ent.max() < y
+    assert np.array_equal(np.sort(rt * y + ent), np.arange(rt_n * y))
+    for e in range(y):
+        assert np.unique(xcd[ent == e]).size == 1, e
