@@ -167,16 +167,20 @@ extern "C" __global__ __launch_bounds__(256) void moe_sort(uint32_t *a, SortPush
   uint32_t first = incl - pk;
   for (uint32_t w = 0; w < wave; w++) first += wsum[w];
   const uint32_t start = first & 0xffffu, tile0 = first >> 16;
-  uint32_t *map = a + p.table_off - TILE_MAP;
+  // the map only where the arena has room for it before the table (a caller's own layout
+  // may put the table first; the runtime then keeps the grouped matmuls off the map)
+  const bool has_map = p.table_off >= TILE_MAP;
+  uint32_t *map = a + (has_map ? p.table_off - TILE_MAP : 0u);
   if (t < n_expert) {
     a[p.table_off + 2 * t] = tot;
     a[p.table_off + 2 * t + 1] = start;
-    for (uint32_t z = 0; z < tiles; z++) {
-      map[1 + 2 * (tile0 + z)] = t | (z << 16);
-      map[2 + 2 * (tile0 + z)] = start | (tot << 16);
-    }
+    if (has_map)
+      for (uint32_t z = 0; z < tiles; z++) {
+        map[1 + 2 * (tile0 + z)] = t | (z << 16);
+        map[2 + 2 * (tile0 + z)] = start | (tot << 16);
+      }
   }
-  if (t == 0) map[0] = (wsum[0] + wsum[1] + wsum[2] + wsum[3]) >> 16;
+  if (t == 0 && has_map) map[0] = (wsum[0] + wsum[1] + wsum[2] + wsum[3]) >> 16;
   count[0][t] = start;
   count[1][t] = start + c0;
   count[2][t] = start + c0 + c1;

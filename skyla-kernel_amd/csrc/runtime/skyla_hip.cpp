@@ -589,9 +589,10 @@ std::vector<Launch> build_launches(skyla_hip_context *ctx, const std::vector<Com
     // gate/up launch's x_div gives
     if (a.kind == Command::Dispatch && a.name == "matmul" && a.push.size() == 13 && a.groups[1] > 1 && a.push[12] > 1)
       moe_used = a.push[12];
+    // (the tile map, 640 words before the table, exists only with table_off >= 640: moe.hip)
     if (xhalf && moe_xh && a.hxm_fn && !a.segmented && a.push.size() == 13 && a.bufs.size() == 5 && a.groups[1] > 1 &&
         a.push[6] % 256 == 0 && a.push[6] <= 12288 && a.push[4] % 4 == 0 && a.push[8] % 4 == 0 &&
-        (a.push[12] > 1 || moe_used > 1)) {
+        a.push[10] >= 640 && (a.push[12] > 1 || moe_used > 1)) {
       const uint32_t per_token = a.push[12] > 1 ? 1u : moe_used;
       const uint32_t rows = a.groups[2] * 32 * per_token;  // token tiles of 32: the chunk's tokens
       const uint64_t h_off = ((uint64_t)rows * 4 + 255) & ~(uint64_t)255;

@@ -511,3 +511,30 @@ def test_route_and_sort_past_128_experts(ctx, moe, n_expert):
         assert list(tiles[1: 1 + 2 * len(entries)]) == [wd for en in entries for wd in en]
     finally:
         arena.buffer.free()
+
+
+def test_sort_without_room_for_the_tile_map(ctx, moe):
+    """moe_sort with its table within the first 640 words of the arena (a layout of the
+    reference's own, no room for the tile map before it): the table and list as the oracle's,
+    and no word below the table written (the map is skipped, not written before the arena)."""
+    arena = E.Arena(ctx, _cfg())
+    try:
+        k = E.Kernels(ctx, moe.weights, arena.buffer)
+        m = arena.moe
+        n_tok, table_off = 100, 64
+        g = np.random.default_rng(3)
+        ids = np.stack([g.choice(N_EXPERT, N_USED, replace=False) for _ in range(n_tok)]).astype(np.uint32)
+        u = arena.u32()
+        u[: m.ids] = np.arange(m.ids, dtype=np.uint32) * np.uint32(2654435761)  # a pattern below the table
+        u[m.ids: m.ids + ids.size] = ids.reshape(-1)
+        arena.set_ctl(0, 0, n_tok)
+        before = arena.u32()[:table_off].copy()
+        arena.buffer.upload()
+        _dispatch(ctx, k.sort, [1, 1, 1], [m.ids, table_off, m.list, N_EXPERT, N_USED])
+        arena.buffer.download()
+        want_table, want_list = so.moe_sort(ids.reshape(-1), N_EXPERT)
+        assert np.array_equal(arena.u32()[table_off: table_off + 2 * N_EXPERT].reshape(N_EXPERT, 2), want_table)
+        assert np.array_equal(arena.u32()[m.list: m.list + ids.size], want_list)
+        assert np.array_equal(arena.u32()[:table_off], before)
+    finally:
+        arena.buffer.free()
