@@ -548,31 +548,12 @@ extern "C" __global__ __launch_bounds__(256) void rmsnorm(const float *w, float 
   if (tok >= ctl[2]) return;
   const uint32_t x = p.x_off + tok * p.stride, y = p.y_off + tok * p.stride;
   if (((x | y | p.w_off | p.n) & 3u) == 0 && p.n <= 4096) {
-    const uint32_t n4 = p.n >> 2;
-    float4 xv[4], wv[4];
-    float ss = 0.0f;
+    float4 yv[4];
+    norm_row4(a + x, w + p.w_off, p.n, p.eps, yv);
 #pragma unroll
     for (int k = 0; k < 4; k++) {
       const uint32_t i = t + 256 * k;
-      xv[k] = wv[k] = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (i < n4) {
-        xv[k] = ((const float4 *)(a + x))[i];
-        wv[k] = ((const float4 *)(w + p.w_off))[i];
-      }
-    }
-#pragma unroll
-    for (int k = 0; k < 4; k++) ss += ((xv[k].x * xv[k].x + xv[k].y * xv[k].y) + xv[k].z * xv[k].z) + xv[k].w * xv[k].w;
-    ss = wave_sum(ss);
-    if ((t & 63) == 0) part[t >> 6] = ss;
-    __syncthreads();
-    const float total = ((part[0] + part[1]) + part[2]) + part[3];
-    const float r = 1.0f / sqrtf(total / (float)p.n + p.eps);
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-      const uint32_t i = t + 256 * k;
-      if (i < n4)
-        ((float4 *)(a + y))[i] = make_float4(xv[k].x * r * wv[k].x, xv[k].y * r * wv[k].y, xv[k].z * r * wv[k].z,
-                                             xv[k].w * r * wv[k].w);
+      if (i < (p.n >> 2)) ((float4 *)(a + y))[i] = yv[k];
     }
     return;
   }

@@ -82,6 +82,37 @@ SK_DEV float lane_sum(float v) {
 
 SK_DEV uint32_t ctl_word(const uint32_t *ctl, uint32_t i) { return ctl[i]; }
 
+// rmsnorm's row (rmsnorm.comp; ops.rs:1-16) of n <= 4096 values at 16-byte aligned x and w,
+// 256 threads: thread t reads values 4 (t + 256 k), k < 4, of x and w as float4 (all loads in
+// flight together) and gets y = x * r * w there (zeros past n), r = 1 / sqrt(mean(x^2) + eps),
+// the sums of squares per wave added in wave order.  One workgroup barrier.
+SK_DEV void norm_row4(const float *xr, const float *wr, uint32_t n, float eps, float4 (&y)[4]) {
+#pragma clang fp contract(off)
+  __shared__ float part[4];
+  const uint32_t t = threadIdx.x, n4 = n >> 2;
+  float4 xv[4], wv[4];
+  float ss = 0.0f;
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    const uint32_t i = t + 256 * k;
+    xv[k] = wv[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (i < n4) {
+      xv[k] = ((const float4 *)xr)[i];
+      wv[k] = ((const float4 *)wr)[i];
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < 4; k++) ss += ((xv[k].x * xv[k].x + xv[k].y * xv[k].y) + xv[k].z * xv[k].z) + xv[k].w * xv[k].w;
+  ss = group_sum<64>(ss);
+  if ((t & 63) == 0) part[t >> 6] = ss;
+  __syncthreads();
+  const float total = ((part[0] + part[1]) + part[2]) + part[3];
+  const float r = 1.0f / sqrtf(total / (float)n + eps);
+#pragma unroll
+  for (int k = 0; k < 4; k++)
+    y[k] = make_float4(xv[k].x * r * wv[k].x, xv[k].y * r * wv[k].y, xv[k].z * r * wv[k].z, xv[k].w * r * wv[k].w);
+}
+
 // ---------------------------------------------------------------------------------------
 // f32 products of exact integer quants (the decode matvecs, matvec.hip).
 // ---------------------------------------------------------------------------------------

@@ -1853,6 +1853,35 @@ extern "C" __global__ __launch_bounds__(256) void silu_half_rows(float *a, uint3
   store_half_row(v, out, p.h_off, p.n_in, t);
 }
 
+// rmsnorm (rmsnorm.comp; ops.rs:1-16) on the rows a dense matmul reads next, with that
+// matmul's f16 row prepass in the same launch: token row tok (tok < ctl[2]) of x becomes
+// y = x * r * w in rmsnorm's expression (the same f32 values, written to y_off as rmsnorm
+// writes them), and its f16 row and exponent go to the workspace as x_half_rows writes them.
+// The runtime uses it only for rows of at most 4096 values with x_off, y_off, w_off, n and
+// stride multiples of 4 (rmsnorm's float4 path).  Grid [1, tokens, 1], as rmsnorm's.
+struct NormHalfPush {
+  uint32_t x_off, w_off, y_off, n;
+  float eps;
+  uint32_t stride, h_off;
+};
+extern "C" __global__ __launch_bounds__(256) void rmsnorm_half_rows(const float *w, float *a, uint32_t *out,
+                                                                    const uint32_t *ctl, NormHalfPush p) {
+  const uint32_t tok = blockIdx.y, t = threadIdx.x;
+  if (tok >= ctl[2]) return;
+  float4 v[HALF_ROW_V / 4];
+#pragma unroll
+  for (int i = 4; i < HALF_ROW_V / 4; i++) v[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+  float4 y4[4];
+  norm_row4(a + p.x_off + tok * p.stride, w + p.w_off, p.n, p.eps, y4);
+  float4 *yr = (float4 *)(a + p.y_off + tok * p.stride);
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    v[k] = y4[k];
+    if (t + 256 * k < (p.n >> 2)) yr[t + 256 * k] = y4[k];
+  }
+  store_half_row(v, out, p.h_off, p.n, tok);
+}
+
 // Workspace of skyla_hip_dispatch_noalloc, the entry point that allocates nothing: the K
 // split's f32 partial tiles (SCRATCH_TILES of 128 x 128), then its per-tile arrival
 // counters (SCRATCH_COUNTERS).  A K-split launch holds at most 256 partial tiles (row tiles

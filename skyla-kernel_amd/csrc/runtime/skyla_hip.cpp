@@ -84,6 +84,8 @@ const Tactic kTactics[] = {
     {"xhalf", "1", "f16 row prepass for matmuls on f32 rows: 1 four-wave tile where it fits, 4 without "
                    "the balanced K halves, 8 eight-wave tile throughout, 0 the tile's own f32 staging"},
     {"xhalf_moe", "1", "expert-group matmuls on f32 rows take the f16 row prepass (0: the tile's own f32 staging)"},
+    {"xhalf_join", "1", "a dense matmul's f16 row prepass runs in the rmsnorm or silu_mul launch that writes its "
+                        "rows (0: a launch of its own)"},
     {"dl", "1", "matmul tiles with their operands loaded straight into LDS (0: register-staged)"},
     {"merge_t", "1", "batched attention merge as one wave per (head, token) (0: 1024-thread form)"},
     {"nograph", "0", "1: recordings replay as direct launches instead of one HIP graph (kernel traces)"},
@@ -193,6 +195,8 @@ struct skyla_hip_context {
   hipFunction_t x_half_rows = nullptr;  // f16 row prepass of dense K-quant matmuls (matmul.hip)
   hipFunction_t silu_half_rows = nullptr;  // silu_mul with the expert down projection's prepass
   hipFunction_t silu_mul = nullptr;        // (moe.hip): the launch it replaces
+  hipFunction_t rmsnorm_half_rows = nullptr;  // rmsnorm with a dense matmul's prepass (matmul.hip)
+  hipFunction_t rmsnorm = nullptr;            // (attention.hip): the launch it replaces
 };
 
 struct HostFree {
@@ -565,6 +569,7 @@ std::vector<Launch> build_launches(skyla_hip_context *ctx, const std::vector<Com
   const bool x4 = xh != "8";       // 8: the eight-wave tile throughout
   const bool balance = xh != "4";  // 4: the plain grid
   const bool moe_xh = tactic_on("xhalf_moe");
+  const bool join = tactic_on("xhalf_join");
   uint32_t moe_used = 0;  // experts used per token: the x_div of the last expert gate/up matmul
   std::vector<Launch> out;
   std::vector<uint32_t> xkey;  // the rows the last prepass converted, until a barrier
@@ -686,7 +691,38 @@ std::vector<Launch> build_launches(skyla_hip_context *ctx, const std::vector<Com
       const std::vector<uint32_t> key = {(uint32_t)((uintptr_t)a.bufs[2] >> 32), (uint32_t)(uintptr_t)a.bufs[2],
                                          a.push[4], a.push[8], a.push[6], a.groups[2]};
       if (key != xkey) {
-        out.push_back(x_half_prepass(ctx, a, h_off, rows));
+        // The rows usually come from the launch just before: rmsnorm (q, k, v; gate and up)
+        // or silu_mul (down).  When it writes exactly these rows, one launch does both
+        // (rmsnorm_half_rows, silu_half_rows: the same f32 rows and the same f16 rows).
+        Launch f = x_half_prepass(ctx, a, h_off, rows);
+        Launch *prev = out.empty() ? nullptr : &out.back();
+        const bool plain = join && prev && !prev->mark && prev->split == 0 && prev->extra.empty() && prev->xh_buf < 0 &&
+                           prev->groups[2] == 1 && prev->threads == 256;
+        if (plain && ctx->rmsnorm_half_rows && prev->fn == ctx->rmsnorm && prev->args.size() == 6 &&
+            prev->bufs.size() == 3 && prev->bufs[1] == a.bufs[2] && prev->bufs[2] == a.bufs[4] &&
+            prev->groups[0] == 1 && prev->args[2] == a.push[4] && prev->args[5] == a.push[8] &&
+            prev->args[3] == a.push[6] && prev->args[3] <= 4096 &&
+            ((prev->args[0] | prev->args[1] | prev->args[2] | prev->args[3] | prev->args[5]) & 3u) == 0) {
+          // NormPush {x_off, w_off, y_off, n, eps, stride} + h_off; rmsnorm's grid
+          f.fn = ctx->rmsnorm_half_rows;
+          f.bufs = {prev->bufs[0], prev->bufs[1], nullptr, prev->bufs[2]};
+          f.xh_buf = 2;
+          f.args = prev->args;
+          f.args.push_back((uint32_t)(h_off / 4));
+          for (int d = 0; d < 3; d++) f.groups[d] = prev->groups[d];
+          *prev = std::move(f);
+        } else if (plain && ctx->silu_half_rows && prev->fn == ctx->silu_mul && prev->args.size() == 4 &&
+                   prev->bufs.size() == 2 && prev->bufs[0] == a.bufs[2] && prev->bufs[1] == a.bufs[4] &&
+                   prev->args[0] == a.push[4] && prev->args[3] == a.push[8] && prev->args[2] == a.push[6] &&
+                   prev->args[1] % 4 == 0) {
+          // SiluPush {g_off, u_off, n, stride}, one row a token: the rows of the prepass's grid
+          f.fn = ctx->silu_half_rows;
+          f.bufs = {prev->bufs[0], nullptr, prev->bufs[1]};
+          f.args = {prev->args[0], prev->args[1], a.push[8], a.push[6], (uint32_t)(h_off / 4), 1u};
+          *prev = std::move(f);
+        } else {
+          out.push_back(std::move(f));
+        }
         xkey = key;
       }
       // Matmuls on the same rows with no barrier between them (q, k, v of a prefill chunk)
@@ -1164,6 +1200,8 @@ int skyla_hip_context_new(int device, skyla_hip_context **out) {
   ctx->x_half_rows = find_function(ctx.get(), "x_half_rows");
   ctx->silu_half_rows = find_function(ctx.get(), "silu_half_rows");
   ctx->silu_mul = find_function(ctx.get(), "silu_mul");
+  ctx->rmsnorm_half_rows = find_function(ctx.get(), "rmsnorm_half_rows");
+  ctx->rmsnorm = find_function(ctx.get(), "rmsnorm");
   if (prop.multiProcessorCount > 0) ctx->n_cu = (uint32_t)prop.multiProcessorCount;
   *out = ctx.release();
   return SKYLA_HIP_OK;

@@ -648,3 +648,31 @@ def test_rope_table_same_logits(ctx, ctx_len):
         finally:
             eng.free()
     assert np.array_equal(got["1"].view(np.uint32), got["0"].view(np.uint32))
+
+
+@pytest.mark.parametrize("quant", ["q4_k_m", "q4_k_m_mixed"])
+def test_prefill_prepass_joined_same_logits(ctx, quant):
+    """Prefill with each dense matmul's f16 row prepass joined to the launch that writes its
+    rows (rmsnorm_half_rows before q/k/v and before gate/up, silu_half_rows before down)
+    against the prepass as a launch of its own (tactic xhalf_join=0): three launches fewer
+    per layer in a prefill recording, and the same logits bit for bit, through the prefill
+    (two chunks, the second ragged) and the decode steps after it."""
+    c = synth.qwen3_config("tiny")
+    tensors = synth.qwen3(f"{CFG}-{quant}", c, quant, "random")
+    prompt = synth.prompt(f"{CFG}-join", E.BATCH + 22, c.n_vocab)
+    got, n_launch = {}, {}
+    for join in ("1", "0"):
+        with tactics(xhalf_join=join):
+            eng = E.Engine(ctx, tensors, c, 8 * E.ATTENTION_CHUNK, P.F16_KEYS_Q8_VALUES)
+            try:
+                rows = [eng.prefill(prompt).copy()]
+                n_launch[join] = eng.recording(True, E.BATCH).launches()
+                tok = int(np.argmax(rows[-1]))
+                for _ in range(3):
+                    rows.append(eng.step(tok).copy())
+                    tok = int(np.argmax(rows[-1]))
+                got[join] = np.stack(rows)
+            finally:
+                eng.free()
+    assert n_launch["0"] - n_launch["1"] == 3 * c.n_layer, n_launch
+    assert np.array_equal(got["1"].view(np.uint32), got["0"].view(np.uint32))
