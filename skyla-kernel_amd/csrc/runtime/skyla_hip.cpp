@@ -81,6 +81,7 @@ const Tactic kTactics[] = {
     {"moe_fuse", "26", "bit mask of the MoE decode forms (2 gate/up pair, 8 down + combine, 16 route + pair)"},
     {"splitk", "1", "dense K-quant matmuls of at most 128 tiles split their super-blocks (0: never)"},
     {"split_slots", "256", "workgroup slots a matmul K split fills (64..2048)"},
+    {"split_stages", "2", "fewest 256-value super-blocks per split of a matmul K split (1..16)"},
     {"xhalf", "1", "f16 row prepass for matmuls on f32 rows: 1 four-wave tile where it fits, 4 without "
                    "the balanced K halves, 8 eight-wave tile throughout, 0 the tile's own f32 staging"},
     {"xhalf_moe", "1", "expert-group matmuls on f32 rows take the f16 row prepass (0: the tile's own f32 staging)"},
@@ -323,13 +324,22 @@ uint64_t split_slots() {
   return v >= 64 && v <= 2048 ? (uint64_t)v : 256;
 }
 
+// Fewest super-blocks per split (the split_stages tactic, default 2: config-5 512-token
+// prefill 15.93-15.94k tok/s against 15.82-15.86k with 4 and 15.81-15.82k with 3, two runs
+// each on one box; at M = 128 the n_in-4096 launches of 32 and 48 tiles then split 8 and 5
+// ways instead of 4).
+uint32_t split_stages() {
+  const long v = std::atol(tactic("split_stages").c_str());
+  return v >= 1 && v <= 16 ? (uint32_t)v : 2u;
+}
+
 uint32_t split_of(const Command &a) {
   if (!a.split_fn || a.push.size() < 7) return 1;
   const uint64_t tiles = (uint64_t)a.groups[0] * a.groups[1] * a.groups[2];
   const uint32_t n_stage = a.push[6] / 256;  // MatmulPush.n_in
   if (tiles == 0 || tiles > 128) return 1;
   uint32_t S = (uint32_t)(split_slots() / tiles);
-  S = std::min(S, n_stage / 4);
+  S = std::min(S, n_stage / split_stages());
   S = std::min(S, 8u);
   return S < 2 ? 1 : S;
 }
@@ -740,7 +750,7 @@ std::vector<Launch> build_launches(skyla_hip_context *ctx, const std::vector<Com
       if (n_run > 1) {
         const uint64_t tiles = row_tiles * a.groups[2];
         uint32_t S = (uint32_t)(split_slots() / tiles);  // split_of's rule on the fused tile count
-        S = std::min(std::min(S, a.push[6] / 256 / 4), 8u);
+        S = std::min(std::min(S, a.push[6] / 256 / split_stages()), 8u);
         if (S < 2) S = 1;
         Launch l;
         l.fn = a.hxs_fn;

@@ -180,9 +180,9 @@ def test_matmul_balanced_grid(ctx, name, dtype, n_in, n_out, n_tok, accum, x4d):
 def test_matmul_segments_qkv(ctx, n_tok, dl):
     """q, k and v of a prefill chunk (Q4_K 4096 -> 4096, 1024, 1024 in one buffer, no barrier
     between them) run as one launch of three segments after the shared f16 row prepass: the
-    bits of the three separate launches (tactic fuse=0; the same K split here), and each
-    within the bar of the oracle; on the direct-to-LDS 128 x 128 tile (dl=1) and the
-    register-staged one (dl=0)."""
+    bits of the three separate launches (tactic fuse=0; the same K split here: at least four
+    super-blocks a split, so four ways for all of them), and each within the bar of the
+    oracle; on the direct-to-LDS 128 x 128 tile (dl=1) and the register-staged one (dl=0)."""
     n_in = 4096
     outs = [4096, 1024, 1024]
     mats = [(E.DType.Q4K, n_in, n, synth.matrix("mm-seg", f"qkv-{i}-{n}", E.DType.Q4K, n_in, n))
@@ -190,7 +190,7 @@ def test_matmul_segments_qkv(ctx, n_tok, dl):
     x = synth.activations("mm-seg", f"x-{n_tok}", (n_tok, n_in))
     got = {}
     for fuse in ("1", "0"):
-        with tactics(fuse=fuse, dl=dl):
+        with tactics(fuse=fuse, dl=dl, split_stages=4):
             s = Setup(ctx, mats, n_in, max(outs), rows=len(outs) * n_tok)
             try:
                 s.set_x(x)
