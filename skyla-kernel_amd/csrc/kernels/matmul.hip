@@ -1834,20 +1834,31 @@ extern "C" __global__ __launch_bounds__(256) void silu_half_rows(float *a, uint3
                                                                  SiluHalfPush p) {
   const uint32_t t = blockIdx.x, tid = threadIdx.x;
   if (t >= ctl[2] * p.rows_per_token) return;
+  // every load in flight before the first is used: the passes the row needs (uniform), a
+  // lane past the row's end reading its last four values (n_in is a multiple of 4)
+  const uint32_t n_pass = (p.n_in + 1023) / 1024;
+  float *gr = a + p.g_off + (size_t)t * p.x_stride;
+  const float *ur = a + p.u_off + (size_t)t * p.x_stride;
+  float4 g[HALF_ROW_V / 4], u[HALF_ROW_V / 4];
+#pragma unroll
+  for (int i = 0; i < HALF_ROW_V / 4; i++)
+    if ((uint32_t)i < n_pass) {
+      const uint32_t k = min(4 * (tid + 256 * i), p.n_in - 4);
+      g[i] = *(const float4 *)(gr + k);
+      u[i] = *(const float4 *)(ur + k);
+    }
   float4 v[HALF_ROW_V / 4];
 #pragma unroll
   for (int i = 0; i < HALF_ROW_V / 4; i++) {
     const uint32_t k = 4 * (tid + 256 * i);
     v[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (k < p.n_in) {
-      float *gr = a + p.g_off + (size_t)t * p.x_stride + k;
-      const float4 g = *(const float4 *)gr, u = *(const float4 *)(a + p.u_off + (size_t)t * p.x_stride + k);
+    if ((uint32_t)i < n_pass && k < p.n_in) {
       {
 #pragma clang fp contract(off)
-        v[i] = make_float4(g.x / (1.0f + expf(-g.x)) * u.x, g.y / (1.0f + expf(-g.y)) * u.y,
-                           g.z / (1.0f + expf(-g.z)) * u.z, g.w / (1.0f + expf(-g.w)) * u.w);
+        v[i] = make_float4(g[i].x / (1.0f + expf(-g[i].x)) * u[i].x, g[i].y / (1.0f + expf(-g[i].y)) * u[i].y,
+                           g[i].z / (1.0f + expf(-g[i].z)) * u[i].z, g[i].w / (1.0f + expf(-g[i].w)) * u[i].w);
       }
-      *(float4 *)gr = v[i];
+      *(float4 *)(gr + k) = v[i];
     }
   }
   store_half_row(v, out, p.h_off, p.n_in, t);
