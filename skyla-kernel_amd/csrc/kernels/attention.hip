@@ -700,6 +700,37 @@ extern "C" __global__ __launch_bounds__(256) void attention_merge_t__128_0(float
   if (tok >= ctl[2] || h >= n_head) return;
   const uint32_t used = min(min((ctl[1] + tok + p.chunk) / p.chunk, p.n_split), MAX_SPLITS);
   const uint32_t first = p.part_off + tok * p.part_stride + h * p.n_split * PART;
+  float *o = a + p.o_off + tok * p.o_stride + h * HD + 2 * lane;
+  if (used <= 16) {
+    // at most 16 splits (a prefill chunk within 1024 positions): every load in flight at
+    // once, then the arithmetic below in the same order (the same bits)
+    float ml = -INFINITY, ll = 0.0f, vx[16], vy[16];
+    if (lane < used) {
+      ml = a[first + lane * PART];
+      ll = a[first + lane * PART + 1];
+    }
+#pragma unroll
+    for (uint32_t j = 0; j < 16; j++)
+      if (j < used) {
+        vx[j] = a[first + j * PART + 2 + 2 * lane];
+        vy[j] = a[first + j * PART + 3 + 2 * lane];
+      }
+    const float big = wave_max(ml);
+    const float wl = lane < used ? expf(ml - big) : 0.0f;
+    float total = lane < used ? __builtin_fmaf(wl, ll, 0.0f) : 0.0f;
+    float ox = 0.0f, oy = 0.0f;
+#pragma unroll
+    for (uint32_t j = 0; j < 16; j++)
+      if (j < used) {
+        const float wj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wl), (int)j));
+        ox = __builtin_fmaf(wj, vx[j], ox);
+        oy = __builtin_fmaf(wj, vy[j], oy);
+      }
+    total = wave_sum(total);
+    o[0] = ox / total;
+    o[1] = oy / total;
+    return;
+  }
   float big = -INFINITY;
   for (uint32_t s = lane; s < used; s += 64) big = fmaxf(big, a[first + s * PART]);
   big = wave_max(big);
@@ -717,7 +748,6 @@ extern "C" __global__ __launch_bounds__(256) void attention_merge_t__128_0(float
     }
   }
   total = wave_sum(total);
-  float *o = a + p.o_off + tok * p.o_stride + h * HD + 2 * lane;
   o[0] = ox / total;
   o[1] = oy / total;
 }

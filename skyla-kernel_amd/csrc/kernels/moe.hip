@@ -218,12 +218,28 @@ extern "C" __global__ __launch_bounds__(256) void moe_combine(float *a, CombineP
 #pragma clang fp contract(off)
   const uint32_t i = blockIdx.x * 256 + threadIdx.x, tok = blockIdx.y;
   if (i >= p.n) return;
+  // the first 16 slots' loads (the engine routes at most 16) all in flight before the sum,
+  // which adds them in the same order; any further slots one by one
+  constexpr uint32_t MAXU = 16;
+  const uint32_t nb = min(p.n_used, MAXU);
+  float wv[MAXU], yv[MAXU];
+#pragma unroll
+  for (uint32_t s = 0; s < MAXU; s++)
+    if (s < nb) {
+      const uint32_t slot = tok * p.n_used + s;
+      wv[s] = a[p.weights_off + slot];
+      yv[s] = a[p.y_off + slot * p.stride + i];
+    }
+  const float x0 = a[p.x_off + tok * p.stride + i];
   float sum = 0.0f;
-  for (uint32_t s = 0; s < p.n_used; s++) {
+#pragma unroll
+  for (uint32_t s = 0; s < MAXU; s++)
+    if (s < nb) sum += wv[s] * yv[s];
+  for (uint32_t s = MAXU; s < p.n_used; s++) {
     const uint32_t slot = tok * p.n_used + s;
     sum += a[p.weights_off + slot] * a[p.y_off + slot * p.stride + i];
   }
-  a[p.x_off + tok * p.stride + i] += sum;
+  a[p.x_off + tok * p.stride + i] = x0 + sum;
 }
 
 // silu_mul (silu_mul.comp:15-23): g <- g / (1 + e^-g) * u for tokens below ctl[2].
