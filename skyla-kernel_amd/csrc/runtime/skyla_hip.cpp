@@ -82,6 +82,7 @@ const Tactic kTactics[] = {
     {"splitk", "1", "dense K-quant matmuls of at most 128 tiles split their super-blocks (0: never)"},
     {"split_slots", "256", "workgroup slots a matmul K split fills (64..2048)"},
     {"split_stages", "2", "fewest 256-value super-blocks per split of a matmul K split (1..16)"},
+    {"seg_big", "512", "slots for a segmented matmul run past 128 tiles (gate and up at M = 128), 0: no such run"},
     {"xhalf", "1", "f16 row prepass for matmuls on f32 rows: 1 four-wave tile where it fits, 4 without "
                    "the balanced K halves, 8 eight-wave tile throughout, 0 the tile's own f32 staging"},
     {"xhalf_moe", "1", "expert-group matmuls on f32 rows take the f16 row prepass (0: the tile's own f32 staging)"},
@@ -737,19 +738,26 @@ std::vector<Launch> build_launches(skyla_hip_context *ctx, const std::vector<Com
       }
       // Matmuls on the same rows with no barrier between them (q, k, v of a prefill chunk)
       // run as one launch of segments while the run stays a K-split launch (at most 128
-      // tiles: the split spreads the few tiles of each small matrix over more CUs).
+      // tiles: the split spreads the few tiles of each small matrix over more CUs).  A run
+      // of up to 256 tiles (gate and up at M = 128: 2 x 96) is one launch too, split over
+      // seg_big slots (512: two ways, 384 workgroups instead of two launches of 192):
+      // config-5 prefill 15.74-15.77k -> 16.06-16.10k tok/s; three, four and five ways
+      // (576, 768, 1024) ran 15.0-15.1k, 14.4k and 13.8-13.9k (one box).
       uint32_t n_run = 1;
       uint64_t row_tiles = a.groups[0];
+      const long seg_big = std::atol(tactic("seg_big").c_str());
+      const uint64_t max_tiles = seg_big > 0 ? 256 : 128;
       if (fuse && a.hxs_fn && a.split_fn) {
         while (n_run < kMaxSeg && i + n_run < cmds.size() && fusable_matmul(a, cmds[i + n_run]) &&
-               (row_tiles + cmds[i + n_run].groups[0]) * a.groups[2] <= 128) {
+               (row_tiles + cmds[i + n_run].groups[0]) * a.groups[2] <= max_tiles) {
           row_tiles += cmds[i + n_run].groups[0];
           n_run++;
         }
       }
       if (n_run > 1) {
         const uint64_t tiles = row_tiles * a.groups[2];
-        uint32_t S = (uint32_t)(split_slots() / tiles);  // split_of's rule on the fused tile count
+        // split_of's rule on the fused tile count
+        uint32_t S = (uint32_t)((tiles > 128 ? (uint64_t)seg_big : split_slots()) / tiles);
         S = std::min(std::min(S, a.push[6] / 256 / split_stages()), 8u);
         if (S < 2) S = 1;
         Launch l;

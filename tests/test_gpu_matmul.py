@@ -215,3 +215,40 @@ def test_matmul_segments_qkv(ctx, n_tok, dl):
     for i, (dt, _, n, d) in enumerate(mats):
         want = so.matmul(int(dt), d, n_in, n, x)
         assert rel_l2(got["1"][1][i * n_tok:(i + 1) * n_tok, :n], want) <= GUARD
+
+
+def test_matmul_gate_up_one_launch(ctx):
+    """Gate and up of a prefill chunk at M = 128 (Q4_K 4096 -> 12288 each on the same f16 rows,
+    no barrier between them: 2 x 96 row tiles) run as one launch of two segments split two
+    ways (tactic seg_big): the bits of the two separate launches (each also split two ways),
+    and within the bar of the oracle over the first 256 rows of each."""
+    n_in, n_out, n_tok = 4096, 12288, 128
+    mats = [(E.DType.Q4K, n_in, n_out, synth.matrix("mm-gu", f"gu-{i}", E.DType.Q4K, n_in, n_out)) for i in range(2)]
+    x = synth.activations("mm-gu", f"x-{n_tok}", (n_tok, n_in))
+    got = {}
+    for big in ("512", "0"):
+        with tactics(seg_big=big):
+            s = Setup(ctx, mats, n_in, n_out, rows=2 * n_tok)
+            try:
+                s.set_x(x)
+
+                def body(r):
+                    g = E.Graph(r, s.k, None, None, True)
+                    for i, m in enumerate(s.q):
+                        g.matvec(m, (s.x_off, s.s_in), (s.y_off + i * n_tok * s.s_out, s.s_out), False, True,
+                                 groups_z=1)
+                rec = ctx.record(False, body)
+                try:
+                    launches = rec.launches()
+                    ctx.replay(rec)
+                finally:
+                    rec.free()
+                got[big] = (launches, s.y(2 * n_tok, s.s_out))
+            finally:
+                s.free()
+    assert got["512"][0] == 2 and got["0"][0] == 3   # prepass + one launch / + two
+    assert np.array_equal(got["512"][1].view(np.uint32), got["0"][1].view(np.uint32))
+    rows = 256
+    for i, (dt, _, n, d) in enumerate(mats):
+        want = so.matmul(int(dt), d[: rows * (n_in // 256) * 144], n_in, rows, x)
+        assert rel_l2(got["512"][1][i * n_tok:(i + 1) * n_tok, :rows], want) <= GUARD
