@@ -355,7 +355,7 @@ def decode_config5(ctx: Context, contexts=(1024, 16384), steps: int = 20, warmup
         # 128-token chunks, each one graph replay of the batched recording)
         prompt = [int(v) for v in synth.rng("qwen3-8b-q4_k_m", "prompt").integers(0, c.n_vocab, 512)]
         eng.reset()
-        eng.prefill(prompt[:128])  # warm-up
+        eng.prefill(prompt)  # warm-up: every chunk's recording made
         times = []
         for _ in range(3):
             eng.reset()

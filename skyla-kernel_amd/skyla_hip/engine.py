@@ -37,7 +37,7 @@ MAX_SPLITS = 4096       # splits the attention merge weighs in LDS (kernels/atte
 # Split counts the engine records its decode and prefill graphs for: a replay uses the
 # smallest that covers the positions in play (each recording's attention grid and merge
 # then span only those splits; the arena's own count is the last bucket).
-SPLIT_BUCKETS = (1, 16, 64, 256)
+SPLIT_BUCKETS = (1, 2, 4, 8, 16, 32, 64, 128, 256)
 BATCH = 128
 # What the MoE kernels hold (moe.hip): moe_route ranks at most 256 logits, one per thread of
 # its workgroup, and picks at most 16; moe_sort ranks at most 1024 slots (moe_sort.comp:15).

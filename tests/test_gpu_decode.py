@@ -563,7 +563,7 @@ def test_split_buckets_same_logits(ctx):
         full_p = E.record(ctx, eng.kernels, eng.weights, a, c, True, False, a.n_split)
         full_d = E.record(ctx, eng.kernels, eng.weights, a, c, False, False, a.n_split)
         prompt = synth.prompt(f"{CFG}-buckets", 150, c.n_vocab)
-        got = eng.prefill(prompt)                      # chunks at positions 0 and 128: 16 splits
+        got = eng.prefill(prompt)                      # chunks at positions 0 and 128: 2 and 4 splits
         assert eng.recording(True, 128 + E.BATCH) is not full_p
         eng.reset()
         for i in range(0, len(prompt), E.BATCH):
