@@ -634,7 +634,7 @@ extern "C" __global__ __launch_bounds__(1024) void attention_merge__128_0(float 
   const uint32_t first = p.part_off + tok * p.part_stride + h * p.n_split * PART;
   float mw = -INFINITY, lw = 0.0f, ax = 0.0f, ay = 0.0f;
   for (uint32_t base = 0; base < used; base += 1024) {
-    // this round's splits of the wave: s_i = base + wave + 16 i, i < n_i
+    // this pass's splits of the wave: s_i = base + wave + 16 i, i < n_i
     const uint32_t s0 = base + wave;
     const uint32_t n_i = s0 < used ? min(64u, (used - s0 + 15) / 16) : 0u;
     if (n_i == 0) break;  // wave-uniform; no later round holds a split of this wave either
