@@ -1254,6 +1254,8 @@ MV_Q6K(8, 0, 1, 0, 32)
 MV_Q6K(8, 1, 1, 0, 32)
 MV_Q6K(4, 0, 1, 0, 16)
 MV_Q6K(4, 1, 1, 0, 16)
+// the Q8_0 output head (65536 rows or more, no accumulation): 16 lanes per row, 16 rows a workgroup
+MV_Q8_0(4, 0, 1, 0, 16)
 
 // K-split Q4_K form for n_in = 4096 (matvec_q4k_ks_body): RPL rows per slot, NG row-groups
 // per workgroup; the runtime picks it for dense Q4_K launches whose rows all have n_in 4096.

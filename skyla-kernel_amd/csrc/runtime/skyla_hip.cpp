@@ -73,6 +73,8 @@ const Tactic kTactics[] = {
     {"fuse", "1", "independent dispatches of one kernel run as one segmented launch (0: one launch each)"},
     {"retile", "1", "dense matvec launches take the variant the size rule gives them (0: the engine's)"},
     {"variant", "", "W_R_L: every dense launch of a matvec kernel on that (waves, rows, lanes) variant"},
+    {"q8_big", "4_1_16", "W_R_L: dense Q8_0 launches of 65536 rows or more (an output head) on that variant "
+                         "(empty: the engine's)"},
     {"ks", "1", "K-split matvec forms for n_in 4096 (Q4_K) and 12288 (Q6_K); 0: none; R_G: Q4_K shape"},
     {"ks6", "", "R_G_D: the Q6_K K-split form on that (rows, groups, groups ahead) shape"},
     {"ks3", "1", "the Q4_K K-split form for n_in 12288 (0: LDS-staged form; R_G: that shape)"},
@@ -1119,7 +1121,19 @@ std::shared_ptr<const Retile> make_retile(skyla_hip_context *ctx, const char *na
   auto t = std::make_shared<Retile>();
   t->n_out_word = 5;
   add_ks(ctx, name, spec, *t);
-  for (VariantRule r : kVariantRules) {
+  std::vector<VariantRule> rules(std::begin(kVariantRules), std::end(kVariantRules));
+  // Dense Q8_0 launches of 65536 rows or more (config 1's tied head, 151936 x 1024): the
+  // engine's (4, 2, 64) variant stages the activations in a workgroup per 8 rows (72.7 us,
+  // 2.1 TB/s); (4, 1, 16) covers 16 rows a workgroup with 16 lanes a row: config 1 0.852 ->
+  // 0.817-0.820 ms per token (1090 -> 1137-1140 tok/s); (8, 1, 16) 0.818-0.821, (4, 2, 16)
+  // 0.820-0.822, (4, 4, 64) 0.833-0.835, (8, 1, 32) 0.834-0.836, (8, 2, 64) 0.838, (2, 1,
+  // 16) 0.861-0.862 (one box).  Other Q8_0 launches keep the engine's variant.
+  {
+    unsigned bw = 0, br = 0, bl = 0;
+    if (std::sscanf(tactic("q8_big").c_str(), "%u_%u_%u", &bw, &br, &bl) == 3)
+      rules.push_back({"matvec_q8_0", 0, 5, {{65536, bw, br, bl}, {0, spec[0], spec[2], spec[4]}}, 2});
+  }
+  for (VariantRule r : rules) {
     if (std::strcmp(r.name, name) != 0 || r.moe != spec[3]) continue;
     // the variant tactic W_R_L puts every dense launch of this kernel on one variant (sweeps)
     if (!spec[3]) {

@@ -500,3 +500,28 @@ def test_ks6_other_widths_keep_their_variant(ctx):
         s.free()
     want = so.matvec(int(E.DType.Q6K), data, n_in, n_out, x)
     assert rel_l2(got, want) <= f32_reorder_bar(E.DType.Q6K, data, n_in, n_out, x, want)
+
+
+def test_q8_0_head_variant(ctx):
+    """Config 1's tied output head (Q8_0 1024 -> 151936): dense Q8_0 launches of 65536 rows or
+    more run the (4, 1, 16) variant (tactic q8_big), within the f32 reordering bar of the
+    oracle, as the engine's own variant (q8_big empty) is; the two sum in different orders."""
+    n_in, n_out = 1024, 151936
+    data = synth.matrix("q8-head", "head", E.DType.Q8_0, n_in, n_out)
+    x = synth.activations("q8-head", "x", n_in)
+    got = {}
+    for v in ("4_1_16", ""):
+        with tactics(q8_big=v):
+            s = Setup(ctx, [(E.DType.Q8_0, n_in, n_out, data)], n_in, n_out)
+            try:
+                s.set_x(x)
+                s.matvec(0)
+                got[v] = s.y(1, n_out)[0].copy()
+            finally:
+                s.free()
+    want = so.matvec(int(E.DType.Q8_0), data, n_in, n_out, x)
+    bar = f32_reorder_bar(E.DType.Q8_0, data, n_in, n_out, x, want)
+    for v, g in got.items():
+        assert rel_l2(g, want) <= bar, (v, rel_l2(g, want), bar)
+    assert not np.array_equal(got["4_1_16"], got[""])
+
