@@ -1225,6 +1225,7 @@ MV_Q6K_F(silu, 1, 4, 1, 1, 16)
 MV_Q6K_F(silu, 1, 8, 1, 1, 32)
 MV_Q8_0_F(norm, 2, 4, 0, 2, 64)
 MV_Q8_0_F(silu, 1, 4, 1, 2, 64)
+MV_Q8_0_F(silu, 1, 4, 1, 1, 64)  // dense Q8_0 launches below 2048 rows
 // gate and up of a decode token in one launch, writing silu(gate) * up (MODE 3): half the
 // waves take gate rows, half the same rows of up, so a workgroup outputs RWG / 2 values
 #define MV_Q4K_GLU(W, R, L)                                                                    \

@@ -73,6 +73,8 @@ const Tactic kTactics[] = {
     {"fuse", "1", "independent dispatches of one kernel run as one segmented launch (0: one launch each)"},
     {"retile", "1", "dense matvec launches take the variant the size rule gives them (0: the engine's)"},
     {"variant", "", "W_R_L: every dense launch of a matvec kernel on that (waves, rows, lanes) variant"},
+    {"q8_small", "4_1_64", "W_R_L: dense Q8_0 launches (plain and SiLU-folded) below 2048 rows on that variant "
+                           "(empty: the engine's)"},
     {"q8_big", "4_1_16", "W_R_L: dense Q8_0 launches of 65536 rows or more (an output head) on that variant "
                          "(empty: the engine's)"},
     {"ks", "1", "K-split matvec forms for n_in 4096 (Q4_K) and 12288 (Q6_K); 0: none; R_G: Q4_K shape"},
@@ -1127,11 +1129,20 @@ std::shared_ptr<const Retile> make_retile(skyla_hip_context *ctx, const char *na
   // 2.1 TB/s); (4, 1, 16) covers 16 rows a workgroup with 16 lanes a row: config 1 0.852 ->
   // 0.817-0.820 ms per token (1090 -> 1137-1140 tok/s); (8, 1, 16) 0.818-0.821, (4, 2, 16)
   // 0.820-0.822, (4, 4, 64) 0.833-0.835, (8, 1, 32) 0.834-0.836, (8, 2, 64) 0.838, (2, 1,
-  // 16) 0.861-0.862 (one box).  Other Q8_0 launches keep the engine's variant.
-  {
-    unsigned bw = 0, br = 0, bl = 0;
-    if (std::sscanf(tactic("q8_big").c_str(), "%u_%u_%u", &bw, &br, &bl) == 3)
-      rules.push_back({"matvec_q8_0", 0, 5, {{65536, bw, br, bl}, {0, spec[0], spec[2], spec[4]}}, 2});
+  // 16) 0.861-0.862 (one box).  Launches below 2048 rows (config 1's o and SiLU-folded
+  // down, 1024 rows: 128 workgroups of 8 rows) take (4, 1, 64), 4 rows a workgroup: 0.818 ->
+  // 0.781-0.782 ms per token (1131-1135 -> 1183-1189 tok/s); (2, 1, 64) 0.832-0.833, (2, 2,
+  // 64) 0.840-0.841, (1, 1, 64) 0.857-0.858 (one box).  The rest keep the engine's variant.
+  if (std::strcmp(name, "matvec_q8_0") == 0 || std::strcmp(name, "matvec_q8_0_silu") == 0) {
+    VariantRule q{name, 0, 5, {}, 0};
+    unsigned bw = 0, br = 0, bl = 0, sw = 0, sr = 0, sl = 0;
+    const bool big = std::strcmp(name, "matvec_q8_0") == 0 && spec[1] == 0 &&
+                     std::sscanf(tactic("q8_big").c_str(), "%u_%u_%u", &bw, &br, &bl) == 3;
+    const bool small = std::sscanf(tactic("q8_small").c_str(), "%u_%u_%u", &sw, &sr, &sl) == 3;
+    if (big) q.v[q.n++] = {65536, bw, br, bl};
+    q.v[q.n++] = {small ? 2048u : 0u, spec[0], spec[2], spec[4]};
+    if (small) q.v[q.n++] = {0, sw, sr, sl};
+    if (q.n > 1) rules.push_back(q);
   }
   for (VariantRule r : rules) {
     if (std::strcmp(r.name, name) != 0 || r.moe != spec[3]) continue;
