@@ -27,10 +27,22 @@ extern "C" __global__ __launch_bounds__(256) void moe_logits(const float *w, con
   const uint32_t e = blockIdx.x, tok = blockIdx.y, tid = threadIdx.x;
   const float4 *row = (const float4 *)(w + p.router_off + e * p.n_embd);
   const float4 *x = (const float4 *)(a + p.x_off + tok * p.x_stride);
+  const uint32_t n4 = p.n_embd / 4;
+  // one float4's product, its rounding order fixed: ((y y + x x) + z z) + w w as three fmas
+  auto dot4 = [](float4 r, float4 v) {
+    return __builtin_fmaf(r.w, v.w, __builtin_fmaf(r.z, v.z, __builtin_fmaf(r.x, v.x, r.y * v.y)));
+  };
   float s = 0.0f;
-  for (uint32_t i = tid; i < p.n_embd / 4; i += 256) {
-    const float4 r = row[i], v = x[i];
-    s += r.x * v.x + r.y * v.y + r.z * v.z + r.w * v.w;
+  if (n4 != 0 && n4 <= 512) {
+    // up to two float4 per thread: both loads issued before the first product (clamped
+    // addresses, products kept only where in range), the same sums as the loop below
+    const uint32_t i0 = min(tid, n4 - 1), i1 = min(tid + 256, n4 - 1);
+    const float4 r0 = row[i0], v0 = x[i0], r1 = row[i1], v1 = x[i1];
+    const float t0 = dot4(r0, v0), t1 = dot4(r1, v1);
+    s = tid < n4 ? s + t0 : s;
+    s = tid + 256 < n4 ? s + t1 : s;
+  } else {
+    for (uint32_t i = tid; i < n4; i += 256) s += dot4(row[i], x[i]);
   }
   s = group_sum<64>(s);
   if ((tid & 63) == 0) part[tid >> 6] = s;
